@@ -1,0 +1,202 @@
+/*
+ * ttperf.h — C ABI of libttperf_hip, the MI355X (gfx950) optimizer-step engine.
+ *
+ * One context owns a flat parameter store on one GPU: every tensor of a model is a
+ * {offset, numel, flags} view into contiguous HBM buffers (param, grad, fp32 master,
+ * exp_avg, exp_avg_sq, momentum).  A step over all tensors is one multi-tensor launch
+ * (plus one grad-norm/inf-check launch when clipping or loss scaling is on).
+ *
+ * Reference interfaces each group of entry points replaces (csirak/tt-perf):
+ *   ttp_create / ttp_destroy / ttp_tensor_*  — per-parameter storage owned by
+ *       autograd::Value (autograd/dynamic/autograd.hpp:38-84), static_autograd::Value
+ *       (autograd/static/value.hpp:27-48) and the per-layer tensors of the traced layers
+ *       (autograd/traced/nn.hpp:54-69); parameters() lists (autograd/dynamic/nn.hpp:35,52-54).
+ *   ttp_set_has_grad / ttp_zero_grad         — `grad = std::nullopt` / `p.grad = None`
+ *       (autograd/dynamic/optim.hpp:30-34, py/optim.py:89-92, py/engine.py:141-142) and
+ *       static zero_grad (autograd/static/nn.hpp:98-101).
+ *   ttp_adam_step                            — Adam.step (py/optim.py:49-87), extended with
+ *       decoupled weight decay, fp32 master weights, loss scaling and global-norm clipping.
+ *   ttp_sgd_step                             — SGD::step (autograd/dynamic/optim.hpp:21-27),
+ *       SGD.step (py/optim.py:13-22), TracedSGD::step / sgd_update
+ *       (autograd/traced/optim.hpp:22-26, autograd/traced/ops.hpp:132-134) and every
+ *       per-module sgd_step (autograd/traced/nn.hpp:93-96,272-275,317-321), extended with
+ *       momentum, dampening, nesterov and L2 weight decay.
+ *   ttp_last_error                           — the ValueError / std::exception paths
+ *       (py/optim.py:9-16,33-41,54-55); no exception crosses this ABI.
+ *
+ * Conventions: every function returns TTP_OK (0) or a negative TTP_ERR_* code and leaves
+ * a message for ttp_last_error() (thread-local).  All work is ordered on the context's
+ * stream and is asynchronous, except ttp_download to host memory, ttp_sync, ttp_scaler_get,
+ * ttp_get_step, ttp_grad_norm and any step call given a non-NULL report, which wait for
+ * the stream.  A context is used by one host thread at a time.
+ */
+#ifndef TTPERF_TTPERF_H
+#define TTPERF_TTPERF_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TTP_ABI_VERSION 1
+
+/* ---- status codes ---------------------------------------------------------------- */
+#define TTP_OK 0
+#define TTP_ERR_INVALID (-1)   /* bad argument: the cases py/optim.py raises ValueError for */
+#define TTP_ERR_NO_DEVICE (-2) /* no HIP device, or device index out of range            */
+#define TTP_ERR_HIP (-3)       /* a HIP runtime call failed                               */
+#define TTP_ERR_OOM (-4)       /* device or pinned-host allocation failed                 */
+#define TTP_ERR_STATE (-5)     /* call not valid in the context's current state/mode      */
+#define TTP_ERR_RANGE (-6)     /* tensor index or element count out of range              */
+
+/* ---- precision modes -------------------------------------------------------------- */
+#define TTP_MODE_FP32 0  /* fp32 params/grads; the param buffer is the master copy    */
+#define TTP_MODE_MIXED 1 /* bf16 params/grads + fp32 master; bf16 param = RNE(master) */
+
+/* ---- buffers of the flat store ---------------------------------------------------- */
+#define TTP_BUF_PARAM 0      /* model-facing weights: fp32 (FP32) or bf16 (MIXED)       */
+#define TTP_BUF_GRAD 1       /* gradients: fp32 (FP32) or bf16 (MIXED)                  */
+#define TTP_BUF_MASTER 2     /* fp32 master weights (same memory as PARAM in FP32 mode) */
+#define TTP_BUF_EXP_AVG 3    /* Adam first moment m, fp32                               */
+#define TTP_BUF_EXP_AVG_SQ 4 /* Adam second moment v, fp32                              */
+#define TTP_BUF_MOMENTUM 5   /* SGD momentum buffer, fp32                               */
+
+/* Pass as `index` to address the whole flat buffer (in layout order, padding included). */
+#define TTP_ALL_TENSORS 0xFFFFFFFFu
+
+/* ---- per-tensor flags -------------------------------------------------------------- */
+#define TTP_TENSOR_DECAY 1u /* weight decay applies to this tensor (e.g. 2-D weights) */
+
+/* Memory kinds for upload/download. */
+#define TTP_HOST 0
+#define TTP_DEVICE 1
+
+typedef struct ttp_ctx ttp_ctx;
+
+typedef struct ttp_tensor_desc {
+    uint64_t numel;  /* elements; 0 is allowed (the tensor is then never touched) */
+    uint32_t flags;  /* TTP_TENSOR_* */
+    uint32_t reserved;
+} ttp_tensor_desc;
+
+/* Adam / AdamW.  Hyperparameters are host doubles (Python floats in py/optim.py:31-47);
+ * the engine rounds lr, betas, 1-beta, eps and the bias corrections to fp32 exactly as
+ * py/optim.py's full_like(fill_value=...) does. */
+typedef struct ttp_adam_hparams {
+    double lr;            /* > 0 */
+    double beta1, beta2;  /* in (0, 1) */
+    double eps;           /* > 0 */
+    double weight_decay;  /* >= 0; applied only to TTP_TENSOR_DECAY tensors */
+    int32_t decoupled;    /* 1: AdamW (p *= 1 - lr*wd first); 0: L2 (g += wd*p)   */
+    int32_t reserved;
+    double max_grad_norm; /* > 0: clip the global L2 norm to this; <= 0: no clipping */
+} ttp_adam_hparams;
+
+/* SGD with optional momentum, dampening, nesterov and L2 weight decay.
+ * momentum = dampening = weight_decay = 0 is exactly `p - lr*g` (two roundings, no FMA)
+ * as autograd/dynamic/optim.hpp:24-25. */
+typedef struct ttp_sgd_hparams {
+    double lr;            /* > 0 */
+    double momentum;      /* >= 0 */
+    double dampening;     /* any; torch semantics */
+    double weight_decay;  /* >= 0 */
+    int32_t nesterov;     /* requires momentum > 0 and dampening == 0 */
+    int32_t reserved;
+    double max_grad_norm; /* > 0: clip; <= 0: off */
+} ttp_sgd_hparams;
+
+/* Dynamic loss scaling (torch.amp.GradScaler semantics).  While enabled, every step
+ * unscales the gradients by 1/scale, skips the whole update when any gradient is
+ * non-finite (params, moments and the step count stay bit-unchanged), and then updates
+ * the scale: x backoff on overflow, x growth after growth_interval clean steps. */
+typedef struct ttp_scaler_config {
+    int32_t enabled;
+    int32_t growth_interval; /* > 0 */
+    double init_scale;       /* > 0 */
+    double growth_factor;    /* > 1 */
+    double backoff_factor;   /* in (0, 1) */
+} ttp_scaler_config;
+
+typedef struct ttp_step_report {
+    int32_t found_inf;      /* non-finite gradient seen (only checked when a norm pass ran) */
+    int32_t skipped;        /* the update was skipped (loss scaling on and found_inf)       */
+    double grad_norm;       /* global L2 norm of the unscaled gradients; NaN if not computed */
+    float clip_coef;        /* multiplier applied to the gradients (1 when not clipping)    */
+    float scale;            /* loss scale after this step's update                          */
+    int32_t growth_tracker; /* clean steps since the last scale change                      */
+    int32_t reserved;
+    uint64_t step;          /* optimizer steps applied so far (bias-correction t)           */
+} ttp_step_report;
+
+/* ---- context lifetime --------------------------------------------------------------- */
+int ttp_device_count(int* count);
+int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n_tensors, int mode,
+               ttp_ctx** out);
+int ttp_destroy(ttp_ctx* ctx);
+/* Use an existing HIP stream (hipStream_t passed as void*); NULL = the context's own. */
+int ttp_set_stream(ttp_ctx* ctx, void* hip_stream);
+int ttp_sync(ttp_ctx* ctx);
+
+/* ---- layout ------------------------------------------------------------------------- */
+int ttp_num_tensors(const ttp_ctx* ctx, uint32_t* n);
+int ttp_mode(const ttp_ctx* ctx, int* mode);
+/* total elements of each flat buffer (tensor footprints are 64-element aligned) */
+int ttp_flat_numel(const ttp_ctx* ctx, uint64_t* total);
+int ttp_tensor_info(const ttp_ctx* ctx, uint32_t index, uint64_t* offset, uint64_t* numel,
+                    uint32_t* flags);
+/* Device address of buffer `which` for tensor `index` (or the flat base for
+ * TTP_ALL_TENSORS).  Moment/momentum buffers are allocated on first use; asking for
+ * one allocates it (zero-filled). */
+int ttp_buffer_ptr(ttp_ctx* ctx, int which, uint32_t index, void** ptr);
+
+/* ---- data movement ------------------------------------------------------------------ */
+/* Copy n elements (exactly the tensor's numel, or the flat total for TTP_ALL_TENSORS)
+ * in the buffer's element type.  Uploading GRAD marks the tensor(s) as having a grad.
+ * MIXED mode keeps the two weight copies consistent: uploading MASTER also writes
+ * PARAM = RNE_bf16(MASTER), uploading PARAM also writes MASTER = float(PARAM). */
+int ttp_upload(ttp_ctx* ctx, int which, uint32_t index, const void* src, uint64_t n,
+               int src_kind);
+int ttp_download(ttp_ctx* ctx, int which, uint32_t index, void* dst, uint64_t n,
+                 int dst_kind);
+
+/* ---- gradients ---------------------------------------------------------------------- */
+/* has_grad = 0 is `grad = None`: the tensor is skipped by every step (its param and
+ * optimizer state are not touched) and left out of the grad norm. */
+int ttp_set_has_grad(ttp_ctx* ctx, uint32_t index, int has_grad);
+int ttp_get_has_grad(const ttp_ctx* ctx, uint32_t index, int* has_grad);
+/* Zero the whole grad buffer; set_to_none = 1 also clears every has_grad flag. */
+int ttp_zero_grad(ttp_ctx* ctx, int set_to_none);
+
+/* ---- optimizer steps ------------------------------------------------------------------ */
+int ttp_adam_step(ttp_ctx* ctx, const ttp_adam_hparams* hp, ttp_step_report* report);
+int ttp_sgd_step(ttp_ctx* ctx, const ttp_sgd_hparams* hp, ttp_step_report* report);
+/* Global L2 norm of the gradients that exist, unscaled by the current loss scale when
+ * scaling is on (synchronous; does not change any state). */
+int ttp_grad_norm(ttp_ctx* ctx, double* norm);
+
+/* ---- step counter and loss scaler ------------------------------------------------------- */
+int ttp_get_step(ttp_ctx* ctx, uint64_t* step);
+int ttp_set_step(ttp_ctx* ctx, uint64_t step);
+int ttp_scaler_configure(ttp_ctx* ctx, const ttp_scaler_config* cfg);
+int ttp_scaler_get(ttp_ctx* ctx, float* scale, int32_t* growth_tracker);
+int ttp_scaler_set(ttp_ctx* ctx, float scale, int32_t growth_tracker);
+
+/* ---- per-kernel timing (HIP events on the context's stream) ------------------------------ */
+#define TTP_KERNEL_NORM 0   /* grad-norm / inf-check / scaler finalize pass */
+#define TTP_KERNEL_UPDATE 1 /* fused multi-tensor update pass               */
+/* on = 1 starts recording an event pair around every launch of every kernel. */
+int ttp_timing_enable(ttp_ctx* ctx, int on);
+/* Waits for the recorded events, returns the summed milliseconds and the launch count
+ * of `kernel` since the last reset, then forgets them. */
+int ttp_timing_collect(ttp_ctx* ctx, int kernel, double* total_ms, uint64_t* launches);
+
+const char* ttp_last_error(void);
+int ttp_abi_version(void);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* TTPERF_TTPERF_H */

@@ -1,0 +1,373 @@
+"""Pins the CPU oracle (oracle/ttp_oracle.c) before it is trusted as the checker.
+
+Each check is chosen so that a plausible slip in the restatement (a dropped term, a wrong
+sign, decay applied after the update, bias correction on the wrong moment, a clip applied
+before the unscale, a scale that grows on the wrong step) fails it:
+  * the reference's own known answers (autograd/tests/test_sgd.cpp:45-70,
+    verify/verify_autograd.py:119-162, tests/adam_optimizer.py:15-92, tests/sgd_optimizer.py:15-39);
+  * torch library goldens for what the reference lacks (tests/golden/make_golden.py);
+  * an exhaustive 2^32 check of the bf16 rounding against an independent method;
+  * fp64 / math.fsum brute force for the norm; closed forms and invariants.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import f32_ulp_diff, golden
+
+
+# ---------------------------------------------------------------------------- helpers
+def split(flat, numels):
+    out, o = [], 0
+    for n in numels:
+        out.append(flat[o:o + n])
+        o += n
+    return out
+
+
+def gather(st, which):
+    return np.concatenate([st.view(which, i) for i in range(st.n)])
+
+
+def run_torch_fixture(d, step_fn, mode=O.MODE_FP32, state_keys=("exp_avg", "exp_avg_sq")):
+    numels = [int(n) for n in d["shapes_numel"]]
+    st = O.OracleStore(numels, flags=[int(x) for x in d["decay"]], mode=mode)
+    for i, x in enumerate(split(d["init"], numels)):
+        st.set_master(i, x)
+    hist = {"param": []}
+    for k in state_keys:
+        hist[k] = []
+    for s in range(d["grads"].shape[0]):
+        for i, g in enumerate(split(d["grads"][s], numels)):
+            st.set_grad(i, g if mode == O.MODE_FP32 else O.bf16_rne(g))
+        step_fn(st)
+        hist["param"].append(gather(st, "master"))
+        for k in state_keys:
+            hist[k].append(gather(st, k))
+    return st, {k: np.stack(v) for k, v in hist.items()}
+
+
+def assert_close_rel(a, b, rtol, atol, what):
+    err = np.abs(a.astype(np.float64) - b.astype(np.float64))
+    lim = rtol * np.abs(b.astype(np.float64)) + atol
+    worst = np.max(err - lim)
+    assert worst <= 0, f"{what}: max excess {worst:g} (max err {err.max():g})"
+
+
+# ---------------------------------------------------------------------------- bf16
+def test_bf16_exhaustive_against_independent_rounding():
+    # every fp32 bit pattern: carry-trick RNE vs nearest-even search in exact double
+    assert O.lib().orc_bf16_check_range(0, 1 << 32, 8) == 0
+
+
+def test_bf16_matches_torch_conversion():
+    d = golden("bf16_torch.npz")
+    x = d["x_bits"].view(np.float32)
+    got = O.bf16_rne(x)
+    nan = np.isnan(x)
+    assert np.array_equal(got[~nan], d["bf16"][~nan])
+    # NaN: canonical 0x7FC0 (c10::BFloat16's scalar conversion); torch's vectorised CPU
+    # path writes 0xFFFF instead, so only NaN-ness is compared against the fixture.
+    assert np.all(got[nan] == 0x7FC0)
+    assert np.all((d["bf16"][nan] & 0x7F80) == 0x7F80) and np.all(d["bf16"][nan] & 0x7F)
+
+
+def test_bf16_round_trip_is_identity():
+    h = np.arange(1 << 16, dtype=np.uint16)
+    f = O.bf16_to_f32(h)
+    back = O.bf16_rne(f)
+    finite_or_inf = ~np.isnan(f)
+    assert np.array_equal(back[finite_or_inf], h[finite_or_inf])
+
+
+# ---------------------------------------------------------------------------- reference known answers
+@pytest.mark.parametrize("mode", [O.MODE_FP32, O.MODE_MIXED])
+def test_sgd_bias_known_answer(mode):
+    # autograd/tests/test_sgd.cpp:45-70 and verify/verify_autograd.py:119-162: a bias of
+    # zeros with grad 32 (batch of ones) at lr 0.01 goes to -0.32, then -0.64.
+    st = O.OracleStore([32], mode=mode)
+    st.set_master(0, np.zeros(32, np.float32))
+    g = np.full(32, 32.0, np.float32)
+    expect = []
+    for _ in range(2):
+        st.set_grad(0, g if mode == O.MODE_FP32 else O.bf16_rne(g))
+        st.sgd_step(lr=0.01)
+        expect.append(st.view("master", 0).copy())
+    np.testing.assert_allclose(expect[0], -0.32, atol=1e-6)
+    np.testing.assert_allclose(expect[1], -0.64, atol=1e-6)
+    # exact fp32 values of two rounded ops per step (multiply, then subtract)
+    u = np.float32(32.0) * np.float32(0.01)
+    assert np.all(expect[0] == np.float32(0) - u)
+    assert np.all(expect[1] == (np.float32(0) - u) - u)
+    if mode == O.MODE_MIXED:
+        assert np.array_equal(st.view("param", 0), O.bf16_rne(expect[1]))
+
+
+def test_adam_one_step_known_answer():
+    # tests/adam_optimizer.py:25-50: Linear(32,32) from seed 31, grad = x^T @ ones, lr 0.1,
+    # compared with the closed form _adam_step_ref (the reference asserts 1e-1; the fp32
+    # restatement lands within a few ulp of the closed form).
+    d = golden("reference_known_answers.npz")
+    st = O.OracleStore([1024])
+    st.set_master(0, d["adam1_w0"])
+    st.set_grad(0, d["adam1_grad"])
+    st.adam_step(lr=0.1, betas=(0.9, 0.999), eps=1e-8)
+    got = st.view("master", 0).reshape(32, 32)
+    np.testing.assert_allclose(got, d["adam1_w1"], atol=1e-1, rtol=1e-1)
+    # the closed form divides lr*m_hat by the denominator, py/optim.py:85 multiplies lr by
+    # m_hat/denom: both within a few ulp of the step size lr (w - lr*sign(g) can cancel, so
+    # the bound is absolute)
+    assert np.abs(got.astype(np.float64) - d["adam1_w1"]).max() <= 8 * np.spacing(np.float32(0.1))
+
+
+def test_adam_two_steps_known_answer():
+    # tests/adam_optimizer.py:53-92: two steps through tanh with grads from the current weights
+    d = golden("reference_known_answers.npz")
+    x = d["adam2_x"].astype(np.float32)
+    st = O.OracleStore([1024])
+    st.set_master(0, d["adam2_w0"])
+    for _ in range(2):
+        w = st.view("master", 0).reshape(32, 32)
+        z = np.tanh(x @ w)
+        st.set_grad(0, (x.T @ (1 - z * z)).astype(np.float32))
+        st.adam_step(lr=0.1, betas=(0.9, 0.999), eps=1e-8)
+        st.zero_grad()
+    got = st.view("master", 0).reshape(32, 32)
+    np.testing.assert_allclose(got, d["adam2_w2"], atol=1e-1, rtol=1e-1)
+    np.testing.assert_allclose(got, d["adam2_w2"], atol=1e-5, rtol=1e-5)
+
+
+def test_sgd_bf16_known_answer():
+    # tests/sgd_optimizer.py:15-39: bf16 w0 - 0.1 * grad (reference tolerance 5e-2)
+    d = golden("reference_known_answers.npz")
+    st = O.OracleStore([1024], mode=O.MODE_MIXED)
+    st.set_master(0, O.bf16_to_f32(d["sgd1_w0"]))
+    st.set_grad(0, d["sgd1_grad"])
+    st.sgd_step(lr=0.1)
+    got = O.bf16_to_f32(st.view("param", 0))
+    np.testing.assert_allclose(got, O.bf16_to_f32(d["sgd1_w1"]).ravel(), atol=5e-2, rtol=5e-2)
+
+
+# ---------------------------------------------------------------------------- torch goldens
+def _adam_run(d, **hp):
+    return run_torch_fixture(d, lambda st: st.adam_step(**hp))[1]
+
+
+@pytest.mark.parametrize("name,hp", [
+    ("torch_adam", dict(lr=0.1, betas=(0.9, 0.999), eps=1e-8)),
+    ("torch_adamw", dict(lr=0.05, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.3,
+                         decoupled=True)),
+    ("torch_adam_l2", dict(lr=0.05, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.3,
+                           decoupled=False)),
+])
+def test_adam_family_matches_torch(name, hp):
+    d = golden(name + ".npz")
+    got = _adam_run(d, **hp)
+    # torch evaluates lr/bc1 * m / (sqrt(v)/sqrt(bc2) + eps) and lerps m; the restatement
+    # keeps py/optim.py's op order, so they agree to a few fp32 roundings per step.
+    assert_close_rel(got["exp_avg"], d["exp_avg"], 2e-6, 1e-7, name + " m")
+    assert_close_rel(got["exp_avg_sq"], d["exp_avg_sq"], 2e-6, 1e-8, name + " v")
+    assert_close_rel(got["param"], d["param"], 2e-6, 2e-7, name + " p")
+
+
+def test_adamw_decay_placement_is_visible():
+    # decay applied after the update instead of before must fail the torch comparison
+    d = golden("torch_adamw.npz")
+    got = _adam_run(d, lr=0.05, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.0)
+    with pytest.raises(AssertionError):
+        assert_close_rel(got["param"], d["param"], 2e-6, 2e-7, "no-decay")
+
+
+@pytest.mark.parametrize("name", ["torch_sgd_plain", "torch_sgd_momentum", "torch_sgd_damp_wd",
+                                  "torch_sgd_nesterov"])
+def test_sgd_family_matches_torch(name):
+    d = golden(name + ".npz")
+    lr, mu, damp, wd, nest = d["hp"]
+    keys = ("momentum",) if mu else ()
+    _, got = run_torch_fixture(
+        d, lambda st: st.sgd_step(lr=lr, momentum=mu, dampening=damp, weight_decay=wd,
+                                  nesterov=bool(nest)), state_keys=keys)
+    assert_close_rel(got["param"], d["param"], 1e-6, 1e-7, name + " p")
+    if mu:
+        assert_close_rel(got["momentum"], d["momentum_buffer"], 1e-6, 1e-7, name + " buf")
+
+
+def test_scaler_sequences_match_torch():
+    d = golden("torch_scaler.npz")
+
+    def run(steps, inf_steps, interval, tracker0=0):
+        st = O.OracleStore([4], mode=O.MODE_MIXED)
+        st.configure_scaler(True, 65536.0, 2.0, 0.5, interval)
+        if tracker0:
+            st.set_scaler_state(65536.0, tracker0)
+        scales, trackers, skipped = [], [], []
+        for s in range(1, steps + 1):
+            g = np.ones(4, np.float32) * st.scale
+            if s in inf_steps:
+                g[1] = np.inf
+            st.set_grad(0, O.bf16_rne(g))
+            r = st.sgd_step(lr=1e-3)
+            scales.append(r["scale"])
+            trackers.append(r["growth_tracker"])
+            skipped.append(r["skipped"])
+        return np.array(scales), np.array(trackers), np.array(skipped)
+
+    s, t, k = run(200, {50, 100, 150, 200}, 2000)
+    assert np.array_equal(s, d["cfg3_scale"]) and np.array_equal(t, d["cfg3_tracker"])
+    assert np.array_equal(k, d["cfg3_skipped"])
+    # closed form of the config-3 schedule: skips at 50/100/150/200, 65536 -> 4096
+    assert list(np.nonzero(k)[0] + 1) == [50, 100, 150, 200] and s[-1] == 4096.0
+    s, t, k = run(14, set(d["short_inf"].tolist()), 3)
+    assert np.array_equal(s, d["short_scale"]) and np.array_equal(t, d["short_tracker"])
+    assert np.array_equal(k, d["short_skipped"])
+    s, t, _ = run(3, set(), 2000, tracker0=1999)
+    assert np.array_equal(s, d["forced_scale"]) and np.array_equal(t, d["forced_tracker"])
+
+
+@pytest.mark.parametrize("case", ["big", "small", "mid"])
+def test_clip_matches_torch(case):
+    d = golden("torch_clip.npz")
+    g = d[f"{case}_grads"]
+    st = O.OracleStore([g.size])
+    st.set_grad(0, g)
+    sumsq, bad = st.grad_sumsq()
+    norm = math.sqrt(sumsq)
+    assert not bad
+    assert abs(norm - float(d[f"{case}_fsum_norm"])) <= 1e-12 * norm
+    assert abs(norm - float(d[f"{case}_norm"])) <= 1e-5 * norm  # torch norms in fp32
+    coef = O.lib().orc_clip_coef(norm, float(d[f"{case}_max"]))
+    clipped = (g * np.float32(coef)).astype(np.float32)
+    assert f32_ulp_diff(clipped, d[f"{case}_clipped"]).max() <= 2
+    if case == "small":
+        assert coef == 1.0
+
+
+# ---------------------------------------------------------------------------- invariants
+def _random_store(rng, mode, numels=(257, 64, 1000, 3), decay=(1, 0, 1, 0)):
+    st = O.OracleStore(list(numels), flags=list(decay), mode=mode)
+    for i, n in enumerate(numels):
+        st.set_master(i, rng.normal(0, 0.5, n).astype(np.float32))
+    return st
+
+
+def _set_random_grads(st, rng, scale=1.0):
+    for i, n in enumerate(st.numels):
+        g = (rng.normal(0, 1e-2, n) * scale).astype(np.float32)
+        st.set_grad(i, g if st.mode == O.MODE_FP32 else O.bf16_rne(g))
+
+
+@pytest.mark.parametrize("mode", [O.MODE_FP32, O.MODE_MIXED])
+def test_opbyop_equals_fused_bitwise(rng, mode):
+    a = _random_store(np.random.default_rng(5), mode)
+    b = _random_store(np.random.default_rng(5), mode)
+    for st in (a, b):
+        st.configure_scaler(True, 1024.0)
+    for s in range(4):
+        r1 = np.random.default_rng(100 + s)
+        r2 = np.random.default_rng(100 + s)
+        _set_random_grads(a, r1, 1024.0)
+        _set_random_grads(b, r2, 1024.0)
+        hp = dict(lr=1e-2, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=0.05)
+        a.adam_step(**hp)
+        b.adam_step(opbyop=True, **hp)
+    for k in ("master", "exp_avg", "exp_avg_sq", "param"):
+        assert np.array_equal(getattr(a, k), getattr(b, k)), k
+
+
+def test_adamw_wd0_is_adam_bitwise(rng):
+    a = _random_store(np.random.default_rng(9), O.MODE_FP32, decay=(0, 0, 0, 0))
+    b = _random_store(np.random.default_rng(9), O.MODE_FP32, decay=(1, 1, 1, 1))
+    for s in range(3):
+        _set_random_grads(a, np.random.default_rng(s))
+        _set_random_grads(b, np.random.default_rng(s))
+        a.adam_step(lr=1e-3)
+        b.adam_step(lr=1e-3, weight_decay=0.0)
+    assert np.array_equal(a.master, b.master)
+
+
+def test_sgd_momentum0_is_plain_sgd(rng):
+    a = _random_store(np.random.default_rng(3), O.MODE_FP32)
+    p0 = a.master.copy()
+    _set_random_grads(a, np.random.default_rng(4))
+    g = a.grad.copy()
+    a.sgd_step(lr=0.05)
+    expect = (p0 - (g * np.float32(0.05))).astype(np.float32)
+    assert np.array_equal(a.master, expect)
+
+
+def test_mixed_param_is_rne_of_master(rng):
+    st = _random_store(rng, O.MODE_MIXED)
+    for s in range(3):
+        _set_random_grads(st, rng)
+        st.adam_step(lr=1e-2, weight_decay=0.1)
+    for i in range(st.n):
+        assert np.array_equal(st.view("param", i), O.bf16_rne(st.view("master", i)))
+
+
+def test_skipped_step_leaves_state_bit_unchanged(rng):
+    st = _random_store(rng, O.MODE_MIXED)
+    st.configure_scaler(True, 65536.0)
+    _set_random_grads(st, rng, 65536.0)
+    st.adam_step(lr=1e-3, weight_decay=0.1, max_grad_norm=1.0)
+    snap = {k: getattr(st, k).copy() for k in ("master", "param", "exp_avg", "exp_avg_sq")}
+    t0 = st.t
+    _set_random_grads(st, rng, 65536.0)
+    st.view("grad", 2)[17] = 0x7F80  # +inf in bf16
+    r = st.adam_step(lr=1e-3, weight_decay=0.1, max_grad_norm=1.0)
+    assert r["found_inf"] and r["skipped"] and st.t == t0 and st.scale == 32768.0
+    for k, v in snap.items():
+        assert np.array_equal(getattr(st, k), v), k
+
+
+def test_none_grad_tensor_untouched(rng):
+    # py/optim.py:56-57 / autograd/dynamic/optim.hpp:23: params without grad are skipped
+    st = _random_store(rng, O.MODE_FP32)
+    _set_random_grads(st, rng)
+    st.set_has_grad(1, False)
+    before = st.view("master", 1).copy()
+    st.adam_step(lr=1e-2, weight_decay=0.5)
+    assert np.array_equal(st.view("master", 1), before)
+    assert not st.view("exp_avg", 1).any()
+    st.zero_grad()
+    assert not any(st.has_grad(i) for i in range(st.n))
+
+
+def test_norm_brute_force_and_scaling(rng):
+    g = rng.normal(0, 1, 37).astype(np.float32)
+    st = O.OracleStore([37])
+    st.set_grad(0, g)
+    s1, _ = st.grad_sumsq()
+    assert s1 == pytest.approx(math.fsum(float(x) ** 2 for x in g), rel=1e-15)
+    s2, _ = st.grad_sumsq(inv_scale=0.25)  # power of two: exact scaling of every square
+    assert s2 == s1 / 16
+    for bad in (np.inf, -np.inf, np.nan):
+        h = g.copy()
+        h[5] = bad
+        st.set_grad(0, h)
+        assert st.grad_sumsq()[1]
+    h = g.copy()
+    h[5] = 3e38  # huge but finite: no overflow flag
+    st.set_grad(0, h)
+    assert not st.grad_sumsq()[1]
+
+
+def test_bias_correction_host_double():
+    # py/optim.py:51-52 in host double, rounded once to fp32
+    for beta in (0.9, 0.95, 0.999):
+        for t in (1, 2, 7, 100, 5000):
+            assert O.lib().orc_bias_correction(beta, t) == np.float32(1.0 - beta ** t)
+
+
+def test_validation_rejects_reference_cases():
+    # tests/adam_optimizer.py:126-151 and tests/sgd_optimizer.py:112-122
+    st = O.OracleStore([4])
+    st.set_grad(0, np.ones(4, np.float32))
+    for hp in (dict(lr=0.0), dict(lr=-1.0), dict(eps=0.0), dict(betas=(1.1, 0.9)),
+               dict(betas=(0.9, 0.0))):
+        with pytest.raises(ValueError):
+            st.adam_step(**hp)
+    for lr in (0.0, -1.0):
+        with pytest.raises(ValueError):
+            st.sgd_step(lr=lr)
