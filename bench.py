@@ -1,0 +1,236 @@
+"""Benchmark of the fused optimizer step: `python bench.py [--gpus 1] [--steps K] [--warmup W]`.
+
+Workload (BASELINE.json metric, configs[2]): GPT-2 124M mixed precision — 148 tensors,
+124,439,808 params, bf16 params/grads, fp32 master/m/v, dynamic loss scaling (2^16),
+global-norm clip 1.0, AdamW lr 6e-4 betas (0.9, 0.95) wd 0.1 on the 2-D tensors.
+One step = the norm/inf-check/scaler pass + the fused multi-tensor AdamW pass over
+synthetic N(0, 1e-3) x scale bf16 gradients already resident in HBM.
+
+Prints ONE JSON line: Gparams/s, ms/step, the roofline of the dominant (update) kernel
+from HIP events recorded on the kernel's stream during the timed region, and the CPU
+oracle baseline timed on this host's cores on a bounded sample.
+"""
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "tt-perf_amd"))
+
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
+# algorithmic bytes per parameter of one update-kernel pass (and of the norm pass)
+UPDATE_BYTES = {("adamw", "mixed"): 28, ("adamw", "fp32"): 28, ("sgdm", "fp32"): 20,
+                ("sgdm", "mixed"): 20}
+NORM_BYTES = {"mixed": 2, "fp32": 4}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="gpt2_124m")
+    ap.add_argument("--optimizer", default="adamw", choices=["adamw", "sgdm"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+def traffic_from_profiles(config):
+    """HBM bytes per update launch from the committed rocprofv3 --pmc summary, if any."""
+    path = os.path.join(REPO, "profiles", f"pmc_update_{config}.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(numels, flags, mode_mixed, grads_host, hp, seconds):
+    """The CPU oracle (C restatement of the reference's optimizer) on this host's cores."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import numpy as np
+    import oracle as O
+    nthreads = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
+    st = O.OracleStore(numels, flags=flags, mode=O.MODE_MIXED if mode_mixed else O.MODE_FP32,
+                       nthreads=nthreads)
+    st.configure_scaler(True, 65536.0)
+    rng = np.random.default_rng(0)
+    st.master[:] = rng.normal(0, 0.02, st.total).astype(np.float32)
+    st.grad[:] = grads_host
+    for i in range(st.n):
+        st.set_has_grad(i, True)
+    res = {}
+    for label, kw, nt in (("fused", {}, nthreads), ("opbyop", {"opbyop": True}, nthreads)):
+        st.s.nthreads = nt
+        st.adam_step(**hp, **kw)  # warm
+        t0 = time.perf_counter()
+        n = 0
+        while True:
+            st.adam_step(**hp, **kw)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds or n >= 200:
+                break
+        res[label] = (n, el)
+    n, el = res["fused"]
+    total = sum(numels)
+    out = {"value": round(total * n / el / 1e9, 4), "unit": "Gparams/s", "cores": nthreads,
+           "kind": "port",
+           "sample": f"full {len(numels)}-tensor table ({total} params), {n} fused steps "
+                     f"(scaler + clip + AdamW) in {el:.1f} s on {nthreads} threads",
+           "ms_per_step": round(el / n * 1e3, 3)}
+    n2, el2 = res["opbyop"]
+    out["opbyop_value"] = round(total * n2 / el2 / 1e9, 4)
+    out["opbyop_sample"] = (f"{n2} steps executing py/optim.py's ops as separate full passes, "
+                            f"{el2:.1f} s on {nthreads} threads")
+    return out
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py: this engine runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the multi-GPU sharding is a design note, not a measured path)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import ttperf
+    from ttperf import _lib as L
+    from ttperf import configs
+
+    names, shapes, decay, numels = configs.table(args.config)
+    mode = configs.CONFIGS[args.config]["mode"]
+    n_params = sum(numels)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    store = ttperf.ParamStore(shapes, mode=mode, decay=decay, names=names)
+    stream = torch.cuda.current_stream()
+    store.set_stream(stream)
+
+    gen = torch.Generator(device=dev).manual_seed(1234)
+    w = torch.randn(store.total, generator=gen, device=dev) * 0.02
+    store.upload(L.BUF_MASTER, L.ALL_TENSORS, w)
+    del w
+    scale = 65536.0
+    store.configure_scaler(True, init_scale=scale)
+    g = torch.randn(store.total, generator=gen, device=dev) * 1e-3 * scale
+    g = g.to(torch.bfloat16) if mode == "mixed" else g
+    store.upload(L.BUF_GRAD, L.ALL_TENSORS, g)
+    grads_host = (g.cpu().view(torch.int16).numpy().view(np.uint16) if mode == "mixed"
+                  else g.cpu().numpy())
+    del g
+
+    hp = dict(lr=6e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
+
+    def step():
+        if args.optimizer == "adamw":
+            store.adam_step(**hp)
+        else:
+            store.sgd_step(lr=1e-3, momentum=0.9, weight_decay=0.1, max_grad_norm=1.0)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    r = store.adam_step(report=True, **hp) if args.optimizer == "adamw" else None
+    if r is not None:
+        assert not r["skipped"], r
+
+    store.timing(True)
+    store.timing_collect(L.KERNEL_NORM)
+    store.timing_collect(L.KERNEL_UPDATE)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    total_ms = e0.elapsed_time(e1)
+    upd_ms, upd_n = store.timing_collect(L.KERNEL_UPDATE)
+    nrm_ms, nrm_n = store.timing_collect(L.KERNEL_NORM)
+    store.timing(False)
+    ms_step = total_ms / args.steps
+    upd_avg = upd_ms / max(upd_n, 1)
+    nrm_avg = nrm_ms / max(nrm_n, 1)
+
+    # a skipped (overflow) step: only the norm pass does work
+    skip_ms = None
+    if args.optimizer == "adamw":
+        store.upload(L.BUF_GRAD, 0, torch.full((store.tensors[0].numel,), float("inf"),
+                                               device=dev, dtype=torch.bfloat16 if mode == "mixed"
+                                               else torch.float32))
+        torch.cuda.synchronize()
+        e0.record(stream)
+        rs = store.adam_step(report=False, **hp)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        skip_ms = e0.elapsed_time(e1)
+        assert rs is None
+
+    # practical ceiling: a plain device copy of the update's byte count
+    ub = UPDATE_BYTES[(args.optimizer, mode)]
+    nb = NORM_BYTES[mode]
+    copy_bytes = n_params * ub // 2
+    src = torch.empty(copy_bytes // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(10):
+        dst.copy_(src)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    copy_gbps = 2 * copy_bytes * 10 / (e0.elapsed_time(e1) / 1e3) / 1e9
+    del src, dst
+
+    achieved = n_params * ub / (upd_avg / 1e3) / 1e9
+    step_gbps = n_params * (ub + nb) / (ms_step / 1e3) / 1e9
+    out = {
+        "metric": "fused AdamW step Gparams/s + % of HBM peak, GPT-2 124M mixed precision",
+        "value": round(n_params / (ms_step / 1e3) / 1e9, 3),
+        "unit": "Gparams/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded N(0,1e-3) x loss-scale bf16 grads, N(0,0.02) fp32 master)",
+        "config": {"workload": f"{args.config} {args.optimizer} step: {len(numels)} tensors, "
+                               f"{n_params} params, {mode} precision, loss scaling 2^16, "
+                               f"clip 1.0, lr 6e-4, betas (0.9,0.95), wd 0.1 on 2-D tensors",
+                   "params": n_params, "tensors": len(numels), "mode": mode,
+                   "bytes_per_param": ub + nb},
+        "step_hbm_GBps": round(step_gbps, 1),
+        "step_hbm_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
+        "kernels_ms": {"norm": round(nrm_avg, 4), "update": round(upd_avg, 4)},
+        "skipped_step_ms": round(skip_ms, 4) if skip_ms is not None else None,
+        "copy_ceiling_GBps": round(copy_gbps, 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic_from_profiles(args.config),
+                     "kernel": "adam_kernel<bf16,mixed>" if mode == "mixed" else "adam_kernel<f32>",
+                     "algorithmic_bytes_per_launch": n_params * ub},
+        "cpu_baseline": None,
+    }
+    store.close()
+    if not args.no_cpu_baseline and args.optimizer == "adamw":
+        log("bench: timing the CPU oracle baseline ...")
+        out["cpu_baseline"] = cpu_baseline(numels, [1 if d else 0 for d in decay],
+                                           mode == "mixed", grads_host, hp, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

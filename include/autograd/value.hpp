@@ -1,0 +1,137 @@
+// value.hpp — parameters of the drop-in autograd API, stored in one flat HBM store.
+//
+// The reference's autograd::Value owns its `data` tensor and an optional `grad`
+// (autograd/dynamic/autograd.hpp:38-84); static_autograd::Value points at external
+// buffers (autograd/static/value.hpp:27-48).  Here every parameter is a non-owning view
+// (arena, index) into a ttp::Store that holds all parameters of a model contiguously, so an
+// optimizer step over all of them is one launch.  Parameters are declared on a ParamArena;
+// the store is created on first use, after which the parameter set is fixed.
+#pragma once
+
+#include <cstdint>
+#include <memory>
+#include <optional>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "ttperf/ttperf.hpp"
+
+namespace autograd {
+
+class ParamArena;
+
+struct ArenaState {
+    ttp::Mode mode = ttp::Mode::FP32;
+    int device = 0;
+    std::vector<ttp::TensorSpec> specs;
+    std::vector<std::vector<float>> init;  // initial fp32 weights (uploaded at creation)
+    std::vector<bool> grad_always;         // pre-allocated grads (traced/static layers)
+    std::unique_ptr<ttp::Store> store;
+
+    ttp::Store& get() {
+        if (!store) {
+            store = std::make_unique<ttp::Store>(specs, mode, device);
+            for (uint32_t i = 0; i < specs.size(); ++i) {
+                if (!init[i].empty()) store->set_weights(i, init[i]);
+                if (grad_always[i]) store->set_has_grad(i, true);
+            }
+            init.clear();
+            init.shrink_to_fit();
+        }
+        return *store;
+    }
+};
+
+struct Value;
+using ValuePtr = std::shared_ptr<Value>;
+
+// `grad` of a parameter: empty (std::nullopt, py `None`) or a tensor in the store's grad
+// buffer.  Same surface as std::optional<Tensor> for what the optimizers use.
+class GradSlot {
+public:
+    GradSlot(std::shared_ptr<ArenaState> a, uint32_t i) : a_(std::move(a)), i_(i) {}
+    bool has_value() const { return a_->get().has_grad(i_); }
+    explicit operator bool() const { return has_value(); }
+    std::vector<float> value() const {
+        if (!has_value()) throw std::runtime_error("grad has no value");
+        return a_->get().grad(i_);
+    }
+    GradSlot& operator=(std::nullopt_t) {
+        a_->get().set_has_grad(i_, false);
+        return *this;
+    }
+    GradSlot& operator=(const std::vector<float>& g) {
+        a_->get().set_grad(i_, g);
+        return *this;
+    }
+
+private:
+    std::shared_ptr<ArenaState> a_;
+    uint32_t i_;
+};
+
+struct Value {
+    std::shared_ptr<ArenaState> arena;
+    uint32_t index;
+    GradSlot grad;
+    bool requires_grad = true;
+    std::string name;
+
+    Value(std::shared_ptr<ArenaState> a, uint32_t i, std::string n)
+        : arena(a), index(i), grad(a, i), name(std::move(n)) {}
+
+    const std::vector<uint64_t>& shape() const { return arena->specs[index].shape; }
+    uint64_t numel() const { return arena->specs[index].numel(); }
+    ttp::Store& store() const { return arena->get(); }
+    std::vector<float> data() const { return store().weights(index); }
+    std::vector<float> master() const { return store().master(index); }
+    void set_data(const std::vector<float>& w) { store().set_weights(index, w); }
+
+    // autograd/dynamic/autograd.hpp:78-83: grad = grad + incoming, or the first assignment
+    void accumulate_grad(const std::vector<float>& incoming) {
+        if (!requires_grad) return;
+        if (!grad.has_value()) {
+            grad = incoming;
+            return;
+        }
+        std::vector<float> g = grad.value();
+        if (g.size() != incoming.size()) throw std::invalid_argument("grad shape mismatch");
+        for (size_t k = 0; k < g.size(); ++k) g[k] = g[k] + incoming[k];
+        grad = g;
+    }
+};
+
+// Declares parameters; all of them live in one store created on first use.
+class ParamArena {
+public:
+    explicit ParamArena(ttp::Mode mode = ttp::Mode::FP32, int device = 0)
+        : s_(std::make_shared<ArenaState>()) {
+        s_->mode = mode;
+        s_->device = device;
+    }
+
+    ValuePtr parameter(std::vector<uint64_t> shape, std::vector<float> init = {},
+                       std::string name = "", bool decay = false, bool grad_always = false) {
+        if (s_->store) throw std::logic_error("parameters must be declared before first use");
+        ttp::TensorSpec spec{std::move(shape), decay, name};
+        if (!init.empty() && init.size() != spec.numel())
+            throw std::invalid_argument("initial value has the wrong size");
+        const uint32_t idx = (uint32_t)s_->specs.size();
+        s_->specs.push_back(spec);
+        s_->init.push_back(std::move(init));
+        s_->grad_always.push_back(grad_always);
+        return std::make_shared<Value>(s_, idx, name);
+    }
+
+    ttp::Store& store() { return s_->get(); }
+    const std::shared_ptr<ArenaState>& state() const { return s_; }
+    size_t size() const { return s_->specs.size(); }
+
+private:
+    std::shared_ptr<ArenaState> s_;
+};
+
+inline std::vector<float> filled(uint64_t n, float v) { return std::vector<float>(n, v); }
+
+}  // namespace autograd

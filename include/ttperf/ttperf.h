@@ -135,8 +135,11 @@ int ttp_device_count(int* count);
 int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n_tensors, int mode,
                ttp_ctx** out);
 int ttp_destroy(ttp_ctx* ctx);
-/* Use an existing HIP stream (hipStream_t passed as void*); NULL = the context's own. */
+/* Order all further work on an existing HIP stream (hipStream_t passed as void*; NULL is
+ * the legacy default stream, e.g. torch's default stream).  Waits for work already queued. */
 int ttp_set_stream(ttp_ctx* ctx, void* hip_stream);
+/* Back to the context's own (non-blocking) stream. */
+int ttp_reset_stream(ttp_ctx* ctx);
 int ttp_sync(ttp_ctx* ctx);
 
 /* ---- layout ------------------------------------------------------------------------- */
@@ -172,6 +175,16 @@ int ttp_zero_grad(ttp_ctx* ctx, int set_to_none);
 /* ---- optimizer steps ------------------------------------------------------------------ */
 int ttp_adam_step(ttp_ctx* ctx, const ttp_adam_hparams* hp, ttp_step_report* report);
 int ttp_sgd_step(ttp_ctx* ctx, const ttp_sgd_hparams* hp, ttp_step_report* report);
+/* The same steps restricted to the listed tensors (each index at most once): what one
+ * module's sgd_step(lr) touches (autograd/traced/nn.hpp:93-96,272-275,317-321,
+ * autograd/static/nn.hpp:92-95) or one optimizer's parameter list (py/optim.py:7,31).
+ * Tensors outside the list, or without a grad, are not touched; the grad norm used for
+ * clipping and the inf check cover the listed tensors only.  The step count and loss
+ * scale are per context. */
+int ttp_adam_step_subset(ttp_ctx* ctx, const ttp_adam_hparams* hp, const uint32_t* indices,
+                         uint32_t n_indices, ttp_step_report* report);
+int ttp_sgd_step_subset(ttp_ctx* ctx, const ttp_sgd_hparams* hp, const uint32_t* indices,
+                        uint32_t n_indices, ttp_step_report* report);
 /* Global L2 norm of the gradients that exist, unscaled by the current loss scale when
  * scaling is on (synchronous; does not change any state). */
 int ttp_grad_norm(ttp_ctx* ctx, double* norm);

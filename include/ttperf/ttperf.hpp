@@ -1,0 +1,221 @@
+// ttperf.hpp — header-only C++ owner of a libttperf_hip context (include/ttperf/ttperf.h).
+//
+// ttp::Store is one flat parameter store on one GPU.  Errors from the C ABI become
+// exceptions here (std::invalid_argument for the argument errors py/optim.py raises
+// ValueError for, std::out_of_range for bad indices/sizes, std::runtime_error otherwise),
+// the way TTNN errors surface as std::exception in the reference
+// (bench/autograd/bench_gpt2_full.cpp:153-165).
+#pragma once
+
+#include <cstdint>
+#include <cstring>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "ttperf/ttperf.h"
+
+namespace ttp {
+
+inline void check(int rc) {
+    if (rc == TTP_OK) return;
+    std::string msg = std::string("libttperf_hip: ") + ttp_last_error();
+    if (rc == TTP_ERR_INVALID) throw std::invalid_argument(msg);
+    if (rc == TTP_ERR_RANGE) throw std::out_of_range(msg);
+    throw std::runtime_error(msg);
+}
+
+enum class Mode { FP32 = TTP_MODE_FP32, Mixed = TTP_MODE_MIXED };
+
+struct TensorSpec {
+    std::vector<uint64_t> shape;
+    bool decay = false;
+    std::string name;
+    uint64_t numel() const {
+        uint64_t n = 1;
+        for (auto d : shape) n *= d;
+        return n;
+    }
+};
+
+struct AdamOptions {
+    double lr = 1e-3, beta1 = 0.9, beta2 = 0.999, eps = 1e-8, weight_decay = 0.0;
+    bool decoupled = true;
+    double max_grad_norm = 0.0;
+    ttp_adam_hparams c() const {
+        ttp_adam_hparams h{};
+        h.lr = lr;
+        h.beta1 = beta1;
+        h.beta2 = beta2;
+        h.eps = eps;
+        h.weight_decay = weight_decay;
+        h.decoupled = decoupled ? 1 : 0;
+        h.max_grad_norm = max_grad_norm;
+        return h;
+    }
+};
+
+struct SgdOptions {
+    double lr = 1e-2, momentum = 0.0, dampening = 0.0, weight_decay = 0.0;
+    bool nesterov = false;
+    double max_grad_norm = 0.0;
+    ttp_sgd_hparams c() const {
+        ttp_sgd_hparams h{};
+        h.lr = lr;
+        h.momentum = momentum;
+        h.dampening = dampening;
+        h.weight_decay = weight_decay;
+        h.nesterov = nesterov ? 1 : 0;
+        h.max_grad_norm = max_grad_norm;
+        return h;
+    }
+};
+
+class Store {
+public:
+    Store(const std::vector<TensorSpec>& specs, Mode mode, int device = 0) : specs_(specs), mode_(mode) {
+        std::vector<ttp_tensor_desc> d(specs.size());
+        for (size_t i = 0; i < specs.size(); ++i) {
+            d[i].numel = specs[i].numel();
+            d[i].flags = specs[i].decay ? TTP_TENSOR_DECAY : 0u;
+            d[i].reserved = 0;
+        }
+        ttp_ctx* c = nullptr;
+        check(ttp_create(device, d.data(), (uint32_t)d.size(), (int)mode, &c));
+        ctx_ = c;
+    }
+    ~Store() {
+        if (ctx_) ttp_destroy(ctx_);
+    }
+    Store(const Store&) = delete;
+    Store& operator=(const Store&) = delete;
+
+    ttp_ctx* get() const { return ctx_; }
+    Mode mode() const { return mode_; }
+    size_t size() const { return specs_.size(); }
+    const TensorSpec& spec(uint32_t i) const { return specs_.at(i); }
+    uint64_t numel(uint32_t i) const { return specs_.at(i).numel(); }
+
+    // ---- data -------------------------------------------------------------------------------
+    // fp32 weights of tensor i: the master copy (and its bf16 RNE copy in Mixed mode)
+    void set_weights(uint32_t i, const std::vector<float>& w) {
+        check(ttp_upload(ctx_, TTP_BUF_MASTER, i, w.data(), w.size(), TTP_HOST));
+    }
+    std::vector<float> master(uint32_t i) const { return download_f32(TTP_BUF_MASTER, i); }
+    // model-facing weights widened to float (bf16 in Mixed mode)
+    std::vector<float> weights(uint32_t i) const {
+        if (mode_ == Mode::FP32) return download_f32(TTP_BUF_PARAM, i);
+        return widen(download_u16(TTP_BUF_PARAM, i));
+    }
+    std::vector<uint16_t> weights_bf16(uint32_t i) const { return download_u16(TTP_BUF_PARAM, i); }
+    std::vector<float> state(int which, uint32_t i) const { return download_f32(which, i); }
+
+    // gradients: fp32 values (rounded to bf16 in Mixed mode, round-to-nearest-even)
+    void set_grad(uint32_t i, const std::vector<float>& g) {
+        if (mode_ == Mode::FP32) {
+            check(ttp_upload(ctx_, TTP_BUF_GRAD, i, g.data(), g.size(), TTP_HOST));
+        } else {
+            std::vector<uint16_t> h(g.size());
+            for (size_t k = 0; k < g.size(); ++k) h[k] = to_bf16(g[k]);
+            check(ttp_upload(ctx_, TTP_BUF_GRAD, i, h.data(), h.size(), TTP_HOST));
+        }
+    }
+    std::vector<float> grad(uint32_t i) const {
+        if (mode_ == Mode::FP32) return download_f32(TTP_BUF_GRAD, i);
+        return widen(download_u16(TTP_BUF_GRAD, i));
+    }
+    bool has_grad(uint32_t i) const {
+        int h = 0;
+        check(ttp_get_has_grad(ctx_, i, &h));
+        return h != 0;
+    }
+    void set_has_grad(uint32_t i, bool h) { check(ttp_set_has_grad(ctx_, i, h ? 1 : 0)); }
+    void zero_grad(bool set_to_none = true) { check(ttp_zero_grad(ctx_, set_to_none ? 1 : 0)); }
+    void* device_ptr(int which, uint32_t i = TTP_ALL_TENSORS) {
+        void* p = nullptr;
+        check(ttp_buffer_ptr(ctx_, which, i, &p));
+        return p;
+    }
+
+    // ---- steps --------------------------------------------------------------------------------
+    ttp_step_report adam_step(const AdamOptions& o, const std::vector<uint32_t>* subset = nullptr,
+                              bool want_report = false) {
+        ttp_adam_hparams h = o.c();
+        ttp_step_report r{};
+        ttp_step_report* rp = want_report ? &r : nullptr;
+        if (subset)
+            check(ttp_adam_step_subset(ctx_, &h, subset->data(), (uint32_t)subset->size(), rp));
+        else
+            check(ttp_adam_step(ctx_, &h, rp));
+        return r;
+    }
+    ttp_step_report sgd_step(const SgdOptions& o, const std::vector<uint32_t>* subset = nullptr,
+                             bool want_report = false) {
+        ttp_sgd_hparams h = o.c();
+        ttp_step_report r{};
+        ttp_step_report* rp = want_report ? &r : nullptr;
+        if (subset)
+            check(ttp_sgd_step_subset(ctx_, &h, subset->data(), (uint32_t)subset->size(), rp));
+        else
+            check(ttp_sgd_step(ctx_, &h, rp));
+        return r;
+    }
+    double grad_norm() {
+        double n = 0;
+        check(ttp_grad_norm(ctx_, &n));
+        return n;
+    }
+    void configure_scaler(double init_scale = 65536.0, double growth = 2.0, double backoff = 0.5,
+                          int interval = 2000, bool enabled = true) {
+        ttp_scaler_config c{enabled ? 1 : 0, interval, init_scale, growth, backoff};
+        check(ttp_scaler_configure(ctx_, &c));
+    }
+    std::pair<float, int32_t> scaler_state() {
+        float s = 0;
+        int32_t t = 0;
+        check(ttp_scaler_get(ctx_, &s, &t));
+        return {s, t};
+    }
+    uint64_t step_count() {
+        uint64_t t = 0;
+        check(ttp_get_step(ctx_, &t));
+        return t;
+    }
+    void sync() { check(ttp_sync(ctx_)); }
+
+    static uint16_t to_bf16(float x) {
+        uint32_t u;
+        std::memcpy(&u, &x, 4);
+        if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+        u += 0x7FFFu + ((u >> 16) & 1u);
+        return (uint16_t)(u >> 16);
+    }
+
+private:
+    static std::vector<float> widen(const std::vector<uint16_t>& h) {
+        std::vector<float> f(h.size());
+        for (size_t k = 0; k < h.size(); ++k) {
+            uint32_t u = (uint32_t)h[k] << 16;
+            std::memcpy(&f[k], &u, 4);
+        }
+        return f;
+    }
+    std::vector<float> download_f32(int which, uint32_t i) const {
+        std::vector<float> v(numel(i));
+        check(ttp_download(ctx_, which, i, v.data(), v.size(), TTP_HOST));
+        return v;
+    }
+    std::vector<uint16_t> download_u16(int which, uint32_t i) const {
+        std::vector<uint16_t> v(numel(i));
+        check(ttp_download(ctx_, which, i, v.data(), v.size(), TTP_HOST));
+        return v;
+    }
+
+    std::vector<TensorSpec> specs_;
+    Mode mode_;
+    ttp_ctx* ctx_ = nullptr;
+};
+
+}  // namespace ttp

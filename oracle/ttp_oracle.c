@@ -268,8 +268,9 @@ static void step_epilogue(orc_store* s, int found_inf, orc_report* rep) {
         orc_scaler_update(&s->scale, &s->growth_tracker, found_inf, s->growth_factor,
                           s->backoff_factor, s->growth_interval);
     if (rep) {
-        rep->scale = s->scale;
-        rep->growth_tracker = s->growth_tracker;
+        /* without loss scaling the report carries scale 1 and tracker 0 */
+        rep->scale = s->scaler_enabled ? s->scale : 1.0f;
+        rep->growth_tracker = s->scaler_enabled ? s->growth_tracker : 0;
         rep->step = s->t;
     }
 }

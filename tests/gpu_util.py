@@ -1,0 +1,106 @@
+"""Helpers of the GPU parity tests: a libttperf_hip store and an oracle store with the same
+layout and the same seeded inputs, gradients generated on the device by torch and copied to
+the host for the oracle, and bit-level comparisons."""
+import os
+import sys
+
+import numpy as np
+
+import oracle as O
+from conftest import REPO, f32_ulp_diff
+
+sys.path.insert(0, os.path.join(REPO, "tt-perf_amd"))
+
+LONG = os.environ.get("TTP_LONG_TESTS", "0") == "1"
+
+
+def torch_mod():
+    import torch
+    return torch
+
+
+def make_pair(shapes, decay, mode, init_std=0.02, seed=0, init="normal"):
+    """GPU store + oracle store holding identical fp32 master weights."""
+    import ttperf
+    from ttperf import _lib as L
+    torch = torch_mod()
+    store = ttperf.ParamStore(shapes, mode="mixed" if mode == O.MODE_MIXED else "fp32",
+                              decay=decay)
+    store.set_stream(torch.cuda.current_stream())
+    numels = [t.numel for t in store.tensors]
+    ref = O.OracleStore(numels, flags=[1 if d else 0 for d in decay], mode=mode,
+                        nthreads=min(16, os.cpu_count() or 1))
+    assert [int(o) for o in ref.offsets] == list(store.offsets)
+    assert ref.total == store.total
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    flat = torch.zeros(store.total, dtype=torch.float32, device="cuda")
+    for i, (t, s) in enumerate(zip(store.tensors, shapes)):
+        o = store.offsets[i]
+        if init == "uniform":  # U(-1/sqrt(fan_in), 1/sqrt(fan_in)), fan_in = first dim
+            b = 1.0 / np.sqrt(s[0])
+            flat[o:o + t.numel].uniform_(-b, b, generator=g)
+        elif len(s) >= 2:
+            flat[o:o + t.numel].normal_(0.0, init_std, generator=g)
+        elif "ln" in t.name and t.name.endswith("weight"):
+            flat[o:o + t.numel].fill_(1.0)
+        else:
+            flat[o:o + t.numel].normal_(0.0, init_std, generator=g)
+    store.upload(L.BUF_MASTER, L.ALL_TENSORS, flat)
+    ref.master[:] = flat.cpu().numpy()
+    if mode == O.MODE_MIXED:
+        ref.param[:] = O.bf16_rne(ref.master)
+    return store, ref
+
+
+def pad_mask(store):
+    m = np.zeros(store.total, dtype=bool)
+    for i, t in enumerate(store.tensors):
+        m[store.offsets[i]:store.offsets[i] + t.numel] = True
+    return m
+
+
+def device_grads(store, gen, std, scale=1.0, heavy_frac=0.0, heavy_std=1.0, inf_at=None):
+    """Seeded N(0, std) * scale grads on the device (bf16 in MIXED), written into the store;
+    returns the host copy (uint16 bits or float32) for the oracle."""
+    torch = torch_mod()
+    g = torch.randn(store.total, generator=gen, device="cuda", dtype=torch.float32) * std
+    if heavy_frac:
+        pick = torch.rand(store.total, generator=gen, device="cuda") < heavy_frac
+        g = torch.where(pick, torch.randn(store.total, generator=gen, device="cuda") * heavy_std, g)
+    if scale != 1.0:
+        g = g * scale
+    if inf_at is not None:
+        g[inf_at] = float("inf")
+    from ttperf import _lib as L
+    if store.mode == L.MODE_MIXED:
+        g = g.to(torch.bfloat16)
+    store.upload(L.BUF_GRAD, L.ALL_TENSORS, g)
+    host = g.cpu()
+    if store.mode == L.MODE_MIXED:
+        return host.view(torch.int16).numpy().view(np.uint16)
+    return host.numpy()
+
+
+def compare_state(store, ref, which=("master", "exp_avg", "exp_avg_sq", "param"), max_ulp=0,
+                  mask=None):
+    """Max ulp difference per buffer (padding excluded); asserts <= max_ulp, and bf16 params
+    bit-exact."""
+    from ttperf import _lib as L
+    bufs = {"master": L.BUF_MASTER, "exp_avg": L.BUF_EXP_AVG, "exp_avg_sq": L.BUF_EXP_AVG_SQ,
+            "param": L.BUF_PARAM, "momentum": L.BUF_MOMENTUM}
+    out = {}
+    if mask is None:
+        mask = pad_mask(store)
+    for name in which:
+        got = store.download(bufs[name])
+        want = getattr(ref, name)
+        if got.dtype == np.uint16:
+            bad = int(np.count_nonzero((got != want) & mask))
+            out[name] = bad
+            assert bad == 0, f"{name}: {bad} bf16 values differ"
+        else:
+            d = f32_ulp_diff(got[mask], want[mask])
+            out[name] = int(d.max()) if d.size else 0
+            assert out[name] <= max_ulp, f"{name}: max {out[name]} ulp (> {max_ulp}), " \
+                                         f"{int(np.count_nonzero(d))} values differ"
+    return out

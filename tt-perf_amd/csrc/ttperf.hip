@@ -1,0 +1,969 @@
+// ttperf.hip — host side of libttperf_hip: the C ABI declared in include/ttperf/ttperf.h.
+//
+// A context is one flat parameter store on one device plus the state of one optimizer:
+//   * layout: tensors in caller order, each starting on a 64-element boundary (256 B for
+//     fp32, 128 B for bf16), so every lane's 4-element vector stays inside one tensor's
+//     footprint; the padding is zero and never written by a step;
+//   * work table: chunks of <= chunk_elems elements of one tensor.  The table of all
+//     tensors is built once; a second table is built only while some tensor has no grad
+//     (py/optim.py:56-57 skip);
+//   * step: [norm pass when clipping or loss scaling] + one fused update pass, both on the
+//     context's stream, no host synchronisation (the skip decision and, with loss scaling,
+//     the step count live on the device).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "ttperf/ttperf.h"
+#include "kernels.hpp"
+
+using ttp::Chunk;
+using ttp::DevState;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                  \
+    do {                                                                               \
+        hipError_t e_ = (expr);                                                        \
+        if (e_ != hipSuccess)                                                          \
+            return fail(TTP_ERR_HIP, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+constexpr uint64_t kAlign = 64;  // elements
+
+uint64_t env_u64(const char* name, uint64_t dflt) {
+    const char* s = std::getenv(name);
+    if (!s || !*s) return dflt;
+    char* end = nullptr;
+    unsigned long long v = std::strtoull(s, &end, 10);
+    return (end && *end == 0) ? (uint64_t)v : dflt;
+}
+
+struct TensorRec {
+    uint64_t offset, numel;
+    uint32_t flags;
+    int has_grad;
+};
+
+struct EventPair {
+    hipEvent_t a, b;
+};
+
+}  // namespace
+
+struct ttp_ctx {
+    int device = 0;
+    int mode = TTP_MODE_FP32;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    int num_cus = 256;
+
+    std::vector<TensorRec> tensors;
+    uint64_t total = 0;
+
+    void* param = nullptr;  // bf16 (MIXED) or == master (FP32)
+    void* grad = nullptr;   // bf16 (MIXED) or fp32 (FP32)
+    float* master = nullptr;
+    float* exp_avg = nullptr;
+    float* exp_avg_sq = nullptr;
+    float* momentum = nullptr;
+    uint32_t* mom_init = nullptr;        // device, per tensor
+    std::vector<uint8_t> host_mom_init;  // host view (exact while loss scaling is off)
+
+    DevState* st = nullptr;
+    double* partials = nullptr;
+    uint32_t partials_cap = 0;
+
+    uint64_t chunk_elems = 16384;
+    uint32_t grid_cap = 0;       // 0: one block per chunk
+    uint32_t norm_grid_cap = 0;  // blocks of the norm pass
+
+    Chunk* chunks_all = nullptr;  // every non-empty tensor
+    uint32_t n_chunks_all = 0;
+    uint32_t n_nonempty = 0;
+    // tables of other active sets (a subset, or tensors without grad left out), keyed by
+    // the sorted active tensor indices
+    std::map<std::vector<uint32_t>, std::pair<Chunk*, uint32_t>> tables;
+
+    float* bias_tab = nullptr;
+    uint32_t bias_len = 0;
+    double bias_b1 = -1.0, bias_b2 = -1.0;
+
+    ttp_scaler_config scaler{0, 2000, 65536.0, 2.0, 0.5};
+    uint64_t host_t = 0;  // step count while loss scaling is off
+
+    bool timing = false;
+    std::vector<EventPair> ev[2];
+    std::vector<hipEvent_t> ev_pool;
+};
+
+namespace {
+
+size_t grad_esize(const ttp_ctx* c) { return c->mode == TTP_MODE_MIXED ? 2 : 4; }
+size_t param_esize(const ttp_ctx* c) { return c->mode == TTP_MODE_MIXED ? 2 : 4; }
+
+void append_chunks(const ttp_ctx* c, const std::vector<uint32_t>& which, std::vector<Chunk>& out) {
+    for (uint32_t i : which) {
+        const TensorRec& t = c->tensors[i];
+        if (!t.numel) continue;
+        for (uint64_t b = 0; b < t.numel; b += c->chunk_elems) {
+            Chunk ch;
+            ch.begin = t.offset + b;
+            ch.count = (uint32_t)std::min<uint64_t>(c->chunk_elems, t.numel - b);
+            ch.meta = (t.flags & TTP_TENSOR_DECAY ? ttp::kChunkDecay : 0u) | ((uint32_t)i << 8);
+            out.push_back(ch);
+        }
+    }
+}
+
+int zero_device(ttp_ctx* c, void* p, uint64_t bytes) {
+    // a fill kernel rather than a memset node, so the step sequence stays capturable
+    if (!bytes) return TTP_OK;
+    const uint64_t words = (bytes + 3) / 4;
+    const uint32_t grid = (uint32_t)std::min<uint64_t>((words + ttp::kBlock - 1) / ttp::kBlock,
+                                                       (uint64_t)c->num_cus * 16);
+    hipLaunchKernelGGL(ttp::fill_zero_kernel, dim3(grid), dim3(ttp::kBlock), 0, c->stream,
+                       (uint32_t*)p, words);
+    HIP_TRY(hipGetLastError());
+    return TTP_OK;
+}
+
+int alloc_zero(ttp_ctx* c, void** p, uint64_t bytes) {
+    // padded to whole 4-byte words for the fill kernel
+    HIP_TRY(hipMalloc(p, std::max<uint64_t>((bytes + 3) / 4 * 4, 4)));
+    return zero_device(c, *p, bytes);
+}
+
+int ensure_adam_state(ttp_ctx* c) {
+    // py/optim.py:58-71: m and v start as zeros on first use
+    int rc;
+    if (!c->exp_avg && (rc = alloc_zero(c, (void**)&c->exp_avg, c->total * 4))) return rc;
+    if (!c->exp_avg_sq && (rc = alloc_zero(c, (void**)&c->exp_avg_sq, c->total * 4))) return rc;
+    return TTP_OK;
+}
+
+int ensure_momentum(ttp_ctx* c) {
+    int rc;
+    if (!c->momentum && (rc = alloc_zero(c, (void**)&c->momentum, c->total * 4))) return rc;
+    return TTP_OK;
+}
+
+// Active set of a step: the listed tensors (all when `subset` is NULL) that have a grad
+// and at least one element; returns its device chunk table (built once per distinct set).
+int select_chunks(ttp_ctx* c, const uint32_t* subset, uint32_t nsub, const Chunk** chunks,
+                  uint32_t* n, std::vector<uint32_t>* active_out) {
+    const uint32_t nt = (uint32_t)c->tensors.size();
+    std::vector<uint32_t> active;
+    if (subset) {
+        std::vector<uint8_t> seen(nt, 0);
+        for (uint32_t k = 0; k < nsub; ++k) {
+            const uint32_t i = subset[k];
+            if (i >= nt) return fail(TTP_ERR_RANGE, "tensor index " + std::to_string(i) + " out of range");
+            if (seen[i]) return fail(TTP_ERR_INVALID, "tensor index " + std::to_string(i) + " listed twice");
+            seen[i] = 1;
+        }
+        for (uint32_t i = 0; i < nt; ++i)
+            if (seen[i] && c->tensors[i].has_grad && c->tensors[i].numel) active.push_back(i);
+    } else {
+        for (uint32_t i = 0; i < nt; ++i)
+            if (c->tensors[i].has_grad && c->tensors[i].numel) active.push_back(i);
+    }
+    if (active.size() == c->n_nonempty) {
+        *chunks = c->chunks_all;
+        *n = c->n_chunks_all;
+    } else {
+        auto it = c->tables.find(active);
+        if (it == c->tables.end()) {
+            if (c->tables.size() >= 64) {
+                // queued work may still read the cached tables
+                HIP_TRY(hipStreamSynchronize(c->stream));
+                for (auto& kv : c->tables) HIP_TRY(hipFree(kv.second.first));
+                c->tables.clear();
+            }
+            std::vector<Chunk> v;
+            append_chunks(c, active, v);
+            Chunk* d = nullptr;
+            HIP_TRY(hipMalloc((void**)&d, std::max<size_t>(v.size(), 1) * sizeof(Chunk)));
+            if (!v.empty())
+                HIP_TRY(hipMemcpy(d, v.data(), v.size() * sizeof(Chunk), hipMemcpyHostToDevice));
+            it = c->tables.emplace(active, std::make_pair(d, (uint32_t)v.size())).first;
+        }
+        *chunks = it->second.first;
+        *n = it->second.second;
+    }
+    if (active_out) *active_out = std::move(active);
+    return TTP_OK;
+}
+
+// (float)(1 - beta^t) for t = 1.. until both round to exactly 1.0f (and stay there, since
+// beta^t only shrinks); py/optim.py:51-52 evaluates the same host-double expression.
+int ensure_bias_table(ttp_ctx* c, double b1, double b2) {
+    if (c->bias_tab && c->bias_b1 == b1 && c->bias_b2 == b2) return TTP_OK;
+    std::vector<float> tab;
+    const uint64_t kMax = 1ull << 24;
+    for (uint64_t t = 1;; ++t) {
+        const float x1 = (float)(1.0 - std::pow(b1, (double)t));
+        const float x2 = (float)(1.0 - std::pow(b2, (double)t));
+        if (x1 == 1.0f && x2 == 1.0f) break;
+        if (t > kMax)
+            return fail(TTP_ERR_INVALID, "beta too close to 1: bias correction table too long");
+        tab.push_back(x1);
+        tab.push_back(x2);
+    }
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    if (c->bias_tab) HIP_TRY(hipFree(c->bias_tab));
+    c->bias_tab = nullptr;
+    HIP_TRY(hipMalloc((void**)&c->bias_tab, std::max<size_t>(tab.size(), 2) * sizeof(float)));
+    if (!tab.empty())
+        HIP_TRY(hipMemcpy(c->bias_tab, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice));
+    c->bias_len = (uint32_t)(tab.size() / 2);
+    c->bias_b1 = b1;
+    c->bias_b2 = b2;
+    return TTP_OK;
+}
+
+hipEvent_t take_event(ttp_ctx* c) {
+    if (!c->ev_pool.empty()) {
+        hipEvent_t e = c->ev_pool.back();
+        c->ev_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+// RAII-free helpers: begin/end an event pair around one launch when timing is on
+struct TimedLaunch {
+    ttp_ctx* c;
+    int kernel;
+    hipEvent_t a = nullptr;
+    TimedLaunch(ttp_ctx* ctx, int k) : c(ctx), kernel(k) {
+        if (c->timing && (a = take_event(c))) (void)hipEventRecord(a, c->stream);
+    }
+    void done() {
+        if (!a) return;
+        hipEvent_t b = take_event(c);
+        if (!b) return;
+        (void)hipEventRecord(b, c->stream);
+        c->ev[kernel].push_back({a, b});
+    }
+};
+
+int check_ctx(const ttp_ctx* c) {
+    if (!c) return fail(TTP_ERR_INVALID, "null context");
+    return TTP_OK;
+}
+
+int set_dev(const ttp_ctx* c) {
+    HIP_TRY(hipSetDevice(c->device));
+    return TTP_OK;
+}
+
+uint32_t update_grid(const ttp_ctx* c, uint32_t nchunks) {
+    uint32_t g = nchunks;
+    if (c->grid_cap) g = std::min(g, c->grid_cap);
+    return std::max<uint32_t>(g, 1);
+}
+
+uint32_t norm_grid(const ttp_ctx* c, uint32_t nchunks) {
+    return std::max<uint32_t>(1, std::min(nchunks, c->norm_grid_cap));
+}
+
+// norm / inf-check / finalize pass; `probe` only computes the norm
+int launch_norm(ttp_ctx* c, const Chunk* chunks, uint32_t n, double max_norm, bool probe,
+                bool want_bias) {
+    ttp::NormArgs a{};
+    a.chunks = chunks;
+    a.nchunks = n;
+    a.scaler_on = c->scaler.enabled ? 1 : 0;
+    a.probe = probe ? 1 : 0;
+    a.growth_interval = c->scaler.growth_interval;
+    a.growth_factor = c->scaler.growth_factor;
+    a.backoff_factor = c->scaler.backoff_factor;
+    a.max_norm = max_norm;
+    a.bias_tab = c->bias_tab;
+    a.bias_len = c->bias_len;
+    a.want_bias = want_bias ? 1 : 0;
+    a.partials = c->partials;
+    a.st = c->st;
+    const uint32_t grid = norm_grid(c, n);
+    TimedLaunch tl(c, TTP_KERNEL_NORM);
+    if (c->mode == TTP_MODE_MIXED)
+        hipLaunchKernelGGL(ttp::norm_kernel<uint16_t>, dim3(grid), dim3(ttp::kBlock), 0,
+                           c->stream, (const uint16_t*)c->grad, a);
+    else
+        hipLaunchKernelGGL(ttp::norm_kernel<float>, dim3(grid), dim3(ttp::kBlock), 0,
+                           c->stream, (const float*)c->grad, a);
+    HIP_TRY(hipGetLastError());
+    tl.done();
+    return TTP_OK;
+}
+
+int read_state(ttp_ctx* c, DevState* out) {
+    HIP_TRY(hipMemcpyAsync(out, c->st, sizeof(DevState), hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return TTP_OK;
+}
+
+int fill_report(ttp_ctx* c, bool norm_ran, ttp_step_report* r) {
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    DevState s;
+    int rc = read_state(c, &s);
+    if (rc) return rc;
+    std::memset(r, 0, sizeof(*r));
+    r->found_inf = norm_ran ? s.found_inf : 0;
+    r->skipped = (norm_ran && c->scaler.enabled) ? s.skip : 0;
+    r->grad_norm = norm_ran ? s.norm : std::nan("");
+    r->clip_coef = norm_ran ? s.clip_coef : 1.0f;
+    r->scale = c->scaler.enabled ? s.scale : 1.0f;
+    r->growth_tracker = c->scaler.enabled ? s.growth_tracker : 0;
+    r->step = c->scaler.enabled ? s.t : c->host_t;
+    return TTP_OK;
+}
+
+int check_index(const ttp_ctx* c, uint32_t i) {
+    if (i >= c->tensors.size())
+        return fail(TTP_ERR_RANGE, "tensor index " + std::to_string(i) + " out of range");
+    return TTP_OK;
+}
+
+void* buffer_base(ttp_ctx* c, int which) {
+    switch (which) {
+        case TTP_BUF_PARAM: return c->param;
+        case TTP_BUF_GRAD: return c->grad;
+        case TTP_BUF_MASTER: return c->master;
+        case TTP_BUF_EXP_AVG: return c->exp_avg;
+        case TTP_BUF_EXP_AVG_SQ: return c->exp_avg_sq;
+        case TTP_BUF_MOMENTUM: return c->momentum;
+    }
+    return nullptr;
+}
+
+size_t buffer_esize(const ttp_ctx* c, int which) {
+    if (which == TTP_BUF_PARAM) return param_esize(c);
+    if (which == TTP_BUF_GRAD) return grad_esize(c);
+    return 4;
+}
+
+int materialize(ttp_ctx* c, int which) {
+    if (which == TTP_BUF_EXP_AVG || which == TTP_BUF_EXP_AVG_SQ) return ensure_adam_state(c);
+    if (which == TTP_BUF_MOMENTUM) return ensure_momentum(c);
+    if (which < TTP_BUF_PARAM || which > TTP_BUF_MOMENTUM)
+        return fail(TTP_ERR_INVALID, "unknown buffer id " + std::to_string(which));
+    return TTP_OK;
+}
+
+int resolve_range(ttp_ctx* c, uint32_t index, uint64_t n, uint64_t* off, uint64_t* count) {
+    if (index == TTP_ALL_TENSORS) {
+        if (n != c->total)
+            return fail(TTP_ERR_RANGE, "flat transfer must cover all " + std::to_string(c->total) +
+                                           " elements, got " + std::to_string(n));
+        *off = 0;
+        *count = n;
+        return TTP_OK;
+    }
+    int rc = check_index(c, index);
+    if (rc) return rc;
+    if (n != c->tensors[index].numel)
+        return fail(TTP_ERR_RANGE, "tensor " + std::to_string(index) + " has " +
+                                       std::to_string(c->tensors[index].numel) +
+                                       " elements, got " + std::to_string(n));
+    *off = c->tensors[index].offset;
+    *count = n;
+    return TTP_OK;
+}
+
+uint32_t elementwise_grid(const ttp_ctx* c, uint64_t n) {
+    return (uint32_t)std::max<uint64_t>(
+        1, std::min<uint64_t>((n + ttp::kBlock - 1) / ttp::kBlock, (uint64_t)c->num_cus * 16));
+}
+
+void release(ttp_ctx* c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    for (void* p : {(void*)c->grad, (void*)c->master, (void*)c->exp_avg, (void*)c->exp_avg_sq,
+                    (void*)c->momentum, (void*)c->mom_init, (void*)c->st, (void*)c->partials,
+                    (void*)c->chunks_all, (void*)c->bias_tab})
+        if (p) (void)hipFree(p);
+    for (auto& kv : c->tables) (void)hipFree(kv.second.first);
+    if (c->mode == TTP_MODE_MIXED && c->param) (void)hipFree(c->param);
+    for (auto& v : c->ev)
+        for (auto& p : v) {
+            (void)hipEventDestroy(p.a);
+            (void)hipEventDestroy(p.b);
+        }
+    for (auto e : c->ev_pool) (void)hipEventDestroy(e);
+    if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
+    delete c;
+}
+
+}  // namespace
+
+// =====================================================================================
+// C ABI
+// =====================================================================================
+extern "C" {
+
+const char* ttp_last_error(void) { return g_last_error.c_str(); }
+int ttp_abi_version(void) { return TTP_ABI_VERSION; }
+
+int ttp_device_count(int* count) {
+    if (!count) return fail(TTP_ERR_INVALID, "null count");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) n = 0;
+    *count = n;
+    return TTP_OK;
+}
+
+int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, ttp_ctx** out) {
+    if (!out) return fail(TTP_ERR_INVALID, "null output pointer");
+    *out = nullptr;
+    if (n && !descs) return fail(TTP_ERR_INVALID, "null tensor table");
+    if (mode != TTP_MODE_FP32 && mode != TTP_MODE_MIXED)
+        return fail(TTP_ERR_INVALID, "mode must be TTP_MODE_FP32 or TTP_MODE_MIXED");
+    if (n > (1u << 24)) return fail(TTP_ERR_INVALID, "too many tensors (max 2^24)");
+    for (uint32_t i = 0; i < n; ++i)
+        if (descs[i].flags & ~TTP_TENSOR_DECAY)
+            return fail(TTP_ERR_INVALID, "unknown flags on tensor " + std::to_string(i));
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0)
+        return fail(TTP_ERR_NO_DEVICE, "no HIP device available");
+    if (device < 0 || device >= ndev)
+        return fail(TTP_ERR_NO_DEVICE, "device " + std::to_string(device) + " out of range");
+
+    ttp_ctx* c = new ttp_ctx();
+    c->device = device;
+    c->mode = mode;
+    auto bail = [&](int rc) {
+        release(c);
+        return rc;
+    };
+    if (hipSetDevice(device) != hipSuccess) return bail(fail(TTP_ERR_HIP, "hipSetDevice failed"));
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
+        c->num_cus = prop.multiProcessorCount;
+    if (hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess)
+        return bail(fail(TTP_ERR_HIP, "hipStreamCreate failed"));
+    c->stream = c->own_stream;
+
+    c->chunk_elems = std::max<uint64_t>(kAlign, env_u64("TTP_CHUNK_ELEMS", 16384) / kAlign * kAlign);
+    c->grid_cap = (uint32_t)env_u64("TTP_GRID_CAP", 0);
+    c->norm_grid_cap = (uint32_t)std::max<uint64_t>(1, env_u64("TTP_NORM_GRID", (uint64_t)c->num_cus * 8));
+
+    // layout
+    c->tensors.resize(n);
+    uint64_t off = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        c->tensors[i] = {off, descs[i].numel, descs[i].flags, 0};
+        off += (descs[i].numel + kAlign - 1) / kAlign * kAlign;
+    }
+    c->total = off;
+    int rc;
+    if ((rc = alloc_zero(c, (void**)&c->master, c->total * 4))) return bail(rc);
+    if ((rc = alloc_zero(c, &c->grad, c->total * grad_esize(c)))) return bail(rc);
+    if (mode == TTP_MODE_MIXED) {
+        if ((rc = alloc_zero(c, &c->param, c->total * 2))) return bail(rc);
+    } else {
+        c->param = c->master;
+    }
+    if ((rc = alloc_zero(c, (void**)&c->mom_init, std::max<uint64_t>(n, 1) * 4))) return bail(rc);
+    c->host_mom_init.assign(n, 0);
+    if ((rc = alloc_zero(c, (void**)&c->st, sizeof(DevState)))) return bail(rc);
+    c->partials_cap = c->norm_grid_cap;
+    if ((rc = alloc_zero(c, (void**)&c->partials, (uint64_t)c->partials_cap * 8))) return bail(rc);
+
+    std::vector<uint32_t> every;
+    for (uint32_t i = 0; i < n; ++i)
+        if (descs[i].numel) every.push_back(i);
+    c->n_nonempty = (uint32_t)every.size();
+    std::vector<Chunk> all;
+    append_chunks(c, every, all);
+    if (all.size() > 0xFFFFFFFFull) return bail(fail(TTP_ERR_INVALID, "too many chunks"));
+    if (hipMalloc((void**)&c->chunks_all, std::max<size_t>(all.size(), 1) * sizeof(Chunk)) != hipSuccess)
+        return bail(fail(TTP_ERR_OOM, "chunk table allocation failed"));
+    if (!all.empty() && hipMemcpy(c->chunks_all, all.data(), all.size() * sizeof(Chunk),
+                                  hipMemcpyHostToDevice) != hipSuccess)
+        return bail(fail(TTP_ERR_HIP, "chunk table upload failed"));
+    c->n_chunks_all = (uint32_t)all.size();
+
+    DevState s{};
+    s.scale = (float)c->scaler.init_scale;
+    if (hipMemcpy(c->st, &s, sizeof(s), hipMemcpyHostToDevice) != hipSuccess)
+        return bail(fail(TTP_ERR_HIP, "state upload failed"));
+    if (hipStreamSynchronize(c->stream) != hipSuccess)
+        return bail(fail(TTP_ERR_HIP, "stream synchronize failed"));
+    *out = c;
+    return TTP_OK;
+}
+
+int ttp_destroy(ttp_ctx* c) {
+    if (!c) return TTP_OK;
+    release(c);
+    return TTP_OK;
+}
+
+int ttp_set_stream(ttp_ctx* c, void* stream) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if ((rc = set_dev(c))) return rc;
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    c->stream = (hipStream_t)stream;
+    return TTP_OK;
+}
+
+int ttp_reset_stream(ttp_ctx* c) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if ((rc = set_dev(c))) return rc;
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    c->stream = c->own_stream;
+    return TTP_OK;
+}
+
+int ttp_sync(ttp_ctx* c) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if ((rc = set_dev(c))) return rc;
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return TTP_OK;
+}
+
+int ttp_num_tensors(const ttp_ctx* c, uint32_t* n) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!n) return fail(TTP_ERR_INVALID, "null output");
+    *n = (uint32_t)c->tensors.size();
+    return TTP_OK;
+}
+
+int ttp_mode(const ttp_ctx* c, int* mode) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!mode) return fail(TTP_ERR_INVALID, "null output");
+    *mode = c->mode;
+    return TTP_OK;
+}
+
+int ttp_flat_numel(const ttp_ctx* c, uint64_t* total) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!total) return fail(TTP_ERR_INVALID, "null output");
+    *total = c->total;
+    return TTP_OK;
+}
+
+int ttp_tensor_info(const ttp_ctx* c, uint32_t i, uint64_t* offset, uint64_t* numel,
+                    uint32_t* flags) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if ((rc = check_index(c, i))) return rc;
+    if (offset) *offset = c->tensors[i].offset;
+    if (numel) *numel = c->tensors[i].numel;
+    if (flags) *flags = c->tensors[i].flags;
+    return TTP_OK;
+}
+
+int ttp_buffer_ptr(ttp_ctx* c, int which, uint32_t index, void** ptr) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!ptr) return fail(TTP_ERR_INVALID, "null output");
+    if ((rc = set_dev(c))) return rc;
+    if ((rc = materialize(c, which))) return rc;
+    char* base = (char*)buffer_base(c, which);
+    if (index == TTP_ALL_TENSORS) {
+        *ptr = base;
+        return TTP_OK;
+    }
+    if ((rc = check_index(c, index))) return rc;
+    *ptr = base + c->tensors[index].offset * buffer_esize(c, which);
+    return TTP_OK;
+}
+
+int ttp_upload(ttp_ctx* c, int which, uint32_t index, const void* src, uint64_t n, int kind) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!src && n) return fail(TTP_ERR_INVALID, "null source");
+    if (kind != TTP_HOST && kind != TTP_DEVICE) return fail(TTP_ERR_INVALID, "bad memory kind");
+    if ((rc = set_dev(c))) return rc;
+    if ((rc = materialize(c, which))) return rc;
+    uint64_t off, cnt;
+    if ((rc = resolve_range(c, index, n, &off, &cnt))) return rc;
+    const size_t es = buffer_esize(c, which);
+    char* dst = (char*)buffer_base(c, which) + off * es;
+    if (cnt) {
+        HIP_TRY(hipMemcpyAsync(dst, src, cnt * es,
+                               kind == TTP_HOST ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice,
+                               c->stream));
+        if (c->mode == TTP_MODE_MIXED && (which == TTP_BUF_MASTER || which == TTP_BUF_PARAM)) {
+            const uint32_t grid = elementwise_grid(c, cnt);
+            if (which == TTP_BUF_MASTER)
+                hipLaunchKernelGGL(ttp::master_to_bf16_kernel, dim3(grid), dim3(ttp::kBlock), 0,
+                                   c->stream, c->master + off, (uint16_t*)c->param + off, cnt);
+            else
+                hipLaunchKernelGGL(ttp::bf16_to_master_kernel, dim3(grid), dim3(ttp::kBlock), 0,
+                                   c->stream, (const uint16_t*)c->param + off, c->master + off, cnt);
+            HIP_TRY(hipGetLastError());
+        }
+        if (kind == TTP_HOST) HIP_TRY(hipStreamSynchronize(c->stream));
+    }
+    if (which == TTP_BUF_GRAD) {
+        if (index == TTP_ALL_TENSORS)
+            for (auto& t : c->tensors) t.has_grad = 1;
+        else
+            c->tensors[index].has_grad = 1;
+    }
+    return TTP_OK;
+}
+
+int ttp_download(ttp_ctx* c, int which, uint32_t index, void* dst, uint64_t n, int kind) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!dst && n) return fail(TTP_ERR_INVALID, "null destination");
+    if (kind != TTP_HOST && kind != TTP_DEVICE) return fail(TTP_ERR_INVALID, "bad memory kind");
+    if ((rc = set_dev(c))) return rc;
+    if ((rc = materialize(c, which))) return rc;
+    uint64_t off, cnt;
+    if ((rc = resolve_range(c, index, n, &off, &cnt))) return rc;
+    const size_t es = buffer_esize(c, which);
+    const char* src = (const char*)buffer_base(c, which) + off * es;
+    if (cnt) {
+        HIP_TRY(hipMemcpyAsync(dst, src, cnt * es,
+                               kind == TTP_HOST ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice,
+                               c->stream));
+        if (kind == TTP_HOST) HIP_TRY(hipStreamSynchronize(c->stream));
+    }
+    return TTP_OK;
+}
+
+int ttp_set_has_grad(ttp_ctx* c, uint32_t i, int has) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if ((rc = check_index(c, i))) return rc;
+    if (c->tensors[i].has_grad != (has ? 1 : 0)) {
+        c->tensors[i].has_grad = has ? 1 : 0;
+    }
+    return TTP_OK;
+}
+
+int ttp_get_has_grad(const ttp_ctx* c, uint32_t i, int* has) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if ((rc = check_index(c, i))) return rc;
+    if (!has) return fail(TTP_ERR_INVALID, "null output");
+    *has = c->tensors[i].has_grad;
+    return TTP_OK;
+}
+
+int ttp_zero_grad(ttp_ctx* c, int set_to_none) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if ((rc = set_dev(c))) return rc;
+    if ((rc = zero_device(c, c->grad, c->total * grad_esize(c)))) return rc;
+    if (set_to_none) {
+        for (auto& t : c->tensors) t.has_grad = 0;
+    }
+    return TTP_OK;
+}
+
+static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t* subset,
+                          uint32_t nsub, ttp_step_report* report) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!hp) return fail(TTP_ERR_INVALID, "null hyperparameters");
+    // py/optim.py:33-41
+    if (!(hp->lr > 0)) return fail(TTP_ERR_INVALID, "lr must be > 0");
+    if (!(hp->eps > 0)) return fail(TTP_ERR_INVALID, "eps must be > 0");
+    if (!(hp->beta1 > 0 && hp->beta1 < 1 && hp->beta2 > 0 && hp->beta2 < 1))
+        return fail(TTP_ERR_INVALID, "betas must be in (0, 1)");
+    if (!(hp->weight_decay >= 0)) return fail(TTP_ERR_INVALID, "weight_decay must be >= 0");
+    if ((rc = set_dev(c))) return rc;
+    if ((rc = ensure_adam_state(c))) return rc;
+    const Chunk* chunks;
+    uint32_t n;
+    if ((rc = select_chunks(c, subset, nsub, &chunks, &n, nullptr))) return rc;
+
+    const bool scaler = c->scaler.enabled != 0;
+    const bool clip = hp->max_grad_norm > 0;
+    const bool need_norm = scaler || clip;
+    if (scaler && (rc = ensure_bias_table(c, hp->beta1, hp->beta2))) return rc;
+    if (need_norm && (rc = launch_norm(c, chunks, n, hp->max_grad_norm, false, scaler))) return rc;
+
+    ttp::AdamArgs a{};
+    a.chunks = chunks;
+    a.nchunks = n;
+    // py/optim.py:60-71: each hyperparameter is a full_like fill, i.e. rounded once to fp32
+    a.lr = (float)hp->lr;
+    a.b1 = (float)hp->beta1;
+    a.omb1 = (float)(1.0 - hp->beta1);
+    a.b2 = (float)hp->beta2;
+    a.omb2 = (float)(1.0 - hp->beta2);
+    a.eps = (float)hp->eps;
+    a.decay_mul = (float)(1.0 - hp->lr * hp->weight_decay);
+    a.wd = (float)hp->weight_decay;
+    a.flags = (hp->decoupled ? ttp::kDecoupled : 0u) | (hp->weight_decay != 0.0 ? ttp::kWdOn : 0u);
+    if (scaler) a.flags |= ttp::kUseInv | ttp::kDevBias | ttp::kCheckSkip;
+    if (clip) a.flags |= ttp::kUseClip;
+    a.st = need_norm ? c->st : nullptr;
+    if (!scaler) {
+        c->host_t += 1;  // py/optim.py:50
+        a.bias1 = (float)(1.0 - std::pow(hp->beta1, (double)c->host_t));
+        a.bias2 = (float)(1.0 - std::pow(hp->beta2, (double)c->host_t));
+    } else {
+        a.bias1 = a.bias2 = 1.0f;  // replaced by the device values
+    }
+    if (n) {
+        const uint32_t grid = update_grid(c, n);
+        TimedLaunch tl(c, TTP_KERNEL_UPDATE);
+        if (c->mode == TTP_MODE_MIXED)
+            hipLaunchKernelGGL((ttp::adam_kernel<uint16_t, true>), dim3(grid), dim3(ttp::kBlock), 0,
+                               c->stream, (const uint16_t*)c->grad, c->master, c->exp_avg,
+                               c->exp_avg_sq, (uint16_t*)c->param, a);
+        else
+            hipLaunchKernelGGL((ttp::adam_kernel<float, false>), dim3(grid), dim3(ttp::kBlock), 0,
+                               c->stream, (const float*)c->grad, c->master, c->exp_avg,
+                               c->exp_avg_sq, (uint16_t*)nullptr, a);
+        HIP_TRY(hipGetLastError());
+        tl.done();
+    }
+    if (report) return fill_report(c, need_norm, report);
+    return TTP_OK;
+}
+
+static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* subset,
+                         uint32_t nsub, ttp_step_report* report) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!hp) return fail(TTP_ERR_INVALID, "null hyperparameters");
+    if (!(hp->lr > 0)) return fail(TTP_ERR_INVALID, "lr must be > 0");  // py/optim.py:9-10
+    if (!(hp->momentum >= 0)) return fail(TTP_ERR_INVALID, "momentum must be >= 0");
+    if (!(hp->weight_decay >= 0)) return fail(TTP_ERR_INVALID, "weight_decay must be >= 0");
+    if (hp->nesterov && (hp->momentum <= 0 || hp->dampening != 0))
+        return fail(TTP_ERR_INVALID, "nesterov needs momentum > 0 and zero dampening");
+    if ((rc = set_dev(c))) return rc;
+    const bool mom = hp->momentum != 0.0;
+    if (mom && (rc = ensure_momentum(c))) return rc;
+    const Chunk* chunks;
+    uint32_t n;
+    std::vector<uint32_t> active;
+    if ((rc = select_chunks(c, subset, nsub, &chunks, &n, &active))) return rc;
+
+    const bool scaler = c->scaler.enabled != 0;
+    const bool clip = hp->max_grad_norm > 0;
+    const bool need_norm = scaler || clip;
+    if (need_norm && (rc = launch_norm(c, chunks, n, hp->max_grad_norm, false, false))) return rc;
+    if (!scaler) c->host_t += 1;
+
+    ttp::SgdArgs a{};
+    a.chunks = chunks;
+    a.nchunks = n;
+    a.lr = (float)hp->lr;
+    a.mu = (float)hp->momentum;
+    a.omd = (float)(1.0 - hp->dampening);
+    a.wd = (float)hp->weight_decay;
+    a.mom_init = c->mom_init;
+    a.flags = (hp->weight_decay != 0.0 ? ttp::kWdOn : 0u) | (mom ? ttp::kMomOn : 0u) |
+              (hp->nesterov ? ttp::kNesterov : 0u);
+    if (scaler) a.flags |= ttp::kUseInv | ttp::kCheckSkip;
+    if (clip) a.flags |= ttp::kUseClip;
+    a.st = need_norm ? c->st : nullptr;
+    if (n) {
+        const uint32_t grid = update_grid(c, n);
+        TimedLaunch tl(c, TTP_KERNEL_UPDATE);
+        if (c->mode == TTP_MODE_MIXED)
+            hipLaunchKernelGGL((ttp::sgd_kernel<uint16_t, true>), dim3(grid), dim3(ttp::kBlock), 0,
+                               c->stream, (const uint16_t*)c->grad, c->master, c->momentum,
+                               (uint16_t*)c->param, a);
+        else
+            hipLaunchKernelGGL((ttp::sgd_kernel<float, false>), dim3(grid), dim3(ttp::kBlock), 0,
+                               c->stream, (const float*)c->grad, c->master, c->momentum,
+                               (uint16_t*)nullptr, a);
+        HIP_TRY(hipGetLastError());
+        tl.done();
+        if (mom) {
+            // the stepped tensors now hold a momentum buffer (torch: state created on first
+            // use); with loss scaling the device decides, since the step may be skipped
+            bool needed = scaler;
+            for (uint32_t i : active)
+                if (!c->host_mom_init[i]) needed = true;
+            if (needed) {
+                const uint32_t g = std::max<uint32_t>(1, std::min<uint32_t>((n + ttp::kBlock - 1) / ttp::kBlock, 1024));
+                hipLaunchKernelGGL(ttp::mark_mom_init_kernel, dim3(g), dim3(ttp::kBlock), 0,
+                                   c->stream, chunks, n, c->mom_init, (const DevState*)c->st,
+                                   scaler ? 1 : 0);
+                HIP_TRY(hipGetLastError());
+            }
+            if (!scaler)
+                for (uint32_t i : active) c->host_mom_init[i] = 1;
+        }
+    }
+    if (report) return fill_report(c, need_norm, report);
+    return TTP_OK;
+}
+
+}  // extern "C"
+
+// (the step implementations above are static; their C entry points follow)
+extern "C" {
+
+int ttp_adam_step(ttp_ctx* c, const ttp_adam_hparams* hp, ttp_step_report* report) {
+    return adam_step_impl(c, hp, nullptr, 0, report);
+}
+
+int ttp_adam_step_subset(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t* indices,
+                         uint32_t n, ttp_step_report* report) {
+    if (n && !indices) return fail(TTP_ERR_INVALID, "null index list");
+    static const uint32_t none = 0;
+    return adam_step_impl(c, hp, indices ? indices : &none, n, report);
+}
+
+int ttp_sgd_step(ttp_ctx* c, const ttp_sgd_hparams* hp, ttp_step_report* report) {
+    return sgd_step_impl(c, hp, nullptr, 0, report);
+}
+
+int ttp_sgd_step_subset(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* indices,
+                        uint32_t n, ttp_step_report* report) {
+    if (n && !indices) return fail(TTP_ERR_INVALID, "null index list");
+    static const uint32_t none = 0;
+    return sgd_step_impl(c, hp, indices ? indices : &none, n, report);
+}
+
+int ttp_grad_norm(ttp_ctx* c, double* norm) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!norm) return fail(TTP_ERR_INVALID, "null output");
+    if ((rc = set_dev(c))) return rc;
+    const Chunk* chunks;
+    uint32_t n;
+    if ((rc = select_chunks(c, nullptr, 0, &chunks, &n, nullptr))) return rc;
+    if ((rc = launch_norm(c, chunks, n, 0.0, true, false))) return rc;
+    DevState s;
+    if ((rc = read_state(c, &s))) return rc;
+    *norm = s.norm;
+    return TTP_OK;
+}
+
+int ttp_get_step(ttp_ctx* c, uint64_t* step) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!step) return fail(TTP_ERR_INVALID, "null output");
+    if (!c->scaler.enabled) {
+        *step = c->host_t;
+        return TTP_OK;
+    }
+    if ((rc = set_dev(c))) return rc;
+    DevState s;
+    if ((rc = read_state(c, &s))) return rc;
+    *step = s.t;
+    return TTP_OK;
+}
+
+int ttp_set_step(ttp_ctx* c, uint64_t step) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if ((rc = set_dev(c))) return rc;
+    c->host_t = step;
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    HIP_TRY(hipMemcpy(&c->st->t, &step, sizeof(step), hipMemcpyHostToDevice));
+    return TTP_OK;
+}
+
+int ttp_scaler_configure(ttp_ctx* c, const ttp_scaler_config* cfg) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!cfg) return fail(TTP_ERR_INVALID, "null scaler config");
+    if (cfg->enabled) {
+        if (!(cfg->init_scale > 0)) return fail(TTP_ERR_INVALID, "init_scale must be > 0");
+        if (!(cfg->growth_factor > 1)) return fail(TTP_ERR_INVALID, "growth_factor must be > 1");
+        if (!(cfg->backoff_factor > 0 && cfg->backoff_factor < 1))
+            return fail(TTP_ERR_INVALID, "backoff_factor must be in (0, 1)");
+        if (cfg->growth_interval <= 0) return fail(TTP_ERR_INVALID, "growth_interval must be > 0");
+    }
+    if ((rc = set_dev(c))) return rc;
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    DevState s;
+    HIP_TRY(hipMemcpy(&s, c->st, sizeof(s), hipMemcpyDeviceToHost));
+    if (c->scaler.enabled && !cfg->enabled) c->host_t = s.t;  // device count -> host
+    if (cfg->enabled) {
+        if (!c->scaler.enabled) s.t = c->host_t;  // host count -> device
+        s.scale = (float)cfg->init_scale;
+        s.growth_tracker = 0;
+    }
+    HIP_TRY(hipMemcpy(c->st, &s, sizeof(s), hipMemcpyHostToDevice));
+    c->scaler = *cfg;
+    return TTP_OK;
+}
+
+int ttp_scaler_get(ttp_ctx* c, float* scale, int32_t* tracker) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if ((rc = set_dev(c))) return rc;
+    DevState s;
+    if ((rc = read_state(c, &s))) return rc;
+    if (scale) *scale = s.scale;
+    if (tracker) *tracker = s.growth_tracker;
+    return TTP_OK;
+}
+
+int ttp_scaler_set(ttp_ctx* c, float scale, int32_t tracker) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!(scale > 0) || tracker < 0) return fail(TTP_ERR_INVALID, "scale must be > 0, tracker >= 0");
+    if ((rc = set_dev(c))) return rc;
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    DevState s;
+    HIP_TRY(hipMemcpy(&s, c->st, sizeof(s), hipMemcpyDeviceToHost));
+    s.scale = scale;
+    s.growth_tracker = tracker;
+    HIP_TRY(hipMemcpy(c->st, &s, sizeof(s), hipMemcpyHostToDevice));
+    return TTP_OK;
+}
+
+int ttp_timing_enable(ttp_ctx* c, int on) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    c->timing = on != 0;
+    return TTP_OK;
+}
+
+int ttp_timing_collect(ttp_ctx* c, int kernel, double* total_ms, uint64_t* launches) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (kernel != TTP_KERNEL_NORM && kernel != TTP_KERNEL_UPDATE)
+        return fail(TTP_ERR_INVALID, "unknown kernel id");
+    if ((rc = set_dev(c))) return rc;
+    double sum = 0.0;
+    uint64_t cnt = 0;
+    auto& v = c->ev[kernel];
+    for (auto& p : v) {
+        HIP_TRY(hipEventSynchronize(p.b));
+        float ms = 0.0f;
+        HIP_TRY(hipEventElapsedTime(&ms, p.a, p.b));
+        sum += ms;
+        ++cnt;
+        c->ev_pool.push_back(p.a);
+        c->ev_pool.push_back(p.b);
+    }
+    v.clear();
+    if (total_ms) *total_ms = sum;
+    if (launches) *launches = cnt;
+    return TTP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,13 @@
+"""ttperf — MI355X (gfx950) optimizer-step engine for csirak/tt-perf's autograd.
+
+Python host side of libttperf_hip: a flat parameter store (`ParamStore`, `Tensor`) and the
+optimizers of the reference's py/optim.py (`SGD`, `Adam`) plus `AdamW`, each step a single
+multi-tensor HIP launch.  Importing fails if the HIP library is not built.
+"""
+from . import _lib
+from ._lib import TTPError, TTPValueError, device_count
+from .optim import SGD, Adam, AdamW
+from .store import GradView, Parameter, ParamStore, Tensor
+
+__all__ = ["SGD", "Adam", "AdamW", "ParamStore", "Tensor", "Parameter", "GradView",
+           "TTPError", "TTPValueError", "device_count", "_lib"]

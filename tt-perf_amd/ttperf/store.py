@@ -1,0 +1,326 @@
+"""Flat parameter store: the host-side owner of one libttperf_hip context.
+
+Replaces the per-parameter tensors the reference's optimizers walk (py/engine.py:74-156
+`Tensor.tt` / `Tensor.grad`; autograd/dynamic/autograd.hpp:38-84 `Value::data` / `grad`) with
+views into contiguous HBM buffers: each `Tensor` here is (store, index) and its data lives
+at `offset` of the store's param / grad / master / moment buffers.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+
+import numpy as np
+
+from . import _lib as L
+
+
+def _is_torch(x):
+    return type(x).__module__.startswith("torch")
+
+
+def _bf16_bits_to_f32(h):
+    return (np.asarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+class Tensor:
+    """A parameter: a view of one tensor of a ParamStore.
+
+    `grad` is None (py/engine.py:141 `grad = None`) until a gradient is written; assigning an
+    array uploads it, assigning None is the reference's `zero_grad` for this parameter.
+    """
+
+    def __init__(self, store: "ParamStore", index: int, shape, name: str = ""):
+        self.store = store
+        self.index = index
+        self.shape = tuple(int(s) for s in shape)
+        self.numel = int(math.prod(self.shape)) if self.shape else 1
+        self.name = name
+        self.requires_grad = True
+
+    def __repr__(self):
+        return f"Tensor(shape={self.shape}, requires_grad=True, index={self.index})"
+
+    @property
+    def decay(self) -> bool:
+        return bool(self.store.flags[self.index] & L.TENSOR_DECAY)
+
+    # ---- gradient ------------------------------------------------------------------------
+    @property
+    def grad(self):
+        return GradView(self) if self.store.has_grad(self.index) else None
+
+    @grad.setter
+    def grad(self, value):
+        if value is None:
+            self.store.set_has_grad(self.index, False)
+        else:
+            self.store.upload(L.BUF_GRAD, self.index, value)
+
+    def zero_grad(self):
+        self.grad = None
+
+    # ---- data ----------------------------------------------------------------------------
+    def numpy(self):
+        """Model-facing weights as float32 (bf16 widened in MIXED mode)."""
+        x = self.store.download(L.BUF_PARAM, self.index)
+        if self.store.mode == L.MODE_MIXED:
+            x = _bf16_bits_to_f32(x)
+        return x.reshape(self.shape)
+
+    def master(self):
+        return self.store.download(L.BUF_MASTER, self.index).reshape(self.shape)
+
+    def set_data(self, value):
+        """fp32 values -> master (and the bf16 copy in MIXED mode)."""
+        self.store.upload(L.BUF_MASTER, self.index, value)
+
+    def data_ptr(self, which=L.BUF_PARAM):
+        return self.store.ptr(which, self.index)
+
+
+Parameter = Tensor
+
+
+class GradView:
+    def __init__(self, p: Tensor):
+        self.p = p
+
+    def numpy(self):
+        x = self.p.store.download(L.BUF_GRAD, self.p.index)
+        if self.p.store.mode == L.MODE_MIXED:
+            x = _bf16_bits_to_f32(x)
+        return x.reshape(self.p.shape)
+
+    def data_ptr(self):
+        return self.p.store.ptr(L.BUF_GRAD, self.p.index)
+
+
+class ParamStore:
+    """One context: tensors laid out 64-element aligned in caller order.
+
+    shapes : list of shapes (tuples) or element counts
+    mode   : "fp32" (fp32 params/grads, params are the master copy) or
+             "mixed" (bf16 params/grads + fp32 master, m, v)
+    decay  : per-tensor bools (weight decay applies), default: tensors with >= 2 dims
+    """
+
+    def __init__(self, shapes, *, mode="fp32", decay=None, names=None, device=0):
+        shapes = [tuple(s) if isinstance(s, (tuple, list)) else (int(s),) for s in shapes]
+        if mode not in ("fp32", "mixed"):
+            raise ValueError("mode must be 'fp32' or 'mixed'")
+        self.mode = L.MODE_MIXED if mode == "mixed" else L.MODE_FP32
+        if decay is None:
+            decay = [len(s) >= 2 for s in shapes]
+        self.flags = [L.TENSOR_DECAY if d else 0 for d in decay]
+        n = len(shapes)
+        descs = (L.TensorDesc * max(n, 1))()
+        for i, s in enumerate(shapes):
+            descs[i].numel = int(math.prod(s)) if s else 1
+            descs[i].flags = self.flags[i]
+        h = C.c_void_p()
+        L.check(L.lib.ttp_create(device, descs, n, self.mode, C.byref(h)))
+        self._h = h
+        self.device = device
+        names = names or [f"p{i}" for i in range(n)]
+        self.tensors = [Tensor(self, i, s, names[i]) for i, s in enumerate(shapes)]
+        self.offsets = []
+        for i in range(n):
+            off = C.c_uint64()
+            L.check(L.lib.ttp_tensor_info(self._h, i, C.byref(off), None, None))
+            self.offsets.append(off.value)
+        tot = C.c_uint64()
+        L.check(L.lib.ttp_flat_numel(self._h, C.byref(tot)))
+        self.total = tot.value
+        self._scaler_enabled = False
+
+    # ---- lifetime --------------------------------------------------------------------------
+    def close(self):
+        if getattr(self, "_h", None):
+            L.lib.ttp_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def handle(self):
+        return self._h
+
+    def parameters(self):
+        return list(self.tensors)
+
+    def set_stream(self, stream):
+        """Queue all work on a torch.cuda.Stream or a raw hipStream_t (int; 0 is the legacy
+        default stream); None returns to the context's own stream."""
+        if stream is None:
+            L.check(L.lib.ttp_reset_stream(self._h))
+            return
+        if hasattr(stream, "cuda_stream"):
+            stream = stream.cuda_stream
+        L.check(L.lib.ttp_set_stream(self._h, C.c_void_p(int(stream))))
+
+    def sync(self):
+        L.check(L.lib.ttp_sync(self._h))
+
+    # ---- buffers -----------------------------------------------------------------------------
+    def ptr(self, which, index=L.ALL_TENSORS):
+        p = C.c_void_p()
+        L.check(L.lib.ttp_buffer_ptr(self._h, which, index, C.byref(p)))
+        return p.value
+
+    def _esize(self, which):
+        if which in (L.BUF_PARAM, L.BUF_GRAD) and self.mode == L.MODE_MIXED:
+            return 2
+        return 4
+
+    def _numel(self, index):
+        return self.total if index == L.ALL_TENSORS else self.tensors[index].numel
+
+    def _host_dtype(self, which):
+        return np.uint16 if self._esize(which) == 2 else np.float32
+
+    def upload(self, which, index, value):
+        """numpy (host) or torch (host or device) data.  For 2-byte buffers pass bf16 as
+        uint16 bits (numpy) or torch.bfloat16; float32 values are rounded by torch/numpy
+        callers, never here."""
+        n = self._numel(index)
+        if _is_torch(value):
+            t = value.detach().contiguous()
+            if t.numel() != n:
+                raise ValueError(f"expected {n} elements, got {t.numel()}")
+            if t.element_size() != self._esize(which):
+                raise ValueError("element size does not match the buffer's type")
+            kind = L.DEVICE if t.is_cuda else L.HOST
+            if t.is_cuda:
+                import torch
+                torch.cuda.current_stream(t.device).synchronize()
+            L.check(L.lib.ttp_upload(self._h, which, index, C.c_void_p(t.data_ptr()), n, kind))
+            if t.is_cuda:
+                self.sync()  # `t` may be freed and reused by torch as soon as we return
+            return
+        a = np.asarray(value)
+        want = self._host_dtype(which)
+        if a.dtype != want:
+            if want == np.uint16:
+                raise ValueError("bf16 buffers take uint16 bit patterns from numpy")
+            a = a.astype(np.float32)
+        a = np.ascontiguousarray(a).ravel()
+        if a.size != n:
+            raise ValueError(f"expected {n} elements, got {a.size}")
+        L.check(L.lib.ttp_upload(self._h, which, index, a.ctypes.data_as(C.c_void_p), n, L.HOST))
+
+    def download(self, which, index=L.ALL_TENSORS, out=None):
+        n = self._numel(index)
+        if out is not None and _is_torch(out):
+            kind = L.DEVICE if out.is_cuda else L.HOST
+            if out.is_cuda:
+                import torch
+                torch.cuda.current_stream(out.device).synchronize()
+            L.check(L.lib.ttp_download(self._h, which, index, C.c_void_p(out.data_ptr()), n, kind))
+            if kind == L.DEVICE:
+                self.sync()
+            return out
+        a = np.empty(n, self._host_dtype(which)) if out is None else out
+        L.check(L.lib.ttp_download(self._h, which, index, a.ctypes.data_as(C.c_void_p), n, L.HOST))
+        return a
+
+    # ---- grads ---------------------------------------------------------------------------------
+    def has_grad(self, index):
+        h = C.c_int()
+        L.check(L.lib.ttp_get_has_grad(self._h, index, C.byref(h)))
+        return bool(h.value)
+
+    def set_has_grad(self, index, has):
+        L.check(L.lib.ttp_set_has_grad(self._h, index, 1 if has else 0))
+
+    def zero_grad(self, set_to_none=True):
+        L.check(L.lib.ttp_zero_grad(self._h, 1 if set_to_none else 0))
+
+    # ---- steps -----------------------------------------------------------------------------------
+    @staticmethod
+    def _index_array(indices):
+        if indices is None:
+            return None, 0
+        idx = (C.c_uint32 * max(len(indices), 1))(*[int(i) for i in indices])
+        return idx, len(indices)
+
+    def adam_step(self, lr, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0, decoupled=True,
+                  max_grad_norm=None, report=False, indices=None):
+        """One Adam/AdamW step over every tensor with a grad, or only over `indices`."""
+        hp = L.AdamHParams(lr=lr, beta1=betas[0], beta2=betas[1], eps=eps,
+                           weight_decay=weight_decay, decoupled=1 if decoupled else 0,
+                           reserved=0, max_grad_norm=max_grad_norm or 0.0)
+        rep = L.StepReport() if report else None
+        rp = C.byref(rep) if report else None
+        idx, n = self._index_array(indices)
+        if idx is None:
+            L.check(L.lib.ttp_adam_step(self._h, C.byref(hp), rp))
+        else:
+            L.check(L.lib.ttp_adam_step_subset(self._h, C.byref(hp), idx, n, rp))
+        return rep.as_dict() if report else None
+
+    def sgd_step(self, lr, momentum=0.0, dampening=0.0, weight_decay=0.0, nesterov=False,
+                 max_grad_norm=None, report=False, indices=None):
+        """One SGD step over every tensor with a grad, or only over `indices`."""
+        hp = L.SgdHParams(lr=lr, momentum=momentum, dampening=dampening,
+                          weight_decay=weight_decay, nesterov=1 if nesterov else 0, reserved=0,
+                          max_grad_norm=max_grad_norm or 0.0)
+        rep = L.StepReport() if report else None
+        rp = C.byref(rep) if report else None
+        idx, n = self._index_array(indices)
+        if idx is None:
+            L.check(L.lib.ttp_sgd_step(self._h, C.byref(hp), rp))
+        else:
+            L.check(L.lib.ttp_sgd_step_subset(self._h, C.byref(hp), idx, n, rp))
+        return rep.as_dict() if report else None
+
+    def grad_norm(self):
+        v = C.c_double()
+        L.check(L.lib.ttp_grad_norm(self._h, C.byref(v)))
+        return v.value
+
+    # ---- step count / loss scaler ---------------------------------------------------------------
+    @property
+    def step_count(self):
+        v = C.c_uint64()
+        L.check(L.lib.ttp_get_step(self._h, C.byref(v)))
+        return v.value
+
+    @step_count.setter
+    def step_count(self, t):
+        L.check(L.lib.ttp_set_step(self._h, int(t)))
+
+    def configure_scaler(self, enabled=True, init_scale=2.0 ** 16, growth_factor=2.0,
+                         backoff_factor=0.5, growth_interval=2000):
+        cfg = L.ScalerConfig(enabled=1 if enabled else 0, growth_interval=growth_interval,
+                             init_scale=init_scale, growth_factor=growth_factor,
+                             backoff_factor=backoff_factor)
+        L.check(L.lib.ttp_scaler_configure(self._h, C.byref(cfg)))
+        self._scaler_enabled = bool(enabled)
+
+    def scaler_state(self):
+        s, t = C.c_float(), C.c_int32()
+        L.check(L.lib.ttp_scaler_get(self._h, C.byref(s), C.byref(t)))
+        return s.value, t.value
+
+    def set_scaler_state(self, scale, growth_tracker):
+        L.check(L.lib.ttp_scaler_set(self._h, scale, growth_tracker))
+
+    # ---- timing -----------------------------------------------------------------------------------
+    def timing(self, on=True):
+        L.check(L.lib.ttp_timing_enable(self._h, 1 if on else 0))
+
+    def timing_collect(self, kernel):
+        ms, n = C.c_double(), C.c_uint64()
+        L.check(L.lib.ttp_timing_collect(self._h, kernel, C.byref(ms), C.byref(n)))
+        return ms.value, n.value
