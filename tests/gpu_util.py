@@ -92,6 +92,7 @@ def compare_state(store, ref, which=("master", "exp_avg", "exp_avg_sq", "param")
     if mask is None:
         mask = pad_mask(store)
     for name in which:
+        print(f"  compare {name} ({store.total} elements)", flush=True)
         got = store.download(bufs[name])
         want = getattr(ref, name)
         if got.dtype == np.uint16:

@@ -102,6 +102,8 @@ def test_cfg3_gpt2_small_scaler_inf_skip():
         e = ref.adam_step(**hp)
         _check_report(r, e)
         assert r["skipped"] == (step % 50 == 0)
+        if step % 10 == 0:
+            print(f"cfg3 step {step}: scale {r['scale']} skipped {r['skipped']}", flush=True)
         if step - 1 in check_at:
             compare_state(store, ref, max_ulp=2)
     expected_scale = 65536.0 / 2 ** (steps // 50)
@@ -139,4 +141,5 @@ def test_cfg4_ragged_table_small_steps():
         _set_ref_grads(ref, host)
         store.adam_step(**hp)
         ref.adam_step(**hp)
+        print(f"cfg4 step {step} done", flush=True)
     compare_state(store, ref, max_ulp=0)
