@@ -45,7 +45,7 @@ def parse():
 
 def traffic_from_profiles(config):
     """HBM bytes per update launch from the committed rocprofv3 --pmc summary, if any."""
-    path = os.path.join(REPO, "profiles", f"pmc_update_{config}.md")
+    path = os.path.join(REPO, "profiles", f"adam_kernel_{config}_pmc.md")
     if not os.path.exists(path):
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())

@@ -1,17 +1,23 @@
 // kernels.hpp — gfx950 device code of libttperf_hip.
 //
-// Two passes make one optimizer step over the flat store:
-//   norm_kernel    reads only the gradients (2 B/param bf16, 4 B/param fp32): fp64 sum of
-//                  squares of the unscaled grads, wave shuffle + LDS block tree, one partial
-//                  per block, and a last-block finalize (atomic ticket) that sums the partials
-//                  in index order (deterministic), decides found_inf / skip, the clip
-//                  coefficient, advances the step count and the loss scale.
-//   adam_kernel /  one fused pass per element: grad transform (unscale, clip), weight decay,
-//   sgd_kernel     the optimizer update and the bf16 copy.  Each element is touched once;
-//                  loads/stores are 16-byte (fp32 x4) and 8-byte (bf16 x4) per lane, so every
-//                  wave instruction covers a contiguous 1 KiB / 512 B span.
-// Work is a table of chunks (<= chunk_elems elements of one tensor, 64-element aligned
-// start); block b takes chunks b, b+grid, ...  No MFMA: nothing here is a contraction.
+// One optimizer step over the flat store is at most three launches on one stream:
+//   norm_partials_kernel  reads only the gradients (2 B/param bf16, 4 B/param fp32): fp64 sum
+//                         of squares of the unscaled grads, one partial per block; no atomics
+//                         and no fences (a per-block device-scope fence + ticket costs ~50 ns
+//                         per block on MI355X, serialised, which tripled the pass's time);
+//   norm_finalize_kernel  one block: sums the partials in index order (deterministic),
+//                         decides found_inf / skip and the clip coefficient, advances the step
+//                         count and the loss scale;
+//   adam_kernel /         one fused pass per element: grad transform (unscale, clip), weight
+//   sgd_kernel            decay, the optimizer update and the bf16 copy.  Each element is
+//                         touched once; loads/stores are 16-byte (fp32 x4) and 8-byte (bf16 x4)
+//                         per lane, so every wave instruction covers a contiguous 1 KiB / 512 B
+//                         span, and each lane keeps two such vectors in flight.
+// Work is a table of chunks of kChunk elements (the last chunk of a tensor is shorter; every
+// chunk starts on a 64-element boundary).  The update runs one block per chunk: blocks are
+// dispatched in chunk order, so the resident blocks sweep a narrow window of each buffer
+// (2048 resident blocks x 2048 elements), which keeps DRAM pages open; 16K-element chunks
+// or a persistent grid measured 6-12% slower.  No MFMA: nothing here is a contraction.
 //
 // Arithmetic matches the oracle bit for bit: no contraction (-ffp-contract=off), IEEE
 // division and square root (HIP's correctly rounded fp32 div/sqrt), denormals kept.
@@ -22,8 +28,10 @@
 
 namespace ttp {
 
-constexpr int kBlock = 256;   // 4 wave64s
-constexpr int kVec = 4;       // elements per lane per vector
+constexpr int kBlock = 256;    // 4 wave64s
+constexpr int kVec = 4;        // elements per lane per vector
+constexpr int kUnroll = 2;     // vectors per lane per chunk in the update kernels
+constexpr uint32_t kChunk = kBlock * kVec * kUnroll;  // 2048 elements
 constexpr uint32_t kChunkDecay = 1u;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -35,8 +43,8 @@ struct Chunk {
     uint32_t meta;   // bit 0: decay; bits 8..31: tensor index
 };
 
-// Device-resident step state.  Written only by the norm pass's last block (and by the
-// host between steps); read by the update pass that follows it on the same stream.
+// Device-resident step state.  Written only by norm_finalize_kernel (and by the host between
+// steps); read by the update pass that follows it on the same stream.
 struct DevState {
     float scale;             // loss scale (persistent)
     int32_t growth_tracker;  // clean steps since the last scale change (persistent)
@@ -48,8 +56,6 @@ struct DevState {
     float bias1, bias2;      // last pass: Adam bias corrections for the new t
     int32_t found_inf;       // last pass: a non-finite gradient was seen
     int32_t skip;            // last pass: the update must not run
-    uint32_t ticket;         // blocks finished; the last block puts it back to 0
-    uint32_t pad;
 };
 
 // ------------------------------------------------------------------------------------
@@ -134,11 +140,84 @@ __device__ __forceinline__ double block_sum(double x, double* lds) {
 }
 
 // ------------------------------------------------------------------------------------
-// norm / inf-check / finalize pass
+// norm pass, part 1: per-block partial sums of squares of the unscaled gradients
 // ------------------------------------------------------------------------------------
-struct NormArgs {
-    const Chunk* chunks;
-    uint32_t nchunks;
+// 16-byte loads: 8 bf16 or 4 fp32 gradients per lane
+template <typename GradT>
+struct GradVec;
+template <>
+struct GradVec<uint16_t> {
+    static constexpr int kElems = 8;
+    typedef uint32_t raw __attribute__((ext_vector_type(4)));
+    static __device__ __forceinline__ float at(const raw& w, int j) {
+        return (j & 1) ? bf16_hi(w[j >> 1]) : bf16_lo(w[j >> 1]);
+    }
+};
+template <>
+struct GradVec<float> {
+    static constexpr int kElems = 4;
+    typedef f32x4 raw;
+    static __device__ __forceinline__ float at(const raw& w, int j) { return w[j]; }
+};
+
+// Grid-stride over the chunk table, two chunks per iteration so every lane has 2 (bf16) or
+// 4 (fp32) independent 16-byte loads in flight.  No atomics and no fences: each block
+// writes one partial; norm_finalize_kernel (next on the stream) combines them.  Squares of
+// fp32 values are exact in fp64, and any inf/NaN gradient makes the sum non-finite.
+template <typename GradT>
+__global__ __launch_bounds__(kBlock) void norm_partials_kernel(const GradT* __restrict__ g,
+                                                               const Chunk* __restrict__ chunks,
+                                                               uint32_t nchunks,
+                                                               const DevState* __restrict__ st,
+                                                               int32_t scaler_on,
+                                                               double* __restrict__ partials) {
+    typedef GradVec<GradT> GV;
+    constexpr int E = GV::kElems;
+    constexpr int L = kChunk / (kBlock * E);  // loads per lane per chunk
+    __shared__ double lds[kBlock / 64];
+    const float inv = scaler_on ? (float)(1.0 / (double)st->scale) : 1.0f;
+    double acc = 0.0;
+    for (uint32_t c = blockIdx.x; c < nchunks; c += 2 * gridDim.x) {
+        typename GV::raw w[2][L];
+        uint32_t n_valid[2][L];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const uint32_t cc = c + k * gridDim.x;
+            Chunk ch{0, 0, 0};
+            if (cc < nchunks) ch = chunks[cc];
+#pragma unroll
+            for (int l = 0; l < L; ++l) {
+                const uint32_t off = (uint32_t)(l * kBlock + threadIdx.x) * E;
+                n_valid[k][l] = off < ch.count ? min(ch.count - off, (uint32_t)E) : 0u;
+                if (n_valid[k][l])
+                    w[k][l] = __builtin_nontemporal_load(
+                        reinterpret_cast<const typename GV::raw*>(g + ch.begin + off));
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+#pragma unroll
+            for (int l = 0; l < L; ++l) {
+                if (!n_valid[k][l]) continue;
+#pragma unroll
+                for (int j = 0; j < E; ++j) {
+                    const float x = (uint32_t)j < n_valid[k][l] ? GV::at(w[k][l], j) * inv : 0.0f;
+                    acc += (double)x * (double)x;
+                }
+            }
+        }
+    }
+    const double b = block_sum(acc, lds);
+    if (threadIdx.x == 0) partials[blockIdx.x] = b;
+}
+
+// ------------------------------------------------------------------------------------
+// norm pass, part 2 (one block): combine the partials in index order (deterministic), then
+// decide found_inf / skip, the clip coefficient, the step count and the loss scale
+// ------------------------------------------------------------------------------------
+struct FinalizeArgs {
+    const double* partials;
+    uint32_t npartials;
     int32_t scaler_on;      // unscale by 1/scale, skip on inf, update the scale, own t
     int32_t probe;          // only compute sumsq/norm (ttp_grad_norm); touch nothing else
     int32_t growth_interval;
@@ -148,51 +227,18 @@ struct NormArgs {
     const float* bias_tab;  // [2*bias_len]: (1-beta1^t, 1-beta2^t) for t = 1..bias_len
     uint32_t bias_len;      // t > bias_len: both corrections are exactly 1.0f
     int32_t want_bias;
-    double* partials;       // [gridDim.x]
     DevState* st;
 };
 
-template <typename GradT>
-__global__ __launch_bounds__(kBlock) void norm_kernel(const GradT* __restrict__ g, NormArgs a) {
+__global__ __launch_bounds__(kBlock) void norm_finalize_kernel(FinalizeArgs a) {
     __shared__ double lds[kBlock / 64];
-    __shared__ int last;
-    const float inv = a.scaler_on ? (float)(1.0 / (double)a.st->scale) : 1.0f;
-    double acc = 0.0;
-    for (uint32_t c = blockIdx.x; c < a.nchunks; c += gridDim.x) {
-        const Chunk ch = a.chunks[c];
-        const uint64_t end = ch.begin + ch.count;
-        for (uint64_t i = ch.begin + (uint64_t)threadIdx.x * kVec; i < end;
-             i += (uint64_t)kBlock * kVec) {
-            f32x4 v = ld_grad4(g, i);
-            const int n = (int)min<uint64_t>(end - i, kVec);
-            v.x = v.x * inv;
-            v.y = n > 1 ? v.y * inv : 0.0f;
-            v.z = n > 2 ? v.z * inv : 0.0f;
-            v.w = n > 3 ? v.w * inv : 0.0f;
-            // squares of fp32 values are exact in fp64; any inf/NaN makes the sum non-finite
-            acc += (double)v.x * (double)v.x;
-            acc += (double)v.y * (double)v.y;
-            acc += (double)v.z * (double)v.z;
-            acc += (double)v.w * (double)v.w;
-        }
-    }
-    const double bsum = block_sum(acc, lds);
-    if (threadIdx.x == 0) {
-        a.partials[blockIdx.x] = bsum;
-        __threadfence();
-        const uint32_t prev = atomicAdd(&a.st->ticket, 1u);
-        last = (prev == gridDim.x - 1);
-    }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
     double s = 0.0;
-    for (uint32_t b = threadIdx.x; b < gridDim.x; b += kBlock) s += a.partials[b];
+    for (uint32_t b = threadIdx.x; b < a.npartials; b += kBlock) s += a.partials[b];
     s = block_sum(s, lds);
     if (threadIdx.x != 0) return;
 
     DevState* st = a.st;
-    st->ticket = 0;
+    const float inv = a.scaler_on ? (float)(1.0 / (double)st->scale) : 1.0f;
     st->sumsq = s;
     st->norm = sqrt(s);
     if (a.probe) return;
@@ -230,7 +276,6 @@ __global__ __launch_bounds__(kBlock) void norm_kernel(const GradT* __restrict__ 
             }
         }
     }
-    __threadfence();
 }
 
 // ------------------------------------------------------------------------------------
@@ -275,6 +320,24 @@ __device__ __forceinline__ void adam_elem(float& p, float g, float& m, float& v,
     p = p - step;
 }
 
+// Stores of one vector: whole (16 B / 8 B) or the first n elements (a tensor's last vector).
+template <bool kMixed>
+__device__ __forceinline__ void store_vec(float* a, float* b, float* c, uint16_t* p16, uint64_t i,
+                                          const f32x4& va, const f32x4& vb, const f32x4& vc,
+                                          int n) {
+    if (n >= kVec) {
+        st4(a + i, va);
+        if (b) st4(b + i, vb);
+        if (c) st4(c + i, vc);
+        if (kMixed) st_bf16x4(p16, i, va);
+    } else {
+        st4_partial(a + i, va, n);
+        if (b) st4_partial(b + i, vb, n);
+        if (c) st4_partial(c + i, vc, n);
+        if (kMixed) st_bf16x4_partial(p16 + i, va, n);
+    }
+}
+
 template <typename GradT, bool kMixed>
 __global__ __launch_bounds__(kBlock) void adam_kernel(const GradT* __restrict__ grad,
                                                       float* __restrict__ master,
@@ -296,33 +359,33 @@ __global__ __launch_bounds__(kBlock) void adam_kernel(const GradT* __restrict__ 
     for (uint32_t c = blockIdx.x; c < a.nchunks; c += gridDim.x) {
         const Chunk ch = a.chunks[c];
         const bool decay = (ch.meta & kChunkDecay) && (a.flags & kWdOn);
-        const uint64_t end = ch.begin + ch.count;
-        for (uint64_t i = ch.begin + (uint64_t)threadIdx.x * kVec; i < end;
-             i += (uint64_t)kBlock * kVec) {
-            const f32x4 g = ld_grad4(grad, i);
-            f32x4 p = ld4(master + i);
-            f32x4 m = ld4(exp_avg + i);
-            f32x4 v = ld4(exp_avg_sq + i);
+        f32x4 g[kUnroll], p[kUnroll], m[kUnroll], v[kUnroll];
+        int n[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const uint32_t off = (uint32_t)(u * kBlock + threadIdx.x) * kVec;
+            n[u] = off < ch.count ? (int)min(ch.count - off, (uint32_t)kVec) : 0;
+            if (n[u]) {
+                const uint64_t i = ch.begin + off;
+                g[u] = ld_grad4(grad, i);
+                p[u] = ld4(master + i);
+                m[u] = ld4(exp_avg + i);
+                v[u] = ld4(exp_avg_sq + i);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            if (!n[u]) continue;
 #pragma unroll
             for (int j = 0; j < kVec; ++j) {
-                float pj = p[j], mj = m[j], vj = v[j];
-                adam_elem(pj, g[j], mj, vj, a, k, use_inv, use_clip, decay);
-                p[j] = pj;
-                m[j] = mj;
-                v[j] = vj;
+                float pj = p[u][j], mj = m[u][j], vj = v[u][j];
+                adam_elem(pj, g[u][j], mj, vj, a, k, use_inv, use_clip, decay);
+                p[u][j] = pj;
+                m[u][j] = mj;
+                v[u][j] = vj;
             }
-            if (i + kVec <= end) {
-                st4(master + i, p);
-                st4(exp_avg + i, m);
-                st4(exp_avg_sq + i, v);
-                if (kMixed) st_bf16x4(param16, i, p);
-            } else {
-                const int n = (int)(end - i);
-                st4_partial(master + i, p, n);
-                st4_partial(exp_avg + i, m, n);
-                st4_partial(exp_avg_sq + i, v, n);
-                if (kMixed) st_bf16x4_partial(param16 + i, p, n);
-            }
+            const uint64_t i = ch.begin + (uint32_t)(u * kBlock + threadIdx.x) * kVec;
+            store_vec<kMixed>(master, exp_avg, exp_avg_sq, param16, i, p[u], m[u], v[u], n[u]);
         }
     }
 }
@@ -360,37 +423,40 @@ __global__ __launch_bounds__(kBlock) void sgd_kernel(const GradT* __restrict__ g
         const Chunk ch = a.chunks[c];
         const bool decay = (ch.meta & kChunkDecay) && (a.flags & kWdOn);
         const bool first = mom_on && a.mom_init[ch.meta >> 8] == 0u;
-        const uint64_t end = ch.begin + ch.count;
-        for (uint64_t i = ch.begin + (uint64_t)threadIdx.x * kVec; i < end;
-             i += (uint64_t)kBlock * kVec) {
-            f32x4 g = ld_grad4(grad, i);
-            f32x4 p = ld4(master + i);
-            f32x4 b = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (mom_on && !first) b = ld4(momentum + i);
+        f32x4 g[kUnroll], p[kUnroll], b[kUnroll];
+        int n[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const uint32_t off = (uint32_t)(u * kBlock + threadIdx.x) * kVec;
+            n[u] = off < ch.count ? (int)min(ch.count - off, (uint32_t)kVec) : 0;
+            b[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (n[u]) {
+                const uint64_t i = ch.begin + off;
+                g[u] = ld_grad4(grad, i);
+                p[u] = ld4(master + i);
+                if (mom_on && !first) b[u] = ld4(momentum + i);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            if (!n[u]) continue;
 #pragma unroll
             for (int j = 0; j < kVec; ++j) {
-                float gj = g[j];
+                float gj = g[u][j];
                 if (use_inv) gj = gj * inv;
                 if (use_clip) gj = gj * clip;
-                if (decay) gj = gj + a.wd * p[j];
+                if (decay) gj = gj + a.wd * p[u][j];
                 if (mom_on) {
-                    const float bj = first ? gj : a.mu * b[j] + a.omd * gj;
-                    b[j] = bj;
+                    const float bj = first ? gj : a.mu * b[u][j] + a.omd * gj;
+                    b[u][j] = bj;
                     gj = nesterov ? gj + a.mu * bj : bj;
                 }
                 const float update = gj * a.lr;  // autograd/dynamic/optim.hpp:24
-                p[j] = p[j] - update;             // autograd/dynamic/optim.hpp:25
+                p[u][j] = p[u][j] - update;       // autograd/dynamic/optim.hpp:25
             }
-            if (i + kVec <= end) {
-                st4(master + i, p);
-                if (mom_on) st4(momentum + i, b);
-                if (kMixed) st_bf16x4(param16, i, p);
-            } else {
-                const int n = (int)(end - i);
-                st4_partial(master + i, p, n);
-                if (mom_on) st4_partial(momentum + i, b, n);
-                if (kMixed) st_bf16x4_partial(param16 + i, p, n);
-            }
+            const uint64_t i = ch.begin + (uint32_t)(u * kBlock + threadIdx.x) * kVec;
+            store_vec<kMixed>(master, mom_on ? momentum : nullptr, nullptr, param16, i, p[u], b[u],
+                              b[u], n[u]);
         }
     }
 }

@@ -4,12 +4,12 @@
 //   * layout: tensors in caller order, each starting on a 64-element boundary (256 B for
 //     fp32, 128 B for bf16), so every lane's 4-element vector stays inside one tensor's
 //     footprint; the padding is zero and never written by a step;
-//   * work table: chunks of <= chunk_elems elements of one tensor.  The table of all
+//   * work table: chunks of <= kChunk (2048) elements of one tensor.  The table of all
 //     tensors is built once; a second table is built only while some tensor has no grad
 //     (py/optim.py:56-57 skip);
-//   * step: [norm pass when clipping or loss scaling] + one fused update pass, both on the
-//     context's stream, no host synchronisation (the skip decision and, with loss scaling,
-//     the step count live on the device).
+//   * step: [norm pass (partials + finalize) when clipping or loss scaling] + one fused
+//     update pass, all on the context's stream, no host synchronisation (the skip decision
+//     and, with loss scaling, the step count live on the device).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -88,9 +88,9 @@ struct ttp_ctx {
     double* partials = nullptr;
     uint32_t partials_cap = 0;
 
-    uint64_t chunk_elems = 16384;
-    uint32_t grid_cap = 0;       // 0: one block per chunk
-    uint32_t norm_grid_cap = 0;  // blocks of the norm pass
+    uint64_t chunk_elems = ttp::kChunk;  // the kernels cover exactly kChunk elements per chunk
+    uint32_t grid_cap = 0;               // 0: one block per chunk
+    uint32_t norm_grid_cap = 0;          // blocks of the norm pass (one partial each)
 
     Chunk* chunks_all = nullptr;  // every non-empty tensor
     uint32_t n_chunks_all = 0;
@@ -284,13 +284,25 @@ uint32_t norm_grid(const ttp_ctx* c, uint32_t nchunks) {
     return std::max<uint32_t>(1, std::min(nchunks, c->norm_grid_cap));
 }
 
-// norm / inf-check / finalize pass; `probe` only computes the norm
+// norm / inf-check / finalize pass (two launches); `probe` only computes the norm
 int launch_norm(ttp_ctx* c, const Chunk* chunks, uint32_t n, double max_norm, bool probe,
                 bool want_bias) {
-    ttp::NormArgs a{};
-    a.chunks = chunks;
-    a.nchunks = n;
-    a.scaler_on = c->scaler.enabled ? 1 : 0;
+    const uint32_t grid = norm_grid(c, n);
+    const int32_t scaler_on = c->scaler.enabled ? 1 : 0;
+    TimedLaunch tl(c, TTP_KERNEL_NORM);
+    if (c->mode == TTP_MODE_MIXED)
+        hipLaunchKernelGGL(ttp::norm_partials_kernel<uint16_t>, dim3(grid), dim3(ttp::kBlock), 0,
+                           c->stream, (const uint16_t*)c->grad, chunks, n,
+                           (const DevState*)c->st, scaler_on, c->partials);
+    else
+        hipLaunchKernelGGL(ttp::norm_partials_kernel<float>, dim3(grid), dim3(ttp::kBlock), 0,
+                           c->stream, (const float*)c->grad, chunks, n, (const DevState*)c->st,
+                           scaler_on, c->partials);
+    HIP_TRY(hipGetLastError());
+    ttp::FinalizeArgs a{};
+    a.partials = c->partials;
+    a.npartials = grid;
+    a.scaler_on = scaler_on;
     a.probe = probe ? 1 : 0;
     a.growth_interval = c->scaler.growth_interval;
     a.growth_factor = c->scaler.growth_factor;
@@ -299,16 +311,8 @@ int launch_norm(ttp_ctx* c, const Chunk* chunks, uint32_t n, double max_norm, bo
     a.bias_tab = c->bias_tab;
     a.bias_len = c->bias_len;
     a.want_bias = want_bias ? 1 : 0;
-    a.partials = c->partials;
     a.st = c->st;
-    const uint32_t grid = norm_grid(c, n);
-    TimedLaunch tl(c, TTP_KERNEL_NORM);
-    if (c->mode == TTP_MODE_MIXED)
-        hipLaunchKernelGGL(ttp::norm_kernel<uint16_t>, dim3(grid), dim3(ttp::kBlock), 0,
-                           c->stream, (const uint16_t*)c->grad, a);
-    else
-        hipLaunchKernelGGL(ttp::norm_kernel<float>, dim3(grid), dim3(ttp::kBlock), 0,
-                           c->stream, (const float*)c->grad, a);
+    hipLaunchKernelGGL(ttp::norm_finalize_kernel, dim3(1), dim3(ttp::kBlock), 0, c->stream, a);
     HIP_TRY(hipGetLastError());
     tl.done();
     return TTP_OK;
@@ -463,9 +467,9 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
         return bail(fail(TTP_ERR_HIP, "hipStreamCreate failed"));
     c->stream = c->own_stream;
 
-    c->chunk_elems = std::max<uint64_t>(kAlign, env_u64("TTP_CHUNK_ELEMS", 16384) / kAlign * kAlign);
     c->grid_cap = (uint32_t)env_u64("TTP_GRID_CAP", 0);
-    c->norm_grid_cap = (uint32_t)std::max<uint64_t>(1, env_u64("TTP_NORM_GRID", (uint64_t)c->num_cus * 8));
+    c->norm_grid_cap = (uint32_t)std::min<uint64_t>(
+        65536, std::max<uint64_t>(1, env_u64("TTP_NORM_GRID", (uint64_t)c->num_cus * 8)));
 
     // layout
     c->tensors.resize(n);
