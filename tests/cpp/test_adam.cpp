@@ -1,0 +1,103 @@
+// test_adam.cpp — autograd::Adam / AdamW over the flat store.  Adam follows py/optim.py:30-92
+// (defaults lr 1e-3, betas (0.9, 0.999), eps 1e-8; t += 1 then bias corrections in host
+// double, rounded to fp32 like full_like(fill_value=...)); the expected values below apply
+// the same op order on the host with one rounding per op.  AdamW decays only the
+// decay-flagged (2-D weight) tensors: p *= (float)(1 - lr*wd) before the Adam update.
+#include <cmath>
+
+#include "autograd/nn.hpp"
+#include "autograd/optim.hpp"
+#include "common.hpp"
+
+using namespace autograd;
+
+struct Ref {
+    std::vector<float> p, m, v;
+};
+
+static void adam_ref(Ref& r, const std::vector<float>& g, double lr, double b1, double b2,
+                     double eps, uint64_t t, double wd, bool decay) {
+    const float flr = (float)lr, fb1 = (float)b1, fb2 = (float)b2, fomb1 = (float)(1.0 - b1),
+                fomb2 = (float)(1.0 - b2), feps = (float)eps;
+    const float bias1 = (float)(1.0 - std::pow(b1, (double)t));
+    const float bias2 = (float)(1.0 - std::pow(b2, (double)t));
+    const float dmul = (float)(1.0 - lr * wd);
+    for (size_t i = 0; i < g.size(); ++i) {
+        float p = r.p[i];
+        if (decay && wd != 0.0) p = p * dmul;
+        const float m = fb1 * r.m[i] + fomb1 * g[i];
+        const float gsq = g[i] * g[i];
+        const float v = fb2 * r.v[i] + fomb2 * gsq;
+        const float mh = m / bias1, vh = v / bias2;
+        const float den = std::sqrt(vh) + feps;
+        const float step = flr * (mh / den);
+        r.p[i] = p - step;
+        r.m[i] = m;
+        r.v[i] = v;
+    }
+}
+
+static std::vector<float> grad_of(size_t n, int seed) {
+    std::vector<float> g(n);
+    uint32_t x = 2463534242u + (uint32_t)seed * 7919u;
+    for (size_t i = 0; i < n; ++i) {
+        x ^= x << 13;
+        x ^= x >> 17;
+        x ^= x << 5;
+        g[i] = ((float)(x & 0xFFFFFF) / 16777216.0f - 0.5f) * 0.02f;
+    }
+    return g;
+}
+
+static void run(bool decoupled) {
+    const std::string tag = decoupled ? "AdamW" : "Adam";
+    ParamArena arena(ttp::Mode::FP32);
+    MLP model(64, 128, 10, arena);  // W1, b1, W2, b2 (decay on the weights)
+    auto params = model.parameters();
+    std::vector<Ref> ref;
+    for (auto& p : params) {
+        Ref r;
+        r.p = p->master();
+        r.m.assign(p->numel(), 0.0f);
+        r.v.assign(p->numel(), 0.0f);
+        ref.push_back(r);
+    }
+    const double lr = 1e-2, wd = decoupled ? 0.1 : 0.0;
+    Adam* opt = decoupled ? new AdamW(params, (float)lr, {0.9, 0.95}, 1e-8f, (float)wd)
+                          : new Adam(params, (float)lr, {0.9, 0.95}, 1e-8f);
+    const double flr = (double)(float)lr, fwd = (double)(float)wd;
+    for (uint64_t t = 1; t <= 5; ++t) {
+        opt->zero_grad();
+        for (size_t k = 0; k < params.size(); ++k) {
+            auto g = grad_of(params[k]->numel(), (int)(t * 10 + k));
+            params[k]->grad = g;
+            adam_ref(ref[k], g, flr, 0.9, 0.95, (double)1e-8f, t, fwd, k % 2 == 0);
+        }
+        opt->step();
+    }
+    for (size_t k = 0; k < params.size(); ++k) {
+        test::assert_bits(params[k]->master(), ref[k].p, tag + " param " + std::to_string(k));
+        test::assert_bits(params[k]->store().state(TTP_BUF_EXP_AVG, params[k]->index), ref[k].m,
+                          tag + " exp_avg " + std::to_string(k));
+        test::assert_bits(params[k]->store().state(TTP_BUF_EXP_AVG_SQ, params[k]->index),
+                          ref[k].v, tag + " exp_avg_sq " + std::to_string(k));
+    }
+    test::check(params[0]->store().step_count() == 5, tag + ": step count 5");
+    delete opt;
+}
+
+int main() {
+    test::DeviceGuard dg;
+    run(false);
+    run(true);
+    // py/optim.py:33-41 validation
+    ParamArena arena;
+    Linear l(4, 4, arena);
+    int thrown = 0;
+    try { Adam a(l.parameters(), 0.0f); } catch (const std::invalid_argument&) { ++thrown; }
+    try { Adam a(l.parameters(), 1e-3f, {0.9, 0.999}, 0.0f); } catch (const std::invalid_argument&) { ++thrown; }
+    try { Adam a(l.parameters(), 1e-3f, {1.1, 0.9}); } catch (const std::invalid_argument&) { ++thrown; }
+    try { Adam a(l.parameters(), 1e-3f, {0.9, 1.0}); } catch (const std::invalid_argument&) { ++thrown; }
+    test::check(thrown == 4, "Adam validation throws std::invalid_argument (" + std::to_string(thrown) + "/4)");
+    return test::finish("test_adam");
+}

@@ -1,0 +1,77 @@
+// test_traced.cpp — the traced layers' optimizer surface: TracedSGD({layers}, lr).step()
+// (autograd/traced/optim.hpp:15-29), per-module sgd_step(lr) (autograd/traced/nn.hpp:93-96,
+// 272-275, 317-321) and sgd_update (autograd/traced/ops.hpp:132-134).  Each is
+// `w - lr*dw` with one rounding per op; each call touches exactly its own tensors.
+#include "autograd/traced.hpp"
+#include "common.hpp"
+
+using autograd::ParamArena;
+using autograd::ValuePtr;
+
+static std::vector<float> ramp(size_t n, float a, float b) {
+    std::vector<float> v(n);
+    for (size_t i = 0; i < n; ++i) v[i] = a + b * (float)(i % 97);
+    return v;
+}
+
+static std::vector<float> sgd_ref(const std::vector<float>& w, const std::vector<float>& g,
+                                  float lr) {
+    std::vector<float> out(w.size());
+    for (size_t i = 0; i < w.size(); ++i) {
+        const float update = g[i] * lr;
+        out[i] = w[i] - update;
+    }
+    return out;
+}
+
+int main() {
+    test::DeviceGuard dg;
+    ParamArena arena(ttp::Mode::FP32);
+    traced::TracedLinear l1(64, 32, 0.01f, arena), l2(32, 10, 0.01f, arena);
+    traced::TracedLayerNorm ln(32, arena);
+    traced::TracedEmbedding emb(65, 32, 0.02f, arena);
+
+    // traced layers pre-allocate their grads: they exist (zero) before any backward
+    test::check(l1.weight->grad.has_value(), "traced grads are pre-allocated");
+
+    std::vector<ValuePtr> all = {l1.weight, l1.bias, l2.weight, l2.bias,
+                                 ln.gamma,  ln.beta, emb.weight};
+    std::vector<std::vector<float>> w, g;
+    for (size_t k = 0; k < all.size(); ++k) {
+        w.push_back(all[k]->master());
+        g.push_back(ramp(all[k]->numel(), 0.5f + (float)k, 0.003f));
+        all[k]->grad = g.back();  // what the backward pass writes into the grad buffers
+    }
+
+    // 1) TracedSGD over both linears: one launch, l1/l2 change, ln/emb do not
+    traced::TracedSGD opt({&l1, &l2}, 0.05f);
+    opt.step();
+    for (size_t k = 0; k < 4; ++k) w[k] = sgd_ref(w[k], g[k], 0.05f);
+    for (size_t k = 0; k < all.size(); ++k)
+        test::assert_bits(all[k]->master(), w[k], "TracedSGD tensor " + std::to_string(k));
+
+    // 2) per-module sgd_step: LayerNorm then Embedding
+    ln.sgd_step(0.1f);
+    w[4] = sgd_ref(w[4], g[4], 0.1f);
+    w[5] = sgd_ref(w[5], g[5], 0.1f);
+    emb.sgd_step(0.2f);
+    w[6] = sgd_ref(w[6], g[6], 0.2f);
+    l2.sgd_step(0.3f);
+    w[2] = sgd_ref(w[2], g[2], 0.3f);
+    w[3] = sgd_ref(w[3], g[3], 0.3f);
+    for (size_t k = 0; k < all.size(); ++k)
+        test::assert_bits(all[k]->master(), w[k], "sgd_step tensor " + std::to_string(k));
+
+    // 3) free function sgd_update on one tensor
+    traced::sgd_update(l1.bias, 0.7f);
+    w[1] = sgd_ref(w[1], g[1], 0.7f);
+    for (size_t k = 0; k < all.size(); ++k)
+        test::assert_bits(all[k]->master(), w[k], "sgd_update tensor " + std::to_string(k));
+
+    // layer init values of the reference's traced layers: LayerNorm gamma 1, beta 0
+    ParamArena fresh(ttp::Mode::FP32);
+    traced::TracedLayerNorm ln2(8, fresh);
+    test::assert_all_close(ln2.gamma->data(), 1.0f, 0.0f, "LayerNorm gamma init");
+    test::assert_all_close(ln2.beta->data(), 0.0f, 0.0f, "LayerNorm beta init");
+    return test::finish("test_traced");
+}

@@ -82,9 +82,10 @@ def device_grads(store, gen, std, scale=1.0, heavy_frac=0.0, heavy_std=1.0, inf_
 
 
 def compare_state(store, ref, which=("master", "exp_avg", "exp_avg_sq", "param"), max_ulp=0,
-                  mask=None):
-    """Max ulp difference per buffer (padding excluded); asserts <= max_ulp, and bf16 params
-    bit-exact."""
+                  mask=None, slice_elems=1 << 25):
+    """Max ulp difference per buffer (padding excluded), compared in slices so that
+    billion-element stores do not need several full-size temporaries; asserts <= max_ulp,
+    and bf16 params bit-exact."""
     from ttperf import _lib as L
     bufs = {"master": L.BUF_MASTER, "exp_avg": L.BUF_EXP_AVG, "exp_avg_sq": L.BUF_EXP_AVG_SQ,
             "param": L.BUF_PARAM, "momentum": L.BUF_MOMENTUM}
@@ -92,16 +93,26 @@ def compare_state(store, ref, which=("master", "exp_avg", "exp_avg_sq", "param")
     if mask is None:
         mask = pad_mask(store)
     for name in which:
-        print(f"  compare {name} ({store.total} elements)", flush=True)
         got = store.download(bufs[name])
         want = getattr(ref, name)
+        worst, nbad = 0, 0
+        for a in range(0, store.total, slice_elems):
+            b = min(store.total, a + slice_elems)
+            m = mask[a:b]
+            if got.dtype == np.uint16:
+                nbad += int(np.count_nonzero((got[a:b] != want[a:b]) & m))
+            else:
+                d = f32_ulp_diff(got[a:b][m], want[a:b][m])
+                if d.size:
+                    worst = max(worst, int(d.max()))
+                    nbad += int(np.count_nonzero(d))
+        out[name] = nbad if got.dtype == np.uint16 else worst
+        print(f"  compare {name} ({store.total} elements): "
+              + (f"{nbad} bf16 values differ" if got.dtype == np.uint16
+                 else f"max {worst} ulp, {nbad} values differ"), flush=True)
         if got.dtype == np.uint16:
-            bad = int(np.count_nonzero((got != want) & mask))
-            out[name] = bad
-            assert bad == 0, f"{name}: {bad} bf16 values differ"
+            assert nbad == 0, f"{name}: {nbad} bf16 values differ"
         else:
-            d = f32_ulp_diff(got[mask], want[mask])
-            out[name] = int(d.max()) if d.size else 0
-            assert out[name] <= max_ulp, f"{name}: max {out[name]} ulp (> {max_ulp}), " \
-                                         f"{int(np.count_nonzero(d))} values differ"
+            assert worst <= max_ulp, f"{name}: max {worst} ulp (> {max_ulp}), {nbad} values differ"
+        del got
     return out

@@ -1,0 +1,163 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports every entry point
+include/ttperf/ttperf.h declares, the ctypes and C struct layouts agree, argument errors are
+reported as the reference reports them (ValueError in py/optim.py), and the C++ drop-in
+headers compile against the library."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import pytest
+
+from conftest import REPO
+
+HEADER = os.path.join(REPO, "include", "ttperf", "ttperf.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ttp_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from ttperf import _lib as L
+    declared = _declared_functions()
+    assert len(declared) >= 30
+    missing = [n for n in declared if not hasattr(L.lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    out = subprocess.run(["nm", "-D", "--defined-only", L.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (ttp_[a-z0-9_]+)$", out, flags=re.M))
+    assert set(declared) <= exported
+    # and the ctypes binding describes each of them
+    assert set(declared) == set(L.SIGNATURES)
+
+
+def test_abi_version():
+    from ttperf import _lib as L
+    assert L.lib.ttp_abi_version() == 1
+
+
+def test_struct_layouts_match_the_header(tmp_path):
+    """Compiles a C probe against the header and compares sizeof/offsetof with ctypes."""
+    from ttperf import _lib as L
+    structs = {"ttp_tensor_desc": L.TensorDesc, "ttp_adam_hparams": L.AdamHParams,
+               "ttp_sgd_hparams": L.SgdHParams, "ttp_scaler_config": L.ScalerConfig,
+               "ttp_step_report": L.StepReport}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "ttperf/ttperf.h"',
+             "int main(void) {"]
+    for cname, ct in structs.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _ in ct._fields_:
+            lines.append(f'printf("{cname}.{f} %zu\\n", offsetof({cname}, {f}));')
+    lines.append("return 0; }")
+    src = tmp_path / "probe.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-std=c11", "-I", os.path.join(REPO, "include"), "-o", str(exe),
+                    str(src)], check=True)
+    got = dict(line.rsplit(" ", 1) for line in
+               subprocess.run([str(exe)], capture_output=True, text=True,
+                              check=True).stdout.splitlines())
+    for cname, ct in structs.items():
+        assert int(got[f"{cname} size"]) == C.sizeof(ct), cname
+        for f, _ in ct._fields_:
+            assert int(got[f"{cname}.{f}"]) == getattr(ct, f).offset, f"{cname}.{f}"
+
+
+def test_c_abi_argument_errors_without_a_device():
+    from ttperf import _lib as L
+    lib = L.lib
+    h = C.c_void_p()
+    d = (L.TensorDesc * 1)()
+    d[0].numel = 10
+    assert lib.ttp_create(0, d, 1, 7, C.byref(h)) == L.ERR_INVALID  # unknown mode
+    assert b"mode" in lib.ttp_last_error()
+    d[0].flags = 0x80
+    assert lib.ttp_create(0, d, 1, L.MODE_FP32, C.byref(h)) == L.ERR_INVALID  # unknown flag
+    assert lib.ttp_create(0, d, 1, L.MODE_FP32, None) == L.ERR_INVALID
+    hp = L.AdamHParams(lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8)
+    assert lib.ttp_adam_step(None, C.byref(hp), None) == L.ERR_INVALID
+    assert b"null context" in lib.ttp_last_error()
+    assert lib.ttp_sync(None) == L.ERR_INVALID
+    assert lib.ttp_destroy(None) == L.OK
+    n = C.c_int(-1)
+    assert lib.ttp_device_count(C.byref(n)) == L.OK and n.value >= 0
+
+
+def test_store_without_a_device_fails_loudly():
+    import ttperf
+    from ttperf import _lib as L
+    if ttperf.device_count() > 0:
+        pytest.skip("a GPU is visible")
+    with pytest.raises(ttperf.TTPError) as e:
+        ttperf.ParamStore([(4, 4)])
+    assert e.value.code == L.ERR_NO_DEVICE
+
+
+# ---- the reference's validation cases (tests/adam_optimizer.py:126-151,
+#      tests/sgd_optimizer.py:112-122, py/optim.py:9-16,33-41) -----------------------------
+
+@pytest.mark.parametrize("kw", [dict(lr=0.0), dict(lr=-1.0), dict(eps=0.0), dict(betas=(0.9,)),
+                                dict(betas=(1.1, 0.9)), dict(betas=(0.9, 1.0)),
+                                dict(betas=0.9), dict(weight_decay=-0.1)])
+def test_adam_validation(kw):
+    import ttperf
+    for cls in (ttperf.Adam, ttperf.AdamW):
+        with pytest.raises(ValueError):
+            cls([], **kw)
+
+
+@pytest.mark.parametrize("kw", [dict(lr=0.0), dict(lr=-1.0), dict(lr=0.1, momentum=-0.5),
+                                dict(lr=0.1, weight_decay=-1.0), dict(lr=0.1, nesterov=True),
+                                dict(lr=0.1, momentum=0.9, dampening=0.1, nesterov=True)])
+def test_sgd_validation(kw):
+    import ttperf
+    with pytest.raises(ValueError):
+        ttperf.SGD([], **kw)
+
+
+def test_sgd_lr_is_keyword_only():
+    import ttperf
+    with pytest.raises(TypeError):
+        ttperf.SGD([], 0.1)  # py/optim.py:7 `SGD(params, *, lr)`
+
+
+def test_adam_defaults_match_reference():
+    import ttperf
+    a = ttperf.Adam([])
+    assert (a.lr, a.beta1, a.beta2, a.eps) == (1e-3, 0.9, 0.999, 1e-8)  # py/optim.py:31
+
+
+def test_non_tensor_params_raise_at_step_and_are_skipped_by_zero_grad():
+    import ttperf
+    for cls, kw in ((ttperf.SGD, dict(lr=0.1)), (ttperf.Adam, {})):
+        opt = cls([object()], **kw)  # construction accepts anything (py/optim.py:8,32)
+        opt.zero_grad()              # skips non-Tensors (py/optim.py:24-27,89-92)
+        with pytest.raises(ValueError, match="expects Tensor parameters"):
+            opt.step()
+
+
+def test_cpp_dropin_headers_compile():
+    """The C++ drop-in tests (tests/cpp) build against include/ and the library."""
+    subprocess.run(["make", "-s", "-C", os.path.join(REPO, "tests", "cpp")], check=True)
+    for t in ("test_sgd", "test_traced", "test_adam", "train_mlp"):
+        assert os.access(os.path.join(REPO, "tests", "cpp", "build", t), os.X_OK)
+
+
+def test_product_code_never_touches_the_oracle():
+    """Only tests/, smoke() and bench.py's cpu_baseline may load oracle/."""
+    pkg = os.path.join(REPO, "tt-perf_amd")
+    hits = []
+    for root, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".hpp", ".cpp", ".h")) or f == "Makefile":
+                text = open(os.path.join(root, f), errors="replace").read()
+                if re.search(r"import oracle|from oracle|ttp_oracle|\borc_[a-z]|oracle/", text):
+                    hits.append(os.path.join(root, f))
+    for root, _, files in os.walk(os.path.join(REPO, "include")):
+        for f in files:
+            if re.search(r"ttp_oracle|orc_", open(os.path.join(root, f)).read()):
+                hits.append(os.path.join(root, f))
+    assert not hits, hits

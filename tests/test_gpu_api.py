@@ -1,0 +1,396 @@
+"""GPU tests of the optimizer API and of the edge cases, through the C ABI (libttperf_hip),
+against the CPU oracle on identical inputs.
+
+The first group restates the reference's own optimizer tests on this engine:
+tests/adam_optimizer.py:25-123 (seeds 31-34: one and two Adam steps of a 32x32 Linear against
+the closed form `_adam_step_ref`, zero_grad clears, None grads are skipped) and
+tests/sgd_optimizer.py:15-110 (seeds 21-24, bf16).  The reference compares with atol/rtol
+1e-1 / 5e-2 because TTNN runs in bf16; here the closed form is met to fp32 rounding (the
+closed form's own op order differs from py/optim.py's in the last bits) and the oracle
+bit for bit.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import f32_ulp_diff
+from gpu_util import LONG, compare_state, device_grads, make_pair, torch_mod
+
+pytestmark = pytest.mark.gpu
+
+
+def _linear_store(seed, mode):
+    """A 32x32 Linear of py/nn.py:28-37: weight [in, out] ~ randn * 1/sqrt(in)."""
+    import ttperf
+    torch = torch_mod()
+    torch.manual_seed(seed)
+    x = torch.randn(32, 32)
+    w0 = torch.randn(32, 32) * (1.0 / np.sqrt(32.0))
+    store = ttperf.ParamStore([(32, 32)], mode=mode)
+    if mode == "mixed":
+        w0 = w0.to(torch.bfloat16).float()  # the reference holds bf16 weights
+    store.tensors[0].set_data(w0.numpy())
+    return store, store.tensors[0], x, w0
+
+
+def _adam_step_ref(weight, grad, lr, betas, eps, step, m, v):
+    # the closed form of tests/adam_optimizer.py:15-22
+    beta1, beta2 = betas
+    m = beta1 * m + (1.0 - beta1) * grad
+    v = beta2 * v + (1.0 - beta2) * (grad * grad)
+    m_hat = m / (1.0 - (beta1 ** step))
+    v_hat = v / (1.0 - (beta2 ** step))
+    weight = weight - lr * m_hat / (v_hat.sqrt() + eps)
+    return weight, m, v
+
+
+def _oracle_for(store, mode_mixed=False):
+    ref = O.OracleStore([t.numel for t in store.tensors],
+                        flags=[int(t.decay) for t in store.tensors],
+                        mode=O.MODE_MIXED if mode_mixed else O.MODE_FP32, nthreads=4)
+    ref.master[:] = store.download(2)  # BUF_MASTER
+    if mode_mixed:
+        ref.param[:] = O.bf16_rne(ref.master)
+    return ref
+
+
+def test_adam_step_matches_closed_form():
+    import ttperf
+    torch = torch_mod()
+    store, w, x, w0 = _linear_store(31, "fp32")
+    ref = _oracle_for(store)
+    grad = x.t() @ torch.ones(32, 32)  # dW of y = x @ W with dY = ones
+    w.grad = grad.numpy()
+    ref.set_grad(0, grad.numpy())
+    opt = ttperf.Adam(store.parameters(), lr=0.1, betas=(0.9, 0.999), eps=1e-8)
+    opt.step()
+    ref.adam_step(lr=0.1, betas=(0.9, 0.999), eps=1e-8, decoupled=False)
+    w1 = w.numpy()
+    w_ref, _, _ = _adam_step_ref(w0, grad, 0.1, (0.9, 0.999), 1e-8, 1, torch.zeros(32, 32),
+                                 torch.zeros(32, 32))
+    assert np.allclose(w1, w_ref.numpy(), atol=1e-6, rtol=1e-6)  # reference: 1e-1
+    assert f32_ulp_diff(w1.ravel(), ref.master[:1024]).max() == 0
+
+
+def test_adam_two_steps_match_closed_form():
+    import ttperf
+    torch = torch_mod()
+    store, w, x, w0 = _linear_store(32, "fp32")
+    ref = _oracle_for(store)
+    opt = ttperf.Adam(store.parameters(), lr=0.1, betas=(0.9, 0.999), eps=1e-8)
+
+    def grad_at(weight):  # y = tanh(x @ W), dY = ones (tests/adam_optimizer.py:61-69)
+        z = torch.tanh(x @ weight)
+        return x.t() @ (1 - z * z)
+
+    m = torch.zeros(32, 32)
+    v = torch.zeros(32, 32)
+    wt = w0.clone()
+    for step in (1, 2):
+        g = grad_at(torch.from_numpy(w.numpy().copy()))
+        w.grad = g.numpy()
+        ref.set_grad(0, g.numpy())
+        opt.step()
+        opt.zero_grad()
+        ref.adam_step(lr=0.1, betas=(0.9, 0.999), eps=1e-8, decoupled=False)
+        wt, m, v = _adam_step_ref(wt, g, 0.1, (0.9, 0.999), 1e-8, step, m, v)
+    assert np.allclose(w.numpy(), wt.numpy(), atol=1e-5, rtol=1e-5)
+    assert f32_ulp_diff(w.numpy().ravel(), ref.master[:1024]).max() == 0
+    assert store.step_count == 2
+
+
+@pytest.mark.parametrize("cls", ["SGD", "Adam", "AdamW"])
+def test_zero_grad_clears(cls):
+    import ttperf
+    store, w, x, _ = _linear_store(33, "fp32")
+    w.grad = np.ones((32, 32), np.float32)
+    assert w.grad is not None
+    kw = dict(lr=0.1)
+    getattr(ttperf, cls)(store.parameters(), **kw).zero_grad()
+    assert w.grad is None
+
+
+@pytest.mark.parametrize("cls", ["SGD", "Adam", "AdamW"])
+def test_skips_none_grad(cls):
+    import ttperf
+    store, w, x, _ = _linear_store(34, "mixed")
+    before = store.download(0).copy()  # bf16 bits of the weight
+    master = w.master().copy()
+    w.grad = np.full((32, 32), 0x3F80, np.uint16)  # a grad exists ...
+    w.grad = None                                   # ... and is dropped
+    getattr(ttperf, cls)(store.parameters(), lr=0.1).step()
+    assert np.array_equal(store.download(0), before)
+    assert np.array_equal(w.master().view(np.uint32), master.view(np.uint32))
+
+
+def test_sgd_step_bf16_matches_closed_form():
+    """tests/sgd_optimizer.py:15-40: bf16 weights, w1 = w0 - 0.1 * (x^T @ ones)."""
+    import ttperf
+    torch = torch_mod()
+    store, w, x, w0 = _linear_store(21, "mixed")
+    ref = _oracle_for(store, mode_mixed=True)
+    gb = x.to(torch.bfloat16).t() @ torch.ones(32, 32, dtype=torch.bfloat16)
+    bits = gb.contiguous().view(torch.int16).numpy().view(np.uint16)
+    w.grad = bits
+    ref.set_grad(0, bits)
+    ttperf.SGD(store.parameters(), lr=0.1).step()
+    ref.sgd_step(lr=0.1)
+    w_ref = w0 - 0.1 * gb.float()
+    assert np.allclose(w.numpy(), w_ref.numpy(), atol=5e-2, rtol=5e-2)  # the reference's bar
+    assert np.array_equal(store.download(0), ref.param[:1024])        # bit-exact bf16
+
+
+def test_sgd_two_steps_bf16():
+    """tests/sgd_optimizer.py:43-78: two steps with tanh-derived grads, bf16."""
+    import ttperf
+    torch = torch_mod()
+    store, w, x, w0 = _linear_store(22, "mixed")
+    ref = _oracle_for(store, mode_mixed=True)
+    opt = ttperf.SGD(store.parameters(), lr=0.1)
+    wt = w0.to(torch.bfloat16)
+    xb = x.to(torch.bfloat16)
+    for _ in range(2):
+        z = torch.tanh(xb @ torch.from_numpy(w.numpy().copy()).to(torch.bfloat16))
+        g = xb.t() @ (1 - z * z)
+        bits = g.contiguous().view(torch.int16).numpy().view(np.uint16)
+        w.grad = bits
+        ref.set_grad(0, bits)
+        opt.step()
+        ref.sgd_step(lr=0.1)
+        wt = wt - 0.1 * g
+    assert np.allclose(w.numpy(), wt.float().numpy(), atol=5e-2, rtol=5e-2)
+    assert np.array_equal(store.download(0), ref.param[:1024])
+
+
+# ---- SGD family at config 2's shapes, both precision modes -------------------------------
+
+SGD_CASES = {
+    "plain": dict(lr=1e-2),
+    "momentum": dict(lr=1e-2, momentum=0.9),
+    "nesterov": dict(lr=1e-2, momentum=0.9, nesterov=True),
+    "damp_wd_clip": dict(lr=1e-2, momentum=0.9, dampening=0.1, weight_decay=0.01,
+                         max_grad_norm=1.0),
+}
+
+
+@pytest.mark.parametrize("mode", [O.MODE_MIXED, O.MODE_FP32])
+@pytest.mark.parametrize("case", list(SGD_CASES))
+def test_sgd_family_parity(case, mode):
+    from ttperf import configs
+    torch = torch_mod()
+    _, shapes, decay, _ = configs.table("nanogpt_char")
+    store, ref = make_pair(shapes, decay, mode, seed=40)
+    gen = torch.Generator(device="cuda").manual_seed(41)
+    hp = SGD_CASES[case]
+    for step in range(3):
+        host = device_grads(store, gen, 1e-1 if hp.get("max_grad_norm") else 1e-3)
+        ref.grad[:] = host
+        for i in range(ref.n):
+            ref.set_has_grad(i, True)
+        r = store.sgd_step(report=True, **hp)
+        e = ref.sgd_step(**{k: v for k, v in hp.items()})
+        assert r["step"] == e["step"] == step + 1
+        if hp.get("max_grad_norm"):
+            assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
+            assert r["clip_coef"] < 1.0
+    which = ["master"] + (["param"] if mode == O.MODE_MIXED else [])
+    if hp.get("momentum"):
+        which.append("momentum")
+    compare_state(store, ref, which=tuple(which), max_ulp=2 if hp.get("max_grad_norm") else 0)
+
+
+# ---- subsets, missing grads, loss-scale growth, ragged and empty tables --------------------
+
+def test_subset_step_touches_only_listed_tensors():
+    """A module's sgd_step / an optimizer over some of a store's tensors: one launch over
+    the listed tensors; the clip norm covers the listed tensors only."""
+    torch = torch_mod()
+    shapes = [(300, 7), (64,), (129, 33), (5,), (2048,), (1, 2049)]
+    decay = [True, False, True, False, False, True]
+    store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=50)
+    gen = torch.Generator(device="cuda").manual_seed(51)
+    host = device_grads(store, gen, 1e-2)
+    ref.grad[:] = host
+    listed = [0, 3, 5]
+    for i in range(ref.n):
+        ref.set_has_grad(i, i in listed)  # the oracle sees only the listed tensors
+    hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=0.05)
+    r = store.adam_step(report=True, indices=listed, **hp)
+    e = ref.adam_step(**hp)
+    assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-9 * e["grad_norm"]
+    compare_state(store, ref, max_ulp=2)
+    r = store.sgd_step(report=True, indices=[1, 4], lr=0.5)
+    for i in range(ref.n):
+        ref.set_has_grad(i, i in (1, 4))
+    ref.sgd_step(lr=0.5)
+    compare_state(store, ref, which=("master", "param"), max_ulp=2)
+
+
+def test_none_grad_tensors_untouched_and_out_of_the_norm():
+    torch = torch_mod()
+    shapes = [(1000,), (64, 64), (77,), (3, 3)]
+    store, ref = make_pair(shapes, [False, True, False, True], O.MODE_FP32, seed=52)
+    gen = torch.Generator(device="cuda").manual_seed(53)
+    host = device_grads(store, gen, 1.0)
+    ref.grad[:] = host
+    for i in range(ref.n):
+        ref.set_has_grad(i, True)
+    store.tensors[1].grad = None
+    ref.set_has_grad(1, False)
+    before = store.tensors[1].master().copy()
+    hp = dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
+    r = store.adam_step(report=True, **hp)
+    e = ref.adam_step(**hp)
+    assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-9 * e["grad_norm"]
+    assert np.array_equal(store.tensors[1].master(), before)
+    compare_state(store, ref, which=("master", "exp_avg", "exp_avg_sq"), max_ulp=2)
+    assert abs(store.grad_norm() - e["grad_norm"]) <= 1e-9 * e["grad_norm"]
+
+
+def test_scaler_growth_and_backoff_sequence():
+    """Tracker forced to growth_interval - 1 through the ABI setter: the next clean step
+    doubles the scale; an overflow step halves it, skips, and keeps t."""
+    torch = torch_mod()
+    shapes = [(4096,), (33, 65)]
+    store, ref = make_pair(shapes, [False, True], O.MODE_MIXED, seed=54)
+    store.configure_scaler(True, init_scale=1024.0, growth_interval=2000)
+    ref.configure_scaler(True, 1024.0, growth_interval=2000)
+    store.set_scaler_state(1024.0, 1999)
+    ref.set_scaler_state(1024.0, 1999)
+    gen = torch.Generator(device="cuda").manual_seed(55)
+    hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+    expect = [(2048.0, 0, 1, 0), (2048.0, 1, 2, 0), (1024.0, 0, 2, 1), (1024.0, 1, 3, 0)]
+    for k, (scale, tracker, t, skipped) in enumerate(expect):
+        host = device_grads(store, gen, 1e-3, scale=ref.scale,
+                            inf_at=store.offsets[1] + 7 if k == 2 else None)
+        ref.grad[:] = host
+        for i in range(ref.n):
+            ref.set_has_grad(i, True)
+        r = store.adam_step(report=True, **hp)
+        e = ref.adam_step(**hp)
+        assert (r["scale"], r["growth_tracker"], r["step"], r["skipped"]) == \
+               (scale, tracker, t, skipped) == \
+               (e["scale"], e["growth_tracker"], e["step"], e["skipped"])
+    compare_state(store, ref, max_ulp=0)
+
+
+def test_ragged_sizes_and_empty_tensors():
+    """Partial vectors (sizes not a multiple of 4/8), chunk boundaries (2047..2049, 4097),
+    single elements and zero-element tensors, with loss scaling + clipping."""
+    torch = torch_mod()
+    sizes = [1, 3, 0, 63, 64, 65, 127, 2047, 2048, 2049, 4097, 0, 5, 10007]
+    shapes = [(n,) for n in sizes]
+    decay = [i % 2 == 0 for i in range(len(sizes))]
+    for mode in (O.MODE_MIXED, O.MODE_FP32):
+        store, ref = make_pair(shapes, decay, mode, seed=56)
+        store.configure_scaler(True, init_scale=256.0)
+        ref.configure_scaler(True, 256.0)
+        gen = torch.Generator(device="cuda").manual_seed(57)
+        hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=0.1)
+        for _ in range(3):
+            host = device_grads(store, gen, 1e-2, scale=ref.scale)
+            ref.grad[:] = host
+            for i in range(ref.n):
+                ref.set_has_grad(i, True)
+            r = store.adam_step(report=True, **hp)
+            e = ref.adam_step(**hp)
+            assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-9 * e["grad_norm"]
+        compare_state(store, ref, max_ulp=2)
+
+
+def test_empty_store_and_no_grads():
+    """No tensors at all, and tensors none of which has a grad: a step launches no update,
+    touches nothing, and still advances t (py/optim.py:50 increments before the loop)."""
+    import ttperf
+    empty = ttperf.ParamStore([], mode="mixed")
+    r = empty.adam_step(report=True, lr=1e-3, max_grad_norm=1.0)
+    assert r["step"] == 1 and r["grad_norm"] == 0.0
+    store = ttperf.ParamStore([(10,), (20,)], mode="fp32")
+    store.tensors[0].set_data(np.arange(10, dtype=np.float32))
+    r = store.sgd_step(report=True, lr=0.1)
+    assert r["step"] == 1
+    assert np.array_equal(store.tensors[0].numpy(), np.arange(10, dtype=np.float32))
+
+
+def test_nan_grad_without_scaler_propagates_like_the_oracle():
+    torch = torch_mod()
+    store, ref = make_pair([(100,), (50,)], [False, False], O.MODE_MIXED, seed=58)
+    gen = torch.Generator(device="cuda").manual_seed(59)
+    host = device_grads(store, gen, 1e-2)
+    host[store.offsets[1] + 3] = 0x7FC0  # one NaN gradient
+    store.upload(1, 0xFFFFFFFF, host)
+    ref.grad[:] = host
+    for i in range(ref.n):
+        ref.set_has_grad(i, True)
+    hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, max_grad_norm=1.0)
+    r = store.adam_step(report=True, **hp)
+    e = ref.adam_step(**hp)
+    assert r["found_inf"] == e["found_inf"] == 1 and r["skipped"] == e["skipped"] == 0
+    assert np.isnan(r["grad_norm"]) and np.isnan(e["grad_norm"])
+    compare_state(store, ref, max_ulp=0)
+
+
+def test_context_stream_and_timing():
+    """Steps on a torch side stream and on the context's own stream agree bit for bit; the
+    timing API counts one norm pass and one update per step."""
+    import ttperf
+    from ttperf import _lib as L
+    torch = torch_mod()
+    shapes = [(5000,), (64, 128)]
+    outs = []
+    for use_side in (False, True):
+        store, ref = make_pair(shapes, [False, True], O.MODE_MIXED, seed=60)
+        if use_side:
+            s = torch.cuda.Stream()
+            store.set_stream(s)
+        else:
+            store.set_stream(None)
+        gen = torch.Generator(device="cuda").manual_seed(61)
+        device_grads(store, gen, 1e-2)
+        store.timing(True)
+        for _ in range(4):
+            store.adam_step(lr=1e-3, betas=(0.9, 0.95), max_grad_norm=0.5, weight_decay=0.1)
+        ms, n = store.timing_collect(L.KERNEL_UPDATE)
+        ms2, n2 = store.timing_collect(L.KERNEL_NORM)
+        assert n == 4 and n2 == 4 and ms > 0 and ms2 > 0
+        outs.append(store.download(L.BUF_MASTER))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
+# ---- config 5: GPT-2 XL shapes, full fp32, AdamW + clip then SGD-momentum ------------------
+
+def test_cfg5_gpt2_xl_fp32_adamw_then_sgd_momentum():
+    """Config 5: 580 tensors, 1.56B fp32 params (~25 GB resident with m and v, ~31 GB with
+    the momentum buffer).  Grads N(0, 1e-3) with 1% drawn from N(0, 1) (clip path active).
+    AdamW lr 1.5e-4 betas (0.9, 0.95) wd 0.1 clip 1.0, then SGD momentum 0.9 on the same
+    buffers.  2 + 2 steps by default, 10 + 10 with TTP_LONG_TESTS=1."""
+    from ttperf import configs
+    torch = torch_mod()
+    _, shapes, decay, numels = configs.table("gpt2_1558m")
+    assert len(shapes) == 580 and sum(numels) == 1557611200
+    store, ref = make_pair(shapes, decay, O.MODE_FP32, seed=70)
+    gen = torch.Generator(device="cuda").manual_seed(71)
+    steps = 10 if LONG else 2
+    hp = dict(lr=1.5e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
+    for step in range(steps):
+        host = device_grads(store, gen, 1e-3, heavy_frac=0.01, heavy_std=1.0)
+        ref.grad[:] = host
+        del host
+        for i in range(ref.n):
+            ref.set_has_grad(i, True)
+        r = store.adam_step(report=True, **hp)
+        e = ref.adam_step(**hp)
+        assert r["clip_coef"] < 1.0
+        assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
+        print(f"cfg5 adamw step {step}: norm {r['grad_norm']:.6f}", flush=True)
+    compare_state(store, ref, which=("master", "exp_avg", "exp_avg_sq"), max_ulp=2)
+    sgd = dict(lr=1e-3, momentum=0.9, max_grad_norm=1.0)
+    for step in range(steps):
+        host = device_grads(store, gen, 1e-3, heavy_frac=0.01, heavy_std=1.0)
+        ref.grad[:] = host
+        del host
+        r = store.sgd_step(report=True, **sgd)
+        e = ref.sgd_step(**sgd)
+        assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
+        print(f"cfg5 sgd-m step {step}: norm {r['grad_norm']:.6f}", flush=True)
+    compare_state(store, ref, which=("master", "momentum"), max_ulp=2)

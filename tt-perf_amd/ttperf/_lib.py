@@ -100,7 +100,24 @@ class TTPValueError(TTPError, ValueError):
     """Argument errors: the cases py/optim.py raises ValueError for."""
 
 
+def _bind_one_hip_runtime():
+    """Load torch (when installed) before libttperf_hip.
+
+    torch ships its own HIP/HSA runtimes (SONAMEs libamdhip64.so.7, libhsa-runtime64.so.1)
+    and loads them by file name from its own lib directory.  The dynamic loader satisfies
+    this library's DT_NEEDED entries with an already-loaded object of the same SONAME, so
+    loading torch first gives one HIP runtime per process, shared by torch and this engine
+    (one device context, one set of streams, tensors and hipStream_t handles valid in both).
+    Loading this library first would instead map /opt/rocm's runtime and let torch map a
+    second copy, with two independent device contexts in one process."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def _load():
+    _bind_one_hip_runtime()
     if not os.path.exists(LIB_PATH):
         raise ImportError(
             f"libttperf_hip.so not found at {LIB_PATH}; build it with `make -C tt-perf_amd` "

@@ -36,9 +36,11 @@ class _Optimizer:
         return _group_by_store(self.params, self._name)
 
     def zero_grad(self):
-        # py/optim.py:89-92 -> Tensor.zero_grad (py/engine.py:141-142): grad = None.  A store
-        # fully owned by this optimizer is cleared with one fill (zeros + no grads).
-        for store, members in self._stores():
+        # py/optim.py:89-92 -> Tensor.zero_grad (py/engine.py:141-142): grad = None, and
+        # non-Tensor entries are skipped (step() is where they raise).  A store fully owned
+        # by this optimizer is cleared with one fill (zeros + no grads).
+        tensors = [p for p in self.params if isinstance(p, Tensor)]
+        for store, members in _group_by_store(tensors, self._name):
             if len(members) == len(store.tensors):
                 store.zero_grad(set_to_none=True)
             else:
