@@ -161,3 +161,13 @@ def test_product_code_never_touches_the_oracle():
             if re.search(r"ttp_oracle|orc_", open(os.path.join(root, f)).read()):
                 hits.append(os.path.join(root, f))
     assert not hits, hits
+
+
+def test_one_hip_runtime_is_mapped():
+    """ttperf loads torch's HIP runtime (when torch is installed) before libttperf_hip, so
+    the process maps a single libamdhip64 / libhsa-runtime64."""
+    import ttperf  # noqa: F401
+    maps = open("/proc/self/maps").read().splitlines()
+    for lib in ("libamdhip64", "libhsa-runtime64"):
+        paths = {line.split()[-1] for line in maps if lib in line}
+        assert len(paths) == 1, paths

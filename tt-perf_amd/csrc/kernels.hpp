@@ -1,8 +1,9 @@
 // kernels.hpp — gfx950 device code of libttperf_hip.
 //
 // One optimizer step over the flat store is at most three launches on one stream:
-//   norm_partials_kernel  reads only the gradients (2 B/param bf16, 4 B/param fp32): fp64 sum
-//                         of squares of the unscaled grads, one partial per block; no atomics
+//   norm_partials_kernel  reads only the gradients (2 B/param bf16, 4 B/param fp32) in 16 KiB
+//                         tiles: fp64 sum of squares of the unscaled grads, one partial per
+//                         block; no atomics
 //                         and no fences (a per-block device-scope fence + ticket costs ~50 ns
 //                         per block on MI355X, serialised, which tripled the pass's time);
 //   norm_finalize_kernel  one block: sums the partials in index order (deterministic),
@@ -12,12 +13,13 @@
 //   sgd_kernel            decay, the optimizer update and the bf16 copy.  Each element is
 //                         touched once; loads/stores are 16-byte (fp32 x4) and 8-byte (bf16 x4)
 //                         per lane, so every wave instruction covers a contiguous 1 KiB / 512 B
-//                         span, and each lane keeps two such vectors in flight.
+//                         span.
 // Work is a table of chunks of kChunk elements (the last chunk of a tensor is shorter; every
-// chunk starts on a 64-element boundary).  The update runs one block per chunk: blocks are
-// dispatched in chunk order, so the resident blocks sweep a narrow window of each buffer
-// (2048 resident blocks x 2048 elements), which keeps DRAM pages open; 16K-element chunks
-// or a persistent grid measured 6-12% slower.  No MFMA: nothing here is a contraction.
+// chunk starts on a 64-element boundary).  The update runs one 512-thread block per chunk,
+// one vector per lane, at most kUpdBlocksPerCU blocks per CU: blocks are dispatched in
+// chunk order, so the resident blocks sweep a narrow window of each buffer, which keeps
+// DRAM pages open.  16K-element chunks, a persistent grid, two or four vectors per lane, and
+// unlimited occupancy each measured 6-12% slower.  No MFMA: nothing here is a contraction.
 //
 // Arithmetic matches the oracle bit for bit: no contraction (-ffp-contract=off), IEEE
 // division and square root (HIP's correctly rounded fp32 div/sqrt), denormals kept.
@@ -28,10 +30,15 @@
 
 namespace ttp {
 
-constexpr int kBlock = 256;    // 4 wave64s
-constexpr int kVec = 4;        // elements per lane per vector
-constexpr int kUnroll = 2;     // vectors per lane per chunk in the update kernels
-constexpr uint32_t kChunk = kBlock * kVec * kUnroll;  // 2048 elements
+constexpr int kBlock = 256;     // 4 wave64s: norm pass, finalize and helper kernels
+constexpr int kUpdBlock = 512;  // 8 wave64s: update kernels
+constexpr int kVec = 4;         // elements per lane per vector
+constexpr uint32_t kChunk = kUpdBlock * kVec;  // 2048 elements: one vector per lane
+// Resident update blocks per CU.  The host reserves LDS_per_CU / kUpdBlocksPerCU bytes of
+// (unused) dynamic LDS per update block so that no more than this many are resident: 24
+// waves per CU sweep the HBM pages of the nine streams with fewer row conflicts than the
+// 32+ waves that registers alone would allow (measured: 554 us vs 622 us on GPT-2 124M).
+constexpr int kUpdBlocksPerCU = 3;
 constexpr uint32_t kChunkDecay = 1u;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -160,50 +167,53 @@ struct GradVec<float> {
     static __device__ __forceinline__ float at(const raw& w, int j) { return w[j]; }
 };
 
-// Grid-stride over the chunk table, two chunks per iteration so every lane has 2 (bf16) or
-// 4 (fp32) independent 16-byte loads in flight.  No atomics and no fences: each block
-// writes one partial; norm_finalize_kernel (next on the stream) combines them.  Squares of
-// fp32 values are exact in fp64, and any inf/NaN gradient makes the sum non-finite.
+// Norm tiles: kNormLoads 16-byte loads per lane, so a tile is 16 KiB of gradients (8192 bf16
+// or 4096 fp32); the pass has its own tile table (same tensors, bigger pieces than the update's
+// chunks) so each descriptor fetch is amortised over 4 loads per lane.
+constexpr int kNormLoads = 4;
+template <typename GradT>
+constexpr uint32_t norm_tile_elems() {
+    return (uint32_t)(kBlock * kNormLoads * 16 / sizeof(GradT));
+}
+
+// Grid-stride over the norm tiles; the next tile's descriptor is fetched while this tile's
+// loads are in flight.  No atomics and no fences: each block writes one partial and
+// norm_finalize_kernel (next on the stream) combines them.  Squares of fp32 values are
+// exact in fp64, and any inf/NaN gradient makes the sum non-finite.
 template <typename GradT>
 __global__ __launch_bounds__(kBlock) void norm_partials_kernel(const GradT* __restrict__ g,
-                                                               const Chunk* __restrict__ chunks,
-                                                               uint32_t nchunks,
+                                                               const Chunk* __restrict__ tiles,
+                                                               uint32_t ntiles,
                                                                const DevState* __restrict__ st,
                                                                int32_t scaler_on,
                                                                double* __restrict__ partials) {
     typedef GradVec<GradT> GV;
     constexpr int E = GV::kElems;
-    constexpr int L = kChunk / (kBlock * E);  // loads per lane per chunk
     __shared__ double lds[kBlock / 64];
     const float inv = scaler_on ? (float)(1.0 / (double)st->scale) : 1.0f;
     double acc = 0.0;
-    for (uint32_t c = blockIdx.x; c < nchunks; c += 2 * gridDim.x) {
-        typename GV::raw w[2][L];
-        uint32_t n_valid[2][L];
+    Chunk next{0, 0, 0};
+    if (blockIdx.x < ntiles) next = tiles[blockIdx.x];
+    for (uint32_t c = blockIdx.x; c < ntiles; c += gridDim.x) {
+        const Chunk ch = next;
+        if (c + gridDim.x < ntiles) next = tiles[c + gridDim.x];
+        typename GV::raw w[kNormLoads];
+        uint32_t nv[kNormLoads];
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const uint32_t cc = c + k * gridDim.x;
-            Chunk ch{0, 0, 0};
-            if (cc < nchunks) ch = chunks[cc];
-#pragma unroll
-            for (int l = 0; l < L; ++l) {
-                const uint32_t off = (uint32_t)(l * kBlock + threadIdx.x) * E;
-                n_valid[k][l] = off < ch.count ? min(ch.count - off, (uint32_t)E) : 0u;
-                if (n_valid[k][l])
-                    w[k][l] = __builtin_nontemporal_load(
-                        reinterpret_cast<const typename GV::raw*>(g + ch.begin + off));
-            }
+        for (int l = 0; l < kNormLoads; ++l) {
+            const uint32_t off = (uint32_t)(l * kBlock + threadIdx.x) * E;
+            nv[l] = off < ch.count ? min(ch.count - off, (uint32_t)E) : 0u;
+            if (nv[l])
+                w[l] = __builtin_nontemporal_load(
+                    reinterpret_cast<const typename GV::raw*>(g + ch.begin + off));
         }
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
+        for (int l = 0; l < kNormLoads; ++l) {
+            if (!nv[l]) continue;
 #pragma unroll
-            for (int l = 0; l < L; ++l) {
-                if (!n_valid[k][l]) continue;
-#pragma unroll
-                for (int j = 0; j < E; ++j) {
-                    const float x = (uint32_t)j < n_valid[k][l] ? GV::at(w[k][l], j) * inv : 0.0f;
-                    acc += (double)x * (double)x;
-                }
+            for (int j = 0; j < E; ++j) {
+                const float x = (uint32_t)j < nv[l] ? GV::at(w[l], j) * inv : 0.0f;
+                acc += (double)x * (double)x;
             }
         }
     }
@@ -232,8 +242,19 @@ struct FinalizeArgs {
 
 __global__ __launch_bounds__(kBlock) void norm_finalize_kernel(FinalizeArgs a) {
     __shared__ double lds[kBlock / 64];
+    // all loads of a round issued before the adds; per-thread order fixed (deterministic)
+    constexpr int kPer = 8;
     double s = 0.0;
-    for (uint32_t b = threadIdx.x; b < a.npartials; b += kBlock) s += a.partials[b];
+    for (uint32_t base = 0; base < a.npartials; base += kBlock * kPer) {
+        double v[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const uint32_t b = base + (uint32_t)k * kBlock + threadIdx.x;
+            v[k] = b < a.npartials ? a.partials[b] : 0.0;
+        }
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) s += v[k];
+    }
     s = block_sum(s, lds);
     if (threadIdx.x != 0) return;
 
@@ -339,12 +360,12 @@ __device__ __forceinline__ void store_vec(float* a, float* b, float* c, uint16_t
 }
 
 template <typename GradT, bool kMixed>
-__global__ __launch_bounds__(kBlock) void adam_kernel(const GradT* __restrict__ grad,
-                                                      float* __restrict__ master,
-                                                      float* __restrict__ exp_avg,
-                                                      float* __restrict__ exp_avg_sq,
-                                                      uint16_t* __restrict__ param16,
-                                                      AdamArgs a) {
+__global__ __launch_bounds__(kUpdBlock) void adam_kernel(const GradT* __restrict__ grad,
+                                                         float* __restrict__ master,
+                                                         float* __restrict__ exp_avg,
+                                                         float* __restrict__ exp_avg_sq,
+                                                         uint16_t* __restrict__ param16,
+                                                         AdamArgs a) {
     Coefs k{1.0f, 1.0f, a.bias1, a.bias2};
     if (a.st) {
         if ((a.flags & kCheckSkip) && a.st->skip) return;
@@ -358,35 +379,24 @@ __global__ __launch_bounds__(kBlock) void adam_kernel(const GradT* __restrict__ 
     const bool use_inv = a.flags & kUseInv, use_clip = a.flags & kUseClip;
     for (uint32_t c = blockIdx.x; c < a.nchunks; c += gridDim.x) {
         const Chunk ch = a.chunks[c];
+        const uint32_t off = threadIdx.x * kVec;
+        if (off >= ch.count) continue;
+        const int n = (int)min(ch.count - off, (uint32_t)kVec);
         const bool decay = (ch.meta & kChunkDecay) && (a.flags & kWdOn);
-        f32x4 g[kUnroll], p[kUnroll], m[kUnroll], v[kUnroll];
-        int n[kUnroll];
+        const uint64_t i = ch.begin + off;
+        const f32x4 g = ld_grad4(grad, i);
+        f32x4 p = ld4(master + i);
+        f32x4 m = ld4(exp_avg + i);
+        f32x4 v = ld4(exp_avg_sq + i);
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const uint32_t off = (uint32_t)(u * kBlock + threadIdx.x) * kVec;
-            n[u] = off < ch.count ? (int)min(ch.count - off, (uint32_t)kVec) : 0;
-            if (n[u]) {
-                const uint64_t i = ch.begin + off;
-                g[u] = ld_grad4(grad, i);
-                p[u] = ld4(master + i);
-                m[u] = ld4(exp_avg + i);
-                v[u] = ld4(exp_avg_sq + i);
-            }
+        for (int j = 0; j < kVec; ++j) {
+            float pj = p[j], mj = m[j], vj = v[j];
+            adam_elem(pj, g[j], mj, vj, a, k, use_inv, use_clip, decay);
+            p[j] = pj;
+            m[j] = mj;
+            v[j] = vj;
         }
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            if (!n[u]) continue;
-#pragma unroll
-            for (int j = 0; j < kVec; ++j) {
-                float pj = p[u][j], mj = m[u][j], vj = v[u][j];
-                adam_elem(pj, g[u][j], mj, vj, a, k, use_inv, use_clip, decay);
-                p[u][j] = pj;
-                m[u][j] = mj;
-                v[u][j] = vj;
-            }
-            const uint64_t i = ch.begin + (uint32_t)(u * kBlock + threadIdx.x) * kVec;
-            store_vec<kMixed>(master, exp_avg, exp_avg_sq, param16, i, p[u], m[u], v[u], n[u]);
-        }
+        store_vec<kMixed>(master, exp_avg, exp_avg_sq, param16, i, p, m, v, n);
     }
 }
 
@@ -406,11 +416,11 @@ struct SgdArgs {
 };
 
 template <typename GradT, bool kMixed>
-__global__ __launch_bounds__(kBlock) void sgd_kernel(const GradT* __restrict__ grad,
-                                                     float* __restrict__ master,
-                                                     float* __restrict__ momentum,
-                                                     uint16_t* __restrict__ param16,
-                                                     SgdArgs a) {
+__global__ __launch_bounds__(kUpdBlock) void sgd_kernel(const GradT* __restrict__ grad,
+                                                        float* __restrict__ master,
+                                                        float* __restrict__ momentum,
+                                                        uint16_t* __restrict__ param16,
+                                                        SgdArgs a) {
     float inv = 1.0f, clip = 1.0f;
     if (a.st) {
         if ((a.flags & kCheckSkip) && a.st->skip) return;
@@ -421,43 +431,31 @@ __global__ __launch_bounds__(kBlock) void sgd_kernel(const GradT* __restrict__ g
     const bool mom_on = a.flags & kMomOn, nesterov = a.flags & kNesterov;
     for (uint32_t c = blockIdx.x; c < a.nchunks; c += gridDim.x) {
         const Chunk ch = a.chunks[c];
+        const uint32_t off = threadIdx.x * kVec;
+        if (off >= ch.count) continue;
+        const int n = (int)min(ch.count - off, (uint32_t)kVec);
         const bool decay = (ch.meta & kChunkDecay) && (a.flags & kWdOn);
         const bool first = mom_on && a.mom_init[ch.meta >> 8] == 0u;
-        f32x4 g[kUnroll], p[kUnroll], b[kUnroll];
-        int n[kUnroll];
+        const uint64_t i = ch.begin + off;
+        f32x4 g = ld_grad4(grad, i);
+        f32x4 p = ld4(master + i);
+        f32x4 b = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (mom_on && !first) b = ld4(momentum + i);
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const uint32_t off = (uint32_t)(u * kBlock + threadIdx.x) * kVec;
-            n[u] = off < ch.count ? (int)min(ch.count - off, (uint32_t)kVec) : 0;
-            b[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (n[u]) {
-                const uint64_t i = ch.begin + off;
-                g[u] = ld_grad4(grad, i);
-                p[u] = ld4(master + i);
-                if (mom_on && !first) b[u] = ld4(momentum + i);
+        for (int j = 0; j < kVec; ++j) {
+            float gj = g[j];
+            if (use_inv) gj = gj * inv;
+            if (use_clip) gj = gj * clip;
+            if (decay) gj = gj + a.wd * p[j];
+            if (mom_on) {
+                const float bj = first ? gj : a.mu * b[j] + a.omd * gj;
+                b[j] = bj;
+                gj = nesterov ? gj + a.mu * bj : bj;
             }
+            const float update = gj * a.lr;  // autograd/dynamic/optim.hpp:24
+            p[j] = p[j] - update;             // autograd/dynamic/optim.hpp:25
         }
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            if (!n[u]) continue;
-#pragma unroll
-            for (int j = 0; j < kVec; ++j) {
-                float gj = g[u][j];
-                if (use_inv) gj = gj * inv;
-                if (use_clip) gj = gj * clip;
-                if (decay) gj = gj + a.wd * p[u][j];
-                if (mom_on) {
-                    const float bj = first ? gj : a.mu * b[u][j] + a.omd * gj;
-                    b[u][j] = bj;
-                    gj = nesterov ? gj + a.mu * bj : bj;
-                }
-                const float update = gj * a.lr;  // autograd/dynamic/optim.hpp:24
-                p[u][j] = p[u][j] - update;       // autograd/dynamic/optim.hpp:25
-            }
-            const uint64_t i = ch.begin + (uint32_t)(u * kBlock + threadIdx.x) * kVec;
-            store_vec<kMixed>(master, mom_on ? momentum : nullptr, nullptr, param16, i, p[u], b[u],
-                              b[u], n[u]);
-        }
+        store_vec<kMixed>(master, mom_on ? momentum : nullptr, nullptr, param16, i, p, b, b, n);
     }
 }
 

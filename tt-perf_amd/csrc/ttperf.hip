@@ -63,6 +63,15 @@ struct EventPair {
     hipEvent_t a, b;
 };
 
+// Device work tables of one active tensor set: the update pass walks `chunks` (<= kChunk
+// elements of one tensor each), the norm pass walks `tiles` (<= 16 KiB of gradients each).
+struct WorkTables {
+    Chunk* chunks = nullptr;
+    uint32_t n_chunks = 0;
+    Chunk* tiles = nullptr;
+    uint32_t n_tiles = 0;
+};
+
 }  // namespace
 
 struct ttp_ctx {
@@ -88,16 +97,15 @@ struct ttp_ctx {
     double* partials = nullptr;
     uint32_t partials_cap = 0;
 
-    uint64_t chunk_elems = ttp::kChunk;  // the kernels cover exactly kChunk elements per chunk
-    uint32_t grid_cap = 0;               // 0: one block per chunk
-    uint32_t norm_grid_cap = 0;          // blocks of the norm pass (one partial each)
+    uint32_t grid_cap = 0;       // 0: one block per chunk
+    uint32_t norm_grid_cap = 0;  // blocks of the norm pass (one partial each)
+    uint32_t upd_lds = 0;        // dynamic LDS per update block (caps blocks per CU)
 
-    Chunk* chunks_all = nullptr;  // every non-empty tensor
-    uint32_t n_chunks_all = 0;
+    WorkTables all;  // every non-empty tensor
     uint32_t n_nonempty = 0;
     // tables of other active sets (a subset, or tensors without grad left out), keyed by
     // the sorted active tensor indices
-    std::map<std::vector<uint32_t>, std::pair<Chunk*, uint32_t>> tables;
+    std::map<std::vector<uint32_t>, WorkTables> tables;
 
     float* bias_tab = nullptr;
     uint32_t bias_len = 0;
@@ -116,18 +124,49 @@ namespace {
 size_t grad_esize(const ttp_ctx* c) { return c->mode == TTP_MODE_MIXED ? 2 : 4; }
 size_t param_esize(const ttp_ctx* c) { return c->mode == TTP_MODE_MIXED ? 2 : 4; }
 
-void append_chunks(const ttp_ctx* c, const std::vector<uint32_t>& which, std::vector<Chunk>& out) {
+uint32_t norm_tile(const ttp_ctx* c) {
+    return c->mode == TTP_MODE_MIXED ? ttp::norm_tile_elems<uint16_t>()
+                                     : ttp::norm_tile_elems<float>();
+}
+
+// pieces of <= `piece` elements of each listed non-empty tensor, in tensor order
+void append_pieces(const ttp_ctx* c, const std::vector<uint32_t>& which, uint64_t piece,
+                   std::vector<Chunk>& out) {
     for (uint32_t i : which) {
         const TensorRec& t = c->tensors[i];
-        if (!t.numel) continue;
-        for (uint64_t b = 0; b < t.numel; b += c->chunk_elems) {
+        for (uint64_t b = 0; b < t.numel; b += piece) {
             Chunk ch;
             ch.begin = t.offset + b;
-            ch.count = (uint32_t)std::min<uint64_t>(c->chunk_elems, t.numel - b);
+            ch.count = (uint32_t)std::min<uint64_t>(piece, t.numel - b);
             ch.meta = (t.flags & TTP_TENSOR_DECAY ? ttp::kChunkDecay : 0u) | ((uint32_t)i << 8);
             out.push_back(ch);
         }
     }
+}
+
+int upload_table(const std::vector<Chunk>& v, Chunk** d, uint32_t* n) {
+    if (v.size() > 0xFFFFFFFFull) return fail(TTP_ERR_INVALID, "too many chunks");
+    HIP_TRY(hipMalloc((void**)d, std::max<size_t>(v.size(), 1) * sizeof(Chunk)));
+    if (!v.empty())
+        HIP_TRY(hipMemcpy(*d, v.data(), v.size() * sizeof(Chunk), hipMemcpyHostToDevice));
+    *n = (uint32_t)v.size();
+    return TTP_OK;
+}
+
+int build_tables(const ttp_ctx* c, const std::vector<uint32_t>& which, WorkTables* w) {
+    std::vector<Chunk> v;
+    append_pieces(c, which, ttp::kChunk, v);
+    int rc = upload_table(v, &w->chunks, &w->n_chunks);
+    if (rc) return rc;
+    v.clear();
+    append_pieces(c, which, norm_tile(c), v);
+    return upload_table(v, &w->tiles, &w->n_tiles);
+}
+
+void free_tables(WorkTables& w) {
+    if (w.chunks) (void)hipFree(w.chunks);
+    if (w.tiles) (void)hipFree(w.tiles);
+    w = WorkTables{};
 }
 
 int zero_device(ttp_ctx* c, void* p, uint64_t bytes) {
@@ -163,9 +202,9 @@ int ensure_momentum(ttp_ctx* c) {
 }
 
 // Active set of a step: the listed tensors (all when `subset` is NULL) that have a grad
-// and at least one element; returns its device chunk table (built once per distinct set).
-int select_chunks(ttp_ctx* c, const uint32_t* subset, uint32_t nsub, const Chunk** chunks,
-                  uint32_t* n, std::vector<uint32_t>* active_out) {
+// and at least one element; returns its device work tables (built once per distinct set).
+int select_tables(ttp_ctx* c, const uint32_t* subset, uint32_t nsub, const WorkTables** out,
+                  std::vector<uint32_t>* active_out) {
     const uint32_t nt = (uint32_t)c->tensors.size();
     std::vector<uint32_t> active;
     if (subset) {
@@ -183,27 +222,25 @@ int select_chunks(ttp_ctx* c, const uint32_t* subset, uint32_t nsub, const Chunk
             if (c->tensors[i].has_grad && c->tensors[i].numel) active.push_back(i);
     }
     if (active.size() == c->n_nonempty) {
-        *chunks = c->chunks_all;
-        *n = c->n_chunks_all;
+        *out = &c->all;
     } else {
         auto it = c->tables.find(active);
         if (it == c->tables.end()) {
             if (c->tables.size() >= 64) {
                 // queued work may still read the cached tables
                 HIP_TRY(hipStreamSynchronize(c->stream));
-                for (auto& kv : c->tables) HIP_TRY(hipFree(kv.second.first));
+                for (auto& kv : c->tables) free_tables(kv.second);
                 c->tables.clear();
             }
-            std::vector<Chunk> v;
-            append_chunks(c, active, v);
-            Chunk* d = nullptr;
-            HIP_TRY(hipMalloc((void**)&d, std::max<size_t>(v.size(), 1) * sizeof(Chunk)));
-            if (!v.empty())
-                HIP_TRY(hipMemcpy(d, v.data(), v.size() * sizeof(Chunk), hipMemcpyHostToDevice));
-            it = c->tables.emplace(active, std::make_pair(d, (uint32_t)v.size())).first;
+            WorkTables w;
+            int rc = build_tables(c, active, &w);
+            if (rc) {
+                free_tables(w);
+                return rc;
+            }
+            it = c->tables.emplace(active, w).first;
         }
-        *chunks = it->second.first;
-        *n = it->second.second;
+        *out = &it->second;
     }
     if (active_out) *active_out = std::move(active);
     return TTP_OK;
@@ -285,8 +322,9 @@ uint32_t norm_grid(const ttp_ctx* c, uint32_t nchunks) {
 }
 
 // norm / inf-check / finalize pass (two launches); `probe` only computes the norm
-int launch_norm(ttp_ctx* c, const Chunk* chunks, uint32_t n, double max_norm, bool probe,
-                bool want_bias) {
+int launch_norm(ttp_ctx* c, const WorkTables* w, double max_norm, bool probe, bool want_bias) {
+    const Chunk* chunks = w->tiles;
+    const uint32_t n = w->n_tiles;
     const uint32_t grid = norm_grid(c, n);
     const int32_t scaler_on = c->scaler.enabled ? 1 : 0;
     TimedLaunch tl(c, TTP_KERNEL_NORM);
@@ -403,9 +441,10 @@ void release(ttp_ctx* c) {
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     for (void* p : {(void*)c->grad, (void*)c->master, (void*)c->exp_avg, (void*)c->exp_avg_sq,
                     (void*)c->momentum, (void*)c->mom_init, (void*)c->st, (void*)c->partials,
-                    (void*)c->chunks_all, (void*)c->bias_tab})
+                    (void*)c->bias_tab})
         if (p) (void)hipFree(p);
-    for (auto& kv : c->tables) (void)hipFree(kv.second.first);
+    free_tables(c->all);
+    for (auto& kv : c->tables) free_tables(kv.second);
     if (c->mode == TTP_MODE_MIXED && c->param) (void)hipFree(c->param);
     for (auto& v : c->ev)
         for (auto& p : v) {
@@ -468,6 +507,20 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
     c->stream = c->own_stream;
 
     c->grid_cap = (uint32_t)env_u64("TTP_GRID_CAP", 0);
+    {
+        // occupancy cap of the update kernels: LDS_per_CU / blocks_per_CU bytes each
+        int lds_cu = 0, lds_blk = 0;
+        const uint64_t per_cu = env_u64("TTP_UPD_BLOCKS_PER_CU", ttp::kUpdBlocksPerCU);
+        if (per_cu &&
+            hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
+                                  device) == hipSuccess &&
+            hipDeviceGetAttribute(&lds_blk, hipDeviceAttributeMaxSharedMemoryPerBlock, device) ==
+                hipSuccess &&
+            lds_cu > 0 && lds_blk > 0) {
+            uint64_t b = (uint64_t)lds_cu / per_cu / 512 * 512;
+            c->upd_lds = (uint32_t)std::min<uint64_t>(b, (uint64_t)lds_blk);
+        }
+    }
     c->norm_grid_cap = (uint32_t)std::min<uint64_t>(
         65536, std::max<uint64_t>(1, env_u64("TTP_NORM_GRID", (uint64_t)c->num_cus * 8)));
 
@@ -497,15 +550,7 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
     for (uint32_t i = 0; i < n; ++i)
         if (descs[i].numel) every.push_back(i);
     c->n_nonempty = (uint32_t)every.size();
-    std::vector<Chunk> all;
-    append_chunks(c, every, all);
-    if (all.size() > 0xFFFFFFFFull) return bail(fail(TTP_ERR_INVALID, "too many chunks"));
-    if (hipMalloc((void**)&c->chunks_all, std::max<size_t>(all.size(), 1) * sizeof(Chunk)) != hipSuccess)
-        return bail(fail(TTP_ERR_OOM, "chunk table allocation failed"));
-    if (!all.empty() && hipMemcpy(c->chunks_all, all.data(), all.size() * sizeof(Chunk),
-                                  hipMemcpyHostToDevice) != hipSuccess)
-        return bail(fail(TTP_ERR_HIP, "chunk table upload failed"));
-    c->n_chunks_all = (uint32_t)all.size();
+    if ((rc = build_tables(c, every, &c->all))) return bail(rc);
 
     DevState s{};
     s.scale = (float)c->scaler.init_scale;
@@ -699,15 +744,16 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
     if (!(hp->weight_decay >= 0)) return fail(TTP_ERR_INVALID, "weight_decay must be >= 0");
     if ((rc = set_dev(c))) return rc;
     if ((rc = ensure_adam_state(c))) return rc;
-    const Chunk* chunks;
-    uint32_t n;
-    if ((rc = select_chunks(c, subset, nsub, &chunks, &n, nullptr))) return rc;
+    const WorkTables* w;
+    if ((rc = select_tables(c, subset, nsub, &w, nullptr))) return rc;
+    const Chunk* chunks = w->chunks;
+    const uint32_t n = w->n_chunks;
 
     const bool scaler = c->scaler.enabled != 0;
     const bool clip = hp->max_grad_norm > 0;
     const bool need_norm = scaler || clip;
     if (scaler && (rc = ensure_bias_table(c, hp->beta1, hp->beta2))) return rc;
-    if (need_norm && (rc = launch_norm(c, chunks, n, hp->max_grad_norm, false, scaler))) return rc;
+    if (need_norm && (rc = launch_norm(c, w, hp->max_grad_norm, false, scaler))) return rc;
 
     ttp::AdamArgs a{};
     a.chunks = chunks;
@@ -736,11 +782,11 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
         const uint32_t grid = update_grid(c, n);
         TimedLaunch tl(c, TTP_KERNEL_UPDATE);
         if (c->mode == TTP_MODE_MIXED)
-            hipLaunchKernelGGL((ttp::adam_kernel<uint16_t, true>), dim3(grid), dim3(ttp::kBlock), 0,
+            hipLaunchKernelGGL((ttp::adam_kernel<uint16_t, true>), dim3(grid), dim3(ttp::kUpdBlock), c->upd_lds,
                                c->stream, (const uint16_t*)c->grad, c->master, c->exp_avg,
                                c->exp_avg_sq, (uint16_t*)c->param, a);
         else
-            hipLaunchKernelGGL((ttp::adam_kernel<float, false>), dim3(grid), dim3(ttp::kBlock), 0,
+            hipLaunchKernelGGL((ttp::adam_kernel<float, false>), dim3(grid), dim3(ttp::kUpdBlock), c->upd_lds,
                                c->stream, (const float*)c->grad, c->master, c->exp_avg,
                                c->exp_avg_sq, (uint16_t*)nullptr, a);
         HIP_TRY(hipGetLastError());
@@ -763,15 +809,16 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
     if ((rc = set_dev(c))) return rc;
     const bool mom = hp->momentum != 0.0;
     if (mom && (rc = ensure_momentum(c))) return rc;
-    const Chunk* chunks;
-    uint32_t n;
+    const WorkTables* w;
     std::vector<uint32_t> active;
-    if ((rc = select_chunks(c, subset, nsub, &chunks, &n, &active))) return rc;
+    if ((rc = select_tables(c, subset, nsub, &w, &active))) return rc;
+    const Chunk* chunks = w->chunks;
+    const uint32_t n = w->n_chunks;
 
     const bool scaler = c->scaler.enabled != 0;
     const bool clip = hp->max_grad_norm > 0;
     const bool need_norm = scaler || clip;
-    if (need_norm && (rc = launch_norm(c, chunks, n, hp->max_grad_norm, false, false))) return rc;
+    if (need_norm && (rc = launch_norm(c, w, hp->max_grad_norm, false, false))) return rc;
     if (!scaler) c->host_t += 1;
 
     ttp::SgdArgs a{};
@@ -791,11 +838,11 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
         const uint32_t grid = update_grid(c, n);
         TimedLaunch tl(c, TTP_KERNEL_UPDATE);
         if (c->mode == TTP_MODE_MIXED)
-            hipLaunchKernelGGL((ttp::sgd_kernel<uint16_t, true>), dim3(grid), dim3(ttp::kBlock), 0,
+            hipLaunchKernelGGL((ttp::sgd_kernel<uint16_t, true>), dim3(grid), dim3(ttp::kUpdBlock), c->upd_lds,
                                c->stream, (const uint16_t*)c->grad, c->master, c->momentum,
                                (uint16_t*)c->param, a);
         else
-            hipLaunchKernelGGL((ttp::sgd_kernel<float, false>), dim3(grid), dim3(ttp::kBlock), 0,
+            hipLaunchKernelGGL((ttp::sgd_kernel<float, false>), dim3(grid), dim3(ttp::kUpdBlock), c->upd_lds,
                                c->stream, (const float*)c->grad, c->master, c->momentum,
                                (uint16_t*)nullptr, a);
         HIP_TRY(hipGetLastError());
@@ -853,10 +900,9 @@ int ttp_grad_norm(ttp_ctx* c, double* norm) {
     if (rc) return rc;
     if (!norm) return fail(TTP_ERR_INVALID, "null output");
     if ((rc = set_dev(c))) return rc;
-    const Chunk* chunks;
-    uint32_t n;
-    if ((rc = select_chunks(c, nullptr, 0, &chunks, &n, nullptr))) return rc;
-    if ((rc = launch_norm(c, chunks, n, 0.0, true, false))) return rc;
+    const WorkTables* w;
+    if ((rc = select_tables(c, nullptr, 0, &w, nullptr))) return rc;
+    if ((rc = launch_norm(c, w, 0.0, true, false))) return rc;
     DevState s;
     if ((rc = read_state(c, &s))) return rc;
     *norm = s.norm;
