@@ -184,7 +184,7 @@ def main():
         skip_ms = e0.elapsed_time(e1)
         assert rs is None
 
-    # practical ceiling: a plain device copy of the update's byte count
+    # context: torch's device copy (a blit kernel) of the update's byte count
     ub = UPDATE_BYTES[(args.optimizer, mode)]
     nb = NORM_BYTES[mode]
     copy_bytes = n_params * ub // 2
@@ -226,7 +226,7 @@ def main():
         "kernels_ms": {"norm_pass": round(nrm_avg, 4), "update": round(upd_avg, 4),
                        "source": "second pass of K steps with an event pair per launch"},
         "skipped_step_ms": round(skip_ms, 4) if skip_ms is not None else None,
-        "copy_ceiling_GBps": round(copy_gbps, 1),
+        "torch_copy_GBps": round(copy_gbps, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": traffic_from_profiles(args.config),
