@@ -75,6 +75,41 @@ struct TracedEmbedding {
 // autograd/traced/ops.hpp:132-134: param = param - lr * grad (one tensor)
 inline void sgd_update(const ValuePtr& param, float lr) { detail::sgd_on({param}, lr); }
 
+// traced::TraceContext (autograd/traced/trace.hpp:21-88) over a ttp::Store: the first
+// run(fn) captures the work fn queues on the store's stream into a hipGraph and executes it;
+// later calls replay it.  Step the captured tensor sets once eagerly before the first run.
+// Release (or destroy) the TraceContext before the store.
+class TraceContext {
+public:
+    explicit TraceContext(ttp::Store& store) : store_(&store) {}
+    TraceContext(const TraceContext&) = delete;
+    TraceContext& operator=(const TraceContext&) = delete;
+    TraceContext(TraceContext&&) = default;
+    TraceContext& operator=(TraceContext&&) = default;
+
+    template <typename Fn>
+    void run(Fn&& fn) {
+        if (!graph_) {
+            store_->begin_capture();
+            try {
+                fn();
+            } catch (...) {
+                store_->discard_capture();
+                throw;
+            }
+            graph_ = store_->end_capture();
+        }
+        graph_.launch();
+    }
+    bool is_captured() const { return (bool)graph_; }
+    void release() { graph_.reset(); }
+    void reset() { release(); }
+
+private:
+    ttp::Store* store_;
+    ttp::Graph graph_;
+};
+
 struct TracedSGD {
     std::vector<TracedLinear*> layers;
     float lr;

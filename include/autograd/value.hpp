@@ -88,18 +88,20 @@ struct Value {
     std::vector<float> master() const { return store().master(index); }
     void set_data(const std::vector<float>& w) { store().set_weights(index, w); }
 
-    // autograd/dynamic/autograd.hpp:78-83: grad = grad + incoming, or the first assignment
+    // autograd/dynamic/autograd.hpp:78-83: grad = grad + incoming, or the first assignment;
+    // done on the GPU in the flat grad buffer (one launch, no host round trip of the grad)
     void accumulate_grad(const std::vector<float>& incoming) {
         if (!requires_grad) return;
-        if (!grad.has_value()) {
-            grad = incoming;
-            return;
-        }
-        std::vector<float> g = grad.value();
-        if (g.size() != incoming.size()) throw std::invalid_argument("grad shape mismatch");
-        for (size_t k = 0; k < g.size(); ++k) g[k] = g[k] + incoming[k];
-        grad = g;
+        if (incoming.size() != numel()) throw std::invalid_argument("grad shape mismatch");
+        store().accumulate_grad(index, incoming);
     }
+    // the same with a device-resident gradient (TTP_DTYPE_F32 or TTP_DTYPE_BF16)
+    void accumulate_grad_device(const void* incoming, int dtype) {
+        if (!requires_grad) return;
+        store().accumulate_grad_device(index, incoming, dtype);
+    }
+    // device address of this parameter's gradient slice, for backward kernels that write it
+    void* grad_ptr() { return store().device_ptr(TTP_BUF_GRAD, index); }
 };
 
 // Declares parameters; all of them live in one store created on first use.

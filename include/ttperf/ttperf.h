@@ -73,7 +73,12 @@ extern "C" {
 #define TTP_HOST 0
 #define TTP_DEVICE 1
 
+/* Element types of incoming gradients (ttp_accumulate_grad). */
+#define TTP_DTYPE_F32 0
+#define TTP_DTYPE_BF16 1
+
 typedef struct ttp_ctx ttp_ctx;
+typedef struct ttp_graph ttp_graph;
 
 typedef struct ttp_tensor_desc {
     uint64_t numel;  /* elements; 0 is allowed (the tensor is then never touched) */
@@ -169,8 +174,18 @@ int ttp_download(ttp_ctx* ctx, int which, uint32_t index, void* dst, uint64_t n,
  * optimizer state are not touched) and left out of the grad norm. */
 int ttp_set_has_grad(ttp_ctx* ctx, uint32_t index, int has_grad);
 int ttp_get_has_grad(const ttp_ctx* ctx, uint32_t index, int* has_grad);
-/* Zero the whole grad buffer; set_to_none = 1 also clears every has_grad flag. */
+/* Zero the whole grad buffer; set_to_none = 1 also clears every has_grad flag.
+ * One fill over the flat buffer replaces the per-tensor zeros_like allocations of
+ * autograd/static/nn.hpp:98-101 and the nullopt loop of autograd/dynamic/optim.hpp:30-34. */
 int ttp_zero_grad(ttp_ctx* ctx, int set_to_none);
+/* Value::accumulate_grad (autograd/dynamic/autograd.hpp:78-83; static_autograd::Value,
+ * autograd/static/value.hpp:39-47) on the flat grad buffer: when tensor `index` has no grad,
+ * its grad becomes the incoming gradient; otherwise grad = grad + incoming, added in fp32 and
+ * rounded once (round-to-nearest-even) to the grad buffer's type.  `src` holds exactly numel
+ * values of `src_dtype` (TTP_DTYPE_*) in host or device memory (`src_kind`).  Marks the
+ * tensor as having a grad.  Stream-ordered; a host source is consumed before returning. */
+int ttp_accumulate_grad(ttp_ctx* ctx, uint32_t index, const void* src, uint64_t n,
+                        int src_dtype, int src_kind);
 
 /* ---- optimizer steps ------------------------------------------------------------------ */
 int ttp_adam_step(ttp_ctx* ctx, const ttp_adam_hparams* hp, ttp_step_report* report);
@@ -195,6 +210,24 @@ int ttp_set_step(ttp_ctx* ctx, uint64_t step);
 int ttp_scaler_configure(ttp_ctx* ctx, const ttp_scaler_config* cfg);
 int ttp_scaler_get(ttp_ctx* ctx, float* scale, int32_t* growth_tracker);
 int ttp_scaler_set(ttp_ctx* ctx, float scale, int32_t growth_tracker);
+
+/* ---- graph capture and replay -------------------------------------------------------------
+ * The counterpart of traced::TraceContext (autograd/traced/trace.hpp:21-88: capture once,
+ * then replay): everything queued on the context's stream between ttp_capture_begin and
+ * ttp_capture_end (the engine's steps, zero_grad and device-side transfers, and the caller's
+ * own kernels when the context uses the caller's stream) becomes one hipGraph, replayed by
+ * ttp_graph_launch.  From ttp_capture_begin on, the context keeps the Adam step count and its
+ * bias corrections on the device, so each replay advances t exactly as an eager step does.
+ * While capturing, calls that would allocate, build a work table or synchronise fail with
+ * TTP_ERR_STATE: step each tensor set (and each optimizer, for its state) eagerly once before
+ * capturing, pass no step report, and use no host transfers.  The legacy default stream
+ * cannot be captured.  A graph replays the tensor sets, hyperparameters and flags seen at
+ * capture time.  Destroy a context's graphs before the context (ttp_destroy refuses). */
+int ttp_capture_begin(ttp_ctx* ctx);
+/* out == NULL discards the capture. */
+int ttp_capture_end(ttp_ctx* ctx, ttp_graph** out);
+int ttp_graph_launch(ttp_graph* graph);
+int ttp_graph_destroy(ttp_graph* graph);
 
 /* ---- per-kernel timing (HIP events on the context's stream) ------------------------------ */
 #define TTP_KERNEL_NORM 0   /* grad-norm / inf-check / scaler finalize pass */

@@ -73,6 +73,34 @@ struct SgdOptions {
     }
 };
 
+// A captured graph of a store's work (ttp_capture_begin .. ttp_capture_end); move-only.
+class Graph {
+public:
+    Graph() = default;
+    explicit Graph(ttp_graph* g) : g_(g) {}
+    Graph(Graph&& o) noexcept : g_(o.g_) { o.g_ = nullptr; }
+    Graph& operator=(Graph&& o) noexcept {
+        if (this != &o) {
+            reset();
+            g_ = o.g_;
+            o.g_ = nullptr;
+        }
+        return *this;
+    }
+    Graph(const Graph&) = delete;
+    Graph& operator=(const Graph&) = delete;
+    ~Graph() { reset(); }
+    void launch() { check(ttp_graph_launch(g_)); }
+    void reset() {
+        if (g_) ttp_graph_destroy(g_);
+        g_ = nullptr;
+    }
+    explicit operator bool() const { return g_ != nullptr; }
+
+private:
+    ttp_graph* g_ = nullptr;
+};
+
 class Store {
 public:
     Store(const std::vector<TensorSpec>& specs, Mode mode, int device = 0) : specs_(specs), mode_(mode) {
@@ -133,6 +161,14 @@ public:
     }
     void set_has_grad(uint32_t i, bool h) { check(ttp_set_has_grad(ctx_, i, h ? 1 : 0)); }
     void zero_grad(bool set_to_none = true) { check(ttp_zero_grad(ctx_, set_to_none ? 1 : 0)); }
+    // grad = g if tensor i has none, else grad + g (fp32 add, one rounding to the grad type)
+    void accumulate_grad(uint32_t i, const std::vector<float>& g) {
+        check(ttp_accumulate_grad(ctx_, i, g.data(), g.size(), TTP_DTYPE_F32, TTP_HOST));
+    }
+    // the same from device memory (fp32 or bf16 bits), e.g. a backward kernel's output
+    void accumulate_grad_device(uint32_t i, const void* src, int dtype) {
+        check(ttp_accumulate_grad(ctx_, i, src, numel(i), dtype, TTP_DEVICE));
+    }
     void* device_ptr(int which, uint32_t i = TTP_ALL_TENSORS) {
         void* p = nullptr;
         check(ttp_buffer_ptr(ctx_, which, i, &p));
@@ -184,6 +220,13 @@ public:
         return t;
     }
     void sync() { check(ttp_sync(ctx_)); }
+    void begin_capture() { check(ttp_capture_begin(ctx_)); }
+    Graph end_capture() {
+        ttp_graph* g = nullptr;
+        check(ttp_capture_end(ctx_, &g));
+        return Graph(g);
+    }
+    void discard_capture() { (void)ttp_capture_end(ctx_, nullptr); }
 
     static uint16_t to_bf16(float x) {
         uint32_t u;

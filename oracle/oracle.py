@@ -91,6 +91,7 @@ def lib():
                                         C.c_double, C.c_double, C.c_int32]
         L.orc_layout.restype = C.c_uint64
         L.orc_layout.argtypes = [C.c_void_p, C.c_uint32, C.c_uint64, C.c_void_p]
+        L.orc_accumulate_grad.argtypes = [C.POINTER(Store), C.c_uint32, C.c_void_p, C.c_int]
         L.orc_grad_sumsq.restype = C.c_double
         L.orc_grad_sumsq.argtypes = [C.POINTER(Store), C.c_float, C.POINTER(C.c_int32)]
         for name, hp in (("orc_adam_step", AdamHP), ("orc_adam_step_opbyop", AdamHP),
@@ -195,6 +196,14 @@ class OracleStore:
         dst = self.view("grad", i)
         dst[:] = np.asarray(g).ravel().astype(dst.dtype, copy=False)
         self._tensors[i].has_grad = 1
+
+    def accumulate_grad(self, i, g):
+        """g: float32 values or uint16 bf16 bits (any mode)."""
+        a = np.ascontiguousarray(g).ravel()
+        if a.dtype != np.uint16:
+            a = a.astype(np.float32)
+        assert a.size == self.numels[i]
+        lib().orc_accumulate_grad(C.byref(self.s), i, _ptr(a), 1 if a.dtype == np.uint16 else 0)
 
     def set_has_grad(self, i, has):
         self._tensors[i].has_grad = 1 if has else 0

@@ -182,6 +182,23 @@ double orc_grad_sumsq(const orc_store* s, float inv_scale, int32_t* found_inf) {
     return sum;
 }
 
+void orc_accumulate_grad(orc_store* s, uint32_t index, const void* src, int src_bf16) {
+    orc_tensor* t = (orc_tensor*)&s->tensors[index];
+    const int first = !t->has_grad;
+    for (uint64_t k = 0; k < t->numel; ++k) {
+        const float in = src_bf16 ? orc_bf16_to_f32(((const uint16_t*)src)[k]) : ((const float*)src)[k];
+        const uint64_t i = t->offset + k;
+        if (s->mode == ORC_MODE_MIXED) {
+            uint16_t* g = (uint16_t*)s->grad;
+            g[i] = orc_bf16_rne(first ? in : orc_bf16_to_f32(g[i]) + in);
+        } else {
+            float* g = (float*)s->grad;
+            g[i] = first ? in : g[i] + in;
+        }
+    }
+    t->has_grad = 1;
+}
+
 /* ------------------------------------------------------------------------------------ */
 /* Adam / AdamW                                                                         */
 /* ------------------------------------------------------------------------------------ */

@@ -114,6 +114,11 @@ uint64_t orc_layout(const uint64_t* numel, uint32_t n, uint64_t align, uint64_t*
  * and whether any of them is non-finite. */
 double orc_grad_sumsq(const orc_store* s, float inv_scale, int32_t* found_inf);
 
+/* Value::accumulate_grad (autograd/dynamic/autograd.hpp:78-83, py/engine.py:149-156): the
+ * tensor's grad becomes src when it has none, else grad + src (fp32 add, one rounding to the
+ * grad type); src is float (src_bf16 = 0) or bf16 bits (src_bf16 = 1). */
+void orc_accumulate_grad(orc_store* s, uint32_t index, const void* src, int src_bf16);
+
 /* one optimizer step over the store (fused: one pass per element) */
 int orc_adam_step(orc_store* s, const orc_adam_hp* hp, orc_report* rep);
 int orc_sgd_step(orc_store* s, const orc_sgd_hp* hp, orc_report* rep);

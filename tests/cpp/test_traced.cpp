@@ -73,5 +73,35 @@ int main() {
     traced::TracedLayerNorm ln2(8, fresh);
     test::assert_all_close(ln2.gamma->data(), 1.0f, 0.0f, "LayerNorm gamma init");
     test::assert_all_close(ln2.beta->data(), 0.0f, 0.0f, "LayerNorm beta init");
+    // TraceContext (autograd/traced/trace.hpp:21-88): the first run() captures the TracedSGD
+    // step into a graph and executes it, later runs replay it; gradients change in between
+    {
+        ParamArena arena3(ttp::Mode::FP32);
+        traced::TracedLinear a(16, 8, 0.01f, arena3), b(8, 4, 0.02f, arena3);
+        traced::TracedSGD opt({&a, &b}, 0.1f);
+        std::vector<ValuePtr> ps = {a.weight, a.bias, b.weight, b.bias};
+        std::vector<std::vector<float>> wr;
+        for (auto& p : ps) wr.push_back(p->master());
+        {
+            traced::TraceContext trace(a.weight->store());
+            for (int it = 0; it < 4; ++it) {
+                std::vector<std::vector<float>> gr;
+                for (size_t k = 0; k < ps.size(); ++k) {
+                    gr.push_back(ramp(ps[k]->numel(), 0.25f * (float)(it + 1), 0.01f * (float)(k + 1)));
+                    ps[k]->grad = gr.back();
+                }
+                if (it == 0)
+                    opt.step();  // eager once: the work tables exist before capture
+                else
+                    trace.run([&] { opt.step(); });
+                for (size_t k = 0; k < ps.size(); ++k) wr[k] = sgd_ref(wr[k], gr[k], 0.1f);
+                for (size_t k = 0; k < ps.size(); ++k)
+                    test::assert_bits(ps[k]->master(), wr[k],
+                                      "TraceContext iteration " + std::to_string(it) + " tensor " +
+                                          std::to_string(k));
+                test::check(trace.is_captured() == (it >= 1), "TraceContext captured flag");
+            }
+        }  // the graph is released before the store
+    }
     return test::finish("test_traced");
 }

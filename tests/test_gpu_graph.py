@@ -1,0 +1,245 @@
+"""GPU tests of graph capture/replay (the counterpart of traced::TraceContext,
+autograd/traced/trace.hpp:21-88) and of gradient accumulation into the flat grad buffer
+(Value::accumulate_grad, autograd/dynamic/autograd.hpp:78-83), through the C ABI, against
+eager steps of the same engine and the CPU oracle.
+
+Every replay is followed by the program's own eager work (new gradients copied in, host
+synchronisation) and is checked on its own, not only after the last one.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_util import compare_state, make_pair, torch_mod
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(300, 7), (64,), (129, 33), (5,), (2048,), (1, 2049), (4097,)]
+DECAY = [True, False, True, False, False, True, False]
+
+
+def _bits_equal(a, b):
+    a = np.asarray(a)
+    b = np.asarray(b)
+    if a.dtype == np.float32:
+        return np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    return np.array_equal(a, b)
+
+
+def _same_grads(stores, gen, std, scale=1.0, inf_at=None, mixed=True):
+    """One seeded gradient tensor on the device, copied into every store's grad buffer."""
+    import torch
+    from ttperf import _lib as L
+    total = stores[0].total
+    g = torch.randn(total, generator=gen, device="cuda") * std * scale
+    if inf_at is not None:
+        g[inf_at] = float("inf")
+    g = g.to(torch.bfloat16) if mixed else g
+    for s in stores:
+        s.upload(L.BUF_GRAD, L.ALL_TENSORS, g)
+    host = g.cpu()
+    return host.view(torch.int16).numpy().view(np.uint16) if mixed else host.numpy()
+
+
+@pytest.mark.parametrize("scaler", [False, True])
+@pytest.mark.parametrize("mode", [O.MODE_MIXED, O.MODE_FP32])
+def test_adam_graph_replays_match_eager_and_oracle(mode, scaler):
+    from ttperf import _lib as L
+    torch = torch_mod()
+    mixed = mode == O.MODE_MIXED
+    eager, ref = make_pair(SHAPES, DECAY, mode, seed=90)
+    graphed, _ = make_pair(SHAPES, DECAY, mode, seed=90)
+    graphed.set_stream(None)  # the context's own stream (the legacy stream cannot be captured)
+    if scaler:
+        for s in (eager, graphed):
+            s.configure_scaler(True, init_scale=1024.0)
+        ref.configure_scaler(True, 1024.0)
+    gen = torch.Generator(device="cuda").manual_seed(91)
+    hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=0.05)
+
+    def oracle_step(host):
+        ref.grad[:] = host
+        for i in range(ref.n):
+            ref.set_has_grad(i, True)
+        return ref.adam_step(**hp)
+
+    # one eager step on both (allocates m/v, builds tables and the bias table)
+    host = _same_grads([eager, graphed], gen, 1e-2, scale=ref.scale, mixed=mixed)
+    eager.adam_step(**hp)
+    graphed.adam_step(**hp)
+    oracle_step(host)
+
+    graphed.begin_capture()
+    graphed.adam_step(**hp)
+    graph = graphed.end_capture()
+    for k in range(5):
+        inf_at = graphed.offsets[2] + 11 if (scaler and k == 2) else None
+        host = _same_grads([eager, graphed], gen, 1e-2, scale=ref.scale, inf_at=inf_at,
+                           mixed=mixed)
+        eager.adam_step(**hp)
+        graph.replay()
+        graphed.sync()
+        e = oracle_step(host)
+        for buf in (L.BUF_MASTER, L.BUF_EXP_AVG, L.BUF_EXP_AVG_SQ, L.BUF_PARAM):
+            assert _bits_equal(graphed.download(buf), eager.download(buf)), (k, buf)
+        assert graphed.step_count == eager.step_count == ref.t
+        if scaler:
+            assert graphed.scaler_state() == eager.scaler_state() == (ref.scale, ref.growth_tracker)
+            assert e["skipped"] == (k == 2)
+    compare_state(graphed, ref, max_ulp=2)
+    graph.close()
+    graphed.close()
+
+
+def test_captured_train_step_zero_accumulate_sgd_momentum():
+    """The whole optimizer side of a training step in one graph: zero_grad, gradients
+    accumulated from a device buffer the program rewrites between replays, SGD momentum
+    with clipping.  The first replay initialises the momentum buffers."""
+    from ttperf import _lib as L
+    torch = torch_mod()
+    store, ref = make_pair(SHAPES, DECAY, O.MODE_MIXED, seed=92)
+    store.set_stream(None)
+    src = torch.zeros(store.total, dtype=torch.bfloat16, device="cuda")
+    gen = torch.Generator(device="cuda").manual_seed(93)
+    hp = dict(lr=1e-2, momentum=0.9, weight_decay=0.01, max_grad_norm=0.5)
+
+    def accumulate_all():
+        for i, t in enumerate(store.tensors):
+            ptr = src.data_ptr() + 2 * store.offsets[i]
+            L.check(L.lib.ttp_accumulate_grad(store.handle, i, C.c_void_p(ptr), t.numel,
+                                              L.DTYPE_BF16, L.DEVICE))
+
+    # eager warm-up of the same sequence (tables, momentum buffer)
+    store.zero_grad(set_to_none=True)
+    accumulate_all()
+    store.sgd_step(**hp)
+    store.sync()
+    ref.zero_grad()
+    for i in range(ref.n):
+        ref.accumulate_grad(i, np.zeros(ref.numels[i], np.uint16))
+    ref.sgd_step(**hp)
+
+    store.begin_capture()
+    store.zero_grad(set_to_none=True)
+    accumulate_all()
+    store.sgd_step(**hp)
+    graph = store.end_capture()
+    for k in range(4):
+        src.copy_((torch.randn(store.total, generator=gen, device="cuda") * 0.1)
+                  .to(torch.bfloat16))
+        torch.cuda.synchronize()
+        host = src.cpu().view(torch.int16).numpy().view(np.uint16)
+        graph.replay()
+        store.sync()
+        ref.zero_grad()
+        for i in range(ref.n):
+            o = int(ref.offsets[i])
+            ref.accumulate_grad(i, host[o:o + ref.numels[i]])
+        ref.sgd_step(**hp)
+        compare_state(store, ref, which=("master", "param", "momentum"), max_ulp=2)
+        assert store.step_count == ref.t == k + 2
+    graph.close()
+    store.close()
+
+
+def test_capture_rejects_what_cannot_be_captured():
+    import ttperf
+    from ttperf import _lib as L
+    store = ttperf.ParamStore([(100,), (64, 8)], mode="mixed")
+    store.tensors[0].grad = np.zeros(100, np.uint16)
+    store.tensors[1].grad = np.zeros(512, np.uint16)
+    store.adam_step(lr=1e-3)
+    # a report synchronises
+    store.begin_capture()
+    with pytest.raises(ttperf.TTPError) as e:
+        store.adam_step(lr=1e-3, report=True)
+    assert e.value.code == L.ERR_STATE
+    # a tensor set never stepped before would build tables
+    with pytest.raises(ttperf.TTPError) as e:
+        store.adam_step(lr=1e-3, indices=[1])
+    assert e.value.code == L.ERR_STATE
+    # host transfers synchronise
+    with pytest.raises(ttperf.TTPError) as e:
+        store.tensors[0].grad = np.zeros(100, np.uint16)
+    assert e.value.code == L.ERR_STATE
+    assert store.end_capture(discard=True) is None
+    # the capture was discarded cleanly: eager work continues
+    r = store.adam_step(lr=1e-3, report=True)
+    assert r["step"] == 2
+    # a context with live graphs cannot be destroyed; its graphs go first
+    store.begin_capture()
+    store.adam_step(lr=1e-3)
+    g = store.end_capture()
+    assert L.lib.ttp_destroy(store.handle) == L.ERR_STATE
+    g.replay()
+    assert store.step_count == 3
+    g.close()
+    # the legacy default stream cannot be captured
+    store.set_stream(0)
+    with pytest.raises(ttperf.TTPError) as e:
+        store.begin_capture()
+    assert e.value.code == L.ERR_STATE
+    store.close()
+
+
+def test_trace_context_run_captures_once_then_replays():
+    import ttperf
+    torch = torch_mod()
+    store, ref = make_pair([(1000,), (32, 32)], [False, True], O.MODE_FP32, seed=94)
+    store.set_stream(None)
+    opt = ttperf.AdamW(store.parameters(), lr=1e-3, weight_decay=0.1)
+    gen = torch.Generator(device="cuda").manual_seed(95)
+    trace = ttperf.TraceContext(store)
+    for k in range(4):
+        host = _same_grads([store], gen, 1e-2, mixed=False)
+        ref.grad[:] = host
+        for i in range(ref.n):
+            ref.set_has_grad(i, True)
+        if k == 0:
+            opt.step()          # eager once: allocates m, v
+        else:
+            trace.run(opt.step)  # k == 1 captures and runs, later calls replay
+        store.sync()
+        ref.adam_step(lr=1e-3, weight_decay=0.1, decoupled=True)
+        compare_state(store, ref, which=("master", "exp_avg", "exp_avg_sq"), max_ulp=0)
+        assert trace.is_captured() == (k >= 1)
+    trace.release()
+    store.close()
+
+
+@pytest.mark.parametrize("mode", [O.MODE_MIXED, O.MODE_FP32])
+def test_accumulate_grad_host_and_device_sources(mode):
+    """First call assigns, later calls add (fp32 add, one rounding to the grad type), from
+    host or device memory, fp32 or bf16 sources; then a step uses the result."""
+    torch = torch_mod()
+    from ttperf import _lib as L
+    store, ref = make_pair(SHAPES, DECAY, mode, seed=96)
+    rng = np.random.default_rng(97)
+    for i, t in enumerate(store.tensors):
+        for kind in ("host_f32", "host_bf16", "dev_f32", "dev_bf16"):
+            x = (rng.standard_normal(t.numel) * 0.3).astype(np.float32)
+            if kind.endswith("bf16"):
+                bits = O.bf16_rne(x)
+                ref.accumulate_grad(i, bits)
+                if kind.startswith("host"):
+                    store.accumulate_grad(i, bits)
+                else:
+                    dt = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda()
+                    store.accumulate_grad(i, dt)
+            else:
+                ref.accumulate_grad(i, x)
+                store.accumulate_grad(i, x if kind.startswith("host")
+                                      else torch.from_numpy(x).cuda())
+    got = store.download(L.BUF_GRAD)
+    mask = np.zeros(store.total, bool)
+    for i, t in enumerate(store.tensors):
+        mask[store.offsets[i]:store.offsets[i] + t.numel] = True
+        assert t.grad is not None
+    assert _bits_equal(got[mask], ref.grad[mask])
+    hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
+    r = store.adam_step(report=True, **hp)
+    e = ref.adam_step(**hp)
+    assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-9 * e["grad_norm"]
+    compare_state(store, ref, max_ulp=2)

@@ -371,3 +371,33 @@ def test_validation_rejects_reference_cases():
     for lr in (0.0, -1.0):
         with pytest.raises(ValueError):
             st.sgd_step(lr=lr)
+
+
+def test_accumulate_grad_matches_torch_bf16_and_fp32_addition(rng):
+    """orc_accumulate_grad: first call assigns, later calls add in fp32 with one rounding to
+    the grad type; pinned on torch's own bf16 / fp32 tensor addition (a library, not the
+    reference) on values chosen to exercise bf16 rounding and ties."""
+    import torch
+    n = 4096
+    a = (rng.standard_normal(n) * 3).astype(np.float32)
+    b = (rng.standard_normal(n) * 1e-2).astype(np.float32)
+    b[:64] = np.ldexp(1.0, -9) * np.sign(a[:64])  # near-tie increments relative to |a|~1
+    for mode in (O.MODE_MIXED, O.MODE_FP32):
+        st = O.OracleStore([n], mode=mode, nthreads=1)
+        for src_kind in ("f32", "bf16"):
+            st.zero_grad()
+            ga = O.bf16_rne(a) if src_kind == "bf16" else a
+            gb = O.bf16_rne(b) if src_kind == "bf16" else b
+            st.accumulate_grad(0, ga)
+            st.accumulate_grad(0, gb)
+            ta = torch.from_numpy(O.bf16_to_f32(ga) if src_kind == "bf16" else a)
+            tb = torch.from_numpy(O.bf16_to_f32(gb) if src_kind == "bf16" else b)
+            if mode == O.MODE_MIXED:
+                g = ta.to(torch.bfloat16)          # first assignment rounds to the grad type
+                g.add_(tb if src_kind == "f32" else tb.to(torch.bfloat16))
+                want = g.view(torch.int16).numpy().view(np.uint16)
+                assert np.array_equal(st.grad[:n], want), (mode, src_kind)
+            else:
+                want = (ta + tb).numpy()
+                assert np.array_equal(st.grad[:n].view(np.uint32), want.view(np.uint32))
+            assert st.has_grad(0)

@@ -229,8 +229,9 @@ __global__ __launch_bounds__(kBlock) void norm_partials_kernel(const GradT* __re
 // ------------------------------------------------------------------------------------
 struct FinalizeArgs {
     const double* partials;
-    uint32_t npartials;
-    int32_t scaler_on;      // unscale by 1/scale, skip on inf, update the scale, own t
+    uint32_t npartials;     // 0: no norm pass ran (step counting only)
+    int32_t scaler_on;      // unscale by 1/scale, skip on inf, update the scale
+    int32_t count_t;        // the step count lives on the device: advance it (unless skipped)
     int32_t probe;          // only compute sumsq/norm (ttp_grad_norm); touch nothing else
     int32_t growth_interval;
     double growth_factor;
@@ -277,13 +278,15 @@ __global__ __launch_bounds__(kBlock) void norm_finalize_kernel(FinalizeArgs a) {
     st->skip = skip;
     st->inv_scale = inv;
     st->clip_coef = coef;
-    if (a.scaler_on) {
+    if (a.count_t) {
         if (!skip) st->t += 1;
         if (a.want_bias) {
             const uint64_t t = st->t;
             st->bias1 = (t >= 1 && t <= a.bias_len) ? a.bias_tab[2 * (t - 1)] : 1.0f;
             st->bias2 = (t >= 1 && t <= a.bias_len) ? a.bias_tab[2 * (t - 1) + 1] : 1.0f;
         }
+    }
+    if (a.scaler_on) {
         // torch _amp_update_scale_ semantics
         if (found) {
             st->scale = (float)((double)st->scale * a.backoff_factor);
@@ -469,6 +472,27 @@ __global__ __launch_bounds__(kBlock) void mark_mom_init_kernel(const Chunk* chun
     if (check_skip && st->skip) return;
     for (uint32_t c = blockIdx.x * kBlock + threadIdx.x; c < n; c += gridDim.x * kBlock)
         mom_init[chunks[c].meta >> 8] = 1u;
+}
+
+// ------------------------------------------------------------------------------------
+// gradient accumulation into the flat grad buffer (the backward side of the store)
+// ------------------------------------------------------------------------------------
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+__device__ __forceinline__ void from_f32(float x, float* out) { *out = x; }
+__device__ __forceinline__ void from_f32(float x, uint16_t* out) { *out = (uint16_t)bf16_rne(x); }
+
+// first: grad = incoming (converted); else grad = grad + incoming (fp32 add, one rounding)
+template <typename SrcT, typename GradT>
+__global__ __launch_bounds__(kBlock) void accumulate_grad_kernel(GradT* __restrict__ grad,
+                                                                 const SrcT* __restrict__ src,
+                                                                 uint64_t n, int first) {
+    for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * kBlock) {
+        const float in = to_f32(src[i]);
+        const float r = first ? in : to_f32(grad[i]) + in;
+        from_f32(r, grad + i);
+    }
 }
 
 // ------------------------------------------------------------------------------------

@@ -107,21 +107,43 @@ struct ttp_ctx {
     // the sorted active tensor indices
     std::map<std::vector<uint32_t>, WorkTables> tables;
 
+    void* staging = nullptr;  // device copy of a host gradient for ttp_accumulate_grad
+    uint64_t staging_bytes = 0;
+
     float* bias_tab = nullptr;
     uint32_t bias_len = 0;
     double bias_b1 = -1.0, bias_b2 = -1.0;
 
     ttp_scaler_config scaler{0, 2000, 65536.0, 2.0, 0.5};
-    uint64_t host_t = 0;  // step count while loss scaling is off
+    uint64_t host_t = 0;     // step count while it lives on the host (see dev_t)
+    bool device_t = false;   // set once the context has been captured: t stays on the device
+    bool capturing = false;  // between ttp_capture_begin and ttp_capture_end
+    uint32_t n_graphs = 0;   // live graphs; the buffers and tables they reference stay put
 
     bool timing = false;
     std::vector<EventPair> ev[2];
     std::vector<hipEvent_t> ev_pool;
 };
 
+struct ttp_graph {
+    ttp_ctx* ctx;
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
 namespace {
 
 size_t grad_esize(const ttp_ctx* c) { return c->mode == TTP_MODE_MIXED ? 2 : 4; }
+
+// The step count (bias-correction t) lives on the device while loss scaling is on (the
+// device decides whether a step is skipped) and once the context has been captured (a
+// replayed graph cannot update host state); otherwise on the host.
+bool t_on_device(const ttp_ctx* c) { return c->scaler.enabled || c->device_t; }
+
+int no_capture(const ttp_ctx* c, const char* what) {
+    if (!c->capturing) return TTP_OK;
+    return fail(TTP_ERR_STATE, std::string(what) + " is not allowed while capturing a graph");
+}
 size_t param_esize(const ttp_ctx* c) { return c->mode == TTP_MODE_MIXED ? 2 : 4; }
 
 uint32_t norm_tile(const ttp_ctx* c) {
@@ -190,6 +212,8 @@ int alloc_zero(ttp_ctx* c, void** p, uint64_t bytes) {
 int ensure_adam_state(ttp_ctx* c) {
     // py/optim.py:58-71: m and v start as zeros on first use
     int rc;
+    if ((!c->exp_avg || !c->exp_avg_sq) && (rc = no_capture(c, "first Adam step (allocates m, v)")))
+        return rc;
     if (!c->exp_avg && (rc = alloc_zero(c, (void**)&c->exp_avg, c->total * 4))) return rc;
     if (!c->exp_avg_sq && (rc = alloc_zero(c, (void**)&c->exp_avg_sq, c->total * 4))) return rc;
     return TTP_OK;
@@ -197,6 +221,7 @@ int ensure_adam_state(ttp_ctx* c) {
 
 int ensure_momentum(ttp_ctx* c) {
     int rc;
+    if (!c->momentum && (rc = no_capture(c, "first momentum step (allocates the buffer)"))) return rc;
     if (!c->momentum && (rc = alloc_zero(c, (void**)&c->momentum, c->total * 4))) return rc;
     return TTP_OK;
 }
@@ -226,14 +251,17 @@ int select_tables(ttp_ctx* c, const uint32_t* subset, uint32_t nsub, const WorkT
     } else {
         auto it = c->tables.find(active);
         if (it == c->tables.end()) {
-            if (c->tables.size() >= 64) {
+            int rc;
+            if ((rc = no_capture(c, "a step over a tensor set not stepped before (builds tables)")))
+                return rc;
+            if (c->tables.size() >= 64 && !c->n_graphs) {
                 // queued work may still read the cached tables
                 HIP_TRY(hipStreamSynchronize(c->stream));
                 for (auto& kv : c->tables) free_tables(kv.second);
                 c->tables.clear();
             }
             WorkTables w;
-            int rc = build_tables(c, active, &w);
+            rc = build_tables(c, active, &w);
             if (rc) {
                 free_tables(w);
                 return rc;
@@ -250,6 +278,10 @@ int select_tables(ttp_ctx* c, const uint32_t* subset, uint32_t nsub, const WorkT
 // beta^t only shrinks); py/optim.py:51-52 evaluates the same host-double expression.
 int ensure_bias_table(ttp_ctx* c, double b1, double b2) {
     if (c->bias_tab && c->bias_b1 == b1 && c->bias_b2 == b2) return TTP_OK;
+    int rc;
+    if ((rc = no_capture(c, "a step with new betas (builds a table)"))) return rc;
+    if (c->n_graphs)
+        return fail(TTP_ERR_STATE, "betas changed while graphs of this context are alive");
     std::vector<float> tab;
     const uint64_t kMax = 1ull << 24;
     for (uint64_t t = 1;; ++t) {
@@ -290,7 +322,7 @@ struct TimedLaunch {
     int kernel;
     hipEvent_t a = nullptr;
     TimedLaunch(ttp_ctx* ctx, int k) : c(ctx), kernel(k) {
-        if (c->timing && (a = take_event(c))) (void)hipEventRecord(a, c->stream);
+        if (c->timing && !c->capturing && (a = take_event(c))) (void)hipEventRecord(a, c->stream);
     }
     void done() {
         if (!a) return;
@@ -321,31 +353,37 @@ uint32_t norm_grid(const ttp_ctx* c, uint32_t nchunks) {
     return std::max<uint32_t>(1, std::min(nchunks, c->norm_grid_cap));
 }
 
-// norm / inf-check / finalize pass (two launches); `probe` only computes the norm
-int launch_norm(ttp_ctx* c, const WorkTables* w, double max_norm, bool probe, bool want_bias) {
+// Step prologue on the device: the norm pass (partials, when `run_norm`) and the one-block
+// finalize (norm, found_inf / skip, clip coefficient, loss scale, and the step count with its
+// bias corrections when `count_t`); `probe` only computes the norm.
+int launch_prologue(ttp_ctx* c, const WorkTables* w, bool run_norm, double max_norm, bool probe,
+                    bool want_bias, bool count_t) {
     const Chunk* chunks = w->tiles;
     const uint32_t n = w->n_tiles;
     const uint32_t grid = norm_grid(c, n);
     const int32_t scaler_on = c->scaler.enabled ? 1 : 0;
     TimedLaunch tl(c, TTP_KERNEL_NORM);
-    if (c->mode == TTP_MODE_MIXED)
-        hipLaunchKernelGGL(ttp::norm_partials_kernel<uint16_t>, dim3(grid), dim3(ttp::kBlock), 0,
-                           c->stream, (const uint16_t*)c->grad, chunks, n,
-                           (const DevState*)c->st, scaler_on, c->partials);
-    else
-        hipLaunchKernelGGL(ttp::norm_partials_kernel<float>, dim3(grid), dim3(ttp::kBlock), 0,
-                           c->stream, (const float*)c->grad, chunks, n, (const DevState*)c->st,
-                           scaler_on, c->partials);
-    HIP_TRY(hipGetLastError());
+    if (run_norm) {
+        if (c->mode == TTP_MODE_MIXED)
+            hipLaunchKernelGGL(ttp::norm_partials_kernel<uint16_t>, dim3(grid), dim3(ttp::kBlock),
+                               0, c->stream, (const uint16_t*)c->grad, chunks, n,
+                               (const DevState*)c->st, scaler_on, c->partials);
+        else
+            hipLaunchKernelGGL(ttp::norm_partials_kernel<float>, dim3(grid), dim3(ttp::kBlock), 0,
+                               c->stream, (const float*)c->grad, chunks, n,
+                               (const DevState*)c->st, scaler_on, c->partials);
+        HIP_TRY(hipGetLastError());
+    }
     ttp::FinalizeArgs a{};
     a.partials = c->partials;
-    a.npartials = grid;
-    a.scaler_on = scaler_on;
+    a.npartials = run_norm ? grid : 0;
+    a.scaler_on = run_norm ? scaler_on : 0;
+    a.count_t = count_t ? 1 : 0;
     a.probe = probe ? 1 : 0;
     a.growth_interval = c->scaler.growth_interval;
     a.growth_factor = c->scaler.growth_factor;
     a.backoff_factor = c->scaler.backoff_factor;
-    a.max_norm = max_norm;
+    a.max_norm = run_norm ? max_norm : 0.0;
     a.bias_tab = c->bias_tab;
     a.bias_len = c->bias_len;
     a.want_bias = want_bias ? 1 : 0;
@@ -374,7 +412,7 @@ int fill_report(ttp_ctx* c, bool norm_ran, ttp_step_report* r) {
     r->clip_coef = norm_ran ? s.clip_coef : 1.0f;
     r->scale = c->scaler.enabled ? s.scale : 1.0f;
     r->growth_tracker = c->scaler.enabled ? s.growth_tracker : 0;
-    r->step = c->scaler.enabled ? s.t : c->host_t;
+    r->step = t_on_device(c) ? s.t : c->host_t;
     return TTP_OK;
 }
 
@@ -441,7 +479,7 @@ void release(ttp_ctx* c) {
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     for (void* p : {(void*)c->grad, (void*)c->master, (void*)c->exp_avg, (void*)c->exp_avg_sq,
                     (void*)c->momentum, (void*)c->mom_init, (void*)c->st, (void*)c->partials,
-                    (void*)c->bias_tab})
+                    (void*)c->bias_tab, c->staging})
         if (p) (void)hipFree(p);
     free_tables(c->all);
     for (auto& kv : c->tables) free_tables(kv.second);
@@ -564,6 +602,14 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
 
 int ttp_destroy(ttp_ctx* c) {
     if (!c) return TTP_OK;
+    if (c->n_graphs)
+        return fail(TTP_ERR_STATE, std::to_string(c->n_graphs) +
+                                       " graph(s) of this context are alive; destroy them first");
+    if (c->capturing) {
+        hipGraph_t g = nullptr;
+        if (hipStreamEndCapture(c->stream, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
+        c->capturing = false;
+    }
     release(c);
     return TTP_OK;
 }
@@ -571,6 +617,7 @@ int ttp_destroy(ttp_ctx* c) {
 int ttp_set_stream(ttp_ctx* c, void* stream) {
     int rc = check_ctx(c);
     if (rc) return rc;
+    if ((rc = no_capture(c, "ttp_set_stream"))) return rc;
     if ((rc = set_dev(c))) return rc;
     HIP_TRY(hipStreamSynchronize(c->stream));
     c->stream = (hipStream_t)stream;
@@ -580,6 +627,7 @@ int ttp_set_stream(ttp_ctx* c, void* stream) {
 int ttp_reset_stream(ttp_ctx* c) {
     int rc = check_ctx(c);
     if (rc) return rc;
+    if ((rc = no_capture(c, "ttp_reset_stream"))) return rc;
     if ((rc = set_dev(c))) return rc;
     HIP_TRY(hipStreamSynchronize(c->stream));
     c->stream = c->own_stream;
@@ -589,6 +637,7 @@ int ttp_reset_stream(ttp_ctx* c) {
 int ttp_sync(ttp_ctx* c) {
     int rc = check_ctx(c);
     if (rc) return rc;
+    if ((rc = no_capture(c, "ttp_sync"))) return rc;
     if ((rc = set_dev(c))) return rc;
     HIP_TRY(hipStreamSynchronize(c->stream));
     return TTP_OK;
@@ -648,6 +697,7 @@ int ttp_buffer_ptr(ttp_ctx* c, int which, uint32_t index, void** ptr) {
 int ttp_upload(ttp_ctx* c, int which, uint32_t index, const void* src, uint64_t n, int kind) {
     int rc = check_ctx(c);
     if (rc) return rc;
+    if (kind == TTP_HOST && (rc = no_capture(c, "an upload from host memory"))) return rc;
     if (!src && n) return fail(TTP_ERR_INVALID, "null source");
     if (kind != TTP_HOST && kind != TTP_DEVICE) return fail(TTP_ERR_INVALID, "bad memory kind");
     if ((rc = set_dev(c))) return rc;
@@ -684,6 +734,7 @@ int ttp_upload(ttp_ctx* c, int which, uint32_t index, const void* src, uint64_t 
 int ttp_download(ttp_ctx* c, int which, uint32_t index, void* dst, uint64_t n, int kind) {
     int rc = check_ctx(c);
     if (rc) return rc;
+    if (kind == TTP_HOST && (rc = no_capture(c, "a download to host memory"))) return rc;
     if (!dst && n) return fail(TTP_ERR_INVALID, "null destination");
     if (kind != TTP_HOST && kind != TTP_DEVICE) return fail(TTP_ERR_INVALID, "bad memory kind");
     if ((rc = set_dev(c))) return rc;
@@ -731,6 +782,63 @@ int ttp_zero_grad(ttp_ctx* c, int set_to_none) {
     return TTP_OK;
 }
 
+int ttp_accumulate_grad(ttp_ctx* c, uint32_t index, const void* src, uint64_t n, int dtype,
+                        int kind) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if ((rc = check_index(c, index))) return rc;
+    if (dtype != TTP_DTYPE_F32 && dtype != TTP_DTYPE_BF16)
+        return fail(TTP_ERR_INVALID, "src_dtype must be TTP_DTYPE_F32 or TTP_DTYPE_BF16");
+    if (kind != TTP_HOST && kind != TTP_DEVICE) return fail(TTP_ERR_INVALID, "bad memory kind");
+    if (kind == TTP_HOST && (rc = no_capture(c, "accumulating a host gradient"))) return rc;
+    TensorRec& t = c->tensors[index];
+    if (n != t.numel)
+        return fail(TTP_ERR_RANGE, "tensor " + std::to_string(index) + " has " +
+                                       std::to_string(t.numel) + " elements, got " +
+                                       std::to_string(n));
+    if (!src && n) return fail(TTP_ERR_INVALID, "null source");
+    if ((rc = set_dev(c))) return rc;
+    const size_t sbytes = dtype == TTP_DTYPE_BF16 ? 2 : 4;
+    if (n) {
+        const void* dsrc = src;
+        if (kind == TTP_HOST) {
+            if (c->staging_bytes < n * sbytes) {
+                HIP_TRY(hipStreamSynchronize(c->stream));  // queued work may read the old one
+                if (c->staging) HIP_TRY(hipFree(c->staging));
+                c->staging = nullptr;
+                c->staging_bytes = 0;
+                HIP_TRY(hipMalloc(&c->staging, n * sbytes));
+                c->staging_bytes = n * sbytes;
+            }
+            HIP_TRY(hipMemcpyAsync(c->staging, src, n * sbytes, hipMemcpyHostToDevice, c->stream));
+            dsrc = c->staging;
+        }
+        const int first = t.has_grad ? 0 : 1;
+        const uint32_t grid = elementwise_grid(c, n);
+        const bool mixed = c->mode == TTP_MODE_MIXED;
+        if (mixed && dtype == TTP_DTYPE_BF16)
+            hipLaunchKernelGGL((ttp::accumulate_grad_kernel<uint16_t, uint16_t>), dim3(grid),
+                               dim3(ttp::kBlock), 0, c->stream, (uint16_t*)c->grad + t.offset,
+                               (const uint16_t*)dsrc, n, first);
+        else if (mixed)
+            hipLaunchKernelGGL((ttp::accumulate_grad_kernel<float, uint16_t>), dim3(grid),
+                               dim3(ttp::kBlock), 0, c->stream, (uint16_t*)c->grad + t.offset,
+                               (const float*)dsrc, n, first);
+        else if (dtype == TTP_DTYPE_BF16)
+            hipLaunchKernelGGL((ttp::accumulate_grad_kernel<uint16_t, float>), dim3(grid),
+                               dim3(ttp::kBlock), 0, c->stream, (float*)c->grad + t.offset,
+                               (const uint16_t*)dsrc, n, first);
+        else
+            hipLaunchKernelGGL((ttp::accumulate_grad_kernel<float, float>), dim3(grid),
+                               dim3(ttp::kBlock), 0, c->stream, (float*)c->grad + t.offset,
+                               (const float*)dsrc, n, first);
+        HIP_TRY(hipGetLastError());
+        if (kind == TTP_HOST) HIP_TRY(hipStreamSynchronize(c->stream));
+    }
+    t.has_grad = 1;
+    return TTP_OK;
+}
+
 static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t* subset,
                           uint32_t nsub, ttp_step_report* report) {
     int rc = check_ctx(c);
@@ -742,6 +850,7 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
     if (!(hp->beta1 > 0 && hp->beta1 < 1 && hp->beta2 > 0 && hp->beta2 < 1))
         return fail(TTP_ERR_INVALID, "betas must be in (0, 1)");
     if (!(hp->weight_decay >= 0)) return fail(TTP_ERR_INVALID, "weight_decay must be >= 0");
+    if (report && (rc = no_capture(c, "a step report (synchronises)"))) return rc;
     if ((rc = set_dev(c))) return rc;
     if ((rc = ensure_adam_state(c))) return rc;
     const WorkTables* w;
@@ -752,8 +861,13 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
     const bool scaler = c->scaler.enabled != 0;
     const bool clip = hp->max_grad_norm > 0;
     const bool need_norm = scaler || clip;
-    if (scaler && (rc = ensure_bias_table(c, hp->beta1, hp->beta2))) return rc;
-    if (need_norm && (rc = launch_norm(c, w, hp->max_grad_norm, false, scaler))) return rc;
+    const bool devt = t_on_device(c);
+    // the device table of bias corrections; built in host-count mode too (once per betas) so
+    // that a later capture finds it, except when betas so close to 1 make it too long
+    if ((rc = ensure_bias_table(c, hp->beta1, hp->beta2)) && devt) return rc;
+    if ((need_norm || devt) &&
+        (rc = launch_prologue(c, w, need_norm, hp->max_grad_norm, false, devt, devt)))
+        return rc;
 
     ttp::AdamArgs a{};
     a.chunks = chunks;
@@ -768,10 +882,11 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
     a.decay_mul = (float)(1.0 - hp->lr * hp->weight_decay);
     a.wd = (float)hp->weight_decay;
     a.flags = (hp->decoupled ? ttp::kDecoupled : 0u) | (hp->weight_decay != 0.0 ? ttp::kWdOn : 0u);
-    if (scaler) a.flags |= ttp::kUseInv | ttp::kDevBias | ttp::kCheckSkip;
+    if (scaler) a.flags |= ttp::kUseInv | ttp::kCheckSkip;
+    if (devt) a.flags |= ttp::kDevBias;
     if (clip) a.flags |= ttp::kUseClip;
-    a.st = need_norm ? c->st : nullptr;
-    if (!scaler) {
+    a.st = (need_norm || devt) ? c->st : nullptr;
+    if (!devt) {
         c->host_t += 1;  // py/optim.py:50
         a.bias1 = (float)(1.0 - std::pow(hp->beta1, (double)c->host_t));
         a.bias2 = (float)(1.0 - std::pow(hp->beta2, (double)c->host_t));
@@ -806,6 +921,7 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
     if (!(hp->weight_decay >= 0)) return fail(TTP_ERR_INVALID, "weight_decay must be >= 0");
     if (hp->nesterov && (hp->momentum <= 0 || hp->dampening != 0))
         return fail(TTP_ERR_INVALID, "nesterov needs momentum > 0 and zero dampening");
+    if (report && (rc = no_capture(c, "a step report (synchronises)"))) return rc;
     if ((rc = set_dev(c))) return rc;
     const bool mom = hp->momentum != 0.0;
     if (mom && (rc = ensure_momentum(c))) return rc;
@@ -818,8 +934,11 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
     const bool scaler = c->scaler.enabled != 0;
     const bool clip = hp->max_grad_norm > 0;
     const bool need_norm = scaler || clip;
-    if (need_norm && (rc = launch_norm(c, w, hp->max_grad_norm, false, false))) return rc;
-    if (!scaler) c->host_t += 1;
+    const bool devt = t_on_device(c);
+    if ((need_norm || devt) &&
+        (rc = launch_prologue(c, w, need_norm, hp->max_grad_norm, false, false, devt)))
+        return rc;
+    if (!devt) c->host_t += 1;
 
     ttp::SgdArgs a{};
     a.chunks = chunks;
@@ -833,7 +952,7 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
               (hp->nesterov ? ttp::kNesterov : 0u);
     if (scaler) a.flags |= ttp::kUseInv | ttp::kCheckSkip;
     if (clip) a.flags |= ttp::kUseClip;
-    a.st = need_norm ? c->st : nullptr;
+    a.st = (need_norm || devt) ? c->st : nullptr;
     if (n) {
         const uint32_t grid = update_grid(c, n);
         TimedLaunch tl(c, TTP_KERNEL_UPDATE);
@@ -849,8 +968,9 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
         tl.done();
         if (mom) {
             // the stepped tensors now hold a momentum buffer (torch: state created on first
-            // use); with loss scaling the device decides, since the step may be skipped
-            bool needed = scaler;
+            // use); with loss scaling the device decides, since the step may be skipped, and
+            // once captured the marking is part of every replay
+            bool needed = scaler || devt;
             for (uint32_t i : active)
                 if (!c->host_mom_init[i]) needed = true;
             if (needed) {
@@ -860,7 +980,7 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
                                    scaler ? 1 : 0);
                 HIP_TRY(hipGetLastError());
             }
-            if (!scaler)
+            if (!scaler && !devt)
                 for (uint32_t i : active) c->host_mom_init[i] = 1;
         }
     }
@@ -899,10 +1019,11 @@ int ttp_grad_norm(ttp_ctx* c, double* norm) {
     int rc = check_ctx(c);
     if (rc) return rc;
     if (!norm) return fail(TTP_ERR_INVALID, "null output");
+    if ((rc = no_capture(c, "ttp_grad_norm (synchronises)"))) return rc;
     if ((rc = set_dev(c))) return rc;
     const WorkTables* w;
     if ((rc = select_tables(c, nullptr, 0, &w, nullptr))) return rc;
-    if ((rc = launch_norm(c, w, 0.0, true, false))) return rc;
+    if ((rc = launch_prologue(c, w, true, 0.0, true, false, false))) return rc;
     DevState s;
     if ((rc = read_state(c, &s))) return rc;
     *norm = s.norm;
@@ -913,10 +1034,11 @@ int ttp_get_step(ttp_ctx* c, uint64_t* step) {
     int rc = check_ctx(c);
     if (rc) return rc;
     if (!step) return fail(TTP_ERR_INVALID, "null output");
-    if (!c->scaler.enabled) {
+    if (!t_on_device(c)) {
         *step = c->host_t;
         return TTP_OK;
     }
+    if ((rc = no_capture(c, "ttp_get_step (synchronises)"))) return rc;
     if ((rc = set_dev(c))) return rc;
     DevState s;
     if ((rc = read_state(c, &s))) return rc;
@@ -927,6 +1049,7 @@ int ttp_get_step(ttp_ctx* c, uint64_t* step) {
 int ttp_set_step(ttp_ctx* c, uint64_t step) {
     int rc = check_ctx(c);
     if (rc) return rc;
+    if ((rc = no_capture(c, "ttp_set_step"))) return rc;
     if ((rc = set_dev(c))) return rc;
     c->host_t = step;
     HIP_TRY(hipStreamSynchronize(c->stream));
@@ -945,13 +1068,15 @@ int ttp_scaler_configure(ttp_ctx* c, const ttp_scaler_config* cfg) {
             return fail(TTP_ERR_INVALID, "backoff_factor must be in (0, 1)");
         if (cfg->growth_interval <= 0) return fail(TTP_ERR_INVALID, "growth_interval must be > 0");
     }
+    if ((rc = no_capture(c, "ttp_scaler_configure"))) return rc;
     if ((rc = set_dev(c))) return rc;
     HIP_TRY(hipStreamSynchronize(c->stream));
     DevState s;
     HIP_TRY(hipMemcpy(&s, c->st, sizeof(s), hipMemcpyDeviceToHost));
-    if (c->scaler.enabled && !cfg->enabled) c->host_t = s.t;  // device count -> host
+    const bool was = t_on_device(c), will = cfg->enabled || c->device_t;
+    if (was && !will) c->host_t = s.t;  // device count -> host
+    if (!was && will) s.t = c->host_t;  // host count -> device
     if (cfg->enabled) {
-        if (!c->scaler.enabled) s.t = c->host_t;  // host count -> device
         s.scale = (float)cfg->init_scale;
         s.growth_tracker = 0;
     }
@@ -963,6 +1088,7 @@ int ttp_scaler_configure(ttp_ctx* c, const ttp_scaler_config* cfg) {
 int ttp_scaler_get(ttp_ctx* c, float* scale, int32_t* tracker) {
     int rc = check_ctx(c);
     if (rc) return rc;
+    if ((rc = no_capture(c, "ttp_scaler_get (synchronises)"))) return rc;
     if ((rc = set_dev(c))) return rc;
     DevState s;
     if ((rc = read_state(c, &s))) return rc;
@@ -975,6 +1101,7 @@ int ttp_scaler_set(ttp_ctx* c, float scale, int32_t tracker) {
     int rc = check_ctx(c);
     if (rc) return rc;
     if (!(scale > 0) || tracker < 0) return fail(TTP_ERR_INVALID, "scale must be > 0, tracker >= 0");
+    if ((rc = no_capture(c, "ttp_scaler_set"))) return rc;
     if ((rc = set_dev(c))) return rc;
     HIP_TRY(hipStreamSynchronize(c->stream));
     DevState s;
@@ -982,6 +1109,71 @@ int ttp_scaler_set(ttp_ctx* c, float scale, int32_t tracker) {
     s.scale = scale;
     s.growth_tracker = tracker;
     HIP_TRY(hipMemcpy(c->st, &s, sizeof(s), hipMemcpyHostToDevice));
+    return TTP_OK;
+}
+
+int ttp_capture_begin(ttp_ctx* c) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if ((rc = no_capture(c, "ttp_capture_begin"))) return rc;
+    if (!c->stream)
+        return fail(TTP_ERR_STATE, "the legacy default stream cannot be captured; use the "
+                                   "context's own stream or a created stream");
+    if ((rc = set_dev(c))) return rc;
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    if (!t_on_device(c)) {  // from now on the step count lives on the device
+        HIP_TRY(hipMemcpy(&c->st->t, &c->host_t, sizeof(c->host_t), hipMemcpyHostToDevice));
+    }
+    c->device_t = true;
+    HIP_TRY(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    c->capturing = true;
+    return TTP_OK;
+}
+
+int ttp_capture_end(ttp_ctx* c, ttp_graph** out) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (out) *out = nullptr;
+    if (!c->capturing) return fail(TTP_ERR_STATE, "not capturing");
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(c->stream, &g);
+    c->capturing = false;
+    if (e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return fail(TTP_ERR_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
+    }
+    if (!out) {  // discard
+        if (g) (void)hipGraphDestroy(g);
+        return TTP_OK;
+    }
+    hipGraphExec_t ex = nullptr;
+    const hipError_t e2 = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    if (e2 != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return fail(TTP_ERR_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(e2));
+    }
+    *out = new ttp_graph{c, g, ex};
+    c->n_graphs += 1;
+    return TTP_OK;
+}
+
+int ttp_graph_launch(ttp_graph* g) {
+    if (!g) return fail(TTP_ERR_INVALID, "null graph");
+    int rc;
+    if ((rc = no_capture(g->ctx, "ttp_graph_launch"))) return rc;
+    if ((rc = set_dev(g->ctx))) return rc;
+    HIP_TRY(hipGraphLaunch(g->exec, g->ctx->stream));
+    return TTP_OK;
+}
+
+int ttp_graph_destroy(ttp_graph* g) {
+    if (!g) return TTP_OK;
+    (void)hipSetDevice(g->ctx->device);
+    if (g->ctx->stream) (void)hipStreamSynchronize(g->ctx->stream);
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    g->ctx->n_graphs -= 1;
+    delete g;
     return TTP_OK;
 }
 

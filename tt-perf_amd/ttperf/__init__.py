@@ -7,7 +7,8 @@ multi-tensor HIP launch.  Importing fails if the HIP library is not built.
 from . import _lib
 from ._lib import TTPError, TTPValueError, device_count
 from .optim import SGD, Adam, AdamW
-from .store import GradView, Parameter, ParamStore, Tensor
+from .store import GradView, Parameter, ParamStore, StepGraph, Tensor, TraceContext
 
 __all__ = ["SGD", "Adam", "AdamW", "ParamStore", "Tensor", "Parameter", "GradView",
+           "StepGraph", "TraceContext",
            "TTPError", "TTPValueError", "device_count", "_lib"]

@@ -17,6 +17,7 @@ BUF_PARAM, BUF_GRAD, BUF_MASTER, BUF_EXP_AVG, BUF_EXP_AVG_SQ, BUF_MOMENTUM = ran
 ALL_TENSORS = 0xFFFFFFFF
 TENSOR_DECAY = 1
 HOST, DEVICE = 0, 1
+DTYPE_F32, DTYPE_BF16 = 0, 1
 KERNEL_NORM, KERNEL_UPDATE = 0, 1
 
 
@@ -71,6 +72,7 @@ SIGNATURES = {
     "ttp_set_has_grad": (C.c_int, [_P, C.c_uint32, C.c_int]),
     "ttp_get_has_grad": (C.c_int, [_P, C.c_uint32, C.POINTER(C.c_int)]),
     "ttp_zero_grad": (C.c_int, [_P, C.c_int]),
+    "ttp_accumulate_grad": (C.c_int, [_P, C.c_uint32, _P, C.c_uint64, C.c_int, C.c_int]),
     "ttp_adam_step": (C.c_int, [_P, C.POINTER(AdamHParams), C.POINTER(StepReport)]),
     "ttp_sgd_step": (C.c_int, [_P, C.POINTER(SgdHParams), C.POINTER(StepReport)]),
     "ttp_adam_step_subset": (C.c_int, [_P, C.POINTER(AdamHParams), C.POINTER(C.c_uint32),
@@ -83,6 +85,10 @@ SIGNATURES = {
     "ttp_scaler_configure": (C.c_int, [_P, C.POINTER(ScalerConfig)]),
     "ttp_scaler_get": (C.c_int, [_P, C.POINTER(C.c_float), C.POINTER(C.c_int32)]),
     "ttp_scaler_set": (C.c_int, [_P, C.c_float, C.c_int32]),
+    "ttp_capture_begin": (C.c_int, [_P]),
+    "ttp_capture_end": (C.c_int, [_P, C.POINTER(_P)]),
+    "ttp_graph_launch": (C.c_int, [_P]),
+    "ttp_graph_destroy": (C.c_int, [_P]),
     "ttp_timing_enable": (C.c_int, [_P, C.c_int]),
     "ttp_timing_collect": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
     "ttp_last_error": (C.c_char_p, []),

@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes as C
 import math
+import weakref
 
 import numpy as np
 
@@ -60,6 +61,11 @@ class Tensor:
     def zero_grad(self):
         self.grad = None
 
+    def accumulate_grad(self, value):
+        """py/engine.py:149-156 `_add_grad`: grad = value if grad is None else grad + value,
+        summed in fp32 and rounded once to the grad buffer's type (bf16 in MIXED mode)."""
+        self.store.accumulate_grad(self.index, value)
+
     # ---- data ----------------------------------------------------------------------------
     def numpy(self):
         """Model-facing weights as float32 (bf16 widened in MIXED mode)."""
@@ -94,6 +100,59 @@ class GradView:
 
     def data_ptr(self):
         return self.p.store.ptr(L.BUF_GRAD, self.p.index)
+
+
+class StepGraph:
+    """A captured hipGraph of a store's work (ttp_capture_begin .. ttp_capture_end)."""
+
+    def __init__(self, store: "ParamStore", handle):
+        self.store = store
+        self._g = handle
+
+    def replay(self):
+        L.check(L.lib.ttp_graph_launch(self._g))
+
+    def close(self):
+        if getattr(self, "_g", None):
+            L.lib.ttp_graph_destroy(self._g)
+            self._g = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class TraceContext:
+    """autograd/traced/trace.hpp:21-88 over a store: the first run(fn) captures what fn
+    queues on the store's stream (its optimizer steps, zero_grad, device transfers) and
+    executes it once; later calls replay the graph."""
+
+    def __init__(self, store: "ParamStore"):
+        self.store = store
+        self.graph = None
+
+    def run(self, fn):
+        if self.graph is None:
+            self.store.begin_capture()
+            try:
+                fn()
+            except BaseException:
+                self.store.end_capture(discard=True)
+                raise
+            self.graph = self.store.end_capture()
+        self.graph.replay()
+
+    def is_captured(self):
+        return self.graph is not None
+
+    def release(self):
+        if self.graph is not None:
+            self.graph.close()
+            self.graph = None
+
+    reset = release
 
 
 class ParamStore:
@@ -133,10 +192,13 @@ class ParamStore:
         L.check(L.lib.ttp_flat_numel(self._h, C.byref(tot)))
         self.total = tot.value
         self._scaler_enabled = False
+        self._graphs = weakref.WeakSet()
 
     # ---- lifetime --------------------------------------------------------------------------
     def close(self):
         if getattr(self, "_h", None):
+            for g in list(getattr(self, "_graphs", ())):
+                g.close()  # a context's graphs go before the context
             L.lib.ttp_destroy(self._h)
             self._h = None
 
@@ -246,6 +308,37 @@ class ParamStore:
     def zero_grad(self, set_to_none=True):
         L.check(L.lib.ttp_zero_grad(self._h, 1 if set_to_none else 0))
 
+    def accumulate_grad(self, index, value):
+        """Add an incoming gradient (numpy float32 / uint16 bf16 bits, or a torch float32 /
+        bfloat16 tensor on the host or the GPU) into tensor `index`'s grad."""
+        n = self.tensors[index].numel
+        if _is_torch(value):
+            import torch
+            t = value.detach().contiguous()
+            if t.dtype not in (torch.float32, torch.bfloat16):
+                raise ValueError("incoming gradients must be float32 or bfloat16")
+            if t.numel() != n:
+                raise ValueError(f"expected {n} elements, got {t.numel()}")
+            dtype = L.DTYPE_BF16 if t.dtype == torch.bfloat16 else L.DTYPE_F32
+            if t.is_cuda:
+                torch.cuda.current_stream(t.device).synchronize()
+            L.check(L.lib.ttp_accumulate_grad(self._h, index, C.c_void_p(t.data_ptr()), n, dtype,
+                                              L.DEVICE if t.is_cuda else L.HOST))
+            if t.is_cuda:
+                self.sync()  # `t` may be freed and reused by torch as soon as we return
+            return
+        a = np.asarray(value)
+        if a.dtype == np.uint16:
+            dtype = L.DTYPE_BF16
+        else:
+            a = a.astype(np.float32, copy=False)
+            dtype = L.DTYPE_F32
+        a = np.ascontiguousarray(a).ravel()
+        if a.size != n:
+            raise ValueError(f"expected {n} elements, got {a.size}")
+        L.check(L.lib.ttp_accumulate_grad(self._h, index, a.ctypes.data_as(C.c_void_p), n, dtype,
+                                          L.HOST))
+
     # ---- steps -----------------------------------------------------------------------------------
     @staticmethod
     def _index_array(indices):
@@ -315,6 +408,22 @@ class ParamStore:
 
     def set_scaler_state(self, scale, growth_tracker):
         L.check(L.lib.ttp_scaler_set(self._h, scale, growth_tracker))
+
+    # ---- graph capture ------------------------------------------------------------------------
+    def begin_capture(self):
+        """Capture the store's work until end_capture() (the store must use its own stream
+        or a created stream, not the legacy default stream)."""
+        L.check(L.lib.ttp_capture_begin(self._h))
+
+    def end_capture(self, discard=False):
+        if discard:
+            L.check(L.lib.ttp_capture_end(self._h, None))
+            return None
+        g = C.c_void_p()
+        L.check(L.lib.ttp_capture_end(self._h, C.byref(g)))
+        graph = StepGraph(self, g)
+        self._graphs.add(graph)
+        return graph
 
     # ---- timing -----------------------------------------------------------------------------------
     def timing(self, on=True):
