@@ -211,6 +211,25 @@ int ttp_scaler_configure(ttp_ctx* ctx, const ttp_scaler_config* cfg);
 int ttp_scaler_get(ttp_ctx* ctx, float* scale, int32_t* growth_tracker);
 int ttp_scaler_set(ttp_ctx* ctx, float scale, int32_t growth_tracker);
 
+/* ---- optimizer-state checkpoint ------------------------------------------------------------
+ * The reference has no optimizer checkpoint (its TTNN tensors live only in device memory).
+ * ttp_save_state writes what a resumed run needs to continue bit for bit: the fp32 master
+ * weights, the Adam moments and the momentum buffer that exist, the per-tensor momentum
+ * initialisation flags, the step count t and the loss scaler (config, scale, tracker), with
+ * the tensor table they belong to and a trailing checksum.  Gradients are not saved.
+ * Layout (little-endian): "TTPSTATE", u32 version 1, u32 mode, u32 n_tensors, u32 buffer
+ * mask (1 master, 2 exp_avg, 4 exp_avg_sq, 8 momentum), u64 total, u64 t, f32 scale,
+ * i32 growth_tracker, i32 scaler enabled, i32 growth_interval, f64 init_scale,
+ * f64 growth_factor, f64 backoff_factor; n_tensors x {u64 numel, u32 flags, u32 momentum
+ * initialised}; each present buffer as total fp32 values (padding included); u64 checksum
+ * of all preceding bytes.  Both calls are synchronous and stream through a 64 MiB pinned
+ * buffer.  ttp_load_state requires the same mode and tensor table (numel and flags); a
+ * buffer the file lacks is zeroed; the bf16 weights are recomputed from the master.  If it
+ * fails after the header checks (read error, checksum mismatch), the context's optimizer
+ * state is undefined until a load succeeds. */
+int ttp_save_state(ttp_ctx* ctx, const char* path);
+int ttp_load_state(ttp_ctx* ctx, const char* path);
+
 /* ---- graph capture and replay -------------------------------------------------------------
  * The counterpart of traced::TraceContext (autograd/traced/trace.hpp:21-88: capture once,
  * then replay): everything queued on the context's stream between ttp_capture_begin and

@@ -220,6 +220,8 @@ public:
         return t;
     }
     void sync() { check(ttp_sync(ctx_)); }
+    void save_state(const std::string& path) { check(ttp_save_state(ctx_, path.c_str())); }
+    void load_state(const std::string& path) { check(ttp_load_state(ctx_, path.c_str())); }
     void begin_capture() { check(ttp_capture_begin(ctx_)); }
     Graph end_capture() {
         ttp_graph* g = nullptr;

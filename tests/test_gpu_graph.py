@@ -243,3 +243,27 @@ def test_accumulate_grad_host_and_device_sources(mode):
     e = ref.adam_step(**hp)
     assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-9 * e["grad_norm"]
     compare_state(store, ref, max_ulp=2)
+
+
+def test_closing_other_stores_during_capture_is_deferred():
+    """A store (or graph) closed while another store is capturing would free device memory on
+    the capturing thread, which invalidates the capture: the close waits for the capture to
+    end.  This is what an unrelated store's finalizer does when Python collects it."""
+    import gc
+    import ttperf
+    other = ttperf.ParamStore([(4096,)], mode="fp32")
+    store = ttperf.ParamStore([(1000,)], mode="mixed")
+    store.tensors[0].grad = np.zeros(1000, np.uint16)
+    store.sgd_step(lr=0.1)
+    store.begin_capture()
+    assert not gc.isenabled()
+    other.close()                      # deferred, not destroyed inside the capture
+    assert other.handle is not None
+    store.sgd_step(lr=0.1)
+    graph = store.end_capture()        # the capture is intact
+    assert other.handle is None        # destroyed once the capture ended
+    assert gc.isenabled()
+    graph.replay()
+    assert store.step_count == 2
+    graph.close()
+    store.close()

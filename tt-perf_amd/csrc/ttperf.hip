@@ -14,6 +14,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -1109,6 +1110,227 @@ int ttp_scaler_set(ttp_ctx* c, float scale, int32_t tracker) {
     s.scale = scale;
     s.growth_tracker = tracker;
     HIP_TRY(hipMemcpy(c->st, &s, sizeof(s), hipMemcpyHostToDevice));
+    return TTP_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+constexpr char kStateMagic[8] = {'T', 'T', 'P', 'S', 'T', 'A', 'T', 'E'};
+constexpr uint32_t kStateVersion = 1;
+constexpr size_t kStageBytes = 64ull << 20;
+
+#pragma pack(push, 1)
+struct StateHeader {
+    char magic[8];
+    uint32_t version, mode, n_tensors, buffers;
+    uint64_t total, t;
+    float scale;
+    int32_t growth_tracker, scaler_enabled, growth_interval;
+    double init_scale, growth_factor, backoff_factor;
+};
+struct StateTensor {
+    uint64_t numel;
+    uint32_t flags, mom_init;
+};
+#pragma pack(pop)
+
+// 64-bit word hash (FNV-1a style multiply over 8-byte words, then a final avalanche)
+struct Hash {
+    uint64_t h = 0xcbf29ce484222325ull;
+    void add(const void* p, size_t n) {
+        const uint8_t* b = (const uint8_t*)p;
+        size_t k = 0;
+        for (; k + 8 <= n; k += 8) {
+            uint64_t w;
+            std::memcpy(&w, b + k, 8);
+            h = (h ^ w) * 0x100000001b3ull;
+            h ^= h >> 29;
+        }
+        for (; k < n; ++k) h = (h ^ b[k]) * 0x100000001b3ull;
+    }
+    uint64_t value() const {
+        uint64_t x = h;
+        x ^= x >> 33;
+        x *= 0xff51afd7ed558ccdull;
+        x ^= x >> 33;
+        return x;
+    }
+};
+
+struct File {
+    FILE* f = nullptr;
+    ~File() {
+        if (f) std::fclose(f);
+    }
+};
+
+struct Pinned {
+    void* p = nullptr;
+    ~Pinned() {
+        if (p) (void)hipHostFree(p);
+    }
+};
+
+float** state_buffer(ttp_ctx* c, int bit) {
+    switch (bit) {
+        case 1: return &c->master;
+        case 2: return &c->exp_avg;
+        case 4: return &c->exp_avg_sq;
+        case 8: return &c->momentum;
+    }
+    return nullptr;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ttp_save_state(ttp_ctx* c, const char* path) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!path) return fail(TTP_ERR_INVALID, "null path");
+    if ((rc = no_capture(c, "ttp_save_state"))) return rc;
+    if ((rc = set_dev(c))) return rc;
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    DevState ds;
+    HIP_TRY(hipMemcpy(&ds, c->st, sizeof(ds), hipMemcpyDeviceToHost));
+    std::vector<uint32_t> mom(std::max<size_t>(c->tensors.size(), 1), 0);
+    HIP_TRY(hipMemcpy(mom.data(), c->mom_init, mom.size() * 4, hipMemcpyDeviceToHost));
+
+    StateHeader h{};
+    std::memcpy(h.magic, kStateMagic, 8);
+    h.version = kStateVersion;
+    h.mode = (uint32_t)c->mode;
+    h.n_tensors = (uint32_t)c->tensors.size();
+    h.buffers = 1u | (c->exp_avg ? 2u : 0u) | (c->exp_avg_sq ? 4u : 0u) | (c->momentum ? 8u : 0u);
+    h.total = c->total;
+    h.t = t_on_device(c) ? ds.t : c->host_t;
+    h.scale = ds.scale;
+    h.growth_tracker = ds.growth_tracker;
+    h.scaler_enabled = c->scaler.enabled;
+    h.growth_interval = c->scaler.growth_interval;
+    h.init_scale = c->scaler.init_scale;
+    h.growth_factor = c->scaler.growth_factor;
+    h.backoff_factor = c->scaler.backoff_factor;
+
+    File f;
+    f.f = std::fopen(path, "wb");
+    if (!f.f) return fail(TTP_ERR_INVALID, std::string("cannot open ") + path + " for writing");
+    Hash hash;
+    auto put = [&](const void* p, size_t n) {
+        hash.add(p, n);
+        return std::fwrite(p, 1, n, f.f) == n;
+    };
+    bool ok = put(&h, sizeof(h));
+    for (size_t i = 0; ok && i < c->tensors.size(); ++i) {
+        StateTensor t{c->tensors[i].numel, c->tensors[i].flags, mom[i]};
+        ok = put(&t, sizeof(t));
+    }
+    Pinned stage;
+    HIP_TRY(hipHostMalloc(&stage.p, kStageBytes));
+    for (int bit = 1; ok && bit <= 8; bit <<= 1) {
+        if (!(h.buffers & (uint32_t)bit)) continue;
+        const char* src = (const char*)*state_buffer(c, bit);
+        const uint64_t bytes = c->total * 4;
+        for (uint64_t o = 0; ok && o < bytes; o += kStageBytes) {
+            const size_t n = (size_t)std::min<uint64_t>(kStageBytes, bytes - o);
+            HIP_TRY(hipMemcpy(stage.p, src + o, n, hipMemcpyDeviceToHost));
+            ok = put(stage.p, n);
+        }
+    }
+    const uint64_t sum = hash.value();
+    ok = ok && std::fwrite(&sum, 1, 8, f.f) == 8;
+    ok = ok && std::fflush(f.f) == 0;
+    if (!ok) return fail(TTP_ERR_INVALID, std::string("write to ") + path + " failed");
+    return TTP_OK;
+}
+
+int ttp_load_state(ttp_ctx* c, const char* path) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!path) return fail(TTP_ERR_INVALID, "null path");
+    if ((rc = no_capture(c, "ttp_load_state"))) return rc;
+    if ((rc = set_dev(c))) return rc;
+    File f;
+    f.f = std::fopen(path, "rb");
+    if (!f.f) return fail(TTP_ERR_INVALID, std::string("cannot open ") + path);
+    Hash hash;
+    auto get = [&](void* p, size_t n) {
+        if (std::fread(p, 1, n, f.f) != n) return false;
+        hash.add(p, n);
+        return true;
+    };
+    StateHeader h;
+    if (!get(&h, sizeof(h)) || std::memcmp(h.magic, kStateMagic, 8) != 0)
+        return fail(TTP_ERR_INVALID, std::string(path) + " is not an optimizer-state file");
+    if (h.version != kStateVersion)
+        return fail(TTP_ERR_INVALID, "unsupported state file version " + std::to_string(h.version));
+    if (h.mode != (uint32_t)c->mode)
+        return fail(TTP_ERR_INVALID, "state file precision mode differs from the context's");
+    if (h.n_tensors != c->tensors.size())
+        return fail(TTP_ERR_INVALID, "state file has " + std::to_string(h.n_tensors) +
+                                         " tensors, the context " +
+                                         std::to_string(c->tensors.size()));
+    if (!(h.buffers & 1u) || (h.buffers & ~15u))
+        return fail(TTP_ERR_INVALID, "state file buffer mask is malformed");
+    std::vector<uint32_t> mom(std::max<size_t>(c->tensors.size(), 1), 0);
+    for (size_t i = 0; i < c->tensors.size(); ++i) {
+        StateTensor t;
+        if (!get(&t, sizeof(t))) return fail(TTP_ERR_INVALID, "state file is truncated");
+        if (t.numel != c->tensors[i].numel || t.flags != c->tensors[i].flags)
+            return fail(TTP_ERR_INVALID, "state file tensor " + std::to_string(i) +
+                                             " differs from the context's (numel or flags)");
+        mom[i] = t.mom_init ? 1u : 0u;
+    }
+    if (h.total != c->total)  // the layout follows from the table; this catches a bad header
+        return fail(TTP_ERR_INVALID, "state file flat size differs from the context's");
+    // allocate what the file holds; zero what the context holds and the file does not
+    if ((h.buffers & 6u) && (rc = ensure_adam_state(c))) return rc;
+    if ((h.buffers & 8u) && (rc = ensure_momentum(c))) return rc;
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    Pinned stage;
+    HIP_TRY(hipHostMalloc(&stage.p, kStageBytes));
+    for (int bit = 1; bit <= 8; bit <<= 1) {
+        float* dst = *state_buffer(c, bit);
+        if (!(h.buffers & (uint32_t)bit)) {
+            if (dst && (rc = zero_device(c, dst, c->total * 4))) return rc;
+            continue;
+        }
+        const uint64_t bytes = c->total * 4;
+        for (uint64_t o = 0; o < bytes; o += kStageBytes) {
+            const size_t n = (size_t)std::min<uint64_t>(kStageBytes, bytes - o);
+            if (!get(stage.p, n)) return fail(TTP_ERR_INVALID, "state file is truncated");
+            HIP_TRY(hipMemcpy((char*)dst + o, stage.p, n, hipMemcpyHostToDevice));
+        }
+    }
+    const uint64_t want = hash.value();
+    uint64_t sum = 0;
+    if (std::fread(&sum, 1, 8, f.f) != 8) return fail(TTP_ERR_INVALID, "state file is truncated");
+    if (sum != want) return fail(TTP_ERR_INVALID, "state file checksum mismatch");
+    if (c->mode == TTP_MODE_MIXED && c->total) {
+        hipLaunchKernelGGL(ttp::master_to_bf16_kernel, dim3(elementwise_grid(c, c->total)),
+                           dim3(ttp::kBlock), 0, c->stream, c->master, (uint16_t*)c->param,
+                           c->total);
+        HIP_TRY(hipGetLastError());
+    }
+    HIP_TRY(hipMemcpyAsync(c->mom_init, mom.data(), mom.size() * 4, hipMemcpyHostToDevice,
+                           c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    for (size_t i = 0; i < c->tensors.size(); ++i) c->host_mom_init[i] = (uint8_t)mom[i];
+    c->scaler.enabled = h.scaler_enabled;
+    c->scaler.growth_interval = h.growth_interval;
+    c->scaler.init_scale = h.init_scale;
+    c->scaler.growth_factor = h.growth_factor;
+    c->scaler.backoff_factor = h.backoff_factor;
+    c->host_t = h.t;
+    DevState ds;
+    HIP_TRY(hipMemcpy(&ds, c->st, sizeof(ds), hipMemcpyDeviceToHost));
+    ds.t = h.t;
+    ds.scale = h.scale;
+    ds.growth_tracker = h.growth_tracker;
+    HIP_TRY(hipMemcpy(c->st, &ds, sizeof(ds), hipMemcpyHostToDevice));
     return TTP_OK;
 }
 

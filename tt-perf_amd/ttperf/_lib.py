@@ -85,6 +85,8 @@ SIGNATURES = {
     "ttp_scaler_configure": (C.c_int, [_P, C.POINTER(ScalerConfig)]),
     "ttp_scaler_get": (C.c_int, [_P, C.POINTER(C.c_float), C.POINTER(C.c_int32)]),
     "ttp_scaler_set": (C.c_int, [_P, C.c_float, C.c_int32]),
+    "ttp_save_state": (C.c_int, [_P, C.c_char_p]),
+    "ttp_load_state": (C.c_int, [_P, C.c_char_p]),
     "ttp_capture_begin": (C.c_int, [_P]),
     "ttp_capture_end": (C.c_int, [_P, C.POINTER(_P)]),
     "ttp_graph_launch": (C.c_int, [_P]),

@@ -8,6 +8,7 @@ at `offset` of the store's param / grad / master / moment buffers.
 from __future__ import annotations
 
 import ctypes as C
+import gc
 import math
 import weakref
 
@@ -102,6 +103,33 @@ class GradView:
         return self.p.store.ptr(L.BUF_GRAD, self.p.index)
 
 
+# Stream capture forbids HIP calls that free memory or synchronise on the capturing thread
+# (they invalidate the capture).  Python may run a finalizer at any allocation (cyclic GC), so
+# while any store is capturing, stores and graphs that get closed are destroyed only after
+# the capture ends, and the cyclic collector is paused.
+_capturing = 0
+_gc_was_enabled = True
+_deferred = []
+
+
+def _capture_started():
+    global _capturing, _gc_was_enabled
+    if _capturing == 0:
+        _gc_was_enabled = gc.isenabled()
+        gc.disable()
+    _capturing += 1
+
+
+def _capture_ended():
+    global _capturing
+    _capturing -= 1
+    if _capturing == 0:
+        if _gc_was_enabled:
+            gc.enable()
+        while _deferred:
+            _deferred.pop().close()
+
+
 class StepGraph:
     """A captured hipGraph of a store's work (ttp_capture_begin .. ttp_capture_end)."""
 
@@ -114,6 +142,9 @@ class StepGraph:
 
     def close(self):
         if getattr(self, "_g", None):
+            if _capturing:
+                _deferred.append(self)
+                return
             L.lib.ttp_graph_destroy(self._g)
             self._g = None
 
@@ -191,12 +222,15 @@ class ParamStore:
         tot = C.c_uint64()
         L.check(L.lib.ttp_flat_numel(self._h, C.byref(tot)))
         self.total = tot.value
-        self._scaler_enabled = False
         self._graphs = weakref.WeakSet()
+        self._in_capture = False
 
     # ---- lifetime --------------------------------------------------------------------------
     def close(self):
         if getattr(self, "_h", None):
+            if _capturing and not getattr(self, "_in_capture", False):
+                _deferred.append(self)  # destroyed when the capture ends
+                return
             for g in list(getattr(self, "_graphs", ())):
                 g.close()  # a context's graphs go before the context
             L.lib.ttp_destroy(self._h)
@@ -399,7 +433,6 @@ class ParamStore:
                              init_scale=init_scale, growth_factor=growth_factor,
                              backoff_factor=backoff_factor)
         L.check(L.lib.ttp_scaler_configure(self._h, C.byref(cfg)))
-        self._scaler_enabled = bool(enabled)
 
     def scaler_state(self):
         s, t = C.c_float(), C.c_int32()
@@ -409,18 +442,34 @@ class ParamStore:
     def set_scaler_state(self, scale, growth_tracker):
         L.check(L.lib.ttp_scaler_set(self._h, scale, growth_tracker))
 
+    # ---- optimizer-state checkpoint ---------------------------------------------------------
+    def save_state(self, path):
+        """Write master weights, moments, momentum, step count and scaler state to `path`."""
+        L.check(L.lib.ttp_save_state(self._h, str(path).encode()))
+
+    def load_state(self, path):
+        """Restore a save_state() file written for the same tensor table and mode."""
+        L.check(L.lib.ttp_load_state(self._h, str(path).encode()))
+
     # ---- graph capture ------------------------------------------------------------------------
     def begin_capture(self):
         """Capture the store's work until end_capture() (the store must use its own stream
         or a created stream, not the legacy default stream)."""
         L.check(L.lib.ttp_capture_begin(self._h))
+        self._in_capture = True
+        _capture_started()
 
     def end_capture(self, discard=False):
-        if discard:
-            L.check(L.lib.ttp_capture_end(self._h, None))
-            return None
         g = C.c_void_p()
-        L.check(L.lib.ttp_capture_end(self._h, C.byref(g)))
+        try:
+            rc = L.lib.ttp_capture_end(self._h, None if discard else C.byref(g))
+        finally:
+            if self._in_capture:
+                self._in_capture = False
+                _capture_ended()
+        L.check(rc)
+        if discard:
+            return None
         graph = StepGraph(self, g)
         self._graphs.add(graph)
         return graph
