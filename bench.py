@@ -27,6 +27,26 @@ UPDATE_BYTES = {("adamw", "mixed"): 28, ("adamw", "fp32"): 28, ("sgdm", "fp32"):
                 ("sgdm", "mixed"): 20}
 NORM_BYTES = {"mixed": 2, "fp32": 4}
 
+# The step of each BASELINE.json configuration: optimizer hyperparameters, loss scaling, and
+# the synthetic gradient distribution (N(0, std), a fraction `heavy` drawn from N(0, 1)).
+BENCH = {
+    "mlp": dict(hp=dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0,
+                        max_grad_norm=None), decoupled=False, scaler=None, std=1e-2, heavy=0.0),
+    "nanogpt_char": dict(hp=dict(lr=6e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1,
+                                 max_grad_norm=1.0), decoupled=True, scaler=None, std=1e-3,
+                         heavy=0.0),
+    "gpt2_124m": dict(hp=dict(lr=6e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1,
+                              max_grad_norm=1.0), decoupled=True, scaler=65536.0, std=1e-3,
+                      heavy=0.0),
+    "gpt2_774m": dict(hp=dict(lr=6e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1,
+                              max_grad_norm=1.0), decoupled=True, scaler=65536.0, std=1e-3,
+                      heavy=0.0),
+    "gpt2_1558m": dict(hp=dict(lr=1.5e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1,
+                               max_grad_norm=1.0), decoupled=True, scaler=None, std=1e-3,
+                       heavy=0.01),
+}
+HEADLINE = "fused AdamW step Gparams/s + % of HBM peak, GPT-2 124M mixed precision"
+
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
@@ -53,22 +73,28 @@ def traffic_from_profiles(config):
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(numels, flags, mode_mixed, grads_host, hp, seconds):
-    """The CPU oracle (C restatement of the reference's optimizer) on this host's cores."""
+def cpu_baseline(numels, flags, mode_mixed, grads_host, hp, seconds, scaler):
+    """The CPU oracle (C restatement of the reference's optimizer) on this host's cores:
+    the fused step on all threads (the reported value), the same on 1 thread, and the
+    op-by-op restatement of py/optim.py (one full pass per ttnn op) on all threads.  Each leg
+    runs for about `seconds`."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import numpy as np
     import oracle as O
     nthreads = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
     st = O.OracleStore(numels, flags=flags, mode=O.MODE_MIXED if mode_mixed else O.MODE_FP32,
                        nthreads=nthreads)
-    st.configure_scaler(True, 65536.0)
+    if scaler:
+        st.configure_scaler(True, scaler)
+    hp = dict(hp, max_grad_norm=hp["max_grad_norm"] or 0.0)
     rng = np.random.default_rng(0)
     st.master[:] = rng.normal(0, 0.02, st.total).astype(np.float32)
     st.grad[:] = grads_host
     for i in range(st.n):
         st.set_has_grad(i, True)
     res = {}
-    for label, kw, nt in (("fused", {}, nthreads), ("opbyop", {"opbyop": True}, nthreads)):
+    for label, kw, nt in (("fused", {}, nthreads), ("fused_1", {}, 1),
+                          ("opbyop", {"opbyop": True}, nthreads)):
         st.s.nthreads = nt
         st.adam_step(**hp, **kw)  # warm
         t0 = time.perf_counter()
@@ -80,13 +106,17 @@ def cpu_baseline(numels, flags, mode_mixed, grads_host, hp, seconds):
             if el >= seconds or n >= 200:
                 break
         res[label] = (n, el)
-    n, el = res["fused"]
+        log(f"bench: cpu {label} on {nt} thread(s): {el / n * 1e3:.1f} ms/step")
     total = sum(numels)
+    n, el = res["fused"]
     out = {"value": round(total * n / el / 1e9, 4), "unit": "Gparams/s", "cores": nthreads,
            "kind": "port",
            "sample": f"full {len(numels)}-tensor table ({total} params), {n} fused steps "
-                     f"(scaler + clip + AdamW) in {el:.1f} s on {nthreads} threads",
+                     f"(the same step as the GPU's) in {el:.1f} s on {nthreads} threads",
            "ms_per_step": round(el / n * 1e3, 3)}
+    n1, el1 = res["fused_1"]
+    out["single_core_value"] = round(total * n1 / el1 / 1e9, 4)
+    out["single_core_sample"] = f"{n1} fused steps in {el1:.1f} s on 1 thread"
     n2, el2 = res["opbyop"]
     out["opbyop_value"] = round(total * n2 / el2 / 1e9, 4)
     out["opbyop_sample"] = (f"{n2} steps executing py/optim.py's ops as separate full passes, "
@@ -116,26 +146,35 @@ def main():
     stream = torch.cuda.current_stream()
     store.set_stream(stream)
 
+    cfg = BENCH[args.config]
+    hp = dict(cfg["hp"], decoupled=cfg["decoupled"])
+    scale = cfg["scaler"] or 1.0
     gen = torch.Generator(device=dev).manual_seed(1234)
     w = torch.randn(store.total, generator=gen, device=dev) * 0.02
     store.upload(L.BUF_MASTER, L.ALL_TENSORS, w)
     del w
-    scale = 65536.0
-    store.configure_scaler(True, init_scale=scale)
-    g = torch.randn(store.total, generator=gen, device=dev) * 1e-3 * scale
+    if cfg["scaler"]:
+        store.configure_scaler(True, init_scale=scale)
+    g = torch.randn(store.total, generator=gen, device=dev) * cfg["std"]
+    if cfg["heavy"]:
+        pick = torch.rand(store.total, generator=gen, device=dev) < cfg["heavy"]
+        g = torch.where(pick, torch.randn(store.total, generator=gen, device=dev), g)
+        del pick
+    g = g * scale
     g = g.to(torch.bfloat16) if mode == "mixed" else g
     store.upload(L.BUF_GRAD, L.ALL_TENSORS, g)
-    grads_host = (g.cpu().view(torch.int16).numpy().view(np.uint16) if mode == "mixed"
-                  else g.cpu().numpy())
+    grads_host = None
+    if not args.no_cpu_baseline and args.optimizer == "adamw":
+        grads_host = (g.cpu().view(torch.int16).numpy().view(np.uint16) if mode == "mixed"
+                      else g.cpu().numpy())
     del g
-
-    hp = dict(lr=6e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
+    torch.cuda.empty_cache()
 
     def step():
         if args.optimizer == "adamw":
             store.adam_step(**hp)
         else:
-            store.sgd_step(lr=1e-3, momentum=0.9, weight_decay=0.1, max_grad_norm=1.0)
+            store.sgd_step(lr=hp["lr"], momentum=0.9, max_grad_norm=hp["max_grad_norm"])
 
     for _ in range(args.warmup):
         step()
@@ -172,7 +211,7 @@ def main():
 
     # a skipped (overflow) step: only the norm pass does work
     skip_ms = None
-    if args.optimizer == "adamw":
+    if args.optimizer == "adamw" and cfg["scaler"]:
         store.upload(L.BUF_GRAD, 0, torch.full((store.tensors[0].numel,), float("inf"),
                                                device=dev, dtype=torch.bfloat16 if mode == "mixed"
                                                else torch.float32))
@@ -204,7 +243,8 @@ def main():
     achieved = n_params * ub / (upd_avg / 1e3) / 1e9
     step_gbps = n_params * (ub + nb) / (ms_step / 1e3) / 1e9
     out = {
-        "metric": "fused AdamW step Gparams/s + % of HBM peak, GPT-2 124M mixed precision",
+        "metric": HEADLINE if args.config == "gpt2_124m" and args.optimizer == "adamw" else
+                  f"fused {args.optimizer} step Gparams/s + % of HBM peak, {args.config} {mode}",
         "value": round(n_params / (ms_step / 1e3) / 1e9, 3),
         "unit": "Gparams/s",
         "n_gpus": 1,
@@ -215,10 +255,18 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
-        "data": "synthetic (seeded N(0,1e-3) x loss-scale bf16 grads, N(0,0.02) fp32 master)",
+        "data": f"synthetic (seeded N(0,{cfg['std']:g})"
+                + (f", {cfg['heavy']:g} of them N(0,1)" if cfg["heavy"] else "")
+                + (f" x loss scale {scale:g}" if cfg["scaler"] else "")
+                + (" bf16" if mode == "mixed" else " fp32") + " grads, N(0,0.02) fp32 master)",
         "config": {"workload": f"{args.config} {args.optimizer} step: {len(numels)} tensors, "
-                               f"{n_params} params, {mode} precision, loss scaling 2^16, "
-                               f"clip 1.0, lr 6e-4, betas (0.9,0.95), wd 0.1 on 2-D tensors",
+                               f"{n_params} params, {mode} precision, "
+                               + (f"loss scaling {scale:g}, " if cfg["scaler"] else "")
+                               + (f"clip {hp['max_grad_norm']}, " if hp["max_grad_norm"] else "")
+                               + (f"lr {hp['lr']:g}, betas {hp['betas']}, "
+                                  f"wd {hp['weight_decay']:g} on 2-D tensors"
+                                  if args.optimizer == "adamw" else
+                                  f"lr {hp['lr']:g}, momentum 0.9"),
                    "params": n_params, "tensors": len(numels), "mode": mode,
                    "bytes_per_param": ub + nb},
         "step_hbm_GBps": round(step_gbps, 1),
@@ -235,10 +283,11 @@ def main():
         "cpu_baseline": None,
     }
     store.close()
-    if not args.no_cpu_baseline and args.optimizer == "adamw":
+    if grads_host is not None:
         log("bench: timing the CPU oracle baseline ...")
         out["cpu_baseline"] = cpu_baseline(numels, [1 if d else 0 for d in decay],
-                                           mode == "mixed", grads_host, hp, args.cpu_seconds)
+                                           mode == "mixed", grads_host, hp, args.cpu_seconds,
+                                           cfg["scaler"])
     print(json.dumps(out), flush=True)
 
 

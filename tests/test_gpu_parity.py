@@ -73,6 +73,7 @@ def test_cfg2_nanogpt_mixed_adamw_clip():
         e = ref.adam_step(**hp)
         _check_report(r, e)
         assert r["clip_coef"] < 1.0  # the clip path is exercised
+        print(f"cfg2 step {step}: norm {r['grad_norm']:.6f}", flush=True)
         if step in (0, steps - 1):
             compare_state(store, ref, max_ulp=2)
 
@@ -126,6 +127,7 @@ def test_cfg4_gpt2_large_ragged():
         r = store.adam_step(report=True, **hp)
         e = ref.adam_step(**hp)
         _check_report(r, e)
+        print(f"cfg4 step {step}: norm {r['grad_norm']:.6f} scale {r['scale']}", flush=True)
     compare_state(store, ref, max_ulp=2)
 
 
