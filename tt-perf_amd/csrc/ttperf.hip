@@ -591,12 +591,14 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
     c->n_nonempty = (uint32_t)every.size();
     if ((rc = build_tables(c, every, &c->all))) return bail(rc);
 
+    // the zero fills above run on the context's non-blocking stream, which the legacy-stream
+    // hipMemcpy below does not wait for: finish them first
+    if (hipStreamSynchronize(c->stream) != hipSuccess)
+        return bail(fail(TTP_ERR_HIP, "stream synchronize failed"));
     DevState s{};
     s.scale = (float)c->scaler.init_scale;
     if (hipMemcpy(c->st, &s, sizeof(s), hipMemcpyHostToDevice) != hipSuccess)
         return bail(fail(TTP_ERR_HIP, "state upload failed"));
-    if (hipStreamSynchronize(c->stream) != hipSuccess)
-        return bail(fail(TTP_ERR_HIP, "stream synchronize failed"));
     *out = c;
     return TTP_OK;
 }
