@@ -61,6 +61,9 @@ def parse():
     ap.add_argument("--optimizer", default="adamw", choices=["adamw", "sgdm"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--graph", action="store_true",
+                    help="time replays of the step captured as a hipGraph (measured equal to "
+                         "eager launches on MI355X, so eager is the default)")
     return ap.parse_args()
 
 
@@ -143,7 +146,9 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     store = ttperf.ParamStore(shapes, mode=mode, decay=decay, names=names)
-    stream = torch.cuda.current_stream()
+    # a created stream (the legacy default stream cannot be captured); torch's events and
+    # synchronisation see it
+    stream = torch.cuda.Stream()
     store.set_stream(stream)
 
     cfg = BENCH[args.config]
@@ -183,13 +188,24 @@ def main():
     if r is not None:
         assert not r["skipped"], r
 
+    # the step as a hipGraph (the reference's trace capture/replay): one capture, K replays
+    run = step
+    if args.graph:
+        store.begin_capture()
+        step()
+        graph = store.end_capture()
+        run = graph.replay
+        for _ in range(2):
+            run()
+        torch.cuda.synchronize()
+
     # timed region: exactly K steps between one event pair (an event per launch would put
     # a marker packet between the kernels and lengthen the step)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record(stream)
     for _ in range(args.steps):
-        step()
+        run()
     e1.record(stream)
     torch.cuda.synchronize()
     total_ms = e0.elapsed_time(e1)
@@ -208,6 +224,9 @@ def main():
     store.timing(False)
     upd_avg = upd_ms / max(upd_n, 1)
     nrm_avg = nrm_ms / max(nrm_n, 1)
+
+    if args.graph:
+        graph.close()
 
     # a skipped (overflow) step: only the norm pass does work
     skip_ms = None
@@ -229,13 +248,14 @@ def main():
     copy_bytes = n_params * ub // 2
     src = torch.empty(copy_bytes // 4, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
-    for _ in range(3):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(10):
-        dst.copy_(src)
-    e1.record(stream)
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(10):
+            dst.copy_(src)
+        e1.record(stream)
     torch.cuda.synchronize()
     copy_gbps = 2 * copy_bytes * 10 / (e0.elapsed_time(e1) / 1e3) / 1e9
     del src, dst
@@ -255,6 +275,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
+        "launch": "hipGraph replay of the captured step" if args.graph else "eager launches",
         "data": f"synthetic (seeded N(0,{cfg['std']:g})"
                 + (f", {cfg['heavy']:g} of them N(0,1)" if cfg["heavy"] else "")
                 + (f" x loss scale {scale:g}" if cfg["scaler"] else "")

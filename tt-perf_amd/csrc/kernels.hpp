@@ -194,7 +194,9 @@ __global__ __launch_bounds__(kBlock) void norm_partials_kernel(const GradT* __re
     constexpr int E = GV::kElems;
     __shared__ double lds[kBlock / 64];
     const float inv = scaler_on ? (float)(1.0 / (double)st->scale) : 1.0f;
-    double acc = 0.0;
+    // two accumulators (element j of a vector goes to acc[j & 1]): a fixed order, so the
+    // sum stays deterministic, with half the dependent-add chain
+    double acc[2] = {0.0, 0.0};
     Chunk next{0, 0, 0};
     if (blockIdx.x < ntiles) next = tiles[blockIdx.x];
     for (uint32_t c = blockIdx.x; c < ntiles; c += gridDim.x) {
@@ -209,17 +211,26 @@ __global__ __launch_bounds__(kBlock) void norm_partials_kernel(const GradT* __re
             // temporal loads: the gradients stay in the Infinity Cache for the update pass
             if (nv[l]) w[l] = *reinterpret_cast<const typename GV::raw*>(g + ch.begin + off);
         }
+        // The square of an fp32 value is exact in fp64, so fma(x, x, acc) rounds exactly as
+        // acc + x*x does (one rounding, of the add) with one instruction instead of two.
 #pragma unroll
         for (int l = 0; l < kNormLoads; ++l) {
-            if (!nv[l]) continue;
+            if (nv[l] == (uint32_t)E) {  // whole vector: no per-element masks
 #pragma unroll
-            for (int j = 0; j < E; ++j) {
-                const float x = (uint32_t)j < nv[l] ? GV::at(w[l], j) * inv : 0.0f;
-                acc += (double)x * (double)x;
+                for (int j = 0; j < E; ++j) {
+                    const double x = (double)(GV::at(w[l], j) * inv);
+                    acc[j & 1] = __builtin_fma(x, x, acc[j & 1]);
+                }
+            } else if (nv[l]) {
+#pragma unroll
+                for (int j = 0; j < E; ++j) {
+                    const double x = (uint32_t)j < nv[l] ? (double)(GV::at(w[l], j) * inv) : 0.0;
+                    acc[j & 1] = __builtin_fma(x, x, acc[j & 1]);
+                }
             }
         }
     }
-    const double b = block_sum(acc, lds);
+    const double b = block_sum(acc[0] + acc[1], lds);
     if (threadIdx.x == 0) partials[blockIdx.x] = b;
 }
 
