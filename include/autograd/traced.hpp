@@ -53,6 +53,8 @@ struct TracedLayerNorm {
     TracedLayerNorm(uint32_t dim, ParamArena& arena)
         : gamma(arena.parameter({1, dim}, autograd::filled(dim, 1.0f), "gamma", false, true)),
           beta(arena.parameter({1, dim}, autograd::filled(dim, 0.0f), "beta", false, true)) {}
+    // the reference's (dim, eps, device) constructor; eps belongs to the forward pass
+    TracedLayerNorm(uint32_t dim, float /*eps*/, ParamArena& arena) : TracedLayerNorm(dim, arena) {}
 
     std::vector<ValuePtr> parameters() const { return {gamma, beta}; }
     void sgd_step(float lr) { detail::sgd_on(parameters(), lr); }
@@ -67,6 +69,11 @@ struct TracedEmbedding {
     TracedEmbedding(uint32_t vocab, uint32_t dim, float init, ParamArena& arena)
         : weight(arena.parameter({vocab, dim}, autograd::filled((uint64_t)vocab * dim, init),
                                  "embedding", true, true)) {}
+    // the reference's (vocab, dim, batch, seq, init, device) constructor; batch and seq size
+    // its forward buffers, which are not part of this engine
+    TracedEmbedding(uint32_t vocab, uint32_t dim, uint32_t /*batch*/, uint32_t /*seq*/, float init,
+                    ParamArena& arena)
+        : TracedEmbedding(vocab, dim, init, arena) {}
 
     std::vector<ValuePtr> parameters() const { return {weight}; }
     void sgd_step(float lr) { detail::sgd_on(parameters(), lr); }
@@ -74,6 +81,117 @@ struct TracedEmbedding {
 
 // autograd/traced/ops.hpp:132-134: param = param - lr * grad (one tensor)
 inline void sgd_update(const ValuePtr& param, float lr) { detail::sgd_on({param}, lr); }
+
+// One transformer block's parameters (autograd/traced/transformer_train.hpp:76-135): ln1,
+// ln2 (gamma, beta), wq, wk, wv, wo [d, d], w1 [d, ffn], w2 [ffn, d] (weight, bias) = 16
+// tensors, linears filled with 0.01.  sgd_step() (:259-268) is one launch over all 16.
+struct TracedTransformerLayerTrainable {
+    TracedLayerNorm ln1, ln2;
+    TracedLinear wq, wk, wv, wo;
+    TracedLinear w1, w2;
+    uint32_t batch, seq, dim, heads, head_dim, ffn_dim;
+    float lr;
+
+    TracedTransformerLayerTrainable(uint32_t b, uint32_t s, uint32_t d, uint32_t h,
+                                    uint32_t ffn_mult, float learning_rate, ParamArena& arena)
+        : ln1(d, 1e-5f, arena),
+          ln2(d, 1e-5f, arena),
+          wq(d, d, 0.01f, arena),
+          wk(d, d, 0.01f, arena),
+          wv(d, d, 0.01f, arena),
+          wo(d, d, 0.01f, arena),
+          w1(d, d * ffn_mult, 0.01f, arena),
+          w2(d * ffn_mult, d, 0.01f, arena),
+          batch(b),
+          seq(s),
+          dim(d),
+          heads(h),
+          head_dim(d / h),
+          ffn_dim(d * ffn_mult),
+          lr(learning_rate) {}
+
+    std::vector<ValuePtr> parameters() const {
+        std::vector<ValuePtr> ps;
+        for (auto* m : {&ln1, &ln2})
+            for (auto& p : m->parameters()) ps.push_back(p);
+        for (auto* m : {&wq, &wk, &wv, &wo, &w1, &w2})
+            for (auto& p : m->parameters()) ps.push_back(p);
+        return ps;
+    }
+    void sgd_step() { detail::sgd_on(parameters(), lr); }
+};
+
+// N blocks (transformer_train.hpp:275-345); sgd_step() (:335-339) is one launch over all.
+template <size_t N>
+struct TracedTransformerStack {
+    static_assert(N >= 1, "Must have at least 1 layer");
+    std::vector<TracedTransformerLayerTrainable> layers;
+    float lr;
+
+    TracedTransformerStack(uint32_t b, uint32_t s, uint32_t d, uint32_t h, uint32_t ffn_mult,
+                           float learning_rate, ParamArena& arena)
+        : lr(learning_rate) {
+        layers.reserve(N);
+        for (size_t i = 0; i < N; ++i) layers.emplace_back(b, s, d, h, ffn_mult, learning_rate, arena);
+    }
+
+    std::vector<ValuePtr> parameters() const {
+        std::vector<ValuePtr> ps;
+        for (auto& l : layers)
+            for (auto& p : l.parameters()) ps.push_back(p);
+        return ps;
+    }
+    void sgd_step() { detail::sgd_on(parameters(), lr); }
+};
+
+// The GPT model (transformer_train.hpp:363-501): token and position embeddings (0.02),
+// N blocks, output projection [d, vocab] (0.02).  sgd_step() (:487-494) is one launch over
+// every tensor of the model (the reference issues two programs per tensor plus an untilize
+// per embedding).
+template <size_t N>
+struct TracedTransformerWithEmbedding {
+    static_assert(N >= 1, "Must have at least 1 layer");
+    TracedEmbedding tok_emb;
+    TracedEmbedding pos_emb;
+    std::vector<TracedTransformerLayerTrainable> layers;
+    TracedLinear output_proj;
+    uint32_t batch, seq, dim, vocab_size;
+    float lr;
+
+    TracedTransformerWithEmbedding(uint32_t b, uint32_t s, uint32_t d, uint32_t h,
+                                   uint32_t ffn_mult, uint32_t vocab, float learning_rate,
+                                   ParamArena& arena)
+        : tok_emb(vocab, d, b, s, 0.02f, arena),
+          pos_emb(s, d, b, s, 0.02f, arena),
+          layers(make_layers(b, s, d, h, ffn_mult, learning_rate, arena)),
+          output_proj(d, vocab, 0.02f, arena),
+          batch(b),
+          seq(s),
+          dim(d),
+          vocab_size(vocab),
+          lr(learning_rate) {}
+
+    std::vector<ValuePtr> parameters() const {
+        std::vector<ValuePtr> ps = {tok_emb.weight, pos_emb.weight};
+        for (auto& l : layers)
+            for (auto& p : l.parameters()) ps.push_back(p);
+        for (auto& p : output_proj.parameters()) ps.push_back(p);
+        return ps;
+    }
+    void sgd_step() { detail::sgd_on(parameters(), lr); }
+
+private:
+    // declared in member order: embeddings, blocks, output projection (the flat layout)
+    static std::vector<TracedTransformerLayerTrainable> make_layers(uint32_t b, uint32_t s,
+                                                                    uint32_t d, uint32_t h,
+                                                                    uint32_t ffn_mult, float lr,
+                                                                    ParamArena& arena) {
+        std::vector<TracedTransformerLayerTrainable> v;
+        v.reserve(N);
+        for (size_t i = 0; i < N; ++i) v.emplace_back(b, s, d, h, ffn_mult, lr, arena);
+        return v;
+    }
+};
 
 // traced::TraceContext (autograd/traced/trace.hpp:21-88) over a ttp::Store: the first
 // run(fn) captures the work fn queues on the store's stream into a hipGraph and executes it;

@@ -178,6 +178,11 @@ int ttp_get_has_grad(const ttp_ctx* ctx, uint32_t index, int* has_grad);
  * One fill over the flat buffer replaces the per-tensor zeros_like allocations of
  * autograd/static/nn.hpp:98-101 and the nullopt loop of autograd/dynamic/optim.hpp:30-34. */
 int ttp_zero_grad(ttp_ctx* ctx, int set_to_none);
+/* A module's zero_grad: the listed tensors' grads (each index at most once) become zeros and
+ * stay present (set_to_none = 0: the static layers' zeros_like, autograd/static/nn.hpp:98-101,
+ * 183-186) or become None (set_to_none = 1).  One launch over the listed tensors. */
+int ttp_zero_grad_subset(ttp_ctx* ctx, const uint32_t* indices, uint32_t n_indices,
+                         int set_to_none);
 /* Value::accumulate_grad (autograd/dynamic/autograd.hpp:78-83; static_autograd::Value,
  * autograd/static/value.hpp:39-47) on the flat grad buffer: when tensor `index` has no grad,
  * its grad becomes the incoming gradient; otherwise grad = grad + incoming, added in fp32 and

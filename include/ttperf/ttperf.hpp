@@ -161,6 +161,10 @@ public:
     }
     void set_has_grad(uint32_t i, bool h) { check(ttp_set_has_grad(ctx_, i, h ? 1 : 0)); }
     void zero_grad(bool set_to_none = true) { check(ttp_zero_grad(ctx_, set_to_none ? 1 : 0)); }
+    void zero_grad(const std::vector<uint32_t>& indices, bool set_to_none) {
+        check(ttp_zero_grad_subset(ctx_, indices.data(), (uint32_t)indices.size(),
+                                   set_to_none ? 1 : 0));
+    }
     // grad = g if tensor i has none, else grad + g (fp32 add, one rounding to the grad type)
     void accumulate_grad(uint32_t i, const std::vector<float>& g) {
         check(ttp_accumulate_grad(ctx_, i, g.data(), g.size(), TTP_DTYPE_F32, TTP_HOST));

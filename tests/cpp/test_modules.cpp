@@ -1,0 +1,118 @@
+// test_modules.cpp — module-level optimizer surfaces: the static layers' sgd_step / zero_grad
+// (autograd/static/nn.hpp:92-101,178-186,213-221,242-250) and the traced transformer's
+// layer / stack / GPT sgd_step (autograd/traced/transformer_train.hpp:259-268,335-339,487-494).
+// Each sgd_step must update exactly its module's tensors, bit-exact against `w - lr*dw`
+// (one rounding per op, bf16 weights = RNE of the fp32 master), in ONE update launch.
+#include "autograd/static.hpp"
+#include "autograd/traced.hpp"
+#include "common.hpp"
+
+using autograd::ParamArena;
+using autograd::ValuePtr;
+
+static std::vector<float> ramp(size_t n, float a, float b) {
+    std::vector<float> v(n);
+    for (size_t i = 0; i < n; ++i) v[i] = a + b * (float)((i * 7) % 113) - 0.4f * b * 113.0f;
+    return v;
+}
+
+struct Ref {
+    std::vector<std::vector<float>> w, g;
+};
+
+static Ref snapshot(const std::vector<ValuePtr>& ps, bool mixed, float seed) {
+    Ref r;
+    for (size_t k = 0; k < ps.size(); ++k) {
+        r.w.push_back(ps[k]->master());
+        auto g = ramp(ps[k]->numel(), 0.01f * seed, 0.003f * (float)(k + 1));
+        ps[k]->grad = g;  // rounded to bf16 by the store in Mixed mode
+        if (mixed)
+            for (auto& x : g) x = test::bf16_round(x);
+        r.g.push_back(g);
+    }
+    return r;
+}
+
+static void apply(Ref& r, size_t k, float lr) {
+    for (size_t i = 0; i < r.w[k].size(); ++i) {
+        const float update = r.g[k][i] * lr;
+        r.w[k][i] = r.w[k][i] - update;
+    }
+}
+
+static void check_all(const std::vector<ValuePtr>& ps, const Ref& r, bool mixed,
+                      const std::string& what) {
+    for (size_t k = 0; k < ps.size(); ++k) {
+        test::assert_bits(ps[k]->master(), r.w[k], what + " master " + std::to_string(k));
+        if (mixed) {
+            std::vector<float> want(r.w[k].size());
+            for (size_t i = 0; i < want.size(); ++i) want[i] = test::bf16_round(r.w[k][i]);
+            test::assert_bits(ps[k]->data(), want, what + " bf16 " + std::to_string(k));
+        }
+    }
+}
+
+static uint64_t update_launches(ttp::Store& s) {
+    double ms = 0;
+    uint64_t n = 0;
+    ttp::check(ttp_timing_collect(s.get(), TTP_KERNEL_UPDATE, &ms, &n));
+    return n;
+}
+
+int main() {
+    test::DeviceGuard dg;
+    // ---- static layers ----------------------------------------------------------------
+    {
+        ParamArena arena(ttp::Mode::FP32);
+        static_autograd::MLP mlp(32, 64, 128, 10, 0.01f, arena);
+        auto ps = mlp.parameters();
+        Ref r = snapshot(ps, false, 1.0f);
+        mlp.sgd_step(0.1f);
+        for (size_t k = 0; k < 4; ++k) apply(r, k, 0.1f);
+        check_all(ps, r, false, "static MLP sgd_step");
+        mlp.layer2.sgd_step(0.2f);  // only layer 2
+        apply(r, 2, 0.2f);
+        apply(r, 3, 0.2f);
+        check_all(ps, r, false, "static Linear sgd_step");
+        mlp.zero_grad();  // zeros_like: grads present and zero
+        for (auto& p : ps) {
+            test::check(p->grad.has_value(), "static zero_grad keeps the grad");
+            test::assert_all_close(p->grad.value(), 0.0f, 0.0f, "static zero_grad zeros");
+        }
+        mlp.sgd_step(0.1f);  // w - 0.1*0 = w
+        check_all(ps, r, false, "static sgd_step after zero_grad");
+    }
+    // ---- traced transformer: GPT with 2 blocks ----------------------------------------
+    {
+        ParamArena arena(ttp::Mode::Mixed);
+        traced::TracedTransformerWithEmbedding<2> gpt(4, 32, 64, 4, 4, 65, 0.05f, arena);
+        auto ps = gpt.parameters();
+        test::check(ps.size() == 2 + 2 * 16 + 2, "GPT parameter count 36");
+        Ref r = snapshot(ps, true, 2.0f);
+        ttp::Store& store = arena.store();
+        ttp::check(ttp_timing_enable(store.get(), 1));
+        update_launches(store);
+        gpt.sgd_step();
+        test::check(update_launches(store) == 1, "GPT sgd_step is one update launch");
+        for (size_t k = 0; k < ps.size(); ++k) apply(r, k, 0.05f);
+        check_all(ps, r, true, "GPT sgd_step");
+        // one block's sgd_step touches its 16 tensors only (offset 2: after the embeddings)
+        gpt.layers[1].sgd_step();
+        test::check(update_launches(store) == 1, "block sgd_step is one update launch");
+        for (size_t k = 2 + 16; k < 2 + 32; ++k) apply(r, k, 0.05f);
+        check_all(ps, r, true, "block sgd_step");
+        ttp::check(ttp_timing_enable(store.get(), 0));
+    }
+    // ---- traced stack -----------------------------------------------------------------
+    {
+        ParamArena arena(ttp::Mode::FP32);
+        traced::TracedTransformerStack<3> stack(2, 16, 32, 2, 4, 0.2f, arena);
+        auto ps = stack.parameters();
+        test::check(ps.size() == 3 * 16, "stack parameter count 48");
+        Ref r = snapshot(ps, false, 3.0f);
+        stack.sgd_step();
+        for (size_t k = 0; k < ps.size(); ++k) apply(r, k, 0.2f);
+        check_all(ps, r, false, "stack sgd_step");
+    }
+    return test::finish("test_modules");
+}

@@ -142,7 +142,7 @@ def test_non_tensor_params_raise_at_step_and_are_skipped_by_zero_grad():
 def test_cpp_dropin_headers_compile():
     """The C++ drop-in tests (tests/cpp) build against include/ and the library."""
     subprocess.run(["make", "-s", "-C", os.path.join(REPO, "tests", "cpp")], check=True)
-    for t in ("test_sgd", "test_traced", "test_adam", "train_mlp"):
+    for t in ("test_sgd", "test_traced", "test_adam", "test_modules", "train_mlp"):
         assert os.access(os.path.join(REPO, "tests", "cpp", "build", t), os.X_OK)
 
 

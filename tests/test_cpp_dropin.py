@@ -1,6 +1,7 @@
 """Runs the C++ drop-in tests (tests/cpp, built by __graft_entry__.build()) on the GPU: the
 reference's autograd/tests/test_sgd.cpp known answers, the traced layers' sgd_step surface,
-Adam/AdamW against a host restatement, and a train_mlp-style loop whose loss must fall."""
+Adam/AdamW against a host restatement, the static layers' and transformer modules'
+sgd_step / zero_grad, and a train_mlp-style loop whose loss must fall."""
 import os
 import subprocess
 
@@ -13,7 +14,8 @@ pytestmark = pytest.mark.gpu
 BUILD = os.path.join(REPO, "tests", "cpp", "build")
 
 
-@pytest.mark.parametrize("name", ["test_sgd", "test_traced", "test_adam", "train_mlp"])
+@pytest.mark.parametrize("name", ["test_sgd", "test_traced", "test_adam", "test_modules",
+                                  "train_mlp"])
 def test_cpp_dropin(name):
     exe = os.path.join(BUILD, name)
     if not os.access(exe, os.X_OK):

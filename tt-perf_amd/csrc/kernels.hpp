@@ -506,6 +506,34 @@ __global__ __launch_bounds__(kBlock) void accumulate_grad_kernel(GradT* __restri
     }
 }
 
+// zero the grads of the chunks' tensors (a module's zero_grad): one vector per lane
+__device__ __forceinline__ void zero_vec(float* g, uint64_t i, int n) {
+    if (n >= kVec) {
+        st4(g + i, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+    } else {
+        for (int j = 0; j < n; ++j) g[i + j] = 0.0f;
+    }
+}
+__device__ __forceinline__ void zero_vec(uint16_t* g, uint64_t i, int n) {
+    if (n >= kVec) {
+        __builtin_nontemporal_store(u32x2{0u, 0u}, reinterpret_cast<u32x2*>(g + i));
+    } else {
+        for (int j = 0; j < n; ++j) g[i + j] = 0;
+    }
+}
+
+template <typename GradT>
+__global__ __launch_bounds__(kUpdBlock) void zero_chunks_kernel(GradT* __restrict__ grad,
+                                                                const Chunk* __restrict__ chunks,
+                                                                uint32_t nchunks) {
+    for (uint32_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
+        const Chunk ch = chunks[c];
+        const uint32_t off = threadIdx.x * kVec;
+        if (off >= ch.count) continue;
+        zero_vec(grad, ch.begin + off, (int)min(ch.count - off, (uint32_t)kVec));
+    }
+}
+
 // ------------------------------------------------------------------------------------
 // small elementwise helpers
 // ------------------------------------------------------------------------------------

@@ -230,7 +230,7 @@ int ensure_momentum(ttp_ctx* c) {
 // Active set of a step: the listed tensors (all when `subset` is NULL) that have a grad
 // and at least one element; returns its device work tables (built once per distinct set).
 int select_tables(ttp_ctx* c, const uint32_t* subset, uint32_t nsub, const WorkTables** out,
-                  std::vector<uint32_t>* active_out) {
+                  std::vector<uint32_t>* active_out, bool require_grad = true) {
     const uint32_t nt = (uint32_t)c->tensors.size();
     std::vector<uint32_t> active;
     if (subset) {
@@ -242,10 +242,12 @@ int select_tables(ttp_ctx* c, const uint32_t* subset, uint32_t nsub, const WorkT
             seen[i] = 1;
         }
         for (uint32_t i = 0; i < nt; ++i)
-            if (seen[i] && c->tensors[i].has_grad && c->tensors[i].numel) active.push_back(i);
+            if (seen[i] && (c->tensors[i].has_grad || !require_grad) && c->tensors[i].numel)
+                active.push_back(i);
     } else {
         for (uint32_t i = 0; i < nt; ++i)
-            if (c->tensors[i].has_grad && c->tensors[i].numel) active.push_back(i);
+            if ((c->tensors[i].has_grad || !require_grad) && c->tensors[i].numel)
+                active.push_back(i);
     }
     if (active.size() == c->n_nonempty) {
         *out = &c->all;
@@ -782,6 +784,29 @@ int ttp_zero_grad(ttp_ctx* c, int set_to_none) {
     if (set_to_none) {
         for (auto& t : c->tensors) t.has_grad = 0;
     }
+    return TTP_OK;
+}
+
+int ttp_zero_grad_subset(ttp_ctx* c, const uint32_t* indices, uint32_t n, int set_to_none) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (n && !indices) return fail(TTP_ERR_INVALID, "null index list");
+    if ((rc = set_dev(c))) return rc;
+    static const uint32_t none = 0;
+    const WorkTables* w;
+    std::vector<uint32_t> active;
+    if ((rc = select_tables(c, indices ? indices : &none, n, &w, &active, false))) return rc;
+    if (w->n_chunks) {
+        const uint32_t grid = update_grid(c, w->n_chunks);
+        if (c->mode == TTP_MODE_MIXED)
+            hipLaunchKernelGGL(ttp::zero_chunks_kernel<uint16_t>, dim3(grid), dim3(ttp::kUpdBlock),
+                               0, c->stream, (uint16_t*)c->grad, w->chunks, w->n_chunks);
+        else
+            hipLaunchKernelGGL(ttp::zero_chunks_kernel<float>, dim3(grid), dim3(ttp::kUpdBlock),
+                               0, c->stream, (float*)c->grad, w->chunks, w->n_chunks);
+        HIP_TRY(hipGetLastError());
+    }
+    for (uint32_t k = 0; k < n; ++k) c->tensors[indices[k]].has_grad = set_to_none ? 0 : 1;
     return TTP_OK;
 }
 

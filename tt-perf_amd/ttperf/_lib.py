@@ -72,6 +72,7 @@ SIGNATURES = {
     "ttp_set_has_grad": (C.c_int, [_P, C.c_uint32, C.c_int]),
     "ttp_get_has_grad": (C.c_int, [_P, C.c_uint32, C.POINTER(C.c_int)]),
     "ttp_zero_grad": (C.c_int, [_P, C.c_int]),
+    "ttp_zero_grad_subset": (C.c_int, [_P, C.POINTER(C.c_uint32), C.c_uint32, C.c_int]),
     "ttp_accumulate_grad": (C.c_int, [_P, C.c_uint32, _P, C.c_uint64, C.c_int, C.c_int]),
     "ttp_adam_step": (C.c_int, [_P, C.POINTER(AdamHParams), C.POINTER(StepReport)]),
     "ttp_sgd_step": (C.c_int, [_P, C.POINTER(SgdHParams), C.POINTER(StepReport)]),

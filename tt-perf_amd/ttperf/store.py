@@ -339,8 +339,14 @@ class ParamStore:
     def set_has_grad(self, index, has):
         L.check(L.lib.ttp_set_has_grad(self._h, index, 1 if has else 0))
 
-    def zero_grad(self, set_to_none=True):
-        L.check(L.lib.ttp_zero_grad(self._h, 1 if set_to_none else 0))
+    def zero_grad(self, set_to_none=True, indices=None):
+        """Zero every grad (one fill), or only the listed tensors' grads (one launch);
+        set_to_none also marks them as having no grad."""
+        if indices is None:
+            L.check(L.lib.ttp_zero_grad(self._h, 1 if set_to_none else 0))
+            return
+        idx, n = self._index_array(indices)
+        L.check(L.lib.ttp_zero_grad_subset(self._h, idx, n, 1 if set_to_none else 0))
 
     def accumulate_grad(self, index, value):
         """Add an incoming gradient (numpy float32 / uint16 bf16 bits, or a torch float32 /
