@@ -401,3 +401,26 @@ def test_accumulate_grad_matches_torch_bf16_and_fp32_addition(rng):
                 want = (ta + tb).numpy()
                 assert np.array_equal(st.grad[:n].view(np.uint32), want.view(np.uint32))
             assert st.has_grad(0)
+
+
+def test_layout_invariants(rng):
+    """orc_layout (the flat store's tensor placement): every tensor starts on a 64-element
+    boundary (16-byte vectors never straddle tensors, 128-byte lines for bf16), tensors do not
+    overlap and keep caller order, and the padding per tensor is < 64 elements."""
+    for trial in range(50):
+        n = int(rng.integers(0, 40))
+        numels = [int(x) for x in rng.integers(0, 5000, n)]
+        if trial % 5 == 0 and n:
+            numels[0] = 0  # empty tensors are allowed
+        offs, total = O.layout(numels)
+        assert len(offs) == n
+        end = 0
+        for o, k in zip(offs, numels):
+            assert o % O.ALIGN == 0
+            assert o >= end  # caller order, no overlap
+            assert o - end < O.ALIGN  # padding below one alignment unit
+            end = int(o) + k
+        assert total % O.ALIGN == 0 and end <= total < end + O.ALIGN
+        assert total <= sum(numels) + O.ALIGN * n
+    offs, total = O.layout([])
+    assert total == 0
