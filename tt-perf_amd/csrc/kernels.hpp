@@ -15,11 +15,12 @@
 //                         per lane, so every wave instruction covers a contiguous 1 KiB / 512 B
 //                         span.
 // Work is a table of chunks of kChunk elements (the last chunk of a tensor is shorter; every
-// chunk starts on a 64-element boundary).  The update runs one 512-thread block per chunk,
+// chunk starts on a 64-element boundary).  The update runs one 256-thread block per chunk,
 // one vector per lane, at most kUpdBlocksPerCU blocks per CU: blocks are dispatched in
 // (reverse) chunk order, so the resident blocks sweep a narrow window of each buffer, which
-// keeps DRAM pages open.  16K-element chunks, a persistent grid, two or four vectors per lane, and
-// unlimited occupancy each measured 6-12% slower.  No MFMA: nothing here is a contraction.
+// keeps DRAM pages open.  16K-element chunks, a persistent grid, two or four vectors per
+// lane, 512-thread blocks and unlimited occupancy each measured 3-12% slower.  No MFMA:
+// nothing here is a contraction.
 //
 // Arithmetic matches the oracle bit for bit: no contraction (-ffp-contract=off), IEEE
 // division and square root (HIP's correctly rounded fp32 div/sqrt), denormals kept.
@@ -31,14 +32,16 @@
 namespace ttp {
 
 constexpr int kBlock = 256;     // 4 wave64s: norm pass, finalize and helper kernels
-constexpr int kUpdBlock = 512;  // 8 wave64s: update kernels
+constexpr int kUpdBlock = 256;  // 4 wave64s: update kernels
 constexpr int kVec = 4;         // elements per lane per vector
-constexpr uint32_t kChunk = kUpdBlock * kVec;  // 2048 elements: one vector per lane
+constexpr uint32_t kChunk = kUpdBlock * kVec;  // 1024 elements: one vector per lane
 // Resident update blocks per CU.  The host reserves LDS_per_CU / kUpdBlocksPerCU bytes of
-// (unused) dynamic LDS per update block so that no more than this many are resident: 24
+// (unused) dynamic LDS per update block so that no more than this many are resident: 16
 // waves per CU sweep the HBM pages of the nine streams with fewer row conflicts than the
-// 32+ waves that registers alone would allow (measured: 554 us vs 622 us on GPT-2 124M).
-constexpr int kUpdBlocksPerCU = 3;
+// 32+ waves that registers alone would allow (GPT-2 124M, same box, interleaved repeats:
+// 568 us vs 588 us for 512-thread blocks at 3 per CU, 622 us uncapped; GPT-2 XL fp32:
+// 7.36 ms vs 7.63 ms).
+constexpr int kUpdBlocksPerCU = 4;
 constexpr uint32_t kChunkDecay = 1u;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));

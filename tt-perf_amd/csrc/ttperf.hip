@@ -4,7 +4,7 @@
 //   * layout: tensors in caller order, each starting on a 64-element boundary (256 B for
 //     fp32, 128 B for bf16), so every lane's 4-element vector stays inside one tensor's
 //     footprint; the padding is zero and never written by a step;
-//   * work table: chunks of <= kChunk (2048) elements of one tensor.  The table of all
+//   * work table: chunks of <= kChunk (1024) elements of one tensor.  The table of all
 //     tensors is built once; a second table is built only while some tensor has no grad
 //     (py/optim.py:56-57 skip);
 //   * step: [norm pass (partials + finalize) when clipping or loss scaling] + one fused
