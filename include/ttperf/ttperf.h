@@ -2,8 +2,9 @@
  * ttperf.h — C ABI of libttperf_hip, the MI355X (gfx950) optimizer-step engine.
  *
  * One context owns a flat parameter store on one GPU: every tensor of a model is a
- * {offset, numel, flags} view into contiguous HBM buffers (param, grad, fp32 master,
- * exp_avg, exp_avg_sq, momentum).  A step over all tensors is one multi-tensor launch
+ * {offset, numel, flags} view into flat HBM buffers (param, grad, fp32 master, exp_avg,
+ * exp_avg_sq, momentum); the optimizer-private fp32 state is interleaved in records of
+ * 64-element slots (see ttp_buffer_layout).  A step over all tensors is one multi-tensor launch
  * (plus one grad-norm/inf-check launch when clipping or loss scaling is on).
  *
  * Reference interfaces each group of entry points replaces (csirak/tt-perf):
@@ -155,9 +156,22 @@ int ttp_flat_numel(const ttp_ctx* ctx, uint64_t* total);
 int ttp_tensor_info(const ttp_ctx* ctx, uint32_t index, uint64_t* offset, uint64_t* numel,
                     uint32_t* flags);
 /* Device address of buffer `which` for tensor `index` (or the flat base for
- * TTP_ALL_TENSORS).  Moment/momentum buffers are allocated on first use; asking for
- * one allocates it (zero-filled). */
+ * TTP_ALL_TENSORS), for the buffers stored contiguously: PARAM, GRAD and MOMENTUM always,
+ * MASTER in FP32 mode (where it is PARAM).  The optimizer-private fp32 state is kept in
+ * interleaved records (MIXED: master, m and v of each 64-element group side by side; FP32:
+ * m and v), for which this returns TTP_ERR_STATE; use ttp_buffer_layout, or ttp_upload /
+ * ttp_download, which convert.  Moment/momentum buffers are allocated on first use; asking
+ * for one allocates it (zero-filled).  Replaces direct access to a Value's data/grad
+ * tensors (autograd/dynamic/autograd.hpp:38-84, autograd/static/value.hpp:27-48). */
 int ttp_buffer_ptr(ttp_ctx* ctx, int which, uint32_t index, void** ptr);
+/* Addressing of any buffer: flat element e of `which` sits at
+ *   base + (e / group) * stride + e % group   (in elements of the buffer's type).
+ * group == stride for a contiguous buffer; MIXED-mode MASTER/EXP_AVG/EXP_AVG_SQ have
+ * group 64, stride 192 (slots 0, 1, 2 of one record); FP32-mode EXP_AVG/EXP_AVG_SQ group 64,
+ * stride 128.  Each tensor starts on a record boundary.  Allocates like ttp_buffer_ptr.
+ * No counterpart in the reference, whose optimizer state is private per-tensor ttnn
+ * tensors (py/optim.py:58-71). */
+int ttp_buffer_layout(ttp_ctx* ctx, int which, void** base, uint32_t* group, uint32_t* stride);
 
 /* ---- data movement ------------------------------------------------------------------ */
 /* Copy n elements (exactly the tensor's numel, or the flat total for TTP_ALL_TENSORS)

@@ -4,6 +4,11 @@
 //   * layout: tensors in caller order, each starting on a 64-element boundary (256 B for
 //     fp32, 128 B for bf16), so every lane's 4-element vector stays inside one tensor's
 //     footprint; the padding is zero and never written by a step;
+//   * optimizer state in records of 64-element slots (ttp::kRec): MIXED mode keeps master,
+//     m and v of each 64-element group in one [master|m|v] record, allocated with the store;
+//     FP32 mode keeps its contiguous master (the model-facing weights) and puts m and v in
+//     [m|v] records on first Adam use.  Momentum and the model-facing buffers are contiguous.
+//     Uploads, downloads and checkpoints convert between records and contiguous arrays;
 //   * work table: chunks of <= kChunk (1024) elements of one tensor.  The table of all
 //     tensors is built once; a second table is built only while some tensor has no grad
 //     (py/optim.py:56-57 skip);
@@ -87,10 +92,13 @@ struct ttp_ctx {
 
     void* param = nullptr;  // bf16 (MIXED) or == master (FP32)
     void* grad = nullptr;   // bf16 (MIXED) or fp32 (FP32)
+    // slot bases (see buffer_stride): MIXED, the three slots of `records`; FP32, the
+    // contiguous master and the two slots of `records` (null until the first Adam use)
     float* master = nullptr;
     float* exp_avg = nullptr;
     float* exp_avg_sq = nullptr;
-    float* momentum = nullptr;
+    float* records = nullptr;   // the state record array (the allocation)
+    float* momentum = nullptr;  // contiguous
     uint32_t* mom_init = nullptr;        // device, per tensor
     std::vector<uint8_t> host_mom_init;  // host view (exact while loss scaling is off)
 
@@ -211,12 +219,15 @@ int alloc_zero(ttp_ctx* c, void** p, uint64_t bytes) {
 }
 
 int ensure_adam_state(ttp_ctx* c) {
-    // py/optim.py:58-71: m and v start as zeros on first use
+    // py/optim.py:58-71: m and v start as zeros on first use.  MIXED mode allocates them
+    // (zero) with the master in its records at ttp_create; FP32 mode allocates the [m|v]
+    // records here.
+    if (c->exp_avg) return TTP_OK;
     int rc;
-    if ((!c->exp_avg || !c->exp_avg_sq) && (rc = no_capture(c, "first Adam step (allocates m, v)")))
-        return rc;
-    if (!c->exp_avg && (rc = alloc_zero(c, (void**)&c->exp_avg, c->total * 4))) return rc;
-    if (!c->exp_avg_sq && (rc = alloc_zero(c, (void**)&c->exp_avg_sq, c->total * 4))) return rc;
+    if ((rc = no_capture(c, "first Adam step (allocates m, v)"))) return rc;
+    if ((rc = alloc_zero(c, (void**)&c->records, c->total * 4 * 2))) return rc;
+    c->exp_avg = c->records;
+    c->exp_avg_sq = c->records + ttp::kRec;
     return TTP_OK;
 }
 
@@ -425,6 +436,20 @@ int check_index(const ttp_ctx* c, uint32_t i) {
     return TTP_OK;
 }
 
+// Elements per record of buffer `which`: element e sits at base + (e / kRec) * stride +
+// e % kRec; kRec means contiguous.
+uint32_t buffer_stride(const ttp_ctx* c, int which) {
+    const bool mixed = c->mode == TTP_MODE_MIXED;
+    switch (which) {
+        case TTP_BUF_MASTER: return mixed ? ttp::kStrideMixed : ttp::kRec;
+        case TTP_BUF_EXP_AVG:
+        case TTP_BUF_EXP_AVG_SQ: return mixed ? ttp::kStrideMixed : ttp::kStrideMV;
+    }
+    return ttp::kRec;
+}
+
+bool in_records(const ttp_ctx* c, int which) { return buffer_stride(c, which) != ttp::kRec; }
+
 void* buffer_base(ttp_ctx* c, int which) {
     switch (which) {
         case TTP_BUF_PARAM: return c->param;
@@ -476,17 +501,89 @@ uint32_t elementwise_grid(const ttp_ctx* c, uint64_t n) {
         1, std::min<uint64_t>((n + ttp::kBlock - 1) / ttp::kBlock, (uint64_t)c->num_cus * 16));
 }
 
+// Device staging buffer of at least `bytes` (host transfers pass through it).  Growing it
+// waits for queued work, which may still read the old one.
+int ensure_staging(ttp_ctx* c, uint64_t bytes) {
+    if (c->staging_bytes >= bytes) return TTP_OK;
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    if (c->staging) HIP_TRY(hipFree(c->staging));
+    c->staging = nullptr;
+    c->staging_bytes = 0;
+    HIP_TRY(hipMalloc(&c->staging, bytes));
+    c->staging_bytes = bytes;
+    return TTP_OK;
+}
+
+// Host transfers of record-stored buffers move through device staging in pieces of at most
+// this many elements (64 MiB of fp32).
+constexpr uint64_t kPieceElems = 16ull << 20;
+
+// slot elements [first, first + n) of record-stored buffer `which` -> contiguous device array
+int gather_slot(ttp_ctx* c, int which, uint64_t first, uint64_t n, float* dst) {
+    if (!n) return TTP_OK;
+    hipLaunchKernelGGL(ttp::gather_slot_kernel, dim3(elementwise_grid(c, n)), dim3(ttp::kBlock),
+                       0, c->stream, (const float*)buffer_base(c, which),
+                       buffer_stride(c, which), first, n, dst);
+    HIP_TRY(hipGetLastError());
+    return TTP_OK;
+}
+
+// contiguous device array (null: zeros) -> slot elements [first, first + n); an upload of
+// MIXED-mode master weights also writes their bf16 copy
+int scatter_slot(ttp_ctx* c, int which, uint64_t first, uint64_t n, const float* src) {
+    if (!n) return TTP_OK;
+    uint16_t* p16 = (c->mode == TTP_MODE_MIXED && which == TTP_BUF_MASTER) ? (uint16_t*)c->param
+                                                                          : nullptr;
+    hipLaunchKernelGGL(ttp::scatter_slot_kernel, dim3(elementwise_grid(c, n)), dim3(ttp::kBlock),
+                       0, c->stream, (float*)buffer_base(c, which), buffer_stride(c, which),
+                       first, n, src, p16);
+    HIP_TRY(hipGetLastError());
+    return TTP_OK;
+}
+
+// upload/download of a record-stored buffer's elements [first, first + n)
+int upload_slot(ttp_ctx* c, int which, uint64_t first, uint64_t n, const void* src, int kind) {
+    if (kind == TTP_DEVICE) return scatter_slot(c, which, first, n, (const float*)src);
+    int rc;
+    const uint64_t piece = std::min(n, kPieceElems);
+    if ((rc = ensure_staging(c, piece * 4))) return rc;
+    for (uint64_t o = 0; o < n; o += piece) {
+        const uint64_t k = std::min(piece, n - o);
+        HIP_TRY(hipMemcpyAsync(c->staging, (const float*)src + o, k * 4, hipMemcpyHostToDevice,
+                               c->stream));
+        if ((rc = scatter_slot(c, which, first + o, k, (const float*)c->staging))) return rc;
+        HIP_TRY(hipStreamSynchronize(c->stream));  // the staging buffer is refilled next
+    }
+    return TTP_OK;
+}
+
+int download_slot(ttp_ctx* c, int which, uint64_t first, uint64_t n, void* dst, int kind) {
+    if (kind == TTP_DEVICE) return gather_slot(c, which, first, n, (float*)dst);
+    int rc;
+    const uint64_t piece = std::min(n, kPieceElems);
+    if ((rc = ensure_staging(c, piece * 4))) return rc;
+    for (uint64_t o = 0; o < n; o += piece) {
+        const uint64_t k = std::min(piece, n - o);
+        if ((rc = gather_slot(c, which, first + o, k, (float*)c->staging))) return rc;
+        HIP_TRY(hipMemcpyAsync((float*)dst + o, c->staging, k * 4, hipMemcpyDeviceToHost,
+                               c->stream));
+        HIP_TRY(hipStreamSynchronize(c->stream));  // the staging buffer is refilled next
+    }
+    return TTP_OK;
+}
+
 void release(ttp_ctx* c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
-    for (void* p : {(void*)c->grad, (void*)c->master, (void*)c->exp_avg, (void*)c->exp_avg_sq,
-                    (void*)c->momentum, (void*)c->mom_init, (void*)c->st, (void*)c->partials,
-                    (void*)c->bias_tab, c->staging})
+    for (void* p : {(void*)c->grad, (void*)c->records, (void*)c->momentum, (void*)c->mom_init,
+                    (void*)c->st, (void*)c->partials, (void*)c->bias_tab, c->staging})
         if (p) (void)hipFree(p);
     free_tables(c->all);
     for (auto& kv : c->tables) free_tables(kv.second);
+    // MIXED: param is the bf16 copy and master lives in `records`; FP32: param == master
     if (c->mode == TTP_MODE_MIXED && c->param) (void)hipFree(c->param);
+    if (c->mode == TTP_MODE_FP32 && c->master) (void)hipFree(c->master);
     for (auto& v : c->ev)
         for (auto& p : v) {
             (void)hipEventDestroy(p.a);
@@ -574,13 +671,18 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
     }
     c->total = off;
     int rc;
-    if ((rc = alloc_zero(c, (void**)&c->master, c->total * 4))) return bail(rc);
-    if ((rc = alloc_zero(c, &c->grad, c->total * grad_esize(c)))) return bail(rc);
     if (mode == TTP_MODE_MIXED) {
+        // [master|m|v] records (m, v zero until the first Adam step) and the bf16 copy
+        if ((rc = alloc_zero(c, (void**)&c->records, c->total * 4 * 3))) return bail(rc);
+        c->master = c->records;
+        c->exp_avg = c->records + ttp::kRec;
+        c->exp_avg_sq = c->records + 2 * ttp::kRec;
         if ((rc = alloc_zero(c, &c->param, c->total * 2))) return bail(rc);
     } else {
+        if ((rc = alloc_zero(c, (void**)&c->master, c->total * 4))) return bail(rc);
         c->param = c->master;
     }
+    if ((rc = alloc_zero(c, &c->grad, c->total * grad_esize(c)))) return bail(rc);
     if ((rc = alloc_zero(c, (void**)&c->mom_init, std::max<uint64_t>(n, 1) * 4))) return bail(rc);
     c->host_mom_init.assign(n, 0);
     if ((rc = alloc_zero(c, (void**)&c->st, sizeof(DevState)))) return bail(rc);
@@ -689,6 +791,11 @@ int ttp_buffer_ptr(ttp_ctx* c, int which, uint32_t index, void** ptr) {
     if (!ptr) return fail(TTP_ERR_INVALID, "null output");
     if ((rc = set_dev(c))) return rc;
     if ((rc = materialize(c, which))) return rc;
+    if (in_records(c, which))
+        return fail(TTP_ERR_STATE,
+                    "buffer " + std::to_string(which) +
+                        " is kept in interleaved state records in this precision mode; use "
+                        "ttp_buffer_layout for its addressing, or ttp_upload / ttp_download");
     char* base = (char*)buffer_base(c, which);
     if (index == TTP_ALL_TENSORS) {
         *ptr = base;
@@ -696,6 +803,17 @@ int ttp_buffer_ptr(ttp_ctx* c, int which, uint32_t index, void** ptr) {
     }
     if ((rc = check_index(c, index))) return rc;
     *ptr = base + c->tensors[index].offset * buffer_esize(c, which);
+    return TTP_OK;
+}
+
+int ttp_buffer_layout(ttp_ctx* c, int which, void** base, uint32_t* group, uint32_t* stride) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if ((rc = set_dev(c))) return rc;
+    if ((rc = materialize(c, which))) return rc;
+    if (base) *base = buffer_base(c, which);
+    if (group) *group = ttp::kRec;
+    if (stride) *stride = buffer_stride(c, which);
     return TTP_OK;
 }
 
@@ -710,19 +828,19 @@ int ttp_upload(ttp_ctx* c, int which, uint32_t index, const void* src, uint64_t 
     uint64_t off, cnt;
     if ((rc = resolve_range(c, index, n, &off, &cnt))) return rc;
     const size_t es = buffer_esize(c, which);
-    char* dst = (char*)buffer_base(c, which) + off * es;
-    if (cnt) {
+    if (cnt && in_records(c, which)) {
+        // record-stored state; a MIXED master upload also writes the bf16 copy
+        if ((rc = upload_slot(c, which, off, cnt, src, kind))) return rc;
+        if (kind == TTP_HOST) HIP_TRY(hipStreamSynchronize(c->stream));
+    } else if (cnt) {
+        char* dst = (char*)buffer_base(c, which) + off * es;
         HIP_TRY(hipMemcpyAsync(dst, src, cnt * es,
                                kind == TTP_HOST ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice,
                                c->stream));
-        if (c->mode == TTP_MODE_MIXED && (which == TTP_BUF_MASTER || which == TTP_BUF_PARAM)) {
-            const uint32_t grid = elementwise_grid(c, cnt);
-            if (which == TTP_BUF_MASTER)
-                hipLaunchKernelGGL(ttp::master_to_bf16_kernel, dim3(grid), dim3(ttp::kBlock), 0,
-                                   c->stream, c->master + off, (uint16_t*)c->param + off, cnt);
-            else
-                hipLaunchKernelGGL(ttp::bf16_to_master_kernel, dim3(grid), dim3(ttp::kBlock), 0,
-                                   c->stream, (const uint16_t*)c->param + off, c->master + off, cnt);
+        if (c->mode == TTP_MODE_MIXED && which == TTP_BUF_PARAM) {
+            hipLaunchKernelGGL(ttp::bf16_to_master_kernel, dim3(elementwise_grid(c, cnt)),
+                               dim3(ttp::kBlock), 0, c->stream, (const uint16_t*)c->param,
+                               c->master, buffer_stride(c, TTP_BUF_MASTER), off, cnt);
             HIP_TRY(hipGetLastError());
         }
         if (kind == TTP_HOST) HIP_TRY(hipStreamSynchronize(c->stream));
@@ -747,8 +865,11 @@ int ttp_download(ttp_ctx* c, int which, uint32_t index, void* dst, uint64_t n, i
     uint64_t off, cnt;
     if ((rc = resolve_range(c, index, n, &off, &cnt))) return rc;
     const size_t es = buffer_esize(c, which);
-    const char* src = (const char*)buffer_base(c, which) + off * es;
-    if (cnt) {
+    if (cnt && in_records(c, which)) {
+        if ((rc = download_slot(c, which, off, cnt, dst, kind))) return rc;
+        if (kind == TTP_HOST) HIP_TRY(hipStreamSynchronize(c->stream));
+    } else if (cnt) {
+        const char* src = (const char*)buffer_base(c, which) + off * es;
         HIP_TRY(hipMemcpyAsync(dst, src, cnt * es,
                                kind == TTP_HOST ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice,
                                c->stream));
@@ -830,14 +951,7 @@ int ttp_accumulate_grad(ttp_ctx* c, uint32_t index, const void* src, uint64_t n,
     if (n) {
         const void* dsrc = src;
         if (kind == TTP_HOST) {
-            if (c->staging_bytes < n * sbytes) {
-                HIP_TRY(hipStreamSynchronize(c->stream));  // queued work may read the old one
-                if (c->staging) HIP_TRY(hipFree(c->staging));
-                c->staging = nullptr;
-                c->staging_bytes = 0;
-                HIP_TRY(hipMalloc(&c->staging, n * sbytes));
-                c->staging_bytes = n * sbytes;
-            }
+            if ((rc = ensure_staging(c, n * sbytes))) return rc;
             HIP_TRY(hipMemcpyAsync(c->staging, src, n * sbytes, hipMemcpyHostToDevice, c->stream));
             dsrc = c->staging;
         }
@@ -1200,14 +1314,14 @@ struct Pinned {
     }
 };
 
-float** state_buffer(ttp_ctx* c, int bit) {
+// buffer id of a state-file buffer bit
+int state_buffer_id(int bit) {
     switch (bit) {
-        case 1: return &c->master;
-        case 2: return &c->exp_avg;
-        case 4: return &c->exp_avg_sq;
-        case 8: return &c->momentum;
+        case 1: return TTP_BUF_MASTER;
+        case 2: return TTP_BUF_EXP_AVG;
+        case 4: return TTP_BUF_EXP_AVG_SQ;
     }
-    return nullptr;
+    return TTP_BUF_MOMENTUM;
 }
 
 }  // namespace
@@ -1255,16 +1369,21 @@ int ttp_save_state(ttp_ctx* c, const char* path) {
         StateTensor t{c->tensors[i].numel, c->tensors[i].flags, mom[i]};
         ok = put(&t, sizeof(t));
     }
+    // each buffer as one contiguous fp32 array, whatever its device layout: gathered into
+    // device staging piece by piece, then through a pinned buffer to the file
     Pinned stage;
     HIP_TRY(hipHostMalloc(&stage.p, kStageBytes));
+    if ((rc = ensure_staging(c, kStageBytes))) return rc;
+    const uint64_t piece = kStageBytes / 4;
     for (int bit = 1; ok && bit <= 8; bit <<= 1) {
         if (!(h.buffers & (uint32_t)bit)) continue;
-        const char* src = (const char*)*state_buffer(c, bit);
-        const uint64_t bytes = c->total * 4;
-        for (uint64_t o = 0; ok && o < bytes; o += kStageBytes) {
-            const size_t n = (size_t)std::min<uint64_t>(kStageBytes, bytes - o);
-            HIP_TRY(hipMemcpy(stage.p, src + o, n, hipMemcpyDeviceToHost));
-            ok = put(stage.p, n);
+        const int which = state_buffer_id(bit);
+        for (uint64_t o = 0; ok && o < c->total; o += piece) {
+            const uint64_t n = std::min(piece, c->total - o);
+            if ((rc = gather_slot(c, which, o, n, (float*)c->staging))) return rc;
+            HIP_TRY(hipMemcpyAsync(stage.p, c->staging, n * 4, hipMemcpyDeviceToHost, c->stream));
+            HIP_TRY(hipStreamSynchronize(c->stream));
+            ok = put(stage.p, n * 4);
         }
     }
     const uint64_t sum = hash.value();
@@ -1319,29 +1438,29 @@ int ttp_load_state(ttp_ctx* c, const char* path) {
     HIP_TRY(hipStreamSynchronize(c->stream));
     Pinned stage;
     HIP_TRY(hipHostMalloc(&stage.p, kStageBytes));
+    if ((rc = ensure_staging(c, kStageBytes))) return rc;
+    const uint64_t piece = kStageBytes / 4;
     for (int bit = 1; bit <= 8; bit <<= 1) {
-        float* dst = *state_buffer(c, bit);
+        const int which = state_buffer_id(bit);
         if (!(h.buffers & (uint32_t)bit)) {
-            if (dst && (rc = zero_device(c, dst, c->total * 4))) return rc;
+            // zeros (scatter with no source) into a buffer the context holds
+            if (buffer_base(c, which) && (rc = scatter_slot(c, which, 0, c->total, nullptr)))
+                return rc;
             continue;
         }
-        const uint64_t bytes = c->total * 4;
-        for (uint64_t o = 0; o < bytes; o += kStageBytes) {
-            const size_t n = (size_t)std::min<uint64_t>(kStageBytes, bytes - o);
-            if (!get(stage.p, n)) return fail(TTP_ERR_INVALID, "state file is truncated");
-            HIP_TRY(hipMemcpy((char*)dst + o, stage.p, n, hipMemcpyHostToDevice));
+        // the master scatter also rewrites the MIXED-mode bf16 copy as RNE(master)
+        for (uint64_t o = 0; o < c->total; o += piece) {
+            const uint64_t n = std::min(piece, c->total - o);
+            if (!get(stage.p, n * 4)) return fail(TTP_ERR_INVALID, "state file is truncated");
+            HIP_TRY(hipMemcpyAsync(c->staging, stage.p, n * 4, hipMemcpyHostToDevice, c->stream));
+            if ((rc = scatter_slot(c, which, o, n, (const float*)c->staging))) return rc;
+            HIP_TRY(hipStreamSynchronize(c->stream));  // stage.p is refilled next
         }
     }
     const uint64_t want = hash.value();
     uint64_t sum = 0;
     if (std::fread(&sum, 1, 8, f.f) != 8) return fail(TTP_ERR_INVALID, "state file is truncated");
     if (sum != want) return fail(TTP_ERR_INVALID, "state file checksum mismatch");
-    if (c->mode == TTP_MODE_MIXED && c->total) {
-        hipLaunchKernelGGL(ttp::master_to_bf16_kernel, dim3(elementwise_grid(c, c->total)),
-                           dim3(ttp::kBlock), 0, c->stream, c->master, (uint16_t*)c->param,
-                           c->total);
-        HIP_TRY(hipGetLastError());
-    }
     HIP_TRY(hipMemcpyAsync(c->mom_init, mom.data(), mom.size() * 4, hipMemcpyHostToDevice,
                            c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));

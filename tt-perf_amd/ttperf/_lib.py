@@ -67,6 +67,8 @@ SIGNATURES = {
     "ttp_tensor_info": (C.c_int, [_P, C.c_uint32, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
                                   C.POINTER(C.c_uint32)]),
     "ttp_buffer_ptr": (C.c_int, [_P, C.c_int, C.c_uint32, C.POINTER(_P)]),
+    "ttp_buffer_layout": (C.c_int, [_P, C.c_int, C.POINTER(_P), C.POINTER(C.c_uint32),
+                                    C.POINTER(C.c_uint32)]),
     "ttp_upload": (C.c_int, [_P, C.c_int, C.c_uint32, _P, C.c_uint64, C.c_int]),
     "ttp_download": (C.c_int, [_P, C.c_int, C.c_uint32, _P, C.c_uint64, C.c_int]),
     "ttp_set_has_grad": (C.c_int, [_P, C.c_uint32, C.c_int]),

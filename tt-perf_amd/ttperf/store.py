@@ -270,9 +270,18 @@ class ParamStore:
 
     # ---- buffers -----------------------------------------------------------------------------
     def ptr(self, which, index=L.ALL_TENSORS):
+        """Device address of a contiguously stored buffer (PARAM, GRAD, MOMENTUM; MASTER in
+        FP32 mode); the interleaved optimizer state raises (see layout())."""
         p = C.c_void_p()
         L.check(L.lib.ttp_buffer_ptr(self._h, which, index, C.byref(p)))
         return p.value
+
+    def layout(self, which):
+        """(base, group, stride): flat element e of `which` sits at
+        base + (e // group * stride + e % group) * element_size."""
+        p, g, s = C.c_void_p(), C.c_uint32(), C.c_uint32()
+        L.check(L.lib.ttp_buffer_layout(self._h, which, C.byref(p), C.byref(g), C.byref(s)))
+        return p.value, g.value, s.value
 
     def _esize(self, which):
         if which in (L.BUF_PARAM, L.BUF_GRAD) and self.mode == L.MODE_MIXED:
