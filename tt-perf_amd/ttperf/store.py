@@ -2,8 +2,11 @@
 
 Replaces the per-parameter tensors the reference's optimizers walk (py/engine.py:74-156
 `Tensor.tt` / `Tensor.grad`; autograd/dynamic/autograd.hpp:38-84 `Value::data` / `grad`) with
-views into contiguous HBM buffers: each `Tensor` here is (store, index) and its data lives
-at `offset` of the store's param / grad / master / moment buffers.
+views into flat HBM buffers: each `Tensor` here is (store, index) and its data lives at
+`offset` of the store's param and grad buffers.  The fp32 optimizer state (master, m, v in
+mixed precision; m, v in fp32 mode) is interleaved in records of 64-element slots;
+upload/download convert it to and from contiguous arrays, and ParamStore.layout() gives its
+device addressing.
 """
 from __future__ import annotations
 
