@@ -82,7 +82,8 @@ typedef struct ttp_ctx ttp_ctx;
 typedef struct ttp_graph ttp_graph;
 
 typedef struct ttp_tensor_desc {
-    uint64_t numel;  /* elements; 0 is allowed (the tensor is then never touched) */
+    uint64_t numel;  /* elements; 0 is allowed (the tensor is then never touched); the
+                        64-element-padded sizes of a table total at most 2^40 */
     uint32_t flags;  /* TTP_TENSOR_* */
     uint32_t reserved;
 } ttp_tensor_desc;

@@ -76,6 +76,18 @@ def test_c_abi_argument_errors_without_a_device():
     assert b"mode" in lib.ttp_last_error()
     d[0].flags = 0x80
     assert lib.ttp_create(0, d, 1, L.MODE_FP32, C.byref(h)) == L.ERR_INVALID  # unknown flag
+    # a table whose padded sizes would wrap 64 bits (or exceed 2^40 elements) is rejected
+    # before any device work: a wrapped footprint would let kernels index past the buffers
+    d[0].flags = 0
+    d[0].numel = 2**64 - 1
+    assert lib.ttp_create(0, d, 1, L.MODE_FP32, C.byref(h)) == L.ERR_INVALID
+    assert b"2^40" in lib.ttp_last_error()
+    d2 = (L.TensorDesc * 3)()
+    for k in range(3):
+        d2[k].numel = 2**39 + 1
+    assert lib.ttp_create(0, d2, 3, L.MODE_FP32, C.byref(h)) == L.ERR_INVALID
+    assert b"total" in lib.ttp_last_error()
+    d[0].numel = 10
     assert lib.ttp_create(0, d, 1, L.MODE_FP32, None) == L.ERR_INVALID
     hp = L.AdamHParams(lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8)
     assert lib.ttp_adam_step(None, C.byref(hp), None) == L.ERR_INVALID

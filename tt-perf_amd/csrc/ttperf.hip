@@ -50,6 +50,9 @@ int fail(int code, const std::string& msg) {
     } while (0)
 
 constexpr uint64_t kAlign = 64;  // elements
+// Largest store: 2^40 elements (4 TiB of fp32 per buffer, far beyond one GPU's 288 GB), so the
+// padded sizes and byte counts computed from it never wrap in 64 bits.
+constexpr uint64_t kMaxElems = 1ull << 40;
 
 uint64_t env_u64(const char* name, uint64_t dflt) {
     const char* s = std::getenv(name);
@@ -620,9 +623,20 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
     if (mode != TTP_MODE_FP32 && mode != TTP_MODE_MIXED)
         return fail(TTP_ERR_INVALID, "mode must be TTP_MODE_FP32 or TTP_MODE_MIXED");
     if (n > (1u << 24)) return fail(TTP_ERR_INVALID, "too many tensors (max 2^24)");
-    for (uint32_t i = 0; i < n; ++i)
+    // the table must describe a store that fits one GPU: the padded footprint sum cannot
+    // wrap, and every chunk index stays inside the buffers the kernels address
+    uint64_t footprint = 0;
+    for (uint32_t i = 0; i < n; ++i) {
         if (descs[i].flags & ~TTP_TENSOR_DECAY)
             return fail(TTP_ERR_INVALID, "unknown flags on tensor " + std::to_string(i));
+        if (descs[i].numel > kMaxElems)
+            return fail(TTP_ERR_INVALID, "tensor " + std::to_string(i) + " has " +
+                                             std::to_string(descs[i].numel) +
+                                             " elements (max 2^40)");
+        footprint += (descs[i].numel + kAlign - 1) / kAlign * kAlign;
+        if (footprint > kMaxElems)
+            return fail(TTP_ERR_INVALID, "the tensors total more than 2^40 elements");
+    }
     int ndev = 0;
     if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0)
         return fail(TTP_ERR_NO_DEVICE, "no HIP device available");
