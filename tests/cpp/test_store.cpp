@@ -1,0 +1,210 @@
+// test_store.cpp — the flat store's data paths through the C ABI: uploads and downloads of
+// every buffer (host and device memory, per tensor and flat, longer than one staging piece),
+// the state-record layout (ttp_buffer_layout, ttp_buffer_ptr refusals), a checkpoint round
+// trip with rejection of a damaged file, and argument errors.  Also built with host-side
+// AddressSanitizer/UBSan (make asan) to check the host code's memory handling.
+//
+// Device memory for the TTP_DEVICE transfers comes from a second context's flat grad buffer,
+// so the test needs only the C ABI.
+#include <cstdio>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+
+namespace {
+
+uint32_t lcg(uint64_t& s) {
+    s = s * 6364136223846793005ull + 1442695040888963407ull;
+    return (uint32_t)(s >> 33);
+}
+
+std::vector<float> randn(size_t n, uint64_t seed) {  // small finite values, any sign
+    std::vector<float> v(n);
+    for (auto& x : v) x = ((float)(lcg(seed) & 0xFFFFFF) / 16777216.0f - 0.5f) * 0.02f;
+    return v;
+}
+
+std::vector<float> download(ttp_ctx* c, int which, uint32_t i, uint64_t n) {
+    std::vector<float> v(n);
+    test::check(ttp_download(c, which, i, v.data(), n, TTP_HOST) == TTP_OK,
+                std::string("download: ") + ttp_last_error());
+    return v;
+}
+
+std::vector<uint16_t> download16(ttp_ctx* c, int which, uint32_t i, uint64_t n) {
+    std::vector<uint16_t> v(n);
+    test::check(ttp_download(c, which, i, v.data(), n, TTP_HOST) == TTP_OK,
+                std::string("download: ") + ttp_last_error());
+    return v;
+}
+
+uint16_t to_bf16(float x) {
+    uint32_t u = test::bits(x);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+ttp_ctx* create(const std::vector<uint64_t>& numel, int mode) {
+    std::vector<ttp_tensor_desc> d(numel.size());
+    for (size_t i = 0; i < numel.size(); ++i) d[i] = {numel[i], (i % 2) ? TTP_TENSOR_DECAY : 0u, 0};
+    ttp_ctx* c = nullptr;
+    if (ttp_create(0, d.data(), (uint32_t)d.size(), mode, &c) != TTP_OK) {
+        std::printf("FAIL: ttp_create: %s\n", ttp_last_error());
+        std::exit(1);
+    }
+    return c;
+}
+
+void run_mode(int mode) {
+    const bool mixed = mode == TTP_MODE_MIXED;
+    const char* tag = mixed ? "mixed" : "fp32";
+    // ragged sizes, and one tensor longer than a 16 Mi-element staging piece
+    const std::vector<uint64_t> numel = {0, 1, 3, 63, 64, 65, 1000, 2049, (20ull << 20) + 7};
+    ttp_ctx* c = create(numel, mode);
+    uint64_t total = 0;
+    test::check(ttp_flat_numel(c, &total) == TTP_OK, "flat_numel");
+    std::vector<uint64_t> off(numel.size());
+    for (uint32_t i = 0; i < numel.size(); ++i) ttp_tensor_info(c, i, &off[i], nullptr, nullptr);
+
+    // weights and grads, then two Adam steps so every state buffer holds values
+    for (uint32_t i = 0; i < numel.size(); ++i) {
+        auto w = randn(numel[i], 100 + i);
+        test::check(ttp_upload(c, TTP_BUF_MASTER, i, w.data(), w.size(), TTP_HOST) == TTP_OK,
+                    std::string(tag) + " upload master: " + ttp_last_error());
+        if (mixed) {
+            auto p = download16(c, TTP_BUF_PARAM, i, numel[i]);
+            size_t bad = 0;
+            for (size_t k = 0; k < p.size(); ++k) bad += p[k] != to_bf16(w[k]);
+            test::check(bad == 0, std::string(tag) + " bf16 copy of an uploaded master");
+        }
+        auto g = randn(numel[i], 200 + i);
+        if (mixed) {
+            std::vector<uint16_t> h(g.size());
+            for (size_t k = 0; k < g.size(); ++k) h[k] = to_bf16(g[k]);
+            ttp_upload(c, TTP_BUF_GRAD, i, h.data(), h.size(), TTP_HOST);
+        } else {
+            ttp_upload(c, TTP_BUF_GRAD, i, g.data(), g.size(), TTP_HOST);
+        }
+    }
+    ttp_adam_hparams hp = {1e-3, 0.9, 0.95, 1e-8, 0.1, 1, 0, 1.0};
+    for (int s = 0; s < 2; ++s)
+        test::check(ttp_adam_step(c, &hp, nullptr) == TTP_OK, std::string("adam: ") + ttp_last_error());
+    ttp_sgd_hparams sp = {1e-3, 0.9, 0.0, 0.0, 0, 0, 0.0};
+    test::check(ttp_sgd_step(c, &sp, nullptr) == TTP_OK, std::string("sgd: ") + ttp_last_error());
+
+    // layout: documented addressing, and pointers only for contiguous buffers
+    const int state[3] = {TTP_BUF_MASTER, TTP_BUF_EXP_AVG, TTP_BUF_EXP_AVG_SQ};
+    for (int which : state) {
+        void* base = nullptr;
+        uint32_t group = 0, stride = 0;
+        test::check(ttp_buffer_layout(c, which, &base, &group, &stride) == TTP_OK, "layout");
+        const uint32_t want = (which == TTP_BUF_MASTER) ? (mixed ? 192u : 64u) : (mixed ? 192u : 128u);
+        test::check(group == 64 && stride == want,
+                    std::string(tag) + " layout of buffer " + std::to_string(which));
+        void* p = nullptr;
+        const int rc = ttp_buffer_ptr(c, which, 3, &p);
+        test::check(stride == 64 ? rc == TTP_OK : rc == TTP_ERR_STATE,
+                    std::string(tag) + " buffer_ptr of buffer " + std::to_string(which));
+    }
+    for (int which : {TTP_BUF_PARAM, TTP_BUF_GRAD, TTP_BUF_MOMENTUM}) {
+        void* p = nullptr;
+        test::check(ttp_buffer_ptr(c, which, TTP_ALL_TENSORS, &p) == TTP_OK && p,
+                    "buffer_ptr of a contiguous buffer");
+    }
+
+    // host round trips of each fp32 buffer: per tensor, then flat
+    for (int which : {TTP_BUF_MASTER, TTP_BUF_EXP_AVG, TTP_BUF_EXP_AVG_SQ, TTP_BUF_MOMENTUM}) {
+        const uint32_t k = 8;  // the long tensor: two staging pieces
+        auto v = randn(numel[k], 300 + which);
+        test::check(ttp_upload(c, which, k, v.data(), v.size(), TTP_HOST) == TTP_OK, "upload");
+        test::assert_bits(download(c, which, k, numel[k]), v, std::string(tag) + " round trip");
+        auto flat = download(c, which, TTP_ALL_TENSORS, total);
+        std::vector<float> mid(flat.begin() + off[k], flat.begin() + off[k] + numel[k]);
+        test::assert_bits(mid, v, std::string(tag) + " flat view of a tensor upload");
+        auto f2 = randn(total, 400 + which);
+        test::check(ttp_upload(c, which, TTP_ALL_TENSORS, f2.data(), total, TTP_HOST) == TTP_OK,
+                    "flat upload");
+        test::assert_bits(download(c, which, TTP_ALL_TENSORS, total), f2,
+                          std::string(tag) + " flat round trip");
+    }
+
+    // device round trips through another context's flat grad buffer (fp32, `total` long)
+    ttp_ctx* scratch = create({total}, TTP_MODE_FP32);
+    void* dev = nullptr;
+    test::check(ttp_buffer_ptr(scratch, TTP_BUF_GRAD, TTP_ALL_TENSORS, &dev) == TTP_OK && dev,
+                "scratch device buffer");
+    for (int which : state) {
+        auto v = randn(total, 500 + which);
+        ttp_upload(scratch, TTP_BUF_GRAD, TTP_ALL_TENSORS, v.data(), total, TTP_HOST);
+        ttp_sync(scratch);
+        test::check(ttp_upload(c, which, TTP_ALL_TENSORS, dev, total, TTP_DEVICE) == TTP_OK,
+                    "device upload");
+        ttp_sync(c);  // the upload reads `dev` on c's stream; the fill below is on scratch's
+        ttp_zero_grad(scratch, 0);
+        ttp_sync(scratch);
+        test::check(ttp_download(c, which, TTP_ALL_TENSORS, dev, total, TTP_DEVICE) == TTP_OK,
+                    "device download");
+        ttp_sync(c);
+        test::assert_bits(download(scratch, TTP_BUF_GRAD, TTP_ALL_TENSORS, total), v,
+                          std::string(tag) + " device round trip");
+    }
+    ttp_destroy(scratch);
+
+    // checkpoint: save, load into a fresh context, every buffer and the counters equal
+    const std::string path = std::string("/tmp/ttp_test_store_") + tag + ".bin";
+    test::check(ttp_adam_step(c, &hp, nullptr) == TTP_OK, "adam before save");
+    test::check(ttp_save_state(c, path.c_str()) == TTP_OK, std::string("save: ") + ttp_last_error());
+    ttp_ctx* d = create(numel, mode);
+    test::check(ttp_load_state(d, path.c_str()) == TTP_OK, std::string("load: ") + ttp_last_error());
+    for (int which : {TTP_BUF_MASTER, TTP_BUF_EXP_AVG, TTP_BUF_EXP_AVG_SQ, TTP_BUF_MOMENTUM})
+        test::assert_bits(download(d, which, TTP_ALL_TENSORS, total),
+                          download(c, which, TTP_ALL_TENSORS, total),
+                          std::string(tag) + " checkpoint buffer " + std::to_string(which));
+    if (mixed) {
+        auto a = download16(c, TTP_BUF_PARAM, TTP_ALL_TENSORS, total);
+        auto b = download16(d, TTP_BUF_PARAM, TTP_ALL_TENSORS, total);
+        test::check(a == b, "checkpoint restores the bf16 copy");
+    }
+    uint64_t t1 = 0, t2 = 0;
+    ttp_get_step(c, &t1);
+    ttp_get_step(d, &t2);
+    test::check(t1 == 4 && t2 == 4, "checkpoint step count (three Adam steps and one SGD step)");
+    // a damaged file is rejected: flip one byte in the middle
+    {
+        FILE* f = std::fopen(path.c_str(), "r+b");
+        std::fseek(f, 0, SEEK_END);
+        const long size = std::ftell(f);
+        std::fseek(f, size / 2, SEEK_SET);
+        int ch = std::fgetc(f);
+        std::fseek(f, size / 2, SEEK_SET);
+        std::fputc(ch ^ 0x40, f);
+        std::fclose(f);
+    }
+    test::check(ttp_load_state(d, path.c_str()) == TTP_ERR_INVALID, "damaged checkpoint rejected");
+    std::remove(path.c_str());
+
+    // argument errors
+    std::vector<float> one(5);
+    test::check(ttp_upload(c, TTP_BUF_MASTER, 2, one.data(), 5, TTP_HOST) == TTP_ERR_RANGE,
+                "wrong element count");
+    test::check(ttp_download(c, TTP_BUF_MASTER, 99, one.data(), 1, TTP_HOST) == TTP_ERR_RANGE,
+                "tensor index out of range");
+    test::check(ttp_buffer_layout(c, 17, nullptr, nullptr, nullptr) == TTP_ERR_INVALID,
+                "unknown buffer id");
+    ttp_destroy(d);
+    ttp_destroy(c);
+}
+
+}  // namespace
+
+int main() {
+    test::DeviceGuard guard;
+    run_mode(TTP_MODE_MIXED);
+    run_mode(TTP_MODE_FP32);
+    // a table past the 2^40-element bound is refused before any allocation
+    ttp_tensor_desc big[2] = {{1ull << 40, 0, 0}, {64, 0, 0}};
+    ttp_ctx* c = nullptr;
+    test::check(ttp_create(0, big, 2, TTP_MODE_MIXED, &c) == TTP_ERR_INVALID && !c,
+                "oversized table rejected");
+    return test::finish("test_store");
+}

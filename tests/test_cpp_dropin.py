@@ -1,7 +1,12 @@
 """Runs the C++ drop-in tests (tests/cpp, built by __graft_entry__.build()) on the GPU: the
 reference's autograd/tests/test_sgd.cpp known answers, the traced layers' sgd_step surface,
 Adam/AdamW against a host restatement, the static layers' and transformer modules'
-sgd_step / zero_grad, and a train_mlp-style loop whose loss must fall."""
+sgd_step / zero_grad, a train_mlp-style loop whose loss must fall, and the store's data paths
+(test_store: uploads/downloads, state records, checkpoint).
+
+Each test also runs as a host-side AddressSanitizer/UBSan build (tests/cpp/build-asan against
+tt-perf_amd/lib/asan): any invalid host memory access or undefined behaviour in the library's
+host code or the C++ headers fails the run.  Device code is the same in both builds."""
 import os
 import subprocess
 
@@ -11,16 +16,35 @@ from conftest import REPO
 
 pytestmark = pytest.mark.gpu
 
-BUILD = os.path.join(REPO, "tests", "cpp", "build")
+CPP = os.path.join(REPO, "tests", "cpp")
+TESTS = ["test_sgd", "test_traced", "test_adam", "test_modules", "train_mlp", "test_store"]
 
 
-@pytest.mark.parametrize("name", ["test_sgd", "test_traced", "test_adam", "test_modules",
-                                  "train_mlp"])
-def test_cpp_dropin(name):
-    exe = os.path.join(BUILD, name)
-    if not os.access(exe, os.X_OK):
-        subprocess.run(["make", "-s", "-C", os.path.join(REPO, "tests", "cpp")], check=True)
-    p = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+def _run(exe, env=None):
+    p = subprocess.run([exe], capture_output=True, text=True, timeout=240, env=env)
     print(p.stdout[-3000:])
+    return p
+
+
+@pytest.mark.parametrize("name", TESTS)
+def test_cpp_dropin(name):
+    exe = os.path.join(CPP, "build", name)
+    if not os.access(exe, os.X_OK):
+        subprocess.run(["make", "-s", "-C", CPP], check=True)
+    p = _run(exe)
     assert p.returncode == 0, f"{name} exited {p.returncode}:\n{p.stdout[-3000:]}\n{p.stderr[-2000:]}"
     assert f"{name}: PASS" in p.stdout
+
+
+@pytest.mark.parametrize("name", TESTS)
+def test_cpp_dropin_host_sanitizers(name):
+    exe = os.path.join(CPP, "build-asan", name)
+    if not os.access(exe, os.X_OK):
+        pytest.skip("sanitizer build absent (make -C tt-perf_amd asan && make -C tests/cpp asan)")
+    # leak checking is off: the HIP runtime keeps allocations until exit by design
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0",
+               UBSAN_OPTIONS="print_stacktrace=1")
+    p = _run(exe, env)
+    assert p.returncode == 0, f"{name} (ASan/UBSan) exited {p.returncode}:\n{p.stdout[-3000:]}\n{p.stderr[-4000:]}"
+    assert f"{name}: PASS" in p.stdout
+    assert "ERROR: AddressSanitizer" not in p.stderr and "runtime error" not in p.stderr, p.stderr[-4000:]
