@@ -22,6 +22,9 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(REPO, "tt-perf_amd"))
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
+# gradient bytes up to which libttperf_hip runs the cached-gradient update instantiation
+# (kCachedGradBytes in tt-perf_amd/csrc/ttperf.hip): names the kernel in the roofline
+CACHED_GRAD_BYTES = 256 << 20
 # algorithmic bytes per parameter of one update-kernel pass (and of the norm pass)
 UPDATE_BYTES = {("adamw", "mixed"): 28, ("adamw", "fp32"): 28, ("sgdm", "fp32"): 20,
                 ("sgdm", "mixed"): 20}
@@ -146,6 +149,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     store = ttperf.ParamStore(shapes, mode=mode, decay=decay, names=names)
+    store_total = store.total
     # a created stream (the legacy default stream cannot be captured); torch's events and
     # synchronisation see it
     stream = torch.cuda.Stream()
@@ -261,6 +265,12 @@ def main():
     del src, dst
 
     achieved = n_params * ub / (upd_avg / 1e3) / 1e9
+    # the instantiation libttperf_hip launches (its rocprof name)
+    grad_t, mixed_t = ("unsigned short", "true") if mode == "mixed" else ("float", "false")
+    grad_bytes = store_total * (2 if mode == "mixed" else 4)
+    cached_t = "true" if grad_bytes <= CACHED_GRAD_BYTES else "false"
+    kname = "adam_kernel" if args.optimizer == "adamw" else "sgd_kernel"
+    upd_kernel = f"{kname}<{grad_t}, {mixed_t}, {cached_t}>"
     step_gbps = n_params * (ub + nb) / (ms_step / 1e3) / 1e9
     out = {
         "metric": HEADLINE if args.config == "gpt2_124m" and args.optimizer == "adamw" else
@@ -299,7 +309,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": traffic_from_profiles(args.config),
-                     "kernel": "adam_kernel<bf16,mixed>" if mode == "mixed" else "adam_kernel<f32>",
+                     "kernel": upd_kernel,
                      "algorithmic_bytes_per_launch": n_params * ub},
         "cpu_baseline": None,
     }
