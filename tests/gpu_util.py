@@ -46,7 +46,8 @@ def make_pair(shapes, decay, mode, init_std=0.02, seed=0, init="normal"):
         else:
             flat[o:o + t.numel].normal_(0.0, init_std, generator=g)
     store.upload(L.BUF_MASTER, L.ALL_TENSORS, flat)
-    ref.master[:] = flat.cpu().numpy()
+    # the oracle's arrays hold at least one element (an all-empty table has total 0)
+    ref.master[:store.total] = flat.cpu().numpy()
     if mode == O.MODE_MIXED:
         ref.param[:] = O.bf16_rne(ref.master)
     return store, ref
