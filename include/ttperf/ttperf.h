@@ -30,6 +30,13 @@
  * stream and is asynchronous, except ttp_download to host memory, ttp_sync, ttp_scaler_get,
  * ttp_get_step, ttp_grad_norm and any step call given a non-NULL report, which wait for
  * the stream.  A context is used by one host thread at a time.
+ *
+ * Environment, read at ttp_create (tuning only):
+ *   TTP_UPD_BLOCKS_PER_CU  resident update blocks per CU (default 4; 0: no cap).  Results do not
+ *                          depend on it.
+ *   TTP_NORM_GRID          blocks of the gradient-norm pass (default 8 x CUs, at most 65536).
+ *                          It fixes the fp64 summation order of the norm: deterministic for a
+ *                          given value, last bits may differ between values.
  */
 #ifndef TTPERF_TTPERF_H
 #define TTPERF_TTPERF_H
