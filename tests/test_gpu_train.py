@@ -1,0 +1,79 @@
+"""The Python caller of the reference's optimizer, end to end: py/experiment.py:259,294-295
+(`opt = Adam(model.parameters(), lr=...)`, then `loss.backward(); opt.step(); opt.zero_grad()`
+per iteration) with torch as the forward/backward and libttperf_hip as the optimizer, sharing
+memory with no copies.
+
+The model's weights are torch views of the store's param buffer (bf16 in mixed precision),
+torch's backward accumulates into views of the store's grad buffer, and the optimizer step
+updates both in place.  Each step is checked against the CPU oracle fed the same gradients
+(downloaded from the store): fp32 state within the 2-ulp bar, bf16 weights bit-exact.  The
+loss must fall.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_util import compare_state, torch_mod
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("mode,opt_name", [("fp32", "Adam"), ("mixed", "AdamW"),
+                                           ("mixed", "SGD")])  # SGD with momentum 0.9
+def test_torch_forward_backward_with_zero_copy_store(mode, opt_name):
+    import ttperf
+    from ttperf import _lib as L
+    torch = torch_mod()
+    shapes = [(32, 64), (64,), (64, 8), (8,)]
+    decay = [True, False, True, False]
+    store = ttperf.ParamStore(shapes, mode=mode, decay=decay)
+    store.set_stream(torch.cuda.current_stream())
+    ref = O.OracleStore([t.numel for t in store.tensors], flags=[int(d) for d in decay],
+                        mode=O.MODE_MIXED if mode == "mixed" else O.MODE_FP32, nthreads=2)
+    g = torch.Generator().manual_seed(5)
+    for i, s in enumerate(shapes):  # [in, out] weights ~ U(+-1/sqrt(in)) as py/nn.py:36
+        b = 1.0 / np.sqrt(shapes[0][0] if i < 2 else shapes[2][0])
+        w = ((torch.rand(s, generator=g) * 2 - 1) * b).numpy().ravel()
+        store.tensors[i].set_data(w)
+        ref.set_master(i, w)
+    params = [torch.nn.Parameter(t.torch_view(L.BUF_PARAM)) for t in store.tensors]
+    for p, t in zip(params, store.tensors):
+        p.grad = t.torch_view(L.BUF_GRAD)
+        assert p.data_ptr() == t.data_ptr(L.BUF_PARAM)  # no copy
+    dt = params[0].dtype
+    x = torch.randn(64, 32, generator=g).to("cuda", dt)
+    y = torch.randn(64, 8, generator=g).to("cuda", dt)
+    if opt_name == "Adam":
+        opt = ttperf.Adam(store.parameters(), lr=1e-2)
+        ref_step = lambda: ref.adam_step(lr=1e-2, betas=(0.9, 0.999), eps=1e-8)
+    elif opt_name == "AdamW":
+        opt = ttperf.AdamW(store.parameters(), lr=1e-2, weight_decay=0.1, max_grad_norm=1.0)
+        ref_step = lambda: ref.adam_step(lr=1e-2, betas=(0.9, 0.999), eps=1e-8,
+                                         weight_decay=0.1, decoupled=True, max_grad_norm=1.0)
+    else:
+        opt = ttperf.SGD(store.parameters(), lr=5e-2, momentum=0.9)
+        ref_step = lambda: ref.sgd_step(lr=5e-2, momentum=0.9)
+    losses = []
+    for it in range(40):
+        opt.zero_grad()
+        h = torch.relu(x @ params[0] + params[1])
+        loss = ((h @ params[2] + params[3] - y).float() ** 2).mean()
+        loss.backward()          # accumulates into the store's grad buffer
+        store.mark_grads()
+        ref.grad[:] = store.download(L.BUF_GRAD)
+        for i in range(ref.n):
+            ref.set_has_grad(i, True)
+        opt.step()
+        ref_step()
+        losses.append(loss.item())
+    print(f"{mode} {opt_name}: loss {losses[0]:.5f} -> {losses[-1]:.5f}", flush=True)
+    assert losses[-1] < 0.6 * losses[0]
+    which = (("master", "momentum", "param") if opt_name == "SGD" else
+             ("master", "exp_avg", "exp_avg_sq", "param"))
+    compare_state(store, ref, which=which, max_ulp=2)
+    # the torch views see the optimizer's writes in place
+    torch.cuda.synchronize()
+    p0 = params[0].detach().float().cpu().numpy().ravel()
+    w0 = store.tensors[0].numpy().ravel()
+    assert np.array_equal(p0.view(np.uint32), w0.astype(np.float32).view(np.uint32))
+    store.close()

@@ -88,6 +88,12 @@ class Tensor:
     def data_ptr(self, which=L.BUF_PARAM):
         return self.store.ptr(which, self.index)
 
+    def torch_view(self, which=L.BUF_PARAM):
+        """A torch tensor of this tensor's shape aliasing its slice of the store's buffer
+        `which` (no copy): the weights a torch forward reads (BUF_PARAM), or the gradients a
+        torch backward accumulates into (BUF_GRAD).  See ParamStore.torch_view."""
+        return self.store.torch_view(which, self.index).view(self.shape)
+
 
 Parameter = Tensor
 
@@ -350,6 +356,37 @@ class ParamStore:
 
     def set_has_grad(self, index, has):
         L.check(L.lib.ttp_set_has_grad(self._h, index, 1 if has else 0))
+
+    def mark_grads(self, indices=None):
+        """Record that grads were written outside the ABI (through torch_view(BUF_GRAD) or a
+        device pointer): the listed tensors, or all, now have a grad."""
+        for i in range(len(self.tensors)) if indices is None else indices:
+            self.set_has_grad(i, True)
+
+    def torch_view(self, which=L.BUF_PARAM, index=L.ALL_TENSORS):
+        """Zero-copy torch tensor over a contiguously stored buffer (PARAM, GRAD, MOMENTUM;
+        MASTER in fp32 mode): the whole flat buffer, or one tensor's slice as a 1-D tensor.
+        bf16 buffers come back as torch.bfloat16.  The view aliases the store's memory for the
+        store's lifetime.  Torch work on it is ordered on torch's current stream and the
+        store's on its own: share one stream (set_stream(torch.cuda.current_stream())) or
+        synchronise between them.  Writes to BUF_GRAD through a view need mark_grads()."""
+        import torch
+        ptr = self.ptr(which, index)
+        n = self._numel(index)
+        two = self._esize(which) == 2
+        if n == 0:
+            return torch.empty(0, dtype=torch.bfloat16 if two else torch.float32,
+                               device=f"cuda:{self.device}")
+
+        class _Device:  # the CUDA array interface torch wraps without copying
+            __cuda_array_interface__ = {"data": (ptr, False), "shape": (n,),
+                                        "typestr": "<u2" if two else "<f4", "strides": None,
+                                        "version": 3}
+
+        t = torch.as_tensor(_Device(), device=f"cuda:{self.device}")
+        if t.data_ptr() != ptr:
+            raise RuntimeError("torch copied the buffer instead of wrapping it")
+        return t.view(torch.bfloat16) if two else t
 
     def zero_grad(self, set_to_none=True, indices=None):
         """Zero every grad (one fill), or only the listed tensors' grads (one launch);
