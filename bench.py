@@ -48,6 +48,8 @@ BENCH = {
                                max_grad_norm=1.0), decoupled=True, scaler=None, std=1e-3,
                        heavy=0.01),
 }
+# one GPU's shard of GPT-2 124M under ZeRO-1 over 8 GPUs (the per-GPU kernel of the design)
+BENCH["gpt2_124m_shard8"] = BENCH["gpt2_124m"]
 HEADLINE = "fused AdamW step Gparams/s + % of HBM peak, GPT-2 124M mixed precision"
 
 
@@ -144,7 +146,7 @@ def main():
     from ttperf import configs
 
     names, shapes, decay, numels = configs.table(args.config)
-    mode = configs.CONFIGS[args.config]["mode"]
+    mode = configs.mode(args.config)
     n_params = sum(numels)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)

@@ -183,3 +183,25 @@ def test_one_hip_runtime_is_mapped():
     for lib in ("libamdhip64", "libhsa-runtime64"):
         paths = {line.split()[-1] for line in maps if lib in line}
         assert len(paths) == 1, paths
+
+
+def test_shard_tables_partition_the_flat_store():
+    """configs.shard_table: the 8 shards of GPT-2 124M cover every element exactly once, each
+    piece starts and ends on 64-element boundaries of the flat layout (whole state records)
+    unless it ends its tensor, and keeps its tensor's decay flag."""
+    from ttperf import configs
+    names, _, decay, numels = configs.table("gpt2_124m")
+    flags = dict(zip(names, decay))
+    covered = {n: 0 for n in names}
+    for k in range(8):
+        pn, ps, pd, pe = configs.shard_table("gpt2_124m", 8, k)
+        for nm, shape, d, e in zip(pn, ps, pd, pe):
+            base, rng = nm.split("[")
+            a, b = (int(x) for x in rng.rstrip("]").split(":"))
+            assert shape == (e,) and b - a == e and d == flags[base]
+            assert a % 64 == 0
+            assert b % 64 == 0 or b == numels[names.index(base)]
+            covered[base] += e
+    assert covered == dict(zip(names, numels))
+    assert configs.table("gpt2_124m_shard8") == configs.shard_table("gpt2_124m", 8, 7)
+    assert configs.mode("gpt2_124m_shard8") == "mixed"

@@ -431,3 +431,29 @@ def test_update_forms_on_both_sides_of_the_cached_gradient_bound():
             print(f"{label} adamw step {step}: norm {r['grad_norm']:.6f}", flush=True)
         compare_state(store, ref, max_ulp=2)
     store.close()
+
+
+def test_zero1_shard_step_matches_oracle():
+    """One GPU's ZeRO-1 shard of GPT-2 124M (the last of 8: 28 pieces of tensors, 15.6M
+    params) stepped with config 3's mixed AdamW, loss scaling and clipping; against the oracle.
+    With sharding, the norm of each shard would be all-reduced; here the shard is its own
+    store, so the clip uses the shard's norm on both sides."""
+    from ttperf import configs
+    torch = torch_mod()
+    _, shapes, decay, numels = configs.table("gpt2_124m_shard8")
+    store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=90)
+    store.configure_scaler(True, init_scale=65536.0)
+    ref.configure_scaler(True, 65536.0)
+    gen = torch.Generator(device="cuda").manual_seed(91)
+    hp = dict(lr=6e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
+    for step in range(3):
+        host = device_grads(store, gen, 1e-3, scale=ref.scale)
+        ref.grad[:] = host
+        for i in range(ref.n):
+            ref.set_has_grad(i, True)
+        r = store.adam_step(report=True, **hp)
+        e = ref.adam_step(**hp)
+        assert r["skipped"] == e["skipped"] == 0 and r["step"] == e["step"]
+        assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
+    compare_state(store, ref, max_ulp=2)
+    store.close()

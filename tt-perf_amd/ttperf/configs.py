@@ -38,11 +38,47 @@ CONFIGS = {
 }
 
 
+# one GPU's share of a data-parallel, ZeRO-1-sharded step: (configuration, shards, index).
+# The last of 8 GPT-2 124M shards: 28 ragged pieces of the last three blocks and ln_f.
+SHARDS = {"gpt2_124m_shard8": ("gpt2_124m", 8, 7)}
+
+
+def mode(name):
+    """Precision mode of a configuration (a shard has its configuration's)."""
+    return CONFIGS[SHARDS[name][0] if name in SHARDS else name]["mode"]
+
+
 def table(name):
     """(names, shapes, decay flags, numels) of a configuration."""
+    if name in SHARDS:
+        return shard_table(*SHARDS[name])
     entries = CONFIGS[name]["params"]()
     names = [n for n, _ in entries]
     shapes = [s for _, s in entries]
     decay = [len(s) >= 2 for s in shapes]
     numels = [int(math.prod(s)) for s in shapes]
     return names, shapes, decay, numels
+
+
+def shard_table(name, n_shards, k, align=64):
+    """Shard k of n_shards of a configuration's flat store, as a ZeRO-1 optimizer shard would
+    own it: the contiguous element range [k*S, (k+1)*S) of the 64-element-aligned flat layout
+    (S rounded up to a multiple of `align`, so state records stay whole), expressed as a table
+    of 1-D pieces of the tensors it covers, each keeping its tensor's decay flag."""
+    names, _, decay, numels = table(name)
+    offsets, total = [], 0
+    for n in numels:
+        offsets.append(total)
+        total += (n + align - 1) // align * align
+    per = (total + n_shards - 1) // n_shards
+    per = (per + align - 1) // align * align
+    lo, hi = k * per, min(total, (k + 1) * per)
+    out_names, out_shapes, out_decay, out_numels = [], [], [], []
+    for nm, d, o, n in zip(names, decay, offsets, numels):
+        a, b = max(o, lo), min(o + n, hi)
+        if a < b:
+            out_names.append(f"{nm}[{a - o}:{b - o}]")
+            out_shapes.append((b - a,))
+            out_decay.append(d)
+            out_numels.append(b - a)
+    return out_names, out_shapes, out_decay, out_numels
