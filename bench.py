@@ -62,7 +62,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="gpt2_124m")
+    ap.add_argument("--config", default="gpt2_124m", choices=sorted(BENCH),
+                    help="a BASELINE.json configuration (gpt2_124m is the headline metric's), "
+                         "or gpt2_124m_shard8: one GPU's ZeRO-1 shard of it")
     ap.add_argument("--optimizer", default="adamw", choices=["adamw", "sgdm"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
