@@ -7,10 +7,16 @@
 // autograd/dynamic/optim.hpp:24-25 does — all parameters of one arena in one launch.
 // Adam follows py/optim.py:30-92 (same defaults and validation); AdamW adds decoupled
 // weight decay on the decay-flagged parameters.  Loss scaling and clipping are options.
+//
+// Every optimizer counts its own steps (py/optim.py:46,50), while the count the kernels read
+// lives in the arena's store: when a different live optimizer stepped an arena last, its
+// count is saved and this optimizer's restored (a synchronising read and a write, on a change
+// of owner only).  Copies of an optimizer share one count.
 #pragma once
 
 #include <algorithm>
 #include <map>
+#include <memory>
 #include <stdexcept>
 #include <utility>
 #include <vector>
@@ -51,6 +57,26 @@ inline std::vector<Group> group(const std::vector<ValuePtr>& params) {
     return out;
 }
 
+// Make the arena's step count `me`'s before `me` steps it.  An arena that no live optimizer
+// stepped last keeps its count (a loaded checkpoint's, say); one that another live optimizer
+// stepped last has that count saved for it, and `me`'s restored (0 if `me` never stepped it).
+inline void claim(ArenaState& a, const std::shared_ptr<StepCounts>& me) {
+    std::shared_ptr<StepCounts> prev = a.t_owner.lock();
+    if (prev == me) return;
+    auto it = me->saved.find(&a);
+    if (prev || it != me->saved.end()) {
+        ttp::Store& s = a.get();
+        if (prev) prev->saved[&a] = s.step_count();
+        uint64_t t = 0;
+        if (it != me->saved.end()) {
+            t = it->second;
+            me->saved.erase(it);
+        }
+        s.set_step_count(t);
+    }
+    a.t_owner = me;
+}
+
 inline void zero_grad(const std::vector<ValuePtr>& params) {
     for (auto& g : group(params)) {
         if (g.whole) {
@@ -67,6 +93,7 @@ struct SGD {
     std::vector<ValuePtr> params;
     float lr;
     ttp::SgdOptions opts;
+    std::shared_ptr<StepCounts> counts = std::make_shared<StepCounts>();
 
     SGD(std::vector<ValuePtr> params_, float lr_, float momentum = 0.0f, float dampening = 0.0f,
         float weight_decay = 0.0f, bool nesterov = false)
@@ -80,8 +107,10 @@ struct SGD {
 
     void step() {
         opts.lr = lr;
-        for (auto& g : detail::group(params))
+        for (auto& g : detail::group(params)) {
+            detail::claim(*g.arena, counts);
             g.arena->get().sgd_step(opts, g.whole ? nullptr : &g.indices);
+        }
     }
 
     void zero_grad() { detail::zero_grad(params); }
@@ -90,6 +119,7 @@ struct SGD {
 struct Adam {
     std::vector<ValuePtr> params;
     ttp::AdamOptions opts;
+    std::shared_ptr<StepCounts> counts = std::make_shared<StepCounts>();
 
     explicit Adam(std::vector<ValuePtr> params_, float lr = 1e-3f,
                   std::pair<double, double> betas = {0.9, 0.999}, float eps = 1e-8f,
@@ -112,8 +142,10 @@ struct Adam {
 
     ttp_step_report step(bool want_report = false) {
         ttp_step_report last{};
-        for (auto& g : detail::group(params))
+        for (auto& g : detail::group(params)) {
+            detail::claim(*g.arena, counts);
             last = g.arena->get().adam_step(opts, g.whole ? nullptr : &g.indices, want_report);
+        }
         return last;
     }
 

@@ -223,6 +223,7 @@ public:
         check(ttp_get_step(ctx_, &t));
         return t;
     }
+    void set_step_count(uint64_t t) { check(ttp_set_step(ctx_, t)); }
     void sync() { check(ttp_sync(ctx_)); }
     void save_state(const std::string& path) { check(ttp_save_state(ctx_, path.c_str())); }
     void load_state(const std::string& path) { check(ttp_load_state(ctx_, path.c_str())); }

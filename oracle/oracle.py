@@ -231,6 +231,10 @@ class OracleStore:
     def t(self):
         return int(self.s.t)
 
+    @t.setter
+    def t(self, v):
+        self.s.t = int(v)
+
     @property
     def scale(self):
         return float(self.s.scale)

@@ -86,10 +86,57 @@ static void run(bool decoupled) {
     delete opt;
 }
 
+// Two optimizers over two parameter groups of one arena, stepped in an uneven order: each
+// group's bias corrections use its own optimizer's step count (py/optim.py:46,50 keeps `_step`
+// per optimizer), and the arena's count reads as the last stepper's.
+static void run_groups() {
+    ParamArena arena(ttp::Mode::FP32);
+    MLP model(64, 128, 10, arena);
+    auto params = model.parameters();
+    std::vector<Ref> ref;
+    for (auto& p : params) {
+        Ref r;
+        r.p = p->master();
+        r.m.assign(p->numel(), 0.0f);
+        r.v.assign(p->numel(), 0.0f);
+        ref.push_back(r);
+    }
+    const std::vector<size_t> ga = {0, 1}, gb = {2, 3};
+    AdamW a({params[0], params[1]}, 1e-2f, {0.9, 0.95}, 1e-8f, 0.1f);
+    Adam b({params[2], params[3]}, 3e-3f, {0.8, 0.999}, 1e-6f);
+    uint64_t ta = 0, tb = 0;
+    const char* order = "abbaab";
+    for (int k = 0; order[k]; ++k) {
+        const bool is_a = order[k] == 'a';
+        const auto& members = is_a ? ga : gb;
+        const uint64_t t = is_a ? ++ta : ++tb;
+        for (size_t j : members) {
+            auto g = grad_of(params[j]->numel(), 100 + k * 10 + (int)j);
+            params[j]->grad = g;
+            if (is_a)
+                adam_ref(ref[j], g, (double)1e-2f, 0.9, 0.95, (double)1e-8f, t, (double)0.1f,
+                         j == 0);
+            else
+                adam_ref(ref[j], g, (double)3e-3f, 0.8, 0.999, (double)1e-6f, t, 0.0, false);
+        }
+        if (is_a) a.step(); else b.step();
+        test::check(params[0]->store().step_count() == t,
+                    "groups: the arena holds the count of the optimizer that stepped last");
+    }
+    for (size_t k = 0; k < params.size(); ++k) {
+        test::assert_bits(params[k]->master(), ref[k].p, "groups param " + std::to_string(k));
+        test::assert_bits(params[k]->store().state(TTP_BUF_EXP_AVG, params[k]->index), ref[k].m,
+                          "groups exp_avg " + std::to_string(k));
+        test::assert_bits(params[k]->store().state(TTP_BUF_EXP_AVG_SQ, params[k]->index),
+                          ref[k].v, "groups exp_avg_sq " + std::to_string(k));
+    }
+}
+
 int main() {
     test::DeviceGuard dg;
     run(false);
     run(true);
+    run_groups();
     // py/optim.py:33-41 validation
     ParamArena arena;
     Linear l(4, 4, arena);

@@ -151,6 +151,79 @@ def test_non_tensor_params_raise_at_step_and_are_skipped_by_zero_grad():
             opt.step()
 
 
+class _CountingStore:
+    """Stands in for a ParamStore: a step count that every step advances, and a count of the
+    synchronising reads and writes of it."""
+
+    def __init__(self, n):
+        import ttperf
+        self._t = 0
+        self.reads = self.writes = 0
+        self._t_owner = None
+        self._in_capture = False
+        self.tensors = [ttperf.Tensor(self, i, (4,)) for i in range(n)]
+        self.log = []
+
+    @property
+    def step_count(self):
+        self.reads += 1
+        return self._t
+
+    @step_count.setter
+    def step_count(self, t):
+        self.writes += 1
+        self._t = t
+
+    def adam_step(self, lr, betas, eps, weight_decay, decoupled, max_grad_norm, indices=None):
+        self._t += 1
+        self.log.append((lr, self._t))
+
+    def sgd_step(self, lr, momentum, dampening, weight_decay, nesterov, max_grad_norm,
+                 indices=None):
+        self._t += 1
+        self.log.append((lr, self._t))
+
+
+def test_each_optimizer_keeps_its_own_step_count():
+    """py/optim.py:46,50: `_step` belongs to the optimizer.  Two optimizers over two groups
+    of one store each see their own count; one optimizer alone never reads the device."""
+    import gc
+    import ttperf
+    s = _CountingStore(4)
+    a = ttperf.Adam(s.tensors[:2], lr=1.0)
+    b = ttperf.Adam(s.tensors[2:], lr=2.0)
+    for opt in (a, a, a):
+        opt.step()
+    assert (s.reads, s.writes) == (0, 0)
+    for opt in (b, a, b, b, a):
+        opt.step()
+    assert [t for _, t in s.log] == [1, 2, 3, 1, 4, 2, 3, 5]
+    assert [lr for lr, _ in s.log] == [1.0] * 3 + [2.0, 1.0, 2.0, 2.0, 1.0]
+    assert s.step_count == 5  # the count of the optimizer that stepped last
+    # an SGD over a third group hands the count over too, so Adam's bias corrections hold
+    c = ttperf.SGD(s.tensors[1:2], lr=3.0)
+    c.step()
+    b.step()
+    a.step()
+    assert s.log[-3:] == [(3.0, 1), (2.0, 4), (1.0, 6)]
+    # a store whose last optimizer is gone keeps its count for the next one (a checkpoint's)
+    del a, c, opt
+    gc.collect()
+    s._t = 41
+    s.log.clear()
+    d = ttperf.AdamW(s.tensors[:2], lr=4.0)
+    d.step()
+    assert s.log == [(4.0, 42)]
+    b.step()
+    assert s.log[-1] == (2.0, 5)
+    # a hand-over reads the device, which a graph capture cannot hold
+    s._in_capture = True
+    with pytest.raises(RuntimeError, match="capture"):
+        d.step()
+    b.step()  # no hand-over: fine while capturing
+    assert s.log[-1] == (2.0, 6)
+
+
 def test_cpp_dropin_headers_compile():
     """The C++ drop-in tests (tests/cpp) build against include/ and the library."""
     subprocess.run(["make", "-s", "-C", os.path.join(REPO, "tests", "cpp")], check=True)

@@ -457,3 +457,36 @@ def test_zero1_shard_step_matches_oracle():
         assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
     compare_state(store, ref, max_ulp=2)
     store.close()
+
+
+def test_two_adam_parameter_groups_keep_their_own_step_counts():
+    """Two optimizers over two parameter groups of one store, stepped in an uneven order:
+    each group's bias corrections use its own optimizer's step count, as two py/optim.py Adam
+    instances (:46,50, `_step` per optimizer) would.  The oracle steps one group at a time with
+    that group's count; the moments of the other group stay untouched."""
+    import ttperf
+    torch = torch_mod()
+    shapes = [(64, 48), (48,), (48, 32), (32,), (300,)]
+    decay = [True, False, True, False, False]
+    store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=95)
+    groups = {"a": [0, 1, 4], "b": [2, 3]}
+    hps = {"a": dict(lr=3e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1),
+           "b": dict(lr=1e-2, betas=(0.8, 0.999), eps=1e-6, weight_decay=0.0)}
+    opts = {"a": ttperf.AdamW([store.tensors[i] for i in groups["a"]], **hps["a"]),
+            "b": ttperf.Adam([store.tensors[i] for i in groups["b"]],
+                             **{k: v for k, v in hps["b"].items() if k != "weight_decay"})}
+    counts = {"a": 0, "b": 0}
+    gen = torch.Generator(device="cuda").manual_seed(96)
+    for k, g in enumerate("aabbbaba"):
+        ref.grad[:store.total] = device_grads(store, gen, 1e-2)
+        for i in range(ref.n):
+            ref.set_has_grad(i, i in groups[g])
+        opts[g].step()
+        ref.t = counts[g]
+        ref.adam_step(decoupled=(g == "a"), **hps[g])
+        counts[g] = ref.t
+        print(f"step {k}: group {g}, its count {counts[g]}", flush=True)
+        assert store.step_count == counts[g]
+    assert counts == {"a": 4, "b": 4}
+    compare_state(store, ref, max_ulp=0)
+    store.close()

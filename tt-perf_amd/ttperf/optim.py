@@ -9,10 +9,18 @@ Adam  — py/optim.py:30-92 (`Adam(params, *, lr=1e-3, betas=(0.9, 0.999), eps=1
 AdamW — Adam with decoupled weight decay (p *= 1 - lr*wd before the update), applied only
         to the store's decay-flagged tensors.
 
+Each optimizer counts its own steps, as py/optim.py:46,50 keeps `_step` per Adam, although
+the count the kernels read lives in the store: when a different live optimizer stepped a
+store last, its count is saved and this optimizer's restored (one synchronising read and
+one write, on a change of owner only), so two optimizers over two parameter groups of one
+store see the bias corrections of their own step counts.
+
 Every step is one libttperf_hip call per store: one multi-tensor launch (plus the norm pass
 when clipping or loss scaling), instead of ~15 elementwise programs per tensor.
 """
 from __future__ import annotations
+
+import weakref
 
 from .store import Tensor
 
@@ -31,9 +39,30 @@ class _Optimizer:
 
     def __init__(self, params):
         self.params = list(params)
+        self._saved_t = weakref.WeakKeyDictionary()  # store -> this optimizer's step count
 
     def _stores(self):
         return _group_by_store(self.params, self._name)
+
+    def _claim(self, store):
+        """Make the store's step count this optimizer's before it steps the store.
+
+        A store that no live optimizer stepped last keeps its count (a loaded checkpoint's,
+        say) for the optimizer that steps it next; one that a different live optimizer
+        stepped last has that optimizer's count saved, and this optimizer's restored (0 if
+        it never stepped the store)."""
+        prev = store._t_owner() if store._t_owner is not None else None
+        if prev is self:
+            return
+        if prev is not None or store in self._saved_t:
+            if store._in_capture:
+                raise RuntimeError(
+                    "a second optimizer steps this store inside a graph capture; the step "
+                    "count hand-over reads the device and cannot be captured")
+            if prev is not None:
+                prev._saved_t[store] = store.step_count
+            store.step_count = self._saved_t.pop(store, 0)
+        store._t_owner = weakref.ref(self)
 
     def zero_grad(self):
         # py/optim.py:89-92 -> Tensor.zero_grad (py/engine.py:141-142): grad = None, and
@@ -49,6 +78,7 @@ class _Optimizer:
 
     def step(self):
         for store, members in self._stores():
+            self._claim(store)
             whole = len(members) == len(store.tensors)
             self._step_store(store, None if whole else sorted({p.index for p in members}))
 

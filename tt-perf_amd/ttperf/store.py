@@ -233,6 +233,7 @@ class ParamStore:
         self.total = tot.value
         self._graphs = weakref.WeakSet()
         self._in_capture = False
+        self._t_owner = None  # weakref to the optimizer whose step count the store holds
 
     # ---- lifetime --------------------------------------------------------------------------
     def close(self):
