@@ -234,6 +234,10 @@ int ttp_grad_norm(ttp_ctx* ctx, double* norm);
 /* ---- step counter and loss scaler ------------------------------------------------------- */
 int ttp_get_step(ttp_ctx* ctx, uint64_t* step);
 int ttp_set_step(ttp_ctx* ctx, uint64_t step);
+/* ttp_scaler_configure also resets the scale to init_scale and the tracker to 0.  Captured
+ * graphs hold `enabled` and the growth / backoff settings as launch arguments: while graphs
+ * of the context are alive, a configuration that changes them fails with TTP_ERR_STATE (the
+ * same settings, to reset the scale, are accepted). */
 int ttp_scaler_configure(ttp_ctx* ctx, const ttp_scaler_config* cfg);
 int ttp_scaler_get(ttp_ctx* ctx, float* scale, int32_t* growth_tracker);
 int ttp_scaler_set(ttp_ctx* ctx, float scale, int32_t growth_tracker);
@@ -250,10 +254,15 @@ int ttp_scaler_set(ttp_ctx* ctx, float scale, int32_t growth_tracker);
  * f64 growth_factor, f64 backoff_factor; n_tensors x {u64 numel, u32 flags, u32 momentum
  * initialised}; each present buffer as total fp32 values (padding included); u64 checksum
  * of all preceding bytes.  Both calls are synchronous and stream through a 64 MiB pinned
- * buffer.  ttp_load_state requires the same mode and tensor table (numel and flags); a
- * buffer the file lacks is zeroed; the bf16 weights are recomputed from the master.  If it
- * fails after the header checks (read error, checksum mismatch), the context's optimizer
- * state is undefined until a load succeeds. */
+ * buffer.  ttp_save_state writes `path`.tmp and renames it over `path` when complete, so a
+ * failed save leaves an earlier file at `path` as it was.  ttp_load_state requires the same
+ * mode and tensor table (numel and flags); a buffer the file lacks is zeroed; the bf16
+ * weights are recomputed from the master.  It reads the whole file and checks its size and
+ * checksum before it changes the context, so a damaged, truncated or mismatched file is
+ * rejected with the context unchanged (only an I/O error on the second read, or a file
+ * replaced during the call, can leave it partly loaded).  While graphs of the context are
+ * alive, a file whose loss-scaler settings differ from the context's is refused
+ * (TTP_ERR_STATE), as ttp_scaler_configure refuses them. */
 int ttp_save_state(ttp_ctx* ctx, const char* path);
 int ttp_load_state(ttp_ctx* ctx, const char* path);
 

@@ -110,10 +110,18 @@ def test_load_rejects_mismatch_and_corruption(tmp_path):
     raw = path.read_bytes()
     master = a.download(L.BUF_MASTER).view(np.uint32).copy()
 
+    def snapshot(store):
+        bufs = [L.BUF_MASTER, L.BUF_PARAM, L.BUF_EXP_AVG, L.BUF_EXP_AVG_SQ]
+        return ([store.download(b).tobytes() for b in bufs], store.step_count,
+                store.scaler_state())
+
     def expect_invalid(store, p, what):
+        before = snapshot(store)
         with pytest.raises(ttperf.TTPValueError) as e:
             store.load_state(p)
         assert what in str(e.value), str(e.value)
+        # the whole file is checked before the store is touched
+        assert snapshot(store) == before, f"a rejected load ({what}) changed the store"
 
     expect_invalid(ttperf.ParamStore([(100,), (64, 9)], mode="mixed"), path, "tensor")
     expect_invalid(ttperf.ParamStore([(100,), (64, 8)], mode="fp32"), path, "mode")
@@ -123,11 +131,24 @@ def test_load_rejects_mismatch_and_corruption(tmp_path):
     bad[len(bad) // 2] ^= 0x40
     (tmp_path / "bad.bin").write_bytes(bytes(bad))
     expect_invalid(a, tmp_path / "bad.bin", "checksum")
+    bad = bytearray(raw)
+    bad[-9] ^= 0x01  # the last data byte, read after every buffer before it
+    (tmp_path / "bad_end.bin").write_bytes(bytes(bad))
+    expect_invalid(a, tmp_path / "bad_end.bin", "checksum")
     (tmp_path / "short.bin").write_bytes(raw[:-100])
     expect_invalid(a, tmp_path / "short.bin", "truncated")
+    (tmp_path / "long.bin").write_bytes(raw + b"\0" * 8)
+    expect_invalid(a, tmp_path / "long.bin", "trailing")
     (tmp_path / "junk.bin").write_bytes(b"not a state file at all" * 4)
     expect_invalid(a, tmp_path / "junk.bin", "not an optimizer-state file")
     expect_invalid(a, tmp_path / "missing.bin", "cannot open")
+    # a save goes through path.tmp: none is left behind, and a failed rename removes it
+    assert not (tmp_path / "s.bin.tmp").exists()
+    (tmp_path / "adir").mkdir()
+    with pytest.raises(ttperf.TTPValueError) as e:
+        a.save_state(tmp_path / "adir")
+    assert "rename" in str(e.value)
+    assert not (tmp_path / "adir.tmp").exists() and (tmp_path / "adir").is_dir()
     # a good load after the failures restores a consistent state
     fresh = ttperf.ParamStore([(100,), (64, 8)], mode="mixed")
     fresh.load_state(path)

@@ -144,7 +144,7 @@ def test_captured_train_step_zero_accumulate_sgd_momentum():
     store.close()
 
 
-def test_capture_rejects_what_cannot_be_captured():
+def test_capture_rejects_what_cannot_be_captured(tmp_path):
     import ttperf
     from ttperf import _lib as L
     store = ttperf.ParamStore([(100,), (64, 8)], mode="mixed")
@@ -173,9 +173,26 @@ def test_capture_rejects_what_cannot_be_captured():
     store.adam_step(lr=1e-3)
     g = store.end_capture()
     assert L.lib.ttp_destroy(store.handle) == L.ERR_STATE
+    # the graph holds the loss-scaler settings (here: off): changing them is refused, also
+    # through a state file, and leaves the store as it was; the same settings are accepted
+    with pytest.raises(ttperf.TTPError) as e:
+        store.configure_scaler(True)
+    assert e.value.code == L.ERR_STATE
+    store.configure_scaler(False)
+    other = ttperf.ParamStore([(100,), (64, 8)], mode="mixed")
+    other.configure_scaler(True, init_scale=1024.0)
+    other.save_state(tmp_path / "scaled.bin")
+    other.close()
+    master = store.download(L.BUF_MASTER).tobytes()
+    with pytest.raises(ttperf.TTPError) as e:
+        store.load_state(tmp_path / "scaled.bin")
+    assert e.value.code == L.ERR_STATE
+    assert store.download(L.BUF_MASTER).tobytes() == master
     g.replay()
     assert store.step_count == 3
     g.close()
+    store.configure_scaler(True)  # no graph holds the settings any more
+    store.configure_scaler(False)
     # the legacy default stream cannot be captured
     store.set_stream(0)
     with pytest.raises(ttperf.TTPError) as e:

@@ -419,6 +419,15 @@ int launch_prologue(ttp_ctx* c, const WorkTables* w, bool run_norm, double max_n
     return TTP_OK;
 }
 
+// Whether two scaler configurations step alike: a captured graph holds `enabled` and the
+// growth / backoff settings as launch arguments (the scale and tracker live on the device).
+bool same_scaler_settings(const ttp_scaler_config& a, const ttp_scaler_config& b) {
+    if ((a.enabled != 0) != (b.enabled != 0)) return false;
+    return !a.enabled || (a.growth_interval == b.growth_interval &&
+                          a.growth_factor == b.growth_factor &&
+                          a.backoff_factor == b.backoff_factor);
+}
+
 int read_state(ttp_ctx* c, DevState* out) {
     HIP_TRY(hipMemcpyAsync(out, c->st, sizeof(DevState), hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));
@@ -1252,6 +1261,9 @@ int ttp_scaler_configure(ttp_ctx* c, const ttp_scaler_config* cfg) {
         if (cfg->growth_interval <= 0) return fail(TTP_ERR_INVALID, "growth_interval must be > 0");
     }
     if ((rc = no_capture(c, "ttp_scaler_configure"))) return rc;
+    if (c->n_graphs && !same_scaler_settings(c->scaler, *cfg))
+        return fail(TTP_ERR_STATE, "the loss-scaler settings are part of this context's captured "
+                                   "graphs; destroy them before changing the settings");
     if ((rc = set_dev(c))) return rc;
     HIP_TRY(hipStreamSynchronize(c->stream));
     DevState s;
@@ -1397,9 +1409,20 @@ int ttp_save_state(ttp_ctx* c, const char* path) {
     h.growth_factor = c->scaler.growth_factor;
     h.backoff_factor = c->scaler.backoff_factor;
 
+    // written to `path`.tmp and renamed over `path` once complete, so a failed save leaves an
+    // earlier file at `path` intact
+    const std::string tmp = std::string(path) + ".tmp";
     File f;
-    f.f = std::fopen(path, "wb");
-    if (!f.f) return fail(TTP_ERR_INVALID, std::string("cannot open ") + path + " for writing");
+    f.f = std::fopen(tmp.c_str(), "wb");
+    if (!f.f) return fail(TTP_ERR_INVALID, "cannot open " + tmp + " for writing");
+    bool done = false;
+    struct Cleanup {
+        const std::string& p;
+        const bool& done;
+        ~Cleanup() {
+            if (!done) (void)std::remove(p.c_str());
+        }
+    } cleanup{tmp, done};
     Hash hash;
     auto put = [&](const void* p, size_t n) {
         hash.add(p, n);
@@ -1430,7 +1453,12 @@ int ttp_save_state(ttp_ctx* c, const char* path) {
     const uint64_t sum = hash.value();
     ok = ok && std::fwrite(&sum, 1, 8, f.f) == 8;
     ok = ok && std::fflush(f.f) == 0;
-    if (!ok) return fail(TTP_ERR_INVALID, std::string("write to ") + path + " failed");
+    const int closed = std::fclose(f.f);
+    f.f = nullptr;
+    if (!ok || closed != 0) return fail(TTP_ERR_INVALID, "write to " + tmp + " failed");
+    if (std::rename(tmp.c_str(), path) != 0)
+        return fail(TTP_ERR_INVALID, "cannot rename " + tmp + " to " + path);
+    done = true;
     return TTP_OK;
 }
 
@@ -1473,12 +1501,43 @@ int ttp_load_state(ttp_ctx* c, const char* path) {
     }
     if (h.total != c->total)  // the layout follows from the table; this catches a bad header
         return fail(TTP_ERR_INVALID, "state file flat size differs from the context's");
+    ttp_scaler_config file_scaler{h.scaler_enabled, h.growth_interval, h.init_scale,
+                                  h.growth_factor, h.backoff_factor};
+    if (c->n_graphs && !same_scaler_settings(c->scaler, file_scaler))
+        return fail(TTP_ERR_STATE, "the state file's loss-scaler settings differ from those in "
+                                   "this context's captured graphs; destroy them first");
+    // The whole file is checked before the context is touched: its size, then its checksum
+    // over every byte, so a damaged file leaves the context as it was.
+    const int64_t data_pos = ftello(f.f);
+    uint64_t nbuf = 0;
+    for (int bit = 1; bit <= 8; bit <<= 1) nbuf += (h.buffers & (uint32_t)bit) ? 1 : 0;
+    const uint64_t data_bytes = nbuf * c->total * 4;
+    if (data_pos < 0 || fseeko(f.f, 0, SEEK_END) != 0)
+        return fail(TTP_ERR_INVALID, std::string("cannot seek in ") + path);
+    const int64_t end = ftello(f.f);
+    if (end < data_pos || (uint64_t)(end - data_pos) < data_bytes + 8)
+        return fail(TTP_ERR_INVALID, "state file is truncated");
+    if ((uint64_t)(end - data_pos) > data_bytes + 8)
+        return fail(TTP_ERR_INVALID, "state file has trailing bytes");
+    if (fseeko(f.f, data_pos, SEEK_SET) != 0)
+        return fail(TTP_ERR_INVALID, std::string("cannot seek in ") + path);
+    Pinned stage;
+    HIP_TRY(hipHostMalloc(&stage.p, kStageBytes));
+    for (uint64_t o = 0; o < data_bytes; o += kStageBytes) {
+        const uint64_t n = std::min<uint64_t>(kStageBytes, data_bytes - o);
+        if (!get(stage.p, n)) return fail(TTP_ERR_INVALID, "state file is truncated");
+    }
+    const uint64_t want = hash.value();
+    uint64_t sum = 0;
+    if (std::fread(&sum, 1, 8, f.f) != 8) return fail(TTP_ERR_INVALID, "state file is truncated");
+    if (sum != want) return fail(TTP_ERR_INVALID, "state file checksum mismatch");
+    if (fseeko(f.f, data_pos, SEEK_SET) != 0)
+        return fail(TTP_ERR_INVALID, std::string("cannot seek in ") + path);
+
     // allocate what the file holds; zero what the context holds and the file does not
     if ((h.buffers & 6u) && (rc = ensure_adam_state(c))) return rc;
     if ((h.buffers & 8u) && (rc = ensure_momentum(c))) return rc;
     HIP_TRY(hipStreamSynchronize(c->stream));
-    Pinned stage;
-    HIP_TRY(hipHostMalloc(&stage.p, kStageBytes));
     if ((rc = ensure_staging(c, kStageBytes))) return rc;
     const uint64_t piece = kStageBytes / 4;
     for (int bit = 1; bit <= 8; bit <<= 1) {
@@ -1492,16 +1551,16 @@ int ttp_load_state(ttp_ctx* c, const char* path) {
         // the master scatter also rewrites the MIXED-mode bf16 copy as RNE(master)
         for (uint64_t o = 0; o < c->total; o += piece) {
             const uint64_t n = std::min(piece, c->total - o);
-            if (!get(stage.p, n * 4)) return fail(TTP_ERR_INVALID, "state file is truncated");
+            // the file was read whole above; a failure here is an I/O error or a file that
+            // changed since, and leaves the context partly loaded
+            if (std::fread(stage.p, 1, n * 4, f.f) != n * 4)
+                return fail(TTP_ERR_INVALID, std::string("read from ") + path +
+                                                 " failed after its checksum was verified");
             HIP_TRY(hipMemcpyAsync(c->staging, stage.p, n * 4, hipMemcpyHostToDevice, c->stream));
             if ((rc = scatter_slot(c, which, o, n, (const float*)c->staging))) return rc;
             HIP_TRY(hipStreamSynchronize(c->stream));  // stage.p is refilled next
         }
     }
-    const uint64_t want = hash.value();
-    uint64_t sum = 0;
-    if (std::fread(&sum, 1, 8, f.f) != 8) return fail(TTP_ERR_INVALID, "state file is truncated");
-    if (sum != want) return fail(TTP_ERR_INVALID, "state file checksum mismatch");
     HIP_TRY(hipMemcpyAsync(c->mom_init, mom.data(), mom.size() * 4, hipMemcpyHostToDevice,
                            c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));
