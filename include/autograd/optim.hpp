@@ -10,8 +10,9 @@
 //
 // Every optimizer counts its own steps (py/optim.py:46,50), while the count the kernels read
 // lives in the arena's store: when a different live optimizer stepped an arena last, its
-// count is saved and this optimizer's restored (a synchronising read and a write, on a change
-// of owner only).  Copies of an optimizer share one count.
+// count is saved and this optimizer's restored (ttp::Store::claim_step_count: a synchronising
+// read and a write, on a change of owner only; a graph hands the count back to the optimizer
+// that held it at capture before each launch).  Copies of an optimizer share one count.
 #pragma once
 
 #include <algorithm>
@@ -57,26 +58,6 @@ inline std::vector<Group> group(const std::vector<ValuePtr>& params) {
     return out;
 }
 
-// Make the arena's step count `me`'s before `me` steps it.  An arena that no live optimizer
-// stepped last keeps its count (a loaded checkpoint's, say); one that another live optimizer
-// stepped last has that count saved for it, and `me`'s restored (0 if `me` never stepped it).
-inline void claim(ArenaState& a, const std::shared_ptr<StepCounts>& me) {
-    std::shared_ptr<StepCounts> prev = a.t_owner.lock();
-    if (prev == me) return;
-    auto it = me->saved.find(&a);
-    if (prev || it != me->saved.end()) {
-        ttp::Store& s = a.get();
-        if (prev) prev->saved[&a] = s.step_count();
-        uint64_t t = 0;
-        if (it != me->saved.end()) {
-            t = it->second;
-            me->saved.erase(it);
-        }
-        s.set_step_count(t);
-    }
-    a.t_owner = me;
-}
-
 inline void zero_grad(const std::vector<ValuePtr>& params) {
     for (auto& g : group(params)) {
         if (g.whole) {
@@ -93,7 +74,7 @@ struct SGD {
     std::vector<ValuePtr> params;
     float lr;
     ttp::SgdOptions opts;
-    std::shared_ptr<StepCounts> counts = std::make_shared<StepCounts>();
+    std::shared_ptr<ttp::StepCounts> counts = std::make_shared<ttp::StepCounts>();
 
     SGD(std::vector<ValuePtr> params_, float lr_, float momentum = 0.0f, float dampening = 0.0f,
         float weight_decay = 0.0f, bool nesterov = false)
@@ -108,7 +89,7 @@ struct SGD {
     void step() {
         opts.lr = lr;
         for (auto& g : detail::group(params)) {
-            detail::claim(*g.arena, counts);
+            g.arena->get().claim_step_count(counts);
             g.arena->get().sgd_step(opts, g.whole ? nullptr : &g.indices);
         }
     }
@@ -119,7 +100,7 @@ struct SGD {
 struct Adam {
     std::vector<ValuePtr> params;
     ttp::AdamOptions opts;
-    std::shared_ptr<StepCounts> counts = std::make_shared<StepCounts>();
+    std::shared_ptr<ttp::StepCounts> counts = std::make_shared<ttp::StepCounts>();
 
     explicit Adam(std::vector<ValuePtr> params_, float lr = 1e-3f,
                   std::pair<double, double> betas = {0.9, 0.999}, float eps = 1e-8f,
@@ -143,7 +124,7 @@ struct Adam {
     ttp_step_report step(bool want_report = false) {
         ttp_step_report last{};
         for (auto& g : detail::group(params)) {
-            detail::claim(*g.arena, counts);
+            g.arena->get().claim_step_count(counts);
             last = g.arena->get().adam_step(opts, g.whole ? nullptr : &g.indices, want_report);
         }
         return last;

@@ -9,7 +9,6 @@
 #pragma once
 
 #include <cstdint>
-#include <map>
 #include <memory>
 #include <optional>
 #include <stdexcept>
@@ -21,13 +20,6 @@
 namespace autograd {
 
 class ParamArena;
-struct ArenaState;
-
-// The step counts an optimizer keeps for the arenas it stepped while another optimizer held
-// the arena's count (py/optim.py:46,50 keeps `_step` per optimizer).
-struct StepCounts {
-    std::map<const ArenaState*, uint64_t> saved;
-};
 
 struct ArenaState {
     ttp::Mode mode = ttp::Mode::FP32;
@@ -36,7 +28,6 @@ struct ArenaState {
     std::vector<std::vector<float>> init;  // initial fp32 weights (uploaded at creation)
     std::vector<bool> grad_always;         // pre-allocated grads (traced/static layers)
     std::unique_ptr<ttp::Store> store;
-    std::weak_ptr<StepCounts> t_owner;     // the optimizer whose step count the store holds
 
     ttp::Store& get() {
         if (!store) {

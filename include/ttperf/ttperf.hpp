@@ -9,6 +9,7 @@
 
 #include <cstdint>
 #include <cstring>
+#include <map>
 #include <memory>
 #include <stdexcept>
 #include <string>
@@ -73,16 +74,33 @@ struct SgdOptions {
     }
 };
 
-// A captured graph of a store's work (ttp_capture_begin .. ttp_capture_end); move-only.
+class Store;
+
+// The step counts an optimizer keeps for the stores whose count another optimizer held when
+// it last stepped them.  py/optim.py:46,50 keeps `_step` per optimizer; the count the
+// kernels read lives in the store, so optimizers hand it over (Store::claim_step_count).
+struct StepCounts {
+    std::map<const Store*, uint64_t> saved;
+};
+
+// A captured graph of a store's work (ttp_capture_begin .. ttp_capture_end); move-only.  It
+// remembers which optimizer held the store's step count at capture, and hands the count back
+// to it before each launch (a no-op unless another optimizer stepped the store since).
 class Graph {
 public:
     Graph() = default;
     explicit Graph(ttp_graph* g) : g_(g) {}
-    Graph(Graph&& o) noexcept : g_(o.g_) { o.g_ = nullptr; }
+    Graph(ttp_graph* g, Store* store, std::weak_ptr<StepCounts> owner)
+        : g_(g), store_(store), owner_(std::move(owner)) {}
+    Graph(Graph&& o) noexcept : g_(o.g_), store_(o.store_), owner_(std::move(o.owner_)) {
+        o.g_ = nullptr;
+    }
     Graph& operator=(Graph&& o) noexcept {
         if (this != &o) {
             reset();
             g_ = o.g_;
+            store_ = o.store_;
+            owner_ = std::move(o.owner_);
             o.g_ = nullptr;
         }
         return *this;
@@ -90,7 +108,7 @@ public:
     Graph(const Graph&) = delete;
     Graph& operator=(const Graph&) = delete;
     ~Graph() { reset(); }
-    void launch() { check(ttp_graph_launch(g_)); }
+    inline void launch();
     void reset() {
         if (g_) ttp_graph_destroy(g_);
         g_ = nullptr;
@@ -99,6 +117,8 @@ public:
 
 private:
     ttp_graph* g_ = nullptr;
+    Store* store_ = nullptr;
+    std::weak_ptr<StepCounts> owner_;
 };
 
 class Store {
@@ -227,13 +247,45 @@ public:
     void sync() { check(ttp_sync(ctx_)); }
     void save_state(const std::string& path) { check(ttp_save_state(ctx_, path.c_str())); }
     void load_state(const std::string& path) { check(ttp_load_state(ctx_, path.c_str())); }
-    void begin_capture() { check(ttp_capture_begin(ctx_)); }
+    void begin_capture() {
+        check(ttp_capture_begin(ctx_));
+        capturing_ = true;
+    }
     Graph end_capture() {
+        capturing_ = false;
         ttp_graph* g = nullptr;
         check(ttp_capture_end(ctx_, &g));
-        return Graph(g);
+        return Graph(g, this, t_owner_);
     }
-    void discard_capture() { (void)ttp_capture_end(ctx_, nullptr); }
+    void discard_capture() {
+        capturing_ = false;
+        (void)ttp_capture_end(ctx_, nullptr);
+    }
+
+    // Make the step count `me`'s before the optimizer `me` steps this store.  A store that no
+    // live optimizer stepped last keeps its count (a loaded checkpoint's, say); one that a
+    // different live optimizer stepped last has that count saved for it and `me`'s restored
+    // (0 if `me` never stepped the store): a synchronising read and a write, on a change of
+    // owner only, which a graph capture cannot hold.
+    void claim_step_count(const std::shared_ptr<StepCounts>& me) {
+        std::shared_ptr<StepCounts> prev = t_owner_.lock();
+        if (prev == me) return;
+        auto it = me->saved.find(this);
+        if (prev || it != me->saved.end()) {
+            if (capturing_)
+                throw std::runtime_error(
+                    "libttperf_hip: a second optimizer steps this store inside a graph capture; "
+                    "the step count hand-over reads the device and cannot be captured");
+            if (prev) prev->saved[this] = step_count();
+            uint64_t t = 0;
+            if (it != me->saved.end()) {
+                t = it->second;
+                me->saved.erase(it);
+            }
+            set_step_count(t);
+        }
+        t_owner_ = me;
+    }
 
     static uint16_t to_bf16(float x) {
         uint32_t u;
@@ -266,6 +318,14 @@ private:
     std::vector<TensorSpec> specs_;
     Mode mode_;
     ttp_ctx* ctx_ = nullptr;
+    bool capturing_ = false;
+    std::weak_ptr<StepCounts> t_owner_;  // the optimizer whose step count the store holds
 };
+
+inline void Graph::launch() {
+    if (store_)
+        if (std::shared_ptr<StepCounts> o = owner_.lock()) store_->claim_step_count(o);
+    check(ttp_graph_launch(g_));
+}
 
 }  // namespace ttp

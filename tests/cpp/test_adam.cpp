@@ -132,11 +132,68 @@ static void run_groups() {
     }
 }
 
+// A graph holding optimizer a's step, launched between optimizer b's eager steps: each launch
+// hands the store's step count back to a (ttp::Graph::launch), so both keep their own.
+static void run_graph_groups() {
+    ParamArena arena(ttp::Mode::FP32);
+    MLP model(64, 128, 10, arena);
+    auto params = model.parameters();
+    std::vector<Ref> ref;
+    for (auto& p : params) {
+        Ref r;
+        r.p = p->master();
+        r.m.assign(p->numel(), 0.0f);
+        r.v.assign(p->numel(), 0.0f);
+        ref.push_back(r);
+    }
+    const std::vector<size_t> ga = {0, 1}, gb = {2, 3};
+    AdamW a({params[0], params[1]}, 1e-2f, {0.9, 0.95}, 1e-8f, 0.1f);
+    Adam b({params[2], params[3]}, 3e-3f, {0.8, 0.999}, 1e-6f);
+    ttp::Store& st = params[0]->store();
+    ttp::Graph graph;
+    uint64_t ta = 0, tb = 0;
+    // lower case: an eager step; 'C': capture a's step (runs nothing); 'A': launch it
+    const char* order = "abaCbAAbbA";
+    for (int k = 0; order[k]; ++k) {
+        const char ch = order[k];
+        if (ch == 'C') {
+            st.begin_capture();
+            a.step();
+            graph = st.end_capture();
+            continue;
+        }
+        const bool is_a = ch == 'a' || ch == 'A';
+        const auto& members = is_a ? ga : gb;
+        const uint64_t t = is_a ? ++ta : ++tb;
+        for (size_t j : members) {
+            auto g = grad_of(params[j]->numel(), 300 + k * 10 + (int)j);
+            params[j]->grad = g;
+            if (is_a)
+                adam_ref(ref[j], g, (double)1e-2f, 0.9, 0.95, (double)1e-8f, t, (double)0.1f,
+                         j == 0);
+            else
+                adam_ref(ref[j], g, (double)3e-3f, 0.8, 0.999, (double)1e-6f, t, 0.0, false);
+        }
+        if (ch == 'A') graph.launch(); else if (is_a) a.step(); else b.step();
+        test::check(st.step_count() == t,
+                    "graph groups: the store holds the count of the optimizer that stepped last");
+    }
+    test::check(ta == 5 && tb == 4, "graph groups: 5 steps of a, 4 of b");
+    for (size_t k = 0; k < params.size(); ++k) {
+        test::assert_bits(params[k]->master(), ref[k].p, "graph groups param " + std::to_string(k));
+        test::assert_bits(st.state(TTP_BUF_EXP_AVG, params[k]->index), ref[k].m,
+                          "graph groups exp_avg " + std::to_string(k));
+        test::assert_bits(st.state(TTP_BUF_EXP_AVG_SQ, params[k]->index), ref[k].v,
+                          "graph groups exp_avg_sq " + std::to_string(k));
+    }
+}
+
 int main() {
     test::DeviceGuard dg;
     run(false);
     run(true);
     run_groups();
+    run_graph_groups();
     // py/optim.py:33-41 validation
     ParamArena arena;
     Linear l(4, 4, arena);

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from gpu_util import compare_state, make_pair, torch_mod
+from gpu_util import compare_state, device_grads, make_pair, torch_mod
 
 pytestmark = pytest.mark.gpu
 
@@ -282,5 +282,51 @@ def test_closing_other_stores_during_capture_is_deferred():
     assert gc.isenabled()
     graph.replay()
     assert store.step_count == 2
+    graph.close()
+    store.close()
+
+
+def test_graph_replay_hands_the_step_count_back_to_its_optimizer():
+    """Optimizers a and b over two groups of one store, with different betas.  a's step is
+    captured once, and its replays interleave with b's eager steps.  Each replay uses a's own
+    step count (the graph hands it back to a), b keeps its own, and each betas pair keeps its
+    own bias-correction table.  Checked against the oracle stepping each group with its own
+    count, after every step."""
+    import ttperf
+    torch = torch_mod()
+    shapes = [(64, 48), (48,), (48, 32), (32,), (300,)]
+    decay = [True, False, True, False, False]
+    store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=98)
+    store.set_stream(None)
+    groups = {"a": [0, 1, 4], "b": [2, 3]}
+    hps = {"a": dict(lr=3e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1),
+           "b": dict(lr=1e-2, betas=(0.8, 0.999), eps=1e-6, weight_decay=0.0)}
+    opts = {"a": ttperf.AdamW([store.tensors[i] for i in groups["a"]], **hps["a"]),
+            "b": ttperf.Adam([store.tensors[i] for i in groups["b"]], **hps["b"])}
+    counts = {"a": 0, "b": 0}
+    gen = torch.Generator(device="cuda").manual_seed(99)
+    graph = None
+    # lower case: an eager step; "C": capture a's step (runs nothing); "A": replay it
+    for k, what in enumerate("abaCbAAbbA"):
+        if what == "C":
+            store.begin_capture()
+            opts["a"].step()
+            graph = store.end_capture()
+            continue
+        g = what.lower()
+        ref.grad[:store.total] = device_grads(store, gen, 1e-2)
+        for i in range(ref.n):
+            ref.set_has_grad(i, i in groups[g])
+        if what == "A":
+            graph.replay()
+        else:
+            opts[g].step()
+        ref.t = counts[g]
+        ref.adam_step(decoupled=(g == "a"), **hps[g])
+        counts[g] = ref.t
+        print(f"step {k}: {what}, count of {g}: {counts[g]}", flush=True)
+        assert store.step_count == counts[g]
+        compare_state(store, ref, max_ulp=0)
+    assert counts == {"a": 5, "b": 4}
     graph.close()
     store.close()

@@ -129,9 +129,11 @@ struct ttp_ctx {
     void* staging = nullptr;  // device copy of a host gradient for ttp_accumulate_grad
     uint64_t staging_bytes = 0;
 
+    // bias-correction tables of every betas pair stepped with (kept, since captured graphs
+    // and queued steps read them) and the current pair's
+    std::map<std::pair<double, double>, std::pair<float*, uint32_t>> bias_tables;
     float* bias_tab = nullptr;
     uint32_t bias_len = 0;
-    double bias_b1 = -1.0, bias_b2 = -1.0;
 
     ttp_scaler_config scaler{0, 2000, 65536.0, 2.0, 0.5};
     uint64_t host_t = 0;     // step count while it lives on the host (see dev_t)
@@ -301,33 +303,48 @@ int select_tables(ttp_ctx* c, const uint32_t* subset, uint32_t nsub, const WorkT
 }
 
 // (float)(1 - beta^t) for t = 1.. until both round to exactly 1.0f (and stay there, since
-// beta^t only shrinks); py/optim.py:51-52 evaluates the same host-double expression.
+// beta^t only shrinks); py/optim.py:51-52 evaluates the same host-double expression.  One
+// table per betas pair, built on first use; optimizers with different betas over one store
+// switch tables without a synchronisation.  Beyond kMaxBiasTables pairs (a betas schedule)
+// the cache is emptied, after the queued work, unless graphs may read the tables.
+constexpr size_t kMaxBiasTables = 16;
+
 int ensure_bias_table(ttp_ctx* c, double b1, double b2) {
-    if (c->bias_tab && c->bias_b1 == b1 && c->bias_b2 == b2) return TTP_OK;
-    int rc;
-    if ((rc = no_capture(c, "a step with new betas (builds a table)"))) return rc;
-    if (c->n_graphs)
-        return fail(TTP_ERR_STATE, "betas changed while graphs of this context are alive");
-    std::vector<float> tab;
-    const uint64_t kMax = 1ull << 24;
-    for (uint64_t t = 1;; ++t) {
-        const float x1 = (float)(1.0 - std::pow(b1, (double)t));
-        const float x2 = (float)(1.0 - std::pow(b2, (double)t));
-        if (x1 == 1.0f && x2 == 1.0f) break;
-        if (t > kMax)
-            return fail(TTP_ERR_INVALID, "beta too close to 1: bias correction table too long");
-        tab.push_back(x1);
-        tab.push_back(x2);
+    const auto key = std::make_pair(b1, b2);
+    auto it = c->bias_tables.find(key);
+    if (it == c->bias_tables.end()) {
+        int rc;
+        if ((rc = no_capture(c, "a step with new betas (builds a table)"))) return rc;
+        std::vector<float> tab;
+        const uint64_t kMax = 1ull << 24;
+        for (uint64_t t = 1;; ++t) {
+            const float x1 = (float)(1.0 - std::pow(b1, (double)t));
+            const float x2 = (float)(1.0 - std::pow(b2, (double)t));
+            if (x1 == 1.0f && x2 == 1.0f) break;
+            if (t > kMax)
+                return fail(TTP_ERR_INVALID, "beta too close to 1: bias correction table too long");
+            tab.push_back(x1);
+            tab.push_back(x2);
+        }
+        if (c->bias_tables.size() >= kMaxBiasTables && !c->n_graphs) {
+            HIP_TRY(hipStreamSynchronize(c->stream));  // queued steps may read them
+            for (auto& kv : c->bias_tables) (void)hipFree(kv.second.first);
+            c->bias_tables.clear();
+            c->bias_tab = nullptr;
+            c->bias_len = 0;
+        }
+        float* d = nullptr;
+        HIP_TRY(hipMalloc((void**)&d, std::max<size_t>(tab.size(), 2) * sizeof(float)));
+        // a synchronous copy into the new allocation, which no queued work reads
+        if (!tab.empty() &&
+            hipMemcpy(d, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
+            (void)hipFree(d);
+            return fail(TTP_ERR_HIP, "bias correction table upload failed");
+        }
+        it = c->bias_tables.emplace(key, std::make_pair(d, (uint32_t)(tab.size() / 2))).first;
     }
-    HIP_TRY(hipStreamSynchronize(c->stream));
-    if (c->bias_tab) HIP_TRY(hipFree(c->bias_tab));
-    c->bias_tab = nullptr;
-    HIP_TRY(hipMalloc((void**)&c->bias_tab, std::max<size_t>(tab.size(), 2) * sizeof(float)));
-    if (!tab.empty())
-        HIP_TRY(hipMemcpy(c->bias_tab, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice));
-    c->bias_len = (uint32_t)(tab.size() / 2);
-    c->bias_b1 = b1;
-    c->bias_b2 = b2;
+    c->bias_tab = it->second.first;
+    c->bias_len = it->second.second;
     return TTP_OK;
 }
 
@@ -597,8 +614,9 @@ void release(ttp_ctx* c) {
     (void)hipSetDevice(c->device);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     for (void* p : {(void*)c->grad, (void*)c->records, (void*)c->momentum, (void*)c->mom_init,
-                    (void*)c->st, (void*)c->partials, (void*)c->bias_tab, c->staging})
+                    (void*)c->st, (void*)c->partials, c->staging})
         if (p) (void)hipFree(p);
+    for (auto& kv : c->bias_tables) (void)hipFree(kv.second.first);
     free_tables(c->all);
     for (auto& kv : c->tables) free_tables(kv.second);
     // MIXED: param is the bf16 copy and master lives in `records`; FP32: param == master

@@ -140,13 +140,21 @@ def _capture_ended():
 
 
 class StepGraph:
-    """A captured hipGraph of a store's work (ttp_capture_begin .. ttp_capture_end)."""
+    """A captured hipGraph of a store's work (ttp_capture_begin .. ttp_capture_end).
+
+    It remembers which optimizer held the store's step count at capture and hands the count
+    back to it before each replay (a no-op unless another optimizer stepped the store since),
+    so the replayed steps use that optimizer's own count."""
 
     def __init__(self, store: "ParamStore", handle):
         self.store = store
         self._g = handle
+        self._owner = store._t_owner
 
     def replay(self):
+        owner = self._owner() if self._owner is not None else None
+        if owner is not None:
+            owner._claim(self.store)
         L.check(L.lib.ttp_graph_launch(self._g))
 
     def close(self):
