@@ -1,0 +1,365 @@
+"""Stateful differential fuzzing of libttperf_hip against the CPU oracle.
+
+Each seeded case builds a small ragged store (empty, 1-element, odd, 2-D tensors; decay
+flags; fp32 or mixed precision) and runs a random sequence of operations drawn from the whole
+host interface, mirrored on the oracle:
+
+  gradients written flat or per tensor, from host or device memory (an occasional +inf while
+  loss scaling is on); gradients accumulated from fp32 or bf16 sources, host or device;
+  `grad = None`; zero_grad of all or of a subset, to zeros or to None; master or bf16 weight
+  uploads; Adam / AdamW / L2 and SGD (momentum, dampening, nesterov, L2) steps over everything
+  or over a subset, with or without clipping, with step reports; the loss scaler switched on
+  or off; the step count set; the gradient norm probed; a checkpoint saved and later loaded;
+  an Adam step captured into a graph and replayed later, between other operations.
+
+After every operation the whole state is compared: master, m, v and momentum within the
+2-ulp bar of the other parity tests (in practice 0), bf16 weights and the gradients bit for
+bit, the has-grad flags, the step count and the loss-scaler state; step reports must agree
+on skip, found_inf, step count and scale.  Every operation is printed before it runs.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_util import compare_state, make_pair, torch_mod
+
+pytestmark = pytest.mark.gpu
+
+SEEDS = list(range(2000, 2100))
+N_OPS = 50
+BETAS = [(0.9, 0.999), (0.9, 0.95), (0.8, 0.99)]
+
+
+def _shapes(rng):
+    out = []
+    for _ in range(int(rng.integers(2, 9))):
+        k = int(rng.integers(0, 8))
+        if k == 0:
+            out.append((0,))
+        elif k == 1:
+            out.append((1,))
+        elif k <= 4:
+            out.append((int(rng.integers(2, 3000)),))
+        else:
+            out.append((int(rng.integers(1, 90)), int(rng.integers(1, 90))))
+    return out
+
+
+class Case:
+    def __init__(self, seed, tmp_path):
+        self.torch = torch_mod()
+        self.rng = np.random.default_rng(seed)
+        rng = self.rng
+        self.shapes = _shapes(rng)
+        self.n = len(self.shapes)
+        self.decay = [len(s) == 2 for s in self.shapes]
+        self.mixed = bool(rng.integers(0, 2))
+        mode = O.MODE_MIXED if self.mixed else O.MODE_FP32
+        self.store, self.ref = make_pair(self.shapes, self.decay, mode, seed=seed)
+        self.store.set_stream(None)  # the store's own stream: capturable
+        self.numels = [t.numel for t in self.store.tensors]
+        self.graphs = []      # (graph, hp, captured active set)
+        self.last_adam = None  # (hp, indices, active set) of the last eager Adam step
+        self.saved = None     # oracle snapshot of the last checkpoint
+        self.path = tmp_path / f"state_{seed}.bin"
+        self.scaler_on = False
+        self.adam_seen = False
+        self.mom_seen = False
+
+    # ---- helpers ------------------------------------------------------------------------
+    def grad_values(self, n, std=None):
+        std = float(10 ** self.rng.uniform(-4, -1)) if std is None else std
+        g = (self.rng.standard_normal(n) * std).astype(np.float32)
+        if self.scaler_on:
+            g *= np.float32(self.ref.scale)
+        return O.bf16_rne(g) if self.mixed else g
+
+    def to_device(self, a):
+        torch = self.torch
+        if a.dtype == np.uint16:
+            return torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16).cuda()
+        return torch.from_numpy(a.copy()).cuda()
+
+    def pick_subset(self):
+        k = int(self.rng.integers(1, self.n + 1))
+        return sorted(int(i) for i in self.rng.choice(self.n, size=k, replace=False))
+
+    def nonempty(self):
+        return [i for i in range(self.n) if self.numels[i]]
+
+    # ---- operations -----------------------------------------------------------------------
+    def op_grads_flat(self):
+        from ttperf import _lib as L
+        g = self.grad_values(self.store.total)
+        inf = self.scaler_on and self.rng.random() < 0.25 and self.nonempty()
+        if inf:
+            i = int(self.rng.choice(self.nonempty()))
+            j = self.store.offsets[i] + int(self.rng.integers(0, self.numels[i]))
+            g[j] = 0x7F80 if self.mixed else np.float32(np.inf)
+        dev = self.rng.random() < 0.5
+        print(f"  grads flat ({'device' if dev else 'host'}, inf={bool(inf)})", flush=True)
+        self.store.upload(L.BUF_GRAD, L.ALL_TENSORS, self.to_device(g) if dev else g)
+        self.ref.grad[:self.store.total] = g
+        for i in range(self.n):
+            self.ref.set_has_grad(i, True)
+
+    def op_grad_one(self):
+        i = int(self.rng.integers(0, self.n))
+        g = self.grad_values(self.numels[i])
+        print(f"  grad of tensor {i} (host)", flush=True)
+        self.store.tensors[i].grad = g
+        self.ref.set_grad(i, g)
+
+    def op_accumulate(self):
+        i = int(self.rng.integers(0, self.n))
+        bf16 = self.rng.random() < 0.5
+        dev = self.rng.random() < 0.5
+        g = (self.rng.standard_normal(self.numels[i]) * 1e-2).astype(np.float32)
+        if self.scaler_on:
+            g *= np.float32(self.ref.scale)
+        src = O.bf16_rne(g) if bf16 else g
+        print(f"  accumulate into tensor {i} ({'bf16' if bf16 else 'fp32'}, "
+              f"{'device' if dev else 'host'}, had grad {self.ref.has_grad(i)})", flush=True)
+        self.store.accumulate_grad(i, self.to_device(src) if dev else src)
+        self.ref.accumulate_grad(i, src)
+
+    def op_drop_grad(self):
+        i = int(self.rng.integers(0, self.n))
+        print(f"  grad of tensor {i} = None", flush=True)
+        self.store.set_has_grad(i, False)
+        self.ref.set_has_grad(i, False)
+
+    def op_zero_grad(self):
+        none = bool(self.rng.integers(0, 2))
+        if self.rng.random() < 0.5:
+            print(f"  zero_grad(set_to_none={none})", flush=True)
+            self.store.zero_grad(set_to_none=none)
+            self.ref.zero_grad(set_to_none=none)
+        else:
+            idx = self.pick_subset()
+            print(f"  zero_grad(set_to_none={none}, indices={idx})", flush=True)
+            self.store.zero_grad(set_to_none=none, indices=idx)
+            for i in idx:
+                self.ref.view("grad", i)[:] = 0
+                self.ref.set_has_grad(i, not none)
+
+    def op_upload_weights(self):
+        i = int(self.rng.integers(0, self.n))
+        x = (self.rng.standard_normal(self.numels[i]) * 0.05).astype(np.float32)
+        if self.mixed and self.rng.random() < 0.5:
+            from ttperf import _lib as L
+            bits = O.bf16_rne(x)
+            print(f"  bf16 weights of tensor {i}", flush=True)
+            self.store.upload(L.BUF_PARAM, i, bits)
+            self.ref.view("param", i)[:] = bits
+            self.ref.view("master", i)[:] = O.bf16_to_f32(bits)
+        else:
+            print(f"  master weights of tensor {i}", flush=True)
+            self.store.tensors[i].set_data(x)
+            self.ref.set_master(i, x)
+
+    def _active(self, indices):
+        cand = range(self.n) if indices is None else indices
+        return [i for i in cand if self.ref.has_grad(i) and self.numels[i]]
+
+    def _ref_step(self, kind, hp, active):
+        """The oracle steps exactly `active` (has-grad flags narrowed, then restored)."""
+        flags = [self.ref.has_grad(i) for i in range(self.n)]
+        for i in range(self.n):
+            self.ref.set_has_grad(i, i in active)
+        if kind == "adam":
+            e = self.ref.adam_step(max_grad_norm=hp["max_grad_norm"] or 0.0,
+                                   **{k: v for k, v in hp.items() if k != "max_grad_norm"})
+        else:
+            e = self.ref.sgd_step(max_grad_norm=hp["max_grad_norm"] or 0.0,
+                                  **{k: v for k, v in hp.items() if k != "max_grad_norm"})
+        for i in range(self.n):
+            self.ref.set_has_grad(i, flags[i])
+        return e
+
+    def _check_report(self, r, e):
+        assert r["skipped"] == e["skipped"] and r["found_inf"] == e["found_inf"], (r, e)
+        assert r["step"] == e["step"], (r, e)
+        if self.scaler_on:
+            assert r["scale"] == e["scale"] and r["growth_tracker"] == e["growth_tracker"]
+        if np.isfinite(e["grad_norm"]) and e["grad_norm"] > 0 and np.isfinite(r["grad_norm"]):
+            assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
+
+    def op_adam(self):
+        rng = self.rng
+        wd = 0.0 if rng.random() < 0.3 else float(rng.uniform(0.01, 0.2))
+        hp = dict(lr=float(10 ** rng.uniform(-4, -1.5)), betas=BETAS[int(rng.integers(0, 3))],
+                  eps=[1e-8, 1e-6][int(rng.integers(0, 2))], weight_decay=wd,
+                  decoupled=bool(rng.integers(0, 2)),
+                  max_grad_norm=None if rng.random() < 0.5 else float(10 ** rng.uniform(-2, 1)))
+        indices = None if rng.random() < 0.6 else self.pick_subset()
+        report = rng.random() < 0.5
+        active = self._active(indices)
+        print(f"  adam {hp} indices={indices} active={active}", flush=True)
+        r = self.store.adam_step(report=report, indices=indices, **hp)
+        e = self._ref_step("adam", hp, active)
+        if report:
+            self._check_report(r, e)
+        self.last_adam = (hp, indices, active)
+        self.adam_seen = True
+
+    def op_sgd(self):
+        rng = self.rng
+        kind = int(rng.integers(0, 4))
+        hp = dict(lr=float(10 ** rng.uniform(-3, -1)), momentum=0.0, dampening=0.0,
+                  weight_decay=0.0, nesterov=False,
+                  max_grad_norm=None if rng.random() < 0.5 else float(10 ** rng.uniform(-2, 1)))
+        if kind == 1:
+            hp.update(momentum=0.9)
+        elif kind == 2:
+            hp.update(momentum=0.9, nesterov=True, weight_decay=0.01)
+        elif kind == 3:
+            hp.update(momentum=0.8, dampening=0.1, weight_decay=0.05)
+        indices = None if rng.random() < 0.6 else self.pick_subset()
+        report = rng.random() < 0.5
+        active = self._active(indices)
+        print(f"  sgd {hp} indices={indices} active={active}", flush=True)
+        r = self.store.sgd_step(report=report, indices=indices, **hp)
+        e = self._ref_step("sgd", hp, active)
+        if report:
+            self._check_report(r, e)
+        self.last_adam = None
+        self.mom_seen = self.mom_seen or hp["momentum"] > 0
+
+    def op_scaler(self):
+        on = not self.scaler_on
+        init = float(2.0 ** int(self.rng.integers(4, 14)))
+        interval = int(self.rng.integers(2, 5))
+        print(f"  scaler {'on' if on else 'off'} (init {init:g}, interval {interval}), "
+              f"{len(self.graphs)} live graph(s)", flush=True)
+        if self.graphs:
+            import ttperf
+            with pytest.raises(ttperf.TTPError):
+                self.store.configure_scaler(on, init_scale=init, growth_interval=interval)
+            return
+        self.store.configure_scaler(on, init_scale=init, growth_interval=interval)
+        if on:
+            self.ref.configure_scaler(True, init, growth_interval=interval)
+        else:
+            self.ref.s.scaler_enabled = 0
+        self.scaler_on = on
+
+    def op_set_step(self):
+        t = int(self.rng.integers(0, 50))
+        print(f"  step count = {t}", flush=True)
+        self.store.step_count = t
+        self.ref.t = t
+
+    def op_grad_norm(self):
+        print("  grad_norm()", flush=True)
+        got = self.store.grad_norm()
+        inv = 1.0 / self.ref.scale if self.scaler_on else 1.0
+        sumsq, _ = self.ref.grad_sumsq(inv)
+        want = float(np.sqrt(sumsq))
+        if np.isfinite(want) and want > 0:
+            assert abs(got - want) <= 1e-5 * want, (got, want)
+
+    def _snapshot(self):
+        r, s = self.ref, self.ref.s
+        return dict(master=r.master.copy(), param=r.param.copy(), exp_avg=r.exp_avg.copy(),
+                    exp_avg_sq=r.exp_avg_sq.copy(), momentum=r.momentum.copy(),
+                    mom_init=r.mom_init.copy(), t=r.t, scale=s.scale,
+                    tracker=s.growth_tracker, enabled=s.scaler_enabled,
+                    interval=s.growth_interval, growth=s.growth_factor,
+                    backoff=s.backoff_factor)
+
+    def op_save(self):
+        print(f"  save_state -> {self.path.name}", flush=True)
+        self.store.save_state(self.path)
+        self.saved = self._snapshot()
+
+    def op_load(self):
+        if self.saved is None:
+            return self.op_save()
+        snap = self.saved
+        differs = bool(snap["enabled"]) != self.scaler_on or (
+            self.scaler_on and snap["interval"] != self.ref.s.growth_interval)
+        print(f"  load_state <- {self.path.name} ({len(self.graphs)} live graph(s), "
+              f"scaler settings differ: {differs})", flush=True)
+        if self.graphs and differs:
+            import ttperf
+            with pytest.raises(ttperf.TTPError):
+                self.store.load_state(self.path)
+            return
+        self.store.load_state(self.path)
+        r, s = self.ref, self.ref.s
+        for k in ("master", "param", "exp_avg", "exp_avg_sq", "momentum", "mom_init"):
+            getattr(r, k)[:] = snap[k]
+        r.t = snap["t"]
+        s.scale, s.growth_tracker = snap["scale"], snap["tracker"]
+        s.scaler_enabled, s.growth_interval = snap["enabled"], snap["interval"]
+        s.growth_factor, s.backoff_factor = snap["growth"], snap["backoff"]
+        self.scaler_on = bool(snap["enabled"])
+
+    def op_capture(self):
+        """Capture the last eager Adam step's call (same hyperparameters, same tensor set: a
+        set never stepped eagerly has no work table, which a capture cannot build)."""
+        if self.last_adam is None or len(self.graphs) >= 3:
+            return self.op_adam()
+        hp, indices, eager_active = self.last_adam
+        active = self._active(indices)
+        if active != eager_active:
+            return self.op_adam()
+        print(f"  capture adam {hp} indices={indices} active={active}", flush=True)
+        self.store.begin_capture()
+        self.store.adam_step(indices=indices, **hp)
+        self.graphs.append((self.store.end_capture(), hp, active))
+
+    def op_replay(self):
+        if not self.graphs:
+            return self.op_capture()
+        g, hp, active = self.graphs[int(self.rng.integers(0, len(self.graphs)))]
+        print(f"  replay adam {hp} active={active}", flush=True)
+        g.replay()
+        self._ref_step("adam", hp, active)
+
+    OPS = [("grads_flat", 6), ("grad_one", 3), ("accumulate", 3), ("drop_grad", 2),
+           ("zero_grad", 2), ("upload_weights", 1), ("adam", 6), ("sgd", 4), ("scaler", 1),
+           ("set_step", 1), ("grad_norm", 1), ("save", 1), ("load", 1), ("capture", 2),
+           ("replay", 3)]
+
+    def compare(self):
+        from ttperf import _lib as L
+        which = ["master", "param"]
+        if self.adam_seen:
+            which += ["exp_avg", "exp_avg_sq"]
+        if self.mom_seen:
+            which += ["momentum"]
+        compare_state(self.store, self.ref, which=tuple(which), max_ulp=2)
+        got = self.store.download(L.BUF_GRAD)
+        want = self.ref.grad[:self.store.total]
+        assert np.array_equal(got.view(np.uint8), want.view(np.uint8)), "gradients differ"
+        assert [self.store.has_grad(i) for i in range(self.n)] == \
+            [self.ref.has_grad(i) for i in range(self.n)], "has-grad flags differ"
+        assert self.store.step_count == self.ref.t
+        if self.scaler_on:
+            scale, tracker = self.store.scaler_state()
+            assert (scale, tracker) == (np.float32(self.ref.scale), self.ref.growth_tracker)
+
+    def close(self):
+        for g, _, _ in self.graphs:
+            g.close()
+        self.graphs.clear()
+        self.store.close()
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_random_operation_sequence(seed, tmp_path):
+    c = Case(seed, tmp_path)
+    print(f"case {seed}: {'mixed' if c.mixed else 'fp32'} shapes={c.shapes}", flush=True)
+    names = [n for n, _ in Case.OPS]
+    weights = np.array([w for _, w in Case.OPS], np.float64)
+    weights /= weights.sum()
+    try:
+        for k in range(N_OPS):
+            op = names[int(c.rng.choice(len(names), p=weights))]
+            print(f" op {k}: {op}", flush=True)
+            getattr(c, "op_" + op)()
+            c.compare()
+    finally:
+        c.close()
