@@ -77,3 +77,64 @@ def test_torch_forward_backward_with_zero_copy_store(mode, opt_name):
     w0 = store.tensors[0].numpy().ravel()
     assert np.array_equal(p0.view(np.uint32), w0.astype(np.float32).view(np.uint32))
     store.close()
+
+
+def test_reference_traced_mlp_known_answers():
+    """examples/train_mlp_traced.cpp:100-186, whose PyTorch reference is
+    verify/verify_comparison.py:13-101: a 512 -> 256 -> 128 MLP with every weight 0.01 and
+    zero biases, x = 1, target = 0.5, batch 1024, MSE, SGD lr 0.01, 5 steps in bf16.  The
+    reference prints the expected initial loss 159.390625 and final loss 0.000244
+    (train_mlp_traced.cpp:183-185).
+
+    Here torch runs the bf16 forward/backward over zero-copy views of a mixed-precision store
+    and libttperf_hip takes the steps (fp32 master weights, bf16 working copy).  Both known
+    answers are met exactly (0.000244 is 2^-12), and each step's master and bf16 weights
+    match the oracle, fed the same gradients, bit for bit."""
+    import ttperf
+    from ttperf import _lib as L
+    torch = torch_mod()
+    F = torch.nn.functional
+    shapes = [(256, 512), (256,), (128, 256), (128,)]  # nn.Linear weights are [out, in]
+    store = ttperf.ParamStore(shapes, mode="mixed", decay=[True, False, True, False])
+    store.set_stream(torch.cuda.current_stream())
+    ref = O.OracleStore([t.numel for t in store.tensors], flags=[1, 0, 1, 0],
+                        mode=O.MODE_MIXED, nthreads=2)
+    for i, s in enumerate(shapes):
+        w = np.full(store.tensors[i].numel, 0.01 if len(s) == 2 else 0.0, np.float32)
+        store.tensors[i].set_data(w)
+        ref.set_master(i, w)
+    params = [torch.nn.Parameter(t.torch_view(L.BUF_PARAM)) for t in store.tensors]
+    for p, t in zip(params, store.tensors):
+        p.grad = t.torch_view(L.BUF_GRAD)
+    w1, b1, w2, b2 = params
+    x = torch.ones(1024, 512, device="cuda", dtype=torch.bfloat16)
+    target = torch.full((1024, 128), 0.5, device="cuda", dtype=torch.bfloat16)
+
+    def loss_of():
+        h = torch.relu(x @ w1.t().contiguous() + b1)
+        pred = h @ w2.t().contiguous() + b2
+        return F.mse_loss(pred.float(), target.float())
+
+    opt = ttperf.SGD(store.parameters(), lr=0.01)
+    with torch.no_grad():
+        initial = loss_of().item()
+    after = []
+    for step in range(5):
+        opt.zero_grad()
+        loss = loss_of()
+        loss.backward()  # into the store's bf16 grad buffer
+        store.mark_grads()
+        ref.grad[:] = store.download(L.BUF_GRAD)
+        for i in range(ref.n):
+            ref.set_has_grad(i, True)
+        opt.step()
+        ref.sgd_step(lr=0.01)
+        compare_state(store, ref, which=("master", "param"), max_ulp=0)
+        with torch.no_grad():
+            after.append(loss_of().item())
+        print(f"step {step}: loss_before={loss.item():.6f}, loss_after={after[-1]:.6f}",
+              flush=True)
+    assert initial == 159.390625, initial            # train_mlp_traced.cpp:184
+    assert f"{after[-1]:.6f}" == "0.000244", after   # train_mlp_traced.cpp:185
+    assert after[-1] == 2.0 ** -12
+    store.close()
