@@ -138,3 +138,65 @@ def test_reference_traced_mlp_known_answers():
     assert f"{after[-1]:.6f}" == "0.000244", after   # train_mlp_traced.cpp:185
     assert after[-1] == 2.0 ** -12
     store.close()
+
+
+def test_reference_verify_mlp_trajectory_fp32():
+    """verify/verify_mlp.py:12-80, the fp32 PyTorch reference of verify/verify_mlp_traced.cpp:
+    a 64 -> 32 -> 32 MLP with every weight 0.01 and zero biases, x = 1, target = 0.5, batch
+    32, MSE, SGD lr 0.1, 10 steps, printed to 6 decimals.  The engine (fp32 store, torch
+    forward/backward over zero-copy views) prints the same 11 losses as torch.optim.SGD on a
+    twin torch model; bitwise the two may differ by the rounding of p - lr*g (the reference's
+    multiply then subtract, verify_mlp_traced.cpp:96-100, against torch's fused add), so the
+    engine is held to the oracle bit for bit instead."""
+    import ttperf
+    from ttperf import _lib as L
+    torch = torch_mod()
+    F = torch.nn.functional
+    shapes = [(32, 64), (32,), (32, 32), (32,)]
+    store = ttperf.ParamStore(shapes, mode="fp32", decay=[True, False, True, False])
+    store.set_stream(torch.cuda.current_stream())
+    ref = O.OracleStore([t.numel for t in store.tensors], flags=[1, 0, 1, 0],
+                        mode=O.MODE_FP32, nthreads=2)
+    twin = []
+    for i, s in enumerate(shapes):
+        w = np.full(store.tensors[i].numel, 0.01 if len(s) == 2 else 0.0, np.float32)
+        store.tensors[i].set_data(w)
+        ref.set_master(i, w)
+        twin.append(torch.nn.Parameter(torch.from_numpy(w.reshape(s)).cuda()))
+    params = [torch.nn.Parameter(t.torch_view(L.BUF_PARAM)) for t in store.tensors]
+    for p, t in zip(params, store.tensors):
+        p.grad = t.torch_view(L.BUF_GRAD)
+    x = torch.ones(32, 64, device="cuda")
+    target = torch.full((32, 32), 0.5, device="cuda")
+
+    def loss_of(w1, b1, w2, b2):
+        h = torch.relu(x @ w1.t().contiguous() + b1)
+        return F.mse_loss(h @ w2.t().contiguous() + b2, target)
+
+    opt = ttperf.SGD(store.parameters(), lr=0.1)
+    torch_opt = torch.optim.SGD(twin, lr=0.1)
+    ours, theirs = [], []
+    with torch.no_grad():
+        ours.append(loss_of(*params).item())
+        theirs.append(loss_of(*twin).item())
+    for step in range(10):
+        opt.zero_grad()
+        loss_of(*params).backward()
+        store.mark_grads()
+        ref.grad[:] = store.download(L.BUF_GRAD)
+        for i in range(ref.n):
+            ref.set_has_grad(i, True)
+        opt.step()
+        ref.sgd_step(lr=0.1)
+        compare_state(store, ref, which=("master",), max_ulp=0)
+        torch_opt.zero_grad()
+        loss_of(*twin).backward()
+        torch_opt.step()
+        with torch.no_grad():
+            ours.append(loss_of(*params).item())
+            theirs.append(loss_of(*twin).item())
+        print(f"step {step + 1}: loss {ours[-1]:.6f} (torch.optim.SGD {theirs[-1]:.6f})",
+              flush=True)
+    assert [f"{v:.6f}" for v in ours] == [f"{v:.6f}" for v in theirs]
+    assert ours[-1] < 1e-2 * ours[0]  # 0.087143 -> 0.000684
+    store.close()
