@@ -12,6 +12,7 @@ its launches on the kernel's stream during a second pass of K steps, and the CPU
 baseline timed on this host's cores on a bounded sample.
 """
 import argparse
+import ctypes
 import json
 import os
 import re
@@ -250,23 +251,51 @@ def main():
         skip_ms = e0.elapsed_time(e1)
         assert rs is None
 
-    # context: torch's device copy (a blit kernel) of the update's byte count
+    # context: the practical ceilings of the update's traffic on this GPU, over the update's
+    # byte count: torch's device copy (a blit kernel), and libttperf_ceiling's non-temporal
+    # 16-byte copy (the update's 50/50 read/write mix) and read-only pass
     ub = UPDATE_BYTES[(args.optimizer, mode)]
     nb = NORM_BYTES[mode]
-    copy_bytes = n_params * ub // 2
+    copy_bytes = n_params * ub // 2 // 16 * 16
     src = torch.empty(copy_bytes // 4, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
-    with torch.cuda.stream(stream):
+    sink = torch.zeros(1, dtype=torch.float32, device=dev)
+    src.normal_()
+    ceil = ctypes.CDLL(os.path.join(REPO, "tt-perf_amd", "lib", "libttperf_ceiling.so"))
+    ceil.ttpc_copy_nt.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64,
+                                  ctypes.c_int, ctypes.c_void_p]
+    ceil.ttpc_read_nt.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int,
+                                  ctypes.c_void_p, ctypes.c_void_p]
+    # the fastest forms measured (see tt-perf_amd/csrc/ceiling.hip): a straight-line copy,
+    # one block per 4 KB tile, and a read over 8 blocks per CU
+    read_grid = torch.cuda.get_device_properties(dev).multi_processor_count * 8
+    n16 = copy_bytes // 16
+
+    def timed(fn, reps=10):
         for _ in range(3):
-            dst.copy_(src)
+            fn()
         torch.cuda.synchronize()
         e0.record(stream)
-        for _ in range(10):
-            dst.copy_(src)
+        for _ in range(reps):
+            fn()
         e1.record(stream)
-    torch.cuda.synchronize()
-    copy_gbps = 2 * copy_bytes * 10 / (e0.elapsed_time(e1) / 1e3) / 1e9
-    del src, dst
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    def nt_copy():
+        rc = ceil.ttpc_copy_nt(src.data_ptr(), dst.data_ptr(), n16, 0, stream.cuda_stream)
+        assert rc == 0, f"ttpc_copy_nt: hipError {rc}"
+
+    def nt_read():
+        rc = ceil.ttpc_read_nt(src.data_ptr(), n16, read_grid, stream.cuda_stream,
+                               sink.data_ptr())
+        assert rc == 0, f"ttpc_read_nt: hipError {rc}"
+
+    with torch.cuda.stream(stream):
+        copy_gbps = 2 * copy_bytes / (timed(lambda: dst.copy_(src)) / 1e3) / 1e9
+    nt_copy_gbps = 2 * copy_bytes / (timed(nt_copy) / 1e3) / 1e9
+    nt_read_gbps = copy_bytes / (timed(nt_read) / 1e3) / 1e9
+    del src, dst, sink
 
     achieved = n_params * ub / (upd_avg / 1e3) / 1e9
     # the instantiation libttperf_hip launches (its rocprof name)
@@ -310,6 +339,15 @@ def main():
                        "source": "second pass of K steps with an event pair per launch"},
         "skipped_step_ms": round(skip_ms, 4) if skip_ms is not None else None,
         "torch_copy_GBps": round(copy_gbps, 1),
+        "ceilings": {"nt_copy_GBps": round(nt_copy_gbps, 1),
+                     "nt_copy_frac": round(nt_copy_gbps / HBM_PEAK_GBPS, 4),
+                     "nt_read_GBps": round(nt_read_gbps, 1),
+                     "bytes_each_way": copy_bytes,
+                     "update_vs_nt_copy": round(achieved / nt_copy_gbps, 4),
+                     "source": "libttperf_ceiling: 16-byte non-temporal straight-line copy "
+                               "(reads + writes counted) and read-only pass over the update's "
+                               "byte count, the fastest plain forms measured; 10 launches "
+                               "between one event pair"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": traffic_from_profiles(args.config),

@@ -34,6 +34,14 @@ def test_library_exports_every_declared_symbol():
     assert set(declared) == set(L.SIGNATURES)
 
 
+def test_ceiling_probe_library_exports_its_entry_points():
+    """bench.py's HBM ceilings come from libttperf_ceiling (built with the engine)."""
+    path = os.path.join(REPO, "tt-perf_amd", "lib", "libttperf_ceiling.so")
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True,
+                         check=True).stdout
+    assert {"ttpc_copy_nt", "ttpc_read_nt"} <= set(re.findall(r"\b(ttpc_\w+)", out))
+
+
 def test_abi_version():
     from ttperf import _lib as L
     assert L.lib.ttp_abi_version() == 1
