@@ -212,9 +212,10 @@ constexpr uint32_t norm_tile_elems() {
 // loads are in flight.  The loads are ordinary (cached) loads, so the last-read gradients are
 // still in the 256 MB Infinity Cache when the update pass, which walks the chunks in reverse
 // order, reads them again (measured on GPT-2 124M: update 531 us after this pass vs 559 us
-// alone; non-temporal loads here, or a forward walk in the update, lose most of that).  No atomics and no fences: each block writes one partial and
-// norm_finalize_kernel (next on the stream) combines them.  Squares of fp32 values are
-// exact in fp64, and any inf/NaN gradient makes the sum non-finite.
+// alone; non-temporal loads here, or a forward walk in the update, lose most of that).  No
+// atomics and no fences: each block writes one partial and norm_finalize_kernel (next on the
+// stream) combines them.  Squares of fp32 values are exact in fp64, and any inf/NaN gradient
+// makes the sum non-finite.
 template <typename GradT>
 __global__ __launch_bounds__(kBlock) void norm_partials_kernel(const GradT* __restrict__ g,
                                                                const Chunk* __restrict__ tiles,

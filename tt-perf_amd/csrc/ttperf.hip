@@ -1184,7 +1184,8 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
             for (uint32_t i : active)
                 if (!c->host_mom_init[i]) needed = true;
             if (needed) {
-                const uint32_t g = std::max<uint32_t>(1, std::min<uint32_t>((n + ttp::kBlock - 1) / ttp::kBlock, 1024));
+                const uint32_t g =
+                    std::max<uint32_t>(1, std::min<uint32_t>((n + ttp::kBlock - 1) / ttp::kBlock, 1024));
                 hipLaunchKernelGGL(ttp::mark_mom_init_kernel, dim3(g), dim3(ttp::kBlock), 0,
                                    c->stream, chunks, n, c->mom_init, (const DevState*)c->st,
                                    scaler ? 1 : 0);
