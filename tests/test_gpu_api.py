@@ -490,3 +490,31 @@ def test_two_adam_parameter_groups_keep_their_own_step_counts():
     assert counts == {"a": 4, "b": 4}
     compare_state(store, ref, max_ulp=0)
     store.close()
+
+
+def test_out_of_memory_is_reported_and_stale_hip_errors_are_not_misattributed():
+    """A store larger than the device fails with TTP_ERR_OOM (TTPMemoryError) and leaves no
+    trace: HIP keeps a failed call's error as the thread's "last error", which the engine's
+    post-launch checks read.  After that failure, and after a failing HIP call of the caller's
+    own (hipSetDevice to a device that does not exist), the next store steps normally and
+    matches the oracle."""
+    import ctypes
+
+    import ttperf
+    from ttperf import _lib as L
+    with pytest.raises(ttperf.TTPMemoryError) as e:
+        ttperf.ParamStore([(1 << 38,)], mode="mixed")  # 3.3 TB of fp32 state records
+    assert e.value.code == L.ERR_OOM and "hipMalloc" in str(e.value)
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    assert hip.hipSetDevice(ctypes.c_int(99)) != 0  # leaves an error in HIP's last-error slot
+    store, ref = make_pair([(300, 7), (64,)], [True, False], O.MODE_MIXED, seed=101)
+    torch = torch_mod()
+    gen = torch.Generator(device="cuda").manual_seed(102)
+    ref.grad[:store.total] = device_grads(store, gen, 1e-2)
+    for i in range(ref.n):
+        ref.set_has_grad(i, True)
+    assert hip.hipSetDevice(ctypes.c_int(99)) != 0
+    store.adam_step(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, decoupled=True)
+    ref.adam_step(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, decoupled=True)
+    compare_state(store, ref, max_ulp=0)
+    store.close()

@@ -42,12 +42,22 @@ int fail(int code, const std::string& msg) {
     return code;
 }
 
+// A failed HIP call returns TTP_ERR_OOM for an allocation that did not fit, else TTP_ERR_HIP.
+// Its error is also left in HIP's per-thread "last error", which clear_hip_error() resets.
 #define HIP_TRY(expr)                                                                  \
     do {                                                                               \
         hipError_t e_ = (expr);                                                        \
-        if (e_ != hipSuccess)                                                          \
-            return fail(TTP_ERR_HIP, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+        if (e_ != hipSuccess) {                                                        \
+            (void)hipGetLastError();                                                   \
+            return fail(e_ == hipErrorOutOfMemory ? TTP_ERR_OOM : TTP_ERR_HIP,         \
+                        std::string(#expr) + ": " + hipGetErrorString(e_));            \
+        }                                                                              \
     } while (0)
+
+// Kernel launches report their errors through hipGetLastError(), which returns the last
+// error of any earlier HIP call on this thread (the caller's or torch's included).  It is
+// reset before each launch, so that the check after it sees that launch's error only.
+inline void clear_hip_error() { (void)hipGetLastError(); }
 
 constexpr uint64_t kAlign = 64;  // elements
 // Largest store: 2^40 elements (4 TiB of fp32 per buffer, far beyond one GPU's 288 GB), so the
@@ -220,6 +230,7 @@ int zero_device(ttp_ctx* c, void* p, uint64_t bytes) {
     const uint64_t words = (bytes + 3) / 4;
     const uint32_t grid = (uint32_t)std::min<uint64_t>((words + ttp::kBlock - 1) / ttp::kBlock,
                                                        (uint64_t)c->num_cus * 16);
+    clear_hip_error();
     hipLaunchKernelGGL(ttp::fill_zero_kernel, dim3(grid), dim3(ttp::kBlock), 0, c->stream,
                        (uint32_t*)p, words);
     HIP_TRY(hipGetLastError());
@@ -406,6 +417,7 @@ int launch_prologue(ttp_ctx* c, const WorkTables* w, bool run_norm, double max_n
     const int32_t scaler_on = c->scaler.enabled ? 1 : 0;
     TimedLaunch tl(c, TTP_KERNEL_NORM);
     if (run_norm) {
+        clear_hip_error();
         if (c->mode == TTP_MODE_MIXED)
             hipLaunchKernelGGL(ttp::norm_partials_kernel<uint16_t>, dim3(grid), dim3(ttp::kBlock),
                                0, c->stream, (const uint16_t*)c->grad, chunks, n,
@@ -430,6 +442,7 @@ int launch_prologue(ttp_ctx* c, const WorkTables* w, bool run_norm, double max_n
     a.bias_len = c->bias_len;
     a.want_bias = want_bias ? 1 : 0;
     a.st = c->st;
+    clear_hip_error();
     hipLaunchKernelGGL(ttp::norm_finalize_kernel, dim3(1), dim3(ttp::kBlock), 0, c->stream, a);
     HIP_TRY(hipGetLastError());
     tl.done();
@@ -558,6 +571,7 @@ constexpr uint64_t kPieceElems = 16ull << 20;
 // slot elements [first, first + n) of record-stored buffer `which` -> contiguous device array
 int gather_slot(ttp_ctx* c, int which, uint64_t first, uint64_t n, float* dst) {
     if (!n) return TTP_OK;
+    clear_hip_error();
     hipLaunchKernelGGL(ttp::gather_slot_kernel, dim3(elementwise_grid(c, n)), dim3(ttp::kBlock),
                        0, c->stream, (const float*)buffer_base(c, which),
                        buffer_stride(c, which), first, n, dst);
@@ -571,6 +585,7 @@ int scatter_slot(ttp_ctx* c, int which, uint64_t first, uint64_t n, const float*
     if (!n) return TTP_OK;
     uint16_t* p16 = (c->mode == TTP_MODE_MIXED && which == TTP_BUF_MASTER) ? (uint16_t*)c->param
                                                                           : nullptr;
+    clear_hip_error();
     hipLaunchKernelGGL(ttp::scatter_slot_kernel, dim3(elementwise_grid(c, n)), dim3(ttp::kBlock),
                        0, c->stream, (float*)buffer_base(c, which), buffer_stride(c, which),
                        first, n, src, p16);
@@ -886,6 +901,7 @@ int ttp_upload(ttp_ctx* c, int which, uint32_t index, const void* src, uint64_t 
                                kind == TTP_HOST ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice,
                                c->stream));
         if (c->mode == TTP_MODE_MIXED && which == TTP_BUF_PARAM) {
+            clear_hip_error();
             hipLaunchKernelGGL(ttp::bf16_to_master_kernel, dim3(elementwise_grid(c, cnt)),
                                dim3(ttp::kBlock), 0, c->stream, (const uint16_t*)c->param,
                                c->master, buffer_stride(c, TTP_BUF_MASTER), off, cnt);
@@ -967,6 +983,7 @@ int ttp_zero_grad_subset(ttp_ctx* c, const uint32_t* indices, uint32_t n, int se
     if ((rc = select_tables(c, indices ? indices : &none, n, &w, &active, false))) return rc;
     if (w->n_chunks) {
         const uint32_t grid = w->n_chunks;
+        clear_hip_error();
         if (c->mode == TTP_MODE_MIXED)
             hipLaunchKernelGGL(ttp::zero_chunks_kernel<uint16_t>, dim3(grid), dim3(ttp::kUpdBlock),
                                0, c->stream, (uint16_t*)c->grad, w->chunks, w->n_chunks);
@@ -1006,6 +1023,7 @@ int ttp_accumulate_grad(ttp_ctx* c, uint32_t index, const void* src, uint64_t n,
         const int first = t.has_grad ? 0 : 1;
         const uint32_t grid = elementwise_grid(c, n);
         const bool mixed = c->mode == TTP_MODE_MIXED;
+        clear_hip_error();
         if (mixed && dtype == TTP_DTYPE_BF16)
             hipLaunchKernelGGL((ttp::accumulate_grad_kernel<uint16_t, uint16_t>), dim3(grid),
                                dim3(ttp::kBlock), 0, c->stream, (uint16_t*)c->grad + t.offset,
@@ -1091,6 +1109,7 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
         const uint16_t* g16 = (const uint16_t*)c->grad;
         const float* g32 = (const float*)c->grad;
         uint16_t* p16 = (uint16_t*)c->param;
+        clear_hip_error();
         if (c->mode == TTP_MODE_MIXED && cached)
             hipLaunchKernelGGL((ttp::adam_kernel<uint16_t, true, true>), grid, block, c->upd_lds,
                                c->stream, g16, c->master, c->exp_avg, c->exp_avg_sq, p16, a);
@@ -1162,6 +1181,7 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
         const uint16_t* g16 = (const uint16_t*)c->grad;
         const float* g32 = (const float*)c->grad;
         uint16_t* p16 = (uint16_t*)c->param;
+        clear_hip_error();
         if (c->mode == TTP_MODE_MIXED && cached)
             hipLaunchKernelGGL((ttp::sgd_kernel<uint16_t, true, true>), grid, block, c->upd_lds,
                                c->stream, g16, c->master, c->momentum, p16, a);
@@ -1186,6 +1206,7 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
             if (needed) {
                 const uint32_t g =
                     std::max<uint32_t>(1, std::min<uint32_t>((n + ttp::kBlock - 1) / ttp::kBlock, 1024));
+                clear_hip_error();
                 hipLaunchKernelGGL(ttp::mark_mom_init_kernel, dim3(g), dim3(ttp::kBlock), 0,
                                    c->stream, chunks, n, c->mom_init, (const DevState*)c->st,
                                    scaler ? 1 : 0);

@@ -5,10 +5,10 @@ optimizers of the reference's py/optim.py (`SGD`, `Adam`) plus `AdamW`, each ste
 multi-tensor HIP launch.  Importing fails if the HIP library is not built.
 """
 from . import _lib
-from ._lib import TTPError, TTPValueError, device_count
+from ._lib import TTPError, TTPMemoryError, TTPValueError, device_count
 from .optim import SGD, Adam, AdamW
 from .store import GradView, Parameter, ParamStore, StepGraph, Tensor, TraceContext
 
 __all__ = ["SGD", "Adam", "AdamW", "ParamStore", "Tensor", "Parameter", "GradView",
            "StepGraph", "TraceContext",
-           "TTPError", "TTPValueError", "device_count", "_lib"]
+           "TTPError", "TTPValueError", "TTPMemoryError", "device_count", "_lib"]

@@ -111,6 +111,10 @@ class TTPValueError(TTPError, ValueError):
     """Argument errors: the cases py/optim.py raises ValueError for."""
 
 
+class TTPMemoryError(TTPError, MemoryError):
+    """A device or pinned-host allocation did not fit (TTP_ERR_OOM)."""
+
+
 def _bind_one_hip_runtime():
     """Load torch (when installed) before libttperf_hip.
 
@@ -149,6 +153,8 @@ def check(rc):
         msg = lib.ttp_last_error().decode(errors="replace")
         if rc in (ERR_INVALID, ERR_RANGE):
             raise TTPValueError(rc, msg)
+        if rc == ERR_OOM:
+            raise TTPMemoryError(rc, msg)
         raise TTPError(rc, msg)
     return rc
 
