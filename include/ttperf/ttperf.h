@@ -185,7 +185,10 @@ int ttp_buffer_layout(ttp_ctx* ctx, int which, void** base, uint32_t* group, uin
 /* Copy n elements (exactly the tensor's numel, or the flat total for TTP_ALL_TENSORS)
  * in the buffer's element type.  Uploading GRAD marks the tensor(s) as having a grad.
  * MIXED mode keeps the two weight copies consistent: uploading MASTER also writes
- * PARAM = RNE_bf16(MASTER), uploading PARAM also writes MASTER = float(PARAM). */
+ * PARAM = RNE_bf16(MASTER), uploading PARAM also writes MASTER = float(PARAM).
+ * A TTP_DEVICE pointer (here and in ttp_accumulate_grad) must be device or managed memory of
+ * the context's device, with all n elements inside one allocation: other pointers are refused
+ * with TTP_ERR_INVALID, a buffer too short with TTP_ERR_RANGE, before any work is queued. */
 int ttp_upload(ttp_ctx* ctx, int which, uint32_t index, const void* src, uint64_t n,
                int src_kind);
 int ttp_download(ttp_ctx* ctx, int which, uint32_t index, void* dst, uint64_t n,

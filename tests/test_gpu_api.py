@@ -518,3 +518,58 @@ def test_out_of_memory_is_reported_and_stale_hip_errors_are_not_misattributed():
     ref.adam_step(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, decoupled=True)
     compare_state(store, ref, max_ulp=0)
     store.close()
+
+
+def test_device_transfers_refuse_host_pointers_and_short_buffers():
+    """TTP_DEVICE uploads and downloads and device gradient sources are read or written by the
+    GPU directly.  A host pointer, or a device buffer shorter than the elements requested, is
+    refused on the host (TTP_ERR_INVALID / TTP_ERR_RANGE) before anything is launched, and the
+    store is left as it was.  Before each refused call the test checks, through the HIP
+    runtime itself, the fact the library's check relies on (the pointer is not device memory;
+    the allocation is shorter than the request)."""
+    import ctypes
+
+    import ttperf
+    from ttperf import _lib as L
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    store = ttperf.ParamStore([(1 << 20,), (64,)], mode="mixed")
+    before = [store.download(b).tobytes() for b in (L.BUF_MASTER, L.BUF_GRAD, L.BUF_PARAM)]
+    n = 1 << 20
+    host = np.zeros(n, np.float32)
+    attr = (ctypes.c_int * 16)()
+    if hip.hipPointerGetAttributes(attr, ctypes.c_void_p(host.ctypes.data)) == 0:
+        assert attr[0] not in (2, 3), "the runtime calls a numpy buffer device memory"
+    hip.hipGetLastError()
+    cases = [
+        lambda: L.lib.ttp_accumulate_grad(store.handle, 0, host.ctypes.data, n, L.DTYPE_F32,
+                                          L.DEVICE),
+        lambda: L.lib.ttp_upload(store.handle, L.BUF_MASTER, 0, host.ctypes.data, n, L.DEVICE),
+        lambda: L.lib.ttp_download(store.handle, L.BUF_MASTER, 0, host.ctypes.data, n, L.DEVICE),
+        lambda: L.lib.ttp_upload(store.handle, L.BUF_GRAD, 0, host.ctypes.data, n, L.DEVICE),
+    ]
+    for k, call in enumerate(cases):
+        assert call() == L.ERR_INVALID, k
+        assert "is not device memory" in L.lib.ttp_last_error().decode()
+    # a 1 MiB device allocation offered as the 4 MiB fp32 source of tensor 0
+    dev = ctypes.c_void_p()
+    assert hip.hipMalloc(ctypes.byref(dev), ctypes.c_size_t(1 << 20)) == 0
+    base, size = ctypes.c_void_p(), ctypes.c_size_t()
+    assert hip.hipMemGetAddressRange(ctypes.byref(base), ctypes.byref(size), dev) == 0
+    assert base.value == dev.value and size.value < 4 * n, size.value
+    try:
+        for call in (
+            lambda: L.lib.ttp_accumulate_grad(store.handle, 0, dev.value, n, L.DTYPE_F32,
+                                              L.DEVICE),
+            lambda: L.lib.ttp_upload(store.handle, L.BUF_MASTER, 0, dev.value, n, L.DEVICE),
+            lambda: L.lib.ttp_download(store.handle, L.BUF_MASTER, 0, dev.value, n, L.DEVICE),
+        ):
+            assert call() == L.ERR_RANGE
+            assert "do not fit its allocation" in L.lib.ttp_last_error().decode()
+        # the same buffer is accepted for what fits in it: the 64-element tensor 1
+        assert L.lib.ttp_download(store.handle, L.BUF_MASTER, 1, dev.value, 64, L.DEVICE) == 0
+        store.sync()
+    finally:
+        assert hip.hipFree(dev) == 0
+    assert [store.download(b).tobytes() for b in (L.BUF_MASTER, L.BUF_GRAD, L.BUF_PARAM)] == before
+    assert not store.has_grad(0)
+    store.close()

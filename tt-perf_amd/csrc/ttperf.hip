@@ -480,6 +480,39 @@ int fill_report(ttp_ctx* c, bool norm_ran, ttp_step_report* r) {
     return TTP_OK;
 }
 
+// A caller's buffer that the GPU reads or writes directly (TTP_DEVICE transfers, device
+// gradient sources): [p, p + bytes) must be device (or managed) memory of this context's
+// device, inside one allocation.  A host pointer, another device's memory or a short buffer
+// is refused here, before any launch or copy touches it.
+int check_device_buffer(const ttp_ctx* c, const void* p, uint64_t bytes, const char* what) {
+    if (!bytes) return TTP_OK;
+    hipPointerAttribute_t at{};
+    if (hipPointerGetAttributes(&at, p) != hipSuccess) {
+        clear_hip_error();
+        return fail(TTP_ERR_INVALID, std::string(what) +
+                                         " is not device memory (use TTP_HOST for host memory)");
+    }
+    if (at.type != hipMemoryTypeDevice && at.type != hipMemoryTypeManaged)
+        return fail(TTP_ERR_INVALID, std::string(what) +
+                                         " is not device memory (use TTP_HOST for host memory)");
+    if (at.type == hipMemoryTypeDevice && at.device != c->device)
+        return fail(TTP_ERR_INVALID, std::string(what) + " is on device " +
+                                         std::to_string(at.device) + ", the context on device " +
+                                         std::to_string(c->device));
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p) != hipSuccess) {
+        clear_hip_error();
+        return fail(TTP_ERR_INVALID, std::string(what) + " lies in no known device allocation");
+    }
+    const uintptr_t lo = (uintptr_t)p, end = (uintptr_t)base + size;
+    if (lo < (uintptr_t)base || bytes > end - lo)
+        return fail(TTP_ERR_RANGE, std::string(what) + ": " + std::to_string(bytes) +
+                                       " bytes do not fit its allocation (" +
+                                       std::to_string(end - lo) + " bytes from the pointer on)");
+    return TTP_OK;
+}
+
 int check_index(const ttp_ctx* c, uint32_t i) {
     if (i >= c->tensors.size())
         return fail(TTP_ERR_RANGE, "tensor index " + std::to_string(i) + " out of range");
@@ -891,6 +924,8 @@ int ttp_upload(ttp_ctx* c, int which, uint32_t index, const void* src, uint64_t 
     uint64_t off, cnt;
     if ((rc = resolve_range(c, index, n, &off, &cnt))) return rc;
     const size_t es = buffer_esize(c, which);
+    if (kind == TTP_DEVICE && (rc = check_device_buffer(c, src, cnt * es, "the upload source")))
+        return rc;
     if (cnt && in_records(c, which)) {
         // record-stored state; a MIXED master upload also writes the bf16 copy
         if ((rc = upload_slot(c, which, off, cnt, src, kind))) return rc;
@@ -929,6 +964,9 @@ int ttp_download(ttp_ctx* c, int which, uint32_t index, void* dst, uint64_t n, i
     uint64_t off, cnt;
     if ((rc = resolve_range(c, index, n, &off, &cnt))) return rc;
     const size_t es = buffer_esize(c, which);
+    if (kind == TTP_DEVICE &&
+        (rc = check_device_buffer(c, dst, cnt * es, "the download destination")))
+        return rc;
     if (cnt && in_records(c, which)) {
         if ((rc = download_slot(c, which, off, cnt, dst, kind))) return rc;
         if (kind == TTP_HOST) HIP_TRY(hipStreamSynchronize(c->stream));
@@ -1013,6 +1051,9 @@ int ttp_accumulate_grad(ttp_ctx* c, uint32_t index, const void* src, uint64_t n,
     if (!src && n) return fail(TTP_ERR_INVALID, "null source");
     if ((rc = set_dev(c))) return rc;
     const size_t sbytes = dtype == TTP_DTYPE_BF16 ? 2 : 4;
+    if (kind == TTP_DEVICE &&
+        (rc = check_device_buffer(c, src, n * sbytes, "the incoming gradient")))
+        return rc;
     if (n) {
         const void* dsrc = src;
         if (kind == TTP_HOST) {
