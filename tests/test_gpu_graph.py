@@ -330,3 +330,27 @@ def test_graph_replay_hands_the_step_count_back_to_its_optimizer():
     assert counts == {"a": 5, "b": 4}
     graph.close()
     store.close()
+
+
+def test_closing_a_capturing_store_ends_its_capture():
+    """Closing a store in the middle of its own capture discards the capture, resumes the
+    cyclic collector the capture paused, and destroys the store; other stores work after."""
+    import gc
+
+    import ttperf
+    from ttperf import store as S
+    was = gc.isenabled()
+    store = ttperf.ParamStore([(100,), (64, 8)], mode="mixed")
+    store.tensors[0].grad = np.zeros(100, np.uint16)
+    store.adam_step(lr=1e-3)
+    store.begin_capture()
+    store.adam_step(lr=1e-3)
+    assert not gc.isenabled() and S._capturing == 1
+    store.close()
+    assert S._capturing == 0 and gc.isenabled() == was
+    assert store.handle is None
+    other = ttperf.ParamStore([(10,)], mode="fp32")
+    other.tensors[0].grad = np.ones(10, np.float32)
+    r = other.adam_step(lr=1e-3, report=True)
+    assert r["step"] == 1
+    other.close()

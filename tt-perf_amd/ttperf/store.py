@@ -246,8 +246,12 @@ class ParamStore:
     # ---- lifetime --------------------------------------------------------------------------
     def close(self):
         if getattr(self, "_h", None):
-            if _capturing and not getattr(self, "_in_capture", False):
-                _deferred.append(self)  # destroyed when the capture ends
+            if getattr(self, "_in_capture", False):
+                # closing a capturing store discards its capture first, which also resumes
+                # the collector and the deferred closes the capture paused
+                self.end_capture(discard=True)
+            if _capturing:
+                _deferred.append(self)  # another store is capturing: destroyed when it ends
                 return
             for g in list(getattr(self, "_graphs", ())):
                 g.close()  # a context's graphs go before the context
