@@ -573,3 +573,30 @@ def test_device_transfers_refuse_host_pointers_and_short_buffers():
     assert [store.download(b).tobytes() for b in (L.BUF_MASTER, L.BUF_GRAD, L.BUF_PARAM)] == before
     assert not store.has_grad(0)
     store.close()
+
+
+def test_download_into_out_checks_the_buffer():
+    """download(..., out=...) fills the caller's buffer in place; one of the wrong size, type
+    or layout is refused before anything is written."""
+    import ttperf
+    from ttperf import _lib as L
+    torch = torch_mod()
+    store = ttperf.ParamStore([(100,), (64, 8)], mode="mixed")
+    store.tensors[1].set_data(np.arange(512, dtype=np.float32))
+    bad = [np.empty(511, np.float32), np.empty(512, np.float64), np.empty(1024, np.float32)[::2],
+           torch.empty(511, device="cuda"), torch.empty(1024, device="cuda")[::2],
+           torch.empty(512, dtype=torch.bfloat16, device="cuda")]
+    for out in bad:
+        with pytest.raises(ValueError):
+            store.download(L.BUF_MASTER, 1, out=out)
+    ro = np.empty(512, np.float32)
+    ro.flags.writeable = False
+    with pytest.raises(ValueError):
+        store.download(L.BUF_MASTER, 1, out=ro)
+    good = np.empty(512, np.float32)
+    assert store.download(L.BUF_MASTER, 1, out=good) is good
+    assert np.array_equal(good, np.arange(512, dtype=np.float32))
+    dev = torch.empty(512, device="cuda")
+    store.download(L.BUF_MASTER, 1, out=dev)
+    assert np.array_equal(dev.cpu().numpy(), good)
+    store.close()

@@ -347,8 +347,15 @@ class ParamStore:
         L.check(L.lib.ttp_upload(self._h, which, index, a.ctypes.data_as(C.c_void_p), n, L.HOST))
 
     def download(self, which, index=L.ALL_TENSORS, out=None):
+        """The buffer's elements (bf16 as uint16 bits), into a new numpy array or into `out`:
+        a contiguous, writable numpy array or torch tensor (host or device) of exactly the
+        element count and element size, which the ABI fills in place."""
         n = self._numel(index)
         if out is not None and _is_torch(out):
+            if out.numel() != n or out.element_size() != self._esize(which) or \
+                    not out.is_contiguous():
+                raise ValueError(f"out must be a contiguous tensor of {n} elements of "
+                                 f"{self._esize(which)} bytes")
             kind = L.DEVICE if out.is_cuda else L.HOST
             if out.is_cuda:
                 import torch
@@ -357,7 +364,14 @@ class ParamStore:
             if kind == L.DEVICE:
                 self.sync()
             return out
-        a = np.empty(n, self._host_dtype(which)) if out is None else out
+        if out is None:
+            a = np.empty(n, self._host_dtype(which))
+        else:
+            a = out
+            if not isinstance(a, np.ndarray) or a.dtype != self._host_dtype(which) or \
+                    a.size != n or not a.flags.c_contiguous or not a.flags.writeable:
+                dt = self._host_dtype(which).__name__
+                raise ValueError(f"out must be a contiguous, writable {dt} array of {n} elements")
         L.check(L.lib.ttp_download(self._h, which, index, a.ctypes.data_as(C.c_void_p), n, L.HOST))
         return a
 
