@@ -600,3 +600,77 @@ def test_download_into_out_checks_the_buffer():
     store.download(L.BUF_MASTER, 1, out=dev)
     assert np.array_equal(dev.cpu().numpy(), good)
     store.close()
+
+
+def test_store_beyond_2_to_the_32_elements():
+    """Offsets past 2^32 elements (64-bit indexing in every kernel and host path): an fp32
+    store of one 4.3G-element tensor and one more tensor behind it (69 GB of HBM).  The big
+    tensor's first and last 2048 weights and grads are set through zero-copy views, its
+    middle stays zero (zero grads leave zero weights and moments unchanged and add nothing to
+    the norm), and the second tensor goes through the API's upload, download and accumulate
+    paths.  Two clipped AdamW steps over the whole store must match an oracle holding just the
+    head, the tail and the second tensor; the moments are read through ttp_buffer_layout's
+    addressing."""
+    import ttperf
+    from ttperf import _lib as L
+    torch = torch_mod()
+    big, k = (1 << 32) + 1000, 2048
+    store = ttperf.ParamStore([(big,), (4096,)], mode="fp32", decay=[True, False])
+    assert store.offsets[1] > (1 << 32)
+    ref = O.OracleStore([k, k, 4096], flags=[1, 1, 0], mode=O.MODE_FP32, nthreads=4)
+    rng = np.random.default_rng(110)
+    master = store.torch_view(L.BUF_MASTER, 0)
+    grad = store.torch_view(L.BUF_GRAD, 0)
+    head_w, tail_w = [rng.normal(0, 0.02, k).astype(np.float32) for _ in range(2)]
+    w1 = rng.normal(0, 0.02, 4096).astype(np.float32)
+    master[:k] = torch.from_numpy(head_w).cuda()
+    master[-k:] = torch.from_numpy(tail_w).cuda()
+    torch.cuda.synchronize()
+    store.tensors[1].set_data(w1)
+    for i, w in enumerate((head_w, tail_w, w1)):
+        ref.set_master(i, w)
+    hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, decoupled=True)
+    for step in range(2):
+        gh, gt, g1 = [(rng.standard_normal(n) * 3e-2).astype(np.float32) for n in (k, k, 4096)]
+        grad[:k] = torch.from_numpy(gh).cuda()
+        grad[-k:] = torch.from_numpy(gt).cuda()
+        torch.cuda.synchronize()
+        store.mark_grads([0])
+        store.set_has_grad(1, False)
+        store.tensors[1].accumulate_grad(g1)  # the accumulate path at an offset past 2^32
+        for i, g in enumerate((gh, gt, g1)):
+            ref.set_grad(i, g)
+        r = store.adam_step(report=True, max_grad_norm=1.0, **hp)
+        e = ref.adam_step(max_grad_norm=1.0, **hp)
+        print(f"step {step}: norm {r['grad_norm']:.6f} (oracle {e['grad_norm']:.6f})", flush=True)
+        assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
+        assert e["clip_coef"] < 1.0  # the clip is active
+    torch.cuda.synchronize()
+
+    def check(got, want, what):
+        d = f32_ulp_diff(np.ascontiguousarray(got), want)
+        assert d.max() <= 2, f"{what}: {d.max()} ulp"
+
+    check(master[:k].cpu().numpy(), ref.view("master", 0), "head master")
+    check(master[-k:].cpu().numpy(), ref.view("master", 1), "tail master")
+    check(store.download(L.BUF_MASTER, 1), ref.view("master", 2), "tensor 1 master")
+    mid = master[k:-k]  # the untouched middle: min and max on the device, no temporaries
+    assert float(mid.min()) == 0.0 and float(mid.max()) == 0.0
+    for which, name in ((L.BUF_EXP_AVG, "exp_avg"), (L.BUF_EXP_AVG_SQ, "exp_avg_sq")):
+        base, group, stride = store.layout(which)
+        assert (group, stride) == (64, 128)
+        for (lo, hi), i in (((0, k), 0), ((big - k, big), 1)):
+            r0, r1 = lo // group, (hi + group - 1) // group
+            addr = base + r0 * stride * 4
+
+            class _Records:  # records r0..r1-1 of the slot, as (records, stride) fp32
+                __cuda_array_interface__ = {"data": (addr, False),
+                                            "shape": (r1 - r0, stride), "typestr": "<f4",
+                                            "strides": None, "version": 3}
+
+            recs = torch.as_tensor(_Records(), device="cuda")[:, :group].reshape(-1)
+            vals = recs[lo - r0 * group: hi - r0 * group].cpu().numpy()
+            check(vals, ref.view(name, i), f"{name} {'head' if i == 0 else 'tail'}")
+        check(store.download(which, 1), ref.view(name, 2), f"{name} tensor 1")
+    del master, grad, mid
+    store.close()
