@@ -78,7 +78,7 @@ int main() {
     {
         ParamArena arena3(ttp::Mode::FP32);
         traced::TracedLinear a(16, 8, 0.01f, arena3), b(8, 4, 0.02f, arena3);
-        traced::TracedSGD opt({&a, &b}, 0.1f);
+        traced::TracedSGD opt2({&a, &b}, 0.1f);
         std::vector<ValuePtr> ps = {a.weight, a.bias, b.weight, b.bias};
         std::vector<std::vector<float>> wr;
         for (auto& p : ps) wr.push_back(p->master());
@@ -91,9 +91,9 @@ int main() {
                     ps[k]->grad = gr.back();
                 }
                 if (it == 0)
-                    opt.step();  // eager once: the work tables exist before capture
+                    opt2.step();  // eager once: the work tables exist before capture
                 else
-                    trace.run([&] { opt.step(); });
+                    trace.run([&] { opt2.step(); });
                 for (size_t k = 0; k < ps.size(); ++k) wr[k] = sgd_ref(wr[k], gr[k], 0.1f);
                 for (size_t k = 0; k < ps.size(); ++k)
                     test::assert_bits(ps[k]->master(), wr[k],
