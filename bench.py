@@ -251,6 +251,59 @@ def main():
         skip_ms = e0.elapsed_time(e1)
         assert rs is None
 
+    # context: the step when its norm comes from per-tensor sums taken bucket by bucket (about
+    # 25 MB of gradients each, reverse tensor order, as a backward produces them), which can
+    # run beside the backward's compute; the step then runs the finalize and the update only
+    sums = None
+    if cfg["hp"]["max_grad_norm"] or cfg["scaler"]:
+        esz = 2 if mode == "mixed" else 4
+        buckets, cur, cur_bytes = [], [], 0
+        for i in reversed(range(len(numels))):
+            cur.append(i)
+            cur_bytes += numels[i] * esz
+            if cur_bytes >= 25 << 20:
+                buckets.append(sorted(cur))
+                cur, cur_bytes = [], 0
+        if cur:
+            buckets.append(sorted(cur))
+
+        def bucket_sums():
+            for b in buckets:
+                store.grad_sumsq_tensors(b)
+
+        def step_from_sums():
+            bucket_sums()
+            if args.optimizer == "adamw":
+                store.adam_step(tensor_sums=True, **hp)
+            else:
+                store.sgd_step(lr=hp["lr"], momentum=0.9, max_grad_norm=hp["max_grad_norm"],
+                               tensor_sums=True)
+
+        store.upload(L.BUF_GRAD, 0, torch.zeros(store.tensors[0].numel, device=dev,
+                                                dtype=torch.bfloat16 if mode == "mixed"
+                                                else torch.float32))  # undo the overflow
+        for _ in range(3):
+            step_from_sums()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(args.steps):
+            bucket_sums()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        sums_ms = e0.elapsed_time(e1) / args.steps
+        e0.record(stream)
+        for _ in range(args.steps):
+            step_from_sums()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        both_ms = e0.elapsed_time(e1) / args.steps
+        sums = {"buckets": len(buckets), "bucket_sums_ms": round(sums_ms, 4),
+                "sums_and_step_ms": round(both_ms, 4),
+                "step_after_sums_ms": round(both_ms - sums_ms, 4),
+                "note": "ttp_grad_sumsq_tensors per bucket, then the step with "
+                        "TTP_STEP_TENSOR_SUMS; in training the bucket sums overlap the "
+                        "backward, leaving step_after_sums_ms on the step's own path"}
+
     # context: the practical ceilings of the update's traffic on this GPU, over the update's
     # byte count: torch's device copy (a blit kernel), and libttperf_ceiling's non-temporal
     # 16-byte copy (the update's 50/50 read/write mix) and read-only pass
@@ -338,6 +391,7 @@ def main():
         "kernels_ms": {"norm_pass": round(nrm_avg, 4), "update": round(upd_avg, 4),
                        "source": "second pass of K steps with an event pair per launch"},
         "skipped_step_ms": round(skip_ms, 4) if skip_ms is not None else None,
+        "bucketed_norm": sums,
         "torch_copy_GBps": round(copy_gbps, 1),
         "ceilings": {"nt_copy_GBps": round(nt_copy_gbps, 1),
                      "nt_copy_frac": round(nt_copy_gbps / HBM_PEAK_GBPS, 4),

@@ -104,7 +104,7 @@ typedef struct ttp_adam_hparams {
     double eps;           /* > 0 */
     double weight_decay;  /* >= 0; applied only to TTP_TENSOR_DECAY tensors */
     int32_t decoupled;    /* 1: AdamW (p *= 1 - lr*wd first); 0: L2 (g += wd*p)   */
-    int32_t reserved;
+    int32_t flags;        /* TTP_STEP_* (0: none) */
     double max_grad_norm; /* > 0: clip the global L2 norm to this; <= 0: no clipping */
 } ttp_adam_hparams;
 
@@ -117,9 +117,20 @@ typedef struct ttp_sgd_hparams {
     double dampening;     /* any; torch semantics */
     double weight_decay;  /* >= 0 */
     int32_t nesterov;     /* requires momentum > 0 and dampening == 0 */
-    int32_t reserved;
+    int32_t flags;        /* TTP_STEP_* (0: none) */
     double max_grad_norm; /* > 0: clip; <= 0: off */
 } ttp_sgd_hparams;
+
+/* Step flags.
+ * TTP_STEP_TENSOR_SUMS: take the gradient norm (and the inf/NaN check) from the per-tensor
+ *   sums of squares that ttp_grad_sumsq_tensors stored for the step's tensors, instead of a
+ *   norm pass over all their gradients.  Every tensor the step updates needs a current sum:
+ *   one computed after its last gradient write through this ABI (upload, accumulate, zero,
+ *   set_has_grad) and after the previous step; otherwise the step fails with TTP_ERR_STATE
+ *   before any work is queued.  Gradients written through a device pointer after their sum
+ *   was taken are the caller's to avoid.  The norm is the same sum of the same squares, added
+ *   in another order: it can differ from the norm pass's in the last bits. */
+#define TTP_STEP_TENSOR_SUMS 1
 
 /* Dynamic loss scaling (torch.amp.GradScaler semantics).  While enabled, every step
  * unscales the gradients by 1/scale, skips the whole update when any gradient is
@@ -233,6 +244,15 @@ int ttp_sgd_step_subset(ttp_ctx* ctx, const ttp_sgd_hparams* hp, const uint32_t*
 /* Global L2 norm of the gradients that exist, unscaled by the current loss scale when
  * scaling is on (synchronous; does not change any state). */
 int ttp_grad_norm(ttp_ctx* ctx, double* norm);
+/* Per-tensor sums of squares of the listed tensors' gradients (those that have one),
+ * unscaled by the current loss scale, kept on the device for a following step with
+ * TTP_STEP_TENSOR_SUMS.  Meant for buckets of tensors whose gradients became final during the
+ * backward: each call is a memory-bound pass over the bucket's gradients that can run on a
+ * stream beside the backward's compute (ttp_set_stream, with the caller's events ordering it
+ * after the bucket's producers), taking the norm pass off the step.  Asynchronous on the
+ * context's stream; each tensor's sum adds its 16 KiB tiles' sums in tile order.  No
+ * counterpart in the reference, whose optimizer has no gradient norm. */
+int ttp_grad_sumsq_tensors(ttp_ctx* ctx, const uint32_t* indices, uint32_t n);
 
 /* ---- step counter and loss scaler ------------------------------------------------------- */
 int ttp_get_step(ttp_ctx* ctx, uint64_t* step);

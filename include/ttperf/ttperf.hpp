@@ -45,8 +45,10 @@ struct AdamOptions {
     double lr = 1e-3, beta1 = 0.9, beta2 = 0.999, eps = 1e-8, weight_decay = 0.0;
     bool decoupled = true;
     double max_grad_norm = 0.0;
+    bool tensor_sums = false;  // norm from Store::grad_sumsq_tensors (TTP_STEP_TENSOR_SUMS)
     ttp_adam_hparams c() const {
         ttp_adam_hparams h{};
+        h.flags = tensor_sums ? TTP_STEP_TENSOR_SUMS : 0;
         h.lr = lr;
         h.beta1 = beta1;
         h.beta2 = beta2;
@@ -62,8 +64,10 @@ struct SgdOptions {
     double lr = 1e-2, momentum = 0.0, dampening = 0.0, weight_decay = 0.0;
     bool nesterov = false;
     double max_grad_norm = 0.0;
+    bool tensor_sums = false;  // norm from Store::grad_sumsq_tensors (TTP_STEP_TENSOR_SUMS)
     ttp_sgd_hparams c() const {
         ttp_sgd_hparams h{};
+        h.flags = tensor_sums ? TTP_STEP_TENSOR_SUMS : 0;
         h.lr = lr;
         h.momentum = momentum;
         h.dampening = dampening;
@@ -221,6 +225,10 @@ public:
         else
             check(ttp_sgd_step(ctx_, &h, rp));
         return r;
+    }
+    // per-tensor gradient sums of the listed tensors, for a step with tensor_sums set
+    void grad_sumsq_tensors(const std::vector<uint32_t>& indices) {
+        check(ttp_grad_sumsq_tensors(ctx_, indices.data(), (uint32_t)indices.size()));
     }
     double grad_norm() {
         double n = 0;

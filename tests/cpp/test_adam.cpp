@@ -3,6 +3,7 @@
 // double, rounded to fp32 like full_like(fill_value=...)); the expected values below apply
 // the same op order on the host with one rounding per op.  AdamW decays only the
 // decay-flagged (2-D weight) tensors: p *= (float)(1 - lr*wd) before the Adam update.
+#include <algorithm>
 #include <cmath>
 
 #include "autograd/nn.hpp"
@@ -188,12 +189,54 @@ static void run_graph_groups() {
     }
 }
 
+// AdamW with clipping, its norm taken from per-tensor gradient sums (Store::grad_sumsq_tensors,
+// AdamOptions::tensor_sums) against the same optimizer running the norm pass: the two add the
+// same squares in different orders, so the weights agree within 2 ulp.
+static void run_tensor_sums() {
+    ParamArena a1(ttp::Mode::FP32), a2(ttp::Mode::FP32);
+    MLP m1(64, 128, 10, a1), m2(64, 128, 10, a2);
+    auto p1 = m1.parameters(), p2 = m2.parameters();
+    for (size_t k = 0; k < p1.size(); ++k) p2[k]->set_data(p1[k]->master());
+    AdamW o1(p1, 1e-2f, {0.9, 0.95}, 1e-8f, 0.1f, /*max_grad_norm*/ 0.05);
+    AdamW o2(p2, 1e-2f, {0.9, 0.95}, 1e-8f, 0.1f, 0.05);
+    o2.opts.tensor_sums = true;
+    std::vector<uint32_t> all;
+    for (auto& p : p2) all.push_back(p->index);
+    for (int t = 1; t <= 4; ++t) {
+        for (size_t k = 0; k < p1.size(); ++k) {
+            auto g = grad_of(p1[k]->numel(), 500 + t * 10 + (int)k);
+            p1[k]->grad = g;
+            p2[k]->grad = g;
+        }
+        p2[0]->store().grad_sumsq_tensors(all);
+        auto r1 = o1.step(true);
+        auto r2 = o2.step(true);
+        test::check(r1.clip_coef < 1.0f && r2.clip_coef == r1.clip_coef,
+                    "tensor sums: the clip is active and has the same coefficient");
+    }
+    for (size_t k = 0; k < p1.size(); ++k) {
+        const auto w1 = p1[k]->master(), w2 = p2[k]->master();
+        uint32_t worst = 0;
+        for (size_t i = 0; i < w1.size(); ++i) {
+            const uint32_t u1 = test::bits(w1[i]), u2 = test::bits(w2[i]);
+            worst = std::max(worst, u1 > u2 ? u1 - u2 : u2 - u1);
+        }
+        test::check(worst <= 2, "tensor sums: param " + std::to_string(k) + " within 2 ulp of the norm-pass step");
+    }
+    // a step with stale sums throws (nothing updated)
+    p2[0]->grad = grad_of(p2[0]->numel(), 999);
+    bool thrown = false;
+    try { o2.step(); } catch (const std::runtime_error&) { thrown = true; }
+    test::check(thrown, "tensor sums: a step after a gradient write without new sums throws");
+}
+
 int main() {
     test::DeviceGuard dg;
     run(false);
     run(true);
     run_groups();
     run_graph_groups();
+    run_tensor_sums();
     // py/optim.py:33-41 validation
     ParamArena arena;
     Linear l(4, 4, arena);

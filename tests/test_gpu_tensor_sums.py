@@ -1,0 +1,180 @@
+"""GPU tests of bucketed gradient sums (ttp_grad_sumsq_tensors) and steps that take their norm
+from them (TTP_STEP_TENSOR_SUMS) instead of running a norm pass.
+
+The per-tensor sums add the same squares as the norm pass in another order, so the norm may
+differ in its last bits and the clip coefficient, rarely, by one rounding: the state is held
+to the oracle within the 2-ulp bar of the other parity tests, and to an eager twin that runs
+the norm pass.  Skip / found_inf / scale / step-count decisions must be identical."""
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import f32_ulp_diff
+from gpu_util import compare_state, device_grads, make_pair, torch_mod
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(300, 7), (64,), (129, 33), (5,), (2048,), (1, 2049), (4097,), (96, 64), (0,),
+          (40000,), (3,), (8192, 3)]
+DECAY = [len(s) == 2 for s in SHAPES]
+
+
+def _buckets(n, size=4):
+    """Reverse tensor order in buckets, as a backward produces them."""
+    order = list(range(n))[::-1]
+    return [sorted(order[k:k + size]) for k in range(0, n, size)]
+
+
+@pytest.mark.parametrize("mode", [O.MODE_MIXED, O.MODE_FP32])
+def test_step_from_bucket_sums_matches_oracle_and_norm_pass(mode):
+    import ttperf
+    torch = torch_mod()
+    store, ref = make_pair(SHAPES, DECAY, mode, seed=120)
+    twin, _ = make_pair(SHAPES, DECAY, mode, seed=120)  # the same step with its norm pass
+    scaler = mode == O.MODE_MIXED
+    if scaler:
+        for s in (store, twin):
+            s.configure_scaler(True, init_scale=1024.0, growth_interval=2)
+        ref.configure_scaler(True, 1024.0, growth_interval=2)
+    hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, decoupled=True,
+              max_grad_norm=0.5)
+    gen = torch.Generator(device="cuda").manual_seed(121)
+    from ttperf import _lib as L
+    for step in range(6):
+        inf_at = store.offsets[9] + 77 if (scaler and step == 3) else None
+        host = device_grads(store, gen, 1e-2, scale=ref.scale if scaler else 1.0, inf_at=inf_at)
+        twin.upload(L.BUF_GRAD, L.ALL_TENSORS, store.download(L.BUF_GRAD))
+        ref.grad[:store.total] = host
+        for i in range(ref.n):
+            ref.set_has_grad(i, True)
+        for b in _buckets(len(SHAPES)):
+            store.grad_sumsq_tensors(b)
+        r = store.adam_step(report=True, tensor_sums=True, **hp)
+        rt = twin.adam_step(report=True, **hp)
+        e = ref.adam_step(**hp)
+        print(f"step {step}: norm {r['grad_norm']!r} (norm pass {rt['grad_norm']!r}, oracle "
+              f"{e['grad_norm']!r}), skipped {r['skipped']}", flush=True)
+        for k in ("skipped", "found_inf", "step", "scale", "growth_tracker"):
+            assert r[k] == rt[k] == e[k], (k, r, rt, e)
+        if np.isfinite(e["grad_norm"]):
+            assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-10 * e["grad_norm"]
+        compare_state(store, ref, max_ulp=2)
+    for which in (L.BUF_MASTER, L.BUF_EXP_AVG, L.BUF_EXP_AVG_SQ):
+        a, b = store.download(which), twin.download(which)
+        assert f32_ulp_diff(a, b).max() <= 2
+    store.close()
+    twin.close()
+
+
+def test_sgd_momentum_subset_step_from_sums():
+    """SGD with momentum over a subset: only the subset's tensors need sums."""
+    from ttperf import _lib as L
+    torch = torch_mod()
+    store, ref = make_pair(SHAPES, DECAY, O.MODE_FP32, seed=122)
+    gen = torch.Generator(device="cuda").manual_seed(123)
+    subset = [0, 2, 4, 9, 11]
+    hp = dict(lr=1e-2, momentum=0.9, max_grad_norm=0.3)
+    for step in range(4):
+        ref.grad[:store.total] = device_grads(store, gen, 1e-2)
+        store.grad_sumsq_tensors(subset)
+        for i in range(ref.n):
+            ref.set_has_grad(i, i in subset)
+        r = store.sgd_step(report=True, indices=subset, tensor_sums=True, **hp)
+        e = ref.sgd_step(**hp)
+        assert r["step"] == e["step"]
+        assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-10 * e["grad_norm"]
+        compare_state(store, ref, which=("master", "momentum"), max_ulp=2)
+    store.close()
+
+
+def test_stale_or_missing_sums_are_refused():
+    """A step with tensor_sums fails (TTP_ERR_STATE, nothing queued, nothing changed) unless
+    every tensor it updates has a sum taken after its last gradient write and after the
+    previous step."""
+    import ttperf
+    from ttperf import _lib as L
+    torch = torch_mod()
+    store, _ = make_pair(SHAPES, DECAY, O.MODE_MIXED, seed=124)
+    gen = torch.Generator(device="cuda").manual_seed(125)
+    device_grads(store, gen, 1e-2)
+    hp = dict(lr=1e-3, max_grad_norm=1.0, tensor_sums=True)
+
+    def refused(why):
+        t0 = store.step_count
+        master = store.download(L.BUF_MASTER).tobytes()
+        with pytest.raises(ttperf.TTPError) as e:
+            store.adam_step(**hp)
+        assert e.value.code == L.ERR_STATE and "no current gradient sum" in str(e.value), why
+        assert store.step_count == t0 and store.download(L.BUF_MASTER).tobytes() == master, why
+
+    refused("no sums taken")
+    store.grad_sumsq_tensors(range(6))
+    refused("sums of some tensors only")
+    store.grad_sumsq_tensors()
+    store.adam_step(**hp)  # current sums: accepted
+    refused("a step consumed the sums")
+    for write in (lambda: store.tensors[2].__setattr__("grad", np.zeros(129 * 33, np.uint16)),
+                  lambda: store.tensors[3].accumulate_grad(np.ones(5, np.float32)),
+                  lambda: store.mark_grads([4]),
+                  lambda: store.zero_grad(set_to_none=False, indices=[7]),
+                  lambda: store.configure_scaler(True, init_scale=512.0)):
+        store.grad_sumsq_tensors()
+        write()
+        refused("a gradient write or scale change after the sums")
+    store.grad_sumsq_tensors()
+    store.adam_step(**hp)
+    # without clipping or loss scaling there is no norm to take: the flag is accepted
+    store.configure_scaler(False)
+    store.adam_step(lr=1e-3, tensor_sums=True)
+    bad = L.AdamHParams(lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, flags=2)
+    assert L.lib.ttp_adam_step(store.handle, bad, None) == L.ERR_INVALID
+    store.close()
+
+
+def test_graph_of_bucket_sums_and_step_replays():
+    """The bucket sums and the step captured together: each replay (new gradients copied in
+    between, outside the graph) matches an eager twin that runs the norm pass, and the oracle."""
+    from ttperf import _lib as L
+    torch = torch_mod()
+    store, ref = make_pair(SHAPES, DECAY, O.MODE_MIXED, seed=126)
+    twin, _ = make_pair(SHAPES, DECAY, O.MODE_MIXED, seed=126)
+    for s in (store, twin):
+        s.set_stream(None)
+        s.configure_scaler(True, init_scale=4096.0, growth_interval=3)
+    ref.configure_scaler(True, 4096.0, growth_interval=3)
+    hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, decoupled=True,
+              max_grad_norm=0.5)
+    buckets = _buckets(len(SHAPES))
+    gen = torch.Generator(device="cuda").manual_seed(127)
+    graph = None
+    for it in range(5):
+        host = device_grads(store, gen, 1e-2, scale=ref.scale)
+        twin.upload(L.BUF_GRAD, L.ALL_TENSORS, store.download(L.BUF_GRAD))
+        ref.grad[:store.total] = host
+        for i in range(ref.n):
+            ref.set_has_grad(i, True)
+        if it == 0:  # eager once: work tables, tile buffer and bias table exist
+            for b in buckets:
+                store.grad_sumsq_tensors(b)
+            store.adam_step(tensor_sums=True, **hp)
+        else:
+            if graph is None:
+                store.begin_capture()
+                for b in buckets:
+                    store.grad_sumsq_tensors(b)
+                store.adam_step(tensor_sums=True, **hp)
+                graph = store.end_capture()
+            graph.replay()
+        twin.adam_step(**hp)
+        ref.adam_step(**hp)
+        store.sync()
+        print(f"iteration {it}: step {store.step_count}, scale {store.scaler_state()[0]}",
+              flush=True)
+        assert store.step_count == twin.step_count == ref.t
+        assert store.scaler_state() == twin.scaler_state()
+        compare_state(store, ref, max_ulp=2)
+        for which in (L.BUF_MASTER, L.BUF_EXP_AVG, L.BUF_EXP_AVG_SQ):
+            assert f32_ulp_diff(store.download(which), twin.download(which)).max() <= 2
+    graph.close()
+    store.close()
+    twin.close()

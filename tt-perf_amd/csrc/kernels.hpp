@@ -273,6 +273,7 @@ __global__ __launch_bounds__(kBlock) void norm_partials_kernel(const GradT* __re
 // ------------------------------------------------------------------------------------
 struct FinalizeArgs {
     const double* partials;
+    const uint32_t* idx;    // non-null: partial k is partials[idx[k]] (per-tensor sums)
     uint32_t npartials;     // 0: no norm pass ran (step counting only)
     int32_t scaler_on;      // unscale by 1/scale, skip on inf, update the scale
     int32_t count_t;        // the step count lives on the device: advance it (unless skipped)
@@ -297,7 +298,7 @@ __global__ __launch_bounds__(kBlock) void norm_finalize_kernel(FinalizeArgs a) {
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
             const uint32_t b = base + (uint32_t)k * kBlock + threadIdx.x;
-            v[k] = b < a.npartials ? a.partials[b] : 0.0;
+            v[k] = b < a.npartials ? a.partials[a.idx ? a.idx[b] : b] : 0.0;
         }
 #pragma unroll
         for (int k = 0; k < kPer; ++k) s += v[k];
@@ -346,6 +347,23 @@ __global__ __launch_bounds__(kBlock) void norm_finalize_kernel(FinalizeArgs a) {
             }
         }
     }
+}
+
+// Per-tensor sums of squares (ttp_grad_sumsq_tensors), from one norm_partials_kernel block per
+// tile: block t adds the tile sums of the t-th listed tensor, tiles tile_start[t] ..
+// tile_start[t+1]-1, each lane in tile order, then the fixed block reduction, into
+// sums[tensor_ids[t]].
+__global__ __launch_bounds__(kBlock) void tensor_sums_kernel(const double* __restrict__ tile_sums,
+                                                             const uint32_t* __restrict__ tile_start,
+                                                             const uint32_t* __restrict__ tensor_ids,
+                                                             double* __restrict__ sums) {
+    __shared__ double lds[kBlock / 64];
+    const uint32_t t = blockIdx.x;
+    const uint32_t b = tile_start[t], e = tile_start[t + 1];
+    double s = 0.0;
+    for (uint32_t k = b + threadIdx.x; k < e; k += kBlock) s += tile_sums[k];
+    s = block_sum(s, lds);
+    if (threadIdx.x == 0) sums[tensor_ids[t]] = s;
 }
 
 // ------------------------------------------------------------------------------------

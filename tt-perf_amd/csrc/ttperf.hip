@@ -90,6 +90,11 @@ struct WorkTables {
     Chunk* tiles = nullptr;
     uint32_t n_tiles = 0;
     uint64_t elems = 0;  // elements the chunks cover
+    // the set's tensors in order, and where each one's tiles start (n_tensors + 1 entries):
+    // per-tensor gradient sums (ttp_grad_sumsq_tensors, TTP_STEP_TENSOR_SUMS)
+    uint32_t* tensor_ids = nullptr;
+    uint32_t* tile_start = nullptr;
+    uint32_t n_tensors = 0;
 };
 
 // Gradient bytes up to which an update reads the gradients with ordinary (cached) loads, in
@@ -138,6 +143,14 @@ struct ttp_ctx {
 
     void* staging = nullptr;  // device copy of a host gradient for ttp_accumulate_grad
     uint64_t staging_bytes = 0;
+
+    // per-tensor sums of squares of the unscaled gradients (ttp_grad_sumsq_tensors) and
+    // whether each is current (host view: cleared by any gradient write through the ABI, a
+    // change of the loss scale, and every step)
+    double* tsum = nullptr;
+    std::vector<uint8_t> tsum_fresh;
+    double* tile_sums = nullptr;  // one per norm tile of a ttp_grad_sumsq_tensors call
+    uint32_t tile_sums_cap = 0;
 
     // bias-correction tables of every betas pair stepped with (kept, since captured graphs
     // and queued steps read them) and the current pair's
@@ -206,6 +219,13 @@ int upload_table(const std::vector<Chunk>& v, Chunk** d, uint32_t* n) {
     return TTP_OK;
 }
 
+int upload_u32(const std::vector<uint32_t>& v, uint32_t** d) {
+    HIP_TRY(hipMalloc((void**)d, std::max<size_t>(v.size(), 1) * sizeof(uint32_t)));
+    if (!v.empty())
+        HIP_TRY(hipMemcpy(*d, v.data(), v.size() * sizeof(uint32_t), hipMemcpyHostToDevice));
+    return TTP_OK;
+}
+
 int build_tables(const ttp_ctx* c, const std::vector<uint32_t>& which, WorkTables* w) {
     std::vector<Chunk> v;
     append_pieces(c, which, ttp::kChunk, v);
@@ -215,13 +235,37 @@ int build_tables(const ttp_ctx* c, const std::vector<uint32_t>& which, WorkTable
     if (rc) return rc;
     v.clear();
     append_pieces(c, which, norm_tile(c), v);
-    return upload_table(v, &w->tiles, &w->n_tiles);
+    if ((rc = upload_table(v, &w->tiles, &w->n_tiles))) return rc;
+    // tiles are appended tensor by tensor, so each tensor's tiles are one run of the table
+    std::vector<uint32_t> start(1, 0);
+    for (uint32_t i : which) {
+        const uint64_t tiles = (c->tensors[i].numel + norm_tile(c) - 1) / norm_tile(c);
+        start.push_back(start.back() + (uint32_t)tiles);
+    }
+    w->n_tensors = (uint32_t)which.size();
+    if ((rc = upload_u32(which, &w->tensor_ids))) return rc;
+    return upload_u32(start, &w->tile_start);
 }
 
 void free_tables(WorkTables& w) {
     if (w.chunks) (void)hipFree(w.chunks);
     if (w.tiles) (void)hipFree(w.tiles);
+    if (w.tensor_ids) (void)hipFree(w.tensor_ids);
+    if (w.tile_start) (void)hipFree(w.tile_start);
     w = WorkTables{};
+}
+
+void stale_sums(ttp_ctx* c) { std::fill(c->tsum_fresh.begin(), c->tsum_fresh.end(), 0); }
+
+// TTP_STEP_TENSOR_SUMS: every tensor the step updates needs a current sum
+int check_sums_current(const ttp_ctx* c, const std::vector<uint32_t>& active) {
+    for (uint32_t i : active)
+        if (!c->tsum_fresh[i])
+            return fail(TTP_ERR_STATE, "tensor " + std::to_string(i) +
+                                           " has no current gradient sum: call "
+                                           "ttp_grad_sumsq_tensors after its last gradient write "
+                                           "and after the previous step");
+    return TTP_OK;
 }
 
 int zero_device(ttp_ctx* c, void* p, uint64_t bytes) {
@@ -410,13 +454,13 @@ uint32_t norm_grid(const ttp_ctx* c, uint32_t nchunks) {
 // finalize (norm, found_inf / skip, clip coefficient, loss scale, and the step count with its
 // bias corrections when `count_t`); `probe` only computes the norm.
 int launch_prologue(ttp_ctx* c, const WorkTables* w, bool run_norm, double max_norm, bool probe,
-                    bool want_bias, bool count_t) {
+                    bool want_bias, bool count_t, bool from_sums = false) {
     const Chunk* chunks = w->tiles;
     const uint32_t n = w->n_tiles;
     const uint32_t grid = norm_grid(c, n);
     const int32_t scaler_on = c->scaler.enabled ? 1 : 0;
     TimedLaunch tl(c, TTP_KERNEL_NORM);
-    if (run_norm) {
+    if (run_norm && !from_sums) {
         clear_hip_error();
         if (c->mode == TTP_MODE_MIXED)
             hipLaunchKernelGGL(ttp::norm_partials_kernel<uint16_t>, dim3(grid), dim3(ttp::kBlock),
@@ -431,6 +475,11 @@ int launch_prologue(ttp_ctx* c, const WorkTables* w, bool run_norm, double max_n
     ttp::FinalizeArgs a{};
     a.partials = c->partials;
     a.npartials = run_norm ? grid : 0;
+    if (run_norm && from_sums) {  // the step's tensors' sums, in tensor order
+        a.partials = c->tsum;
+        a.idx = w->tensor_ids;
+        a.npartials = w->n_tensors;
+    }
     a.scaler_on = run_norm ? scaler_on : 0;
     a.count_t = count_t ? 1 : 0;
     a.probe = probe ? 1 : 0;
@@ -662,7 +711,8 @@ void release(ttp_ctx* c) {
     (void)hipSetDevice(c->device);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     for (void* p : {(void*)c->grad, (void*)c->records, (void*)c->momentum, (void*)c->mom_init,
-                    (void*)c->st, (void*)c->partials, c->staging})
+                    (void*)c->st, (void*)c->partials, c->staging, (void*)c->tsum,
+                    (void*)c->tile_sums})
         if (p) (void)hipFree(p);
     for (auto& kv : c->bias_tables) (void)hipFree(kv.second.first);
     free_tables(c->all);
@@ -784,6 +834,8 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
     if ((rc = alloc_zero(c, (void**)&c->st, sizeof(DevState)))) return bail(rc);
     c->partials_cap = c->norm_grid_cap;
     if ((rc = alloc_zero(c, (void**)&c->partials, (uint64_t)c->partials_cap * 8))) return bail(rc);
+    if ((rc = alloc_zero(c, (void**)&c->tsum, std::max<uint64_t>(n, 1) * 8))) return bail(rc);
+    c->tsum_fresh.assign(n, 0);
 
     std::vector<uint32_t> every;
     for (uint32_t i = 0; i < n; ++i)
@@ -945,10 +997,13 @@ int ttp_upload(ttp_ctx* c, int which, uint32_t index, const void* src, uint64_t 
         if (kind == TTP_HOST) HIP_TRY(hipStreamSynchronize(c->stream));
     }
     if (which == TTP_BUF_GRAD) {
-        if (index == TTP_ALL_TENSORS)
+        if (index == TTP_ALL_TENSORS) {
             for (auto& t : c->tensors) t.has_grad = 1;
-        else
+            stale_sums(c);
+        } else {
             c->tensors[index].has_grad = 1;
+            c->tsum_fresh[index] = 0;
+        }
     }
     return TTP_OK;
 }
@@ -984,9 +1039,8 @@ int ttp_set_has_grad(ttp_ctx* c, uint32_t i, int has) {
     int rc = check_ctx(c);
     if (rc) return rc;
     if ((rc = check_index(c, i))) return rc;
-    if (c->tensors[i].has_grad != (has ? 1 : 0)) {
-        c->tensors[i].has_grad = has ? 1 : 0;
-    }
+    c->tensors[i].has_grad = has ? 1 : 0;
+    c->tsum_fresh[i] = 0;  // marks grads written outside the ABI, or drops them
     return TTP_OK;
 }
 
@@ -1007,6 +1061,7 @@ int ttp_zero_grad(ttp_ctx* c, int set_to_none) {
     if (set_to_none) {
         for (auto& t : c->tensors) t.has_grad = 0;
     }
+    stale_sums(c);
     return TTP_OK;
 }
 
@@ -1030,7 +1085,10 @@ int ttp_zero_grad_subset(ttp_ctx* c, const uint32_t* indices, uint32_t n, int se
                                0, c->stream, (float*)c->grad, w->chunks, w->n_chunks);
         HIP_TRY(hipGetLastError());
     }
-    for (uint32_t k = 0; k < n; ++k) c->tensors[indices[k]].has_grad = set_to_none ? 0 : 1;
+    for (uint32_t k = 0; k < n; ++k) {
+        c->tensors[indices[k]].has_grad = set_to_none ? 0 : 1;
+        c->tsum_fresh[indices[k]] = 0;
+    }
     return TTP_OK;
 }
 
@@ -1085,6 +1143,7 @@ int ttp_accumulate_grad(ttp_ctx* c, uint32_t index, const void* src, uint64_t n,
         if (kind == TTP_HOST) HIP_TRY(hipStreamSynchronize(c->stream));
     }
     t.has_grad = 1;
+    c->tsum_fresh[index] = 0;
     return TTP_OK;
 }
 
@@ -1099,11 +1158,13 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
     if (!(hp->beta1 > 0 && hp->beta1 < 1 && hp->beta2 > 0 && hp->beta2 < 1))
         return fail(TTP_ERR_INVALID, "betas must be in (0, 1)");
     if (!(hp->weight_decay >= 0)) return fail(TTP_ERR_INVALID, "weight_decay must be >= 0");
+    if (hp->flags & ~TTP_STEP_TENSOR_SUMS) return fail(TTP_ERR_INVALID, "unknown step flags");
     if (report && (rc = no_capture(c, "a step report (synchronises)"))) return rc;
     if ((rc = set_dev(c))) return rc;
     if ((rc = ensure_adam_state(c))) return rc;
     const WorkTables* w;
-    if ((rc = select_tables(c, subset, nsub, &w, nullptr))) return rc;
+    std::vector<uint32_t> active;
+    if ((rc = select_tables(c, subset, nsub, &w, &active))) return rc;
     const Chunk* chunks = w->chunks;
     const uint32_t n = w->n_chunks;
 
@@ -1111,11 +1172,13 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
     const bool clip = hp->max_grad_norm > 0;
     const bool need_norm = scaler || clip;
     const bool devt = t_on_device(c);
+    const bool from_sums = need_norm && (hp->flags & TTP_STEP_TENSOR_SUMS);
+    if (from_sums && (rc = check_sums_current(c, active))) return rc;
     // the device table of bias corrections; built in host-count mode too (once per betas) so
     // that a later capture finds it, except when betas so close to 1 make it too long
     if ((rc = ensure_bias_table(c, hp->beta1, hp->beta2)) && devt) return rc;
     if ((need_norm || devt) &&
-        (rc = launch_prologue(c, w, need_norm, hp->max_grad_norm, false, devt, devt)))
+        (rc = launch_prologue(c, w, need_norm, hp->max_grad_norm, false, devt, devt, from_sums)))
         return rc;
 
     ttp::AdamArgs a{};
@@ -1168,6 +1231,7 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
         HIP_TRY(hipGetLastError());
         tl.done();
     }
+    stale_sums(c);  // a step consumes the sums (the gradients are spent, the scale may move)
     if (report) return fill_report(c, need_norm, report);
     return TTP_OK;
 }
@@ -1182,6 +1246,7 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
     if (!(hp->weight_decay >= 0)) return fail(TTP_ERR_INVALID, "weight_decay must be >= 0");
     if (hp->nesterov && (hp->momentum <= 0 || hp->dampening != 0))
         return fail(TTP_ERR_INVALID, "nesterov needs momentum > 0 and zero dampening");
+    if (hp->flags & ~TTP_STEP_TENSOR_SUMS) return fail(TTP_ERR_INVALID, "unknown step flags");
     if (report && (rc = no_capture(c, "a step report (synchronises)"))) return rc;
     if ((rc = set_dev(c))) return rc;
     const bool mom = hp->momentum != 0.0;
@@ -1196,8 +1261,10 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
     const bool clip = hp->max_grad_norm > 0;
     const bool need_norm = scaler || clip;
     const bool devt = t_on_device(c);
+    const bool from_sums = need_norm && (hp->flags & TTP_STEP_TENSOR_SUMS);
+    if (from_sums && (rc = check_sums_current(c, active))) return rc;
     if ((need_norm || devt) &&
-        (rc = launch_prologue(c, w, need_norm, hp->max_grad_norm, false, false, devt)))
+        (rc = launch_prologue(c, w, need_norm, hp->max_grad_norm, false, false, devt, from_sums)))
         return rc;
     if (!devt) c->host_t += 1;
 
@@ -1257,6 +1324,7 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
                 for (uint32_t i : active) c->host_mom_init[i] = 1;
         }
     }
+    stale_sums(c);  // a step consumes the sums (the gradients are spent, the scale may move)
     if (report) return fill_report(c, need_norm, report);
     return TTP_OK;
 }
@@ -1300,6 +1368,49 @@ int ttp_grad_norm(ttp_ctx* c, double* norm) {
     DevState s;
     if ((rc = read_state(c, &s))) return rc;
     *norm = s.norm;
+    return TTP_OK;
+}
+
+int ttp_grad_sumsq_tensors(ttp_ctx* c, const uint32_t* indices, uint32_t n) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (n && !indices) return fail(TTP_ERR_INVALID, "null index list");
+    if ((rc = set_dev(c))) return rc;
+    static const uint32_t none = 0;
+    const WorkTables* w;
+    std::vector<uint32_t> active;
+    if ((rc = select_tables(c, indices ? indices : &none, n, &w, &active))) return rc;
+    if (w->n_tiles > c->tile_sums_cap) {
+        if ((rc = no_capture(c, "a first gradient-sum call over this many tiles (allocates)")))
+            return rc;
+        HIP_TRY(hipStreamSynchronize(c->stream));  // queued calls may still use the old buffer
+        if (c->tile_sums) HIP_TRY(hipFree(c->tile_sums));
+        c->tile_sums = nullptr;
+        c->tile_sums_cap = 0;
+        HIP_TRY(hipMalloc((void**)&c->tile_sums, (size_t)w->n_tiles * sizeof(double)));
+        c->tile_sums_cap = w->n_tiles;
+    }
+    if (w->n_tiles) {
+        // one norm-pass block per tile (each block's partial is its tile's sum), then one
+        // block per tensor over its run of tiles
+        const int32_t scaler_on = c->scaler.enabled ? 1 : 0;
+        clear_hip_error();
+        if (c->mode == TTP_MODE_MIXED)
+            hipLaunchKernelGGL(ttp::norm_partials_kernel<uint16_t>, dim3(w->n_tiles),
+                               dim3(ttp::kBlock), 0, c->stream, (const uint16_t*)c->grad,
+                               w->tiles, w->n_tiles, (const DevState*)c->st, scaler_on,
+                               c->tile_sums);
+        else
+            hipLaunchKernelGGL(ttp::norm_partials_kernel<float>, dim3(w->n_tiles),
+                               dim3(ttp::kBlock), 0, c->stream, (const float*)c->grad, w->tiles,
+                               w->n_tiles, (const DevState*)c->st, scaler_on, c->tile_sums);
+        HIP_TRY(hipGetLastError());
+        clear_hip_error();
+        hipLaunchKernelGGL(ttp::tensor_sums_kernel, dim3(w->n_tensors), dim3(ttp::kBlock), 0,
+                           c->stream, c->tile_sums, w->tile_start, w->tensor_ids, c->tsum);
+        HIP_TRY(hipGetLastError());
+    }
+    for (uint32_t i : active) c->tsum_fresh[i] = 1;
     return TTP_OK;
 }
 
@@ -1358,6 +1469,7 @@ int ttp_scaler_configure(ttp_ctx* c, const ttp_scaler_config* cfg) {
     }
     HIP_TRY(hipMemcpy(c->st, &s, sizeof(s), hipMemcpyHostToDevice));
     c->scaler = *cfg;
+    stale_sums(c);  // the sums are of gradients unscaled by the old scale
     return TTP_OK;
 }
 
@@ -1385,6 +1497,7 @@ int ttp_scaler_set(ttp_ctx* c, float scale, int32_t tracker) {
     s.scale = scale;
     s.growth_tracker = tracker;
     HIP_TRY(hipMemcpy(c->st, &s, sizeof(s), hipMemcpyHostToDevice));
+    stale_sums(c);
     return TTP_OK;
 }
 
@@ -1658,6 +1771,7 @@ int ttp_load_state(ttp_ctx* c, const char* path) {
     ds.scale = h.scale;
     ds.growth_tracker = h.growth_tracker;
     HIP_TRY(hipMemcpy(c->st, &ds, sizeof(ds), hipMemcpyHostToDevice));
+    stale_sums(c);
     return TTP_OK;
 }
 

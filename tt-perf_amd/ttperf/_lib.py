@@ -18,6 +18,7 @@ ALL_TENSORS = 0xFFFFFFFF
 TENSOR_DECAY = 1
 HOST, DEVICE = 0, 1
 DTYPE_F32, DTYPE_BF16 = 0, 1
+STEP_TENSOR_SUMS = 1
 KERNEL_NORM, KERNEL_UPDATE = 0, 1
 
 
@@ -28,12 +29,12 @@ class TensorDesc(C.Structure):
 class AdamHParams(C.Structure):
     _fields_ = [("lr", C.c_double), ("beta1", C.c_double), ("beta2", C.c_double),
                 ("eps", C.c_double), ("weight_decay", C.c_double), ("decoupled", C.c_int32),
-                ("reserved", C.c_int32), ("max_grad_norm", C.c_double)]
+                ("flags", C.c_int32), ("max_grad_norm", C.c_double)]
 
 
 class SgdHParams(C.Structure):
     _fields_ = [("lr", C.c_double), ("momentum", C.c_double), ("dampening", C.c_double),
-                ("weight_decay", C.c_double), ("nesterov", C.c_int32), ("reserved", C.c_int32),
+                ("weight_decay", C.c_double), ("nesterov", C.c_int32), ("flags", C.c_int32),
                 ("max_grad_norm", C.c_double)]
 
 
@@ -83,6 +84,7 @@ SIGNATURES = {
     "ttp_sgd_step_subset": (C.c_int, [_P, C.POINTER(SgdHParams), C.POINTER(C.c_uint32),
                                       C.c_uint32, C.POINTER(StepReport)]),
     "ttp_grad_norm": (C.c_int, [_P, C.POINTER(C.c_double)]),
+    "ttp_grad_sumsq_tensors": (C.c_int, [_P, C.POINTER(C.c_uint32), C.c_uint32]),
     "ttp_get_step": (C.c_int, [_P, C.POINTER(C.c_uint64)]),
     "ttp_set_step": (C.c_int, [_P, C.c_uint64]),
     "ttp_scaler_configure": (C.c_int, [_P, C.POINTER(ScalerConfig)]),

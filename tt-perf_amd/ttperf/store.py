@@ -464,11 +464,13 @@ class ParamStore:
         return idx, len(indices)
 
     def adam_step(self, lr, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0, decoupled=True,
-                  max_grad_norm=None, report=False, indices=None):
-        """One Adam/AdamW step over every tensor with a grad, or only over `indices`."""
+                  max_grad_norm=None, report=False, indices=None, tensor_sums=False):
+        """One Adam/AdamW step over every tensor with a grad, or only over `indices`.
+        tensor_sums: take the norm from grad_sumsq_tensors() instead of a norm pass."""
         hp = L.AdamHParams(lr=lr, beta1=betas[0], beta2=betas[1], eps=eps,
                            weight_decay=weight_decay, decoupled=1 if decoupled else 0,
-                           reserved=0, max_grad_norm=max_grad_norm or 0.0)
+                           flags=L.STEP_TENSOR_SUMS if tensor_sums else 0,
+                           max_grad_norm=max_grad_norm or 0.0)
         rep = L.StepReport() if report else None
         rp = C.byref(rep) if report else None
         idx, n = self._index_array(indices)
@@ -479,10 +481,12 @@ class ParamStore:
         return rep.as_dict() if report else None
 
     def sgd_step(self, lr, momentum=0.0, dampening=0.0, weight_decay=0.0, nesterov=False,
-                 max_grad_norm=None, report=False, indices=None):
-        """One SGD step over every tensor with a grad, or only over `indices`."""
+                 max_grad_norm=None, report=False, indices=None, tensor_sums=False):
+        """One SGD step over every tensor with a grad, or only over `indices`.
+        tensor_sums: take the norm from grad_sumsq_tensors() instead of a norm pass."""
         hp = L.SgdHParams(lr=lr, momentum=momentum, dampening=dampening,
-                          weight_decay=weight_decay, nesterov=1 if nesterov else 0, reserved=0,
+                          weight_decay=weight_decay, nesterov=1 if nesterov else 0,
+                          flags=L.STEP_TENSOR_SUMS if tensor_sums else 0,
                           max_grad_norm=max_grad_norm or 0.0)
         rep = L.StepReport() if report else None
         rp = C.byref(rep) if report else None
@@ -492,6 +496,15 @@ class ParamStore:
         else:
             L.check(L.lib.ttp_sgd_step_subset(self._h, C.byref(hp), idx, n, rp))
         return rep.as_dict() if report else None
+
+    def grad_sumsq_tensors(self, indices=None):
+        """Per-tensor sums of squares of the listed tensors' grads (all when None), kept on the
+        device for the next step with tensor_sums=True: a bucket's norm work, done once its
+        grads are final, so the step itself runs no norm pass."""
+        if indices is None:
+            indices = range(len(self.tensors))
+        idx, n = self._index_array(list(indices))
+        L.check(L.lib.ttp_grad_sumsq_tensors(self._h, idx, n))
 
     def grad_norm(self):
         v = C.c_double()
