@@ -178,3 +178,48 @@ def test_graph_of_bucket_sums_and_step_replays():
     graph.close()
     store.close()
     twin.close()
+
+
+def test_growing_the_tile_buffer_keeps_captured_graphs_valid():
+    """A captured bucket-sum call writes the tile buffer it was captured with.  An eager call
+    over a larger bucket grows that buffer while the graph is alive; the old one is kept until
+    the store closes, so the graph's replays stay correct (against the oracle), and so does
+    the eager step that uses the new buffer."""
+    from ttperf import _lib as L
+    torch = torch_mod()
+    store, ref = make_pair(SHAPES, DECAY, O.MODE_MIXED, seed=128)
+    store.set_stream(None)
+    hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, decoupled=True,
+              max_grad_norm=0.05)
+    small = [0, 1]  # one 16 KiB tile each: the smallest tile buffer
+    gen = torch.Generator(device="cuda").manual_seed(129)
+
+    def grads(active):
+        ref.grad[:store.total] = device_grads(store, gen, 1e-2)
+        for i in range(ref.n):
+            ref.set_has_grad(i, i in active)
+
+    grads(small)
+    store.grad_sumsq_tensors(small)
+    store.adam_step(indices=small, tensor_sums=True, **hp)
+    ref.adam_step(**hp)
+    store.begin_capture()
+    store.grad_sumsq_tensors(small)
+    store.adam_step(indices=small, tensor_sums=True, **hp)
+    graph = store.end_capture()
+    for it in range(3):
+        grads(list(range(len(SHAPES))))
+        store.grad_sumsq_tensors()  # every tensor: a larger tile buffer while the graph lives
+        r = store.adam_step(report=True, tensor_sums=True, **hp)
+        e = ref.adam_step(**hp)
+        assert r["step"] == e["step"]
+        compare_state(store, ref, max_ulp=2)
+        grads(small)
+        graph.replay()
+        store.sync()
+        ref.adam_step(**hp)
+        print(f"round {it}: replay after growth, step {store.step_count}", flush=True)
+        assert store.step_count == ref.t
+        compare_state(store, ref, max_ulp=2)
+    graph.close()
+    store.close()

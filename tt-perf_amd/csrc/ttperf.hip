@@ -151,6 +151,7 @@ struct ttp_ctx {
     std::vector<uint8_t> tsum_fresh;
     double* tile_sums = nullptr;  // one per norm tile of a ttp_grad_sumsq_tensors call
     uint32_t tile_sums_cap = 0;
+    std::vector<void*> retired;   // replaced buffers that live graphs may still write
 
     // bias-correction tables of every betas pair stepped with (kept, since captured graphs
     // and queued steps read them) and the current pair's
@@ -717,6 +718,7 @@ void release(ttp_ctx* c) {
     for (auto& kv : c->bias_tables) (void)hipFree(kv.second.first);
     free_tables(c->all);
     for (auto& kv : c->tables) free_tables(kv.second);
+    for (void* p : c->retired) (void)hipFree(p);
     // MIXED: param is the bf16 copy and master lives in `records`; FP32: param == master
     if (c->mode == TTP_MODE_MIXED && c->param) (void)hipFree(c->param);
     if (c->mode == TTP_MODE_FP32 && c->master) (void)hipFree(c->master);
@@ -1384,7 +1386,12 @@ int ttp_grad_sumsq_tensors(ttp_ctx* c, const uint32_t* indices, uint32_t n) {
         if ((rc = no_capture(c, "a first gradient-sum call over this many tiles (allocates)")))
             return rc;
         HIP_TRY(hipStreamSynchronize(c->stream));  // queued calls may still use the old buffer
-        if (c->tile_sums) HIP_TRY(hipFree(c->tile_sums));
+        if (c->tile_sums) {
+            if (c->n_graphs)
+                c->retired.push_back(c->tile_sums);  // a captured call may write it on replay
+            else
+                HIP_TRY(hipFree(c->tile_sums));
+        }
         c->tile_sums = nullptr;
         c->tile_sums_cap = 0;
         HIP_TRY(hipMalloc((void**)&c->tile_sums, (size_t)w->n_tiles * sizeof(double)));
