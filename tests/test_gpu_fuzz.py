@@ -8,9 +8,11 @@ host interface, mirrored on the oracle:
   loss scaling is on); gradients accumulated from fp32 or bf16 sources, host or device;
   `grad = None`; zero_grad of all or of a subset, to zeros or to None; master or bf16 weight
   uploads; Adam / AdamW / L2 and SGD (momentum, dampening, nesterov, L2) steps over everything
-  or over a subset, with or without clipping, with step reports; the loss scaler switched on
-  or off; the step count set; the gradient norm probed; a checkpoint saved and later loaded;
-  an Adam step captured into a graph and replayed later, between other operations.
+  or over a subset, with or without clipping, with step reports; steps that take their norm
+  from bucket sums (ttp_grad_sumsq_tensors), and their refusal after a gradient write; the
+  loss scaler switched on or off; the step count set; the gradient norm probed; a checkpoint
+  saved and later loaded; an Adam step captured into a graph and replayed later, between
+  other operations.
 
 After every operation the whole state is compared: master, m, v and momentum within the
 2-ulp bar of the other parity tests (in practice 0), bf16 weights and the gradients bit for
@@ -226,6 +228,56 @@ class Case:
         self.last_adam = None
         self.mom_seen = self.mom_seen or hp["momentum"] > 0
 
+    def op_sums_step(self):
+        """Bucket sums over a random partition of the tensors, then a step that takes its norm
+        from them; sometimes a gradient write in between, after which the step is refused
+        with nothing changed."""
+        import ttperf
+        from ttperf import _lib as L
+        rng = self.rng
+        perm = [int(i) for i in rng.permutation(self.n)]
+        cuts = sorted(set(int(c) for c in rng.integers(1, self.n + 1, size=2)))
+        buckets = [sorted(perm[a:b]) for a, b in zip([0] + cuts, cuts + [self.n]) if b > a]
+        for b in buckets:
+            self.store.grad_sumsq_tensors(b)
+        adam = rng.random() < 0.6
+        clip = None if rng.random() < 0.3 else float(10 ** rng.uniform(-2, 1))
+        indices = None if rng.random() < 0.6 else self.pick_subset()
+        if adam:
+            kind, hp = "adam", dict(lr=float(10 ** rng.uniform(-4, -1.5)),
+                                    betas=BETAS[int(rng.integers(0, 3))], eps=1e-8,
+                                    weight_decay=0.05, decoupled=True, max_grad_norm=clip)
+        else:
+            kind, hp = "sgd", dict(lr=float(10 ** rng.uniform(-3, -1)), momentum=0.9,
+                                   dampening=0.0, weight_decay=0.0, nesterov=False,
+                                   max_grad_norm=clip)
+        cand = [i for i in (range(self.n) if indices is None else indices) if self.numels[i]]
+        stale = (clip or self.scaler_on) and cand and rng.random() < 0.3
+        print(f"  sums over {buckets} then {kind} {hp} indices={indices}"
+              f"{' after a gradient write' if stale else ''}", flush=True)
+        if stale:
+            i = int(rng.choice(cand))
+            g = self.grad_values(self.numels[i])
+            self.store.tensors[i].grad = g
+            self.ref.set_grad(i, g)
+            t0 = self.store.step_count
+            with pytest.raises(ttperf.TTPError) as e:
+                step = self.store.adam_step if adam else self.store.sgd_step
+                step(indices=indices, tensor_sums=True, **hp)
+            assert e.value.code == L.ERR_STATE and self.store.step_count == t0
+            return
+        active = self._active(indices)
+        step = self.store.adam_step if adam else self.store.sgd_step
+        r = step(report=True, indices=indices, tensor_sums=True, **hp)
+        e = self._ref_step(kind, hp, active)
+        self._check_report(r, e)
+        if adam:
+            self.last_adam = (hp, indices, active)
+            self.adam_seen = True
+        else:
+            self.last_adam = None
+            self.mom_seen = True
+
     def op_scaler(self):
         on = not self.scaler_on
         init = float(2.0 ** int(self.rng.integers(4, 14)))
@@ -321,7 +373,7 @@ class Case:
     OPS = [("grads_flat", 6), ("grad_one", 3), ("accumulate", 3), ("drop_grad", 2),
            ("zero_grad", 2), ("upload_weights", 1), ("adam", 6), ("sgd", 4), ("scaler", 1),
            ("set_step", 1), ("grad_norm", 1), ("save", 1), ("load", 1), ("capture", 2),
-           ("replay", 3)]
+           ("replay", 3), ("sums_step", 4)]
 
     def compare(self):
         from ttperf import _lib as L
