@@ -69,6 +69,9 @@ def parse():
     ap.add_argument("--optimizer", default="adamw", choices=["adamw", "sgdm"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--overlap", action="store_true",
+                    help="also time the bucket sums beside a bf16 GEMM on another stream (the "
+                         "backward's compute stand-in) against each alone")
     ap.add_argument("--graph", action="store_true",
                     help="time replays of the step captured as a hipGraph (measured equal to "
                          "eager launches on MI355X, so eager is the default)")
@@ -297,12 +300,53 @@ def main():
         e1.record(stream)
         torch.cuda.synchronize()
         both_ms = e0.elapsed_time(e1) / args.steps
+        overlap = None
+        if args.overlap:
+            # a bf16 GEMM on its own stream stands in for the backward's compute; the bucket
+            # sums run on the store's stream at the same time
+            comp = torch.cuda.Stream()
+            a = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16)
+            b = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16)
+            c_out = torch.empty(8192, 8192, device=dev, dtype=torch.bfloat16)
+
+            def gemm():
+                with torch.cuda.stream(comp):
+                    torch.mm(a, b, out=c_out)
+
+            def both():
+                gemm()
+                bucket_sums()
+
+            # interleaved rounds, each launch synchronised and host-timed; medians
+            runs = {"gemm": [], "sums": [], "both": []}
+            fns = {"gemm": gemm, "sums": bucket_sums, "both": both}
+            for _ in range(3):
+                for fn in fns.values():
+                    fn()
+            torch.cuda.synchronize()
+            for _ in range(30):
+                for name, fn in fns.items():
+                    t0 = time.perf_counter()
+                    fn()
+                    torch.cuda.synchronize()
+                    runs[name].append((time.perf_counter() - t0) * 1e3)
+            gemm_ms, sums_alone_ms, both_ms_ = (float(np.median(runs[k]))
+                                                for k in ("gemm", "sums", "both"))
+            overlap = {"gemm_ms": round(gemm_ms, 4), "bucket_sums_ms": round(sums_alone_ms, 4),
+                       "together_ms": round(both_ms_, 4),
+                       "sums_hidden_frac": round((gemm_ms + sums_alone_ms - both_ms_)
+                                                 / sums_alone_ms, 3),
+                       "note": "bf16 8192^3 torch.mm on one stream, the bucket sums on the "
+                               "store's stream; medians of 30 interleaved rounds, each launch "
+                               "synchronised and host-timed"}
+            del a, b, c_out
         sums = {"buckets": len(buckets), "bucket_sums_ms": round(sums_ms, 4),
                 "sums_and_step_ms": round(both_ms, 4),
                 "step_after_sums_ms": round(both_ms - sums_ms, 4),
                 "note": "ttp_grad_sumsq_tensors per bucket, then the step with "
                         "TTP_STEP_TENSOR_SUMS; in training the bucket sums overlap the "
-                        "backward, leaving step_after_sums_ms on the step's own path"}
+                        "backward, leaving step_after_sums_ms on the step's own path",
+                "overlap": overlap}
 
     # context: the practical ceilings of the update's traffic on this GPU, over the update's
     # byte count: torch's device copy (a blit kernel), and libttperf_ceiling's non-temporal
