@@ -254,17 +254,19 @@ def main():
         skip_ms = e0.elapsed_time(e1)
         assert rs is None
 
-    # context: the step when its norm comes from per-tensor sums taken bucket by bucket (about
-    # 25 MB of gradients each, reverse tensor order, as a backward produces them), which can
-    # run beside the backward's compute; the step then runs the finalize and the update only
+    # context: the step when its norm comes from per-tensor sums taken bucket by bucket (in
+    # reverse tensor order, as a backward produces them; 25 MB of gradients each, or a
+    # sixteenth of them for large models), which can run beside the backward's compute; the
+    # step then runs the finalize and the update only
     sums = None
     if cfg["hp"]["max_grad_norm"] or cfg["scaler"]:
         esz = 2 if mode == "mixed" else 4
+        bucket_bytes = max(25 << 20, n_params * esz // 16)
         buckets, cur, cur_bytes = [], [], 0
         for i in reversed(range(len(numels))):
             cur.append(i)
             cur_bytes += numels[i] * esz
-            if cur_bytes >= 25 << 20:
+            if cur_bytes >= bucket_bytes:
                 buckets.append(sorted(cur))
                 cur, cur_bytes = [], 0
         if cur:
@@ -288,18 +290,24 @@ def main():
         for _ in range(3):
             step_from_sums()
         torch.cuda.synchronize()
-        e0.record(stream)
-        for _ in range(args.steps):
+        # an event pair around the bucket calls and one around the step, per iteration, on the
+        # store's stream: the GPU time of each (subtracting loop totals would mislead where
+        # hundreds of small bucket launches make the bucket loop host-bound)
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)]
+               for _ in range(args.steps)]
+        for k in range(args.steps):
+            evs[k][0].record(stream)
             bucket_sums()
-        e1.record(stream)
+            evs[k][1].record(stream)
+            if args.optimizer == "adamw":
+                store.adam_step(tensor_sums=True, **hp)
+            else:
+                store.sgd_step(lr=hp["lr"], momentum=0.9, max_grad_norm=hp["max_grad_norm"],
+                               tensor_sums=True)
+            evs[k][2].record(stream)
         torch.cuda.synchronize()
-        sums_ms = e0.elapsed_time(e1) / args.steps
-        e0.record(stream)
-        for _ in range(args.steps):
-            step_from_sums()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        both_ms = e0.elapsed_time(e1) / args.steps
+        sums_ms = sum(a.elapsed_time(b) for a, b, _ in evs) / args.steps
+        after_ms = sum(b.elapsed_time(c) for _, b, c in evs) / args.steps
         overlap = None
         if args.overlap:
             # a bf16 GEMM on its own stream stands in for the backward's compute; the bucket
@@ -341,8 +349,7 @@ def main():
                                "synchronised and host-timed"}
             del a, b, c_out
         sums = {"buckets": len(buckets), "bucket_sums_ms": round(sums_ms, 4),
-                "sums_and_step_ms": round(both_ms, 4),
-                "step_after_sums_ms": round(both_ms - sums_ms, 4),
+                "step_after_sums_ms": round(after_ms, 4),
                 "note": "ttp_grad_sumsq_tensors per bucket, then the step with "
                         "TTP_STEP_TENSOR_SUMS; in training the bucket sums overlap the "
                         "backward, leaving step_after_sums_ms on the step's own path",
