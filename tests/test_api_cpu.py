@@ -182,12 +182,13 @@ class _CountingStore:
         self.writes += 1
         self._t = t
 
-    def adam_step(self, lr, betas, eps, weight_decay, decoupled, max_grad_norm, indices=None):
+    def adam_step(self, lr, betas, eps, weight_decay, decoupled, max_grad_norm, indices=None,
+                  tensor_sums=False):
         self._t += 1
         self.log.append((lr, self._t))
 
     def sgd_step(self, lr, momentum, dampening, weight_decay, nesterov, max_grad_norm,
-                 indices=None):
+                 indices=None, tensor_sums=False):
         self._t += 1
         self.log.append((lr, self._t))
 

@@ -223,3 +223,29 @@ def test_growing_the_tile_buffer_keeps_captured_graphs_valid():
         compare_state(store, ref, max_ulp=2)
     graph.close()
     store.close()
+
+
+def test_optimizer_step_with_tensor_sums():
+    """The drop-in AdamW's step(tensor_sums=True) after bucket sums matches the same optimizer
+    stepping with its norm pass, within 2 ulp, and is refused without current sums."""
+    import ttperf
+    from ttperf import _lib as L
+    torch = torch_mod()
+    a, _ = make_pair(SHAPES, DECAY, O.MODE_MIXED, seed=130)
+    b, _ = make_pair(SHAPES, DECAY, O.MODE_MIXED, seed=130)
+    oa = ttperf.AdamW(a.parameters(), lr=1e-3, weight_decay=0.1, max_grad_norm=0.2)
+    ob = ttperf.AdamW(b.parameters(), lr=1e-3, weight_decay=0.1, max_grad_norm=0.2)
+    gen = torch.Generator(device="cuda").manual_seed(131)
+    for _ in range(3):
+        device_grads(a, gen, 1e-2)
+        b.upload(L.BUF_GRAD, L.ALL_TENSORS, a.download(L.BUF_GRAD))
+        for bucket in _buckets(len(SHAPES)):
+            a.grad_sumsq_tensors(bucket)
+        oa.step(tensor_sums=True)
+        ob.step()
+    for which in (L.BUF_MASTER, L.BUF_EXP_AVG, L.BUF_EXP_AVG_SQ):
+        assert f32_ulp_diff(a.download(which), b.download(which)).max() <= 2
+    with pytest.raises(ttperf.TTPError):
+        oa.step(tensor_sums=True)  # the last step consumed the sums
+    a.close()
+    b.close()

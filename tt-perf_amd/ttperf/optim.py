@@ -76,13 +76,17 @@ class _Optimizer:
                 for p in members:
                     p.zero_grad()
 
-    def step(self):
+    def step(self, tensor_sums=False):
+        """py/optim.py's step().  tensor_sums=True (an extension): take the gradient norm from
+        the sums ParamStore.grad_sumsq_tensors() took for these tensors, bucket by bucket
+        during the backward, instead of a norm pass."""
         for store, members in self._stores():
             self._claim(store)
             whole = len(members) == len(store.tensors)
-            self._step_store(store, None if whole else sorted({p.index for p in members}))
+            self._step_store(store, None if whole else sorted({p.index for p in members}),
+                             tensor_sums)
 
-    def _step_store(self, store, indices):  # pragma: no cover - abstract
+    def _step_store(self, store, indices, tensor_sums):  # pragma: no cover - abstract
         raise NotImplementedError
 
 
@@ -107,9 +111,10 @@ class SGD(_Optimizer):
         self.nesterov = bool(nesterov)
         self.max_grad_norm = max_grad_norm
 
-    def _step_store(self, store, indices):
+    def _step_store(self, store, indices, tensor_sums):
         store.sgd_step(self.lr, self.momentum, self.dampening, self.weight_decay,
-                       self.nesterov, self.max_grad_norm, indices=indices)
+                       self.nesterov, self.max_grad_norm, indices=indices,
+                       tensor_sums=tensor_sums)
 
 
 class Adam(_Optimizer):
@@ -138,9 +143,10 @@ class Adam(_Optimizer):
         self.weight_decay = float(weight_decay)
         self.max_grad_norm = max_grad_norm
 
-    def _step_store(self, store, indices):
+    def _step_store(self, store, indices, tensor_sums):
         store.adam_step(self.lr, (self.beta1, self.beta2), self.eps, self.weight_decay,
-                        self._decoupled, self.max_grad_norm, indices=indices)
+                        self._decoupled, self.max_grad_norm, indices=indices,
+                        tensor_sums=tensor_sums)
 
 
 class AdamW(Adam):
