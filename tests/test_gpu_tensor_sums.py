@@ -249,3 +249,58 @@ def test_optimizer_step_with_tensor_sums():
         oa.step(tensor_sums=True)  # the last step consumed the sums
     a.close()
     b.close()
+
+
+def test_bucket_sums_on_a_side_stream_wait_for_the_backward():
+    """INTEGRATION.md's pattern: the backward writes each bucket's gradients on its own stream
+    (through the zero-copy grad views, after a long GEMM standing in for its compute) and
+    records an event; the bucket sums run on a side stream, each after its bucket's event; the
+    step follows on the side stream once the whole backward is done.  A sum that ran before its
+    event would see the zeroed gradients, and the clip would differ from the twin's."""
+    import ttperf
+    from ttperf import _lib as L
+    torch = torch_mod()
+    store, _ = make_pair(SHAPES, DECAY, O.MODE_MIXED, seed=132)
+    twin, _ = make_pair(SHAPES, DECAY, O.MODE_MIXED, seed=132)
+    hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, decoupled=True,
+              max_grad_norm=0.05)
+    main, side = torch.cuda.Stream(), torch.cuda.Stream()
+    gen = torch.Generator(device="cuda").manual_seed(133)
+    a = torch.randn(4096, 4096, device="cuda", dtype=torch.bfloat16)
+    views = [store.torch_view(L.BUF_GRAD, i) for i in range(len(SHAPES))]  # 1-D views
+    buckets = _buckets(len(SHAPES))
+    for it in range(3):
+        src = [(torch.randn(t.numel, generator=gen, device="cuda") * 1e-2).to(torch.bfloat16)
+               for t in store.tensors]
+        torch.cuda.synchronize()
+        store.set_stream(side)
+        store.zero_grad(set_to_none=False)  # the previous iteration's grads are gone
+        store.mark_grads()  # the grads about to be written: marked before their sums
+        store.sync()
+        events = []
+        with torch.cuda.stream(main):
+            for b in buckets:
+                for _ in range(3):
+                    torch.mm(a, a)  # the backward's compute before this bucket is ready
+                for i in b:
+                    views[i].copy_(src[i])
+                ev = torch.cuda.Event()
+                ev.record(main)
+                events.append(ev)
+        for b, ev in zip(buckets, events):
+            side.wait_event(ev)
+            store.grad_sumsq_tensors(b)
+        side.wait_stream(main)
+        r = store.adam_step(report=True, tensor_sums=True, **hp)
+        torch.cuda.synchronize()
+        for i, t in enumerate(twin.tensors):
+            twin.upload(L.BUF_GRAD, i, src[i])
+        rt = twin.adam_step(report=True, **hp)
+        print(f"iteration {it}: norm {r['grad_norm']!r} (twin {rt['grad_norm']!r})", flush=True)
+        assert abs(r["grad_norm"] - rt["grad_norm"]) <= 1e-12 * rt["grad_norm"]
+        assert r["clip_coef"] == rt["clip_coef"] < 1.0
+        for which in (L.BUF_MASTER, L.BUF_EXP_AVG, L.BUF_EXP_AVG_SQ):
+            assert f32_ulp_diff(store.download(which), twin.download(which)).max() <= 2
+    del views
+    store.close()
+    twin.close()
