@@ -9,6 +9,7 @@
 #pragma once
 
 #include <initializer_list>
+#include <memory>
 #include <vector>
 
 #include "autograd/value.hpp"
@@ -226,6 +227,85 @@ public:
 private:
     ttp::Store* store_;
     ttp::Graph graph_;
+};
+
+// The partitioned layers of autograd/traced/mesh.hpp:25-290: N model replicas, each pinned to
+// its own partition of a Tenstorrent core grid, each updated by its own sgd_step.  On MI355X
+// the hardware spreads every launch over all CUs, so a partition keeps only its id; the
+// replicas' tensors share one ParamArena and TracedMeshModel::sgd_step is one launch over all
+// of them (the reference issues two programs per tensor, four per layer, per replica).
+struct PartitionConfig {
+    uint32_t partition_id;
+    explicit PartitionConfig(uint32_t id) : partition_id(id) {}
+};
+
+struct MeshConfig {
+    uint32_t n_partitions = 0;
+    std::vector<PartitionConfig> partitions;
+    // mesh.hpp:42-53 defaults n_partitions = 0 to one partition per 8 Tensix cores; here it
+    // is one per MI355X XCD (8)
+    static MeshConfig create(uint32_t n_partitions) {
+        MeshConfig c;
+        c.n_partitions = n_partitions ? n_partitions : 8;
+        for (uint32_t i = 0; i < c.n_partitions; ++i) c.partitions.emplace_back(i);
+        return c;
+    }
+};
+
+// weight [out, in] filled with `init`, bias [1, out] zeros (mesh.hpp:129-138); sgd_step
+// (:167-170) is one launch over both
+struct TracedPartitionedLinear : TracedLinear {
+    uint32_t partition_id;
+    TracedPartitionedLinear(uint32_t in_f, uint32_t out_f, float init, ParamArena& arena,
+                            const PartitionConfig& config)
+        : TracedLinear(in_f, out_f, init, arena), partition_id(config.partition_id) {}
+};
+
+// two layers filled with 0.01 (mesh.hpp:192-200); sgd_step (:221-224) is one launch over both
+struct TracedPartitionedMLP {
+    TracedPartitionedLinear layer1, layer2;
+    uint32_t batch, dim;
+
+    TracedPartitionedMLP(uint32_t b, uint32_t in_dim, uint32_t hidden_dim, uint32_t out_dim,
+                         ParamArena& arena, const PartitionConfig& config)
+        : layer1(in_dim, hidden_dim, 0.01f, arena, config),
+          layer2(hidden_dim, out_dim, 0.01f, arena, config),
+          batch(b),
+          dim(hidden_dim) {}
+
+    std::vector<ValuePtr> parameters() const {
+        return {layer1.weight, layer1.bias, layer2.weight, layer2.bias};
+    }
+    void sgd_step(float lr) { detail::sgd_on(parameters(), lr); }
+};
+
+// N replicas (mesh.hpp:231-290); create_mlp builds N TracedPartitionedMLP in one arena
+template <typename ModelType>
+struct TracedMeshModel {
+    std::vector<std::unique_ptr<ModelType>> models;
+    MeshConfig config;
+
+    static TracedMeshModel<TracedPartitionedMLP> create_mlp(ParamArena& arena,
+                                                            uint32_t n_partitions, uint32_t batch,
+                                                            uint32_t in_dim, uint32_t hidden_dim,
+                                                            uint32_t out_dim) {
+        TracedMeshModel<TracedPartitionedMLP> m;
+        m.config = MeshConfig::create(n_partitions);
+        for (const auto& part : m.config.partitions)
+            m.models.push_back(std::make_unique<TracedPartitionedMLP>(batch, in_dim, hidden_dim,
+                                                                      out_dim, arena, part));
+        return m;
+    }
+
+    std::vector<ValuePtr> parameters() const {
+        std::vector<ValuePtr> ps;
+        for (const auto& model : models)
+            for (auto& p : model->parameters()) ps.push_back(p);
+        return ps;
+    }
+    // every replica's update in one launch (mesh.hpp:270-274 steps them one by one)
+    void sgd_step(float lr) { detail::sgd_on(parameters(), lr); }
+    size_t size() const { return models.size(); }
 };
 
 struct TracedSGD {

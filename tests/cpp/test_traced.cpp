@@ -1,6 +1,7 @@
 // test_traced.cpp — the traced layers' optimizer surface: TracedSGD({layers}, lr).step()
 // (autograd/traced/optim.hpp:15-29), per-module sgd_step(lr) (autograd/traced/nn.hpp:93-96,
-// 272-275, 317-321) and sgd_update (autograd/traced/ops.hpp:132-134).  Each is
+// 272-275, 317-321), sgd_update (autograd/traced/ops.hpp:132-134) and the partitioned mesh
+// layers (autograd/traced/mesh.hpp:167-170, 221-224, 270-274).  Each is
 // `w - lr*dw` with one rounding per op; each call touches exactly its own tensors.
 #include "autograd/traced.hpp"
 #include "common.hpp"
@@ -102,6 +103,33 @@ int main() {
                 test::check(trace.is_captured() == (it >= 1), "TraceContext captured flag");
             }
         }  // the graph is released before the store
+    }
+    // the partitioned mesh layers (autograd/traced/mesh.hpp:119-290): three replicas in one
+    // arena; a replica's sgd_step touches only its tensors, the mesh model's steps them all
+    {
+        ParamArena arena4(ttp::Mode::FP32);
+        auto mesh = traced::TracedMeshModel<traced::TracedPartitionedMLP>::create_mlp(
+            arena4, 3, /*batch*/ 32, 64, 32, 16);
+        test::check(mesh.size() == 3 && mesh.models[2]->layer1.partition_id == 2,
+                    "mesh: three replicas with their partition ids");
+        auto ps = mesh.parameters();
+        test::check(ps.size() == 12, "mesh: 4 tensors per replica");
+        test::assert_all_close(mesh.models[1]->layer2.weight->data(), 0.01f, 0.0f,
+                               "mesh: linears filled with 0.01");
+        std::vector<std::vector<float>> wm, gm;
+        for (size_t k = 0; k < ps.size(); ++k) {
+            wm.push_back(ps[k]->master());
+            gm.push_back(ramp(ps[k]->numel(), 0.1f * (float)(k + 1), 0.002f));
+            ps[k]->grad = gm.back();
+        }
+        mesh.models[1]->sgd_step(0.05f);  // replica 1 only
+        for (size_t k = 4; k < 8; ++k) wm[k] = sgd_ref(wm[k], gm[k], 0.05f);
+        mesh.sgd_step(0.02f);  // every replica, one launch
+        for (size_t k = 0; k < ps.size(); ++k) wm[k] = sgd_ref(wm[k], gm[k], 0.02f);
+        for (size_t k = 0; k < ps.size(); ++k)
+            test::assert_bits(ps[k]->master(), wm[k], "mesh tensor " + std::to_string(k));
+        test::check(traced::MeshConfig::create(0).n_partitions == 8,
+                    "mesh: n_partitions 0 is one per XCD");
     }
     return test::finish("test_traced");
 }
