@@ -91,4 +91,24 @@ struct FusedMLP {
     void zero_grad() { detail::zero(parameters()); }
 };
 
+// autograd/static/nn.hpp:257-345: two dim x dim Linear layers filled with 0.01 and a learning
+// rate; the reference's train_step builds and runs the forward / backward graph (model
+// compute, not this engine) and ends with layer1.sgd_step(lr); layer2.sgd_step(lr)
+// (:343-344), which sgd_step() does here in one launch.
+struct PersistentMLP {
+    Linear layer1, layer2;
+    float lr;
+
+    PersistentMLP(uint32_t batch, uint32_t dim, float learning_rate, ParamArena& arena)
+        : layer1(batch, dim, dim, 0.01f, arena),
+          layer2(batch, dim, dim, 0.01f, arena),
+          lr(learning_rate) {}
+
+    std::vector<ValuePtr> parameters() const {
+        return {layer1.weight, layer1.bias, layer2.weight, layer2.bias};
+    }
+    void sgd_step() { detail::sgd(parameters(), lr); }
+    void zero_grad() { detail::zero(parameters()); }  // the graph's zero_grad: grads stay, zero
+};
+
 }  // namespace static_autograd

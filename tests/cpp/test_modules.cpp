@@ -1,5 +1,5 @@
 // test_modules.cpp — module-level optimizer surfaces: the static layers' sgd_step / zero_grad
-// (autograd/static/nn.hpp:92-101,178-186,213-221,242-250) and the traced transformer's
+// (autograd/static/nn.hpp:92-101,178-186,213-221,242-250,332-345) and the traced transformer's
 // layer / stack / GPT sgd_step (autograd/traced/transformer_train.hpp:259-268,335-339,487-494).
 // Each sgd_step must update exactly its module's tensors, bit-exact against `w - lr*dw`
 // (one rounding per op, bf16 weights = RNE of the fp32 master), in ONE update launch.
@@ -81,6 +81,22 @@ int main() {
         }
         mlp.sgd_step(0.1f);  // w - 0.1*0 = w
         check_all(ps, r, false, "static sgd_step after zero_grad");
+    }
+    // ---- static PersistentMLP (autograd/static/nn.hpp:257-345): the train_step's update ---
+    {
+        ParamArena arena(ttp::Mode::FP32);
+        static_autograd::PersistentMLP pm(32, 64, 0.05f, arena);
+        auto ps = pm.parameters();
+        test::assert_all_close(pm.layer2.weight->data(), 0.01f, 0.0f, "PersistentMLP init 0.01");
+        Ref r = snapshot(ps, false, 4.0f);
+        ttp::Store& store = arena.store();
+        ttp::check(ttp_timing_enable(store.get(), 1));
+        update_launches(store);
+        pm.sgd_step();
+        test::check(update_launches(store) == 1, "PersistentMLP sgd_step is one update launch");
+        ttp::check(ttp_timing_enable(store.get(), 0));
+        for (size_t k = 0; k < 4; ++k) apply(r, k, 0.05f);
+        check_all(ps, r, false, "PersistentMLP sgd_step");
     }
     // ---- traced transformer: GPT with 2 blocks ----------------------------------------
     {
