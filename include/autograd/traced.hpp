@@ -83,6 +83,30 @@ struct TracedEmbedding {
 // autograd/traced/ops.hpp:132-134: param = param - lr * grad (one tensor)
 inline void sgd_update(const ValuePtr& param, float lr) { detail::sgd_on({param}, lr); }
 
+// N dim x dim linears filled with 0.01 (autograd/traced/mlp.hpp:18-70); sgd_step (:106-110)
+// updates all N layers at the member lr, here in one launch.  The forward / backward buffers
+// and train_step's passes are model compute, not part of this engine.
+template <size_t N>
+struct TracedMLP {
+    std::vector<TracedLinear> layers;
+    uint32_t batch, dim;
+    float lr;
+
+    TracedMLP(uint32_t b, uint32_t d, float learning_rate, ParamArena& arena)
+        : batch(b), dim(d), lr(learning_rate) {
+        layers.reserve(N);
+        for (size_t i = 0; i < N; ++i) layers.emplace_back(d, d, 0.01f, arena);
+    }
+
+    std::vector<ValuePtr> parameters() const {
+        std::vector<ValuePtr> ps;
+        for (const auto& l : layers)
+            for (auto& p : l.parameters()) ps.push_back(p);
+        return ps;
+    }
+    void sgd_step() { detail::sgd_on(parameters(), lr); }
+};
+
 // One transformer block's parameters (autograd/traced/transformer_train.hpp:76-135): ln1,
 // ln2 (gamma, beta), wq, wk, wv, wo [d, d], w1 [d, ffn], w2 [ffn, d] (weight, bias) = 16
 // tensors, linears filled with 0.01.  sgd_step() (:259-268) is one launch over all 16.

@@ -1,6 +1,7 @@
 // test_modules.cpp — module-level optimizer surfaces: the static layers' sgd_step / zero_grad
 // (autograd/static/nn.hpp:92-101,178-186,213-221,242-250,332-345) and the traced transformer's
-// layer / stack / GPT sgd_step (autograd/traced/transformer_train.hpp:259-268,335-339,487-494).
+// layer / stack / GPT sgd_step (autograd/traced/transformer_train.hpp:259-268,335-339,487-494)
+// and TracedMLP<N>::sgd_step (autograd/traced/mlp.hpp:106-110).
 // Each sgd_step must update exactly its module's tensors, bit-exact against `w - lr*dw`
 // (one rounding per op, bf16 weights = RNE of the fp32 master), in ONE update launch.
 #include "autograd/static.hpp"
@@ -118,6 +119,22 @@ int main() {
         for (size_t k = 2 + 16; k < 2 + 32; ++k) apply(r, k, 0.05f);
         check_all(ps, r, true, "block sgd_step");
         ttp::check(ttp_timing_enable(store.get(), 0));
+    }
+    // ---- traced MLP<4> (autograd/traced/mlp.hpp:106-110) -------------------------------
+    {
+        ParamArena arena(ttp::Mode::Mixed);
+        traced::TracedMLP<4> tm(8, 48, 0.03f, arena);
+        auto ps = tm.parameters();
+        test::check(ps.size() == 8, "TracedMLP<4> parameter count 8");
+        Ref r = snapshot(ps, true, 5.0f);
+        ttp::Store& store = arena.store();
+        ttp::check(ttp_timing_enable(store.get(), 1));
+        update_launches(store);
+        tm.sgd_step();
+        test::check(update_launches(store) == 1, "TracedMLP sgd_step is one update launch");
+        ttp::check(ttp_timing_enable(store.get(), 0));
+        for (size_t k = 0; k < ps.size(); ++k) apply(r, k, 0.03f);
+        check_all(ps, r, true, "TracedMLP sgd_step");
     }
     // ---- traced stack -----------------------------------------------------------------
     {
