@@ -138,6 +138,157 @@ def cpu_baseline(numels, flags, mode_mixed, grads_host, hp, seconds, scaler):
     return out
 
 
+def bucketed_norm(store, stream, args, hp, mode, numels):
+    """The step when its norm comes from per-tensor sums taken bucket by bucket (in reverse
+    tensor order, as a backward produces them; 25 MB of gradients each, or a sixteenth of them
+    for large models), which can run beside the backward's compute; the step then runs the
+    finalize and the update only.  With --overlap, also the share of the bucket sums' time
+    hidden beside a GEMM on another stream.  Returns the JSON object."""
+    import numpy as np
+    import torch
+
+    dev = torch.device("cuda:0")
+    esz = 2 if mode == "mixed" else 4
+    bucket_bytes = max(25 << 20, sum(numels) * esz // 16)
+    buckets, cur, cur_bytes = [], [], 0
+    for i in reversed(range(len(numels))):
+        cur.append(i)
+        cur_bytes += numels[i] * esz
+        if cur_bytes >= bucket_bytes:
+            buckets.append(sorted(cur))
+            cur, cur_bytes = [], 0
+    if cur:
+        buckets.append(sorted(cur))
+
+    def bucket_sums():
+        for b in buckets:
+            store.grad_sumsq_tensors(b)
+
+    def step_after_sums():
+        if args.optimizer == "adamw":
+            store.adam_step(tensor_sums=True, **hp)
+        else:
+            store.sgd_step(lr=hp["lr"], momentum=0.9, max_grad_norm=hp["max_grad_norm"],
+                           tensor_sums=True)
+
+    for _ in range(3):
+        bucket_sums()
+        step_after_sums()
+    torch.cuda.synchronize()
+    # an event pair around the bucket calls and one around the step, per iteration, on the
+    # store's stream: the GPU time of each (subtracting loop totals would mislead where
+    # hundreds of small bucket launches make the bucket loop host-bound)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    for k in range(args.steps):
+        evs[k][0].record(stream)
+        bucket_sums()
+        evs[k][1].record(stream)
+        step_after_sums()
+        evs[k][2].record(stream)
+    torch.cuda.synchronize()
+    sums_ms = sum(a.elapsed_time(b) for a, b, _ in evs) / args.steps
+    after_ms = sum(b.elapsed_time(c) for _, b, c in evs) / args.steps
+    overlap = None
+    if args.overlap:
+        # a bf16 GEMM on its own stream stands in for the backward's compute; the bucket
+        # sums run on the store's stream at the same time
+        comp = torch.cuda.Stream()
+        a = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16)
+        b = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16)
+        c_out = torch.empty(8192, 8192, device=dev, dtype=torch.bfloat16)
+
+        def gemm():
+            with torch.cuda.stream(comp):
+                torch.mm(a, b, out=c_out)
+
+        def both():
+            gemm()
+            bucket_sums()
+
+        # interleaved rounds, each launch synchronised and host-timed; medians
+        runs = {"gemm": [], "sums": [], "both": []}
+        fns = {"gemm": gemm, "sums": bucket_sums, "both": both}
+        for _ in range(3):
+            for fn in fns.values():
+                fn()
+        torch.cuda.synchronize()
+        for _ in range(30):
+            for name, fn in fns.items():
+                t0 = time.perf_counter()
+                fn()
+                torch.cuda.synchronize()
+                runs[name].append((time.perf_counter() - t0) * 1e3)
+        gemm_ms, sums_alone_ms, both_ms = (float(np.median(runs[k]))
+                                           for k in ("gemm", "sums", "both"))
+        overlap = {"gemm_ms": round(gemm_ms, 4), "bucket_sums_ms": round(sums_alone_ms, 4),
+                   "together_ms": round(both_ms, 4),
+                   "sums_hidden_frac": round((gemm_ms + sums_alone_ms - both_ms)
+                                             / sums_alone_ms, 3),
+                   "note": "bf16 8192^3 torch.mm on one stream, the bucket sums on the "
+                           "store's stream; medians of 30 interleaved rounds, each launch "
+                           "synchronised and host-timed"}
+        del a, b, c_out
+    return {"buckets": len(buckets), "bucket_sums_ms": round(sums_ms, 4),
+            "step_after_sums_ms": round(after_ms, 4),
+            "note": "ttp_grad_sumsq_tensors per bucket, then the step with "
+                    "TTP_STEP_TENSOR_SUMS; in training the bucket sums overlap the "
+                    "backward, leaving step_after_sums_ms on the step's own path",
+            "overlap": overlap}
+
+
+def ceilings(stream, update_bytes):
+    """The practical ceilings of the update's traffic on this GPU, over its byte count
+    `update_bytes`: torch's device copy (a blit kernel), and libttperf_ceiling's non-temporal
+    16-byte copy (the update's 50/50 read/write mix) and read-only pass, each timed over 10
+    launches between one event pair on `stream`.  Returns (torch copy GB/s, NT copy GB/s,
+    NT read GB/s, bytes each way)."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    copy_bytes = update_bytes // 2 // 16 * 16
+    src = torch.empty(copy_bytes // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    sink = torch.zeros(1, dtype=torch.float32, device=dev)
+    src.normal_()
+    ceil = ctypes.CDLL(os.path.join(REPO, "tt-perf_amd", "lib", "libttperf_ceiling.so"))
+    ceil.ttpc_copy_nt.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64,
+                                  ctypes.c_int, ctypes.c_void_p]
+    ceil.ttpc_read_nt.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int,
+                                  ctypes.c_void_p, ctypes.c_void_p]
+    # the fastest forms measured (see tt-perf_amd/csrc/ceiling.hip): a straight-line copy,
+    # one block per 4 KB tile, and a read over 8 blocks per CU
+    read_grid = torch.cuda.get_device_properties(dev).multi_processor_count * 8
+    n16 = copy_bytes // 16
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(fn, reps=10):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    def nt_copy():
+        rc = ceil.ttpc_copy_nt(src.data_ptr(), dst.data_ptr(), n16, 0, stream.cuda_stream)
+        assert rc == 0, f"ttpc_copy_nt: hipError {rc}"
+
+    def nt_read():
+        rc = ceil.ttpc_read_nt(src.data_ptr(), n16, read_grid, stream.cuda_stream,
+                               sink.data_ptr())
+        assert rc == 0, f"ttpc_read_nt: hipError {rc}"
+
+    with torch.cuda.stream(stream):
+        copy_gbps = 2 * copy_bytes / (timed(lambda: dst.copy_(src)) / 1e3) / 1e9
+    nt_copy_gbps = 2 * copy_bytes / (timed(nt_copy) / 1e3) / 1e9
+    nt_read_gbps = copy_bytes / (timed(nt_read) / 1e3) / 1e9
+    del src, dst, sink
+    return copy_gbps, nt_copy_gbps, nt_read_gbps, copy_bytes
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -254,152 +405,17 @@ def main():
         skip_ms = e0.elapsed_time(e1)
         assert rs is None
 
-    # context: the step when its norm comes from per-tensor sums taken bucket by bucket (in
-    # reverse tensor order, as a backward produces them; 25 MB of gradients each, or a
-    # sixteenth of them for large models), which can run beside the backward's compute; the
-    # step then runs the finalize and the update only
+    # context: the step with its norm from bucketed per-tensor sums (first undoing the overflow
+    # planted above), and the practical ceilings of the update's traffic on this GPU
     sums = None
     if cfg["hp"]["max_grad_norm"] or cfg["scaler"]:
-        esz = 2 if mode == "mixed" else 4
-        bucket_bytes = max(25 << 20, n_params * esz // 16)
-        buckets, cur, cur_bytes = [], [], 0
-        for i in reversed(range(len(numels))):
-            cur.append(i)
-            cur_bytes += numels[i] * esz
-            if cur_bytes >= bucket_bytes:
-                buckets.append(sorted(cur))
-                cur, cur_bytes = [], 0
-        if cur:
-            buckets.append(sorted(cur))
-
-        def bucket_sums():
-            for b in buckets:
-                store.grad_sumsq_tensors(b)
-
-        def step_from_sums():
-            bucket_sums()
-            if args.optimizer == "adamw":
-                store.adam_step(tensor_sums=True, **hp)
-            else:
-                store.sgd_step(lr=hp["lr"], momentum=0.9, max_grad_norm=hp["max_grad_norm"],
-                               tensor_sums=True)
-
         store.upload(L.BUF_GRAD, 0, torch.zeros(store.tensors[0].numel, device=dev,
                                                 dtype=torch.bfloat16 if mode == "mixed"
-                                                else torch.float32))  # undo the overflow
-        for _ in range(3):
-            step_from_sums()
-        torch.cuda.synchronize()
-        # an event pair around the bucket calls and one around the step, per iteration, on the
-        # store's stream: the GPU time of each (subtracting loop totals would mislead where
-        # hundreds of small bucket launches make the bucket loop host-bound)
-        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)]
-               for _ in range(args.steps)]
-        for k in range(args.steps):
-            evs[k][0].record(stream)
-            bucket_sums()
-            evs[k][1].record(stream)
-            if args.optimizer == "adamw":
-                store.adam_step(tensor_sums=True, **hp)
-            else:
-                store.sgd_step(lr=hp["lr"], momentum=0.9, max_grad_norm=hp["max_grad_norm"],
-                               tensor_sums=True)
-            evs[k][2].record(stream)
-        torch.cuda.synchronize()
-        sums_ms = sum(a.elapsed_time(b) for a, b, _ in evs) / args.steps
-        after_ms = sum(b.elapsed_time(c) for _, b, c in evs) / args.steps
-        overlap = None
-        if args.overlap:
-            # a bf16 GEMM on its own stream stands in for the backward's compute; the bucket
-            # sums run on the store's stream at the same time
-            comp = torch.cuda.Stream()
-            a = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16)
-            b = torch.randn(8192, 8192, device=dev, dtype=torch.bfloat16)
-            c_out = torch.empty(8192, 8192, device=dev, dtype=torch.bfloat16)
-
-            def gemm():
-                with torch.cuda.stream(comp):
-                    torch.mm(a, b, out=c_out)
-
-            def both():
-                gemm()
-                bucket_sums()
-
-            # interleaved rounds, each launch synchronised and host-timed; medians
-            runs = {"gemm": [], "sums": [], "both": []}
-            fns = {"gemm": gemm, "sums": bucket_sums, "both": both}
-            for _ in range(3):
-                for fn in fns.values():
-                    fn()
-            torch.cuda.synchronize()
-            for _ in range(30):
-                for name, fn in fns.items():
-                    t0 = time.perf_counter()
-                    fn()
-                    torch.cuda.synchronize()
-                    runs[name].append((time.perf_counter() - t0) * 1e3)
-            gemm_ms, sums_alone_ms, both_ms_ = (float(np.median(runs[k]))
-                                                for k in ("gemm", "sums", "both"))
-            overlap = {"gemm_ms": round(gemm_ms, 4), "bucket_sums_ms": round(sums_alone_ms, 4),
-                       "together_ms": round(both_ms_, 4),
-                       "sums_hidden_frac": round((gemm_ms + sums_alone_ms - both_ms_)
-                                                 / sums_alone_ms, 3),
-                       "note": "bf16 8192^3 torch.mm on one stream, the bucket sums on the "
-                               "store's stream; medians of 30 interleaved rounds, each launch "
-                               "synchronised and host-timed"}
-            del a, b, c_out
-        sums = {"buckets": len(buckets), "bucket_sums_ms": round(sums_ms, 4),
-                "step_after_sums_ms": round(after_ms, 4),
-                "note": "ttp_grad_sumsq_tensors per bucket, then the step with "
-                        "TTP_STEP_TENSOR_SUMS; in training the bucket sums overlap the "
-                        "backward, leaving step_after_sums_ms on the step's own path",
-                "overlap": overlap}
-
-    # context: the practical ceilings of the update's traffic on this GPU, over the update's
-    # byte count: torch's device copy (a blit kernel), and libttperf_ceiling's non-temporal
-    # 16-byte copy (the update's 50/50 read/write mix) and read-only pass
+                                                else torch.float32))
+        sums = bucketed_norm(store, stream, args, hp, mode, numels)
     ub = UPDATE_BYTES[(args.optimizer, mode)]
     nb = NORM_BYTES[mode]
-    copy_bytes = n_params * ub // 2 // 16 * 16
-    src = torch.empty(copy_bytes // 4, dtype=torch.float32, device=dev)
-    dst = torch.empty_like(src)
-    sink = torch.zeros(1, dtype=torch.float32, device=dev)
-    src.normal_()
-    ceil = ctypes.CDLL(os.path.join(REPO, "tt-perf_amd", "lib", "libttperf_ceiling.so"))
-    ceil.ttpc_copy_nt.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64,
-                                  ctypes.c_int, ctypes.c_void_p]
-    ceil.ttpc_read_nt.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int,
-                                  ctypes.c_void_p, ctypes.c_void_p]
-    # the fastest forms measured (see tt-perf_amd/csrc/ceiling.hip): a straight-line copy,
-    # one block per 4 KB tile, and a read over 8 blocks per CU
-    read_grid = torch.cuda.get_device_properties(dev).multi_processor_count * 8
-    n16 = copy_bytes // 16
-
-    def timed(fn, reps=10):
-        for _ in range(3):
-            fn()
-        torch.cuda.synchronize()
-        e0.record(stream)
-        for _ in range(reps):
-            fn()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / reps
-
-    def nt_copy():
-        rc = ceil.ttpc_copy_nt(src.data_ptr(), dst.data_ptr(), n16, 0, stream.cuda_stream)
-        assert rc == 0, f"ttpc_copy_nt: hipError {rc}"
-
-    def nt_read():
-        rc = ceil.ttpc_read_nt(src.data_ptr(), n16, read_grid, stream.cuda_stream,
-                               sink.data_ptr())
-        assert rc == 0, f"ttpc_read_nt: hipError {rc}"
-
-    with torch.cuda.stream(stream):
-        copy_gbps = 2 * copy_bytes / (timed(lambda: dst.copy_(src)) / 1e3) / 1e9
-    nt_copy_gbps = 2 * copy_bytes / (timed(nt_copy) / 1e3) / 1e9
-    nt_read_gbps = copy_bytes / (timed(nt_read) / 1e3) / 1e9
-    del src, dst, sink
+    copy_gbps, nt_copy_gbps, nt_read_gbps, copy_bytes = ceilings(stream, n_params * ub)
 
     achieved = n_params * ub / (upd_avg / 1e3) / 1e9
     # the instantiation libttperf_hip launches (its rocprof name)
