@@ -129,7 +129,11 @@ typedef struct ttp_sgd_hparams {
  *   set_has_grad) and after the previous step; otherwise the step fails with TTP_ERR_STATE
  *   before any work is queued.  Gradients written through a device pointer after their sum
  *   was taken are the caller's to avoid.  The norm is the same sum of the same squares, added
- *   in another order: it can differ from the norm pass's in the last bits. */
+ *   in another order: it can differ from the norm pass's in the last bits.
+ *   Captured calls count when their graph is launched, not when they are captured: each
+ *   launch consumes or renews sums as its captured steps and sums calls do eagerly, and a
+ *   graph whose step reads sums taken before the capture is refused at launch (TTP_ERR_STATE,
+ *   nothing queued) unless those sums are current. */
 #define TTP_STEP_TENSOR_SUMS 1
 
 /* Dynamic loss scaling (torch.amp.GradScaler semantics).  While enabled, every step

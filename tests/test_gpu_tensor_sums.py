@@ -180,6 +180,74 @@ def test_graph_of_bucket_sums_and_step_replays():
     twin.close()
 
 
+def test_sums_freshness_follows_graph_launches():
+    """Captured calls change which sums are current when their graph is launched, not when
+    they are captured: captured sums make nothing current until a launch, a launched step
+    consumes sums, and a graph whose step reads sums taken before its capture is refused at
+    launch (nothing queued, nothing changed) unless they are current.  Every accepted step
+    matches the oracle."""
+    import ttperf
+    from ttperf import _lib as L
+    torch = torch_mod()
+    store, ref = make_pair(SHAPES, DECAY, O.MODE_MIXED, seed=130)
+    store.set_stream(None)
+    hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, decoupled=True,
+              max_grad_norm=0.05)
+    gen = torch.Generator(device="cuda").manual_seed(131)
+
+    def grads():
+        ref.grad[:store.total] = device_grads(store, gen, 1e-2)
+        for i in range(ref.n):
+            ref.set_has_grad(i, True)
+
+    def refused(fn, why):
+        t0 = store.step_count
+        master = store.download(L.BUF_MASTER).tobytes()
+        with pytest.raises(ttperf.TTPError) as e:
+            fn()
+        assert e.value.code == L.ERR_STATE and "no current gradient sum" in str(e.value), why
+        assert store.step_count == t0, why
+        assert store.download(L.BUF_MASTER).tobytes() == master, why
+        print(f"refused as expected: {why}", flush=True)
+
+    def eager_step():
+        store.adam_step(tensor_sums=True, **hp)
+        ref.adam_step(**hp)
+        compare_state(store, ref, max_ulp=2)
+
+    grads()
+    store.grad_sumsq_tensors()
+    eager_step()  # eager once: work tables, tile buffer and bias table exist
+    # a graph of sums alone: its capture makes nothing current, its launch does
+    grads()
+    store.begin_capture()
+    store.grad_sumsq_tensors()
+    sums_graph = store.end_capture()
+    refused(lambda: store.adam_step(tensor_sums=True, **hp), "the captured sums have not run")
+    sums_graph.replay()
+    eager_step()
+    # a graph of a step reading sums taken before its capture
+    grads()
+    store.grad_sumsq_tensors()
+    store.begin_capture()
+    store.adam_step(tensor_sums=True, **hp)
+    step_graph = store.end_capture()
+    eager_step()  # the capture ran nothing: the eager sums are still current
+    refused(step_graph.replay, "the eager step consumed the sums the graph reads")
+    grads()
+    sums_graph.replay()  # current sums of the new gradients
+    step_graph.replay()
+    ref.adam_step(**hp)
+    store.sync()
+    assert store.step_count == ref.t
+    compare_state(store, ref, max_ulp=2)
+    refused(lambda: store.adam_step(tensor_sums=True, **hp), "the launched step consumed them")
+    refused(step_graph.replay, "the launched step consumed them")
+    sums_graph.close()
+    step_graph.close()
+    store.close()
+
+
 def test_growing_the_tile_buffer_keeps_captured_graphs_valid():
     """A captured bucket-sum call writes the tile buffer it was captured with.  An eager call
     over a larger bucket grows that buffer while the graph is alive; the old one is kept until

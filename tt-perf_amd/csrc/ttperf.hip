@@ -149,6 +149,9 @@ struct ttp_ctx {
     // change of the loss scale, and every step)
     double* tsum = nullptr;
     std::vector<uint8_t> tsum_fresh;
+    std::vector<uint8_t> cap_touched;  // tensors whose freshness the running capture changed
+    std::vector<uint8_t> cap_saved;    // tsum_fresh at ttp_capture_begin
+    std::vector<uint8_t> cap_needs;    // sums a captured step reads that predate the capture
     double* tile_sums = nullptr;  // one per norm tile of a ttp_grad_sumsq_tensors call
     uint32_t tile_sums_cap = 0;
     std::vector<void*> retired;   // replaced buffers that live graphs may still write
@@ -174,6 +177,13 @@ struct ttp_graph {
     ttp_ctx* ctx;
     hipGraph_t graph;
     hipGraphExec_t exec;
+    // what a replay leaves of the per-tensor sums' freshness: the captured calls that changed
+    // it (a step, a gradient write, a sums call) and the state each tensor ended the capture in
+    std::vector<uint32_t> fresh_idx;
+    std::vector<uint8_t> fresh_val;
+    // tensors whose sums a captured step reads without a captured sums call before it: they
+    // must be current at each launch
+    std::vector<uint32_t> needs_fresh;
 };
 
 namespace {
@@ -256,16 +266,29 @@ void free_tables(WorkTables& w) {
     w = WorkTables{};
 }
 
-void stale_sums(ttp_ctx* c) { std::fill(c->tsum_fresh.begin(), c->tsum_fresh.end(), 0); }
+// Freshness of the per-tensor sums changes only through these two, which also note, while a
+// capture runs, which tensors it touched (a replay repeats the change).
+void stale_sums(ttp_ctx* c) {
+    std::fill(c->tsum_fresh.begin(), c->tsum_fresh.end(), 0);
+    if (c->capturing) std::fill(c->cap_touched.begin(), c->cap_touched.end(), 1);
+}
+void set_fresh(ttp_ctx* c, uint32_t i, bool fresh) {
+    c->tsum_fresh[i] = fresh ? 1 : 0;
+    if (c->capturing) c->cap_touched[i] = 1;
+}
 
-// TTP_STEP_TENSOR_SUMS: every tensor the step updates needs a current sum
-int check_sums_current(const ttp_ctx* c, const std::vector<uint32_t>& active) {
+// TTP_STEP_TENSOR_SUMS: every tensor the step updates needs a current sum.  A step being
+// captured notes the sums it reads from before the capture: each launch checks them.
+int check_sums_current(ttp_ctx* c, const std::vector<uint32_t>& active) {
     for (uint32_t i : active)
         if (!c->tsum_fresh[i])
             return fail(TTP_ERR_STATE, "tensor " + std::to_string(i) +
                                            " has no current gradient sum: call "
                                            "ttp_grad_sumsq_tensors after its last gradient write "
                                            "and after the previous step");
+    if (c->capturing)
+        for (uint32_t i : active)
+            if (!c->cap_touched[i]) c->cap_needs[i] = 1;
     return TTP_OK;
 }
 
@@ -426,7 +449,10 @@ struct TimedLaunch {
     void done() {
         if (!a) return;
         hipEvent_t b = take_event(c);
-        if (!b) return;
+        if (!b) {
+            c->ev_pool.push_back(a);  // no pair for it: back to the pool
+            return;
+        }
         (void)hipEventRecord(b, c->stream);
         c->ev[kernel].push_back({a, b});
     }
@@ -1004,7 +1030,7 @@ int ttp_upload(ttp_ctx* c, int which, uint32_t index, const void* src, uint64_t 
             stale_sums(c);
         } else {
             c->tensors[index].has_grad = 1;
-            c->tsum_fresh[index] = 0;
+            set_fresh(c, index, false);
         }
     }
     return TTP_OK;
@@ -1042,7 +1068,7 @@ int ttp_set_has_grad(ttp_ctx* c, uint32_t i, int has) {
     if (rc) return rc;
     if ((rc = check_index(c, i))) return rc;
     c->tensors[i].has_grad = has ? 1 : 0;
-    c->tsum_fresh[i] = 0;  // marks grads written outside the ABI, or drops them
+    set_fresh(c, i, false);  // marks grads written outside the ABI, or drops them
     return TTP_OK;
 }
 
@@ -1089,7 +1115,7 @@ int ttp_zero_grad_subset(ttp_ctx* c, const uint32_t* indices, uint32_t n, int se
     }
     for (uint32_t k = 0; k < n; ++k) {
         c->tensors[indices[k]].has_grad = set_to_none ? 0 : 1;
-        c->tsum_fresh[indices[k]] = 0;
+        set_fresh(c, indices[k], false);
     }
     return TTP_OK;
 }
@@ -1145,7 +1171,7 @@ int ttp_accumulate_grad(ttp_ctx* c, uint32_t index, const void* src, uint64_t n,
         if (kind == TTP_HOST) HIP_TRY(hipStreamSynchronize(c->stream));
     }
     t.has_grad = 1;
-    c->tsum_fresh[index] = 0;
+    set_fresh(c, index, false);
     return TTP_OK;
 }
 
@@ -1417,7 +1443,7 @@ int ttp_grad_sumsq_tensors(ttp_ctx* c, const uint32_t* indices, uint32_t n) {
                            c->stream, c->tile_sums, w->tile_start, w->tensor_ids, c->tsum);
         HIP_TRY(hipGetLastError());
     }
-    for (uint32_t i : active) c->tsum_fresh[i] = 1;
+    for (uint32_t i : active) set_fresh(c, i, true);
     return TTP_OK;
 }
 
@@ -1797,6 +1823,9 @@ int ttp_capture_begin(ttp_ctx* c) {
     c->device_t = true;
     HIP_TRY(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
     c->capturing = true;
+    c->cap_touched.assign(c->tensors.size(), 0);
+    c->cap_needs.assign(c->tensors.size(), 0);
+    c->cap_saved = c->tsum_fresh;
     return TTP_OK;
 }
 
@@ -1808,6 +1837,18 @@ int ttp_capture_end(ttp_ctx* c, ttp_graph** out) {
     hipGraph_t g = nullptr;
     const hipError_t e = hipStreamEndCapture(c->stream, &g);
     c->capturing = false;
+    // nothing captured has run: the sums' freshness returns to its state at ttp_capture_begin,
+    // and each replay applies the captured calls' effect on it
+    std::vector<uint32_t> fresh_idx, needs;
+    std::vector<uint8_t> fresh_val;
+    for (uint32_t i = 0; i < (uint32_t)c->cap_touched.size(); ++i) {
+        if (c->cap_touched[i]) {
+            fresh_idx.push_back(i);
+            fresh_val.push_back(c->tsum_fresh[i]);
+        }
+        if (c->cap_needs[i]) needs.push_back(i);
+    }
+    c->tsum_fresh = c->cap_saved;
     if (e != hipSuccess) {
         if (g) (void)hipGraphDestroy(g);
         return fail(TTP_ERR_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
@@ -1822,7 +1863,7 @@ int ttp_capture_end(ttp_ctx* c, ttp_graph** out) {
         (void)hipGraphDestroy(g);
         return fail(TTP_ERR_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(e2));
     }
-    *out = new ttp_graph{c, g, ex};
+    *out = new ttp_graph{c, g, ex, std::move(fresh_idx), std::move(fresh_val), std::move(needs)};
     c->n_graphs += 1;
     return TTP_OK;
 }
@@ -1830,9 +1871,18 @@ int ttp_capture_end(ttp_ctx* c, ttp_graph** out) {
 int ttp_graph_launch(ttp_graph* g) {
     if (!g) return fail(TTP_ERR_INVALID, "null graph");
     int rc;
-    if ((rc = no_capture(g->ctx, "ttp_graph_launch"))) return rc;
-    if ((rc = set_dev(g->ctx))) return rc;
-    HIP_TRY(hipGraphLaunch(g->exec, g->ctx->stream));
+    ttp_ctx* c = g->ctx;
+    if ((rc = no_capture(c, "ttp_graph_launch"))) return rc;
+    for (uint32_t i : g->needs_fresh)
+        if (!c->tsum_fresh[i])
+            return fail(TTP_ERR_STATE, "the graph steps with per-tensor sums taken before it, and "
+                                       "tensor " + std::to_string(i) + " has no current gradient "
+                                       "sum: call ttp_grad_sumsq_tensors before launching it");
+    if ((rc = set_dev(c))) return rc;
+    HIP_TRY(hipGraphLaunch(g->exec, c->stream));
+    // a replayed step consumes the sums and a replayed sums call renews them, as eagerly
+    for (size_t k = 0; k < g->fresh_idx.size(); ++k)
+        c->tsum_fresh[g->fresh_idx[k]] = g->fresh_val[k];
     return TTP_OK;
 }
 
@@ -1863,16 +1913,21 @@ int ttp_timing_collect(ttp_ctx* c, int kernel, double* total_ms, uint64_t* launc
     double sum = 0.0;
     uint64_t cnt = 0;
     auto& v = c->ev[kernel];
+    // every pair goes back to the pool, also after a failure, so no event is listed twice
+    hipError_t e = hipSuccess;
     for (auto& p : v) {
-        HIP_TRY(hipEventSynchronize(p.b));
         float ms = 0.0f;
-        HIP_TRY(hipEventElapsedTime(&ms, p.a, p.b));
-        sum += ms;
-        ++cnt;
+        if (e == hipSuccess) e = hipEventSynchronize(p.b);
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, p.a, p.b);
+        if (e == hipSuccess) {
+            sum += ms;
+            ++cnt;
+        }
         c->ev_pool.push_back(p.a);
         c->ev_pool.push_back(p.b);
     }
     v.clear();
+    HIP_TRY(e);
     if (total_ms) *total_ms = sum;
     if (launches) *launches = cnt;
     return TTP_OK;
