@@ -304,7 +304,10 @@ int ttp_load_state(ttp_ctx* ctx, const char* path);
  * TTP_ERR_STATE: step each tensor set (and each optimizer, for its state) eagerly once before
  * capturing, pass no step report, and use no host transfers.  The legacy default stream
  * cannot be captured.  A graph replays the tensor sets, hyperparameters and flags seen at
- * capture time.  Destroy a context's graphs before the context (ttp_destroy refuses). */
+ * capture time.  Captured calls change the per-tensor host flags (whether a gradient exists,
+ * whether its sum is current) when the graph is launched: ttp_capture_end restores them to
+ * their state at ttp_capture_begin, and each launch applies what the captured calls did to
+ * them.  Destroy a context's graphs before the context (ttp_destroy refuses). */
 int ttp_capture_begin(ttp_ctx* ctx);
 /* out == NULL discards the capture. */
 int ttp_capture_end(ttp_ctx* ctx, ttp_graph** out);

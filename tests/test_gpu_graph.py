@@ -144,6 +144,55 @@ def test_captured_train_step_zero_accumulate_sgd_momentum():
     store.close()
 
 
+def test_captured_zero_grad_clears_grad_flags_at_launch():
+    """Capturing runs nothing, so it changes no has-grad flag: after capturing
+    zero_grad(set_to_none=True) every gradient is still present, and an eager step updates
+    every tensor, as in the oracle.  Each launch clears the flags (and the gradients) as the
+    eager call does, after which an eager step updates nothing."""
+    from ttperf import _lib as L
+    torch = torch_mod()
+    store, ref = make_pair(SHAPES, DECAY, O.MODE_FP32, seed=94)
+    store.set_stream(None)
+    gen = torch.Generator(device="cuda").manual_seed(95)
+    hp = dict(lr=1e-2, momentum=0.9)
+
+    def grads():
+        ref.grad[:store.total] = device_grads(store, gen, 1e-2)
+        for i in range(ref.n):
+            ref.set_has_grad(i, True)
+
+    def flags():
+        return [store.has_grad(i) for i in range(len(SHAPES))]
+
+    grads()
+    store.sgd_step(**hp)  # eager once: tables and the momentum buffer exist
+    ref.sgd_step(**hp)
+    store.begin_capture()
+    store.zero_grad(set_to_none=True)
+    graph = store.end_capture()
+    assert flags() == [True] * len(SHAPES), "a capture changed the has-grad flags"
+    store.sgd_step(**hp)
+    ref.sgd_step(**hp)
+    compare_state(store, ref, which=("master", "momentum"), max_ulp=2)
+    for k in range(2):
+        graph.replay()
+        store.sync()
+        ref.zero_grad(set_to_none=True)
+        assert flags() == [False] * len(SHAPES), f"launch {k} left has-grad flags set"
+        assert not store.download(L.BUF_GRAD).any()
+        store.sgd_step(**hp)  # no gradients: nothing changes
+        ref.sgd_step(**hp)
+        compare_state(store, ref, which=("master", "momentum"), max_ulp=2)
+        grads()
+        assert flags() == [True] * len(SHAPES)
+        store.sgd_step(**hp)
+        ref.sgd_step(**hp)
+        compare_state(store, ref, which=("master", "momentum"), max_ulp=2)
+        print(f"launch {k}: flags cleared, then set by new gradients", flush=True)
+    graph.close()
+    store.close()
+
+
 def test_capture_rejects_what_cannot_be_captured(tmp_path):
     import ttperf
     from ttperf import _lib as L

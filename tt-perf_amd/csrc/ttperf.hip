@@ -149,9 +149,10 @@ struct ttp_ctx {
     // change of the loss scale, and every step)
     double* tsum = nullptr;
     std::vector<uint8_t> tsum_fresh;
-    std::vector<uint8_t> cap_touched;  // tensors whose freshness the running capture changed
-    std::vector<uint8_t> cap_saved;    // tsum_fresh at ttp_capture_begin
-    std::vector<uint8_t> cap_needs;    // sums a captured step reads that predate the capture
+    // while capturing: which per-tensor host flags the captured calls changed (kCapFresh,
+    // kCapGrad bits), the flags at ttp_capture_begin, and the sums a captured step reads that
+    // predate the capture
+    std::vector<uint8_t> cap_touched, cap_fresh0, cap_grad0, cap_needs;
     double* tile_sums = nullptr;  // one per norm tile of a ttp_grad_sumsq_tensors call
     uint32_t tile_sums_cap = 0;
     std::vector<void*> retired;   // replaced buffers that live graphs may still write
@@ -177,10 +178,13 @@ struct ttp_graph {
     ttp_ctx* ctx;
     hipGraph_t graph;
     hipGraphExec_t exec;
-    // what a replay leaves of the per-tensor sums' freshness: the captured calls that changed
-    // it (a step, a gradient write, a sums call) and the state each tensor ended the capture in
-    std::vector<uint32_t> fresh_idx;
-    std::vector<uint8_t> fresh_val;
+    // what a launch does to the per-tensor host flags (whether a gradient exists, whether its
+    // sum is current): the flags each tensor that a captured call changed ended the capture with
+    struct FlagEffect {
+        uint32_t tensor;
+        uint8_t mask, fresh, has_grad;
+    };
+    std::vector<FlagEffect> effects;
     // tensors whose sums a captured step reads without a captured sums call before it: they
     // must be current at each launch
     std::vector<uint32_t> needs_fresh;
@@ -266,15 +270,22 @@ void free_tables(WorkTables& w) {
     w = WorkTables{};
 }
 
-// Freshness of the per-tensor sums changes only through these two, which also note, while a
-// capture runs, which tensors it touched (a replay repeats the change).
+// The per-tensor host flags (a gradient exists; its sum is current) change only through these
+// three, which also note, while a capture runs, what it changed: nothing captured runs before
+// a launch, so ttp_capture_end restores the flags and each launch applies the change.
+constexpr uint8_t kCapFresh = 1, kCapGrad = 2;
 void stale_sums(ttp_ctx* c) {
     std::fill(c->tsum_fresh.begin(), c->tsum_fresh.end(), 0);
-    if (c->capturing) std::fill(c->cap_touched.begin(), c->cap_touched.end(), 1);
+    if (c->capturing)
+        for (uint8_t& m : c->cap_touched) m |= kCapFresh;
 }
 void set_fresh(ttp_ctx* c, uint32_t i, bool fresh) {
     c->tsum_fresh[i] = fresh ? 1 : 0;
-    if (c->capturing) c->cap_touched[i] = 1;
+    if (c->capturing) c->cap_touched[i] |= kCapFresh;
+}
+void set_grad_flag(ttp_ctx* c, uint32_t i, bool has) {
+    c->tensors[i].has_grad = has ? 1 : 0;
+    if (c->capturing) c->cap_touched[i] |= kCapGrad;
 }
 
 // TTP_STEP_TENSOR_SUMS: every tensor the step updates needs a current sum.  A step being
@@ -288,7 +299,7 @@ int check_sums_current(ttp_ctx* c, const std::vector<uint32_t>& active) {
                                            "and after the previous step");
     if (c->capturing)
         for (uint32_t i : active)
-            if (!c->cap_touched[i]) c->cap_needs[i] = 1;
+            if (!(c->cap_touched[i] & kCapFresh)) c->cap_needs[i] = 1;
     return TTP_OK;
 }
 
@@ -1026,10 +1037,10 @@ int ttp_upload(ttp_ctx* c, int which, uint32_t index, const void* src, uint64_t 
     }
     if (which == TTP_BUF_GRAD) {
         if (index == TTP_ALL_TENSORS) {
-            for (auto& t : c->tensors) t.has_grad = 1;
+            for (uint32_t i = 0; i < (uint32_t)c->tensors.size(); ++i) set_grad_flag(c, i, true);
             stale_sums(c);
         } else {
-            c->tensors[index].has_grad = 1;
+            set_grad_flag(c, index, true);
             set_fresh(c, index, false);
         }
     }
@@ -1067,7 +1078,7 @@ int ttp_set_has_grad(ttp_ctx* c, uint32_t i, int has) {
     int rc = check_ctx(c);
     if (rc) return rc;
     if ((rc = check_index(c, i))) return rc;
-    c->tensors[i].has_grad = has ? 1 : 0;
+    set_grad_flag(c, i, has != 0);
     set_fresh(c, i, false);  // marks grads written outside the ABI, or drops them
     return TTP_OK;
 }
@@ -1087,7 +1098,7 @@ int ttp_zero_grad(ttp_ctx* c, int set_to_none) {
     if ((rc = set_dev(c))) return rc;
     if ((rc = zero_device(c, c->grad, c->total * grad_esize(c)))) return rc;
     if (set_to_none) {
-        for (auto& t : c->tensors) t.has_grad = 0;
+        for (uint32_t i = 0; i < (uint32_t)c->tensors.size(); ++i) set_grad_flag(c, i, false);
     }
     stale_sums(c);
     return TTP_OK;
@@ -1114,7 +1125,7 @@ int ttp_zero_grad_subset(ttp_ctx* c, const uint32_t* indices, uint32_t n, int se
         HIP_TRY(hipGetLastError());
     }
     for (uint32_t k = 0; k < n; ++k) {
-        c->tensors[indices[k]].has_grad = set_to_none ? 0 : 1;
+        set_grad_flag(c, indices[k], !set_to_none);
         set_fresh(c, indices[k], false);
     }
     return TTP_OK;
@@ -1170,7 +1181,7 @@ int ttp_accumulate_grad(ttp_ctx* c, uint32_t index, const void* src, uint64_t n,
         HIP_TRY(hipGetLastError());
         if (kind == TTP_HOST) HIP_TRY(hipStreamSynchronize(c->stream));
     }
-    t.has_grad = 1;
+    set_grad_flag(c, index, true);
     set_fresh(c, index, false);
     return TTP_OK;
 }
@@ -1825,7 +1836,9 @@ int ttp_capture_begin(ttp_ctx* c) {
     c->capturing = true;
     c->cap_touched.assign(c->tensors.size(), 0);
     c->cap_needs.assign(c->tensors.size(), 0);
-    c->cap_saved = c->tsum_fresh;
+    c->cap_fresh0 = c->tsum_fresh;
+    c->cap_grad0.resize(c->tensors.size());
+    for (size_t i = 0; i < c->tensors.size(); ++i) c->cap_grad0[i] = (uint8_t)c->tensors[i].has_grad;
     return TTP_OK;
 }
 
@@ -1837,18 +1850,18 @@ int ttp_capture_end(ttp_ctx* c, ttp_graph** out) {
     hipGraph_t g = nullptr;
     const hipError_t e = hipStreamEndCapture(c->stream, &g);
     c->capturing = false;
-    // nothing captured has run: the sums' freshness returns to its state at ttp_capture_begin,
-    // and each replay applies the captured calls' effect on it
-    std::vector<uint32_t> fresh_idx, needs;
-    std::vector<uint8_t> fresh_val;
+    // nothing captured has run: the per-tensor flags return to their state at
+    // ttp_capture_begin, and each launch applies the captured calls' effect on them
+    std::vector<ttp_graph::FlagEffect> effects;
+    std::vector<uint32_t> needs;
     for (uint32_t i = 0; i < (uint32_t)c->cap_touched.size(); ++i) {
-        if (c->cap_touched[i]) {
-            fresh_idx.push_back(i);
-            fresh_val.push_back(c->tsum_fresh[i]);
-        }
+        if (c->cap_touched[i])
+            effects.push_back({i, c->cap_touched[i], c->tsum_fresh[i],
+                               (uint8_t)c->tensors[i].has_grad});
         if (c->cap_needs[i]) needs.push_back(i);
+        c->tsum_fresh[i] = c->cap_fresh0[i];
+        c->tensors[i].has_grad = c->cap_grad0[i];
     }
-    c->tsum_fresh = c->cap_saved;
     if (e != hipSuccess) {
         if (g) (void)hipGraphDestroy(g);
         return fail(TTP_ERR_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
@@ -1863,7 +1876,7 @@ int ttp_capture_end(ttp_ctx* c, ttp_graph** out) {
         (void)hipGraphDestroy(g);
         return fail(TTP_ERR_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(e2));
     }
-    *out = new ttp_graph{c, g, ex, std::move(fresh_idx), std::move(fresh_val), std::move(needs)};
+    *out = new ttp_graph{c, g, ex, std::move(effects), std::move(needs)};
     c->n_graphs += 1;
     return TTP_OK;
 }
@@ -1880,9 +1893,12 @@ int ttp_graph_launch(ttp_graph* g) {
                                        "sum: call ttp_grad_sumsq_tensors before launching it");
     if ((rc = set_dev(c))) return rc;
     HIP_TRY(hipGraphLaunch(g->exec, c->stream));
-    // a replayed step consumes the sums and a replayed sums call renews them, as eagerly
-    for (size_t k = 0; k < g->fresh_idx.size(); ++k)
-        c->tsum_fresh[g->fresh_idx[k]] = g->fresh_val[k];
+    // as the captured calls do eagerly: a step consumes the sums, a sums call renews them,
+    // gradient writes and zero_grad set or clear the has-grad flags
+    for (const auto& f : g->effects) {
+        if (f.mask & kCapFresh) c->tsum_fresh[f.tensor] = f.fresh;
+        if (f.mask & kCapGrad) c->tensors[f.tensor].has_grad = f.has_grad;
+    }
     return TTP_OK;
 }
 
