@@ -322,6 +322,12 @@ class ParamStore:
         callers, never here."""
         n = self._numel(index)
         if _is_torch(value):
+            if value.is_cuda and self._in_capture:
+                self._check_captured_tensor(value, n, which)
+                # a captured copy, ordered on the store's stream: nothing synchronises here
+                L.check(L.lib.ttp_upload(self._h, which, index, C.c_void_p(value.data_ptr()), n,
+                                         L.DEVICE))
+                return
             t = value.detach().contiguous()
             if t.numel() != n:
                 raise ValueError(f"expected {n} elements, got {t.numel()}")
@@ -346,11 +352,25 @@ class ParamStore:
             raise ValueError(f"expected {n} elements, got {a.size}")
         L.check(L.lib.ttp_upload(self._h, which, index, a.ctypes.data_as(C.c_void_p), n, L.HOST))
 
+    def _check_captured_tensor(self, t, n, which):
+        """While capturing, a device transfer becomes a copy node that reads or writes `t`'s
+        memory at every launch of the graph: `t` itself must be contiguous, of the buffer's
+        element count and size, and kept alive (and ordered on the store's stream) by the
+        caller for as long as the graph is launched."""
+        if t.numel() != n or t.element_size() != self._esize(which) or not t.is_contiguous():
+            raise ValueError(f"a captured transfer needs a contiguous device tensor of {n} "
+                             f"elements of {self._esize(which)} bytes, used in place")
+
     def download(self, which, index=L.ALL_TENSORS, out=None):
         """The buffer's elements (bf16 as uint16 bits), into a new numpy array or into `out`:
         a contiguous, writable numpy array or torch tensor (host or device) of exactly the
         element count and element size, which the ABI fills in place."""
         n = self._numel(index)
+        if out is not None and _is_torch(out) and out.is_cuda and self._in_capture:
+            self._check_captured_tensor(out, n, which)
+            L.check(L.lib.ttp_download(self._h, which, index, C.c_void_p(out.data_ptr()), n,
+                                       L.DEVICE))
+            return out
         if out is not None and _is_torch(out):
             if out.numel() != n or out.element_size() != self._esize(which) or \
                     not out.is_contiguous():
@@ -430,12 +450,21 @@ class ParamStore:
         n = self.tensors[index].numel
         if _is_torch(value):
             import torch
-            t = value.detach().contiguous()
-            if t.dtype not in (torch.float32, torch.bfloat16):
+            if value.dtype not in (torch.float32, torch.bfloat16):
                 raise ValueError("incoming gradients must be float32 or bfloat16")
+            dtype = L.DTYPE_BF16 if value.dtype == torch.bfloat16 else L.DTYPE_F32
+            if value.is_cuda and self._in_capture:
+                # captured: the graph reads `value` in place at every launch (see
+                # _check_captured_tensor); nothing synchronises here
+                if value.numel() != n or not value.is_contiguous():
+                    raise ValueError(f"a captured accumulate needs a contiguous device tensor "
+                                     f"of {n} elements, used in place")
+                L.check(L.lib.ttp_accumulate_grad(self._h, index, C.c_void_p(value.data_ptr()),
+                                                  n, dtype, L.DEVICE))
+                return
+            t = value.detach().contiguous()
             if t.numel() != n:
                 raise ValueError(f"expected {n} elements, got {t.numel()}")
-            dtype = L.DTYPE_BF16 if t.dtype == torch.bfloat16 else L.DTYPE_F32
             if t.is_cuda:
                 torch.cuda.current_stream(t.device).synchronize()
             L.check(L.lib.ttp_accumulate_grad(self._h, index, C.c_void_p(t.data_ptr()), n, dtype,
