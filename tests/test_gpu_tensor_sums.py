@@ -66,6 +66,54 @@ def test_step_from_bucket_sums_matches_oracle_and_norm_pass(mode):
     twin.close()
 
 
+def test_bucket_sums_at_gpt2_124m_full_size():
+    """Config 3 at its real shapes (148 tensors, 124.4M params, bf16 gradients): loss scaling,
+    clipping and AdamW, the norm taken from bench.py's buckets (25 MB of gradients each, in
+    reverse tensor order), with an overflow at a seeded index on the second step.  Against the
+    oracle: the same skip / scale / step decisions, the norm within 1e-10 relative, the state
+    within 2 ulp."""
+    from ttperf import configs
+    from ttperf import _lib as L
+    torch = torch_mod()
+    _, shapes, decay, numels = configs.table("gpt2_124m")
+    assert len(shapes) == 148 and sum(numels) == 124439808
+    store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=132)
+    store.configure_scaler(True, init_scale=65536.0)
+    ref.configure_scaler(True, 65536.0)
+    buckets, cur, cur_bytes = [], [], 0
+    for i in reversed(range(len(numels))):
+        cur.append(i)
+        cur_bytes += numels[i] * 2
+        if cur_bytes >= 25 << 20:
+            buckets.append(sorted(cur))
+            cur, cur_bytes = [], 0
+    if cur:
+        buckets.append(sorted(cur))
+    assert sorted(i for b in buckets for i in b) == list(range(len(numels)))
+    hp = dict(lr=6e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
+    gen = torch.Generator(device="cuda").manual_seed(133)
+    for step in range(3):
+        inf_at = store.offsets[76] + 12345 if step == 1 else None  # h.6 attn.c_attn.weight
+        host = device_grads(store, gen, 1e-3, scale=ref.scale, inf_at=inf_at)
+        ref.grad[:store.total] = host
+        del host
+        for i in range(ref.n):
+            ref.set_has_grad(i, True)
+        for b in buckets:
+            store.grad_sumsq_tensors(b)
+        r = store.adam_step(report=True, tensor_sums=True, **hp)
+        e = ref.adam_step(**hp)
+        print(f"step {step}: {len(buckets)} buckets, norm {r['grad_norm']!r} (oracle "
+              f"{e['grad_norm']!r}), skipped {r['skipped']}, scale {r['scale']}", flush=True)
+        for k in ("skipped", "found_inf", "step", "scale", "growth_tracker"):
+            assert r[k] == e[k], (k, r, e)
+        assert r["skipped"] == (step == 1)
+        if np.isfinite(e["grad_norm"]):
+            assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-10 * e["grad_norm"]
+    compare_state(store, ref, max_ulp=2)
+    store.close()
+
+
 def test_sgd_momentum_subset_step_from_sums():
     """SGD with momentum over a subset: only the subset's tensors need sums."""
     from ttperf import _lib as L
