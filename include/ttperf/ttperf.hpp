@@ -7,6 +7,7 @@
 // (bench/autograd/bench_gpt2_full.cpp:153-165).
 #pragma once
 
+#include <atomic>
 #include <cstdint>
 #include <cstring>
 #include <map>
@@ -83,8 +84,10 @@ class Store;
 // The step counts an optimizer keeps for the stores whose count another optimizer held when
 // it last stepped them.  py/optim.py:46,50 keeps `_step` per optimizer; the count the
 // kernels read lives in the store, so optimizers hand it over (Store::claim_step_count).
+// Keyed by Store::uid(), never reused within a process, so a store allocated where a
+// destroyed one lived does not inherit its count.
 struct StepCounts {
-    std::map<const Store*, uint64_t> saved;
+    std::map<uint64_t, uint64_t> saved;
 };
 
 // A captured graph of a store's work (ttp_capture_begin .. ttp_capture_end); move-only.  It
@@ -145,6 +148,7 @@ public:
     Store& operator=(const Store&) = delete;
 
     ttp_ctx* get() const { return ctx_; }
+    uint64_t uid() const { return uid_; }
     Mode mode() const { return mode_; }
     size_t size() const { return specs_.size(); }
     const TensorSpec& spec(uint32_t i) const { return specs_.at(i); }
@@ -278,13 +282,13 @@ public:
     void claim_step_count(const std::shared_ptr<StepCounts>& me) {
         std::shared_ptr<StepCounts> prev = t_owner_.lock();
         if (prev == me) return;
-        auto it = me->saved.find(this);
+        auto it = me->saved.find(uid_);
         if (prev || it != me->saved.end()) {
             if (capturing_)
                 throw std::runtime_error(
                     "libttperf_hip: a second optimizer steps this store inside a graph capture; "
                     "the step count hand-over reads the device and cannot be captured");
-            if (prev) prev->saved[this] = step_count();
+            if (prev) prev->saved[uid_] = step_count();
             uint64_t t = 0;
             if (it != me->saved.end()) {
                 t = it->second;
@@ -323,8 +327,14 @@ private:
         return v;
     }
 
+    static uint64_t next_uid() {
+        static std::atomic<uint64_t> n{0};
+        return ++n;
+    }
+
     std::vector<TensorSpec> specs_;
     Mode mode_;
+    uint64_t uid_ = next_uid();
     ttp_ctx* ctx_ = nullptr;
     bool capturing_ = false;
     std::weak_ptr<StepCounts> t_owner_;  // the optimizer whose step count the store holds

@@ -230,6 +230,30 @@ static void run_tensor_sums() {
     test::check(thrown, "tensor sums: a step after a gradient write without new sums throws");
 }
 
+// Saved step counts belong to the store they were saved for: a store created after another
+// was destroyed (here most likely at the same heap address) starts from its own count, not
+// from what an optimizer saved for the destroyed one.
+static void run_counts_outlive_store() {
+    const std::vector<ttp::TensorSpec> specs = {{{256}, false, "w"}};
+    auto a = std::make_shared<ttp::StepCounts>(), b = std::make_shared<ttp::StepCounts>();
+    ttp::AdamOptions o;
+    auto s1 = std::make_unique<ttp::Store>(specs, ttp::Mode::FP32);
+    s1->set_grad(0, std::vector<float>(256, 0.5f));
+    s1->claim_step_count(a);
+    for (int k = 0; k < 3; ++k) s1->adam_step(o);
+    s1->claim_step_count(b);  // a's count (3) saved for s1
+    s1->adam_step(o);
+    const void* where = s1.get();
+    s1.reset();
+    auto s2 = std::make_unique<ttp::Store>(specs, ttp::Mode::FP32);
+    s2->set_grad(0, std::vector<float>(256, 0.5f));
+    s2->claim_step_count(a);
+    s2->adam_step(o);
+    std::printf("counts: new store %s the destroyed one's address\n",
+                (const void*)s2.get() == where ? "at" : "not at");
+    test::check(s2->step_count() == 1, "a new store does not inherit a destroyed store's count");
+}
+
 int main() {
     test::DeviceGuard dg;
     run(false);
@@ -237,6 +261,7 @@ int main() {
     run_groups();
     run_graph_groups();
     run_tensor_sums();
+    run_counts_outlive_store();
     // py/optim.py:33-41 validation
     ParamArena arena;
     Linear l(4, 4, arena);
