@@ -283,7 +283,8 @@ int ttp_scaler_set(ttp_ctx* ctx, float scale, int32_t growth_tracker);
  * of all preceding bytes.  Both calls are synchronous and stream through a 64 MiB pinned
  * buffer.  ttp_save_state writes `path`.tmp and renames it over `path` when complete, so a
  * failed save leaves an earlier file at `path` as it was.  ttp_load_state requires the same
- * mode and tensor table (numel and flags); a buffer the file lacks is zeroed; the bf16
+ * mode and tensor table (numel and flags), and loss-scaler values in the ranges that
+ * ttp_scaler_configure and ttp_scaler_set accept; a buffer the file lacks is zeroed; the bf16
  * weights are recomputed from the master.  It reads the whole file and checks its size and
  * checksum before it changes the context, so a damaged, truncated or mismatched file is
  * rejected with the context unchanged (only an I/O error on the second read, or a file

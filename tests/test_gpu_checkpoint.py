@@ -1,6 +1,8 @@
 """GPU tests of the optimizer-state checkpoint (ttp_save_state / ttp_load_state): a run that
 is saved, loaded into a fresh context and continued ends bit-identical to the uninterrupted
 run; malformed, mismatched and corrupted files are rejected."""
+import struct
+
 import numpy as np
 import pytest
 
@@ -142,6 +144,38 @@ def test_load_rejects_mismatch_and_corruption(tmp_path):
     (tmp_path / "junk.bin").write_bytes(b"not a state file at all" * 4)
     expect_invalid(a, tmp_path / "junk.bin", "not an optimizer-state file")
     expect_invalid(a, tmp_path / "missing.bin", "cannot open")
+    # a well-formed file whose loss-scaler fields are out of range is refused, before the
+    # store is touched.  The file is re-signed with the format's checksum: a 64-bit
+    # multiply-xor hash over the 8-byte little-endian words of everything before it (for a
+    # store this small every hashed piece is whole words), then a final avalanche.
+    def resign(body):
+        m = (1 << 64) - 1
+        h = 0xcbf29ce484222325
+        for (w,) in struct.iter_unpack("<Q", body):
+            h = ((h ^ w) * 0x100000001b3) & m
+            h ^= h >> 29
+        h ^= h >> 33
+        h = (h * 0xff51afd7ed558ccd) & m
+        h ^= h >> 33
+        return body + struct.pack("<Q", h)
+
+    assert len(raw) % 8 == 0 and resign(raw[:-8]) == raw, "the checksum restatement"
+    scaled = ttperf.ParamStore([(100,), (64, 8)], mode="mixed")
+    scaled.configure_scaler(True, init_scale=1024.0, growth_interval=3)
+    scaled.save_state(tmp_path / "scaled.bin")
+    good = (tmp_path / "scaled.bin").read_bytes()
+    assert resign(good[:-8]) == good
+    # header: magic[8], u32 version/mode/n_tensors/buffers, u64 total/t, f32 scale,
+    # i32 growth_tracker/scaler_enabled/growth_interval, f64 init_scale/growth/backoff
+    for off, fmt, value, what in ((52, "<i", 0, "loss-scaler settings"),
+                                  (72, "<d", 1.5, "loss-scaler settings"),
+                                  (40, "<f", -1.0, "loss scale"),
+                                  (44, "<i", -2, "growth tracker")):
+        bad = bytearray(good[:-8])
+        struct.pack_into(fmt, bad, off, value)
+        (tmp_path / "bad_scaler.bin").write_bytes(resign(bytes(bad)))
+        expect_invalid(a, tmp_path / "bad_scaler.bin", what)
+    scaled.close()
     # a save goes through path.tmp: none is left behind, and a failed rename removes it
     assert not (tmp_path / "s.bin.tmp").exists()
     (tmp_path / "adir").mkdir()

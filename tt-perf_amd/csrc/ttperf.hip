@@ -1728,6 +1728,13 @@ int ttp_load_state(ttp_ctx* c, const char* path) {
                                          std::to_string(c->tensors.size()));
     if (!(h.buffers & 1u) || (h.buffers & ~15u))
         return fail(TTP_ERR_INVALID, "state file buffer mask is malformed");
+    // the ranges ttp_scaler_configure and ttp_scaler_set accept
+    if (h.scaler_enabled &&
+        (!(h.init_scale > 0) || !(h.growth_factor > 1) ||
+         !(h.backoff_factor > 0 && h.backoff_factor < 1) || h.growth_interval <= 0))
+        return fail(TTP_ERR_INVALID, "state file loss-scaler settings are out of range");
+    if (!(h.scale > 0) || h.growth_tracker < 0)
+        return fail(TTP_ERR_INVALID, "state file loss scale or growth tracker is out of range");
     std::vector<uint32_t> mom(std::max<size_t>(c->tensors.size(), 1), 0);
     for (size_t i = 0; i < c->tensors.size(); ++i) {
         StateTensor t;
