@@ -92,7 +92,7 @@ typedef struct ttp_tensor_desc {
     uint64_t numel;  /* elements; 0 is allowed (the tensor is then never touched); the
                         64-element-padded sizes of a table total at most 2^40 */
     uint32_t flags;  /* TTP_TENSOR_* */
-    uint32_t reserved;
+    uint32_t reserved; /* must be 0 */
 } ttp_tensor_desc;
 
 /* Adam / AdamW.  Hyperparameters are host doubles (Python floats in py/optim.py:31-47);

@@ -84,6 +84,11 @@ def test_c_abi_argument_errors_without_a_device():
     assert b"mode" in lib.ttp_last_error()
     d[0].flags = 0x80
     assert lib.ttp_create(0, d, 1, L.MODE_FP32, C.byref(h)) == L.ERR_INVALID  # unknown flag
+    d[0].flags = 0
+    d[0].reserved = 1
+    assert lib.ttp_create(0, d, 1, L.MODE_FP32, C.byref(h)) == L.ERR_INVALID  # reserved != 0
+    assert b"reserved" in lib.ttp_last_error()
+    d[0].reserved = 0
     # a table whose padded sizes would wrap 64 bits (or exceed 2^40 elements) is rejected
     # before any device work: a wrapped footprint would let kernels index past the buffers
     d[0].flags = 0

@@ -801,6 +801,8 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
     for (uint32_t i = 0; i < n; ++i) {
         if (descs[i].flags & ~TTP_TENSOR_DECAY)
             return fail(TTP_ERR_INVALID, "unknown flags on tensor " + std::to_string(i));
+        if (descs[i].reserved)
+            return fail(TTP_ERR_INVALID, "tensor " + std::to_string(i) + ": reserved must be 0");
         if (descs[i].numel > kMaxElems)
             return fail(TTP_ERR_INVALID, "tensor " + std::to_string(i) + " has " +
                                              std::to_string(descs[i].numel) +
