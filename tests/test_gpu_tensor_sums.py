@@ -368,11 +368,12 @@ def test_optimizer_step_with_tensor_sums():
 
 
 def test_bucket_sums_on_a_side_stream_wait_for_the_backward():
-    """INTEGRATION.md's pattern: the backward writes each bucket's gradients on its own stream
-    (through the zero-copy grad views, after a long GEMM standing in for its compute) and
-    records an event; the bucket sums run on a side stream, each after its bucket's event; the
-    step follows on the side stream once the whole backward is done.  A sum that ran before its
-    event would see the zeroed gradients, and the clip would differ from the twin's."""
+    """The documented side-stream pattern: the backward writes each bucket's gradients on its
+    own stream (through the zero-copy grad views, after a long GEMM standing in for its
+    compute) and records an event; the bucket sums run on a side stream, each after its
+    bucket's event; the step follows on the side stream once the whole backward is done.  A
+    sum that ran before its event would see the zeroed gradients, and the clip would differ
+    from the twin's."""
     import ttperf
     from ttperf import _lib as L
     torch = torch_mod()
