@@ -6,6 +6,7 @@ import ctypes as C
 import os
 import re
 import subprocess
+import sys
 
 import pytest
 
@@ -260,6 +261,17 @@ def test_product_code_never_touches_the_oracle():
             if re.search(r"ttp_oracle|orc_", open(os.path.join(root, f)).read()):
                 hits.append(os.path.join(root, f))
     assert not hits, hits
+
+
+@pytest.mark.parametrize("args, env", [(["--gpus", "2"], {}), ([], {"WORLD_SIZE": "2"})])
+def test_bench_refuses_more_than_one_gpu(args, env):
+    """This build measures one GPU: bench.py with --gpus above 1 (or under a multi-rank
+    launcher) exits with status 2 and says so, before it touches a GPU."""
+    e = dict(os.environ, **env)
+    r = subprocess.run([sys.executable, os.path.join(REPO, "bench.py")] + args, env=e,
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2, (r.returncode, r.stderr)
+    assert "one GPU" in r.stderr and not r.stdout.strip()
 
 
 def test_one_hip_runtime_is_mapped():
