@@ -250,6 +250,42 @@ def test_captured_python_device_transfers_use_the_callers_tensors():
     store.close()
 
 
+def test_per_launch_timing_skips_captured_work():
+    """With per-kernel timing on, eager steps record one event pair per kernel launch; a
+    capture records none (an event recorded into it would become part of the graph), and
+    launches of the graph are not timed.  The replayed steps still run (the step count)."""
+    import ttperf
+    from ttperf import _lib as L
+    store = ttperf.ParamStore([(300, 7), (64,)], mode="mixed")
+    store.set_stream(None)
+    store.configure_scaler(True, init_scale=1024.0)
+    for t in store.tensors:
+        t.grad = np.zeros(t.numel, np.uint16)
+    store.adam_step(lr=1e-3, max_grad_norm=1.0)  # eager once: tables and bias table
+    store.timing(True)
+    store.adam_step(lr=1e-3, max_grad_norm=1.0)
+    store.sync()
+    for k in (L.KERNEL_NORM, L.KERNEL_UPDATE):
+        ms, n = store.timing_collect(k)
+        assert n == 1 and ms > 0, (k, n, ms)
+    store.begin_capture()
+    store.adam_step(lr=1e-3, max_grad_norm=1.0)
+    graph = store.end_capture()
+    t0 = store.step_count
+    for _ in range(3):
+        graph.replay()
+    store.sync()
+    assert store.step_count == t0 + 3
+    for k in (L.KERNEL_NORM, L.KERNEL_UPDATE):
+        assert store.timing_collect(k) == (0.0, 0), k
+    store.adam_step(lr=1e-3, max_grad_norm=1.0)
+    store.sync()
+    assert store.timing_collect(L.KERNEL_UPDATE)[1] == 1
+    store.timing(False)
+    graph.close()
+    store.close()
+
+
 def test_capture_rejects_what_cannot_be_captured(tmp_path):
     import ttperf
     from ttperf import _lib as L
