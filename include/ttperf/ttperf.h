@@ -165,7 +165,10 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n_tensors, int
                ttp_ctx** out);
 int ttp_destroy(ttp_ctx* ctx);
 /* Order all further work on an existing HIP stream (hipStream_t passed as void*; NULL is
- * the legacy default stream, e.g. torch's default stream).  Waits for work already queued. */
+ * the legacy default stream, e.g. torch's default stream).  Waits for work already queued.
+ * The stream stays the caller's: it must remain valid until the context moves to another
+ * stream (ttp_set_stream, ttp_reset_stream) or is destroyed, since ttp_destroy and
+ * ttp_graph_destroy wait on it. */
 int ttp_set_stream(ttp_ctx* ctx, void* hip_stream);
 /* Back to the context's own (non-blocking) stream. */
 int ttp_reset_stream(ttp_ctx* ctx);
