@@ -242,6 +242,7 @@ class ParamStore:
         self._graphs = weakref.WeakSet()
         self._in_capture = False
         self._t_owner = None  # weakref to the optimizer whose step count the store holds
+        self._stream_obj = None  # the adopted stream (set_stream), kept alive while in use
 
     # ---- lifetime --------------------------------------------------------------------------
     def close(self):
@@ -282,10 +283,13 @@ class ParamStore:
         default stream); None returns to the context's own stream."""
         if stream is None:
             L.check(L.lib.ttp_reset_stream(self._h))
+            self._stream_obj = None
             return
-        if hasattr(stream, "cuda_stream"):
-            stream = stream.cuda_stream
-        L.check(L.lib.ttp_set_stream(self._h, C.c_void_p(int(stream))))
+        handle = stream.cuda_stream if hasattr(stream, "cuda_stream") else stream
+        L.check(L.lib.ttp_set_stream(self._h, C.c_void_p(int(handle))))
+        # the store queues work on this stream until it moves or closes: keep the object
+        # (a torch.cuda.Stream, say) alive as long
+        self._stream_obj = stream
 
     def sync(self):
         L.check(L.lib.ttp_sync(self._h))
