@@ -11,8 +11,8 @@ host interface, mirrored on the oracle:
   or over a subset, with or without clipping, with step reports; steps that take their norm
   from bucket sums (ttp_grad_sumsq_tensors), and their refusal after a gradient write; the
   loss scaler switched on or off; the step count set; the gradient norm probed; a checkpoint
-  saved and later loaded; an Adam step captured into a graph and replayed later, between
-  other operations.
+  saved and later loaded; an Adam step captured into a graph (half of them together with
+  the bucket sums it takes its norm from) and replayed later, between other operations.
 
 After every operation the whole state is compared: master, m, v and momentum within the
 2-ulp bar of the other parity tests (in practice 0), bf16 weights and the gradients bit for
@@ -357,9 +357,18 @@ class Case:
         active = self._active(indices)
         if active != eager_active:
             return self.op_adam()
-        print(f"  capture adam {hp} indices={indices} active={active}", flush=True)
+        # half the graphs take their norm from bucket sums captured with the step (an eager
+        # sums call first gives the tile buffer its size: a capture cannot allocate)
+        sums = bool(self.rng.random() < 0.5)
+        print(f"  capture adam{' from captured bucket sums' if sums else ''} {hp} "
+              f"indices={indices} active={active}", flush=True)
+        bucket = list(range(self.n)) if indices is None else indices
+        if sums:
+            self.store.grad_sumsq_tensors(bucket)
         self.store.begin_capture()
-        self.store.adam_step(indices=indices, **hp)
+        if sums:
+            self.store.grad_sumsq_tensors(bucket)
+        self.store.adam_step(indices=indices, tensor_sums=sums, **hp)
         self.graphs.append((self.store.end_capture(), hp, active))
 
     def op_replay(self):
