@@ -12,7 +12,8 @@ host interface, mirrored on the oracle:
   from bucket sums (ttp_grad_sumsq_tensors), and their refusal after a gradient write; the
   loss scaler switched on or off; the step count set; the gradient norm probed; a checkpoint
   saved and later loaded; an Adam step captured into a graph (half of them together with
-  the bucket sums it takes its norm from) and replayed later, between other operations.
+  the bucket sums it takes its norm from), and a zero_grad captured into one, replayed
+  later, between other operations.
 
 After every operation the whole state is compared: master, m, v and momentum within the
 2-ulp bar of the other parity tests (in practice 0), bf16 weights and the gradients bit for
@@ -61,6 +62,7 @@ class Case:
         self.store.set_stream(None)  # the store's own stream: capturable
         self.numels = [t.numel for t in self.store.tensors]
         self.graphs = []      # (graph, hp, captured active set)
+        self.zero_graphs = []  # (graph, set_to_none, indices) of captured zero_grad calls
         self.last_adam = None  # (hp, indices, active set) of the last eager Adam step
         self.saved = None     # oracle snapshot of the last checkpoint
         self.path = tmp_path / f"state_{seed}.bin"
@@ -282,9 +284,10 @@ class Case:
         on = not self.scaler_on
         init = float(2.0 ** int(self.rng.integers(4, 14)))
         interval = int(self.rng.integers(2, 5))
+        live = len(self.graphs) + len(self.zero_graphs)  # every graph holds the settings
         print(f"  scaler {'on' if on else 'off'} (init {init:g}, interval {interval}), "
-              f"{len(self.graphs)} live graph(s)", flush=True)
-        if self.graphs:
+              f"{live} live graph(s)", flush=True)
+        if live:
             import ttperf
             with pytest.raises(ttperf.TTPError):
                 self.store.configure_scaler(on, init_scale=init, growth_interval=interval)
@@ -331,9 +334,10 @@ class Case:
         snap = self.saved
         differs = bool(snap["enabled"]) != self.scaler_on or (
             self.scaler_on and snap["interval"] != self.ref.s.growth_interval)
-        print(f"  load_state <- {self.path.name} ({len(self.graphs)} live graph(s), "
+        live = len(self.graphs) + len(self.zero_graphs)
+        print(f"  load_state <- {self.path.name} ({live} live graph(s), "
               f"scaler settings differ: {differs})", flush=True)
-        if self.graphs and differs:
+        if live and differs:
             import ttperf
             with pytest.raises(ttperf.TTPError):
                 self.store.load_state(self.path)
@@ -379,10 +383,39 @@ class Case:
         g.replay()
         self._ref_step("adam", hp, active)
 
+    def _zero_ref(self, none, idx):
+        if idx is None:
+            self.ref.zero_grad(set_to_none=none)
+            return
+        for i in idx:
+            self.ref.view("grad", i)[:] = 0
+            self.ref.set_has_grad(i, not none)
+
+    def op_zero_graph(self):
+        """A captured zero_grad (all tensors or a subset, to zeros or to None).  Capturing it
+        changes nothing, neither the gradients nor the has-grad flags; each launch does what
+        the eager call does.  A subset is zeroed eagerly once first, since a capture cannot
+        build its work table."""
+        if self.zero_graphs and (len(self.zero_graphs) >= 2 or self.rng.random() < 0.7):
+            g, none, idx = self.zero_graphs[int(self.rng.integers(0, len(self.zero_graphs)))]
+            print(f"  replay zero_grad(set_to_none={none}, indices={idx})", flush=True)
+            g.replay()
+            self._zero_ref(none, idx)
+            return
+        none = bool(self.rng.integers(0, 2))
+        idx = None if self.rng.random() < 0.5 else self.pick_subset()
+        print(f"  capture zero_grad(set_to_none={none}, indices={idx})", flush=True)
+        if idx is not None:
+            self.store.zero_grad(set_to_none=none, indices=idx)
+            self._zero_ref(none, idx)
+        self.store.begin_capture()
+        self.store.zero_grad(set_to_none=none, indices=idx)
+        self.zero_graphs.append((self.store.end_capture(), none, idx))
+
     OPS = [("grads_flat", 6), ("grad_one", 3), ("accumulate", 3), ("drop_grad", 2),
            ("zero_grad", 2), ("upload_weights", 1), ("adam", 6), ("sgd", 4), ("scaler", 1),
            ("set_step", 1), ("grad_norm", 1), ("save", 1), ("load", 1), ("capture", 2),
-           ("replay", 3), ("sums_step", 4)]
+           ("replay", 3), ("sums_step", 4), ("zero_graph", 2)]
 
     def compare(self):
         from ttperf import _lib as L
@@ -403,9 +436,10 @@ class Case:
             assert (scale, tracker) == (np.float32(self.ref.scale), self.ref.growth_tracker)
 
     def close(self):
-        for g, _, _ in self.graphs:
+        for g, _, _ in self.graphs + self.zero_graphs:
             g.close()
         self.graphs.clear()
+        self.zero_graphs.clear()
         self.store.close()
 
 
