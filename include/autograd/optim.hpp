@@ -13,6 +13,10 @@
 // count is saved and this optimizer's restored (ttp::Store::claim_step_count: a synchronising
 // read and a write, on a change of owner only; a graph hands the count back to the optimizer
 // that held it at capture before each launch).  Copies of an optimizer share one count.
+// With loss scaling on an arena stepped by several optimizers in one iteration, set
+// opts.update_scale = false on every one but the last (or on all, then call the store's
+// scaler_update()): the scale then moves once per iteration, from the overflow of all of
+// them, as torch's GradScaler.step per optimizer followed by one GradScaler.update.
 #pragma once
 
 #include <algorithm>

@@ -31,9 +31,14 @@ inline void sgd(const std::vector<ValuePtr>& ps, float lr) {
     auto idx = indices(ps);
     ps.front()->store().sgd_step(o, &idx);
 }
+// zeros_like gradients (autograd/static/nn.hpp:98-101): zeroed and present afterwards, so
+// the next sgd_step updates every listed tensor even before a backward has written it
 inline void zero(const std::vector<ValuePtr>& ps) {
     if (ps.empty()) return;
-    ps.front()->store().zero_grad(indices(ps), /*set_to_none=*/false);
+    ttp::Store& st = ps.front()->store();
+    const auto idx = indices(ps);
+    st.zero_grad(idx, /*set_to_none=*/false);
+    for (uint32_t i : idx) st.set_has_grad(i, true);
 }
 }  // namespace detail
 

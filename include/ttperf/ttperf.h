@@ -90,7 +90,8 @@ typedef struct ttp_graph ttp_graph;
 
 typedef struct ttp_tensor_desc {
     uint64_t numel;  /* elements; 0 is allowed (the tensor is then never touched); the
-                        64-element-padded sizes of a table total at most 2^40 */
+                        64-element-padded sizes of a table total at most 2^40; at most
+                        2^24 - 1 tensors */
     uint32_t flags;  /* TTP_TENSOR_* */
     uint32_t reserved; /* must be 0 */
 } ttp_tensor_desc;
@@ -126,15 +127,29 @@ typedef struct ttp_sgd_hparams {
  *   sums of squares that ttp_grad_sumsq_tensors stored for the step's tensors, instead of a
  *   norm pass over all their gradients.  Every tensor the step updates needs a current sum:
  *   one computed after its last gradient write through this ABI (upload, accumulate, zero,
- *   set_has_grad) and after the previous step; otherwise the step fails with TTP_ERR_STATE
- *   before any work is queued.  Gradients written through a device pointer after their sum
- *   was taken are the caller's to avoid.  The norm is the same sum of the same squares, added
+ *   set_has_grad), after the last step that updated that tensor, and after the last change
+ *   of the loss scale (a step that updates it, ttp_scaler_update, configure, set or a loaded
+ *   state); otherwise the step fails with TTP_ERR_STATE before any work is queued.
+ *   Gradients written through a device pointer after their sum was taken are the caller's
+ *   to avoid.  The norm is the same sum of the same squares, added
  *   in another order: it can differ from the norm pass's in the last bits.
  *   Captured calls count when their graph is launched, not when they are captured: each
  *   launch consumes or renews sums as its captured steps and sums calls do eagerly, and a
  *   graph whose step reads sums taken before the capture is refused at launch (TTP_ERR_STATE,
  *   nothing queued) unless those sums are current. */
 #define TTP_STEP_TENSOR_SUMS 1
+/* TTP_STEP_DEFER_SCALE: with loss scaling on, the step unscales, checks its own tensors for
+ *   inf/NaN and skips its own update on overflow, but leaves the loss scale and the growth
+ *   tracker as they are and notes the overflow instead.  This is torch's GradScaler.step for
+ *   one of several optimizers of an iteration: give it to every step of the iteration but
+ *   the last, or to all of them and then call ttp_scaler_update.  The next step without the
+ *   flag (or ttp_scaler_update) updates the scale once, backing off if that step or any
+ *   deferred step since the last update saw an overflow (GradScaler.update).  Without the
+ *   flag every step updates the scale itself, which is right for one optimizer per store:
+ *   several optimizers over disjoint tensor groups of one store that each update it would
+ *   unscale later groups by a moved scale and advance the tracker once per optimizer.
+ *   Ignored while loss scaling is off. */
+#define TTP_STEP_DEFER_SCALE 2
 
 /* Dynamic loss scaling (torch.amp.GradScaler semantics).  While enabled, every step
  * unscales the gradients by 1/scale, skips the whole update when any gradient is
@@ -221,9 +236,12 @@ int ttp_get_has_grad(const ttp_ctx* ctx, uint32_t index, int* has_grad);
  * One fill over the flat buffer replaces the per-tensor zeros_like allocations of
  * autograd/static/nn.hpp:98-101 and the nullopt loop of autograd/dynamic/optim.hpp:30-34. */
 int ttp_zero_grad(ttp_ctx* ctx, int set_to_none);
-/* A module's zero_grad: the listed tensors' grads (each index at most once) become zeros and
- * stay present (set_to_none = 0: the static layers' zeros_like, autograd/static/nn.hpp:98-101,
- * 183-186) or become None (set_to_none = 1).  One launch over the listed tensors. */
+/* A module's zero_grad: the listed tensors' grads (each index at most once) become zeros
+ * (set_to_none = 0: the static layers' zeros_like, autograd/static/nn.hpp:98-101, 183-186)
+ * or become None (set_to_none = 1).  As with ttp_zero_grad, set_to_none = 0 leaves the
+ * has-grad flags as they are (a tensor without a grad stays without one, as in torch's
+ * zero_grad(set_to_none=False)); a caller whose zeroed grads count as present, like the
+ * static layers, marks them with ttp_set_has_grad.  One launch over the listed tensors. */
 int ttp_zero_grad_subset(ttp_ctx* ctx, const uint32_t* indices, uint32_t n_indices,
                          int set_to_none);
 /* Value::accumulate_grad (autograd/dynamic/autograd.hpp:78-83; static_autograd::Value,
@@ -231,7 +249,11 @@ int ttp_zero_grad_subset(ttp_ctx* ctx, const uint32_t* indices, uint32_t n_indic
  * its grad becomes the incoming gradient; otherwise grad = grad + incoming, added in fp32 and
  * rounded once (round-to-nearest-even) to the grad buffer's type.  `src` holds exactly numel
  * values of `src_dtype` (TTP_DTYPE_*) in host or device memory (`src_kind`).  Marks the
- * tensor as having a grad.  Stream-ordered; a host source is consumed before returning. */
+ * tensor as having a grad.  Stream-ordered; a host source is consumed before returning.
+ * Captured, the call's choice between assigning and adding is fixed at capture time, so it
+ * is refused (TTP_ERR_STATE) unless an earlier call of the same capture set that tensor's
+ * has-grad flag (ttp_zero_grad[_subset] with set_to_none = 1, ttp_set_has_grad, a gradient
+ * upload or an accumulate): every launch then finds the flag as the capture did. */
 int ttp_accumulate_grad(ttp_ctx* ctx, uint32_t index, const void* src, uint64_t n,
                         int src_dtype, int src_kind);
 
@@ -271,6 +293,12 @@ int ttp_set_step(ttp_ctx* ctx, uint64_t step);
 int ttp_scaler_configure(ttp_ctx* ctx, const ttp_scaler_config* cfg);
 int ttp_scaler_get(ttp_ctx* ctx, float* scale, int32_t* growth_tracker);
 int ttp_scaler_set(ttp_ctx* ctx, float scale, int32_t growth_tracker);
+/* The scale update of an iteration whose steps all passed TTP_STEP_DEFER_SCALE
+ * (torch.amp.GradScaler.update after several GradScaler.step calls): back off if any of them
+ * saw an overflow, else count one clean step toward growth.  Stream-ordered, capturable; a
+ * no-op while loss scaling is off.  ttp_scaler_configure, ttp_scaler_set and ttp_load_state
+ * drop a pending overflow; ttp_save_state does not record one (save between iterations). */
+int ttp_scaler_update(ttp_ctx* ctx);
 
 /* ---- optimizer-state checkpoint ------------------------------------------------------------
  * The reference has no optimizer checkpoint (its TTNN tensors live only in device memory).

@@ -47,9 +47,12 @@ struct AdamOptions {
     bool decoupled = true;
     double max_grad_norm = 0.0;
     bool tensor_sums = false;  // norm from Store::grad_sumsq_tensors (TTP_STEP_TENSOR_SUMS)
+    // false: leave the loss scale to the iteration's last step or Store::scaler_update()
+    // (TTP_STEP_DEFER_SCALE), for all but the last of several optimizers over one store
+    bool update_scale = true;
     ttp_adam_hparams c() const {
         ttp_adam_hparams h{};
-        h.flags = tensor_sums ? TTP_STEP_TENSOR_SUMS : 0;
+        h.flags = (tensor_sums ? TTP_STEP_TENSOR_SUMS : 0) | (update_scale ? 0 : TTP_STEP_DEFER_SCALE);
         h.lr = lr;
         h.beta1 = beta1;
         h.beta2 = beta2;
@@ -66,9 +69,10 @@ struct SgdOptions {
     bool nesterov = false;
     double max_grad_norm = 0.0;
     bool tensor_sums = false;  // norm from Store::grad_sumsq_tensors (TTP_STEP_TENSOR_SUMS)
+    bool update_scale = true;  // as AdamOptions::update_scale
     ttp_sgd_hparams c() const {
         ttp_sgd_hparams h{};
-        h.flags = tensor_sums ? TTP_STEP_TENSOR_SUMS : 0;
+        h.flags = (tensor_sums ? TTP_STEP_TENSOR_SUMS : 0) | (update_scale ? 0 : TTP_STEP_DEFER_SCALE);
         h.lr = lr;
         h.momentum = momentum;
         h.dampening = dampening;
@@ -244,6 +248,8 @@ public:
         ttp_scaler_config c{enabled ? 1 : 0, interval, init_scale, growth, backoff};
         check(ttp_scaler_configure(ctx_, &c));
     }
+    // GradScaler.update() after steps that all had update_scale = false
+    void scaler_update() { check(ttp_scaler_update(ctx_)); }
     std::pair<float, int32_t> scaler_state() {
         float s = 0;
         int32_t t = 0;

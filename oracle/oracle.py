@@ -21,6 +21,7 @@ _LIB_PATH = os.path.join(_HERE, "build", "libttp_oracle.so")
 MODE_FP32 = 0
 MODE_MIXED = 1
 DECAY = 1
+DEFER_SCALE = 2  # ORC_STEP_DEFER_SCALE
 ALIGN = 64  # elements; the engine's tensor alignment
 
 
@@ -38,18 +39,18 @@ class Store(C.Structure):
                 ("growth_interval", C.c_int32), ("growth_factor", C.c_double),
                 ("backoff_factor", C.c_double), ("scale", C.c_float),
                 ("growth_tracker", C.c_int32), ("t", C.c_uint64), ("nthreads", C.c_int32),
-                ("reserved", C.c_int32)]
+                ("pending_inf", C.c_int32)]
 
 
 class AdamHP(C.Structure):
     _fields_ = [("lr", C.c_double), ("beta1", C.c_double), ("beta2", C.c_double),
                 ("eps", C.c_double), ("weight_decay", C.c_double), ("decoupled", C.c_int32),
-                ("reserved", C.c_int32), ("max_grad_norm", C.c_double)]
+                ("flags", C.c_int32), ("max_grad_norm", C.c_double)]
 
 
 class SgdHP(C.Structure):
     _fields_ = [("lr", C.c_double), ("momentum", C.c_double), ("dampening", C.c_double),
-                ("weight_decay", C.c_double), ("nesterov", C.c_int32), ("reserved", C.c_int32),
+                ("weight_decay", C.c_double), ("nesterov", C.c_int32), ("flags", C.c_int32),
                 ("max_grad_norm", C.c_double)]
 
 
@@ -89,6 +90,7 @@ def lib():
         L.orc_clip_coef.argtypes = [C.c_double, C.c_double]
         L.orc_scaler_update.argtypes = [C.POINTER(C.c_float), C.POINTER(C.c_int32), C.c_int,
                                         C.c_double, C.c_double, C.c_int32]
+        L.orc_scaler_update_pending.argtypes = [C.POINTER(Store)]
         L.orc_layout.restype = C.c_uint64
         L.orc_layout.argtypes = [C.c_void_p, C.c_uint32, C.c_uint64, C.c_void_p]
         L.orc_accumulate_grad.argtypes = [C.POINTER(Store), C.c_uint32, C.c_void_p, C.c_int]
@@ -226,6 +228,7 @@ class OracleStore:
         self.s.backoff_factor = backoff_factor
         self.s.growth_interval = growth_interval
         self.s.growth_tracker = 0
+        self.s.pending_inf = 0
 
     @property
     def t(self):
@@ -246,12 +249,18 @@ class OracleStore:
     def set_scaler_state(self, scale, tracker):
         self.s.scale = scale
         self.s.growth_tracker = tracker
+        self.s.pending_inf = 0
+
+    def scaler_update(self):
+        """The scale update after steps that all deferred it (update_scale=False)."""
+        lib().orc_scaler_update_pending(C.byref(self.s))
 
     # ---- steps -----------------------------------------------------------------------------
     def adam_step(self, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0,
-                  decoupled=True, max_grad_norm=0.0, opbyop=False):
+                  decoupled=True, max_grad_norm=0.0, opbyop=False, update_scale=True):
         hp = AdamHP(lr=lr, beta1=betas[0], beta2=betas[1], eps=eps, weight_decay=weight_decay,
-                    decoupled=1 if decoupled else 0, reserved=0, max_grad_norm=max_grad_norm)
+                    decoupled=1 if decoupled else 0, flags=0 if update_scale else DEFER_SCALE,
+                    max_grad_norm=max_grad_norm)
         rep = Report()
         fn = lib().orc_adam_step_opbyop if opbyop else lib().orc_adam_step
         rc = fn(C.byref(self.s), C.byref(hp), C.byref(rep))
@@ -260,9 +269,10 @@ class OracleStore:
         return rep.as_dict()
 
     def sgd_step(self, lr, momentum=0.0, dampening=0.0, weight_decay=0.0, nesterov=False,
-                 max_grad_norm=0.0):
+                 max_grad_norm=0.0, update_scale=True):
         hp = SgdHP(lr=lr, momentum=momentum, dampening=dampening, weight_decay=weight_decay,
-                   nesterov=1 if nesterov else 0, reserved=0, max_grad_norm=max_grad_norm)
+                   nesterov=1 if nesterov else 0, flags=0 if update_scale else DEFER_SCALE,
+                   max_grad_norm=max_grad_norm)
         rep = Report()
         rc = lib().orc_sgd_step(C.byref(self.s), C.byref(hp), C.byref(rep))
         if rc != 0:

@@ -280,10 +280,21 @@ static void step_prologue(orc_store* s, double max_norm, float* inv_scale, float
     }
 }
 
-static void step_epilogue(orc_store* s, int found_inf, orc_report* rep) {
-    if (s->scaler_enabled)
-        orc_scaler_update(&s->scale, &s->growth_tracker, found_inf, s->growth_factor,
-                          s->backoff_factor, s->growth_interval);
+/* torch GradScaler: each optimizer's step checks and skips on its own overflow; update()
+ * then moves the scale once, on the overflow found by any optimizer since the last update
+ * (found_inf summed over optimizers, torch/amp/grad_scaler.py update) */
+void orc_scaler_update_pending(orc_store* s) {
+    if (!s->scaler_enabled) return;
+    orc_scaler_update(&s->scale, &s->growth_tracker, s->pending_inf, s->growth_factor,
+                      s->backoff_factor, s->growth_interval);
+    s->pending_inf = 0;
+}
+
+static void step_epilogue(orc_store* s, int found_inf, int defer, orc_report* rep) {
+    if (s->scaler_enabled) {
+        s->pending_inf |= found_inf ? 1 : 0;
+        if (!defer) orc_scaler_update_pending(s);
+    }
     if (rep) {
         /* without loss scaling the report carries scale 1 and tracker 0 */
         rep->scale = s->scaler_enabled ? s->scale : 1.0f;
@@ -323,7 +334,7 @@ int orc_adam_step(orc_store* s, const orc_adam_hp* hp, orc_report* rep) {
         }
         free(ch);
     }
-    step_epilogue(s, r->found_inf, r);
+    step_epilogue(s, r->found_inf, hp->flags & ORC_STEP_DEFER_SCALE, r);
     return 0;
 }
 
@@ -404,7 +415,7 @@ int orc_adam_step_opbyop(orc_store* s, const orc_adam_hp* hp, orc_report* rep) {
             free(mh); free(vh); free(den);
         }
     }
-    step_epilogue(s, r->found_inf, r);
+    step_epilogue(s, r->found_inf, hp->flags & ORC_STEP_DEFER_SCALE, r);
     return 0;
 }
 
@@ -476,6 +487,6 @@ int orc_sgd_step(orc_store* s, const orc_sgd_hp* hp, orc_report* rep) {
             for (uint64_t k = 0; k < nc; ++k) s->mom_init[ch[k].tensor] = 1;
         free(ch);
     }
-    step_epilogue(s, r->found_inf, r);
+    step_epilogue(s, r->found_inf, hp->flags & ORC_STEP_DEFER_SCALE, r);
     return 0;
 }

@@ -66,18 +66,23 @@ typedef struct orc_store {
     int32_t growth_tracker;
     uint64_t t;            /* applied steps */
     int32_t nthreads;
-    int32_t reserved;
+    int32_t pending_inf;   /* overflow seen by steps that deferred the scale update */
 } orc_store;
+
+/* step flag: with loss scaling on, skip this step's own update on overflow but leave the
+ * scale update to the iteration's last step or orc_scaler_update_pending (torch's
+ * GradScaler.step for one of several optimizers, then one GradScaler.update) */
+#define ORC_STEP_DEFER_SCALE 2
 
 typedef struct orc_adam_hp {
     double lr, beta1, beta2, eps, weight_decay;
-    int32_t decoupled, reserved;
+    int32_t decoupled, flags;
     double max_grad_norm;
 } orc_adam_hp;
 
 typedef struct orc_sgd_hp {
     double lr, momentum, dampening, weight_decay;
-    int32_t nesterov, reserved;
+    int32_t nesterov, flags;
     double max_grad_norm;
 } orc_sgd_hp;
 
@@ -106,6 +111,8 @@ float orc_bias_correction(double beta, uint64_t t);
 float orc_clip_coef(double norm, double max_norm);
 void orc_scaler_update(float* scale, int32_t* tracker, int found_inf, double growth_factor,
                        double backoff_factor, int32_t growth_interval);
+/* GradScaler.update after deferred steps: the scale update over their pending overflow */
+void orc_scaler_update_pending(orc_store* s);
 
 /* layout: offsets of n tensors, each aligned up to `align` elements; returns total */
 uint64_t orc_layout(const uint64_t* numel, uint32_t n, uint64_t align, uint64_t* offsets);

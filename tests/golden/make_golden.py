@@ -168,6 +168,43 @@ def gen_scaler():
     np.savez(os.path.join(OUT, "torch_scaler.npz"), **out)
 
 
+def gen_scaler_two_optimizers(steps=14, inf1=(4, 9), inf2=(5, 9, 12), interval=3):
+    """GradScaler with two optimizers over two parameters: GradScaler.step(opt) for each,
+    then one GradScaler.update() per iteration.  Each optimizer skips on its own overflow;
+    the scale moves once, on the overflow of either (and grows after `interval` iterations
+    in which neither overflowed)."""
+    p1 = torch.nn.Parameter(torch.ones(4))
+    p2 = torch.nn.Parameter(torch.ones(3))
+    o1 = torch.optim.SGD([p1], lr=0.0)
+    o2 = torch.optim.SGD([p2], lr=0.0)
+    sc = torch.amp.GradScaler("cpu", init_scale=2.0 ** 16, growth_factor=2.0,
+                              backoff_factor=0.5, growth_interval=interval)
+    scales, trackers, skip1, skip2 = [], [], [], []
+    for s in range(1, steps + 1):
+        sc.scale(p1.sum() + p2.sum()).backward()
+        if s in inf1:
+            p1.grad[2] = float("inf")
+        if s in inf2:
+            p2.grad[0] = float("inf")
+        sc.unscale_(o1)
+        sc.unscale_(o2)
+        f1 = sum(v.item() for v in sc._found_inf_per_device(o1).values())
+        f2 = sum(v.item() for v in sc._found_inf_per_device(o2).values())
+        sc.step(o1)
+        sc.step(o2)
+        sc.update()
+        o1.zero_grad()
+        o2.zero_grad()
+        scales.append(sc.get_scale())
+        trackers.append(int(sc._growth_tracker.item()))
+        skip1.append(int(f1 > 0))
+        skip2.append(int(f2 > 0))
+    np.savez(os.path.join(OUT, "torch_scaler_two_opt.npz"),
+             scale=np.array(scales, np.float64), tracker=np.array(trackers, np.int32),
+             skip1=np.array(skip1, np.int32), skip2=np.array(skip2, np.int32),
+             inf1=np.array(inf1), inf2=np.array(inf2), interval=np.array(interval))
+
+
 def gen_clip():
     out = {}
     g = torch.Generator().manual_seed(5)
@@ -244,6 +281,7 @@ if __name__ == "__main__":
     gen_adam_family()
     gen_sgd_family()
     gen_scaler()
+    gen_scaler_two_optimizers()
     gen_clip()
     gen_reference_known_answers()
     print("fixtures written to", OUT)

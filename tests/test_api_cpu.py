@@ -189,12 +189,12 @@ class _CountingStore:
         self._t = t
 
     def adam_step(self, lr, betas, eps, weight_decay, decoupled, max_grad_norm, indices=None,
-                  tensor_sums=False):
+                  tensor_sums=False, update_scale=True):
         self._t += 1
         self.log.append((lr, self._t))
 
     def sgd_step(self, lr, momentum, dampening, weight_decay, nesterov, max_grad_norm,
-                 indices=None, tensor_sums=False):
+                 indices=None, tensor_sums=False, update_scale=True):
         self._t += 1
         self.log.append((lr, self._t))
 

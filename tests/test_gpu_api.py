@@ -492,6 +492,73 @@ def test_two_adam_parameter_groups_keep_their_own_step_counts():
     store.close()
 
 
+@pytest.mark.parametrize("how", ["defer_first", "defer_all_then_update"])
+def test_two_optimizers_share_one_scale_update_per_iteration(how):
+    """Loss scaling with two optimizers over two groups of one store, as torch's
+    GradScaler.step(opt_a), GradScaler.step(opt_b), GradScaler.update(): each optimizer skips
+    on an overflow in its own gradients only, the scale moves once per iteration (backing off
+    if either group overflowed, growing after `interval` clean iterations), and each group's
+    step count is its own.  Either the first step defers the update to the second, or both
+    defer and ParamStore.scaler_update() runs.  Checked against the oracle after every
+    iteration (reports, scale, tracker) and in the final state."""
+    import ttperf
+    from ttperf import _lib as L
+    torch = torch_mod()
+    shapes = [(64, 48), (48,), (48, 32), (32,), (300,)]
+    decay = [True, False, True, False, False]
+    store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=97)
+    store.configure_scaler(True, init_scale=2.0 ** 12, growth_interval=3)
+    ref.configure_scaler(True, 2.0 ** 12, growth_interval=3)
+    groups = {"a": [0, 1, 4], "b": [2, 3]}
+    hp = dict(lr=3e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
+    opts = {g: ttperf.AdamW([store.tensors[i] for i in groups[g]], **hp) for g in groups}
+    counts = {"a": 0, "b": 0}
+    inf_in = {3: "a", 5: "b", 8: "ab", 12: "a"}
+    gen = torch.Generator(device="cuda").manual_seed(98)
+    rng = np.random.default_rng(99)
+    scales = []
+    for it in range(1, 15):
+        inf_at = []
+        for g in inf_in.get(it, ""):
+            t = groups[g][int(rng.integers(0, len(groups[g])))]
+            inf_at.append(store.offsets[t] + int(rng.integers(0, store.tensors[t].numel)))
+        host = device_grads(store, gen, 1e-2, scale=ref.scale)
+        if inf_at:  # +inf in the chosen groups, on the device and in the oracle's copy
+            g16 = store.download(L.BUF_GRAD)
+            for k in inf_at:
+                g16[k] = 0x7F80  # bf16 +inf
+            store.upload(L.BUF_GRAD, L.ALL_TENSORS, g16)
+            host = g16
+        ref.grad[:store.total] = host
+        for g in "ab":
+            last = g == "b" and how == "defer_first"
+            for i in range(ref.n):
+                ref.set_has_grad(i, i in groups[g])
+            opts[g].step(update_scale=last)
+            ref.t = counts[g]
+            e = ref.adam_step(update_scale=last, **hp)
+            assert e["skipped"] == (g in inf_in.get(it, "")), (it, g)
+            assert e["step"] == counts[g] + (0 if e["skipped"] else 1)
+            counts[g] = ref.t
+            # the store holds the stepping optimizer's count: a skip leaves it unchanged
+            assert store.step_count == e["step"], (it, g)
+            assert store.scaler_state() == (e["scale"], e["growth_tracker"]), (it, g)
+        if how == "defer_all_then_update":
+            store.scaler_update()
+            ref.scaler_update()
+        scale, tracker = store.scaler_state()
+        assert (scale, tracker) == (ref.scale, ref.growth_tracker), it
+        scales.append(scale)
+        print(f"iteration {it}: overflow in {inf_in.get(it, '-')!r}, scale {scale}, "
+              f"tracker {tracker}, counts {counts}", flush=True)
+    # one move per iteration: a backoff at iterations 3, 5, 8 (both groups: once) and 12,
+    # growth after the three clean iterations 9-11
+    assert scales == [4096.0, 4096.0, 2048.0, 2048.0, 1024.0, 1024.0, 1024.0, 512.0, 512.0,
+                      512.0, 1024.0, 512.0, 512.0, 512.0]
+    compare_state(store, ref, max_ulp=2)
+    store.close()
+
+
 def test_out_of_memory_is_reported_and_stale_hip_errors_are_not_misattributed():
     """A store larger than the device fails with TTP_ERR_OOM (TTPMemoryError) and leaves no
     trace: HIP keeps a failed call's error as the thread's "last error", which the engine's

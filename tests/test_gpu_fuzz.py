@@ -145,7 +145,8 @@ class Case:
             self.store.zero_grad(set_to_none=none, indices=idx)
             for i in idx:
                 self.ref.view("grad", i)[:] = 0
-                self.ref.set_has_grad(i, not none)
+                if none:  # set_to_none=False leaves the has-grad flags as they are
+                    self.ref.set_has_grad(i, False)
 
     def op_upload_weights(self):
         i = int(self.rng.integers(0, self.n))
@@ -389,7 +390,8 @@ class Case:
             return
         for i in idx:
             self.ref.view("grad", i)[:] = 0
-            self.ref.set_has_grad(i, not none)
+            if none:
+                self.ref.set_has_grad(i, False)
 
     def op_zero_graph(self):
         """A captured zero_grad (all tensors or a subset, to zeros or to None).  Capturing it

@@ -496,3 +496,96 @@ def test_closing_a_capturing_store_ends_its_capture():
     r = other.adam_step(lr=1e-3, report=True)
     assert r["step"] == 1
     other.close()
+
+
+def test_captured_accumulate_needs_its_flag_set_in_the_same_capture():
+    """Whether an accumulate assigns (no grad yet) or adds is fixed when it is captured, so a
+    captured accumulate is refused (TTP_ERR_STATE, nothing queued, the capture still valid)
+    unless an earlier call of the same capture set that tensor's has-grad flag: an
+    accumulate-only graph would otherwise overwrite on every launch when captured without a
+    grad, or add onto stale values after an eager set_has_grad(0).  Zeroing to zeros leaves
+    the flag as a launch finds it, so it does not count.  A graph that sets the flag itself
+    (set_has_grad(0), then two accumulates: assign, then add) replays as the eager calls do,
+    whatever the flag is at launch: launched twice in a row, and after an eager
+    set_has_grad(1) and an eager set_has_grad(0), each time equal to the oracle."""
+    import ttperf
+    from ttperf import _lib as L
+    torch = torch_mod()
+    store, ref = make_pair(SHAPES, DECAY, O.MODE_MIXED, seed=140)
+    store.set_stream(None)
+    i = 2
+    n = store.tensors[i].numel
+    a = torch.zeros(n, dtype=torch.float32, device="cuda")
+    b = torch.zeros(n, dtype=torch.bfloat16, device="cuda")
+    gen = torch.Generator(device="cuda").manual_seed(141)
+    store.tensors[i].accumulate_grad(a)  # eager once: staging, and the one-tensor table
+    store.zero_grad(set_to_none=False, indices=[i])
+
+    def refused(calls, why):
+        store.begin_capture()
+        try:
+            calls()
+            with pytest.raises(ttperf.TTPError) as e:
+                store.accumulate_grad(i, a)
+            assert e.value.code == L.ERR_STATE and "fixed when it is captured" in str(e.value)
+        finally:
+            store.end_capture(discard=True)
+        print(f"refused as expected: {why}", flush=True)
+
+    refused(lambda: None, "an accumulate-only capture")
+    refused(lambda: store.zero_grad(set_to_none=False, indices=[i]),
+            "zeroing to zeros does not set the flag")
+    refused(lambda: store.zero_grad(set_to_none=False), "nor does the whole-store zero_grad")
+    refused(lambda: store.set_has_grad(1, False), "a flag set for another tensor")
+
+    store.begin_capture()
+    store.set_has_grad(i, False)
+    store.accumulate_grad(i, a)  # assigns
+    store.accumulate_grad(i, b)  # adds
+    graph = store.end_capture()
+    for k, before in enumerate([None, None, True, False]):
+        a.copy_(torch.randn(n, generator=gen, device="cuda") * 0.1)
+        b.copy_((torch.randn(n, generator=gen, device="cuda") * 0.1).to(torch.bfloat16))
+        torch.cuda.synchronize()
+        if before is not None:  # an eager flag change between launches
+            store.set_has_grad(i, before)
+        graph.replay()
+        store.sync()
+        ref.set_has_grad(i, False)
+        ref.accumulate_grad(i, a.cpu().numpy())
+        ref.accumulate_grad(i, b.cpu().view(torch.int16).numpy().view(np.uint16))
+        got = store.download(L.BUF_GRAD, i)
+        assert np.array_equal(got, ref.view("grad", i)), f"launch {k}"
+        assert store.has_grad(i)
+        print(f"launch {k} (flag before: {before}): grad equals the oracle's", flush=True)
+    graph.close()
+    store.close()
+
+
+def test_zero_grad_subset_to_zeros_keeps_the_has_grad_flags():
+    """zero_grad(set_to_none=False) over some tensors zeroes their grads and leaves their
+    has-grad flags as they were, as the whole-store call and torch's
+    zero_grad(set_to_none=False) do: a tensor without a grad is still skipped by the next
+    step (py/optim.py:56-57), one with a grad is stepped with a zero gradient."""
+    from ttperf import _lib as L
+    torch = torch_mod()
+    store, ref = make_pair(SHAPES, DECAY, O.MODE_FP32, seed=142)
+    gen = torch.Generator(device="cuda").manual_seed(143)
+    ref.grad[:store.total] = device_grads(store, gen, 1e-2)
+    for k in range(ref.n):
+        ref.set_has_grad(k, True)
+    store.tensors[1].grad = None
+    ref.set_has_grad(1, False)
+    store.zero_grad(set_to_none=False, indices=[1, 3])
+    for k in (1, 3):
+        ref.view("grad", k)[:] = 0
+    assert [store.has_grad(k) for k in range(len(SHAPES))] == \
+        [ref.has_grad(k) for k in range(len(SHAPES))] == [k != 1 for k in range(len(SHAPES))]
+    assert not store.download(L.BUF_GRAD, 3).any()
+    before = store.tensors[1].master().copy()
+    hp = dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
+    store.adam_step(**hp)
+    ref.adam_step(**hp)
+    assert np.array_equal(store.tensors[1].master(), before)
+    compare_state(store, ref, which=("master", "exp_avg", "exp_avg_sq"), max_ulp=2)
+    store.close()

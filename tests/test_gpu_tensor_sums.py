@@ -161,6 +161,12 @@ def test_stale_or_missing_sums_are_refused():
     store.grad_sumsq_tensors()
     store.adam_step(**hp)  # current sums: accepted
     refused("a step consumed the sums")
+    # a step consumes the sums of the tensors it updates only: without a scale update the
+    # others stay current, for the iteration's other optimizers
+    store.grad_sumsq_tensors()
+    store.adam_step(indices=[0, 1, 2], **hp)
+    refused("the first group's sums were consumed")
+    store.adam_step(indices=[3, 4, 5, 6, 7], **hp)
     for write in (lambda: store.tensors[2].__setattr__("grad", np.zeros(129 * 33, np.uint16)),
                   lambda: store.tensors[3].accumulate_grad(np.ones(5, np.float32)),
                   lambda: store.mark_grads([4]),
@@ -174,7 +180,7 @@ def test_stale_or_missing_sums_are_refused():
     # without clipping or loss scaling there is no norm to take: the flag is accepted
     store.configure_scaler(False)
     store.adam_step(lr=1e-3, tensor_sums=True)
-    bad = L.AdamHParams(lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, flags=2)
+    bad = L.AdamHParams(lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, flags=4)
     assert L.lib.ttp_adam_step(store.handle, bad, None) == L.ERR_INVALID
     store.close()
 

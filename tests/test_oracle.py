@@ -226,6 +226,53 @@ def test_scaler_sequences_match_torch():
     assert np.array_equal(s, d["forced_scale"]) and np.array_equal(t, d["forced_tracker"])
 
 
+def _two_optimizer_scaler_run(d, defer_first=True, call_update=False):
+    """Two parameter groups of one loss-scaled oracle store stepped as two optimizers per
+    iteration (group 0 = tensor 0, group 1 = tensor 1), as tests/golden's
+    torch_scaler_two_opt fixture steps two torch optimizers under one GradScaler."""
+    st = O.OracleStore([4, 3], mode=O.MODE_MIXED)
+    st.configure_scaler(True, 65536.0, 2.0, 0.5, int(d["interval"]))
+    inf1, inf2 = set(d["inf1"].tolist()), set(d["inf2"].tolist())
+    scales, trackers, skip1, skip2 = [], [], [], []
+    for s in range(1, len(d["scale"]) + 1):
+        g0 = np.ones(4, np.float32) * st.scale
+        g1 = np.ones(3, np.float32) * st.scale
+        if s in inf1:
+            g0[2] = np.inf
+        if s in inf2:
+            g1[0] = np.inf
+        st.set_grad(0, O.bf16_rne(g0))
+        st.set_grad(1, O.bf16_rne(g1))
+        st.set_has_grad(1, False)  # optimizer 1 owns tensor 0
+        r1 = st.sgd_step(lr=1e-3, update_scale=not defer_first)
+        st.set_has_grad(0, False)
+        st.set_has_grad(1, True)   # optimizer 2 owns tensor 1
+        r2 = st.sgd_step(lr=1e-3, update_scale=not call_update)
+        if call_update:
+            st.scaler_update()
+        scales.append(st.scale)
+        trackers.append(st.growth_tracker)
+        skip1.append(r1["skipped"])
+        skip2.append(r2["skipped"])
+    return np.array(scales), np.array(trackers), np.array(skip1), np.array(skip2)
+
+
+def test_scaler_with_two_optimizers_matches_torch():
+    """Each optimizer skips on its own overflow and the scale moves once per iteration, on
+    the overflow of either: torch's GradScaler.step per optimizer and one update().  The
+    deferred first step plus an updating second step, and two deferred steps plus
+    scaler_update, both give torch's sequence; updating the scale in each step does not."""
+    d = golden("torch_scaler_two_opt.npz")
+    for call_update in (False, True):
+        s, t, k1, k2 = _two_optimizer_scaler_run(d, call_update=call_update)
+        assert np.array_equal(s, d["scale"]) and np.array_equal(t, d["tracker"])
+        assert np.array_equal(k1, d["skip1"]) and np.array_equal(k2, d["skip2"])
+    # both overflowing in one iteration backs off once (65536 -> 32768 at step 9, not 16384)
+    assert d["scale"][8] == d["scale"][7] / 2 and d["skip1"][8] and d["skip2"][8]
+    s, t, _, _ = _two_optimizer_scaler_run(d, defer_first=False)
+    assert not (np.array_equal(s, d["scale"]) and np.array_equal(t, d["tracker"]))
+
+
 @pytest.mark.parametrize("case", ["big", "small", "mid"])
 def test_clip_matches_torch(case):
     d = golden("torch_clip.npz")

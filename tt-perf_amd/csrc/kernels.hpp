@@ -88,7 +88,13 @@ struct DevState {
     float bias1, bias2;      // last pass: Adam bias corrections for the new t
     int32_t found_inf;       // last pass: a non-finite gradient was seen
     int32_t skip;            // last pass: the update must not run
+    // overflow seen by steps that deferred the scale update (several optimizers over one
+    // store: torch's GradScaler.step per optimizer, then one update); the next scale update
+    // combines it with its own and clears it (persistent)
+    int32_t pending_inf;
+    int32_t reserved;
 };
+static_assert(sizeof(DevState) == 64, "DevState is one 64-byte block");
 
 // ------------------------------------------------------------------------------------
 // bf16
@@ -276,6 +282,7 @@ struct FinalizeArgs {
     const uint32_t* idx;    // non-null: partial k is partials[idx[k]] (per-tensor sums)
     uint32_t npartials;     // 0: no norm pass ran (step counting only)
     int32_t scaler_on;      // unscale by 1/scale, skip on inf, update the scale
+    int32_t defer_scale;    // with scaler_on: note found_inf in pending_inf, keep the scale
     int32_t count_t;        // the step count lives on the device: advance it (unless skipped)
     int32_t probe;          // only compute sumsq/norm (ttp_grad_norm); touch nothing else
     int32_t growth_interval;
@@ -287,6 +294,27 @@ struct FinalizeArgs {
     int32_t want_bias;
     DevState* st;
 };
+
+// torch _amp_update_scale_ semantics, over this step's overflow and the pending overflow of
+// the steps that deferred their update since the last one (found_inf summed over optimizers,
+// as GradScaler.update does); clears the pending flag
+__device__ __forceinline__ void scaler_update(DevState* st, int32_t found, int32_t growth_interval,
+                                              double growth_factor, double backoff_factor) {
+    if (found || st->pending_inf) {
+        st->scale = (float)((double)st->scale * backoff_factor);
+        st->growth_tracker = 0;
+    } else {
+        const int32_t ok = st->growth_tracker + 1;
+        if (ok == growth_interval) {
+            const float ns = (float)((double)st->scale * growth_factor);
+            if (ns - ns == 0.0f) st->scale = ns;  // finite
+            st->growth_tracker = 0;
+        } else {
+            st->growth_tracker = ok;
+        }
+    }
+    st->pending_inf = 0;
+}
 
 __global__ __launch_bounds__(kBlock) void norm_finalize_kernel(FinalizeArgs a) {
     __shared__ double lds[kBlock / 64];
@@ -332,21 +360,18 @@ __global__ __launch_bounds__(kBlock) void norm_finalize_kernel(FinalizeArgs a) {
         }
     }
     if (a.scaler_on) {
-        // torch _amp_update_scale_ semantics
-        if (found) {
-            st->scale = (float)((double)st->scale * a.backoff_factor);
-            st->growth_tracker = 0;
-        } else {
-            const int32_t ok = st->growth_tracker + 1;
-            if (ok == a.growth_interval) {
-                const float ns = (float)((double)st->scale * a.growth_factor);
-                if (ns - ns == 0.0f) st->scale = ns;  // finite
-                st->growth_tracker = 0;
-            } else {
-                st->growth_tracker = ok;
-            }
-        }
+        if (a.defer_scale)
+            st->pending_inf |= found;
+        else
+            scaler_update(st, found, a.growth_interval, a.growth_factor, a.backoff_factor);
     }
+}
+
+// ttp_scaler_update: the scale update of an iteration whose steps all deferred it
+__global__ void scaler_update_kernel(DevState* st, int32_t growth_interval, double growth_factor,
+                                     double backoff_factor) {
+    if (threadIdx.x == 0 && blockIdx.x == 0)
+        scaler_update(st, 0, growth_interval, growth_factor, backoff_factor);
 }
 
 // Per-tensor sums of squares (ttp_grad_sumsq_tensors), from one norm_partials_kernel block per

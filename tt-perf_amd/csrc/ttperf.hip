@@ -303,6 +303,20 @@ int check_sums_current(ttp_ctx* c, const std::vector<uint32_t>& active) {
     return TTP_OK;
 }
 
+// After a step: the stepped tensors' sums are spent (their gradients were consumed).  A step
+// that updates the loss scale also makes every other sum stale, since those are of gradients
+// unscaled by the old scale; a step that defers the update leaves the other tensors' sums
+// current for the iteration's other optimizers.
+void consume_sums(ttp_ctx* c, const std::vector<uint32_t>& active, bool scale_moves) {
+    if (scale_moves) {
+        stale_sums(c);
+        return;
+    }
+    for (uint32_t i : active) set_fresh(c, i, false);
+}
+
+constexpr int32_t kStepFlags = TTP_STEP_TENSOR_SUMS | TTP_STEP_DEFER_SCALE;
+
 int zero_device(ttp_ctx* c, void* p, uint64_t bytes) {
     // a fill kernel rather than a memset node, so the step sequence stays capturable
     if (!bytes) return TTP_OK;
@@ -484,6 +498,14 @@ bool grads_cached(const ttp_ctx* c, const WorkTables* w) {
     return w->elems * grad_esize(c) <= kCachedGradBytes;
 }
 
+// Largest grid of the chunk-walking kernels: 2^22 blocks of 256 lanes is 2^30 work-items, well
+// inside the 2^32 a launch may hold.  Their grid-stride forms loop over the rest.
+constexpr uint32_t kMaxGridBlocks = 1u << 22;
+
+// Update grid over n chunks: the straight-line form (gradients that fit the Infinity Cache,
+// at most 2^17 chunks) takes one block per chunk; the grid-stride form at most kMaxGridBlocks.
+uint32_t update_grid(bool cached, uint32_t n) { return cached ? n : std::min(n, kMaxGridBlocks); }
+
 uint32_t norm_grid(const ttp_ctx* c, uint32_t nchunks) {
     return std::max<uint32_t>(1, std::min(nchunks, c->norm_grid_cap));
 }
@@ -492,7 +514,8 @@ uint32_t norm_grid(const ttp_ctx* c, uint32_t nchunks) {
 // finalize (norm, found_inf / skip, clip coefficient, loss scale, and the step count with its
 // bias corrections when `count_t`); `probe` only computes the norm.
 int launch_prologue(ttp_ctx* c, const WorkTables* w, bool run_norm, double max_norm, bool probe,
-                    bool want_bias, bool count_t, bool from_sums = false) {
+                    bool want_bias, bool count_t, bool from_sums = false,
+                    bool defer_scale = false) {
     const Chunk* chunks = w->tiles;
     const uint32_t n = w->n_tiles;
     const uint32_t grid = norm_grid(c, n);
@@ -519,6 +542,7 @@ int launch_prologue(ttp_ctx* c, const WorkTables* w, bool run_norm, double max_n
         a.npartials = w->n_tensors;
     }
     a.scaler_on = run_norm ? scaler_on : 0;
+    a.defer_scale = defer_scale ? 1 : 0;
     a.count_t = count_t ? 1 : 0;
     a.probe = probe ? 1 : 0;
     a.growth_interval = c->scaler.growth_interval;
@@ -794,7 +818,8 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
     if (n && !descs) return fail(TTP_ERR_INVALID, "null tensor table");
     if (mode != TTP_MODE_FP32 && mode != TTP_MODE_MIXED)
         return fail(TTP_ERR_INVALID, "mode must be TTP_MODE_FP32 or TTP_MODE_MIXED");
-    if (n > (1u << 24)) return fail(TTP_ERR_INVALID, "too many tensors (max 2^24)");
+    // per-tensor kernels launch one 256-lane block per tensor: fewer than 2^32 work-items
+    if (n >= (1u << 24)) return fail(TTP_ERR_INVALID, "too many tensors (max 2^24 - 1)");
     // the table must describe a store that fits one GPU: the padded footprint sum cannot
     // wrap, and every chunk index stays inside the buffers the kernels address
     uint64_t footprint = 0;
@@ -1116,7 +1141,7 @@ int ttp_zero_grad_subset(ttp_ctx* c, const uint32_t* indices, uint32_t n, int se
     std::vector<uint32_t> active;
     if ((rc = select_tables(c, indices ? indices : &none, n, &w, &active, false))) return rc;
     if (w->n_chunks) {
-        const uint32_t grid = w->n_chunks;
+        const uint32_t grid = std::min(w->n_chunks, kMaxGridBlocks);  // grid-stride kernel
         clear_hip_error();
         if (c->mode == TTP_MODE_MIXED)
             hipLaunchKernelGGL(ttp::zero_chunks_kernel<uint16_t>, dim3(grid), dim3(ttp::kUpdBlock),
@@ -1126,8 +1151,10 @@ int ttp_zero_grad_subset(ttp_ctx* c, const uint32_t* indices, uint32_t n, int se
                                0, c->stream, (float*)c->grad, w->chunks, w->n_chunks);
         HIP_TRY(hipGetLastError());
     }
+    // set_to_none = 0 leaves the has-grad flags as they are, as ttp_zero_grad(ctx, 0) and
+    // torch's zero_grad(set_to_none=False) do: a tensor without a grad stays without one
     for (uint32_t k = 0; k < n; ++k) {
-        set_grad_flag(c, indices[k], !set_to_none);
+        if (set_to_none) set_grad_flag(c, indices[k], false);
         set_fresh(c, indices[k], false);
     }
     return TTP_OK;
@@ -1142,6 +1169,17 @@ int ttp_accumulate_grad(ttp_ctx* c, uint32_t index, const void* src, uint64_t n,
         return fail(TTP_ERR_INVALID, "src_dtype must be TTP_DTYPE_F32 or TTP_DTYPE_BF16");
     if (kind != TTP_HOST && kind != TTP_DEVICE) return fail(TTP_ERR_INVALID, "bad memory kind");
     if (kind == TTP_HOST && (rc = no_capture(c, "accumulating a host gradient"))) return rc;
+    // Whether the kernel assigns (no grad yet) or adds is fixed when the call is captured.
+    // Every launch must therefore find the flag as the capture did: a call earlier in the same
+    // capture must have set it (zero_grad with set_to_none, set_has_grad, a gradient upload
+    // or an accumulate; zeroing to zeros leaves the flag as the launch finds it).
+    if (c->capturing && !(c->cap_touched[index] & kCapGrad))
+        return fail(TTP_ERR_STATE,
+                    "a captured accumulate into tensor " + std::to_string(index) +
+                        " must follow a call of the same capture that sets that tensor's "
+                        "has-grad flag (zero_grad with set_to_none, set_has_grad, a gradient "
+                        "upload or an accumulate): whether it assigns or adds is fixed when it "
+                        "is captured");
     TensorRec& t = c->tensors[index];
     if (n != t.numel)
         return fail(TTP_ERR_RANGE, "tensor " + std::to_string(index) + " has " +
@@ -1199,7 +1237,7 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
     if (!(hp->beta1 > 0 && hp->beta1 < 1 && hp->beta2 > 0 && hp->beta2 < 1))
         return fail(TTP_ERR_INVALID, "betas must be in (0, 1)");
     if (!(hp->weight_decay >= 0)) return fail(TTP_ERR_INVALID, "weight_decay must be >= 0");
-    if (hp->flags & ~TTP_STEP_TENSOR_SUMS) return fail(TTP_ERR_INVALID, "unknown step flags");
+    if (hp->flags & ~kStepFlags) return fail(TTP_ERR_INVALID, "unknown step flags");
     if (report && (rc = no_capture(c, "a step report (synchronises)"))) return rc;
     if ((rc = set_dev(c))) return rc;
     if ((rc = ensure_adam_state(c))) return rc;
@@ -1214,12 +1252,14 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
     const bool need_norm = scaler || clip;
     const bool devt = t_on_device(c);
     const bool from_sums = need_norm && (hp->flags & TTP_STEP_TENSOR_SUMS);
+    const bool defer = scaler && (hp->flags & TTP_STEP_DEFER_SCALE);
     if (from_sums && (rc = check_sums_current(c, active))) return rc;
     // the device table of bias corrections; built in host-count mode too (once per betas) so
     // that a later capture finds it, except when betas so close to 1 make it too long
     if ((rc = ensure_bias_table(c, hp->beta1, hp->beta2)) && devt) return rc;
     if ((need_norm || devt) &&
-        (rc = launch_prologue(c, w, need_norm, hp->max_grad_norm, false, devt, devt, from_sums)))
+        (rc = launch_prologue(c, w, need_norm, hp->max_grad_norm, false, devt, devt, from_sums,
+                              defer)))
         return rc;
 
     ttp::AdamArgs a{};
@@ -1247,9 +1287,8 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
         a.bias1 = a.bias2 = 1.0f;  // replaced by the device values
     }
     if (n) {
-        // one block per chunk (the straight-line kernel forms rely on it)
-        const dim3 grid(n), block(ttp::kUpdBlock);
         const bool cached = grads_cached(c, w);
+        const dim3 grid(update_grid(cached, n)), block(ttp::kUpdBlock);
         TimedLaunch tl(c, TTP_KERNEL_UPDATE);
         const uint16_t* g16 = (const uint16_t*)c->grad;
         const float* g32 = (const float*)c->grad;
@@ -1272,7 +1311,7 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
         HIP_TRY(hipGetLastError());
         tl.done();
     }
-    stale_sums(c);  // a step consumes the sums (the gradients are spent, the scale may move)
+    consume_sums(c, active, scaler && !defer);
     if (report) return fill_report(c, need_norm, report);
     return TTP_OK;
 }
@@ -1287,7 +1326,7 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
     if (!(hp->weight_decay >= 0)) return fail(TTP_ERR_INVALID, "weight_decay must be >= 0");
     if (hp->nesterov && (hp->momentum <= 0 || hp->dampening != 0))
         return fail(TTP_ERR_INVALID, "nesterov needs momentum > 0 and zero dampening");
-    if (hp->flags & ~TTP_STEP_TENSOR_SUMS) return fail(TTP_ERR_INVALID, "unknown step flags");
+    if (hp->flags & ~kStepFlags) return fail(TTP_ERR_INVALID, "unknown step flags");
     if (report && (rc = no_capture(c, "a step report (synchronises)"))) return rc;
     if ((rc = set_dev(c))) return rc;
     const bool mom = hp->momentum != 0.0;
@@ -1303,9 +1342,11 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
     const bool need_norm = scaler || clip;
     const bool devt = t_on_device(c);
     const bool from_sums = need_norm && (hp->flags & TTP_STEP_TENSOR_SUMS);
+    const bool defer = scaler && (hp->flags & TTP_STEP_DEFER_SCALE);
     if (from_sums && (rc = check_sums_current(c, active))) return rc;
     if ((need_norm || devt) &&
-        (rc = launch_prologue(c, w, need_norm, hp->max_grad_norm, false, false, devt, from_sums)))
+        (rc = launch_prologue(c, w, need_norm, hp->max_grad_norm, false, false, devt, from_sums,
+                              defer)))
         return rc;
     if (!devt) c->host_t += 1;
 
@@ -1323,9 +1364,8 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
     if (clip) a.flags |= ttp::kUseClip;
     a.st = (need_norm || devt) ? c->st : nullptr;
     if (n) {
-        // one block per chunk (the straight-line kernel forms rely on it)
-        const dim3 grid(n), block(ttp::kUpdBlock);
         const bool cached = grads_cached(c, w);
+        const dim3 grid(update_grid(cached, n)), block(ttp::kUpdBlock);
         TimedLaunch tl(c, TTP_KERNEL_UPDATE);
         const uint16_t* g16 = (const uint16_t*)c->grad;
         const float* g32 = (const float*)c->grad;
@@ -1365,7 +1405,7 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
                 for (uint32_t i : active) c->host_mom_init[i] = 1;
         }
     }
-    stale_sums(c);  // a step consumes the sums (the gradients are spent, the scale may move)
+    consume_sums(c, active, scaler && !defer);
     if (report) return fill_report(c, need_norm, report);
     return TTP_OK;
 }
@@ -1421,6 +1461,11 @@ int ttp_grad_sumsq_tensors(ttp_ctx* c, const uint32_t* indices, uint32_t n) {
     const WorkTables* w;
     std::vector<uint32_t> active;
     if ((rc = select_tables(c, indices ? indices : &none, n, &w, &active))) return rc;
+    // one 256-lane block per tile, and a launch holds fewer than 2^32 work-items
+    if (w->n_tiles >= (1u << 24))
+        return fail(TTP_ERR_RANGE, "a gradient-sum call covers " + std::to_string(w->n_tiles) +
+                                       " tiles of 16 KiB; at most 2^24 - 1 (256 GiB of "
+                                       "gradients) per call: split the bucket");
     if (w->n_tiles > c->tile_sums_cap) {
         if ((rc = no_capture(c, "a first gradient-sum call over this many tiles (allocates)")))
             return rc;
@@ -1513,6 +1558,7 @@ int ttp_scaler_configure(ttp_ctx* c, const ttp_scaler_config* cfg) {
         s.scale = (float)cfg->init_scale;
         s.growth_tracker = 0;
     }
+    s.pending_inf = 0;
     HIP_TRY(hipMemcpy(c->st, &s, sizeof(s), hipMemcpyHostToDevice));
     c->scaler = *cfg;
     stale_sums(c);  // the sums are of gradients unscaled by the old scale
@@ -1542,8 +1588,23 @@ int ttp_scaler_set(ttp_ctx* c, float scale, int32_t tracker) {
     HIP_TRY(hipMemcpy(&s, c->st, sizeof(s), hipMemcpyDeviceToHost));
     s.scale = scale;
     s.growth_tracker = tracker;
+    s.pending_inf = 0;
     HIP_TRY(hipMemcpy(c->st, &s, sizeof(s), hipMemcpyHostToDevice));
     stale_sums(c);
+    return TTP_OK;
+}
+
+int ttp_scaler_update(ttp_ctx* c) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (!c->scaler.enabled) return TTP_OK;  // nothing to update, as GradScaler when disabled
+    if ((rc = set_dev(c))) return rc;
+    clear_hip_error();
+    hipLaunchKernelGGL(ttp::scaler_update_kernel, dim3(1), dim3(64), 0, c->stream, c->st,
+                       (int32_t)c->scaler.growth_interval, c->scaler.growth_factor,
+                       c->scaler.backoff_factor);
+    HIP_TRY(hipGetLastError());
+    stale_sums(c);  // the scale may have moved
     return TTP_OK;
 }
 
@@ -1823,6 +1884,7 @@ int ttp_load_state(ttp_ctx* c, const char* path) {
     ds.t = h.t;
     ds.scale = h.scale;
     ds.growth_tracker = h.growth_tracker;
+    ds.pending_inf = 0;
     HIP_TRY(hipMemcpy(c->st, &ds, sizeof(ds), hipMemcpyHostToDevice));
     stale_sums(c);
     return TTP_OK;

@@ -19,6 +19,7 @@ TENSOR_DECAY = 1
 HOST, DEVICE = 0, 1
 DTYPE_F32, DTYPE_BF16 = 0, 1
 STEP_TENSOR_SUMS = 1
+STEP_DEFER_SCALE = 2
 KERNEL_NORM, KERNEL_UPDATE = 0, 1
 
 
@@ -90,6 +91,7 @@ SIGNATURES = {
     "ttp_scaler_configure": (C.c_int, [_P, C.POINTER(ScalerConfig)]),
     "ttp_scaler_get": (C.c_int, [_P, C.POINTER(C.c_float), C.POINTER(C.c_int32)]),
     "ttp_scaler_set": (C.c_int, [_P, C.c_float, C.c_int32]),
+    "ttp_scaler_update": (C.c_int, [_P]),
     "ttp_save_state": (C.c_int, [_P, C.c_char_p]),
     "ttp_load_state": (C.c_int, [_P, C.c_char_p]),
     "ttp_capture_begin": (C.c_int, [_P]),

@@ -76,17 +76,20 @@ class _Optimizer:
                 for p in members:
                     p.zero_grad()
 
-    def step(self, tensor_sums=False):
-        """py/optim.py's step().  tensor_sums=True (an extension): take the gradient norm from
+    def step(self, tensor_sums=False, update_scale=True):
+        """py/optim.py's step().  Extensions: tensor_sums=True takes the gradient norm from
         the sums ParamStore.grad_sumsq_tensors() took for these tensors, bucket by bucket
-        during the backward, instead of a norm pass."""
+        during the backward, instead of a norm pass.  update_scale=False, for all but the last
+        of several optimizers stepping one loss-scaled store in an iteration, leaves the loss
+        scale to that last step (or to ParamStore.scaler_update()), as torch's
+        GradScaler.step(opt) per optimizer followed by one GradScaler.update() does."""
         for store, members in self._stores():
             self._claim(store)
             whole = len(members) == len(store.tensors)
             self._step_store(store, None if whole else sorted({p.index for p in members}),
-                             tensor_sums)
+                             tensor_sums, update_scale)
 
-    def _step_store(self, store, indices, tensor_sums):  # pragma: no cover - abstract
+    def _step_store(self, store, indices, tensor_sums, update_scale):  # pragma: no cover
         raise NotImplementedError
 
 
@@ -111,10 +114,10 @@ class SGD(_Optimizer):
         self.nesterov = bool(nesterov)
         self.max_grad_norm = max_grad_norm
 
-    def _step_store(self, store, indices, tensor_sums):
+    def _step_store(self, store, indices, tensor_sums, update_scale):
         store.sgd_step(self.lr, self.momentum, self.dampening, self.weight_decay,
                        self.nesterov, self.max_grad_norm, indices=indices,
-                       tensor_sums=tensor_sums)
+                       tensor_sums=tensor_sums, update_scale=update_scale)
 
 
 class Adam(_Optimizer):
@@ -143,10 +146,10 @@ class Adam(_Optimizer):
         self.weight_decay = float(weight_decay)
         self.max_grad_norm = max_grad_norm
 
-    def _step_store(self, store, indices, tensor_sums):
+    def _step_store(self, store, indices, tensor_sums, update_scale):
         store.adam_step(self.lr, (self.beta1, self.beta2), self.eps, self.weight_decay,
                         self._decoupled, self.max_grad_norm, indices=indices,
-                        tensor_sums=tensor_sums)
+                        tensor_sums=tensor_sums, update_scale=update_scale)
 
 
 class AdamW(Adam):

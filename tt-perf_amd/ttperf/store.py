@@ -441,7 +441,9 @@ class ParamStore:
 
     def zero_grad(self, set_to_none=True, indices=None):
         """Zero every grad (one fill), or only the listed tensors' grads (one launch);
-        set_to_none also marks them as having no grad."""
+        set_to_none also marks them as having no grad.  set_to_none=False leaves the has-grad
+        flags alone, as torch's zero_grad(set_to_none=False) does: a tensor without a grad
+        stays without one (mark_grads() marks zeroed grads present)."""
         if indices is None:
             L.check(L.lib.ttp_zero_grad(self._h, 1 if set_to_none else 0))
             return
@@ -496,13 +498,21 @@ class ParamStore:
         idx = (C.c_uint32 * max(len(indices), 1))(*[int(i) for i in indices])
         return idx, len(indices)
 
+    @staticmethod
+    def _step_flags(tensor_sums, update_scale):
+        return ((L.STEP_TENSOR_SUMS if tensor_sums else 0)
+                | (0 if update_scale else L.STEP_DEFER_SCALE))
+
     def adam_step(self, lr, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0, decoupled=True,
-                  max_grad_norm=None, report=False, indices=None, tensor_sums=False):
+                  max_grad_norm=None, report=False, indices=None, tensor_sums=False,
+                  update_scale=True):
         """One Adam/AdamW step over every tensor with a grad, or only over `indices`.
-        tensor_sums: take the norm from grad_sumsq_tensors() instead of a norm pass."""
+        tensor_sums: take the norm from grad_sumsq_tensors() instead of a norm pass.
+        update_scale=False (loss scaling on): leave the loss scale to the iteration's last
+        step or to scaler_update(), as GradScaler.step does for one of several optimizers."""
         hp = L.AdamHParams(lr=lr, beta1=betas[0], beta2=betas[1], eps=eps,
                            weight_decay=weight_decay, decoupled=1 if decoupled else 0,
-                           flags=L.STEP_TENSOR_SUMS if tensor_sums else 0,
+                           flags=self._step_flags(tensor_sums, update_scale),
                            max_grad_norm=max_grad_norm or 0.0)
         rep = L.StepReport() if report else None
         rp = C.byref(rep) if report else None
@@ -514,12 +524,13 @@ class ParamStore:
         return rep.as_dict() if report else None
 
     def sgd_step(self, lr, momentum=0.0, dampening=0.0, weight_decay=0.0, nesterov=False,
-                 max_grad_norm=None, report=False, indices=None, tensor_sums=False):
+                 max_grad_norm=None, report=False, indices=None, tensor_sums=False,
+                 update_scale=True):
         """One SGD step over every tensor with a grad, or only over `indices`.
-        tensor_sums: take the norm from grad_sumsq_tensors() instead of a norm pass."""
+        tensor_sums and update_scale as in adam_step."""
         hp = L.SgdHParams(lr=lr, momentum=momentum, dampening=dampening,
                           weight_decay=weight_decay, nesterov=1 if nesterov else 0,
-                          flags=L.STEP_TENSOR_SUMS if tensor_sums else 0,
+                          flags=self._step_flags(tensor_sums, update_scale),
                           max_grad_norm=max_grad_norm or 0.0)
         rep = L.StepReport() if report else None
         rp = C.byref(rep) if report else None
@@ -569,6 +580,11 @@ class ParamStore:
 
     def set_scaler_state(self, scale, growth_tracker):
         L.check(L.lib.ttp_scaler_set(self._h, scale, growth_tracker))
+
+    def scaler_update(self):
+        """GradScaler.update() for an iteration whose steps all passed update_scale=False:
+        back off if any of them saw an overflow, else count a clean step toward growth."""
+        L.check(L.lib.ttp_scaler_update(self._h))
 
     # ---- optimizer-state checkpoint ---------------------------------------------------------
     def save_state(self, path):
