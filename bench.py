@@ -9,7 +9,10 @@ synthetic N(0, 1e-3) x scale bf16 gradients already resident in HBM.
 Prints ONE JSON line: Gparams/s and ms/step of the timed region (K steps between one event
 pair), the roofline of the dominant (update) kernel from HIP events recorded around each of
 its launches on the kernel's stream during a second pass of K steps, and the CPU oracle
-baseline timed on this host's cores on a bounded sample.
+baseline timed on this host's cores on a bounded sample.  Beside the headline: the step
+with a cold Infinity Cache (512 MB of unrelated reads before each step, outside its event
+pair), the mean skipped (overflow) step, and the other large configurations' steps
+(GPT-2 774M mixed AdamW, GPT-2 XL fp32 AdamW and SGD momentum), each in a store of its own.
 """
 import argparse
 import ctypes
@@ -75,6 +78,8 @@ def parse():
     ap.add_argument("--graph", action="store_true",
                     help="time replays of the step captured as a hipGraph (measured equal to "
                          "eager launches on MI355X, so eager is the default)")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the GPT-2 774M and XL steps timed after the headline")
     return ap.parse_args()
 
 
@@ -289,6 +294,106 @@ def ceilings(stream, update_bytes):
     return copy_gbps, nt_copy_gbps, nt_read_gbps, copy_bytes
 
 
+def make_store(config, seed=1234):
+    """A store of `config`'s table on cuda:0 with N(0, 0.02) master weights and the
+    configuration's synthetic gradients resident in HBM, on a created stream.  Returns
+    (store, stream, grads as a device tensor)."""
+    import torch
+    import ttperf
+    from ttperf import _lib as L
+    from ttperf import configs
+
+    names, shapes, decay, numels = configs.table(config)
+    mode = configs.mode(config)
+    dev = torch.device("cuda:0")
+    store = ttperf.ParamStore(shapes, mode=mode, decay=decay, names=names)
+    # a created stream (the legacy default stream cannot be captured); torch's events and
+    # synchronisation see it
+    stream = torch.cuda.Stream()
+    store.set_stream(stream)
+    cfg = BENCH[config]
+    scale = cfg["scaler"] or 1.0
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    w = torch.randn(store.total, generator=gen, device=dev) * 0.02
+    store.upload(L.BUF_MASTER, L.ALL_TENSORS, w)
+    del w
+    if cfg["scaler"]:
+        store.configure_scaler(True, init_scale=scale)
+    g = torch.randn(store.total, generator=gen, device=dev) * cfg["std"]
+    if cfg["heavy"]:
+        pick = torch.rand(store.total, generator=gen, device=dev) < cfg["heavy"]
+        g = torch.where(pick, torch.randn(store.total, generator=gen, device=dev), g)
+        del pick
+    g = g * scale
+    g = g.to(torch.bfloat16) if mode == "mixed" else g
+    store.upload(L.BUF_GRAD, L.ALL_TENSORS, g)
+    return store, stream, g
+
+
+def step_fn(store, optimizer, hp):
+    if optimizer == "adamw":
+        return lambda: store.adam_step(**hp)
+    return lambda: store.sgd_step(lr=hp["lr"], momentum=0.9, max_grad_norm=hp["max_grad_norm"])
+
+
+def other_config(config, optimizer, steps, warmup):
+    """One more configuration's step in a store of its own (created, timed, closed): K steps
+    between one event pair, then K more with an event pair around every launch for the update
+    kernel's own time.  Returns the JSON object."""
+    import torch
+    from ttperf import _lib as L
+    from ttperf import configs
+
+    _, _, _, numels = configs.table(config)
+    mode = configs.mode(config)
+    n_params = sum(numels)
+    cfg = BENCH[config]
+    hp = dict(cfg["hp"], decoupled=cfg["decoupled"])
+    store, stream, g = make_store(config)
+    del g
+    torch.cuda.empty_cache()
+    step = step_fn(store, optimizer, hp)
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    store.timing(True)
+    store.timing_collect(L.KERNEL_NORM)
+    store.timing_collect(L.KERNEL_UPDATE)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    upd_ms, upd_n = store.timing_collect(L.KERNEL_UPDATE)
+    nrm_ms, nrm_n = store.timing_collect(L.KERNEL_NORM)
+    store.close()
+    torch.cuda.empty_cache()
+    ub, nb = UPDATE_BYTES[(optimizer, mode)], NORM_BYTES[mode]
+    upd_avg = upd_ms / max(upd_n, 1)
+    step_gbps = n_params * (ub + nb) / (ms / 1e3) / 1e9
+    upd_gbps = n_params * ub / (upd_avg / 1e3) / 1e9
+    # the plain non-temporal copy of the update's bytes on this GPU, in the same run
+    _, nt_copy_gbps, _, _ = ceilings(stream, n_params * ub)
+    log(f"bench: {config} {optimizer}: {ms:.4f} ms/step, update {upd_avg:.4f} ms "
+        f"({upd_gbps / nt_copy_gbps:.3f} x the NT copy)")
+    return {"ms_per_step": round(ms, 4),
+            "Gparams_per_s": round(n_params / (ms / 1e3) / 1e9, 3),
+            "step_bytes_per_param": ub + nb,
+            "step_hbm_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
+            "update_ms": round(upd_avg, 4),
+            "update_frac": round(upd_gbps / HBM_PEAK_GBPS, 4),
+            "update_vs_nt_copy": round(upd_gbps / nt_copy_gbps, 4),
+            "nt_copy_GBps": round(nt_copy_gbps, 1),
+            "norm_pass_ms": round(nrm_ms / max(nrm_n, 1), 4),
+            "params": n_params, "tensors": len(numels), "mode": mode,
+            "steps": steps, "warmup": warmup}
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -307,30 +412,11 @@ def main():
     n_params = sum(numels)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    store = ttperf.ParamStore(shapes, mode=mode, decay=decay, names=names)
-    store_total = store.total
-    # a created stream (the legacy default stream cannot be captured); torch's events and
-    # synchronisation see it
-    stream = torch.cuda.Stream()
-    store.set_stream(stream)
-
     cfg = BENCH[args.config]
     hp = dict(cfg["hp"], decoupled=cfg["decoupled"])
     scale = cfg["scaler"] or 1.0
-    gen = torch.Generator(device=dev).manual_seed(1234)
-    w = torch.randn(store.total, generator=gen, device=dev) * 0.02
-    store.upload(L.BUF_MASTER, L.ALL_TENSORS, w)
-    del w
-    if cfg["scaler"]:
-        store.configure_scaler(True, init_scale=scale)
-    g = torch.randn(store.total, generator=gen, device=dev) * cfg["std"]
-    if cfg["heavy"]:
-        pick = torch.rand(store.total, generator=gen, device=dev) < cfg["heavy"]
-        g = torch.where(pick, torch.randn(store.total, generator=gen, device=dev), g)
-        del pick
-    g = g * scale
-    g = g.to(torch.bfloat16) if mode == "mixed" else g
-    store.upload(L.BUF_GRAD, L.ALL_TENSORS, g)
+    store, stream, g = make_store(args.config)
+    store_total = store.total
     grads_host = None
     if not args.no_cpu_baseline and args.optimizer == "adamw":
         grads_host = (g.cpu().view(torch.int16).numpy().view(np.uint16) if mode == "mixed"
@@ -338,11 +424,7 @@ def main():
     del g
     torch.cuda.empty_cache()
 
-    def step():
-        if args.optimizer == "adamw":
-            store.adam_step(**hp)
-        else:
-            store.sgd_step(lr=hp["lr"], momentum=0.9, max_grad_norm=hp["max_grad_norm"])
+    step = step_fn(store, args.optimizer, hp)
 
     for _ in range(args.warmup):
         step()
@@ -391,19 +473,41 @@ def main():
     if args.graph:
         graph.close()
 
-    # a skipped (overflow) step: only the norm pass does work
+    # the step with a cold Infinity Cache: before each step, a read of 512 MB of unrelated
+    # data (twice the 256 MB cache) on the same stream, outside the step's event pair
+    flush = torch.ones(128 << 20, dtype=torch.float32, device=dev)
+    sink = torch.zeros((), dtype=torch.float32, device=dev)
+    cold = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for a, b in cold:
+            torch.sum(flush, out=sink)
+            a.record(stream)
+            step()
+            b.record(stream)
+    torch.cuda.synchronize()
+    cold_ms = sum(a.elapsed_time(b) for a, b in cold) / args.steps
+    del flush, sink
+
+    # skipped (overflow) steps: only the norm pass and the finalize do work; K of them
+    # between one event pair (each backs the loss scale off; it is reset afterwards)
     skip_ms = None
     if args.optimizer == "adamw" and cfg["scaler"]:
         store.upload(L.BUF_GRAD, 0, torch.full((store.tensors[0].numel,), float("inf"),
                                                device=dev, dtype=torch.bfloat16 if mode == "mixed"
                                                else torch.float32))
+        rs = store.adam_step(report=True, **hp)
+        assert rs["skipped"], rs
+        n_skip = min(args.steps, 20)
         torch.cuda.synchronize()
         e0.record(stream)
-        rs = store.adam_step(report=False, **hp)
+        for _ in range(n_skip):
+            store.adam_step(**hp)
         e1.record(stream)
         torch.cuda.synchronize()
-        skip_ms = e0.elapsed_time(e1)
-        assert rs is None
+        skip_ms = e0.elapsed_time(e1) / n_skip
+        store.configure_scaler(True, init_scale=scale)
 
     # context: the step with its norm from bucketed per-tensor sums (first undoing the overflow
     # planted above), and the practical ceilings of the update's traffic on this GPU
@@ -457,7 +561,12 @@ def main():
         "step_hbm_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
         "kernels_ms": {"norm_pass": round(nrm_avg, 4), "update": round(upd_avg, 4),
                        "source": "second pass of K steps with an event pair per launch"},
+        "cold_ms_per_step": round(cold_ms, 4),
+        "cold_Gparams_per_s": round(n_params / (cold_ms / 1e3) / 1e9, 3),
+        "cold_note": "each step after a 512 MB read of unrelated data on its stream (outside "
+                     "its event pair), so no gradient is left in the 256 MB Infinity Cache",
         "skipped_step_ms": round(skip_ms, 4) if skip_ms is not None else None,
+        "skipped_step_note": "mean of 20 overflow steps between one event pair",
         "bucketed_norm": sums,
         "torch_copy_GBps": round(copy_gbps, 1),
         "ceilings": {"nt_copy_GBps": round(nt_copy_gbps, 1),
@@ -475,8 +584,23 @@ def main():
                      "kernel": upd_kernel,
                      "algorithmic_bytes_per_launch": n_params * ub},
         "cpu_baseline": None,
+        "other_configs": None,
     }
     store.close()
+    del store
+    torch.cuda.empty_cache()
+    if not args.no_other_configs and args.config == "gpt2_124m" and args.optimizer == "adamw":
+        # the other large configurations, one store at a time (GPT-2 XL fp32 holds 31 GB)
+        out["other_configs"] = {
+            "gpt2_774m_mixed_adamw": other_config("gpt2_774m", "adamw", args.steps,
+                                                  args.warmup),
+            "gpt2_1558m_fp32_adamw": other_config("gpt2_1558m", "adamw", args.steps,
+                                                  args.warmup),
+            "gpt2_1558m_fp32_sgdm": other_config("gpt2_1558m", "sgdm", args.steps,
+                                                 args.warmup),
+            "note": "each in a store of its own, created, timed (K steps between one event "
+                    "pair; the update alone from a second pass with an event pair per launch) "
+                    "and closed before the next; no CPU leg"}
     if grads_host is not None:
         log("bench: timing the CPU oracle baseline ...")
         out["cpu_baseline"] = cpu_baseline(numels, [1 if d else 0 for d in decay],
