@@ -482,7 +482,7 @@ def main():
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
         for a, b in cold:
-            torch.sum(flush, out=sink)
+            torch.sum(flush, dim=0, out=sink)
             a.record(stream)
             step()
             b.record(stream)
