@@ -270,6 +270,22 @@ int ttp_adam_step_subset(ttp_ctx* ctx, const ttp_adam_hparams* hp, const uint32_
                          uint32_t n_indices, ttp_step_report* report);
 int ttp_sgd_step_subset(ttp_ctx* ctx, const ttp_sgd_hparams* hp, const uint32_t* indices,
                         uint32_t n_indices, ttp_step_report* report);
+/* The Adam step of ttp_adam_step (indices NULL: every tensor) or ttp_adam_step_subset (the
+ * listed tensors), with the same arithmetic and results, allocating nothing: no device or
+ * pinned memory, no work or bias-correction table, no timing event.  No counterpart in the
+ * reference; it is for callers that cannot allocate: code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc.  Its norm pass writes its per-block
+ * partials into a fixed 64 KiB array of the library on each device (8192 fp64 partials,
+ * held until the process ends) instead of the context's own buffer; a step whose norm pass
+ * would need more blocks (TTP_NORM_GRID above 8192) fails with TTP_ERR_RANGE.  Every
+ * no-allocation step on one device shares that array: two that overlap in time on one
+ * device (contexts on different streams) race, so order them (one stream, or events).
+ * Whatever the step would have to allocate is refused with TTP_ERR_STATE before any work is
+ * queued: a tensor set, or (with loss scaling or after a capture) betas, not stepped before,
+ * and in FP32 mode the m and v of the first Adam step.  Step once with ttp_adam_step[_subset]
+ * first.  There is no report: ttp_scaler_get and ttp_get_step read the results. */
+int ttp_adam_step_noalloc(ttp_ctx* ctx, const ttp_adam_hparams* hp, const uint32_t* indices,
+                          uint32_t n_indices);
 /* Global L2 norm of the gradients that exist, unscaled by the current loss scale when
  * scaling is on (synchronous; does not change any state). */
 int ttp_grad_norm(ttp_ctx* ctx, double* norm);

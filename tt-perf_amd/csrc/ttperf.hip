@@ -23,6 +23,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <string>
 #include <utility>
 #include <vector>
@@ -103,6 +104,38 @@ struct WorkTables {
 // steps 1.8% faster that way.  Larger stores keep non-temporal loads and the grid-stride form,
 // which measured 0.5-1% faster at 774M and 1.56B.
 constexpr uint64_t kCachedGradBytes = 256ull << 20;
+
+}  // namespace
+
+// Norm-pass partials of ttp_adam_step_noalloc, the step entry point that allocates nothing: a
+// fixed array of the library, one copy on each device, held until the process ends.  Host code
+// never uses its name as an address: ttp_create looks up each device's copy once
+// (hipGetSymbolAddress, with that device current) and the kernels take that pointer.  Every
+// no-allocation step on a device shares the array, so such steps of different contexts must
+// not overlap on one device.
+constexpr uint32_t kNoAllocPartials = 8192;  // 64 KiB: one fp64 partial per norm-pass block
+static __device__ __align__(256) double scratch[kNoAllocPartials];
+
+namespace {
+
+std::mutex g_scratch_mu;
+std::map<int, double*> g_scratch;  // device -> its copy of `scratch`
+
+// Called with `device` current: finds this device's copy of the scratch array once.
+int ensure_scratch(int device) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch.count(device)) return TTP_OK;
+    double* ptr = nullptr;
+    HIP_TRY(hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch)));
+    g_scratch[device] = ptr;
+    return TTP_OK;
+}
+
+double* scratch_ptr(int device) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    auto it = g_scratch.find(device);
+    return it == g_scratch.end() ? nullptr : it->second;
+}
 
 }  // namespace
 
@@ -359,7 +392,8 @@ int ensure_momentum(ttp_ctx* c) {
 // Active set of a step: the listed tensors (all when `subset` is NULL) that have a grad
 // and at least one element; returns its device work tables (built once per distinct set).
 int select_tables(ttp_ctx* c, const uint32_t* subset, uint32_t nsub, const WorkTables** out,
-                  std::vector<uint32_t>* active_out, bool require_grad = true) {
+                  std::vector<uint32_t>* active_out, bool require_grad = true,
+                  bool may_build = true) {
     const uint32_t nt = (uint32_t)c->tensors.size();
     std::vector<uint32_t> active;
     if (subset) {
@@ -384,6 +418,10 @@ int select_tables(ttp_ctx* c, const uint32_t* subset, uint32_t nsub, const WorkT
         auto it = c->tables.find(active);
         if (it == c->tables.end()) {
             int rc;
+            if (!may_build)
+                return fail(TTP_ERR_STATE, "this tensor set has no work table yet and the "
+                                           "no-allocation step builds none: step the same "
+                                           "set once with ttp_adam_step[_subset] first");
             if ((rc = no_capture(c, "a step over a tensor set not stepped before (builds tables)")))
                 return rc;
             if (c->tables.size() >= 64 && !c->n_graphs) {
@@ -413,11 +451,15 @@ int select_tables(ttp_ctx* c, const uint32_t* subset, uint32_t nsub, const WorkT
 // the cache is emptied, after the queued work, unless graphs may read the tables.
 constexpr size_t kMaxBiasTables = 16;
 
-int ensure_bias_table(ttp_ctx* c, double b1, double b2) {
+int ensure_bias_table(ttp_ctx* c, double b1, double b2, bool may_build = true) {
     const auto key = std::make_pair(b1, b2);
     auto it = c->bias_tables.find(key);
     if (it == c->bias_tables.end()) {
         int rc;
+        if (!may_build)
+            return fail(TTP_ERR_STATE, "no bias-correction table for these betas yet and the "
+                                       "no-allocation step builds none: step once with "
+                                       "ttp_adam_step[_subset] and the same betas first");
         if ((rc = no_capture(c, "a step with new betas (builds a table)"))) return rc;
         std::vector<float> tab;
         const uint64_t kMax = 1ull << 24;
@@ -468,8 +510,9 @@ struct TimedLaunch {
     ttp_ctx* c;
     int kernel;
     hipEvent_t a = nullptr;
-    TimedLaunch(ttp_ctx* ctx, int k) : c(ctx), kernel(k) {
-        if (c->timing && !c->capturing && (a = take_event(c))) (void)hipEventRecord(a, c->stream);
+    TimedLaunch(ttp_ctx* ctx, int k, bool enabled = true) : c(ctx), kernel(k) {
+        if (enabled && c->timing && !c->capturing && (a = take_event(c)))
+            (void)hipEventRecord(a, c->stream);
     }
     void done() {
         if (!a) return;
@@ -513,28 +556,31 @@ uint32_t norm_grid(const ttp_ctx* c, uint32_t nchunks) {
 // Step prologue on the device: the norm pass (partials, when `run_norm`) and the one-block
 // finalize (norm, found_inf / skip, clip coefficient, loss scale, and the step count with its
 // bias corrections when `count_t`); `probe` only computes the norm.
+// `partials` (null: the context's own) holds one partial per norm-pass block; a caller-given
+// array (the no-allocation step's) also turns the per-launch timing events off.
 int launch_prologue(ttp_ctx* c, const WorkTables* w, bool run_norm, double max_norm, bool probe,
                     bool want_bias, bool count_t, bool from_sums = false,
-                    bool defer_scale = false) {
+                    bool defer_scale = false, double* partials = nullptr) {
     const Chunk* chunks = w->tiles;
     const uint32_t n = w->n_tiles;
     const uint32_t grid = norm_grid(c, n);
     const int32_t scaler_on = c->scaler.enabled ? 1 : 0;
-    TimedLaunch tl(c, TTP_KERNEL_NORM);
+    TimedLaunch tl(c, TTP_KERNEL_NORM, partials == nullptr);
+    if (!partials) partials = c->partials;
     if (run_norm && !from_sums) {
         clear_hip_error();
         if (c->mode == TTP_MODE_MIXED)
             hipLaunchKernelGGL(ttp::norm_partials_kernel<uint16_t>, dim3(grid), dim3(ttp::kBlock),
                                0, c->stream, (const uint16_t*)c->grad, chunks, n,
-                               (const DevState*)c->st, scaler_on, c->partials);
+                               (const DevState*)c->st, scaler_on, partials);
         else
             hipLaunchKernelGGL(ttp::norm_partials_kernel<float>, dim3(grid), dim3(ttp::kBlock), 0,
                                c->stream, (const float*)c->grad, chunks, n,
-                               (const DevState*)c->st, scaler_on, c->partials);
+                               (const DevState*)c->st, scaler_on, partials);
         HIP_TRY(hipGetLastError());
     }
     ttp::FinalizeArgs a{};
-    a.partials = c->partials;
+    a.partials = partials;
     a.npartials = run_norm ? grid : 0;
     if (run_norm && from_sums) {  // the step's tensors' sums, in tensor order
         a.partials = c->tsum;
@@ -850,6 +896,8 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
         return rc;
     };
     if (hipSetDevice(device) != hipSuccess) return bail(fail(TTP_ERR_HIP, "hipSetDevice failed"));
+    int rc0 = ensure_scratch(device);  // this device's copy of the no-allocation scratch array
+    if (rc0) return bail(rc0);
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
         c->num_cus = prop.multiProcessorCount;
@@ -1226,8 +1274,13 @@ int ttp_accumulate_grad(ttp_ctx* c, uint32_t index, const void* src, uint64_t n,
     return TTP_OK;
 }
 
+// `scratch_partials` non-null: the no-allocation step.  It builds no work or bias table and
+// allocates no state (each missing one is refused with TTP_ERR_STATE), records no timing
+// events, and its norm pass writes its partials there (at most kNoAllocPartials).
 static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t* subset,
-                          uint32_t nsub, ttp_step_report* report) {
+                          uint32_t nsub, ttp_step_report* report,
+                          double* scratch_partials = nullptr) {
+    const bool noalloc = scratch_partials != nullptr;
     int rc = check_ctx(c);
     if (rc) return rc;
     if (!hp) return fail(TTP_ERR_INVALID, "null hyperparameters");
@@ -1240,10 +1293,14 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
     if (hp->flags & ~kStepFlags) return fail(TTP_ERR_INVALID, "unknown step flags");
     if (report && (rc = no_capture(c, "a step report (synchronises)"))) return rc;
     if ((rc = set_dev(c))) return rc;
+    if (noalloc && !c->exp_avg)
+        return fail(TTP_ERR_STATE, "the first Adam step of an FP32 store allocates m and v, "
+                                   "which the no-allocation step does not: step once with "
+                                   "ttp_adam_step[_subset] first");
     if ((rc = ensure_adam_state(c))) return rc;
     const WorkTables* w;
     std::vector<uint32_t> active;
-    if ((rc = select_tables(c, subset, nsub, &w, &active))) return rc;
+    if ((rc = select_tables(c, subset, nsub, &w, &active, true, !noalloc))) return rc;
     const Chunk* chunks = w->chunks;
     const uint32_t n = w->n_chunks;
 
@@ -1254,12 +1311,20 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
     const bool from_sums = need_norm && (hp->flags & TTP_STEP_TENSOR_SUMS);
     const bool defer = scaler && (hp->flags & TTP_STEP_DEFER_SCALE);
     if (from_sums && (rc = check_sums_current(c, active))) return rc;
+    if (noalloc && need_norm && !from_sums && norm_grid(c, w->n_tiles) > kNoAllocPartials)
+        return fail(TTP_ERR_RANGE,
+                    "the norm pass would write " + std::to_string(norm_grid(c, w->n_tiles)) +
+                        " partials; the no-allocation step holds at most " +
+                        std::to_string(kNoAllocPartials) + " (lower TTP_NORM_GRID)");
     // the device table of bias corrections; built in host-count mode too (once per betas) so
-    // that a later capture finds it, except when betas so close to 1 make it too long
-    if ((rc = ensure_bias_table(c, hp->beta1, hp->beta2)) && devt) return rc;
+    // that a later capture finds it, except when betas so close to 1 make it too long.  The
+    // no-allocation step needs it only when the step count lives on the device.
+    if ((!noalloc || devt) &&
+        (rc = ensure_bias_table(c, hp->beta1, hp->beta2, !noalloc)) && (devt || noalloc))
+        return rc;
     if ((need_norm || devt) &&
         (rc = launch_prologue(c, w, need_norm, hp->max_grad_norm, false, devt, devt, from_sums,
-                              defer)))
+                              defer, scratch_partials)))
         return rc;
 
     ttp::AdamArgs a{};
@@ -1289,7 +1354,7 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
     if (n) {
         const bool cached = grads_cached(c, w);
         const dim3 grid(update_grid(cached, n)), block(ttp::kUpdBlock);
-        TimedLaunch tl(c, TTP_KERNEL_UPDATE);
+        TimedLaunch tl(c, TTP_KERNEL_UPDATE, !noalloc);
         const uint16_t* g16 = (const uint16_t*)c->grad;
         const float* g32 = (const float*)c->grad;
         uint16_t* p16 = (uint16_t*)c->param;
@@ -1424,6 +1489,16 @@ int ttp_adam_step_subset(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t*
     if (n && !indices) return fail(TTP_ERR_INVALID, "null index list");
     static const uint32_t none = 0;
     return adam_step_impl(c, hp, indices ? indices : &none, n, report);
+}
+
+int ttp_adam_step_noalloc(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t* indices,
+                          uint32_t n) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (n && !indices) return fail(TTP_ERR_INVALID, "null index list");
+    double* sp = scratch_ptr(c->device);
+    if (!sp) return fail(TTP_ERR_STATE, "no scratch array found for this device");
+    return adam_step_impl(c, hp, indices, n, nullptr, sp);
 }
 
 int ttp_sgd_step(ttp_ctx* c, const ttp_sgd_hparams* hp, ttp_step_report* report) {

@@ -84,6 +84,8 @@ SIGNATURES = {
                                        C.c_uint32, C.POINTER(StepReport)]),
     "ttp_sgd_step_subset": (C.c_int, [_P, C.POINTER(SgdHParams), C.POINTER(C.c_uint32),
                                       C.c_uint32, C.POINTER(StepReport)]),
+    "ttp_adam_step_noalloc": (C.c_int, [_P, C.POINTER(AdamHParams), C.POINTER(C.c_uint32),
+                                        C.c_uint32]),
     "ttp_grad_norm": (C.c_int, [_P, C.POINTER(C.c_double)]),
     "ttp_grad_sumsq_tensors": (C.c_int, [_P, C.POINTER(C.c_uint32), C.c_uint32]),
     "ttp_get_step": (C.c_int, [_P, C.POINTER(C.c_uint64)]),
