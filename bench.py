@@ -244,9 +244,10 @@ def bucketed_norm(store, stream, args, hp, mode, numels):
 def ceilings(stream, update_bytes):
     """The practical ceilings of the update's traffic on this GPU, over its byte count
     `update_bytes`: torch's device copy (a blit kernel), and libttperf_ceiling's non-temporal
-    16-byte copy (the update's 50/50 read/write mix) and read-only pass, each timed over 10
+    16-byte copies (the update's 50/50 read/write mix; 256-lane blocks of 4 KiB and 64-lane
+    blocks of 1 KiB, the fastest copy measured) and read-only pass, each timed over 10
     launches between one event pair on `stream`.  Returns (torch copy GB/s, NT copy GB/s,
-    NT read GB/s, bytes each way)."""
+    NT read GB/s, bytes each way, 64-lane NT copy GB/s)."""
     import torch
 
     dev = torch.device("cuda:0")
@@ -260,6 +261,8 @@ def ceilings(stream, update_bytes):
                                   ctypes.c_int, ctypes.c_void_p]
     ceil.ttpc_read_nt.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int,
                                   ctypes.c_void_p, ctypes.c_void_p]
+    ceil.ttpc_copy_nt64.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64,
+                                    ctypes.c_void_p]
     # the fastest forms measured (see tt-perf_amd/csrc/ceiling.hip): a straight-line copy,
     # one block per 4 KB tile, and a read over 8 blocks per CU
     read_grid = torch.cuda.get_device_properties(dev).multi_processor_count * 8
@@ -281,6 +284,10 @@ def ceilings(stream, update_bytes):
         rc = ceil.ttpc_copy_nt(src.data_ptr(), dst.data_ptr(), n16, 0, stream.cuda_stream)
         assert rc == 0, f"ttpc_copy_nt: hipError {rc}"
 
+    def nt_copy64():
+        rc = ceil.ttpc_copy_nt64(src.data_ptr(), dst.data_ptr(), n16, stream.cuda_stream)
+        assert rc == 0, f"ttpc_copy_nt64: hipError {rc}"
+
     def nt_read():
         rc = ceil.ttpc_read_nt(src.data_ptr(), n16, read_grid, stream.cuda_stream,
                                sink.data_ptr())
@@ -289,9 +296,10 @@ def ceilings(stream, update_bytes):
     with torch.cuda.stream(stream):
         copy_gbps = 2 * copy_bytes / (timed(lambda: dst.copy_(src)) / 1e3) / 1e9
     nt_copy_gbps = 2 * copy_bytes / (timed(nt_copy) / 1e3) / 1e9
+    nt_copy64_gbps = 2 * copy_bytes / (timed(nt_copy64) / 1e3) / 1e9
     nt_read_gbps = copy_bytes / (timed(nt_read) / 1e3) / 1e9
     del src, dst, sink
-    return copy_gbps, nt_copy_gbps, nt_read_gbps, copy_bytes
+    return copy_gbps, nt_copy_gbps, nt_read_gbps, copy_bytes, nt_copy64_gbps
 
 
 def make_store(config, seed=1234):
@@ -377,8 +385,8 @@ def other_config(config, optimizer, steps, warmup):
     upd_avg = upd_ms / max(upd_n, 1)
     step_gbps = n_params * (ub + nb) / (ms / 1e3) / 1e9
     upd_gbps = n_params * ub / (upd_avg / 1e3) / 1e9
-    # the plain non-temporal copy of the update's bytes on this GPU, in the same run
-    _, nt_copy_gbps, _, _ = ceilings(stream, n_params * ub)
+    # the plain non-temporal copies of the update's bytes on this GPU, in the same run
+    _, nt_copy_gbps, _, _, nt_copy64_gbps = ceilings(stream, n_params * ub)
     log(f"bench: {config} {optimizer}: {ms:.4f} ms/step, update {upd_avg:.4f} ms "
         f"({upd_gbps / nt_copy_gbps:.3f} x the NT copy)")
     return {"ms_per_step": round(ms, 4),
@@ -389,6 +397,8 @@ def other_config(config, optimizer, steps, warmup):
             "update_frac": round(upd_gbps / HBM_PEAK_GBPS, 4),
             "update_vs_nt_copy": round(upd_gbps / nt_copy_gbps, 4),
             "nt_copy_GBps": round(nt_copy_gbps, 1),
+            "update_vs_nt_copy64": round(upd_gbps / nt_copy64_gbps, 4),
+            "nt_copy64_GBps": round(nt_copy64_gbps, 1),
             "norm_pass_ms": round(nrm_ms / max(nrm_n, 1), 4),
             "params": n_params, "tensors": len(numels), "mode": mode,
             "steps": steps, "warmup": warmup}
@@ -519,7 +529,8 @@ def main():
         sums = bucketed_norm(store, stream, args, hp, mode, numels)
     ub = UPDATE_BYTES[(args.optimizer, mode)]
     nb = NORM_BYTES[mode]
-    copy_gbps, nt_copy_gbps, nt_read_gbps, copy_bytes = ceilings(stream, n_params * ub)
+    copy_gbps, nt_copy_gbps, nt_read_gbps, copy_bytes, nt_copy64_gbps = \
+        ceilings(stream, n_params * ub)
 
     achieved = n_params * ub / (upd_avg / 1e3) / 1e9
     # the instantiation libttperf_hip launches (its rocprof name)
@@ -574,10 +585,12 @@ def main():
                      "nt_read_GBps": round(nt_read_gbps, 1),
                      "bytes_each_way": copy_bytes,
                      "update_vs_nt_copy": round(achieved / nt_copy_gbps, 4),
-                     "source": "libttperf_ceiling: 16-byte non-temporal straight-line copy "
-                               "(reads + writes counted) and read-only pass over the update's "
-                               "byte count, the fastest plain forms measured; 10 launches "
-                               "between one event pair"},
+                     "nt_copy64_GBps": round(nt_copy64_gbps, 1),
+                     "update_vs_nt_copy64": round(achieved / nt_copy64_gbps, 4),
+                     "source": "libttperf_ceiling: 16-byte non-temporal straight-line copies "
+                               "(reads + writes counted; 256-lane blocks, and 64-lane blocks, "
+                               "the fastest copy measured) and read-only pass over the "
+                               "update's byte count; 10 launches between one event pair"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": traffic_from_profiles(args.config),

@@ -40,7 +40,8 @@ def test_ceiling_probe_library_exports_its_entry_points():
     path = os.path.join(REPO, "tt-perf_amd", "lib", "libttperf_ceiling.so")
     out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True,
                          check=True).stdout
-    assert {"ttpc_copy_nt", "ttpc_read_nt"} <= set(re.findall(r"\b(ttpc_\w+)", out))
+    names = set(re.findall(r"\b(ttpc_\w+)", out))
+    assert {"ttpc_copy_nt", "ttpc_copy_nt64", "ttpc_read_nt"} <= names
 
 
 def test_abi_version():
