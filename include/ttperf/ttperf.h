@@ -312,7 +312,8 @@ int ttp_scaler_set(ttp_ctx* ctx, float scale, int32_t growth_tracker);
 /* The scale update of an iteration whose steps all passed TTP_STEP_DEFER_SCALE
  * (torch.amp.GradScaler.update after several GradScaler.step calls): back off if any of them
  * saw an overflow, else count one clean step toward growth.  Stream-ordered, capturable; a
- * no-op while loss scaling is off.  ttp_scaler_configure, ttp_scaler_set and ttp_load_state
+ * no-op while loss scaling is off, and when no step deferred the update since the last one
+ * (torch raises there), so an iteration's scale never moves twice.  ttp_scaler_configure, ttp_scaler_set and ttp_load_state
  * drop a pending overflow; ttp_save_state does not record one (save between iterations). */
 int ttp_scaler_update(ttp_ctx* ctx);
 

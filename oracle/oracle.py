@@ -39,7 +39,7 @@ class Store(C.Structure):
                 ("growth_interval", C.c_int32), ("growth_factor", C.c_double),
                 ("backoff_factor", C.c_double), ("scale", C.c_float),
                 ("growth_tracker", C.c_int32), ("t", C.c_uint64), ("nthreads", C.c_int32),
-                ("pending_inf", C.c_int32)]
+                ("pending", C.c_int32)]
 
 
 class AdamHP(C.Structure):
@@ -228,7 +228,7 @@ class OracleStore:
         self.s.backoff_factor = backoff_factor
         self.s.growth_interval = growth_interval
         self.s.growth_tracker = 0
-        self.s.pending_inf = 0
+        self.s.pending = 0
 
     @property
     def t(self):
@@ -249,10 +249,11 @@ class OracleStore:
     def set_scaler_state(self, scale, tracker):
         self.s.scale = scale
         self.s.growth_tracker = tracker
-        self.s.pending_inf = 0
+        self.s.pending = 0
 
     def scaler_update(self):
-        """The scale update after steps that all deferred it (update_scale=False)."""
+        """The scale update after steps that all deferred it (update_scale=False); nothing
+        if no step deferred it since the last update."""
         lib().orc_scaler_update_pending(C.byref(self.s))
 
     # ---- steps -----------------------------------------------------------------------------

@@ -284,15 +284,15 @@ static void step_prologue(orc_store* s, double max_norm, float* inv_scale, float
  * then moves the scale once, on the overflow found by any optimizer since the last update
  * (found_inf summed over optimizers, torch/amp/grad_scaler.py update) */
 void orc_scaler_update_pending(orc_store* s) {
-    if (!s->scaler_enabled) return;
-    orc_scaler_update(&s->scale, &s->growth_tracker, s->pending_inf, s->growth_factor,
-                      s->backoff_factor, s->growth_interval);
-    s->pending_inf = 0;
+    if (!s->scaler_enabled || !(s->pending & ORC_PENDING_STEP)) return;
+    orc_scaler_update(&s->scale, &s->growth_tracker, s->pending & ORC_PENDING_INF,
+                      s->growth_factor, s->backoff_factor, s->growth_interval);
+    s->pending = 0;
 }
 
 static void step_epilogue(orc_store* s, int found_inf, int defer, orc_report* rep) {
     if (s->scaler_enabled) {
-        s->pending_inf |= found_inf ? 1 : 0;
+        s->pending |= ORC_PENDING_STEP | (found_inf ? ORC_PENDING_INF : 0);
         if (!defer) orc_scaler_update_pending(s);
     }
     if (rep) {

@@ -66,13 +66,16 @@ typedef struct orc_store {
     int32_t growth_tracker;
     uint64_t t;            /* applied steps */
     int32_t nthreads;
-    int32_t pending_inf;   /* overflow seen by steps that deferred the scale update */
+    int32_t pending;       /* steps that deferred the scale update since the last one:
+                              ORC_PENDING_STEP once one ran, | ORC_PENDING_INF on overflow */
 } orc_store;
 
 /* step flag: with loss scaling on, skip this step's own update on overflow but leave the
  * scale update to the iteration's last step or orc_scaler_update_pending (torch's
  * GradScaler.step for one of several optimizers, then one GradScaler.update) */
 #define ORC_STEP_DEFER_SCALE 2
+#define ORC_PENDING_INF 1
+#define ORC_PENDING_STEP 2
 
 typedef struct orc_adam_hp {
     double lr, beta1, beta2, eps, weight_decay;
@@ -111,7 +114,8 @@ float orc_bias_correction(double beta, uint64_t t);
 float orc_clip_coef(double norm, double max_norm);
 void orc_scaler_update(float* scale, int32_t* tracker, int found_inf, double growth_factor,
                        double backoff_factor, int32_t growth_interval);
-/* GradScaler.update after deferred steps: the scale update over their pending overflow */
+/* GradScaler.update after deferred steps: the scale update over their pending overflow;
+ * nothing if no step deferred it since the last update */
 void orc_scaler_update_pending(orc_store* s);
 
 /* layout: offsets of n tensors, each aligned up to `align` elements; returns total */

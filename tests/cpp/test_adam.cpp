@@ -133,6 +133,65 @@ static void run_groups() {
     }
 }
 
+// Two AdamW optimizers over two groups of one loss-scaled arena, torch's GradScaler way: the
+// first defers the scale update (opts.update_scale = false), the second updates it once per
+// iteration from both overflows.  Each optimizer skips its own update on its own overflow.
+// Scale 1024, growth 2 every 2 clean iterations, backoff 0.5; +inf in group a at iteration 2,
+// in group b at 4, in both at 5: the scale goes 1024, 2048, 1024, 1024, 512, 256 (one backoff
+// at 5), against 2048 at iteration 1 then a backoff per overflowing optimizer if each step
+// updated it.
+static void run_scaled_groups() {
+    ParamArena arena(ttp::Mode::FP32);
+    MLP model(64, 128, 10, arena);
+    auto params = model.parameters();
+    std::vector<Ref> ref;
+    for (auto& p : params) {
+        Ref r;
+        r.p = p->master();
+        r.m.assign(p->numel(), 0.0f);
+        r.v.assign(p->numel(), 0.0f);
+        ref.push_back(r);
+    }
+    ttp::Store& store = params[0]->store();
+    store.configure_scaler(1024.0, 2.0, 0.5, 2, true);
+    AdamW a({params[0], params[1]}, 1e-2f, {0.9, 0.95}, 1e-8f, 0.1f);
+    AdamW b({params[2], params[3]}, 1e-2f, {0.9, 0.95}, 1e-8f, 0.1f);
+    a.opts.update_scale = false;
+    const float want_scale[6] = {1024.0f, 2048.0f, 1024.0f, 1024.0f, 512.0f, 256.0f};
+    const bool inf_a[6] = {false, false, true, false, false, true};
+    const bool inf_b[6] = {false, false, false, false, true, true};
+    uint64_t ta = 0, tb = 0;
+    float scale = 1024.0f;
+    for (int k = 0; k < 6; ++k) {
+        for (size_t j = 0; j < params.size(); ++j) {
+            auto g = grad_of(params[j]->numel(), 300 + k * 10 + (int)j);
+            std::vector<float> scaled(g.size());
+            for (size_t i = 0; i < g.size(); ++i) scaled[i] = g[i] * scale;  // exact: 2^n
+            const bool group_a = j < 2;
+            if ((group_a ? inf_a[k] : inf_b[k]) && j % 2 == 0) scaled[3] = INFINITY;
+            params[j]->grad = scaled;
+            const bool skipped = group_a ? inf_a[k] : inf_b[k];
+            if (!skipped) {
+                const uint64_t t = (group_a ? ta : tb) + 1;
+                adam_ref(ref[j], g, (double)1e-2f, 0.9, 0.95, (double)1e-8f, t, (double)0.1f,
+                         j % 2 == 0);
+            }
+        }
+        if (!inf_a[k]) ++ta;
+        if (!inf_b[k]) ++tb;
+        a.step();
+        b.step();
+        const auto st = store.scaler_state();
+        scale = st.first;
+        test::check(scale == want_scale[k],
+                    "scaled groups: iteration " + std::to_string(k) + " scale " +
+                        std::to_string(scale) + ", want " + std::to_string(want_scale[k]));
+        test::check(store.step_count() == tb, "scaled groups: the arena holds b's count");
+    }
+    for (size_t k = 0; k < params.size(); ++k)
+        test::assert_bits(params[k]->master(), ref[k].p, "scaled groups param " + std::to_string(k));
+}
+
 // A graph holding optimizer a's step, launched between optimizer b's eager steps: each launch
 // hands the store's step count back to a (ttp::Graph::launch), so both keep their own.
 static void run_graph_groups() {
@@ -259,6 +318,7 @@ int main() {
     run(false);
     run(true);
     run_groups();
+    run_scaled_groups();
     run_graph_groups();
     run_tensor_sums();
     run_counts_outlive_store();

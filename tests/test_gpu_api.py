@@ -551,6 +551,10 @@ def test_two_optimizers_share_one_scale_update_per_iteration(how):
         scales.append(scale)
         print(f"iteration {it}: overflow in {inf_in.get(it, '-')!r}, scale {scale}, "
               f"tracker {tracker}, counts {counts}", flush=True)
+    # an update after the iteration's updating step changes nothing
+    store.scaler_update()
+    ref.scaler_update()
+    assert store.scaler_state() == (ref.scale, ref.growth_tracker) == (scales[-1], tracker)
     # one move per iteration: a backoff at iterations 3, 5, 8 (both groups: once) and 12,
     # growth after the three clean iterations 9-11
     assert scales == [4096.0, 4096.0, 2048.0, 2048.0, 1024.0, 1024.0, 1024.0, 512.0, 512.0,

@@ -13,7 +13,9 @@ host interface, mirrored on the oracle:
   loss scaler switched on or off; the step count set; the gradient norm probed; a checkpoint
   saved and later loaded; an Adam step captured into a graph (half of them together with
   the bucket sums it takes its norm from), and a zero_grad captured into one, replayed
-  later, between other operations.
+  later, between other operations; with loss scaling on, steps that defer the scale update
+  to a later step or to ttp_scaler_update; Adam steps through the no-allocation entry point
+  (ttp_adam_step_noalloc), and its refusals when a tensor set or betas were never stepped.
 
 After every operation the whole state is compared: master, m, v and momentum within the
 2-ulp bar of the other parity tests (in practice 0), bf16 weights and the gradients bit for
@@ -167,16 +169,18 @@ class Case:
         cand = range(self.n) if indices is None else indices
         return [i for i in cand if self.ref.has_grad(i) and self.numels[i]]
 
-    def _ref_step(self, kind, hp, active):
+    def _ref_step(self, kind, hp, active, update_scale=True):
         """The oracle steps exactly `active` (has-grad flags narrowed, then restored)."""
         flags = [self.ref.has_grad(i) for i in range(self.n)]
         for i in range(self.n):
             self.ref.set_has_grad(i, i in active)
         if kind == "adam":
             e = self.ref.adam_step(max_grad_norm=hp["max_grad_norm"] or 0.0,
+                                   update_scale=update_scale,
                                    **{k: v for k, v in hp.items() if k != "max_grad_norm"})
         else:
             e = self.ref.sgd_step(max_grad_norm=hp["max_grad_norm"] or 0.0,
+                                  update_scale=update_scale,
                                   **{k: v for k, v in hp.items() if k != "max_grad_norm"})
         for i in range(self.n):
             self.ref.set_has_grad(i, flags[i])
@@ -199,14 +203,50 @@ class Case:
                   max_grad_norm=None if rng.random() < 0.5 else float(10 ** rng.uniform(-2, 1)))
         indices = None if rng.random() < 0.6 else self.pick_subset()
         report = rng.random() < 0.5
+        defer = self.scaler_on and rng.random() < 0.3
+        noalloc = not report and rng.random() < 0.3
         active = self._active(indices)
-        print(f"  adam {hp} indices={indices} active={active}", flush=True)
-        r = self.store.adam_step(report=report, indices=indices, **hp)
-        e = self._ref_step("adam", hp, active)
+        print(f"  adam {hp} indices={indices} active={active}"
+              f"{' deferring the scale update' if defer else ''}"
+              f"{' (no-allocation entry point)' if noalloc else ''}", flush=True)
+        r = None
+        if noalloc and not self._noalloc_adam(hp, indices, defer):
+            noalloc = False  # refused, nothing changed: the allocating step instead
+        if not noalloc:
+            r = self.store.adam_step(report=report, indices=indices, update_scale=not defer,
+                                     **hp)
+        e = self._ref_step("adam", hp, active, update_scale=not defer)
         if report:
             self._check_report(r, e)
-        self.last_adam = (hp, indices, active)
+        if not noalloc:
+            # a capture repeats the last allocating step: the no-allocation step builds no
+            # bias table in host-count mode, which a capture could then not build either
+            self.last_adam = (hp, indices, active)
         self.adam_seen = True
+
+    def _noalloc_adam(self, hp, indices, defer):
+        """ttp_adam_step_noalloc; False when it refuses (a tensor set, betas or FP32 moments
+        that would need an allocation), after checking that the refusal changed nothing."""
+        import ctypes as C
+        from ttperf import _lib as L
+        h = L.AdamHParams(lr=hp["lr"], beta1=hp["betas"][0], beta2=hp["betas"][1],
+                          eps=hp["eps"], weight_decay=hp["weight_decay"],
+                          decoupled=1 if hp["decoupled"] else 0,
+                          flags=L.STEP_DEFER_SCALE if defer else 0,
+                          max_grad_norm=hp["max_grad_norm"] or 0.0)
+        t0 = self.store.step_count
+        if indices is None:
+            rc = L.lib.ttp_adam_step_noalloc(self.store.handle, C.byref(h), None, 0)
+        else:
+            idx = (C.c_uint32 * len(indices))(*indices)
+            rc = L.lib.ttp_adam_step_noalloc(self.store.handle, C.byref(h), idx, len(indices))
+        if rc == L.OK:
+            return True
+        msg = L.lib.ttp_last_error().decode()
+        assert rc == L.ERR_STATE and "no-allocation" in msg and "first" in msg, (rc, msg)
+        assert self.store.step_count == t0
+        print(f"   refused: {msg}", flush=True)
+        return False
 
     def op_sgd(self):
         rng = self.rng
@@ -222,10 +262,12 @@ class Case:
             hp.update(momentum=0.8, dampening=0.1, weight_decay=0.05)
         indices = None if rng.random() < 0.6 else self.pick_subset()
         report = rng.random() < 0.5
+        defer = self.scaler_on and rng.random() < 0.3
         active = self._active(indices)
-        print(f"  sgd {hp} indices={indices} active={active}", flush=True)
-        r = self.store.sgd_step(report=report, indices=indices, **hp)
-        e = self._ref_step("sgd", hp, active)
+        print(f"  sgd {hp} indices={indices} active={active}"
+              f"{' deferring the scale update' if defer else ''}", flush=True)
+        r = self.store.sgd_step(report=report, indices=indices, update_scale=not defer, **hp)
+        e = self._ref_step("sgd", hp, active, update_scale=not defer)
         if report:
             self._check_report(r, e)
         self.last_adam = None
@@ -298,7 +340,15 @@ class Case:
             self.ref.configure_scaler(True, init, growth_interval=interval)
         else:
             self.ref.s.scaler_enabled = 0
+            self.ref.s.pending = 0  # a configure drops a pending overflow
         self.scaler_on = on
+
+    def op_scaler_update(self):
+        """GradScaler.update() after deferred steps (a no-op while loss scaling is off)."""
+        print(f"  scaler_update (scaler {'on' if self.scaler_on else 'off'}, pending overflow "
+              f"{self.ref.s.pending})", flush=True)
+        self.store.scaler_update()
+        self.ref.scaler_update()
 
     def op_set_step(self):
         t = int(self.rng.integers(0, 50))
@@ -351,6 +401,7 @@ class Case:
         s.scale, s.growth_tracker = snap["scale"], snap["tracker"]
         s.scaler_enabled, s.growth_interval = snap["enabled"], snap["interval"]
         s.growth_factor, s.backoff_factor = snap["growth"], snap["backoff"]
+        s.pending = 0  # a loaded state has no pending overflow
         self.scaler_on = bool(snap["enabled"])
 
     def op_capture(self):
@@ -417,7 +468,7 @@ class Case:
     OPS = [("grads_flat", 6), ("grad_one", 3), ("accumulate", 3), ("drop_grad", 2),
            ("zero_grad", 2), ("upload_weights", 1), ("adam", 6), ("sgd", 4), ("scaler", 1),
            ("set_step", 1), ("grad_norm", 1), ("save", 1), ("load", 1), ("capture", 2),
-           ("replay", 3), ("sums_step", 4), ("zero_graph", 2)]
+           ("replay", 3), ("sums_step", 4), ("zero_graph", 2), ("scaler_update", 1)]
 
     def compare(self):
         from ttperf import _lib as L

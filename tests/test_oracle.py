@@ -273,6 +273,43 @@ def test_scaler_with_two_optimizers_matches_torch():
     assert not (np.array_equal(s, d["scale"]) and np.array_equal(t, d["tracker"]))
 
 
+def test_scaler_update_moves_the_scale_once_per_iteration():
+    """scaler_update applies only after a step that deferred the update: after an updating
+    step, or a second time, it changes nothing; after deferred steps it counts one clean
+    step, or backs off once however many of them overflowed."""
+    st = O.OracleStore([4, 3], mode=O.MODE_MIXED)
+    st.configure_scaler(True, 1024.0, 2.0, 0.5, 3)
+
+    def step(update_scale, inf=False):
+        g = np.ones(4, np.float32) * st.scale
+        if inf:
+            g[0] = np.inf
+        st.set_grad(0, O.bf16_rne(g))
+        return st.sgd_step(lr=1e-3, update_scale=update_scale)
+
+    step(True)
+    assert (st.scale, st.growth_tracker) == (1024.0, 1)
+    st.scaler_update()  # no deferred step since the last update: nothing
+    assert (st.scale, st.growth_tracker) == (1024.0, 1)
+    step(False)
+    step(False)
+    st.scaler_update()  # two clean deferred steps: one clean iteration
+    assert (st.scale, st.growth_tracker) == (1024.0, 2)
+    st.scaler_update()
+    assert (st.scale, st.growth_tracker) == (1024.0, 2)
+    r = step(False, inf=True)
+    assert r["skipped"] and r["scale"] == 1024.0  # deferred: the scale waits
+    step(False, inf=True)
+    step(False)
+    st.scaler_update()  # two overflows in the iteration: one backoff
+    assert (st.scale, st.growth_tracker) == (512.0, 0)
+    step(False)
+    step(True)  # the updating step closes the iteration ...
+    assert (st.scale, st.growth_tracker) == (512.0, 1)
+    st.scaler_update()  # ... so this changes nothing
+    assert (st.scale, st.growth_tracker) == (512.0, 1)
+
+
 @pytest.mark.parametrize("case", ["big", "small", "mid"])
 def test_clip_matches_torch(case):
     d = golden("torch_clip.npz")

@@ -88,13 +88,15 @@ struct DevState {
     float bias1, bias2;      // last pass: Adam bias corrections for the new t
     int32_t found_inf;       // last pass: a non-finite gradient was seen
     int32_t skip;            // last pass: the update must not run
-    // overflow seen by steps that deferred the scale update (several optimizers over one
-    // store: torch's GradScaler.step per optimizer, then one update); the next scale update
-    // combines it with its own and clears it (persistent)
-    int32_t pending_inf;
+    // steps that deferred the scale update since the last one (several optimizers over one
+    // store: torch's GradScaler.step per optimizer, then one update): kPendingStep once such a
+    // step ran, | kPendingInf if one of them saw an overflow.  The next scale update combines
+    // it with its own and clears it (persistent).
+    int32_t pending;
     int32_t reserved;
 };
 static_assert(sizeof(DevState) == 64, "DevState is one 64-byte block");
+constexpr int32_t kPendingInf = 1, kPendingStep = 2;
 
 // ------------------------------------------------------------------------------------
 // bf16
@@ -282,7 +284,8 @@ struct FinalizeArgs {
     const uint32_t* idx;    // non-null: partial k is partials[idx[k]] (per-tensor sums)
     uint32_t npartials;     // 0: no norm pass ran (step counting only)
     int32_t scaler_on;      // unscale by 1/scale, skip on inf, update the scale
-    int32_t defer_scale;    // with scaler_on: note found_inf in pending_inf, keep the scale
+    int32_t defer_scale;    // with scaler_on: note the step and its overflow in `pending`;
+                            // leave the scale as it is
     int32_t count_t;        // the step count lives on the device: advance it (unless skipped)
     int32_t probe;          // only compute sumsq/norm (ttp_grad_norm); touch nothing else
     int32_t growth_interval;
@@ -300,7 +303,7 @@ struct FinalizeArgs {
 // as GradScaler.update does); clears the pending flag
 __device__ __forceinline__ void scaler_update(DevState* st, int32_t found, int32_t growth_interval,
                                               double growth_factor, double backoff_factor) {
-    if (found || st->pending_inf) {
+    if (found || (st->pending & kPendingInf)) {
         st->scale = (float)((double)st->scale * backoff_factor);
         st->growth_tracker = 0;
     } else {
@@ -313,7 +316,7 @@ __device__ __forceinline__ void scaler_update(DevState* st, int32_t found, int32
             st->growth_tracker = ok;
         }
     }
-    st->pending_inf = 0;
+    st->pending = 0;
 }
 
 __global__ __launch_bounds__(kBlock) void norm_finalize_kernel(FinalizeArgs a) {
@@ -361,16 +364,17 @@ __global__ __launch_bounds__(kBlock) void norm_finalize_kernel(FinalizeArgs a) {
     }
     if (a.scaler_on) {
         if (a.defer_scale)
-            st->pending_inf |= found;
+            st->pending |= kPendingStep | (found ? kPendingInf : 0);
         else
             scaler_update(st, found, a.growth_interval, a.growth_factor, a.backoff_factor);
     }
 }
 
-// ttp_scaler_update: the scale update of an iteration whose steps all deferred it
+// ttp_scaler_update: the scale update of an iteration whose steps all deferred it; nothing
+// when no step deferred it since the last update, so an iteration's scale never moves twice
 __global__ void scaler_update_kernel(DevState* st, int32_t growth_interval, double growth_factor,
                                      double backoff_factor) {
-    if (threadIdx.x == 0 && blockIdx.x == 0)
+    if (threadIdx.x == 0 && blockIdx.x == 0 && (st->pending & kPendingStep))
         scaler_update(st, 0, growth_interval, growth_factor, backoff_factor);
 }
 

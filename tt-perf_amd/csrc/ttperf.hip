@@ -1633,7 +1633,7 @@ int ttp_scaler_configure(ttp_ctx* c, const ttp_scaler_config* cfg) {
         s.scale = (float)cfg->init_scale;
         s.growth_tracker = 0;
     }
-    s.pending_inf = 0;
+    s.pending = 0;
     HIP_TRY(hipMemcpy(c->st, &s, sizeof(s), hipMemcpyHostToDevice));
     c->scaler = *cfg;
     stale_sums(c);  // the sums are of gradients unscaled by the old scale
@@ -1663,7 +1663,7 @@ int ttp_scaler_set(ttp_ctx* c, float scale, int32_t tracker) {
     HIP_TRY(hipMemcpy(&s, c->st, sizeof(s), hipMemcpyDeviceToHost));
     s.scale = scale;
     s.growth_tracker = tracker;
-    s.pending_inf = 0;
+    s.pending = 0;
     HIP_TRY(hipMemcpy(c->st, &s, sizeof(s), hipMemcpyHostToDevice));
     stale_sums(c);
     return TTP_OK;
@@ -1959,7 +1959,7 @@ int ttp_load_state(ttp_ctx* c, const char* path) {
     ds.t = h.t;
     ds.scale = h.scale;
     ds.growth_tracker = h.growth_tracker;
-    ds.pending_inf = 0;
+    ds.pending = 0;
     HIP_TRY(hipMemcpy(c->st, &ds, sizeof(ds), hipMemcpyHostToDevice));
     stale_sums(c);
     return TTP_OK;

@@ -583,7 +583,8 @@ class ParamStore:
 
     def scaler_update(self):
         """GradScaler.update() for an iteration whose steps all passed update_scale=False:
-        back off if any of them saw an overflow, else count a clean step toward growth."""
+        back off if any of them saw an overflow, else count a clean step toward growth.
+        Nothing happens when no step deferred the update since the last one."""
         L.check(L.lib.ttp_scaler_update(self._h))
 
     # ---- optimizer-state checkpoint ---------------------------------------------------------
