@@ -396,20 +396,39 @@ def test_cfg5_gpt2_xl_fp32_adamw_then_sgd_momentum():
     compare_state(store, ref, which=("master", "momentum"), max_ulp=2)
 
 
-def test_update_forms_on_both_sides_of_the_cached_gradient_bound():
-    """The update kernels have two forms, chosen by the stepped set's gradient bytes (cached
-    gradient loads up to 256 MiB, non-temporal beyond).  Mixed-precision SGD with momentum and
-    Adam on a 140.7M-parameter store (281 MB of bf16 grads: the non-temporal form), then the same
-    optimizers over a subset of it (the cached form); each against the oracle."""
+@pytest.mark.parametrize("mode", ["mixed", "fp32"])
+def test_update_forms_on_both_sides_of_the_cached_gradient_bound(mode):
+    """The update kernels have two forms, chosen by the stepped set's gradient bytes: four
+    elements per lane up to 256 MiB, the lane forms (one or two elements per lane) beyond.
+    SGD with momentum and dampening, then AdamW, on a store just over the bound, each against
+    the oracle: the whole store and a subset that stays over it (lane forms with inactive
+    tensors between and after the active ones), then a subset under it (four-element form).
+    The FP32 store's first tensor has an odd element count, so the two-element lanes end on a
+    lone element."""
     torch = torch_mod()
-    shapes = [(50257, 768), (8192, 8192), (7000, 5000), (768,), (3,)]  # 140.7M params
-    decay = [True, True, True, False, False]
-    store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=80)
-    assert store.total * 2 > 256 << 20
+    if mode == "mixed":
+        shapes = [(50257, 768), (8192, 8192), (7000, 5000), (768,), (3,)]  # 140.7M params
+        decay = [True, True, True, False, False]
+        subsets = (None, [0, 1, 2], [0, 3, 4])
+        store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=80)
+        gbytes = 2
+    else:
+        shapes = [(8193, 8191), (77,), (3,)]  # 67.1M params
+        decay = [True, False, False]
+        subsets = (None, [0, 2], [1, 2])
+        store, ref = make_pair(shapes, decay, O.MODE_FP32, seed=82)
+        gbytes = 4
+    sizes = [int(np.prod(sh)) for sh in shapes]
+    bound = 256 << 20
+    assert sum(sizes) * gbytes > bound
+    assert sum(sizes[i] for i in subsets[1]) * gbytes > bound
+    assert sum(sizes[i] for i in subsets[2]) * gbytes <= bound
     gen = torch.Generator(device="cuda").manual_seed(81)
     sgd = dict(lr=1e-2, momentum=0.9, dampening=0.1, max_grad_norm=1.0)
     adam = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
-    for label, subset in (("whole store", None), ("subset", [0, 3, 4])):
+    slots = ("master", "param", "momentum") if mode == "mixed" else ("master", "momentum")
+    adam_slots = ("master", "exp_avg", "exp_avg_sq") + (("param",) if mode == "mixed" else ())
+    for label, subset in zip(("whole store", "lane-form subset", "four-element subset"), subsets):
         for step in range(2):
             host = device_grads(store, gen, 1e-3)
             ref.grad[:] = host
@@ -418,8 +437,8 @@ def test_update_forms_on_both_sides_of_the_cached_gradient_bound():
             r = store.sgd_step(report=True, indices=subset, **sgd)
             e = ref.sgd_step(**sgd)
             assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
-            print(f"{label} sgd-m step {step}: norm {r['grad_norm']:.6f}", flush=True)
-        compare_state(store, ref, which=("master", "param", "momentum"), max_ulp=2)
+            print(f"{mode} {label} sgd-m step {step}: norm {r['grad_norm']:.6f}", flush=True)
+        compare_state(store, ref, which=slots, max_ulp=2)
         for step in range(2):
             host = device_grads(store, gen, 1e-3)
             ref.grad[:] = host
@@ -428,8 +447,8 @@ def test_update_forms_on_both_sides_of_the_cached_gradient_bound():
             r = store.adam_step(report=True, indices=subset, **adam)
             e = ref.adam_step(**adam)
             assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
-            print(f"{label} adamw step {step}: norm {r['grad_norm']:.6f}", flush=True)
-        compare_state(store, ref, max_ulp=2)
+            print(f"{mode} {label} adamw step {step}: norm {r['grad_norm']:.6f}", flush=True)
+        compare_state(store, ref, which=adam_slots, max_ulp=2)
     store.close()
 
 

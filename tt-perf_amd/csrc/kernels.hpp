@@ -125,17 +125,14 @@ __device__ __forceinline__ void st4(float* p, f32x4 v) {
     __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
 }
 
-// 4 gradients as fp32 from either storage type.  kCached: ordinary (temporal) loads, for
-// gradients that are still in the 256 MB Infinity Cache (the norm pass or the backward touched
-// them last); otherwise non-temporal, like every other stream of the update.
-template <bool kCached>
+// 4 gradients as fp32 from either storage type, with ordinary (temporal) loads: the
+// four-element update runs only on gradients that fit the 256 MB Infinity Cache, where the
+// norm pass or the backward left them
 __device__ __forceinline__ f32x4 ld_grad4(const float* g, uint64_t i) {
-    return kCached ? *reinterpret_cast<const f32x4*>(g + i) : ld4(g + i);
+    return *reinterpret_cast<const f32x4*>(g + i);
 }
-template <bool kCached>
 __device__ __forceinline__ f32x4 ld_grad4(const uint16_t* g, uint64_t i) {
-    const u32x2* q = reinterpret_cast<const u32x2*>(g + i);
-    const u32x2 w = kCached ? *q : __builtin_nontemporal_load(q);
+    const u32x2 w = *reinterpret_cast<const u32x2*>(g + i);
     f32x4 r;
     r.x = bf16_lo(w.x);
     r.y = bf16_hi(w.x);
@@ -457,16 +454,32 @@ __device__ __forceinline__ void store_vec(float* a, float* b, float* c, uint16_t
     }
 }
 
-// One chunk of the Adam update: this lane's vector of chunk c (from the end of the table).
-template <typename GradT, bool kMixed, bool kGradCached>
-__device__ __forceinline__ void adam_chunk(const GradT* __restrict__ grad, float* __restrict__ master,
-                                           float* __restrict__ exp_avg,
-                                           float* __restrict__ exp_avg_sq,
-                                           uint16_t* __restrict__ param16, const AdamArgs& a,
-                                           const Coefs& k, bool use_inv, bool use_clip,
-                                           uint32_t c) {
+// The four-element Adam update: one block per chunk (grid == nchunks), blocks in reverse
+// chunk order, one 4-element vector per lane.  It runs the updates whose gradients fit the
+// Infinity Cache (kCachedGradBytes on the host: at most 2^17 chunks); larger ones take the
+// lane forms below.  master, exp_avg, exp_avg_sq are slot bases: MIXED, the three slots of
+// the [master|m|v] records; FP32, the contiguous master and the two slots of the [m|v]
+// records.
+template <typename GradT, bool kMixed>
+__global__ __launch_bounds__(kUpdBlock) void adam_kernel(const GradT* __restrict__ grad,
+                                                         float* __restrict__ master,
+                                                         float* __restrict__ exp_avg,
+                                                         float* __restrict__ exp_avg_sq,
+                                                         uint16_t* __restrict__ param16,
+                                                         AdamArgs a) {
     constexpr uint32_t kStateStride = kMixed ? kStrideMixed : kStrideMV;
-    const Chunk ch = a.chunks[a.nchunks - 1 - c];  // last chunks first (see norm pass)
+    Coefs k{1.0f, 1.0f, a.bias1, a.bias2};
+    if (a.st) {
+        if ((a.flags & kCheckSkip) && a.st->skip) return;
+        k.inv = a.st->inv_scale;
+        k.clip = a.st->clip_coef;
+        if (a.flags & kDevBias) {
+            k.bias1 = a.st->bias1;
+            k.bias2 = a.st->bias2;
+        }
+    }
+    const bool use_inv = a.flags & kUseInv, use_clip = a.flags & kUseClip;
+    const Chunk ch = a.chunks[a.nchunks - 1 - blockIdx.x];  // last chunks first (see norm pass)
     const uint32_t off = threadIdx.x * kVec;
     if (off >= ch.count) return;
     const int n = (int)min(ch.count - off, (uint32_t)kVec);
@@ -476,7 +489,7 @@ __device__ __forceinline__ void adam_chunk(const GradT* __restrict__ grad, float
     float* pp = master + (kMixed ? s : i);
     float* mp = exp_avg + s;
     float* vp = exp_avg_sq + s;
-    const f32x4 g = ld_grad4<kGradCached>(grad, i);
+    const f32x4 g = ld_grad4(grad, i);
     f32x4 p = ld4(pp);
     f32x4 m = ld4(mp);
     f32x4 v = ld4(vp);
@@ -491,39 +504,132 @@ __device__ __forceinline__ void adam_chunk(const GradT* __restrict__ grad, float
     store_vec<kMixed>(pp, mp, vp, param16, i, p, m, v, n);
 }
 
-// The Adam update.  The host launches one block per chunk (grid == nchunks), blocks in reverse
-// chunk order.  master, exp_avg, exp_avg_sq are slot bases: MIXED, the three slots of the
-// [master|m|v] records; FP32, the contiguous master and the two slots of the [m|v] records.
-// kGradCached (stores whose gradients fit the Infinity Cache) also selects the straight-line
-// form; larger stores use the grid-stride form, which runs one iteration at this grid.  Each
-// form measured faster in its own size class (interleaved A/B, three sweeps: GPT-2 124M
-// 561 vs 572 us per step; 774M 3795-3850 vs 3827-3891 us; 1.56B fp32 0.5%).
-template <typename GradT, bool kMixed, bool kGradCached>
-__global__ __launch_bounds__(kUpdBlock) void adam_kernel(const GradT* __restrict__ grad,
-                                                         float* __restrict__ master,
-                                                         float* __restrict__ exp_avg,
-                                                         float* __restrict__ exp_avg_sq,
-                                                         uint16_t* __restrict__ param16,
-                                                         AdamArgs a) {
-    Coefs k{1.0f, 1.0f, a.bias1, a.bias2};
-    if (a.st) {
-        if ((a.flags & kCheckSkip) && a.st->skip) return;
-        k.inv = a.st->inv_scale;
-        k.clip = a.st->clip_coef;
-        if (a.flags & kDevBias) {
-            k.bias1 = a.st->bias1;
-            k.bias2 = a.st->bias2;
-        }
-    }
-    const bool use_inv = a.flags & kUseInv, use_clip = a.flags & kUseClip;
-    if constexpr (kGradCached) {
-        adam_chunk<GradT, kMixed, true>(grad, master, exp_avg, exp_avg_sq, param16, a, k, use_inv,
-                                        use_clip, blockIdx.x);
+// ------------------------------------------------------------------------------------
+// lane forms: one or two elements per lane, for stores whose gradients exceed the Infinity
+// Cache
+// ------------------------------------------------------------------------------------
+// Each 256-lane block takes 1/lane_parts(kE) of a chunk (the last chunks first), each lane kE
+// consecutive elements, with no occupancy cap: a lane holds 14-32 B of loads in flight
+// instead of the four-element form's 56-64 B, so full occupancy (registers allow 32 waves
+// per CU) keeps about 28-32 KiB in flight per CU, where these read-modify-write streams run
+// fastest on MI355X.  The state is addressed from the record base alone (one 64-bit address
+// per lane, the other slots at immediate offsets), and the chunk descriptor is one 16-byte
+// scalar load issued together with the device-state loads, so two dependent scalar round
+// trips (arguments, then descriptor and state) precede the data loads.
+// Measured (interleaved rounds, x a plain 256-lane non-temporal copy of the same bytes):
+// GPT-2 774M mixed, one element: 0.965-0.967 against 0.920-0.925 for the four-element form;
+// GPT-2 1558M fp32, two elements: 0.926-0.929 against 0.904-0.906.  Below the Infinity Cache
+// bound the four-element form stays as fast or faster (GPT-2 124M: 0.99-1.00 against
+// 0.97-0.99), and keeps the four-times-smaller grid that a skipped step's early exit walks.
+template <int kE>
+constexpr uint32_t lane_parts() {
+    return kChunk / (kUpdBlock * kE);
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// chunk k of a table as one 16-byte load (a field-wise read compiles to two dependent loads:
+// the count first, then begin and meta)
+__device__ __forceinline__ Chunk load_chunk(const Chunk* t, uint64_t k) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(t + k);
+    return Chunk{(uint64_t)w.x | ((uint64_t)w.y << 32), w.z, w.w};
+}
+
+// kE gradients as fp32 (ordinary loads: faster here than non-temporal ones at 774M)
+template <int kE>
+__device__ __forceinline__ void ld_grad_lane(const uint16_t* g, uint64_t i, float* out) {
+    if constexpr (kE == 1) {
+        out[0] = __uint_as_float((uint32_t)g[i] << 16);
     } else {
-        for (uint32_t c = blockIdx.x; c < a.nchunks; c += gridDim.x)
-            adam_chunk<GradT, kMixed, false>(grad, master, exp_avg, exp_avg_sq, param16, a, k,
-                                             use_inv, use_clip, c);
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(g + i);
+        out[0] = bf16_lo(w);
+        out[1] = bf16_hi(w);
     }
+}
+template <int kE>
+__device__ __forceinline__ void ld_grad_lane(const float* g, uint64_t i, float* out) {
+    if constexpr (kE == 1) {
+        out[0] = g[i];
+    } else {
+        const f32x2 w = *reinterpret_cast<const f32x2*>(g + i);
+        out[0] = w.x;
+        out[1] = w.y;
+    }
+}
+// kE fp32 values, non-temporal
+template <int kE>
+__device__ __forceinline__ void ld_lane(const float* p, float* out) {
+    if constexpr (kE == 1) {
+        out[0] = __builtin_nontemporal_load(p);
+    } else {
+        const f32x2 w = __builtin_nontemporal_load(reinterpret_cast<const f32x2*>(p));
+        out[0] = w.x;
+        out[1] = w.y;
+    }
+}
+// the first n (1..kE) of kE fp32 values, non-temporal
+template <int kE>
+__device__ __forceinline__ void st_lane(float* p, const float* v, int n) {
+    if (kE == 2 && n == 2)
+        __builtin_nontemporal_store(f32x2{v[0], v[kE - 1]}, reinterpret_cast<f32x2*>(p));
+    else
+        __builtin_nontemporal_store(v[0], p);
+}
+template <int kE>
+__device__ __forceinline__ void st_bf16_lane(uint16_t* p, const float* v, int n) {
+    if (kE == 2 && n == 2)
+        __builtin_nontemporal_store(bf16_pack(v[0], v[kE - 1]), reinterpret_cast<uint32_t*>(p));
+    else
+        __builtin_nontemporal_store((uint16_t)bf16_rne(v[0]), p);
+}
+
+// The lane-form Adam update: one block per part, r = nparts - 1 - (part0 + blockIdx.x) (the
+// last chunks first, as the norm pass); the host splits stores beyond one launch's 2^32
+// work-items into launches at increasing part0.  One part per block with an early return
+// measured 2% faster at 774M than a grid-stride loop (which re-reads the descriptor per
+// iteration).  records is the record array's base ([master|m|v] in MIXED, [m|v] in FP32),
+// master the contiguous FP32 weights (unused in MIXED).  a.st must be valid: its fields are
+// read unconditionally and used as a.flags say.  The arithmetic is adam_elem's, so results
+// equal the four-element form's bit for bit.
+template <typename GradT, bool kMixed, int kE>
+__global__ __launch_bounds__(kUpdBlock) void adam_lane_kernel(const GradT* __restrict__ grad,
+                                                              float* __restrict__ records,
+                                                              float* __restrict__ master,
+                                                              uint16_t* __restrict__ param16,
+                                                              AdamArgs a, uint64_t part0) {
+    constexpr uint32_t kP = lane_parts<kE>();
+    constexpr uint32_t kStateStride = kMixed ? kStrideMixed : kStrideMV;
+    const uint64_t r = (uint64_t)a.nchunks * kP - 1 - (part0 + blockIdx.x);
+    const Chunk ch = load_chunk(a.chunks, r / kP);
+    const DevState* st = a.st;
+    // `|` and `&`, not `||` and `&&`: the skip flag and the descriptor are both needed before
+    // the first branch, so their loads issue together
+    const bool run = ((a.flags & kCheckSkip) == 0) | (st->skip == 0);
+    const uint32_t off = ((uint32_t)(r % kP) * kUpdBlock + threadIdx.x) * kE;
+    if (!(run & (off < ch.count))) return;
+    const bool dev_bias = a.flags & kDevBias;
+    const Coefs k{st->inv_scale, st->clip_coef, dev_bias ? st->bias1 : a.bias1,
+                  dev_bias ? st->bias2 : a.bias2};
+    const bool use_inv = a.flags & kUseInv, use_clip = a.flags & kUseClip;
+    const int n = (int)min(ch.count - off, (uint32_t)kE);
+    const bool decay = (ch.meta & kChunkDecay) && (a.flags & kWdOn);
+    const uint64_t i = ch.begin + off;
+    const uint64_t s = rec_index(i, kStateStride);
+    float* pp = kMixed ? records + s : master + i;
+    float* mp = kMixed ? records + s + kRec : records + s;
+    float* vp = mp + kRec;
+    float g[kE], p[kE], m[kE], v[kE];
+    ld_grad_lane<kE>(grad, i, g);
+    ld_lane<kE>(pp, p);
+    ld_lane<kE>(mp, m);
+    ld_lane<kE>(vp, v);
+#pragma unroll
+    for (int j = 0; j < kE; ++j) adam_elem(p[j], g[j], m[j], v[j], a, k, use_inv, use_clip, decay);
+    st_lane<kE>(pp, p, n);
+    st_lane<kE>(mp, m, n);
+    st_lane<kE>(vp, v, n);
+    if (kMixed) st_bf16_lane<kE>(param16 + i, p, n);
 }
 
 // ------------------------------------------------------------------------------------
@@ -541,48 +647,27 @@ struct SgdArgs {
     const DevState* st;
 };
 
-// One chunk of the SGD update (see sgd_kernel).
-template <typename GradT, bool kMixed, bool kGradCached>
-__device__ __forceinline__ void sgd_chunk(const GradT* __restrict__ grad, float* __restrict__ master,
-                                          float* __restrict__ momentum,
-                                          uint16_t* __restrict__ param16, const SgdArgs& a,
-                                          float inv, float clip, uint32_t c) {
-    const bool use_inv = a.flags & kUseInv, use_clip = a.flags & kUseClip;
-    const bool mom_on = a.flags & kMomOn, nesterov = a.flags & kNesterov;
-    const Chunk ch = a.chunks[a.nchunks - 1 - c];  // last chunks first (see norm pass)
-    const uint32_t off = threadIdx.x * kVec;
-    if (off >= ch.count) return;
-    const int n = (int)min(ch.count - off, (uint32_t)kVec);
-    const bool decay = (ch.meta & kChunkDecay) && (a.flags & kWdOn);
-    const bool first = mom_on && a.mom_init[ch.meta >> 8] == 0u;
-    const uint64_t i = ch.begin + off;
-    float* pp = master + (kMixed ? rec_index(i, kStrideMixed) : i);
-    f32x4 g = ld_grad4<kGradCached>(grad, i);
-    f32x4 p = ld4(pp);
-    f32x4 b = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (mom_on && !first) b = ld4(momentum + i);
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-        float gj = g[j];
-        if (use_inv) gj = gj * inv;
-        if (use_clip) gj = gj * clip;
-        if (decay) gj = gj + a.wd * p[j];
-        if (mom_on) {
-            const float bj = first ? gj : a.mu * b[j] + a.omd * gj;
-            b[j] = bj;
-            gj = nesterov ? gj + a.mu * bj : bj;
-        }
-        const float update = gj * a.lr;  // autograd/dynamic/optim.hpp:24
-        p[j] = p[j] - update;             // autograd/dynamic/optim.hpp:25
+// One element of SGD: grad transforms, L2 decay, momentum / dampening / nesterov, then
+// `p - g*lr` rounded after the multiply and after the subtract.
+__device__ __forceinline__ void sgd_elem(float& p, float g, float& b, const SgdArgs& a, float inv,
+                                         float clip, bool use_inv, bool use_clip, bool decay,
+                                         bool mom_on, bool first, bool nesterov) {
+    if (use_inv) g = g * inv;
+    if (use_clip) g = g * clip;
+    if (decay) g = g + a.wd * p;
+    if (mom_on) {
+        const float bj = first ? g : a.mu * b + a.omd * g;
+        b = bj;
+        g = nesterov ? g + a.mu * bj : bj;
     }
-    store_vec<kMixed>(pp, mom_on ? momentum + i : nullptr, nullptr, param16, i, p, b, b, n);
+    const float update = g * a.lr;  // autograd/dynamic/optim.hpp:24
+    p = p - update;                 // autograd/dynamic/optim.hpp:25
 }
 
-// The SGD update, launched and shaped as adam_kernel (one block per chunk; straight-line form
-// for stores whose gradients fit the Infinity Cache, grid-stride form otherwise).  master is
-// the master slot base (MIXED: slot 0 of the [master|m|v] records; FP32: the contiguous
-// weights); momentum is contiguous.
-template <typename GradT, bool kMixed, bool kGradCached>
+// The four-element SGD update, launched and shaped as adam_kernel (one block per chunk, for
+// gradients that fit the Infinity Cache).  master is the master slot base (MIXED: slot 0 of
+// the [master|m|v] records; FP32: the contiguous weights); momentum is contiguous.
+template <typename GradT, bool kMixed>
 __global__ __launch_bounds__(kUpdBlock) void sgd_kernel(const GradT* __restrict__ grad,
                                                         float* __restrict__ master,
                                                         float* __restrict__ momentum,
@@ -594,12 +679,69 @@ __global__ __launch_bounds__(kUpdBlock) void sgd_kernel(const GradT* __restrict_
         inv = a.st->inv_scale;
         clip = a.st->clip_coef;
     }
-    if constexpr (kGradCached) {
-        sgd_chunk<GradT, kMixed, true>(grad, master, momentum, param16, a, inv, clip, blockIdx.x);
-    } else {
-        for (uint32_t c = blockIdx.x; c < a.nchunks; c += gridDim.x)
-            sgd_chunk<GradT, kMixed, false>(grad, master, momentum, param16, a, inv, clip, c);
+    const bool use_inv = a.flags & kUseInv, use_clip = a.flags & kUseClip;
+    const bool mom_on = a.flags & kMomOn, nesterov = a.flags & kNesterov;
+    const Chunk ch = a.chunks[a.nchunks - 1 - blockIdx.x];  // last chunks first (see norm pass)
+    const uint32_t off = threadIdx.x * kVec;
+    if (off >= ch.count) return;
+    const int n = (int)min(ch.count - off, (uint32_t)kVec);
+    const bool decay = (ch.meta & kChunkDecay) && (a.flags & kWdOn);
+    const bool first = mom_on && a.mom_init[ch.meta >> 8] == 0u;
+    const uint64_t i = ch.begin + off;
+    float* pp = master + (kMixed ? rec_index(i, kStrideMixed) : i);
+    f32x4 g = ld_grad4(grad, i);
+    f32x4 p = ld4(pp);
+    f32x4 b = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (mom_on && !first) b = ld4(momentum + i);
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+        float pj = p[j], bj = b[j];
+        sgd_elem(pj, g[j], bj, a, inv, clip, use_inv, use_clip, decay, mom_on, first, nesterov);
+        p[j] = pj;
+        b[j] = bj;
     }
+    store_vec<kMixed>(pp, mom_on ? momentum + i : nullptr, nullptr, param16, i, p, b, b, n);
+}
+
+// The lane-form SGD update, launched and shaped as adam_lane_kernel.  master is the master
+// slot base (MIXED: the [master|m|v] record array; FP32: the contiguous weights); momentum is
+// contiguous.  a.st must be valid.
+template <typename GradT, bool kMixed, int kE>
+__global__ __launch_bounds__(kUpdBlock) void sgd_lane_kernel(const GradT* __restrict__ grad,
+                                                             float* __restrict__ master,
+                                                             float* __restrict__ momentum,
+                                                             uint16_t* __restrict__ param16,
+                                                             SgdArgs a, uint64_t part0) {
+    constexpr uint32_t kP = lane_parts<kE>();
+    const uint64_t r = (uint64_t)a.nchunks * kP - 1 - (part0 + blockIdx.x);
+    const Chunk ch = load_chunk(a.chunks, r / kP);
+    const DevState* st = a.st;
+    const bool run = ((a.flags & kCheckSkip) == 0) | (st->skip == 0);  // see adam_lane_kernel
+    const uint32_t off = ((uint32_t)(r % kP) * kUpdBlock + threadIdx.x) * kE;
+    if (!(run & (off < ch.count))) return;
+    const bool use_inv = a.flags & kUseInv, use_clip = a.flags & kUseClip;
+    const bool mom_on = a.flags & kMomOn, nesterov = a.flags & kNesterov;
+    const int n = (int)min(ch.count - off, (uint32_t)kE);
+    const bool decay = (ch.meta & kChunkDecay) && (a.flags & kWdOn);
+    const bool first = mom_on && a.mom_init[ch.meta >> 8] == 0u;
+    const uint64_t i = ch.begin + off;
+    float* pp = master + (kMixed ? rec_index(i, kStrideMixed) : i);
+    float g[kE], p[kE], bm[kE];
+    ld_grad_lane<kE>(grad, i, g);
+    ld_lane<kE>(pp, p);
+    if (mom_on && !first) {
+        ld_lane<kE>(momentum + i, bm);
+    } else {
+#pragma unroll
+        for (int j = 0; j < kE; ++j) bm[j] = 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < kE; ++j)
+        sgd_elem(p[j], g[j], bm[j], a, st->inv_scale, st->clip_coef, use_inv, use_clip, decay,
+                 mom_on, first, nesterov);
+    st_lane<kE>(pp, p, n);
+    if (mom_on) st_lane<kE>(momentum + i, bm, n);
+    if (kMixed) st_bf16_lane<kE>(param16 + i, p, n);
 }
 
 // after a momentum step: mark the stepped tensors' buffers as initialised (unless skipped)

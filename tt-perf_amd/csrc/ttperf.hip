@@ -98,11 +98,11 @@ struct WorkTables {
     uint32_t n_tensors = 0;
 };
 
-// Gradient bytes up to which an update reads the gradients with ordinary (cached) loads, in
-// the kernels' straight-line form: MI355X's Infinity Cache (256 MB) still holds most of them
-// after the norm pass or the backward that wrote them.  GPT-2 124M (249 MB of bf16 grads)
-// steps 1.8% faster that way.  Larger stores keep non-temporal loads and the grid-stride form,
-// which measured 0.5-1% faster at 774M and 1.56B.
+// Gradient bytes up to which an update runs the four-element kernels: MI355X's Infinity Cache
+// (256 MB) still holds most of the gradients after the norm pass or the backward that wrote
+// them, and that form reads them fastest (GPT-2 124M, 249 MB of bf16 grads: 0.99-1.00x a
+// plain copy of the same bytes, against 0.97-0.99x for the one-element lane form).  Larger
+// stores take the lane forms (see kLaneAdamMixed).
 constexpr uint64_t kCachedGradBytes = 256ull << 20;
 
 }  // namespace
@@ -536,18 +536,32 @@ int set_dev(const ttp_ctx* c) {
     return TTP_OK;
 }
 
-// whether an update over `w` reads its gradients with cached loads (see kCachedGradBytes)
+// whether an update over `w` runs the four-element kernels (see kCachedGradBytes)
 bool grads_cached(const ttp_ctx* c, const WorkTables* w) {
     return w->elems * grad_esize(c) <= kCachedGradBytes;
 }
 
-// Largest grid of the chunk-walking kernels: 2^22 blocks of 256 lanes is 2^30 work-items, well
-// inside the 2^32 a launch may hold.  Their grid-stride forms loop over the rest.
+// Largest grid of the grid-stride chunk kernels (gradient zeroing): 2^22 blocks of 256 lanes is
+// 2^30 work-items, well inside the 2^32 a launch may hold; they loop over the rest.
 constexpr uint32_t kMaxGridBlocks = 1u << 22;
 
-// Update grid over n chunks: the straight-line form (gradients that fit the Infinity Cache,
-// at most 2^17 chunks) takes one block per chunk; the grid-stride form at most kMaxGridBlocks.
-uint32_t update_grid(bool cached, uint32_t n) { return cached ? n : std::min(n, kMaxGridBlocks); }
+// Updates whose gradients fit the Infinity Cache run the four-element kernels, one block per
+// chunk (at most 2^17 chunks); larger ones the lane forms, one block per 1/lane_parts<kE>() of
+// a chunk, with kE elements per lane chosen per case as the faster of 1 and 2 at GPT-2
+// 774M / 1558M (interleaved rounds, x a 256-lane non-temporal copy of the same bytes): Adam
+// MIXED 1 (0.97 against 0.90 at 2), Adam FP32 2 (0.95 against 0.92 at 1), SGD 2 (MIXED
+// 0.90 against 0.77, FP32 0.93 against 0.76).
+constexpr int kLaneAdamMixed = 1, kLaneAdamFp32 = 2, kLaneSgd = 2;
+
+// One launch holds at most 2^32 - 1 work-items: 2^24 - 1 blocks of 256 lanes.  A lane-form
+// update over more parts is split into launches at increasing part offsets.
+constexpr uint64_t kMaxLaneBlocks = (1u << 24) - 1;
+
+template <typename Launch>
+void launch_lanes(uint64_t nparts, Launch&& launch) {
+    for (uint64_t p0 = 0; p0 < nparts; p0 += kMaxLaneBlocks)
+        launch(dim3((uint32_t)std::min<uint64_t>(nparts - p0, kMaxLaneBlocks)), p0);
+}
 
 uint32_t norm_grid(const ttp_ctx* c, uint32_t nchunks) {
     return std::max<uint32_t>(1, std::min(nchunks, c->norm_grid_cap));
@@ -1352,27 +1366,33 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
         a.bias1 = a.bias2 = 1.0f;  // replaced by the device values
     }
     if (n) {
-        const bool cached = grads_cached(c, w);
-        const dim3 grid(update_grid(cached, n)), block(ttp::kUpdBlock);
+        const dim3 block(ttp::kUpdBlock);
         TimedLaunch tl(c, TTP_KERNEL_UPDATE, !noalloc);
         const uint16_t* g16 = (const uint16_t*)c->grad;
         const float* g32 = (const float*)c->grad;
         uint16_t* p16 = (uint16_t*)c->param;
+        ttp::AdamArgs al = a;
+        al.st = c->st;  // the lane forms read the device state unconditionally
         clear_hip_error();
-        if (c->mode == TTP_MODE_MIXED && cached)
-            hipLaunchKernelGGL((ttp::adam_kernel<uint16_t, true, true>), grid, block, c->upd_lds,
+        if (grads_cached(c, w) && c->mode == TTP_MODE_MIXED)
+            hipLaunchKernelGGL((ttp::adam_kernel<uint16_t, true>), dim3(n), block, c->upd_lds,
                                c->stream, g16, c->master, c->exp_avg, c->exp_avg_sq, p16, a);
+        else if (grads_cached(c, w))
+            hipLaunchKernelGGL((ttp::adam_kernel<float, false>), dim3(n), block, c->upd_lds,
+                               c->stream, g32, c->master, c->exp_avg, c->exp_avg_sq,
+                               (uint16_t*)nullptr, a);
         else if (c->mode == TTP_MODE_MIXED)
-            hipLaunchKernelGGL((ttp::adam_kernel<uint16_t, true, false>), grid, block, c->upd_lds,
-                               c->stream, g16, c->master, c->exp_avg, c->exp_avg_sq, p16, a);
-        else if (cached)
-            hipLaunchKernelGGL((ttp::adam_kernel<float, false, true>), grid, block, c->upd_lds,
-                               c->stream, g32, c->master, c->exp_avg, c->exp_avg_sq,
-                               (uint16_t*)nullptr, a);
+            launch_lanes((uint64_t)n * ttp::lane_parts<kLaneAdamMixed>(), [&](dim3 g, uint64_t p0) {
+                hipLaunchKernelGGL((ttp::adam_lane_kernel<uint16_t, true, kLaneAdamMixed>), g,
+                                   block, 0, c->stream, g16, c->records, (float*)nullptr, p16,
+                                   al, p0);
+            });
         else
-            hipLaunchKernelGGL((ttp::adam_kernel<float, false, false>), grid, block, c->upd_lds,
-                               c->stream, g32, c->master, c->exp_avg, c->exp_avg_sq,
-                               (uint16_t*)nullptr, a);
+            launch_lanes((uint64_t)n * ttp::lane_parts<kLaneAdamFp32>(), [&](dim3 g, uint64_t p0) {
+                hipLaunchKernelGGL((ttp::adam_lane_kernel<float, false, kLaneAdamFp32>), g, block,
+                                   0, c->stream, g32, c->records, c->master, (uint16_t*)nullptr,
+                                   al, p0);
+            });
         HIP_TRY(hipGetLastError());
         tl.done();
     }
@@ -1429,25 +1449,32 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
     if (clip) a.flags |= ttp::kUseClip;
     a.st = (need_norm || devt) ? c->st : nullptr;
     if (n) {
-        const bool cached = grads_cached(c, w);
-        const dim3 grid(update_grid(cached, n)), block(ttp::kUpdBlock);
+        const dim3 block(ttp::kUpdBlock);
         TimedLaunch tl(c, TTP_KERNEL_UPDATE);
         const uint16_t* g16 = (const uint16_t*)c->grad;
         const float* g32 = (const float*)c->grad;
         uint16_t* p16 = (uint16_t*)c->param;
+        ttp::SgdArgs al = a;
+        al.st = c->st;  // the lane forms read the device state unconditionally
+        const uint64_t nparts = (uint64_t)n * ttp::lane_parts<kLaneSgd>();
         clear_hip_error();
-        if (c->mode == TTP_MODE_MIXED && cached)
-            hipLaunchKernelGGL((ttp::sgd_kernel<uint16_t, true, true>), grid, block, c->upd_lds,
+        if (grads_cached(c, w) && c->mode == TTP_MODE_MIXED)
+            hipLaunchKernelGGL((ttp::sgd_kernel<uint16_t, true>), dim3(n), block, c->upd_lds,
                                c->stream, g16, c->master, c->momentum, p16, a);
+        else if (grads_cached(c, w))
+            hipLaunchKernelGGL((ttp::sgd_kernel<float, false>), dim3(n), block, c->upd_lds,
+                               c->stream, g32, c->master, c->momentum, (uint16_t*)nullptr, a);
         else if (c->mode == TTP_MODE_MIXED)
-            hipLaunchKernelGGL((ttp::sgd_kernel<uint16_t, true, false>), grid, block, c->upd_lds,
-                               c->stream, g16, c->master, c->momentum, p16, a);
-        else if (cached)
-            hipLaunchKernelGGL((ttp::sgd_kernel<float, false, true>), grid, block, c->upd_lds,
-                               c->stream, g32, c->master, c->momentum, (uint16_t*)nullptr, a);
+            launch_lanes(nparts, [&](dim3 g, uint64_t p0) {
+                hipLaunchKernelGGL((ttp::sgd_lane_kernel<uint16_t, true, kLaneSgd>), g, block, 0,
+                                   c->stream, g16, c->master, c->momentum, p16, al, p0);
+            });
         else
-            hipLaunchKernelGGL((ttp::sgd_kernel<float, false, false>), grid, block, c->upd_lds,
-                               c->stream, g32, c->master, c->momentum, (uint16_t*)nullptr, a);
+            launch_lanes(nparts, [&](dim3 g, uint64_t p0) {
+                hipLaunchKernelGGL((ttp::sgd_lane_kernel<float, false, kLaneSgd>), g, block, 0,
+                                   c->stream, g32, c->master, c->momentum, (uint16_t*)nullptr,
+                                   al, p0);
+            });
         HIP_TRY(hipGetLastError());
         tl.done();
         if (mom) {
