@@ -67,13 +67,22 @@ __host__ __device__ __forceinline__ uint64_t rec_index(uint64_t i, uint32_t stri
 }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct Chunk {
     uint64_t begin;  // first element (flat index)
     uint32_t count;  // elements in this chunk (exact, not padded)
     uint32_t meta;   // bit 0: decay; bits 8..31: tensor index
 };
+
+// chunk k of a table as one 16-byte load (a field-wise read compiles to two dependent loads:
+// the count first, then begin and meta)
+__device__ __forceinline__ Chunk load_chunk(const Chunk* t, uint64_t k) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(t + k);
+    return Chunk{(uint64_t)w.x | ((uint64_t)w.y << 32), w.z, w.w};
+}
 
 // Device-resident step state.  Written only by norm_finalize_kernel (and by the host between
 // steps); read by the update pass that follows it on the same stream.
@@ -213,57 +222,65 @@ constexpr uint32_t norm_tile_elems() {
     return (uint32_t)(kBlock * kNormLoads * 16 / sizeof(GradT));
 }
 
-// Grid-stride over the norm tiles; the next tile's descriptor is fetched while this tile's
-// loads are in flight.  The loads are ordinary (cached) loads, so the last-read gradients are
-// still in the 256 MB Infinity Cache when the update pass, which walks the chunks in reverse
-// order, reads them again (measured on GPT-2 124M: update 531 us after this pass vs 559 us
-// alone; non-temporal loads here, or a forward walk in the update, lose most of that).  No
-// atomics and no fences: each block writes one partial and norm_finalize_kernel (next on the
-// stream) combines them.  Squares of fp32 values are exact in fp64, and any inf/NaN gradient
-// makes the sum non-finite.
-template <typename GradT>
+// Grid-stride over the norm tiles t0 .. t1-1, one partial per block.  A whole tile (every tile
+// but a tensor's last) is four unconditional 16-byte loads per lane, all issued before the
+// arithmetic (the scheduling barrier keeps the compiler from interleaving them with it, which
+// left one or two loads in flight: 6.0-6.3 TB/s against 6.7-6.9 at GPT-2 774M / 1558M).
+// kNT selects non-temporal loads.  The host runs the pass as two launches: non-temporal over
+// all but the last kCachedGradBytes of gradients, then cached loads over those, which the
+// update, walking the chunks in reverse, reads first and so finds in the 256 MB Infinity
+// Cache (measured on GPT-2 124M: update 531 us after this pass vs 559 us alone; at 774M and
+// 1558M fp32 the split pass runs 232 and 931 us against 246-260 and 978-1030 us with cached
+// loads throughout, the update unchanged).  No atomics and no fences: each block writes one
+// partial and norm_finalize_kernel (next on the stream) combines them.  Squares of fp32
+// values are exact in fp64, and any inf/NaN gradient makes the sum non-finite.
+template <typename GradT, bool kNT>
 __global__ __launch_bounds__(kBlock) void norm_partials_kernel(const GradT* __restrict__ g,
                                                                const Chunk* __restrict__ tiles,
-                                                               uint32_t ntiles,
+                                                               uint32_t t0, uint32_t t1,
                                                                const DevState* __restrict__ st,
                                                                int32_t scaler_on,
                                                                double* __restrict__ partials) {
     typedef GradVec<GradT> GV;
+    typedef typename GV::raw R;
     constexpr int E = GV::kElems;
+    constexpr uint32_t kTile = norm_tile_elems<GradT>();
     __shared__ double lds[kBlock / 64];
     const float inv = scaler_on ? (float)(1.0 / (double)st->scale) : 1.0f;
     // two accumulators (element j of a vector goes to acc[j & 1]): a fixed order, so the
-    // sum stays deterministic, with half the dependent-add chain
+    // sum stays deterministic, with half the dependent-add chain.  The square of an fp32 value
+    // is exact in fp64, so fma(x, x, acc) rounds exactly as acc + x*x does (one rounding, of
+    // the add) with one instruction instead of two.
     double acc[2] = {0.0, 0.0};
-    Chunk next{0, 0, 0};
-    if (blockIdx.x < ntiles) next = tiles[blockIdx.x];
-    for (uint32_t c = blockIdx.x; c < ntiles; c += gridDim.x) {
-        const Chunk ch = next;
-        if (c + gridDim.x < ntiles) next = tiles[c + gridDim.x];
-        typename GV::raw w[kNormLoads];
-        uint32_t nv[kNormLoads];
+    for (uint32_t c = t0 + blockIdx.x; c < t1; c += gridDim.x) {
+        const Chunk ch = load_chunk(tiles, c);
+        const R* q = reinterpret_cast<const R*>(g + ch.begin) + threadIdx.x;
+        if (ch.count == kTile) {
+            R w[kNormLoads];
 #pragma unroll
-        for (int l = 0; l < kNormLoads; ++l) {
-            const uint32_t off = (uint32_t)(l * kBlock + threadIdx.x) * E;
-            nv[l] = off < ch.count ? min(ch.count - off, (uint32_t)E) : 0u;
-            // temporal loads: the gradients stay in the Infinity Cache for the update pass
-            if (nv[l]) w[l] = *reinterpret_cast<const typename GV::raw*>(g + ch.begin + off);
-        }
-        // The square of an fp32 value is exact in fp64, so fma(x, x, acc) rounds exactly as
-        // acc + x*x does (one rounding, of the add) with one instruction instead of two.
+            for (int l = 0; l < kNormLoads; ++l)
+                w[l] = kNT ? __builtin_nontemporal_load(q + l * kBlock) : q[l * kBlock];
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int l = 0; l < kNormLoads; ++l) {
-            if (nv[l] == (uint32_t)E) {  // whole vector: no per-element masks
+            for (int l = 0; l < kNormLoads; ++l) {
 #pragma unroll
                 for (int j = 0; j < E; ++j) {
                     const double x = (double)(GV::at(w[l], j) * inv);
                     acc[j & 1] = __builtin_fma(x, x, acc[j & 1]);
                 }
-            } else if (nv[l]) {
+            }
+        } else {  // a tensor's last tile: only the vectors (and elements) below its count
 #pragma unroll
-                for (int j = 0; j < E; ++j) {
-                    const double x = (uint32_t)j < nv[l] ? (double)(GV::at(w[l], j) * inv) : 0.0;
-                    acc[j & 1] = __builtin_fma(x, x, acc[j & 1]);
+            for (int l = 0; l < kNormLoads; ++l) {
+                const uint32_t off = (uint32_t)(l * kBlock + threadIdx.x) * E;
+                const uint32_t nv = off < ch.count ? min(ch.count - off, (uint32_t)E) : 0u;
+                if (nv) {
+                    const R w = q[l * kBlock];
+#pragma unroll
+                    for (int j = 0; j < E; ++j) {
+                        const double x = (uint32_t)j < nv ? (double)(GV::at(w, j) * inv) : 0.0;
+                        acc[j & 1] = __builtin_fma(x, x, acc[j & 1]);
+                    }
                 }
             }
         }
@@ -524,16 +541,6 @@ __global__ __launch_bounds__(kUpdBlock) void adam_kernel(const GradT* __restrict
 template <int kE>
 constexpr uint32_t lane_parts() {
     return kChunk / (kUpdBlock * kE);
-}
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-
-// chunk k of a table as one 16-byte load (a field-wise read compiles to two dependent loads:
-// the count first, then begin and meta)
-__device__ __forceinline__ Chunk load_chunk(const Chunk* t, uint64_t k) {
-    const u32x4 w = *reinterpret_cast<const u32x4*>(t + k);
-    return Chunk{(uint64_t)w.x | ((uint64_t)w.y << 32), w.z, w.w};
 }
 
 // kE gradients as fp32 (ordinary loads: faster here than non-temporal ones at 774M)

@@ -102,7 +102,8 @@ struct WorkTables {
 // (256 MB) still holds most of the gradients after the norm pass or the backward that wrote
 // them, and that form reads them fastest (GPT-2 124M, 249 MB of bf16 grads: 0.99-1.00x a
 // plain copy of the same bytes, against 0.97-0.99x for the one-element lane form).  Larger
-// stores take the lane forms (see kLaneAdamMixed).
+// stores take the lane forms (see kLaneAdamMixed).  The norm pass reads about this many bytes
+// of the last tiles with cached loads, the rest non-temporal (see NormSplit).
 constexpr uint64_t kCachedGradBytes = 256ull << 20;
 
 }  // namespace
@@ -567,6 +568,37 @@ uint32_t norm_grid(const ttp_ctx* c, uint32_t nchunks) {
     return std::max<uint32_t>(1, std::min(nchunks, c->norm_grid_cap));
 }
 
+// The norm pass over n tiles as two launches (see norm_partials_kernel): non-temporal loads
+// over tiles [0, split), cached loads over [split, n), the last kCachedGradBytes of gradients.
+// Partials: g_nt of the first launch, then g_cached of the second.
+struct NormSplit {
+    uint32_t split, g_nt, g_cached;
+    uint32_t partials() const { return g_nt + g_cached; }
+};
+NormSplit norm_split(const ttp_ctx* c, uint32_t n) {
+    const uint32_t keep = (uint32_t)std::min<uint64_t>(
+        n, kCachedGradBytes / ((uint64_t)norm_tile(c) * grad_esize(c)));
+    NormSplit s;
+    s.split = n - keep;
+    s.g_nt = s.split ? norm_grid(c, s.split) : 0;
+    s.g_cached = norm_grid(c, keep);
+    return s;
+}
+
+template <typename GradT>
+void launch_norm_pass(ttp_ctx* c, const WorkTables* w, const NormSplit& ns, int32_t scaler_on,
+                      double* partials) {
+    const GradT* g = (const GradT*)c->grad;
+    const DevState* st = c->st;
+    if (ns.g_nt)
+        hipLaunchKernelGGL((ttp::norm_partials_kernel<GradT, true>), dim3(ns.g_nt),
+                           dim3(ttp::kBlock), 0, c->stream, g, w->tiles, 0u, ns.split, st,
+                           scaler_on, partials);
+    hipLaunchKernelGGL((ttp::norm_partials_kernel<GradT, false>), dim3(ns.g_cached),
+                       dim3(ttp::kBlock), 0, c->stream, g, w->tiles, ns.split, w->n_tiles, st,
+                       scaler_on, partials + ns.g_nt);
+}
+
 // Step prologue on the device: the norm pass (partials, when `run_norm`) and the one-block
 // finalize (norm, found_inf / skip, clip coefficient, loss scale, and the step count with its
 // bias corrections when `count_t`); `probe` only computes the norm.
@@ -575,27 +607,21 @@ uint32_t norm_grid(const ttp_ctx* c, uint32_t nchunks) {
 int launch_prologue(ttp_ctx* c, const WorkTables* w, bool run_norm, double max_norm, bool probe,
                     bool want_bias, bool count_t, bool from_sums = false,
                     bool defer_scale = false, double* partials = nullptr) {
-    const Chunk* chunks = w->tiles;
-    const uint32_t n = w->n_tiles;
-    const uint32_t grid = norm_grid(c, n);
+    const NormSplit ns = norm_split(c, w->n_tiles);
     const int32_t scaler_on = c->scaler.enabled ? 1 : 0;
     TimedLaunch tl(c, TTP_KERNEL_NORM, partials == nullptr);
     if (!partials) partials = c->partials;
     if (run_norm && !from_sums) {
         clear_hip_error();
         if (c->mode == TTP_MODE_MIXED)
-            hipLaunchKernelGGL(ttp::norm_partials_kernel<uint16_t>, dim3(grid), dim3(ttp::kBlock),
-                               0, c->stream, (const uint16_t*)c->grad, chunks, n,
-                               (const DevState*)c->st, scaler_on, partials);
+            launch_norm_pass<uint16_t>(c, w, ns, scaler_on, partials);
         else
-            hipLaunchKernelGGL(ttp::norm_partials_kernel<float>, dim3(grid), dim3(ttp::kBlock), 0,
-                               c->stream, (const float*)c->grad, chunks, n,
-                               (const DevState*)c->st, scaler_on, partials);
+            launch_norm_pass<float>(c, w, ns, scaler_on, partials);
         HIP_TRY(hipGetLastError());
     }
     ttp::FinalizeArgs a{};
     a.partials = partials;
-    a.npartials = run_norm ? grid : 0;
+    a.npartials = run_norm ? ns.partials() : 0;
     if (run_norm && from_sums) {  // the step's tensors' sums, in tensor order
         a.partials = c->tsum;
         a.idx = w->tensor_ids;
@@ -960,7 +986,7 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
     if ((rc = alloc_zero(c, (void**)&c->mom_init, std::max<uint64_t>(n, 1) * 4))) return bail(rc);
     c->host_mom_init.assign(n, 0);
     if ((rc = alloc_zero(c, (void**)&c->st, sizeof(DevState)))) return bail(rc);
-    c->partials_cap = c->norm_grid_cap;
+    c->partials_cap = 2 * c->norm_grid_cap;  // the norm pass's two launches (NormSplit)
     if ((rc = alloc_zero(c, (void**)&c->partials, (uint64_t)c->partials_cap * 8))) return bail(rc);
     if ((rc = alloc_zero(c, (void**)&c->tsum, std::max<uint64_t>(n, 1) * 8))) return bail(rc);
     c->tsum_fresh.assign(n, 0);
@@ -1325,9 +1351,10 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
     const bool from_sums = need_norm && (hp->flags & TTP_STEP_TENSOR_SUMS);
     const bool defer = scaler && (hp->flags & TTP_STEP_DEFER_SCALE);
     if (from_sums && (rc = check_sums_current(c, active))) return rc;
-    if (noalloc && need_norm && !from_sums && norm_grid(c, w->n_tiles) > kNoAllocPartials)
+    if (noalloc && need_norm && !from_sums && norm_split(c, w->n_tiles).partials() > kNoAllocPartials)
         return fail(TTP_ERR_RANGE,
-                    "the norm pass would write " + std::to_string(norm_grid(c, w->n_tiles)) +
+                    "the norm pass would write " +
+                        std::to_string(norm_split(c, w->n_tiles).partials()) +
                         " partials; the no-allocation step holds at most " +
                         std::to_string(kNoAllocPartials) + " (lower TTP_NORM_GRID)");
     // the device table of bias corrections; built in host-count mode too (once per betas) so
@@ -1589,14 +1616,14 @@ int ttp_grad_sumsq_tensors(ttp_ctx* c, const uint32_t* indices, uint32_t n) {
         const int32_t scaler_on = c->scaler.enabled ? 1 : 0;
         clear_hip_error();
         if (c->mode == TTP_MODE_MIXED)
-            hipLaunchKernelGGL(ttp::norm_partials_kernel<uint16_t>, dim3(w->n_tiles),
+            hipLaunchKernelGGL((ttp::norm_partials_kernel<uint16_t, false>), dim3(w->n_tiles),
                                dim3(ttp::kBlock), 0, c->stream, (const uint16_t*)c->grad,
-                               w->tiles, w->n_tiles, (const DevState*)c->st, scaler_on,
+                               w->tiles, 0u, w->n_tiles, (const DevState*)c->st, scaler_on,
                                c->tile_sums);
         else
-            hipLaunchKernelGGL(ttp::norm_partials_kernel<float>, dim3(w->n_tiles),
+            hipLaunchKernelGGL((ttp::norm_partials_kernel<float, false>), dim3(w->n_tiles),
                                dim3(ttp::kBlock), 0, c->stream, (const float*)c->grad, w->tiles,
-                               w->n_tiles, (const DevState*)c->st, scaler_on, c->tile_sums);
+                               0u, w->n_tiles, (const DevState*)c->st, scaler_on, c->tile_sums);
         HIP_TRY(hipGetLastError());
         clear_hip_error();
         hipLaunchKernelGGL(ttp::tensor_sums_kernel, dim3(w->n_tensors), dim3(ttp::kBlock), 0,
