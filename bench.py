@@ -26,8 +26,8 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(REPO, "tt-perf_amd"))
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
-# gradient bytes up to which libttperf_hip runs the cached-gradient update instantiation
-# (kCachedGradBytes in tt-perf_amd/csrc/ttperf.hip): names the kernel in the roofline
+# gradient bytes up to which libttperf_hip runs the four-element update kernels, the lane forms
+# beyond (kCachedGradBytes in tt-perf_amd/csrc/ttperf.hip): names the kernel in the roofline
 CACHED_GRAD_BYTES = 256 << 20
 # algorithmic bytes per parameter of one update-kernel pass (and of the norm pass)
 UPDATE_BYTES = {("adamw", "mixed"): 28, ("adamw", "fp32"): 28, ("sgdm", "fp32"): 20,
@@ -537,12 +537,16 @@ def main():
         ceilings(stream, n_params * ub)
 
     achieved = n_params * ub / (upd_avg / 1e3) / 1e9
-    # the instantiation libttperf_hip launches (its rocprof name)
+    # the instantiation libttperf_hip launches (its rocprof name): the four-element kernel
+    # while the gradients fit the Infinity Cache, else the lane form with its elements per lane
     grad_t, mixed_t = ("unsigned short", "true") if mode == "mixed" else ("float", "false")
     grad_bytes = store_total * (2 if mode == "mixed" else 4)
-    cached_t = "true" if grad_bytes <= CACHED_GRAD_BYTES else "false"
-    kname = "adam_kernel" if args.optimizer == "adamw" else "sgd_kernel"
-    upd_kernel = f"{kname}<{grad_t}, {mixed_t}, {cached_t}>"
+    kname = "adam" if args.optimizer == "adamw" else "sgd"
+    if grad_bytes <= CACHED_GRAD_BYTES:
+        upd_kernel = f"{kname}_kernel<{grad_t}, {mixed_t}>"
+    else:
+        per_lane = 1 if (kname == "adam" and mode == "mixed") else 2
+        upd_kernel = f"{kname}_lane_kernel<{grad_t}, {mixed_t}, {per_lane}>"
     step_gbps = n_params * (ub + nb) / (ms_step / 1e3) / 1e9
     out = {
         "metric": HEADLINE if args.config == "gpt2_124m" and args.optimizer == "adamw" else
