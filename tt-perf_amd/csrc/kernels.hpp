@@ -1,19 +1,21 @@
 // kernels.hpp — gfx950 device code of libttperf_hip.
 //
-// One optimizer step over the flat store is at most three launches on one stream:
+// One optimizer step over the flat store is at most four launches on one stream:
 //   norm_partials_kernel  reads only the gradients (2 B/param bf16, 4 B/param fp32) in 16 KiB
 //                         tiles: fp64 sum of squares of the unscaled grads, one partial per
-//                         block; no atomics
-//                         and no fences (a per-block device-scope fence + ticket costs ~50 ns
-//                         per block on MI355X, serialised, which tripled the pass's time);
+//                         block; no atomics and no fences (a per-block device-scope fence +
+//                         ticket costs ~50 ns per block on MI355X, serialised, which tripled
+//                         the pass's time).  Two launches above 256 MiB of gradients:
+//                         non-temporal loads, then cached loads for the last 256 MiB;
 //   norm_finalize_kernel  one block: sums the partials in index order (deterministic),
 //                         decides found_inf / skip and the clip coefficient, advances the step
 //                         count and the loss scale;
 //   adam_kernel /         one fused pass per element: grad transform (unscale, clip), weight
-//   sgd_kernel            decay, the optimizer update and the bf16 copy.  Each element is
-//                         touched once; loads/stores are 16-byte (fp32 x4) and 8-byte (bf16 x4)
-//                         per lane, so every wave instruction covers a contiguous 1 KiB / 512 B
-//                         span.
+//   sgd_kernel            decay, the optimizer update and the bf16 copy, four elements per
+//                         lane (16-byte fp32 and 8-byte bf16 vectors), for stores whose
+//                         gradients fit the Infinity Cache; above that the lane forms
+//                         adam_lane_kernel / sgd_lane_kernel do the same with one or two
+//                         elements per lane.  Each element is touched once.
 // Optimizer state is stored in records (see kRec): in MIXED mode each 64-element group of the
 // flat store keeps its fp32 master, m and v side by side in one 768-byte record; in FP32 mode
 // (where the fp32 master is the model-facing weight and stays contiguous) m and v share
@@ -23,9 +25,9 @@
 // relative to each other (GPT-2 124M, fresh allocations, 6 rounds: 571-617 us per step with
 // separate buffers, 570-580 us with records).
 // Work is a table of chunks of kChunk elements (the last chunk of a tensor is shorter; every
-// chunk starts on a 64-element boundary).  The update runs one 256-thread block per chunk,
-// one vector per lane, at most kUpdBlocksPerCU blocks per CU: blocks are dispatched in
-// (reverse) chunk order, so the resident blocks sweep a narrow window of each buffer, which
+// chunk starts on a 64-element boundary).  The four-element update runs one 256-thread block
+// per chunk, one vector per lane, at most kUpdBlocksPerCU blocks per CU: blocks are dispatched
+// in (reverse) chunk order, so the resident blocks sweep a narrow window of each buffer, which
 // keeps DRAM pages open.  16K-element chunks, a persistent grid, two or four vectors per
 // lane, 512-thread blocks and unlimited occupancy each measured 3-12% slower.  No MFMA:
 // nothing here is a contraction.
