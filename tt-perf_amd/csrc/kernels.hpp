@@ -527,22 +527,23 @@ __global__ __launch_bounds__(kUpdBlock) void adam_kernel(const GradT* __restrict
 // lane forms: one or two elements per lane, for stores whose gradients exceed the Infinity
 // Cache
 // ------------------------------------------------------------------------------------
-// Each 256-lane block takes 1/lane_parts(kE) of a chunk (the last chunks first), each lane kE
-// consecutive elements, with no occupancy cap: a lane holds 14-32 B of loads in flight
-// instead of the four-element form's 56-64 B, so full occupancy (registers allow 32 waves
-// per CU) keeps about 28-32 KiB in flight per CU, where these read-modify-write streams run
-// fastest on MI355X.  The state is addressed from the record base alone (one 64-bit address
-// per lane, the other slots at immediate offsets), and the chunk descriptor is one 16-byte
-// scalar load issued together with the device-state loads, so two dependent scalar round
-// trips (arguments, then descriptor and state) precede the data loads.
+// Each block of kLanes lanes takes 1/lane_parts<kE, kLanes>() of a chunk (the last chunks
+// first), each lane kE consecutive elements, with no occupancy cap: a lane holds 14-32 B of
+// loads in flight instead of the four-element form's 56-64 B, and full occupancy (registers
+// allow 32 waves per CU) hides the arithmetic.  The state is addressed from the record base
+// alone (one 64-bit address per lane, the other slots at immediate offsets), and the chunk
+// descriptor is one 16-byte scalar load issued together with the device-state loads, so two
+// dependent scalar round trips (arguments, then descriptor and state) precede the data loads.
+// The host picks kE and kLanes per optimizer and mode (see kLaneAdamMixed in ttperf.hip).
 // Measured (interleaved rounds, x a plain 256-lane non-temporal copy of the same bytes):
-// GPT-2 774M mixed, one element: 0.965-0.967 against 0.920-0.925 for the four-element form;
-// GPT-2 1558M fp32, two elements: 0.926-0.929 against 0.904-0.906.  Below the Infinity Cache
-// bound the four-element form stays as fast or faster (GPT-2 124M: 0.99-1.00 against
-// 0.97-0.99), and keeps the four-times-smaller grid that a skipped step's early exit walks.
-template <int kE>
+// GPT-2 774M mixed AdamW, one element in 256-lane blocks: 0.970-0.979 against 0.910-0.930 for
+// the four-element form; GPT-2 1558M fp32 AdamW, two elements in 64-lane blocks: 0.966-0.976
+// against 0.905-0.927.  Below the Infinity Cache bound the four-element form stays as fast or
+// faster (GPT-2 124M: 1.01 against 0.97-1.01), and keeps the smaller grid that a skipped
+// step's early exit walks.
+template <int kE, int kLanes>
 constexpr uint32_t lane_parts() {
-    return kChunk / (kUpdBlock * kE);
+    return kChunk / (kLanes * kE);
 }
 
 // kE gradients as fp32 (ordinary loads: faster here than non-temporal ones at 774M)
@@ -594,20 +595,20 @@ __device__ __forceinline__ void st_bf16_lane(uint16_t* p, const float* v, int n)
 }
 
 // The lane-form Adam update: one block per part, r = nparts - 1 - (part0 + blockIdx.x) (the
-// last chunks first, as the norm pass); the host splits stores beyond one launch's 2^32
+// last chunks first, as the norm pass); the host splits stores beyond one launch's 2^32 - 1
 // work-items into launches at increasing part0.  One part per block with an early return
 // measured 2% faster at 774M than a grid-stride loop (which re-reads the descriptor per
 // iteration).  records is the record array's base ([master|m|v] in MIXED, [m|v] in FP32),
 // master the contiguous FP32 weights (unused in MIXED).  a.st must be valid: its fields are
 // read unconditionally and used as a.flags say.  The arithmetic is adam_elem's, so results
 // equal the four-element form's bit for bit.
-template <typename GradT, bool kMixed, int kE>
-__global__ __launch_bounds__(kUpdBlock) void adam_lane_kernel(const GradT* __restrict__ grad,
-                                                              float* __restrict__ records,
-                                                              float* __restrict__ master,
-                                                              uint16_t* __restrict__ param16,
-                                                              AdamArgs a, uint64_t part0) {
-    constexpr uint32_t kP = lane_parts<kE>();
+template <typename GradT, bool kMixed, int kE, int kLanes>
+__global__ __launch_bounds__(kLanes) void adam_lane_kernel(const GradT* __restrict__ grad,
+                                                           float* __restrict__ records,
+                                                           float* __restrict__ master,
+                                                           uint16_t* __restrict__ param16,
+                                                           AdamArgs a, uint64_t part0) {
+    constexpr uint32_t kP = lane_parts<kE, kLanes>();
     constexpr uint32_t kStateStride = kMixed ? kStrideMixed : kStrideMV;
     const uint64_t r = (uint64_t)a.nchunks * kP - 1 - (part0 + blockIdx.x);
     const Chunk ch = load_chunk(a.chunks, r / kP);
@@ -615,7 +616,7 @@ __global__ __launch_bounds__(kUpdBlock) void adam_lane_kernel(const GradT* __res
     // `|` and `&`, not `||` and `&&`: the skip flag and the descriptor are both needed before
     // the first branch, so their loads issue together
     const bool run = ((a.flags & kCheckSkip) == 0) | (st->skip == 0);
-    const uint32_t off = ((uint32_t)(r % kP) * kUpdBlock + threadIdx.x) * kE;
+    const uint32_t off = ((uint32_t)(r % kP) * kLanes + threadIdx.x) * kE;
     if (!(run & (off < ch.count))) return;
     const bool dev_bias = a.flags & kDevBias;
     const Coefs k{st->inv_scale, st->clip_coef, dev_bias ? st->bias1 : a.bias1,
@@ -715,18 +716,18 @@ __global__ __launch_bounds__(kUpdBlock) void sgd_kernel(const GradT* __restrict_
 // The lane-form SGD update, launched and shaped as adam_lane_kernel.  master is the master
 // slot base (MIXED: the [master|m|v] record array; FP32: the contiguous weights); momentum is
 // contiguous.  a.st must be valid.
-template <typename GradT, bool kMixed, int kE>
-__global__ __launch_bounds__(kUpdBlock) void sgd_lane_kernel(const GradT* __restrict__ grad,
-                                                             float* __restrict__ master,
-                                                             float* __restrict__ momentum,
-                                                             uint16_t* __restrict__ param16,
-                                                             SgdArgs a, uint64_t part0) {
-    constexpr uint32_t kP = lane_parts<kE>();
+template <typename GradT, bool kMixed, int kE, int kLanes>
+__global__ __launch_bounds__(kLanes) void sgd_lane_kernel(const GradT* __restrict__ grad,
+                                                          float* __restrict__ master,
+                                                          float* __restrict__ momentum,
+                                                          uint16_t* __restrict__ param16,
+                                                          SgdArgs a, uint64_t part0) {
+    constexpr uint32_t kP = lane_parts<kE, kLanes>();
     const uint64_t r = (uint64_t)a.nchunks * kP - 1 - (part0 + blockIdx.x);
     const Chunk ch = load_chunk(a.chunks, r / kP);
     const DevState* st = a.st;
     const bool run = ((a.flags & kCheckSkip) == 0) | (st->skip == 0);  // see adam_lane_kernel
-    const uint32_t off = ((uint32_t)(r % kP) * kUpdBlock + threadIdx.x) * kE;
+    const uint32_t off = ((uint32_t)(r % kP) * kLanes + threadIdx.x) * kE;
     if (!(run & (off < ch.count))) return;
     const bool use_inv = a.flags & kUseInv, use_clip = a.flags & kUseClip;
     const bool mom_on = a.flags & kMomOn, nesterov = a.flags & kNesterov;

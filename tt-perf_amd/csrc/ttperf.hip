@@ -547,21 +547,25 @@ bool grads_cached(const ttp_ctx* c, const WorkTables* w) {
 constexpr uint32_t kMaxGridBlocks = 1u << 22;
 
 // Updates whose gradients fit the Infinity Cache run the four-element kernels, one block per
-// chunk (at most 2^17 chunks); larger ones the lane forms, one block per 1/lane_parts<kE>() of
-// a chunk, with kE elements per lane chosen per case as the faster of 1 and 2 at GPT-2
-// 774M / 1558M (interleaved rounds, x a 256-lane non-temporal copy of the same bytes): Adam
-// MIXED 1 (0.97 against 0.90 at 2), Adam FP32 2 (0.95 against 0.92 at 1), SGD 2 (MIXED
-// 0.90 against 0.77, FP32 0.93 against 0.76).
-constexpr int kLaneAdamMixed = 1, kLaneAdamFp32 = 2, kLaneSgd = 2;
+// chunk (at most 2^17 chunks); larger ones the lane forms, kE elements per lane in blocks of
+// kLanes, one block per 1/lane_parts<kE, kLanes>() of a chunk.  Each shape is the fastest of
+// 1 or 2 elements in 64-, 128- or 256-lane blocks at GPT-2 774M mixed / 1558M fp32
+// (interleaved rounds, x a 256-lane non-temporal copy of the same bytes):
+//   Adam MIXED  1 x 256: 0.970-0.976 (1 x 128 0.94, 2 x 256 0.90, four-element 0.91-0.92)
+//   Adam FP32   2 x 64:  0.966-0.976 (2 x 256 0.93-0.95, 1 x 256 0.91, four-element 0.91)
+//   SGD MIXED   2 x 128: 0.910-0.914 (2 x 256 0.90, 1 x 256 0.81, four-element 0.90)
+//   SGD FP32    2 x 128: 0.996       (2 x 256 0.96, 1 x 256 0.82, four-element 0.98)
+constexpr int kLaneAdamMixed = 1, kLanesAdamMixed = 256;
+constexpr int kLaneAdamFp32 = 2, kLanesAdamFp32 = 64;
+constexpr int kLaneSgd = 2, kLanesSgd = 128;
 
-// One launch holds at most 2^32 - 1 work-items: 2^24 - 1 blocks of 256 lanes.  A lane-form
-// update over more parts is split into launches at increasing part offsets.
-constexpr uint64_t kMaxLaneBlocks = (1u << 24) - 1;
-
+// One launch holds at most 2^32 - 1 work-items, so at most (2^32 - 1) / lanes blocks.  A
+// lane-form update over more parts is split into launches at increasing part offsets.
 template <typename Launch>
-void launch_lanes(uint64_t nparts, Launch&& launch) {
-    for (uint64_t p0 = 0; p0 < nparts; p0 += kMaxLaneBlocks)
-        launch(dim3((uint32_t)std::min<uint64_t>(nparts - p0, kMaxLaneBlocks)), p0);
+void launch_lanes(uint64_t nparts, uint32_t lanes, Launch&& launch) {
+    const uint64_t max_blocks = 0xFFFFFFFFull / lanes;
+    for (uint64_t p0 = 0; p0 < nparts; p0 += max_blocks)
+        launch(dim3((uint32_t)std::min<uint64_t>(nparts - p0, max_blocks)), p0);
 }
 
 uint32_t norm_grid(const ttp_ctx* c, uint32_t nchunks) {
@@ -1409,16 +1413,20 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
                                c->stream, g32, c->master, c->exp_avg, c->exp_avg_sq,
                                (uint16_t*)nullptr, a);
         else if (c->mode == TTP_MODE_MIXED)
-            launch_lanes((uint64_t)n * ttp::lane_parts<kLaneAdamMixed>(), [&](dim3 g, uint64_t p0) {
-                hipLaunchKernelGGL((ttp::adam_lane_kernel<uint16_t, true, kLaneAdamMixed>), g,
-                                   block, 0, c->stream, g16, c->records, (float*)nullptr, p16,
-                                   al, p0);
+            launch_lanes((uint64_t)n * ttp::lane_parts<kLaneAdamMixed, kLanesAdamMixed>(),
+                         kLanesAdamMixed, [&](dim3 g, uint64_t p0) {
+                hipLaunchKernelGGL(
+                    (ttp::adam_lane_kernel<uint16_t, true, kLaneAdamMixed, kLanesAdamMixed>), g,
+                    dim3(kLanesAdamMixed), 0, c->stream, g16, c->records, (float*)nullptr, p16,
+                    al, p0);
             });
         else
-            launch_lanes((uint64_t)n * ttp::lane_parts<kLaneAdamFp32>(), [&](dim3 g, uint64_t p0) {
-                hipLaunchKernelGGL((ttp::adam_lane_kernel<float, false, kLaneAdamFp32>), g, block,
-                                   0, c->stream, g32, c->records, c->master, (uint16_t*)nullptr,
-                                   al, p0);
+            launch_lanes((uint64_t)n * ttp::lane_parts<kLaneAdamFp32, kLanesAdamFp32>(),
+                         kLanesAdamFp32, [&](dim3 g, uint64_t p0) {
+                hipLaunchKernelGGL(
+                    (ttp::adam_lane_kernel<float, false, kLaneAdamFp32, kLanesAdamFp32>), g,
+                    dim3(kLanesAdamFp32), 0, c->stream, g32, c->records, c->master,
+                    (uint16_t*)nullptr, al, p0);
             });
         HIP_TRY(hipGetLastError());
         tl.done();
@@ -1483,7 +1491,7 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
         uint16_t* p16 = (uint16_t*)c->param;
         ttp::SgdArgs al = a;
         al.st = c->st;  // the lane forms read the device state unconditionally
-        const uint64_t nparts = (uint64_t)n * ttp::lane_parts<kLaneSgd>();
+        const uint64_t nparts = (uint64_t)n * ttp::lane_parts<kLaneSgd, kLanesSgd>();
         clear_hip_error();
         if (grads_cached(c, w) && c->mode == TTP_MODE_MIXED)
             hipLaunchKernelGGL((ttp::sgd_kernel<uint16_t, true>), dim3(n), block, c->upd_lds,
@@ -1492,15 +1500,16 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
             hipLaunchKernelGGL((ttp::sgd_kernel<float, false>), dim3(n), block, c->upd_lds,
                                c->stream, g32, c->master, c->momentum, (uint16_t*)nullptr, a);
         else if (c->mode == TTP_MODE_MIXED)
-            launch_lanes(nparts, [&](dim3 g, uint64_t p0) {
-                hipLaunchKernelGGL((ttp::sgd_lane_kernel<uint16_t, true, kLaneSgd>), g, block, 0,
-                                   c->stream, g16, c->master, c->momentum, p16, al, p0);
+            launch_lanes(nparts, kLanesSgd, [&](dim3 g, uint64_t p0) {
+                hipLaunchKernelGGL((ttp::sgd_lane_kernel<uint16_t, true, kLaneSgd, kLanesSgd>), g,
+                                   dim3(kLanesSgd), 0, c->stream, g16, c->master, c->momentum,
+                                   p16, al, p0);
             });
         else
-            launch_lanes(nparts, [&](dim3 g, uint64_t p0) {
-                hipLaunchKernelGGL((ttp::sgd_lane_kernel<float, false, kLaneSgd>), g, block, 0,
-                                   c->stream, g32, c->master, c->momentum, (uint16_t*)nullptr,
-                                   al, p0);
+            launch_lanes(nparts, kLanesSgd, [&](dim3 g, uint64_t p0) {
+                hipLaunchKernelGGL((ttp::sgd_lane_kernel<float, false, kLaneSgd, kLanesSgd>), g,
+                                   dim3(kLanesSgd), 0, c->stream, g32, c->master, c->momentum,
+                                   (uint16_t*)nullptr, al, p0);
             });
         HIP_TRY(hipGetLastError());
         tl.done();
