@@ -379,6 +379,23 @@ def other_config(config, optimizer, steps, warmup):
     torch.cuda.synchronize()
     upd_ms, upd_n = store.timing_collect(L.KERNEL_UPDATE)
     nrm_ms, nrm_n = store.timing_collect(L.KERNEL_NORM)
+    store.timing(False)
+    # with loss scaling: 20 overflow steps between one event pair (a +inf planted in the
+    # first tensor's gradients), as for the headline configuration
+    skip_ms = None
+    if optimizer == "adamw" and cfg["scaler"]:
+        store.upload(L.BUF_GRAD, 0, torch.full((numels[0],), float("inf"), device="cuda",
+                                               dtype=torch.bfloat16 if mode == "mixed"
+                                               else torch.float32))
+        rs = store.adam_step(report=True, **hp)
+        assert rs["skipped"], rs
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(20):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        skip_ms = e0.elapsed_time(e1) / 20
     store.close()
     torch.cuda.empty_cache()
     ub = UPDATE_BYTES[(optimizer, mode)]
@@ -404,6 +421,7 @@ def other_config(config, optimizer, steps, warmup):
             "update_vs_nt_copy64": round(upd_gbps / nt_copy64_gbps, 4) if nt_copy64_gbps else None,
             "nt_copy64_GBps": round(nt_copy64_gbps, 1) if nt_copy64_gbps else None,
             "norm_pass_ms": round(nrm_ms / max(nrm_n, 1), 4),
+            "skipped_step_ms": round(skip_ms, 4) if skip_ms is not None else None,
             "params": n_params, "tensors": len(numels), "mode": mode,
             "steps": steps, "warmup": warmup}
 

@@ -34,9 +34,13 @@
  * Environment, read at ttp_create (tuning only):
  *   TTP_UPD_BLOCKS_PER_CU  resident update blocks per CU (default 4; 0: no cap).  Results do not
  *                          depend on it.
- *   TTP_NORM_GRID          blocks of the gradient-norm pass (default 8 x CUs, at most 65536).
- *                          It fixes the fp64 summation order of the norm: deterministic for a
+ *   TTP_NORM_GRID          blocks of each gradient-norm launch (default 8 x CUs, at most
+ *                          65536; the pass is two launches above 256 MiB of gradients).  It
+ *                          fixes the fp64 summation order of the norm: deterministic for a
  *                          given value, last bits may differ between values.
+ *   TTP_LANE_LAUNCH_BLOCKS most blocks per launch of the update for stores above 256 MiB of
+ *                          gradients (default: what 2^32 - 1 work-items allow); a larger
+ *                          update is split into several launches.  Results do not depend on it.
  */
 #ifndef TTPERF_TTPERF_H
 #define TTPERF_TTPERF_H
@@ -277,7 +281,8 @@ int ttp_sgd_step_subset(ttp_ctx* ctx, const ttp_sgd_hparams* hp, const uint32_t*
  * serving loops, harnesses that forbid hipMalloc.  Its norm pass writes its per-block
  * partials into a fixed 64 KiB array of the library on each device (8192 fp64 partials,
  * held until the process ends) instead of the context's own buffer; a step whose norm pass
- * would need more blocks (TTP_NORM_GRID above 8192) fails with TTP_ERR_RANGE.  Every
+ * would write more (one per block: up to TTP_NORM_GRID, twice that above 256 MiB of
+ * gradients) fails with TTP_ERR_RANGE.  Every
  * no-allocation step on one device shares that array: two that overlap in time on one
  * device (contexts on different streams) race, so order them (one stream, or events).
  * Whatever the step would have to allocate is refused with TTP_ERR_STATE before any work is

@@ -452,6 +452,46 @@ def test_update_forms_on_both_sides_of_the_cached_gradient_bound(mode):
     store.close()
 
 
+@pytest.mark.parametrize("mode", ["mixed", "fp32"])
+def test_lane_form_update_split_into_several_launches(mode, monkeypatch):
+    """A lane-form update over more blocks than one launch may hold runs as several launches
+    at increasing part offsets.  TTP_LANE_LAUNCH_BLOCKS (read at ttp_create) lowers that limit
+    to 4099 blocks, so that a store just over the 256 MiB bound takes dozens of launches, whose
+    boundaries fall inside chunks and tensors; SGD with momentum and AdamW on the whole store
+    and on a subset, against the oracle."""
+    torch = torch_mod()
+    monkeypatch.setenv("TTP_LANE_LAUNCH_BLOCKS", "4099")
+    if mode == "mixed":
+        shapes = [(50257, 768), (8192, 8192), (7000, 5000), (768,), (3,)]
+        decay = [True, True, True, False, False]
+        subset = [0, 1, 2]
+        store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=84)
+    else:
+        shapes = [(8193, 8191), (77,), (3,)]
+        decay = [True, False, False]
+        subset = [0, 2]
+        store, ref = make_pair(shapes, decay, O.MODE_FP32, seed=85)
+    gen = torch.Generator(device="cuda").manual_seed(86)
+    sgd = dict(lr=1e-2, momentum=0.9, dampening=0.1, max_grad_norm=1.0)
+    adam = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
+    slots = ("master", "param", "momentum") if mode == "mixed" else ("master", "momentum")
+    adam_slots = ("master", "exp_avg", "exp_avg_sq") + (("param",) if mode == "mixed" else ())
+    for label, sub in (("whole store", None), ("subset", subset)):
+        for name, hp in (("sgd-m", sgd), ("adamw", adam)):
+            host = device_grads(store, gen, 1e-3)
+            ref.grad[:] = host
+            for i in range(ref.n):
+                ref.set_has_grad(i, sub is None or i in sub)
+            step = store.sgd_step if name == "sgd-m" else store.adam_step
+            r = step(report=True, indices=sub, **hp)
+            e = (ref.sgd_step if name == "sgd-m" else ref.adam_step)(**hp)
+            assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
+            print(f"{mode} {label} {name}: norm {r['grad_norm']:.6f}", flush=True)
+        compare_state(store, ref, which=slots, max_ulp=2)
+        compare_state(store, ref, which=adam_slots, max_ulp=2)
+    store.close()
+
+
 def test_zero1_shard_step_matches_oracle():
     """One GPU's ZeRO-1 shard of GPT-2 124M (the last of 8: 28 pieces of tensors, 15.6M
     params) stepped with config 3's mixed AdamW, loss scaling and clipping; against the oracle.

@@ -168,6 +168,7 @@ struct ttp_ctx {
 
     uint32_t norm_grid_cap = 0;  // blocks of the norm pass (one partial each)
     uint32_t upd_lds = 0;        // dynamic LDS per update block (caps blocks per CU)
+    uint64_t lane_launch_cap = 0;  // most blocks per lane-form launch (0: the grid limit)
 
     WorkTables all;  // every non-empty tensor
     uint32_t n_nonempty = 0;
@@ -560,10 +561,13 @@ constexpr int kLaneAdamFp32 = 2, kLanesAdamFp32 = 64;
 constexpr int kLaneSgd = 2, kLanesSgd = 128;
 
 // One launch holds at most 2^32 - 1 work-items, so at most (2^32 - 1) / lanes blocks.  A
-// lane-form update over more parts is split into launches at increasing part offsets.
+// lane-form update over more parts is split into launches at increasing part offsets
+// (TTP_LANE_LAUNCH_BLOCKS lowers the per-launch limit, so tests reach the split on small
+// stores).
 template <typename Launch>
-void launch_lanes(uint64_t nparts, uint32_t lanes, Launch&& launch) {
-    const uint64_t max_blocks = 0xFFFFFFFFull / lanes;
+void launch_lanes(const ttp_ctx* c, uint64_t nparts, uint32_t lanes, Launch&& launch) {
+    uint64_t max_blocks = 0xFFFFFFFFull / lanes;
+    if (c->lane_launch_cap) max_blocks = std::min(max_blocks, c->lane_launch_cap);
     for (uint64_t p0 = 0; p0 < nparts; p0 += max_blocks)
         launch(dim3((uint32_t)std::min<uint64_t>(nparts - p0, max_blocks)), p0);
 }
@@ -965,6 +969,7 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
     }
     c->norm_grid_cap = (uint32_t)std::min<uint64_t>(
         65536, std::max<uint64_t>(1, env_u64("TTP_NORM_GRID", (uint64_t)c->num_cus * 8)));
+    c->lane_launch_cap = env_u64("TTP_LANE_LAUNCH_BLOCKS", 0);
 
     // layout
     c->tensors.resize(n);
@@ -1413,7 +1418,7 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
                                c->stream, g32, c->master, c->exp_avg, c->exp_avg_sq,
                                (uint16_t*)nullptr, a);
         else if (c->mode == TTP_MODE_MIXED)
-            launch_lanes((uint64_t)n * ttp::lane_parts<kLaneAdamMixed, kLanesAdamMixed>(),
+            launch_lanes(c, (uint64_t)n * ttp::lane_parts<kLaneAdamMixed, kLanesAdamMixed>(),
                          kLanesAdamMixed, [&](dim3 g, uint64_t p0) {
                 hipLaunchKernelGGL(
                     (ttp::adam_lane_kernel<uint16_t, true, kLaneAdamMixed, kLanesAdamMixed>), g,
@@ -1421,7 +1426,7 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
                     al, p0);
             });
         else
-            launch_lanes((uint64_t)n * ttp::lane_parts<kLaneAdamFp32, kLanesAdamFp32>(),
+            launch_lanes(c, (uint64_t)n * ttp::lane_parts<kLaneAdamFp32, kLanesAdamFp32>(),
                          kLanesAdamFp32, [&](dim3 g, uint64_t p0) {
                 hipLaunchKernelGGL(
                     (ttp::adam_lane_kernel<float, false, kLaneAdamFp32, kLanesAdamFp32>), g,
@@ -1500,13 +1505,13 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
             hipLaunchKernelGGL((ttp::sgd_kernel<float, false>), dim3(n), block, c->upd_lds,
                                c->stream, g32, c->master, c->momentum, (uint16_t*)nullptr, a);
         else if (c->mode == TTP_MODE_MIXED)
-            launch_lanes(nparts, kLanesSgd, [&](dim3 g, uint64_t p0) {
+            launch_lanes(c, nparts, kLanesSgd, [&](dim3 g, uint64_t p0) {
                 hipLaunchKernelGGL((ttp::sgd_lane_kernel<uint16_t, true, kLaneSgd, kLanesSgd>), g,
                                    dim3(kLanesSgd), 0, c->stream, g16, c->master, c->momentum,
                                    p16, al, p0);
             });
         else
-            launch_lanes(nparts, kLanesSgd, [&](dim3 g, uint64_t p0) {
+            launch_lanes(c, nparts, kLanesSgd, [&](dim3 g, uint64_t p0) {
                 hipLaunchKernelGGL((ttp::sgd_lane_kernel<float, false, kLaneSgd, kLanesSgd>), g,
                                    dim3(kLanesSgd), 0, c->stream, g32, c->master, c->momentum,
                                    (uint16_t*)nullptr, al, p0);
