@@ -124,6 +124,42 @@ def test_noalloc_step_equals_the_allocating_step_on_calls_in_a_row():
         s.close()
 
 
+def test_noalloc_step_over_the_infinity_cache_bound():
+    """Above 256 MiB of gradients the norm pass runs as two launches (non-temporal, then
+    cached loads: about 2850 partials) and the update takes its lane form.  The no-allocation
+    step equals the allocating one there too, on a whole-store call followed by a smaller
+    subset call that stays over the bound and by one under it."""
+    from ttperf import _lib as L
+    torch = torch_mod()
+    gen = torch.Generator(device="cuda").manual_seed(170)
+    shapes = [(50257, 768), (8192, 8192), (7000, 5000), (768,), (3,)]  # 281 MB of bf16 grads
+    decay = [True, True, True, False, False]
+    A, A2, refA = _pair_of_twins(shapes, decay, 171)
+    del refA  # the allocating entry point is the reference here
+    over, under = [0, 1, 2], [0, 3, 4]
+    for sub in (None, over, under):  # set-up: bias table and work tables
+        _same_grads_no_oracle(A, A2, gen)
+        A.adam_step(indices=sub, **HP)
+        A2.adam_step(indices=sub, **HP)
+    torch.cuda.synchronize()
+    _identical(A, A2, "set-up")
+    for label, sub in (("whole store", None), ("subset over the bound", over),
+                       ("subset under the bound", under)):
+        _same_grads_no_oracle(A, A2, gen)
+        A.adam_step(indices=sub, **HP)
+        assert _noalloc(A2, sub) == L.OK, L.lib.ttp_last_error()
+        torch.cuda.synchronize()
+        _identical(A, A2, label)
+    A.close()
+    A2.close()
+
+
+def _same_grads_no_oracle(a, b, gen):
+    from ttperf import _lib as L
+    host = device_grads(a, gen, 1e-3, scale=a.scaler_state()[0])
+    b.upload(L.BUF_GRAD, L.ALL_TENSORS, host)
+
+
 def test_noalloc_step_refuses_what_it_would_have_to_allocate():
     """Each refusal comes before any work is queued and leaves the store as it was."""
     import ttperf
