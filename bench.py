@@ -562,9 +562,10 @@ def main():
     kname = "adam" if args.optimizer == "adamw" else "sgd"
     if grad_bytes <= CACHED_GRAD_BYTES:
         upd_kernel = f"{kname}_kernel<{grad_t}, {mixed_t}>"
-    else:  # elements per lane and lanes per block (kLaneAdamMixed ... in ttperf.hip)
-        shape = {("adam", "mixed"): (1, 256), ("adam", "fp32"): (2, 64)}.get((kname, mode), (2, 128))
-        upd_kernel = f"{kname}_lane_kernel<{grad_t}, {mixed_t}, {shape[0]}, {shape[1]}>"
+    else:  # elements per lane, lanes per block, pieces per block (kLaneAdamMixed ... in ttperf.hip)
+        shape = {("adam", "mixed"): (1, 256, 2),
+                 ("adam", "fp32"): (1, 128, 2)}.get((kname, mode), (2, 128, 1))
+        upd_kernel = f"{kname}_lane_kernel<{grad_t}, {mixed_t}, {shape[0]}, {shape[1]}, {shape[2]}>"
     step_gbps = n_params * (ub + nb) / (ms_step / 1e3) / 1e9
     out = {
         "metric": HEADLINE if args.config == "gpt2_124m" and args.optimizer == "adamw" else

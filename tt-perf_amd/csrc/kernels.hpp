@@ -541,9 +541,9 @@ __global__ __launch_bounds__(kUpdBlock) void adam_kernel(const GradT* __restrict
 // against 0.905-0.927.  Below the Infinity Cache bound the four-element form stays as fast or
 // faster (GPT-2 124M: 1.01 against 0.97-1.01), and keeps the smaller grid that a skipped
 // step's early exit walks.
-template <int kE, int kLanes>
+template <int kE, int kLanes, int kIt>
 constexpr uint32_t lane_parts() {
-    return kChunk / (kLanes * kE);
+    return kChunk / (kLanes * kE * kIt);
 }
 
 // kE gradients as fp32 (ordinary loads: faster here than non-temporal ones at 774M)
@@ -594,37 +594,15 @@ __device__ __forceinline__ void st_bf16_lane(uint16_t* p, const float* v, int n)
         __builtin_nontemporal_store((uint16_t)bf16_rne(v[0]), p);
 }
 
-// The lane-form Adam update: one block per part, r = nparts - 1 - (part0 + blockIdx.x) (the
-// last chunks first, as the norm pass); the host splits stores beyond one launch's 2^32 - 1
-// work-items into launches at increasing part0.  One part per block with an early return
-// measured 2% faster at 774M than a grid-stride loop (which re-reads the descriptor per
-// iteration).  records is the record array's base ([master|m|v] in MIXED, [m|v] in FP32),
-// master the contiguous FP32 weights (unused in MIXED).  a.st must be valid: its fields are
-// read unconditionally and used as a.flags say.  The arithmetic is adam_elem's, so results
-// equal the four-element form's bit for bit.
-template <typename GradT, bool kMixed, int kE, int kLanes>
-__global__ __launch_bounds__(kLanes) void adam_lane_kernel(const GradT* __restrict__ grad,
-                                                           float* __restrict__ records,
-                                                           float* __restrict__ master,
-                                                           uint16_t* __restrict__ param16,
-                                                           AdamArgs a, uint64_t part0) {
-    constexpr uint32_t kP = lane_parts<kE, kLanes>();
+// One piece of the lane-form Adam update: this lane's kE elements at flat index i (the first
+// n of them stored: a tensor's last piece may end inside the lane).
+template <typename GradT, bool kMixed, int kE>
+__device__ __forceinline__ void adam_piece(const GradT* __restrict__ grad,
+                                           float* __restrict__ records, float* __restrict__ master,
+                                           uint16_t* __restrict__ param16, const AdamArgs& a,
+                                           const Coefs& k, bool use_inv, bool use_clip,
+                                           bool decay, uint64_t i, int n) {
     constexpr uint32_t kStateStride = kMixed ? kStrideMixed : kStrideMV;
-    const uint64_t r = (uint64_t)a.nchunks * kP - 1 - (part0 + blockIdx.x);
-    const Chunk ch = load_chunk(a.chunks, r / kP);
-    const DevState* st = a.st;
-    // `|` and `&`, not `||` and `&&`: the skip flag and the descriptor are both needed before
-    // the first branch, so their loads issue together
-    const bool run = ((a.flags & kCheckSkip) == 0) | (st->skip == 0);
-    const uint32_t off = ((uint32_t)(r % kP) * kLanes + threadIdx.x) * kE;
-    if (!(run & (off < ch.count))) return;
-    const bool dev_bias = a.flags & kDevBias;
-    const Coefs k{st->inv_scale, st->clip_coef, dev_bias ? st->bias1 : a.bias1,
-                  dev_bias ? st->bias2 : a.bias2};
-    const bool use_inv = a.flags & kUseInv, use_clip = a.flags & kUseClip;
-    const int n = (int)min(ch.count - off, (uint32_t)kE);
-    const bool decay = (ch.meta & kChunkDecay) && (a.flags & kWdOn);
-    const uint64_t i = ch.begin + off;
     const uint64_t s = rec_index(i, kStateStride);
     float* pp = kMixed ? records + s : master + i;
     float* mp = kMixed ? records + s + kRec : records + s;
@@ -640,6 +618,52 @@ __global__ __launch_bounds__(kLanes) void adam_lane_kernel(const GradT* __restri
     st_lane<kE>(mp, m, n);
     st_lane<kE>(vp, v, n);
     if (kMixed) st_bf16_lane<kE>(param16 + i, p, n);
+}
+
+// The lane-form Adam update: one block per part of kIt consecutive pieces of kLanes x kE
+// elements, r = nparts - 1 - (part0 + blockIdx.x) (the last chunks first, as the norm pass);
+// the host splits stores beyond one launch's 2^32 - 1 work-items into launches at increasing
+// part0.  With kIt = 2 each lane walks its two pieces in turn (a loop the compiler keeps
+// rolled): at GPT-2 774M mixed that measured 1.01x the copy against 0.96-0.98x for one piece
+// per block, and halves the grid a skipped step dispatches.  records is the record array's
+// base ([master|m|v] in MIXED, [m|v] in FP32), master the contiguous FP32 weights (unused in
+// MIXED).  a.st must be valid: its fields are read unconditionally and used as a.flags say.
+// The arithmetic is adam_elem's, so results equal the four-element form's bit for bit.
+template <typename GradT, bool kMixed, int kE, int kLanes, int kIt>
+__global__ __launch_bounds__(kLanes) void adam_lane_kernel(const GradT* __restrict__ grad,
+                                                           float* __restrict__ records,
+                                                           float* __restrict__ master,
+                                                           uint16_t* __restrict__ param16,
+                                                           AdamArgs a, uint64_t part0) {
+    constexpr uint32_t kPiece = kLanes * kE;
+    constexpr uint32_t kP = lane_parts<kE, kLanes, kIt>();
+    const uint64_t r = (uint64_t)a.nchunks * kP - 1 - (part0 + blockIdx.x);
+    const Chunk ch = load_chunk(a.chunks, r / kP);
+    const DevState* st = a.st;
+    // `|` and `&`, not `||` and `&&`: the skip flag and the descriptor are both needed before
+    // the first branch, so their loads issue together
+    const bool run = ((a.flags & kCheckSkip) == 0) | (st->skip == 0);
+    const uint32_t off = (uint32_t)(r % kP) * (kPiece * kIt) + threadIdx.x * kE;
+    if (!(run & (off < ch.count))) return;
+    const bool dev_bias = a.flags & kDevBias;
+    const Coefs k{st->inv_scale, st->clip_coef, dev_bias ? st->bias1 : a.bias1,
+                  dev_bias ? st->bias2 : a.bias2};
+    const bool use_inv = a.flags & kUseInv, use_clip = a.flags & kUseClip;
+    const bool decay = (ch.meta & kChunkDecay) && (a.flags & kWdOn);
+    if constexpr (kIt == 1) {
+        adam_piece<GradT, kMixed, kE>(grad, records, master, param16, a, k, use_inv, use_clip,
+                                      decay, ch.begin + off,
+                                      (int)min(ch.count - off, (uint32_t)kE));
+    } else {
+#pragma unroll 1
+        for (int q = 0; q < kIt; ++q) {
+            const uint32_t o = off + q * kPiece;
+            if (o >= ch.count) break;
+            adam_piece<GradT, kMixed, kE>(grad, records, master, param16, a, k, use_inv,
+                                          use_clip, decay, ch.begin + o,
+                                          (int)min(ch.count - o, (uint32_t)kE));
+        }
+    }
 }
 
 // ------------------------------------------------------------------------------------
@@ -713,28 +737,15 @@ __global__ __launch_bounds__(kUpdBlock) void sgd_kernel(const GradT* __restrict_
     store_vec<kMixed>(pp, mom_on ? momentum + i : nullptr, nullptr, param16, i, p, b, b, n);
 }
 
-// The lane-form SGD update, launched and shaped as adam_lane_kernel.  master is the master
-// slot base (MIXED: the [master|m|v] record array; FP32: the contiguous weights); momentum is
-// contiguous.  a.st must be valid.
-template <typename GradT, bool kMixed, int kE, int kLanes>
-__global__ __launch_bounds__(kLanes) void sgd_lane_kernel(const GradT* __restrict__ grad,
-                                                          float* __restrict__ master,
-                                                          float* __restrict__ momentum,
-                                                          uint16_t* __restrict__ param16,
-                                                          SgdArgs a, uint64_t part0) {
-    constexpr uint32_t kP = lane_parts<kE, kLanes>();
-    const uint64_t r = (uint64_t)a.nchunks * kP - 1 - (part0 + blockIdx.x);
-    const Chunk ch = load_chunk(a.chunks, r / kP);
-    const DevState* st = a.st;
-    const bool run = ((a.flags & kCheckSkip) == 0) | (st->skip == 0);  // see adam_lane_kernel
-    const uint32_t off = ((uint32_t)(r % kP) * kLanes + threadIdx.x) * kE;
-    if (!(run & (off < ch.count))) return;
-    const bool use_inv = a.flags & kUseInv, use_clip = a.flags & kUseClip;
-    const bool mom_on = a.flags & kMomOn, nesterov = a.flags & kNesterov;
-    const int n = (int)min(ch.count - off, (uint32_t)kE);
-    const bool decay = (ch.meta & kChunkDecay) && (a.flags & kWdOn);
-    const bool first = mom_on && a.mom_init[ch.meta >> 8] == 0u;
-    const uint64_t i = ch.begin + off;
+// One piece of the lane-form SGD update (see adam_piece).
+template <typename GradT, bool kMixed, int kE>
+__device__ __forceinline__ void sgd_piece(const GradT* __restrict__ grad,
+                                          float* __restrict__ master,
+                                          float* __restrict__ momentum,
+                                          uint16_t* __restrict__ param16, const SgdArgs& a,
+                                          float inv, float clip, bool use_inv, bool use_clip,
+                                          bool decay, bool mom_on, bool first, bool nesterov,
+                                          uint64_t i, int n) {
     float* pp = master + (kMixed ? rec_index(i, kStrideMixed) : i);
     float g[kE], p[kE], bm[kE];
     ld_grad_lane<kE>(grad, i, g);
@@ -747,11 +758,49 @@ __global__ __launch_bounds__(kLanes) void sgd_lane_kernel(const GradT* __restric
     }
 #pragma unroll
     for (int j = 0; j < kE; ++j)
-        sgd_elem(p[j], g[j], bm[j], a, st->inv_scale, st->clip_coef, use_inv, use_clip, decay,
-                 mom_on, first, nesterov);
+        sgd_elem(p[j], g[j], bm[j], a, inv, clip, use_inv, use_clip, decay, mom_on, first,
+                 nesterov);
     st_lane<kE>(pp, p, n);
     if (mom_on) st_lane<kE>(momentum + i, bm, n);
     if (kMixed) st_bf16_lane<kE>(param16 + i, p, n);
+}
+
+// The lane-form SGD update, launched and shaped as adam_lane_kernel.  master is the master
+// slot base (MIXED: the [master|m|v] record array; FP32: the contiguous weights); momentum is
+// contiguous.  a.st must be valid.
+template <typename GradT, bool kMixed, int kE, int kLanes, int kIt>
+__global__ __launch_bounds__(kLanes) void sgd_lane_kernel(const GradT* __restrict__ grad,
+                                                          float* __restrict__ master,
+                                                          float* __restrict__ momentum,
+                                                          uint16_t* __restrict__ param16,
+                                                          SgdArgs a, uint64_t part0) {
+    constexpr uint32_t kPiece = kLanes * kE;
+    constexpr uint32_t kP = lane_parts<kE, kLanes, kIt>();
+    const uint64_t r = (uint64_t)a.nchunks * kP - 1 - (part0 + blockIdx.x);
+    const Chunk ch = load_chunk(a.chunks, r / kP);
+    const DevState* st = a.st;
+    const bool run = ((a.flags & kCheckSkip) == 0) | (st->skip == 0);  // see adam_lane_kernel
+    const uint32_t off = (uint32_t)(r % kP) * (kPiece * kIt) + threadIdx.x * kE;
+    if (!(run & (off < ch.count))) return;
+    const bool use_inv = a.flags & kUseInv, use_clip = a.flags & kUseClip;
+    const bool mom_on = a.flags & kMomOn, nesterov = a.flags & kNesterov;
+    const bool decay = (ch.meta & kChunkDecay) && (a.flags & kWdOn);
+    const bool first = mom_on && a.mom_init[ch.meta >> 8] == 0u;
+    const float inv = st->inv_scale, clip = st->clip_coef;
+    if constexpr (kIt == 1) {
+        sgd_piece<GradT, kMixed, kE>(grad, master, momentum, param16, a, inv, clip, use_inv,
+                                     use_clip, decay, mom_on, first, nesterov, ch.begin + off,
+                                     (int)min(ch.count - off, (uint32_t)kE));
+    } else {
+#pragma unroll 1
+        for (int q = 0; q < kIt; ++q) {
+            const uint32_t o = off + q * kPiece;
+            if (o >= ch.count) break;
+            sgd_piece<GradT, kMixed, kE>(grad, master, momentum, param16, a, inv, clip, use_inv,
+                                         use_clip, decay, mom_on, first, nesterov,
+                                         ch.begin + o, (int)min(ch.count - o, (uint32_t)kE));
+        }
+    }
 }
 
 // after a momentum step: mark the stepped tensors' buffers as initialised (unless skipped)

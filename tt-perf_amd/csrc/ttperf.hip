@@ -548,17 +548,17 @@ bool grads_cached(const ttp_ctx* c, const WorkTables* w) {
 constexpr uint32_t kMaxGridBlocks = 1u << 22;
 
 // Updates whose gradients fit the Infinity Cache run the four-element kernels, one block per
-// chunk (at most 2^17 chunks); larger ones the lane forms, kE elements per lane in blocks of
-// kLanes, one block per 1/lane_parts<kE, kLanes>() of a chunk.  Each shape is the fastest of
-// 1 or 2 elements in 64-, 128- or 256-lane blocks at GPT-2 774M mixed / 1558M fp32
-// (interleaved rounds, x a 256-lane non-temporal copy of the same bytes):
-//   Adam MIXED  1 x 256: 0.970-0.976 (1 x 128 0.94, 2 x 256 0.90, four-element 0.91-0.92)
-//   Adam FP32   2 x 64:  0.966-0.976 (2 x 256 0.93-0.95, 1 x 256 0.91, four-element 0.91)
-//   SGD MIXED   2 x 128: 0.910-0.914 (2 x 256 0.90, 1 x 256 0.81, four-element 0.90)
-//   SGD FP32    2 x 128: 0.996       (2 x 256 0.96, 1 x 256 0.82, four-element 0.98)
-constexpr int kLaneAdamMixed = 1, kLanesAdamMixed = 256;
-constexpr int kLaneAdamFp32 = 2, kLanesAdamFp32 = 64;
-constexpr int kLaneSgd = 2, kLanesSgd = 128;
+// chunk (at most 2^17 chunks); larger ones the lane forms: kE elements per lane in blocks of
+// kLanes, each block walking kIt consecutive pieces of kLanes x kE elements, one block per
+// 1/lane_parts<kE, kLanes, kIt>() of a chunk.  Each shape is the fastest measured at GPT-2
+// 774M mixed / 1558M fp32 (interleaved rounds, x a 256-lane non-temporal copy of the same
+// bytes; elements x lanes x pieces):
+//   Adam MIXED  1 x 256 x 2: 1.014-1.016 (1x128x2 1.01, 1x256x1 0.96-0.98, four-element 0.91)
+//   Adam FP32   1 x 128 x 2: 1.022-1.027 (1x256x2 1.01-1.02, 2x64x1 0.98, 2x64x2 0.89)
+//   SGD         2 x 128 x 1: MIXED 0.91, FP32 0.97-1.00 (2x128x2 0.96, 1x256x2 0.95)
+constexpr int kLaneAdamMixed = 1, kLanesAdamMixed = 256, kItAdamMixed = 2;
+constexpr int kLaneAdamFp32 = 1, kLanesAdamFp32 = 128, kItAdamFp32 = 2;
+constexpr int kLaneSgd = 2, kLanesSgd = 128, kItSgd = 1;
 
 // One launch holds at most 2^32 - 1 work-items, so at most (2^32 - 1) / lanes blocks.  A
 // lane-form update over more parts is split into launches at increasing part offsets
@@ -1418,18 +1418,24 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
                                c->stream, g32, c->master, c->exp_avg, c->exp_avg_sq,
                                (uint16_t*)nullptr, a);
         else if (c->mode == TTP_MODE_MIXED)
-            launch_lanes(c, (uint64_t)n * ttp::lane_parts<kLaneAdamMixed, kLanesAdamMixed>(),
+            launch_lanes(c,
+                         (uint64_t)n *
+                             ttp::lane_parts<kLaneAdamMixed, kLanesAdamMixed, kItAdamMixed>(),
                          kLanesAdamMixed, [&](dim3 g, uint64_t p0) {
                 hipLaunchKernelGGL(
-                    (ttp::adam_lane_kernel<uint16_t, true, kLaneAdamMixed, kLanesAdamMixed>), g,
+                    (ttp::adam_lane_kernel<uint16_t, true, kLaneAdamMixed, kLanesAdamMixed,
+                                           kItAdamMixed>), g,
                     dim3(kLanesAdamMixed), 0, c->stream, g16, c->records, (float*)nullptr, p16,
                     al, p0);
             });
         else
-            launch_lanes(c, (uint64_t)n * ttp::lane_parts<kLaneAdamFp32, kLanesAdamFp32>(),
+            launch_lanes(c,
+                         (uint64_t)n *
+                             ttp::lane_parts<kLaneAdamFp32, kLanesAdamFp32, kItAdamFp32>(),
                          kLanesAdamFp32, [&](dim3 g, uint64_t p0) {
                 hipLaunchKernelGGL(
-                    (ttp::adam_lane_kernel<float, false, kLaneAdamFp32, kLanesAdamFp32>), g,
+                    (ttp::adam_lane_kernel<float, false, kLaneAdamFp32, kLanesAdamFp32,
+                                           kItAdamFp32>), g,
                     dim3(kLanesAdamFp32), 0, c->stream, g32, c->records, c->master,
                     (uint16_t*)nullptr, al, p0);
             });
@@ -1496,7 +1502,7 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
         uint16_t* p16 = (uint16_t*)c->param;
         ttp::SgdArgs al = a;
         al.st = c->st;  // the lane forms read the device state unconditionally
-        const uint64_t nparts = (uint64_t)n * ttp::lane_parts<kLaneSgd, kLanesSgd>();
+        const uint64_t nparts = (uint64_t)n * ttp::lane_parts<kLaneSgd, kLanesSgd, kItSgd>();
         clear_hip_error();
         if (grads_cached(c, w) && c->mode == TTP_MODE_MIXED)
             hipLaunchKernelGGL((ttp::sgd_kernel<uint16_t, true>), dim3(n), block, c->upd_lds,
@@ -1506,13 +1512,13 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
                                c->stream, g32, c->master, c->momentum, (uint16_t*)nullptr, a);
         else if (c->mode == TTP_MODE_MIXED)
             launch_lanes(c, nparts, kLanesSgd, [&](dim3 g, uint64_t p0) {
-                hipLaunchKernelGGL((ttp::sgd_lane_kernel<uint16_t, true, kLaneSgd, kLanesSgd>), g,
+                hipLaunchKernelGGL((ttp::sgd_lane_kernel<uint16_t, true, kLaneSgd, kLanesSgd, kItSgd>), g,
                                    dim3(kLanesSgd), 0, c->stream, g16, c->master, c->momentum,
                                    p16, al, p0);
             });
         else
             launch_lanes(c, nparts, kLanesSgd, [&](dim3 g, uint64_t p0) {
-                hipLaunchKernelGGL((ttp::sgd_lane_kernel<float, false, kLaneSgd, kLanesSgd>), g,
+                hipLaunchKernelGGL((ttp::sgd_lane_kernel<float, false, kLaneSgd, kLanesSgd, kItSgd>), g,
                                    dim3(kLanesSgd), 0, c->stream, g32, c->master, c->momentum,
                                    (uint16_t*)nullptr, al, p0);
             });
