@@ -527,20 +527,21 @@ __global__ __launch_bounds__(kUpdBlock) void adam_kernel(const GradT* __restrict
 // lane forms: one or two elements per lane, for stores whose gradients exceed the Infinity
 // Cache
 // ------------------------------------------------------------------------------------
-// Each block of kLanes lanes takes 1/lane_parts<kE, kLanes>() of a chunk (the last chunks
-// first), each lane kE consecutive elements, with no occupancy cap: a lane holds 14-32 B of
-// loads in flight instead of the four-element form's 56-64 B, and full occupancy (registers
-// allow 32 waves per CU) hides the arithmetic.  The state is addressed from the record base
-// alone (one 64-bit address per lane, the other slots at immediate offsets), and the chunk
-// descriptor is one 16-byte scalar load issued together with the device-state loads, so two
-// dependent scalar round trips (arguments, then descriptor and state) precede the data loads.
-// The host picks kE and kLanes per optimizer and mode (see kLaneAdamMixed in ttperf.hip).
-// Measured (interleaved rounds, x a plain 256-lane non-temporal copy of the same bytes):
-// GPT-2 774M mixed AdamW, one element in 256-lane blocks: 0.970-0.979 against 0.910-0.930 for
-// the four-element form; GPT-2 1558M fp32 AdamW, two elements in 64-lane blocks: 0.966-0.976
-// against 0.905-0.927.  Below the Infinity Cache bound the four-element form stays as fast or
-// faster (GPT-2 124M: 1.01 against 0.97-1.01), and keeps the smaller grid that a skipped
-// step's early exit walks.
+// Each block of kLanes lanes takes 1/lane_parts<kE, kLanes, kIt>() of a chunk (the last chunks
+// first): kIt consecutive pieces of kLanes x kE elements, each lane kE consecutive elements of
+// each piece, with no occupancy cap.  A lane holds 14-32 B of loads in flight instead of the
+// four-element form's 56-64 B, and full occupancy (registers allow 32 waves per CU) hides the
+// arithmetic.  The state is addressed from the record base alone (one 64-bit address per
+// lane, the other slots at immediate offsets), and the chunk descriptor is one 16-byte scalar
+// load issued together with the device-state loads, so two dependent scalar round trips
+// (arguments, then descriptor and state) precede the data loads.  The host picks the shape
+// per optimizer and mode (see kLaneAdamMixed in ttperf.hip).  Measured (interleaved rounds,
+// x a plain 256-lane non-temporal copy of the same bytes): GPT-2 774M mixed AdamW, one element
+// per lane, 256 lanes, two pieces: 1.014-1.018 against 0.96-0.98 with one piece and
+// 0.91-0.93 for the four-element form; GPT-2 1558M fp32 AdamW, one element, 128 lanes, two
+// pieces: 1.018-1.027 against 0.977 for two elements in one piece and 0.905-0.927.  Below
+// the Infinity Cache bound the four-element form stays as fast or faster (GPT-2 124M: 1.01
+// against 0.98-0.99), and keeps the smaller grid that a skipped step's early exit walks.
 template <int kE, int kLanes, int kIt>
 constexpr uint32_t lane_parts() {
     return kChunk / (kLanes * kE * kIt);
