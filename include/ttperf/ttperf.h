@@ -4,8 +4,10 @@
  * One context owns a flat parameter store on one GPU: every tensor of a model is a
  * {offset, numel, flags} view into flat HBM buffers (param, grad, fp32 master, exp_avg,
  * exp_avg_sq, momentum); the optimizer-private fp32 state is interleaved in records of
- * 64-element slots (see ttp_buffer_layout).  A step over all tensors is one multi-tensor launch
- * (plus one grad-norm/inf-check launch when clipping or loss scaling is on).
+ * 64-element slots (see ttp_buffer_layout).  A step over all tensors is one multi-tensor update
+ * launch (split in several only beyond 2^32 work-items), plus, when clipping or loss scaling
+ * is on, a grad-norm/inf-check pass (one launch, two above 256 MiB of gradients) and a
+ * one-block finalize.
  *
  * Reference interfaces each group of entry points replaces (csirak/tt-perf):
  *   ttp_create / ttp_destroy / ttp_tensor_*  — per-parameter storage owned by
@@ -373,8 +375,9 @@ int ttp_graph_destroy(ttp_graph* graph);
 #define TTP_KERNEL_UPDATE 1 /* fused multi-tensor update pass               */
 /* on = 1 starts recording an event pair around every launch of every kernel. */
 int ttp_timing_enable(ttp_ctx* ctx, int on);
-/* Waits for the recorded events, returns the summed milliseconds and the launch count
- * of `kernel` since the last reset, then forgets them. */
+/* Waits for the recorded events, returns the summed milliseconds and the count of `kernel`
+ * passes since the last reset (an event pair spans each pass: a norm pass with its finalize,
+ * an update with all its launches), then forgets them. */
 int ttp_timing_collect(ttp_ctx* ctx, int kernel, double* total_ms, uint64_t* launches);
 
 const char* ttp_last_error(void);
