@@ -405,8 +405,19 @@ __global__ __launch_bounds__(kBlock) void tensor_sums_kernel(const double* __res
     __shared__ double lds[kBlock / 64];
     const uint32_t t = blockIdx.x;
     const uint32_t b = tile_start[t], e = tile_start[t + 1];
+    // as norm_finalize_kernel: a round's loads issued before its adds, each lane's order fixed
+    constexpr int kPer = 8;
     double s = 0.0;
-    for (uint32_t k = b + threadIdx.x; k < e; k += kBlock) s += tile_sums[k];
+    for (uint32_t base = b; base < e; base += kBlock * kPer) {
+        double v[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const uint32_t i = base + (uint32_t)k * kBlock + threadIdx.x;
+            v[k] = i < e ? tile_sums[i] : 0.0;
+        }
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) s += v[k];
+    }
     s = block_sum(s, lds);
     if (threadIdx.x == 0) sums[tensor_ids[t]] = s;
 }
