@@ -93,6 +93,65 @@ def test_adam_graph_replays_match_eager_and_oracle(mode, scaler):
     graphed.close()
 
 
+@pytest.mark.parametrize("mode,opt", [(O.MODE_MIXED, "adamw"), (O.MODE_FP32, "adamw"),
+                                      (O.MODE_FP32, "sgdm")])
+def test_graph_replays_over_the_cache_bound(mode, opt):
+    """A captured step over a store just above 256 MiB of gradients: a two-launch norm pass
+    and a lane-form update (split into several launches by TTP_LANE_LAUNCH_BLOCKS in the
+    graphed store).  Replays with new gradients, one of them with an overflow, match an eager
+    twin bit for bit."""
+    import os
+    from ttperf import _lib as L
+    torch = torch_mod()
+    mixed = mode == O.MODE_MIXED
+    if mixed:
+        shapes = [(50257, 768), (8192, 8192), (7000, 5000), (768,), (3,)]
+        decay = [True, True, True, False, False]
+    else:
+        shapes = [(8193, 8191), (77,), (3,)]
+        decay = [True, False, False]
+    eager, _ = make_pair(shapes, decay, mode, seed=95)
+    os.environ["TTP_LANE_LAUNCH_BLOCKS"] = "70001"
+    try:
+        graphed, _ = make_pair(shapes, decay, mode, seed=95)
+    finally:
+        del os.environ["TTP_LANE_LAUNCH_BLOCKS"]
+    graphed.set_stream(None)
+    for s in (eager, graphed):
+        s.configure_scaler(True, init_scale=1024.0)
+    gen = torch.Generator(device="cuda").manual_seed(96)
+    if opt == "adamw":
+        hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
+        step = lambda s: s.adam_step(**hp)
+        bufs = (L.BUF_MASTER, L.BUF_EXP_AVG, L.BUF_EXP_AVG_SQ, L.BUF_PARAM)
+    else:
+        hp = dict(lr=1e-2, momentum=0.9, max_grad_norm=1.0)
+        step = lambda s: s.sgd_step(**hp)
+        bufs = (L.BUF_MASTER, L.BUF_MOMENTUM, L.BUF_PARAM)
+    _same_grads([eager, graphed], gen, 1e-3, scale=1024.0, mixed=mixed)
+    step(eager)
+    step(graphed)
+    graphed.begin_capture()
+    step(graphed)
+    graph = graphed.end_capture()
+    for k in range(3):
+        scale = eager.scaler_state()[0]
+        inf_at = int(graphed.offsets[1]) + 5 if k == 1 else None
+        _same_grads([eager, graphed], gen, 1e-3, scale=scale, inf_at=inf_at, mixed=mixed)
+        step(eager)
+        graph.replay()
+        graphed.sync()
+        for buf in bufs:
+            assert _bits_equal(graphed.download(buf), eager.download(buf)), (k, buf)
+        assert graphed.scaler_state() == eager.scaler_state(), k
+        assert graphed.step_count == eager.step_count, k
+        print(f"replay {k}: identical to the eager step (scale {eager.scaler_state()[0]})",
+              flush=True)
+    graph.close()
+    graphed.close()
+    eager.close()
+
+
 def test_captured_train_step_zero_accumulate_sgd_momentum():
     """The whole optimizer side of a training step in one graph: zero_grad, gradients
     accumulated from a device buffer the program rewrites between replays, SGD momentum
