@@ -66,17 +66,19 @@ def test_step_from_bucket_sums_matches_oracle_and_norm_pass(mode):
     twin.close()
 
 
-def test_bucket_sums_at_gpt2_124m_full_size():
-    """Config 3 at its real shapes (148 tensors, 124.4M params, bf16 gradients): loss scaling,
-    clipping and AdamW, the norm taken from bench.py's buckets (25 MB of gradients each, in
-    reverse tensor order), with an overflow at a seeded index on the second step.  Against the
-    oracle: the same skip / scale / step decisions, the norm within 1e-10 relative, the state
-    within 2 ulp."""
+@pytest.mark.parametrize("config,ntensors,nparams", [("gpt2_124m", 148, 124439808),
+                                                     ("gpt2_774m", 436, 774030080)])
+def test_bucket_sums_at_full_size(config, ntensors, nparams):
+    """Configs 3 and 4 at their real shapes (bf16 gradients; at 774M the update takes its lane
+    form): loss scaling, clipping and AdamW, the norm taken from bench.py's buckets (25 MB of
+    gradients each, in reverse tensor order), with an overflow at a seeded index on the second
+    step.  Against the oracle: the same skip / scale / step decisions, the norm within 1e-10
+    relative, the state within 2 ulp."""
     from ttperf import configs
     from ttperf import _lib as L
     torch = torch_mod()
-    _, shapes, decay, numels = configs.table("gpt2_124m")
-    assert len(shapes) == 148 and sum(numels) == 124439808
+    _, shapes, decay, numels = configs.table(config)
+    assert len(shapes) == ntensors and sum(numels) == nparams
     store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=132)
     store.configure_scaler(True, init_scale=65536.0)
     ref.configure_scaler(True, 65536.0)
@@ -93,7 +95,8 @@ def test_bucket_sums_at_gpt2_124m_full_size():
     hp = dict(lr=6e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
     gen = torch.Generator(device="cuda").manual_seed(133)
     for step in range(3):
-        inf_at = store.offsets[76] + 12345 if step == 1 else None  # h.6 attn.c_attn.weight
+        # a weight matrix in the middle of the table (GPT-2 124M: h.6 attn.c_attn.weight)
+        inf_at = store.offsets[ntensors // 2 + 2] + 12345 if step == 1 else None
         host = device_grads(store, gen, 1e-3, scale=ref.scale, inf_at=inf_at)
         ref.grad[:store.total] = host
         del host
