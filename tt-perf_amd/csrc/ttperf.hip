@@ -555,7 +555,8 @@ constexpr uint32_t kMaxGridBlocks = 1u << 22;
 // bytes; elements x lanes x pieces):
 //   Adam MIXED  1 x 256 x 2: 1.014-1.016 (1x128x2 1.01, 1x256x1 0.96-0.98, four-element 0.91)
 //   Adam FP32   1 x 128 x 2: 1.022-1.027 (1x256x2 1.01-1.02, 2x64x1 0.98, 2x64x2 0.89)
-//   SGD         2 x 128 x 1: MIXED 0.91, FP32 0.97-1.00 (2x128x2 0.96, 1x256x2 0.95)
+//   SGD         2 x 128 x 1: MIXED 0.90-0.91, FP32 0.97-1.00 (2x128x2 0.82 / 0.95, 1x256x2
+//                            0.90 / 0.92, four-element 0.88-0.90 / 0.98)
 constexpr int kLaneAdamMixed = 1, kLanesAdamMixed = 256, kItAdamMixed = 2;
 constexpr int kLaneAdamFp32 = 1, kLanesAdamFp32 = 128, kItAdamFp32 = 2;
 constexpr int kLaneSgd = 2, kLanesSgd = 128, kItSgd = 1;
