@@ -34,7 +34,8 @@
  * the stream.  A context is used by one host thread at a time.
  *
  * Environment, read at ttp_create (tuning only):
- *   TTP_UPD_BLOCKS_PER_CU  resident update blocks per CU (default 4; 0: no cap).  Results do not
+ *   TTP_UPD_BLOCKS_PER_CU  resident update blocks per CU for stores up to 256 MiB of gradients
+ *                          (default 4; 0: no cap; larger stores run uncapped).  Results do not
  *                          depend on it.
  *   TTP_NORM_GRID          blocks of each gradient-norm launch (default 8 x CUs, at most
  *                          65536; the pass is two launches above 256 MiB of gradients).  It
