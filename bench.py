@@ -344,6 +344,20 @@ def step_fn(store, optimizer, hp):
     return lambda: store.sgd_step(lr=hp["lr"], momentum=0.9, max_grad_norm=hp["max_grad_norm"])
 
 
+def update_kernel_name(optimizer, mode, total_elems):
+    """The update instantiation libttperf_hip launches for a store (its rocprof name): the
+    four-element kernel while the gradients fit the Infinity Cache, else the lane form with
+    its elements per lane, lanes per block and pieces per block (kLaneAdamMixed ... in
+    tt-perf_amd/csrc/ttperf.hip)."""
+    grad_t, mixed_t = ("unsigned short", "true") if mode == "mixed" else ("float", "false")
+    kname = "adam" if optimizer == "adamw" else "sgd"
+    if total_elems * (2 if mode == "mixed" else 4) <= CACHED_GRAD_BYTES:
+        return f"{kname}_kernel<{grad_t}, {mixed_t}>"
+    shape = {("adam", "mixed"): (1, 256, 2),
+             ("adam", "fp32"): (1, 128, 2)}.get((kname, mode), (2, 128, 1))
+    return f"{kname}_lane_kernel<{grad_t}, {mixed_t}, {shape[0]}, {shape[1]}, {shape[2]}>"
+
+
 def other_config(config, optimizer, steps, warmup):
     """One more configuration's step in a store of its own (created, timed, closed): K steps
     between one event pair, then K more with an event pair around every launch for the update
@@ -380,6 +394,7 @@ def other_config(config, optimizer, steps, warmup):
     upd_ms, upd_n = store.timing_collect(L.KERNEL_UPDATE)
     nrm_ms, nrm_n = store.timing_collect(L.KERNEL_NORM)
     store.timing(False)
+    upd_kernel = update_kernel_name(optimizer, mode, store.total)
     # with loss scaling: 20 overflow steps between one event pair (a +inf planted in the
     # first tensor's gradients), as for the headline configuration
     skip_ms = None
@@ -422,6 +437,7 @@ def other_config(config, optimizer, steps, warmup):
             "nt_copy64_GBps": round(nt_copy64_gbps, 1) if nt_copy64_gbps else None,
             "norm_pass_ms": round(nrm_ms / max(nrm_n, 1), 4),
             "skipped_step_ms": round(skip_ms, 4) if skip_ms is not None else None,
+            "update_kernel": upd_kernel,
             "params": n_params, "tensors": len(numels), "mode": mode,
             "steps": steps, "warmup": warmup}
 
@@ -555,17 +571,7 @@ def main():
         ceilings(stream, n_params * ub)
 
     achieved = n_params * ub / (upd_avg / 1e3) / 1e9
-    # the instantiation libttperf_hip launches (its rocprof name): the four-element kernel
-    # while the gradients fit the Infinity Cache, else the lane form with its elements per lane
-    grad_t, mixed_t = ("unsigned short", "true") if mode == "mixed" else ("float", "false")
-    grad_bytes = store_total * (2 if mode == "mixed" else 4)
-    kname = "adam" if args.optimizer == "adamw" else "sgd"
-    if grad_bytes <= CACHED_GRAD_BYTES:
-        upd_kernel = f"{kname}_kernel<{grad_t}, {mixed_t}>"
-    else:  # elements per lane, lanes per block, pieces per block (kLaneAdamMixed ... in ttperf.hip)
-        shape = {("adam", "mixed"): (1, 256, 2),
-                 ("adam", "fp32"): (1, 128, 2)}.get((kname, mode), (2, 128, 1))
-        upd_kernel = f"{kname}_lane_kernel<{grad_t}, {mixed_t}, {shape[0]}, {shape[1]}, {shape[2]}>"
+    upd_kernel = update_kernel_name(args.optimizer, mode, store_total)
     step_gbps = n_params * (ub + nb) / (ms_step / 1e3) / 1e9
     out = {
         "metric": HEADLINE if args.config == "gpt2_124m" and args.optimizer == "adamw" else
