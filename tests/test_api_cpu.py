@@ -305,3 +305,34 @@ def test_shard_tables_partition_the_flat_store():
     assert covered == dict(zip(names, numels))
     assert configs.table("gpt2_124m_shard8") == configs.shard_table("gpt2_124m", 8, 7)
     assert configs.mode("gpt2_124m_shard8") == "mixed"
+
+
+def test_bench_names_the_update_shapes_the_library_launches():
+    """bench.py reports the update instantiation it timed (its rocprof name); the shapes it
+    assumes for the lane forms must be the library's (ttperf.hip's kLane* constants) and its
+    Infinity Cache bound the library's kCachedGradBytes."""
+    src = open(os.path.join(REPO, "tt-perf_amd", "csrc", "ttperf.hip")).read()
+
+    def shape(name):
+        m = re.search(r"constexpr int kLane%s = (\d+), kLanes%s = (\d+), kIt%s = (\d+);"
+                      % (name, name, name), src)
+        assert m, name
+        return tuple(int(x) for x in m.groups())
+
+    m = re.search(r"constexpr uint64_t kCachedGradBytes = (\d+)ull << (\d+);", src)
+    assert m
+    bound = int(m.group(1)) << int(m.group(2))
+    sys.path.insert(0, REPO)
+    import bench
+    assert bench.CACHED_GRAD_BYTES == bound
+    big = 1 << 30
+    for (opt, mode, name, grad_t, mixed_t) in (
+            ("adamw", "mixed", "AdamMixed", "unsigned short", "true"),
+            ("adamw", "fp32", "AdamFp32", "float", "false"),
+            ("sgdm", "mixed", "Sgd", "unsigned short", "true"),
+            ("sgdm", "fp32", "Sgd", "float", "false")):
+        e, lanes, it = shape(name)
+        kname = "adam" if opt == "adamw" else "sgd"
+        assert bench.update_kernel_name(opt, mode, big) == \
+            f"{kname}_lane_kernel<{grad_t}, {mixed_t}, {e}, {lanes}, {it}>"
+        assert bench.update_kernel_name(opt, mode, 1 << 20) == f"{kname}_kernel<{grad_t}, {mixed_t}>"
