@@ -492,6 +492,51 @@ def test_lane_form_update_split_into_several_launches(mode, monkeypatch):
     store.close()
 
 
+@pytest.mark.parametrize("mode", ["mixed", "fp32"])
+def test_lane_form_with_many_small_tensors(mode):
+    """A store just over the 256 MiB bound made of one large tensor of odd length and 1500
+    small ones of 1..200 elements (most chunks hold less than one lane-form piece, many
+    blocks have nothing to do): AdamW with loss scaling and clipping, then SGD with Nesterov
+    momentum, against the oracle; the second Adam step on a subset of every third tensor."""
+    torch = torch_mod()
+    rng = np.random.default_rng(87)
+    big = (1 << 27) + 3 if mode == "mixed" else (1 << 26) + 5
+    small = [int(x) for x in rng.integers(1, 201, size=1500)]
+    shapes = [(big,)] + [(n,) for n in small]
+    decay = [True] + [bool(x) for x in rng.integers(0, 2, size=len(small))]
+    store, ref = make_pair(shapes, decay, O.MODE_MIXED if mode == "mixed" else O.MODE_FP32,
+                           seed=88)
+    store.configure_scaler(True, init_scale=4096.0)
+    ref.configure_scaler(True, 4096.0)
+    gen = torch.Generator(device="cuda").manual_seed(89)
+    adam = dict(lr=1e-3, betas=(0.9, 0.99), eps=1e-8, weight_decay=0.05, max_grad_norm=0.5)
+    subset = list(range(0, len(shapes), 3))
+    for step, sub in enumerate((None, subset)):
+        host = device_grads(store, gen, 1e-3, scale=ref.scale)
+        ref.grad[:] = host
+        for i in range(ref.n):
+            ref.set_has_grad(i, sub is None or i in sub)
+        r = store.adam_step(report=True, indices=sub, **adam)
+        e = ref.adam_step(**adam)
+        assert r["skipped"] == e["skipped"] and r["step"] == e["step"]
+        assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
+        print(f"{mode} adamw step {step}: norm {r['grad_norm']:.6f}", flush=True)
+    slots = ("master", "exp_avg", "exp_avg_sq") + (("param",) if mode == "mixed" else ())
+    compare_state(store, ref, which=slots, max_ulp=2)
+    sgd = dict(lr=1e-2, momentum=0.9, nesterov=True, max_grad_norm=0.5)
+    for step in range(2):
+        host = device_grads(store, gen, 1e-3, scale=ref.scale)
+        ref.grad[:] = host
+        for i in range(ref.n):
+            ref.set_has_grad(i, True)
+        r = store.sgd_step(report=True, **sgd)
+        e = ref.sgd_step(**sgd)
+        assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
+    compare_state(store, ref, which=("master", "momentum") + (("param",) if mode == "mixed" else ()),
+                  max_ulp=2)
+    store.close()
+
+
 def test_zero1_shard_step_matches_oracle():
     """One GPU's ZeRO-1 shard of GPT-2 124M (the last of 8: 28 pieces of tensors, 15.6M
     params) stepped with config 3's mixed AdamW, loss scaling and clipping; against the oracle.
