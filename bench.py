@@ -353,8 +353,8 @@ def update_kernel_name(optimizer, mode, total_elems):
     kname = "adam" if optimizer == "adamw" else "sgd"
     if total_elems * (2 if mode == "mixed" else 4) <= CACHED_GRAD_BYTES:
         return f"{kname}_kernel<{grad_t}, {mixed_t}>"
-    shape = {("adam", "mixed"): (1, 256, 2),
-             ("adam", "fp32"): (1, 128, 2)}.get((kname, mode), (2, 128, 1))
+    shape = {("adam", "mixed"): (1, 256, 2), ("adam", "fp32"): (1, 128, 2),
+             ("sgd", "mixed"): (1, 256, 2), ("sgd", "fp32"): (2, 64, 1)}[(kname, mode)]
     return f"{kname}_lane_kernel<{grad_t}, {mixed_t}, {shape[0]}, {shape[1]}, {shape[2]}>"
 
 

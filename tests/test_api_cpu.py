@@ -329,8 +329,8 @@ def test_bench_names_the_update_shapes_the_library_launches():
     for (opt, mode, name, grad_t, mixed_t) in (
             ("adamw", "mixed", "AdamMixed", "unsigned short", "true"),
             ("adamw", "fp32", "AdamFp32", "float", "false"),
-            ("sgdm", "mixed", "Sgd", "unsigned short", "true"),
-            ("sgdm", "fp32", "Sgd", "float", "false")):
+            ("sgdm", "mixed", "SgdMixed", "unsigned short", "true"),
+            ("sgdm", "fp32", "SgdFp32", "float", "false")):
         e, lanes, it = shape(name)
         kname = "adam" if opt == "adamw" else "sgd"
         assert bench.update_kernel_name(opt, mode, big) == \

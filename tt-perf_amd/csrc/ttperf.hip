@@ -555,11 +555,16 @@ constexpr uint32_t kMaxGridBlocks = 1u << 22;
 // bytes; elements x lanes x pieces):
 //   Adam MIXED  1 x 256 x 2: 1.014-1.016 (1x128x2 1.01, 1x256x1 0.96-0.98, four-element 0.91)
 //   Adam FP32   1 x 128 x 2: 1.022-1.027 (1x256x2 1.01-1.02, 2x64x1 0.98, 2x64x2 0.89)
-//   SGD         2 x 128 x 1: MIXED 0.90-0.91, FP32 0.97-1.00 (2x128x2 0.82 / 0.95, 1x256x2
-//                            0.90 / 0.92, four-element 0.88-0.90 / 0.98)
+//   SGD MIXED   1 x 256 x 2: 0.923-0.926 (slower by: 2x128x1 0.4-1.1%, 1x128x2 0.4-0.6%,
+//                            2x256x1 3.3%, 2x64x1 3.7%, 1x256x1 14%)
+//   SGD FP32    2 x 64 x 1:  1.001-1.026 (slower by: 2x128x1 0.8-2.8%, 1x128x2 3.1-3.3%,
+//                            1x64x2 3.6%, 1x256x2 3.7-5.6%, 2x64x2 9%, 1x64x1 27%)
+// (SGD with momentum; each variant a build of its own, timed in turn on the same box, two
+// boxes per mode.)
 constexpr int kLaneAdamMixed = 1, kLanesAdamMixed = 256, kItAdamMixed = 2;
 constexpr int kLaneAdamFp32 = 1, kLanesAdamFp32 = 128, kItAdamFp32 = 2;
-constexpr int kLaneSgd = 2, kLanesSgd = 128, kItSgd = 1;
+constexpr int kLaneSgdMixed = 1, kLanesSgdMixed = 256, kItSgdMixed = 2;
+constexpr int kLaneSgdFp32 = 2, kLanesSgdFp32 = 64, kItSgdFp32 = 1;
 
 // One launch holds at most 2^32 - 1 work-items, so at most (2^32 - 1) / lanes blocks.  A
 // lane-form update over more parts is split into launches at increasing part offsets
@@ -1503,7 +1508,6 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
         uint16_t* p16 = (uint16_t*)c->param;
         ttp::SgdArgs al = a;
         al.st = c->st;  // the lane forms read the device state unconditionally
-        const uint64_t nparts = (uint64_t)n * ttp::lane_parts<kLaneSgd, kLanesSgd, kItSgd>();
         clear_hip_error();
         if (grads_cached(c, w) && c->mode == TTP_MODE_MIXED)
             hipLaunchKernelGGL((ttp::sgd_kernel<uint16_t, true>), dim3(n), block, c->upd_lds,
@@ -1512,16 +1516,23 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
             hipLaunchKernelGGL((ttp::sgd_kernel<float, false>), dim3(n), block, c->upd_lds,
                                c->stream, g32, c->master, c->momentum, (uint16_t*)nullptr, a);
         else if (c->mode == TTP_MODE_MIXED)
-            launch_lanes(c, nparts, kLanesSgd, [&](dim3 g, uint64_t p0) {
-                hipLaunchKernelGGL((ttp::sgd_lane_kernel<uint16_t, true, kLaneSgd, kLanesSgd, kItSgd>), g,
-                                   dim3(kLanesSgd), 0, c->stream, g16, c->master, c->momentum,
-                                   p16, al, p0);
+            launch_lanes(c,
+                         (uint64_t)n *
+                             ttp::lane_parts<kLaneSgdMixed, kLanesSgdMixed, kItSgdMixed>(),
+                         kLanesSgdMixed, [&](dim3 g, uint64_t p0) {
+                hipLaunchKernelGGL(
+                    (ttp::sgd_lane_kernel<uint16_t, true, kLaneSgdMixed, kLanesSgdMixed,
+                                          kItSgdMixed>), g,
+                    dim3(kLanesSgdMixed), 0, c->stream, g16, c->master, c->momentum, p16, al, p0);
             });
         else
-            launch_lanes(c, nparts, kLanesSgd, [&](dim3 g, uint64_t p0) {
-                hipLaunchKernelGGL((ttp::sgd_lane_kernel<float, false, kLaneSgd, kLanesSgd, kItSgd>), g,
-                                   dim3(kLanesSgd), 0, c->stream, g32, c->master, c->momentum,
-                                   (uint16_t*)nullptr, al, p0);
+            launch_lanes(c,
+                         (uint64_t)n * ttp::lane_parts<kLaneSgdFp32, kLanesSgdFp32, kItSgdFp32>(),
+                         kLanesSgdFp32, [&](dim3 g, uint64_t p0) {
+                hipLaunchKernelGGL(
+                    (ttp::sgd_lane_kernel<float, false, kLaneSgdFp32, kLanesSgdFp32, kItSgdFp32>),
+                    g, dim3(kLanesSgdFp32), 0, c->stream, g32, c->master, c->momentum,
+                    (uint16_t*)nullptr, al, p0);
             });
         HIP_TRY(hipGetLastError());
         tl.done();
