@@ -538,9 +538,12 @@ int set_dev(const ttp_ctx* c) {
     return TTP_OK;
 }
 
-// whether an update over `w` runs the four-element kernels (see kCachedGradBytes)
+// whether an update over `w` runs the four-element kernels (see kCachedGradBytes).  Those
+// launch one 256-lane block per chunk in one launch, which holds at most 2^32 - 1 work-items;
+// a set of that many chunks (millions of tiny tensors) takes the lane forms, which split.
 bool grads_cached(const ttp_ctx* c, const WorkTables* w) {
-    return w->elems * grad_esize(c) <= kCachedGradBytes;
+    return w->elems * grad_esize(c) <= kCachedGradBytes &&
+           w->n_chunks <= 0xFFFFFFFFu / ttp::kUpdBlock;
 }
 
 // Largest grid of the grid-stride chunk kernels (gradient zeroing): 2^22 blocks of 256 lanes is
