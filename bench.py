@@ -7,12 +7,13 @@ One step = the norm/inf-check/scaler pass + the fused multi-tensor AdamW pass ov
 synthetic N(0, 1e-3) x scale bf16 gradients already resident in HBM.
 
 Prints ONE JSON line: Gparams/s and ms/step of the timed region (K steps between one event
-pair), the roofline of the dominant (update) kernel from HIP events recorded around each of
-its launches on the kernel's stream during a second pass of K steps, and the CPU oracle
-baseline timed on this host's cores on a bounded sample.  Beside the headline: the step
-with a cold Infinity Cache (512 MB of unrelated reads before each step, outside its event
-pair), the mean skipped (overflow) step, and the other large configurations' steps
-(GPT-2 774M mixed AdamW, GPT-2 XL fp32 AdamW and SGD momentum), each in a store of its own.
+pair, after --settle-ms of untimed steps and then W warmup steps), the roofline of the
+dominant (update) kernel from HIP events recorded around each of its launches on the
+kernel's stream during a second pass of K steps, and the CPU oracle baseline timed on this
+host's cores on a bounded sample.  Beside the headline: the step with a cold Infinity Cache
+(512 MB of unrelated reads before each step, outside its event pair), the mean skipped
+(overflow) step, and the other configurations' steps (the MLP, nanoGPT-char, GPT-2 774M
+mixed AdamW, GPT-2 XL fp32 AdamW and SGD momentum), each in a store of its own.
 """
 import argparse
 import ctypes
@@ -80,7 +81,32 @@ def parse():
                          "eager launches on MI355X, so eager is the default)")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the GPT-2 774M and XL steps timed after the headline")
+    ap.add_argument("--settle-ms", type=float, default=200.0,
+                    help="run the step back to back for this long before the W warmup steps "
+                         "(0: not at all); see settle() ")
     return ap.parse_args()
+
+
+def settle(step, ms):
+    """Run `step` back to back, in batches of 20 with a synchronisation after each, for at
+    least `ms` milliseconds; returns (steps, ms).  After an idle phase (process start, store
+    set-up) MI355X runs its first tens of milliseconds of work at lower clocks: the busy-cycle
+    counter of the GPT-2 124M update read 17 cycles/ns at first and 19 after about 15 ms, and
+    20 steps timed after 5 warmup steps ran 0.571 ms (four-element update) and 0.59-0.61 ms
+    (lane form) against 0.560 and 0.553-0.557 ms after 50 ms or more of steps.  A training
+    loop keeps the GPU busy between its steps, so the step is timed at those clocks.  The
+    settle steps are not timed and precede the W warmup steps."""
+    import torch
+
+    n, t0 = 0, time.perf_counter()
+    while ms > 0:
+        for _ in range(20):
+            step()
+        torch.cuda.synchronize()
+        n += 20
+        if (time.perf_counter() - t0) * 1e3 >= ms:
+            break
+    return n, round((time.perf_counter() - t0) * 1e3, 1)
 
 
 def traffic_from_profiles(config):
@@ -345,23 +371,25 @@ def step_fn(store, optimizer, hp):
 
 
 def update_kernel_name(optimizer, mode, total_elems):
-    """The update instantiation libttperf_hip launches for a store (its rocprof name): the
-    four-element kernel while the gradients fit the Infinity Cache, else the lane form with
-    its elements per lane, lanes per block and pieces per block (kLaneAdamMixed ... in
-    tt-perf_amd/csrc/ttperf.hip)."""
+    """The update instantiation libttperf_hip launches for a store (its rocprof name): while
+    the gradients fit the Infinity Cache, the lane form of kLaneAdamMixedCached for MIXED Adam
+    and the four-element kernel otherwise; beyond, the lane form with its elements per lane,
+    lanes per block and pieces per block (kLaneAdamMixed ... in tt-perf_amd/csrc/ttperf.hip)."""
     grad_t, mixed_t = ("unsigned short", "true") if mode == "mixed" else ("float", "false")
     kname = "adam" if optimizer == "adamw" else "sgd"
     if total_elems * (2 if mode == "mixed" else 4) <= CACHED_GRAD_BYTES:
+        if kname == "adam" and mode == "mixed":
+            return f"adam_lane_kernel<{grad_t}, {mixed_t}, 1, 128, 2>"
         return f"{kname}_kernel<{grad_t}, {mixed_t}>"
     shape = {("adam", "mixed"): (1, 256, 2), ("adam", "fp32"): (1, 128, 2),
              ("sgd", "mixed"): (1, 256, 2), ("sgd", "fp32"): (2, 64, 1)}[(kname, mode)]
     return f"{kname}_lane_kernel<{grad_t}, {mixed_t}, {shape[0]}, {shape[1]}, {shape[2]}>"
 
 
-def other_config(config, optimizer, steps, warmup):
-    """One more configuration's step in a store of its own (created, timed, closed): K steps
-    between one event pair, then K more with an event pair around every launch for the update
-    kernel's own time.  Returns the JSON object."""
+def other_config(config, optimizer, steps, warmup, settle_ms):
+    """One more configuration's step in a store of its own (created, timed, closed): settle
+    steps and W warmup steps, K steps between one event pair, then K more with an event pair
+    around every launch for the update kernel's own time.  Returns the JSON object."""
     import torch
     from ttperf import _lib as L
     from ttperf import configs
@@ -375,6 +403,7 @@ def other_config(config, optimizer, steps, warmup):
     del g
     torch.cuda.empty_cache()
     step = step_fn(store, optimizer, hp)
+    settle(step, settle_ms)
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -474,12 +503,13 @@ def main():
 
     step = step_fn(store, args.optimizer, hp)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
     r = store.adam_step(report=True, **hp) if args.optimizer == "adamw" else None
     if r is not None:
         assert not r["skipped"], r
+    settle_n, settle_ms = settle(step, args.settle_ms)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
 
     # the step as a hipGraph (the reference's trace capture/replay): one capture, K replays
     run = step
@@ -605,6 +635,10 @@ def main():
         "step_hbm_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
         "kernels_ms": {"norm_pass": round(nrm_avg, 4), "update": round(upd_avg, 4),
                        "source": "second pass of K steps with an event pair per launch"},
+        "settle": {"steps": settle_n, "ms": settle_ms,
+                   "note": "untimed steps run back to back before the W warmup steps, so that "
+                           "the timed steps see the clocks of a busy GPU, as in a training loop "
+                           "(the first tens of ms after an idle phase run at lower clocks)"},
         "cold_ms_per_step": round(cold_ms, 4),
         "cold_Gparams_per_s": round(n_params / (cold_ms / 1e3) / 1e9, 3),
         "cold_note": "each step after a 512 MB read of unrelated data on its stream (outside "
@@ -637,21 +671,20 @@ def main():
     torch.cuda.empty_cache()
     if not args.no_other_configs and args.config == "gpt2_124m" and args.optimizer == "adamw":
         # the other large configurations, one store at a time (GPT-2 XL fp32 holds 31 GB)
+        legs = (("mlp_fp32_adam", "mlp", "adamw"),
+                ("nanogpt_char_mixed_adamw", "nanogpt_char", "adamw"),
+                ("gpt2_774m_mixed_adamw", "gpt2_774m", "adamw"),
+                ("gpt2_1558m_fp32_adamw", "gpt2_1558m", "adamw"),
+                ("gpt2_1558m_fp32_sgdm", "gpt2_1558m", "sgdm"))
         out["other_configs"] = {
-            "mlp_fp32_adam": other_config("mlp", "adamw", args.steps, args.warmup),
-            "nanogpt_char_mixed_adamw": other_config("nanogpt_char", "adamw", args.steps,
-                                                     args.warmup),
-            "gpt2_774m_mixed_adamw": other_config("gpt2_774m", "adamw", args.steps,
-                                                  args.warmup),
-            "gpt2_1558m_fp32_adamw": other_config("gpt2_1558m", "adamw", args.steps,
-                                                  args.warmup),
-            "gpt2_1558m_fp32_sgdm": other_config("gpt2_1558m", "sgdm", args.steps,
-                                                 args.warmup),
-            "note": "each in a store of its own, created, timed (K steps between one event "
-                    "pair; the update alone from a second pass with an event pair per launch) "
-                    "and closed before the next; no CPU leg; the copy ceilings only where the "
-                    "update moves at least 1 GiB (the MLP's 269 KB step is launch-bound and "
-                    "the char model's 323 MB mostly Infinity-Cache resident)"}
+            key: other_config(config, opt, args.steps, args.warmup, args.settle_ms)
+            for key, config, opt in legs}
+        out["other_configs"]["note"] = (
+            "each in a store of its own, created, timed (settle steps and W warmup steps, then "
+            "K steps between one event pair; the update alone from a second pass with an event "
+            "pair per launch) and closed before the next; no CPU leg; the copy ceilings only "
+            "where the update moves at least 1 GiB (the MLP's 269 KB step is launch-bound and "
+            "the char model's 323 MB mostly Infinity-Cache resident)")
     if grads_host is not None:
         log("bench: timing the CPU oracle baseline ...")
         out["cpu_baseline"] = cpu_baseline(numels, [1 if d else 0 for d in decay],

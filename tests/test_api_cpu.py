@@ -307,6 +307,30 @@ def test_shard_tables_partition_the_flat_store():
     assert configs.mode("gpt2_124m_shard8") == "mixed"
 
 
+def test_bench_calls_match_its_function_signatures():
+    """Every call in bench.py of one of its own functions passes as many positional arguments
+    as the function takes without defaults, at most as many as it takes in all, and only
+    keywords it names (a mismatch would surface only on the GPU box, after minutes of
+    timing)."""
+    import ast
+    tree = ast.parse(open(os.path.join(REPO, "bench.py")).read())
+    defs = {f.name: f for f in tree.body if isinstance(f, ast.FunctionDef)}
+    calls = 0
+    for node in ast.walk(tree):
+        if not (isinstance(node, ast.Call) and isinstance(node.func, ast.Name)
+                and node.func.id in defs):
+            continue
+        a = defs[node.func.id].args
+        names = [x.arg for x in a.args]
+        required = len(names) - len(a.defaults)
+        given = len(node.args) + sum(1 for k in node.keywords if k.arg in names[len(node.args):])
+        assert given >= required, (node.func.id, node.lineno)
+        assert len(node.args) <= len(names) or a.vararg, (node.func.id, node.lineno)
+        assert all(k.arg in names or a.kwarg for k in node.keywords), (node.func.id, node.lineno)
+        calls += 1
+    assert calls >= 10
+
+
 def test_bench_names_the_update_shapes_the_library_launches():
     """bench.py reports the update instantiation it timed (its rocprof name); the shapes it
     assumes for the lane forms must be the library's (ttperf.hip's kLane* constants) and its
@@ -335,4 +359,10 @@ def test_bench_names_the_update_shapes_the_library_launches():
         kname = "adam" if opt == "adamw" else "sgd"
         assert bench.update_kernel_name(opt, mode, big) == \
             f"{kname}_lane_kernel<{grad_t}, {mixed_t}, {e}, {lanes}, {it}>"
-        assert bench.update_kernel_name(opt, mode, 1 << 20) == f"{kname}_kernel<{grad_t}, {mixed_t}>"
+        if name == "AdamMixed":  # MIXED Adam takes a lane form below the bound too
+            e, lanes, it = shape("AdamMixedCached")
+            assert bench.update_kernel_name(opt, mode, 1 << 20) == \
+                f"adam_lane_kernel<{grad_t}, {mixed_t}, {e}, {lanes}, {it}>"
+        else:
+            assert bench.update_kernel_name(opt, mode, 1 << 20) == \
+                f"{kname}_kernel<{grad_t}, {mixed_t}>"

@@ -398,13 +398,13 @@ def test_cfg5_gpt2_xl_fp32_adamw_then_sgd_momentum():
 
 @pytest.mark.parametrize("mode", ["mixed", "fp32"])
 def test_update_forms_on_both_sides_of_the_cached_gradient_bound(mode):
-    """The update kernels have two forms, chosen by the stepped set's gradient bytes: four
-    elements per lane up to 256 MiB, the lane forms (one or two elements per lane) beyond.
-    SGD with momentum and dampening, then AdamW, on a store just over the bound, each against
-    the oracle: the whole store and a subset that stays over it (lane forms with inactive
-    tensors between and after the active ones), then a subset under it (four-element form).
-    The FP32 store's first tensor has an odd element count, so the two-element lanes end on a
-    lone element."""
+    """The update kernels take their form from the stepped set's gradient bytes: up to 256 MiB
+    the four-element kernels (FP32 Adam, SGD) or MIXED Adam's 128-lane form, beyond that the
+    lane forms (one or two elements per lane).  SGD with momentum and dampening, then AdamW,
+    on a store just over the bound, each against the oracle: the whole store and a subset that
+    stays over it (lane forms with inactive tensors between and after the active ones), then
+    a subset under it.  The FP32 store's first tensor has an odd element count, so the
+    two-element lanes end on a lone element."""
     torch = torch_mod()
     if mode == "mixed":
         shapes = [(50257, 768), (8192, 8192), (7000, 5000), (768,), (3,)]  # 140.7M params
@@ -428,7 +428,8 @@ def test_update_forms_on_both_sides_of_the_cached_gradient_bound(mode):
     adam = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
     slots = ("master", "param", "momentum") if mode == "mixed" else ("master", "momentum")
     adam_slots = ("master", "exp_avg", "exp_avg_sq") + (("param",) if mode == "mixed" else ())
-    for label, subset in zip(("whole store", "lane-form subset", "four-element subset"), subsets):
+    for label, subset in zip(("whole store", "lane-form subset", "cached-gradient subset"),
+                             subsets):
         for step in range(2):
             host = device_grads(store, gen, 1e-3)
             ref.grad[:] = host
@@ -458,7 +459,8 @@ def test_lane_form_update_split_into_several_launches(mode, monkeypatch):
     at increasing part offsets.  TTP_LANE_LAUNCH_BLOCKS (read at ttp_create) lowers that limit
     to 4099 blocks, so that a store just over the 256 MiB bound takes dozens of launches, whose
     boundaries fall inside chunks and tensors; SGD with momentum and AdamW on the whole store
-    and on a subset, against the oracle."""
+    and on a subset, against the oracle.  In mixed precision also a subset under the bound,
+    which MIXED Adam steps in its 128-lane form (37 launches)."""
     torch = torch_mod()
     monkeypatch.setenv("TTP_LANE_LAUNCH_BLOCKS", "4099")
     if mode == "mixed":
@@ -476,7 +478,10 @@ def test_lane_form_update_split_into_several_launches(mode, monkeypatch):
     adam = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
     slots = ("master", "param", "momentum") if mode == "mixed" else ("master", "momentum")
     adam_slots = ("master", "exp_avg", "exp_avg_sq") + (("param",) if mode == "mixed" else ())
-    for label, sub in (("whole store", None), ("subset", subset)):
+    legs = [("whole store", None), ("subset", subset)]
+    if mode == "mixed":
+        legs.append(("cached-gradient subset", [0, 3, 4]))
+    for label, sub in legs:
         for name, hp in (("sgd-m", sgd), ("adamw", adam)):
             host = device_grads(store, gen, 1e-3)
             ref.grad[:] = host

@@ -98,12 +98,10 @@ struct WorkTables {
     uint32_t n_tensors = 0;
 };
 
-// Gradient bytes up to which an update runs the four-element kernels: MI355X's Infinity Cache
-// (256 MB) still holds most of the gradients after the norm pass or the backward that wrote
-// them, and that form reads them fastest (GPT-2 124M, 249 MB of bf16 grads: 0.99-1.00x a
-// plain copy of the same bytes, against 0.97-0.99x for the one-element lane form).  Larger
-// stores take the lane forms (see kLaneAdamMixed).  The norm pass reads about this many bytes
-// of the last tiles with cached loads, the rest non-temporal (see NormSplit).
+// Gradient bytes up to which MI355X's Infinity Cache (256 MB) still holds most of the
+// gradients after the norm pass or the backward that wrote them.  The update's form is chosen
+// on each side of it (see kLaneAdamMixed), and the norm pass reads about this many bytes of
+// the last tiles with cached loads, the rest non-temporal (see NormSplit).
 constexpr uint64_t kCachedGradBytes = 256ull << 20;
 
 }  // namespace
@@ -538,9 +536,11 @@ int set_dev(const ttp_ctx* c) {
     return TTP_OK;
 }
 
-// whether an update over `w` runs the four-element kernels (see kCachedGradBytes).  Those
-// launch one 256-lane block per chunk in one launch, which holds at most 2^32 - 1 work-items;
-// a set of that many chunks (millions of tiny tensors) takes the lane forms, which split.
+// whether the gradients of an update over `w` fit the Infinity Cache (see kCachedGradBytes):
+// FP32 Adam and SGD then run the four-element kernels, MIXED Adam its cached-gradient lane
+// shape.  The four-element kernels launch one 256-lane block per chunk in one launch, which
+// holds at most 2^32 - 1 work-items; a set of that many chunks (millions of tiny tensors)
+// counts as not cached and takes the lane forms, which split.
 bool grads_cached(const ttp_ctx* c, const WorkTables* w) {
     return w->elems * grad_esize(c) <= kCachedGradBytes &&
            w->n_chunks <= 0xFFFFFFFFu / ttp::kUpdBlock;
@@ -550,12 +550,23 @@ bool grads_cached(const ttp_ctx* c, const WorkTables* w) {
 // 2^30 work-items, well inside the 2^32 a launch may hold; they loop over the rest.
 constexpr uint32_t kMaxGridBlocks = 1u << 22;
 
-// Updates whose gradients fit the Infinity Cache run the four-element kernels, one block per
-// chunk (at most 2^17 chunks); larger ones the lane forms: kE elements per lane in blocks of
-// kLanes, each block walking kIt consecutive pieces of kLanes x kE elements, one block per
-// 1/lane_parts<kE, kLanes, kIt>() of a chunk.  Each shape is the fastest measured at GPT-2
-// 774M mixed / 1558M fp32 (interleaved rounds, x a 256-lane non-temporal copy of the same
-// bytes; elements x lanes x pieces):
+// FP32 Adam and SGD updates whose gradients fit the Infinity Cache run the four-element
+// kernels, one block per chunk (at most 2^17 chunks); MIXED Adam at any size, and the others
+// beyond the cache, the lane forms: kE elements per lane in blocks of kLanes, each block
+// walking kIt consecutive pieces of kLanes x kE elements, one block per
+// 1/lane_parts<kE, kLanes, kIt>() of a chunk.
+// MIXED Adam with cached gradients (GPT-2 124M; whole steps of bench.py after its settle
+// phase, 5 warmup + 20 timed steps, three interleaved rounds on one box; four-element /
+// 1 x 128 x 2 / 1 x 256 x 2):
+//   back-to-back step       0.5589-0.5597 / 0.5519-0.5547 / 0.5602-0.5621 ms
+//   update kernel alone     0.5222-0.5225 / 0.5123-0.5141 / 0.5195-0.5220 ms
+//   249 MB gradient copy + step (a backward rewrites the gradients just before the step;
+//   400 steps, 3 rounds, 2 processes)  0.660-0.662 / 0.631-0.632 / 0.633-0.634 ms
+//   skipped step            0.069 / 0.148 / 0.096 ms (the early exit of every block)
+//   nanoGPT-char (10.8M)    0.0543-0.0551 / 0.0544-0.0547 / 0.0556 ms
+// The four-element form wins only the rare skipped step.  Beyond the cache the shapes are
+// the fastest measured at GPT-2 774M mixed / 1558M fp32 (interleaved rounds, x a 256-lane
+// non-temporal copy of the same bytes; elements x lanes x pieces):
 //   Adam MIXED  1 x 256 x 2: 1.014-1.016 (1x128x2 1.01, 1x256x1 0.96-0.98, four-element 0.91)
 //   Adam FP32   1 x 128 x 2: 1.022-1.027 (1x256x2 1.01-1.02, 2x64x1 0.98, 2x64x2 0.89)
 //   SGD MIXED   1 x 256 x 2: 0.923-0.926 (slower by: 2x128x1 0.4-1.1%, 1x128x2 0.4-0.6%,
@@ -563,7 +574,10 @@ constexpr uint32_t kMaxGridBlocks = 1u << 22;
 //   SGD FP32    2 x 64 x 1:  1.001-1.026 (slower by: 2x128x1 0.8-2.8%, 1x128x2 3.1-3.3%,
 //                            1x64x2 3.6%, 1x256x2 3.7-5.6%, 2x64x2 9%, 1x64x1 27%)
 // (SGD with momentum; each variant a build of its own, timed in turn on the same box, two
-// boxes per mode.)
+// boxes per mode.)  At 774M the 1 x 128 x 2 shape ties 1 x 256 x 2 on clean steps, back to
+// back and after a gradient copy (3.476 against 3.472 ms, 4.095 against 4.089 ms), and
+// dispatches twice the workgroups on a skipped step.
+constexpr int kLaneAdamMixedCached = 1, kLanesAdamMixedCached = 128, kItAdamMixedCached = 2;
 constexpr int kLaneAdamMixed = 1, kLanesAdamMixed = 256, kItAdamMixed = 2;
 constexpr int kLaneAdamFp32 = 1, kLanesAdamFp32 = 128, kItAdamFp32 = 2;
 constexpr int kLaneSgdMixed = 1, kLanesSgdMixed = 256, kItSgdMixed = 2;
@@ -1420,8 +1434,16 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
         al.st = c->st;  // the lane forms read the device state unconditionally
         clear_hip_error();
         if (grads_cached(c, w) && c->mode == TTP_MODE_MIXED)
-            hipLaunchKernelGGL((ttp::adam_kernel<uint16_t, true>), dim3(n), block, c->upd_lds,
-                               c->stream, g16, c->master, c->exp_avg, c->exp_avg_sq, p16, a);
+            launch_lanes(c,
+                         (uint64_t)n * ttp::lane_parts<kLaneAdamMixedCached, kLanesAdamMixedCached,
+                                                       kItAdamMixedCached>(),
+                         kLanesAdamMixedCached, [&](dim3 g, uint64_t p0) {
+                hipLaunchKernelGGL(
+                    (ttp::adam_lane_kernel<uint16_t, true, kLaneAdamMixedCached,
+                                           kLanesAdamMixedCached, kItAdamMixedCached>), g,
+                    dim3(kLanesAdamMixedCached), 0, c->stream, g16, c->records, (float*)nullptr,
+                    p16, al, p0);
+            });
         else if (grads_cached(c, w))
             hipLaunchKernelGGL((ttp::adam_kernel<float, false>), dim3(n), block, c->upd_lds,
                                c->stream, g32, c->master, c->exp_avg, c->exp_avg_sq,
