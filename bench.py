@@ -403,7 +403,7 @@ def other_config(config, optimizer, steps, warmup, settle_ms):
     del g
     torch.cuda.empty_cache()
     step = step_fn(store, optimizer, hp)
-    settle(step, settle_ms)
+    settle_n, _ = settle(step, settle_ms)
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -468,7 +468,7 @@ def other_config(config, optimizer, steps, warmup, settle_ms):
             "skipped_step_ms": round(skip_ms, 4) if skip_ms is not None else None,
             "update_kernel": upd_kernel,
             "params": n_params, "tensors": len(numels), "mode": mode,
-            "steps": steps, "warmup": warmup}
+            "steps": steps, "warmup": warmup, "settle_steps": settle_n}
 
 
 def main():
