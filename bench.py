@@ -568,6 +568,28 @@ def main():
     cold_ms = sum(a.elapsed_time(b) for a, b in cold) / args.steps
     del flush, sink
 
+    # the step right after its gradients were rewritten, as a backward leaves them: K times a
+    # device copy of the gradients from a second buffer, then the step, between one event pair;
+    # then the K copies alone
+    gview = store.torch_view(L.BUF_GRAD)
+    backup = gview.clone()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for _ in range(args.steps):
+            gview.copy_(backup)
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        pair_ms = e0.elapsed_time(e1) / args.steps
+        e0.record(stream)
+        for _ in range(args.steps):
+            gview.copy_(backup)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        gcopy_ms = e0.elapsed_time(e1) / args.steps
+    del gview, backup
+
     # skipped (overflow) steps: only the norm pass and the finalize do work; K of them
     # between one event pair (each backs the loss scale off; it is reset afterwards)
     skip_ms = None
@@ -643,6 +665,13 @@ def main():
         "cold_Gparams_per_s": round(n_params / (cold_ms / 1e3) / 1e9, 3),
         "cold_note": "each step after a 512 MB read of unrelated data on its stream (outside "
                      "its event pair), so no gradient is left in the 256 MB Infinity Cache",
+        "after_grad_write": {
+            "pair_ms": round(pair_ms, 4), "grad_copy_ms": round(gcopy_ms, 4),
+            "step_ms": round(pair_ms - gcopy_ms, 4),
+            "Gparams_per_s": round(n_params / ((pair_ms - gcopy_ms) / 1e3) / 1e9, 3),
+            "note": "K times a device copy of the gradients from a second buffer (as a backward "
+                    "writes them) then the step, between one event pair (pair_ms); the copies "
+                    "alone (grad_copy_ms); step_ms is the difference"},
         "skipped_step_ms": round(skip_ms, 4) if skip_ms is not None else None,
         "skipped_step_note": "mean of 20 overflow steps between one event pair",
         "bucketed_norm": sums,
