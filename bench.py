@@ -371,16 +371,16 @@ def step_fn(store, optimizer, hp):
 
 
 def update_kernel_name(optimizer, mode, total_elems):
-    """The update instantiation libttperf_hip launches for a store (its rocprof name): while
-    the gradients fit the Infinity Cache, the lane form of kLaneAdamMixedCached for MIXED Adam
-    and the four-element kernel otherwise; beyond, the lane form with its elements per lane,
-    lanes per block and pieces per block (kLaneAdamMixed ... in tt-perf_amd/csrc/ttperf.hip)."""
+    """The update instantiation libttperf_hip launches for a store (its rocprof name): the lane
+    form with its elements per lane, lanes per block and pieces per block (kLaneAdamMixed ...
+    in tt-perf_amd/csrc/ttperf.hip), except while the gradients fit the Infinity Cache: MIXED
+    Adam then takes the kLaneAdamMixedCached shape, and MIXED SGD the four-element kernel."""
     grad_t, mixed_t = ("unsigned short", "true") if mode == "mixed" else ("float", "false")
     kname = "adam" if optimizer == "adamw" else "sgd"
-    if total_elems * (2 if mode == "mixed" else 4) <= CACHED_GRAD_BYTES:
-        if kname == "adam" and mode == "mixed":
+    if mode == "mixed" and total_elems * 2 <= CACHED_GRAD_BYTES:
+        if kname == "adam":
             return f"adam_lane_kernel<{grad_t}, {mixed_t}, 1, 128, 2>"
-        return f"{kname}_kernel<{grad_t}, {mixed_t}>"
+        return f"sgd_kernel<{grad_t}, {mixed_t}>"
     shape = {("adam", "mixed"): (1, 256, 2), ("adam", "fp32"): (1, 128, 2),
              ("sgd", "mixed"): (1, 256, 2), ("sgd", "fp32"): (2, 64, 1)}[(kname, mode)]
     return f"{kname}_lane_kernel<{grad_t}, {mixed_t}, {shape[0]}, {shape[1]}, {shape[2]}>"

@@ -359,10 +359,14 @@ def test_bench_names_the_update_shapes_the_library_launches():
         kname = "adam" if opt == "adamw" else "sgd"
         assert bench.update_kernel_name(opt, mode, big) == \
             f"{kname}_lane_kernel<{grad_t}, {mixed_t}, {e}, {lanes}, {it}>"
-        if name == "AdamMixed":  # MIXED Adam takes a lane form below the bound too
+        # below the bound: MIXED Adam its cached-gradient lane shape, MIXED SGD the
+        # four-element kernel, FP32 Adam and SGD the same lane forms as above it
+        if name == "AdamMixed":
             e, lanes, it = shape("AdamMixedCached")
-            assert bench.update_kernel_name(opt, mode, 1 << 20) == \
-                f"adam_lane_kernel<{grad_t}, {mixed_t}, {e}, {lanes}, {it}>"
-        else:
-            assert bench.update_kernel_name(opt, mode, 1 << 20) == \
-                f"{kname}_kernel<{grad_t}, {mixed_t}>"
+        small = (f"sgd_kernel<{grad_t}, {mixed_t}>" if name == "SgdMixed" else
+                 f"{kname}_lane_kernel<{grad_t}, {mixed_t}, {e}, {lanes}, {it}>")
+        assert bench.update_kernel_name(opt, mode, 1 << 20) == small
+    # the library launches no four-element Adam kernel, and the four-element SGD kernel only
+    # in mixed precision
+    assert "adam_kernel<" not in src
+    assert "sgd_kernel<float" not in src

@@ -398,13 +398,14 @@ def test_cfg5_gpt2_xl_fp32_adamw_then_sgd_momentum():
 
 @pytest.mark.parametrize("mode", ["mixed", "fp32"])
 def test_update_forms_on_both_sides_of_the_cached_gradient_bound(mode):
-    """The update kernels take their form from the stepped set's gradient bytes: up to 256 MiB
-    the four-element kernels (FP32 Adam, SGD) or MIXED Adam's 128-lane form, beyond that the
-    lane forms (one or two elements per lane).  SGD with momentum and dampening, then AdamW,
-    on a store just over the bound, each against the oracle: the whole store and a subset that
-    stays over it (lane forms with inactive tensors between and after the active ones), then
-    a subset under it.  The FP32 store's first tensor has an odd element count, so the
-    two-element lanes end on a lone element."""
+    """Mixed-precision updates take their form from the stepped set's gradient bytes: up to
+    256 MiB the four-element kernel (SGD) or Adam's 128-lane form, beyond that the 256-lane
+    lane forms; FP32 updates run the same lane forms (one or two elements per lane) on both
+    sides.  SGD with momentum and dampening, then AdamW, on a store just over the bound, each
+    against the oracle: the whole store and a subset that stays over it (lane forms with
+    inactive tensors between and after the active ones), then a subset under it.  The FP32
+    store's first tensor has an odd element count, so the two-element lanes end on a lone
+    element."""
     torch = torch_mod()
     if mode == "mixed":
         shapes = [(50257, 768), (8192, 8192), (7000, 5000), (768,), (3,)]  # 140.7M params

@@ -12,11 +12,9 @@
 //                         count and the loss scale;
 //   adam_lane_kernel /    one fused pass per element: grad transform (unscale, clip), weight
 //   sgd_lane_kernel       decay, the optimizer update and the bf16 copy, one or two elements
-//                         per lane (MIXED Adam at every size; the other updates beyond the
-//                         Infinity Cache); adam_kernel / sgd_kernel do the same with four
-//                         elements per lane (16-byte fp32 and 8-byte bf16 vectors) for FP32
-//                         Adam and SGD updates whose gradients fit the Infinity Cache.  Each
-//                         element is touched once.
+//                         per lane; sgd_kernel does the same with four elements per lane
+//                         (16-byte fp32 and 8-byte bf16 vectors) for MIXED SGD updates whose
+//                         gradients fit the Infinity Cache.  Each element is touched once.
 // Optimizer state is stored in records (see kRec): in MIXED mode each 64-element group of the
 // flat store keeps its fp32 master, m and v side by side in one 768-byte record; in FP32 mode
 // (where the fp32 master is the model-facing weight and stays contiguous) m and v share
@@ -26,12 +24,13 @@
 // relative to each other (GPT-2 124M, fresh allocations, 6 rounds: 571-617 us per step with
 // separate buffers, 570-580 us with records).
 // Work is a table of chunks of kChunk elements (the last chunk of a tensor is shorter; every
-// chunk starts on a 64-element boundary).  The four-element update runs one 256-thread block
-// per chunk, one vector per lane, at most kUpdBlocksPerCU blocks per CU: blocks are dispatched
-// in (reverse) chunk order, so the resident blocks sweep a narrow window of each buffer, which
-// keeps DRAM pages open.  16K-element chunks, a persistent grid, two or four vectors per
-// lane, 512-thread blocks and unlimited occupancy each measured 3-12% slower.  No MFMA:
-// nothing here is a contraction.
+// chunk starts on a 64-element boundary).  Update blocks are dispatched in (reverse) chunk
+// order, so the resident blocks sweep a narrow window of each buffer, which keeps DRAM pages
+// open.  The four-element update (MIXED SGD with cached gradients) runs one 256-thread block
+// per chunk, one vector per lane, at most kUpdBlocksPerCU blocks per CU; for it 16K-element
+// chunks, a persistent grid, two or four vectors per lane, 512-thread blocks and unlimited
+// occupancy each measured 3-12% slower (as a four-element Adam update, which the lane forms
+// have replaced).  No MFMA: nothing here is a contraction.
 //
 // Arithmetic matches the oracle bit for bit: no contraction (-ffp-contract=off), IEEE
 // division and square root (HIP's correctly rounded fp32 div/sqrt), denormals kept.
@@ -138,7 +137,7 @@ __device__ __forceinline__ void st4(float* p, f32x4 v) {
 }
 
 // 4 gradients as fp32 from either storage type, with ordinary (temporal) loads: the
-// four-element updates run only on gradients that fit the 256 MB Infinity Cache, where the
+// four-element update runs only on gradients that fit the 256 MB Infinity Cache, where the
 // norm pass or the backward left them
 __device__ __forceinline__ f32x4 ld_grad4(const float* g, uint64_t i) {
     return *reinterpret_cast<const f32x4*>(g + i);
@@ -485,56 +484,6 @@ __device__ __forceinline__ void store_vec(float* a, float* b, float* c, uint16_t
     }
 }
 
-// The four-element Adam update: one block per chunk (grid == nchunks), blocks in reverse
-// chunk order, one 4-element vector per lane.  The host runs it for FP32 updates whose
-// gradients fit the Infinity Cache (kCachedGradBytes: at most 2^17 chunks); MIXED updates and
-// larger ones take the lane forms below.  master, exp_avg, exp_avg_sq are slot bases: MIXED,
-// the three slots of the [master|m|v] records; FP32, the contiguous master and the two slots
-// of the [m|v] records.
-template <typename GradT, bool kMixed>
-__global__ __launch_bounds__(kUpdBlock) void adam_kernel(const GradT* __restrict__ grad,
-                                                         float* __restrict__ master,
-                                                         float* __restrict__ exp_avg,
-                                                         float* __restrict__ exp_avg_sq,
-                                                         uint16_t* __restrict__ param16,
-                                                         AdamArgs a) {
-    constexpr uint32_t kStateStride = kMixed ? kStrideMixed : kStrideMV;
-    Coefs k{1.0f, 1.0f, a.bias1, a.bias2};
-    if (a.st) {
-        if ((a.flags & kCheckSkip) && a.st->skip) return;
-        k.inv = a.st->inv_scale;
-        k.clip = a.st->clip_coef;
-        if (a.flags & kDevBias) {
-            k.bias1 = a.st->bias1;
-            k.bias2 = a.st->bias2;
-        }
-    }
-    const bool use_inv = a.flags & kUseInv, use_clip = a.flags & kUseClip;
-    const Chunk ch = a.chunks[a.nchunks - 1 - blockIdx.x];  // last chunks first (see norm pass)
-    const uint32_t off = threadIdx.x * kVec;
-    if (off >= ch.count) return;
-    const int n = (int)min(ch.count - off, (uint32_t)kVec);
-    const bool decay = (ch.meta & kChunkDecay) && (a.flags & kWdOn);
-    const uint64_t i = ch.begin + off;
-    const uint64_t s = rec_index(i, kStateStride);
-    float* pp = master + (kMixed ? s : i);
-    float* mp = exp_avg + s;
-    float* vp = exp_avg_sq + s;
-    const f32x4 g = ld_grad4(grad, i);
-    f32x4 p = ld4(pp);
-    f32x4 m = ld4(mp);
-    f32x4 v = ld4(vp);
-#pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-        float pj = p[j], mj = m[j], vj = v[j];
-        adam_elem(pj, g[j], mj, vj, a, k, use_inv, use_clip, decay);
-        p[j] = pj;
-        m[j] = mj;
-        v[j] = vj;
-    }
-    store_vec<kMixed>(pp, mp, vp, param16, i, p, m, v, n);
-}
-
 // ------------------------------------------------------------------------------------
 // lane forms: one or two elements per lane, for stores whose gradients exceed the Infinity
 // Cache
@@ -542,7 +491,8 @@ __global__ __launch_bounds__(kUpdBlock) void adam_kernel(const GradT* __restrict
 // Each block of kLanes lanes takes 1/lane_parts<kE, kLanes, kIt>() of a chunk (the last chunks
 // first): kIt consecutive pieces of kLanes x kE elements, each lane kE consecutive elements of
 // each piece, with no occupancy cap.  A lane holds 14-32 B of loads in flight instead of the
-// four-element form's 56-64 B, and full occupancy (registers allow 32 waves per CU) hides the
+// four-element form's 56-64 B (one 4-element vector per stream), and full occupancy
+// (registers allow 32 waves per CU) hides the
 // arithmetic.  The state is addressed from the record base alone (one 64-bit address per
 // lane, the other slots at immediate offsets), and the chunk descriptor is one 16-byte scalar
 // load issued together with the device-state loads, so two dependent scalar round trips
@@ -550,12 +500,13 @@ __global__ __launch_bounds__(kUpdBlock) void adam_kernel(const GradT* __restrict
 // per optimizer and mode (see kLaneAdamMixed in ttperf.hip).  Measured (interleaved rounds,
 // x a plain 256-lane non-temporal copy of the same bytes): GPT-2 774M mixed AdamW, one element
 // per lane, 256 lanes, two pieces: 1.014-1.018 against 0.96-0.98 with one piece and
-// 0.91-0.93 for the four-element form; GPT-2 1558M fp32 AdamW, one element, 128 lanes, two
+// 0.91-0.93 for a four-element Adam form; GPT-2 1558M fp32 AdamW, one element, 128 lanes, two
 // pieces: 1.018-1.027 against 0.977 for two elements in one piece and 0.905-0.927.  Below
 // the Infinity Cache bound, GPT-2 124M mixed AdamW with 128-lane blocks of two pieces runs its
-// update in 0.512-0.514 ms against 0.522 ms for the four-element form, and 5% faster when a
-// backward has just rewritten the gradients; the four-element form keeps half the grid for a
-// skipped step's early exit.
+// update in 0.512-0.514 ms against 0.522 ms for the four-element Adam form, and 5% faster when
+// a backward has just rewritten the gradients; FP32 AdamW and SGD momentum at 57.5M params run
+// their steps 2-3% faster than in four-element forms.  A four-element form dispatched half the
+// grid for a skipped step's early exit.
 template <int kE, int kLanes, int kIt>
 constexpr uint32_t lane_parts() {
     return kChunk / (kLanes * kE * kIt);
@@ -643,7 +594,7 @@ __device__ __forceinline__ void adam_piece(const GradT* __restrict__ grad,
 // per block, and halves the grid a skipped step dispatches.  records is the record array's
 // base ([master|m|v] in MIXED, [m|v] in FP32), master the contiguous FP32 weights (unused in
 // MIXED).  a.st must be valid: its fields are read unconditionally and used as a.flags say.
-// The arithmetic is adam_elem's, so results equal the four-element form's bit for bit.
+// The arithmetic is adam_elem's, so every shape gives the same results bit for bit.
 template <typename GradT, bool kMixed, int kE, int kLanes, int kIt>
 __global__ __launch_bounds__(kLanes) void adam_lane_kernel(const GradT* __restrict__ grad,
                                                            float* __restrict__ records,
@@ -713,8 +664,10 @@ __device__ __forceinline__ void sgd_elem(float& p, float g, float& b, const SgdA
     p = p - update;                 // autograd/dynamic/optim.hpp:25
 }
 
-// The four-element SGD update, launched and shaped as adam_kernel (one block per chunk, for
-// gradients that fit the Infinity Cache).  master is the master slot base (MIXED: slot 0 of
+// The four-element SGD update: one block per chunk (grid == nchunks), blocks in reverse chunk
+// order, one 4-element vector per lane, for MIXED gradients that fit the Infinity Cache (at
+// most 2^17 chunks), at most kUpdBlocksPerCU blocks per CU.  master is the master slot base
+// (MIXED: slot 0 of
 // the [master|m|v] records; FP32: the contiguous weights); momentum is contiguous.
 template <typename GradT, bool kMixed>
 __global__ __launch_bounds__(kUpdBlock) void sgd_kernel(const GradT* __restrict__ grad,

@@ -537,10 +537,10 @@ int set_dev(const ttp_ctx* c) {
 }
 
 // whether the gradients of an update over `w` fit the Infinity Cache (see kCachedGradBytes):
-// FP32 Adam and SGD then run the four-element kernels, MIXED Adam its cached-gradient lane
-// shape.  The four-element kernels launch one 256-lane block per chunk in one launch, which
-// holds at most 2^32 - 1 work-items; a set of that many chunks (millions of tiny tensors)
-// counts as not cached and takes the lane forms, which split.
+// MIXED SGD then runs the four-element kernel, MIXED Adam its cached-gradient lane shape.
+// The four-element kernel launches one 256-lane block per chunk in one launch, which holds
+// at most 2^32 - 1 work-items; a set of that many chunks (millions of tiny tensors) counts as
+// not cached and takes the lane forms, which split.
 bool grads_cached(const ttp_ctx* c, const WorkTables* w) {
     return w->elems * grad_esize(c) <= kCachedGradBytes &&
            w->n_chunks <= 0xFFFFFFFFu / ttp::kUpdBlock;
@@ -550,11 +550,10 @@ bool grads_cached(const ttp_ctx* c, const WorkTables* w) {
 // 2^30 work-items, well inside the 2^32 a launch may hold; they loop over the rest.
 constexpr uint32_t kMaxGridBlocks = 1u << 22;
 
-// FP32 Adam and SGD updates whose gradients fit the Infinity Cache run the four-element
-// kernels, one block per chunk (at most 2^17 chunks); MIXED Adam at any size, and the others
-// beyond the cache, the lane forms: kE elements per lane in blocks of kLanes, each block
-// walking kIt consecutive pieces of kLanes x kE elements, one block per
-// 1/lane_parts<kE, kLanes, kIt>() of a chunk.
+// MIXED SGD updates whose gradients fit the Infinity Cache run the four-element kernel, one
+// block per chunk (at most 2^17 chunks); every other update runs a lane form: kE elements per
+// lane in blocks of kLanes, each block walking kIt consecutive pieces of kLanes x kE
+// elements, one block per 1/lane_parts<kE, kLanes, kIt>() of a chunk.
 // MIXED Adam with cached gradients (GPT-2 124M; whole steps of bench.py after its settle
 // phase, 5 warmup + 20 timed steps, three interleaved rounds on one box; four-element /
 // 1 x 128 x 2 / 1 x 256 x 2):
@@ -564,9 +563,16 @@ constexpr uint32_t kMaxGridBlocks = 1u << 22;
 //   400 steps, 3 rounds, 2 processes)  0.660-0.662 / 0.631-0.632 / 0.633-0.634 ms
 //   skipped step            0.069 / 0.148 / 0.096 ms (the early exit of every block)
 //   nanoGPT-char (10.8M)    0.0543-0.0551 / 0.0544-0.0547 / 0.0556 ms
-// The four-element form wins only the rare skipped step.  Beyond the cache the shapes are
-// the fastest measured at GPT-2 774M mixed / 1558M fp32 (interleaved rounds, x a 256-lane
-// non-temporal copy of the same bytes; elements x lanes x pieces):
+// The four-element form wins only the rare skipped step.  FP32 stores with cached gradients
+// (8 GPT-2 blocks without wte, 57.5M params; four-element / lane form of the FP32 shapes
+// below; 300 steps per event pair, 3 rounds, 2 processes): AdamW 0.2763-0.2768 / 0.2685-0.2687
+// ms back to back, 0.3571-0.3577 / 0.3468-0.3474 ms with a gradient copy; SGD momentum
+// 0.2124-0.2128 / 0.2068-0.2071 and 0.2938-0.2941 / 0.2858-0.2860 ms.  MIXED SGD momentum at
+// GPT-2 124M keeps the four-element form (bench.py --optimizer sgdm, three rounds: 0.4365-0.4372
+// against 0.4408-0.4423 ms for 1 x 256 x 2 back to back, 0.4424-0.4439 against 0.4562-0.4589
+// with a cold cache).  Beyond the cache the shapes are the fastest measured at GPT-2 774M
+// mixed / 1558M fp32 (interleaved rounds, x a 256-lane non-temporal copy of the same bytes;
+// elements x lanes x pieces):
 //   Adam MIXED  1 x 256 x 2: 1.014-1.016 (1x128x2 1.01, 1x256x1 0.96-0.98, four-element 0.91)
 //   Adam FP32   1 x 128 x 2: 1.022-1.027 (1x256x2 1.01-1.02, 2x64x1 0.98, 2x64x2 0.89)
 //   SGD MIXED   1 x 256 x 2: 0.923-0.926 (slower by: 2x128x1 0.4-1.1%, 1x128x2 0.4-0.6%,
@@ -1425,7 +1431,6 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
         a.bias1 = a.bias2 = 1.0f;  // replaced by the device values
     }
     if (n) {
-        const dim3 block(ttp::kUpdBlock);
         TimedLaunch tl(c, TTP_KERNEL_UPDATE, !noalloc);
         const uint16_t* g16 = (const uint16_t*)c->grad;
         const float* g32 = (const float*)c->grad;
@@ -1444,10 +1449,6 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
                     dim3(kLanesAdamMixedCached), 0, c->stream, g16, c->records, (float*)nullptr,
                     p16, al, p0);
             });
-        else if (grads_cached(c, w))
-            hipLaunchKernelGGL((ttp::adam_kernel<float, false>), dim3(n), block, c->upd_lds,
-                               c->stream, g32, c->master, c->exp_avg, c->exp_avg_sq,
-                               (uint16_t*)nullptr, a);
         else if (c->mode == TTP_MODE_MIXED)
             launch_lanes(c,
                          (uint64_t)n *
@@ -1537,9 +1538,6 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
         if (grads_cached(c, w) && c->mode == TTP_MODE_MIXED)
             hipLaunchKernelGGL((ttp::sgd_kernel<uint16_t, true>), dim3(n), block, c->upd_lds,
                                c->stream, g16, c->master, c->momentum, p16, a);
-        else if (grads_cached(c, w))
-            hipLaunchKernelGGL((ttp::sgd_kernel<float, false>), dim3(n), block, c->upd_lds,
-                               c->stream, g32, c->master, c->momentum, (uint16_t*)nullptr, a);
         else if (c->mode == TTP_MODE_MIXED)
             launch_lanes(c,
                          (uint64_t)n *
