@@ -42,13 +42,14 @@
 namespace ttp {
 
 constexpr int kBlock = 256;     // 4 wave64s: norm pass, finalize and helper kernels
-constexpr int kUpdBlock = 256;  // 4 wave64s: update kernels
+constexpr int kUpdBlock = 256;  // 4 wave64s: the four-element update
 constexpr int kVec = 4;         // elements per lane per vector
 constexpr uint32_t kChunk = kUpdBlock * kVec;  // 1024 elements: one vector per lane
-// Resident update blocks per CU.  The host reserves LDS_per_CU / kUpdBlocksPerCU bytes of
-// (unused) dynamic LDS per update block so that no more than this many are resident: 16
-// waves per CU sweep the HBM pages of the streams with fewer row conflicts than the 32+
-// waves that registers alone would allow (separate state arrays, GPT-2 124M, same box,
+// Resident blocks per CU of the four-element update.  The host reserves LDS_per_CU /
+// kUpdBlocksPerCU bytes of (unused) dynamic LDS per block so that no more than this many are
+// resident: 16 waves per CU sweep the HBM pages of the streams with fewer row conflicts than
+// the 32+ waves that registers alone would allow (measured on the four-element Adam update
+// that the lane forms have replaced: separate state arrays, GPT-2 124M, same box,
 // interleaved repeats: 568 us vs 588 us for 512-thread blocks at 3 per CU, 622 us uncapped;
 // GPT-2 XL fp32: 7.36 ms vs 7.63 ms).  With state records, 4, 5, 6 and 8 blocks per CU
 // measure alike and 3 is 27% slower.

@@ -983,7 +983,8 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
     c->stream = c->own_stream;
 
     {
-        // occupancy cap of the update kernels: LDS_per_CU / blocks_per_CU bytes each
+        // occupancy cap of the four-element update (MIXED SGD with cached gradients):
+        // LDS_per_CU / blocks_per_CU bytes of dynamic LDS per block
         int lds_cu = 0, lds_blk = 0;
         const uint64_t per_cu = env_u64("TTP_UPD_BLOCKS_PER_CU", ttp::kUpdBlocksPerCU);
         if (per_cu &&
