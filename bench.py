@@ -506,6 +506,18 @@ def main():
     r = store.adam_step(report=True, **hp) if args.optimizer == "adamw" else None
     if r is not None:
         assert not r["skipped"], r
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # for comparison, the same W warmup + K timed steps right after the set-up, before the
+    # settle phase: they fall in the clocks' ramp after the idle set-up
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    unsettled_ms = e0.elapsed_time(e1) / args.steps
     settle_n, settle_ms = settle(step, args.settle_ms)
     for _ in range(args.warmup):
         step()
@@ -658,9 +670,12 @@ def main():
         "kernels_ms": {"norm_pass": round(nrm_avg, 4), "update": round(upd_avg, 4),
                        "source": "second pass of K steps with an event pair per launch"},
         "settle": {"steps": settle_n, "ms": settle_ms,
+                   "unsettled_ms_per_step": round(unsettled_ms, 4),
                    "note": "untimed steps run back to back before the W warmup steps, so that "
                            "the timed steps see the clocks of a busy GPU, as in a training loop "
-                           "(the first tens of ms after an idle phase run at lower clocks)"},
+                           "(the first tens of ms after an idle phase run at lower clocks); "
+                           "unsettled_ms_per_step: W warmup + K timed steps right after the "
+                           "set-up, before the settle steps"},
         "cold_ms_per_step": round(cold_ms, 4),
         "cold_Gparams_per_s": round(n_params / (cold_ms / 1e3) / 1e9, 3),
         "cold_note": "each step after a 512 MB read of unrelated data on its stream (outside "
