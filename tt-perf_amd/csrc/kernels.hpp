@@ -317,53 +317,94 @@ struct FinalizeArgs {
 
 // torch _amp_update_scale_ semantics, over this step's overflow and the pending overflow of
 // the steps that deferred their update since the last one (found_inf summed over optimizers,
-// as GradScaler.update does); clears the pending flag
-__device__ __forceinline__ void scaler_update(DevState* st, int32_t found, int32_t growth_interval,
-                                              double growth_factor, double backoff_factor) {
-    if (found || (st->pending & kPendingInf)) {
-        st->scale = (float)((double)st->scale * backoff_factor);
-        st->growth_tracker = 0;
-    } else {
-        const int32_t ok = st->growth_tracker + 1;
-        if (ok == growth_interval) {
-            const float ns = (float)((double)st->scale * growth_factor);
-            if (ns - ns == 0.0f) st->scale = ns;  // finite
-            st->growth_tracker = 0;
-        } else {
-            st->growth_tracker = ok;
-        }
+// as GradScaler.update does): the new scale and growth tracker (the pending flag is cleared)
+struct ScaleUpdate {
+    float scale;
+    int32_t tracker;
+};
+__device__ __forceinline__ ScaleUpdate next_scale(float scale, int32_t tracker, int32_t pending,
+                                                  int32_t found, int32_t growth_interval,
+                                                  double growth_factor, double backoff_factor) {
+    if (found || (pending & kPendingInf)) return {(float)((double)scale * backoff_factor), 0};
+    const int32_t ok = tracker + 1;
+    if (ok == growth_interval) {
+        const float ns = (float)((double)scale * growth_factor);
+        return {ns - ns == 0.0f ? ns : scale, 0};  // grows only to a finite scale
     }
-    st->pending = 0;
+    return {scale, ok};
+}
+
+// (float)(1 - beta^t) for t = 1 .. bias_len from the host-built table; 1.0f beyond (and for
+// t = 0, which no applied step has)
+__device__ __forceinline__ float bias_entry(const float* tab, uint32_t len, uint64_t t, int j) {
+    return (t >= 1 && t <= len) ? tab[2 * (t - 1) + j] : 1.0f;
 }
 
 __global__ __launch_bounds__(kBlock) void norm_finalize_kernel(FinalizeArgs a) {
     __shared__ double lds[kBlock / 64];
-    // all loads of a round issued before the adds; per-thread order fixed (deterministic)
+    DevState* st = a.st;
+    // Every load is issued before thread 0 decides: the first round of partials, then the
+    // whole step state (one 64-byte block, uniform, so scalar loads) and the bias corrections
+    // of both outcomes (t + 1 if the step applies, t if it is skipped), whose latency overlaps
+    // the partials' and their sum.  Read one after another, as the decisions need them, they
+    // were six dependent round trips on thread 0 after the sum.
+    // Partials: all loads of a round issued before the adds, each thread's order fixed
+    // (deterministic); with an index list (per-tensor sums), a round's indices load first.
+    // Loads past the end read the last entry and count as 0 in the adds (a branch or a select
+    // at each load made the compiler wait for it there).
     constexpr int kPer = 8;
-    double s = 0.0;
-    for (uint32_t base = 0; base < a.npartials; base += kBlock * kPer) {
-        double v[kPer];
+    const uint32_t n = a.npartials;
+    double v[kPer];
+    auto load_round = [&](uint32_t base) {  // base < n
+        uint32_t at[kPer];
 #pragma unroll
-        for (int k = 0; k < kPer; ++k) {
-            const uint32_t b = base + (uint32_t)k * kBlock + threadIdx.x;
-            v[k] = b < a.npartials ? a.partials[a.idx ? a.idx[b] : b] : 0.0;
+        for (int k = 0; k < kPer; ++k) at[k] = min(base + (uint32_t)k * kBlock + threadIdx.x, n - 1);
+        if (a.idx) {
+#pragma unroll
+            for (int k = 0; k < kPer; ++k) at[k] = a.idx[at[k]];
         }
 #pragma unroll
-        for (int k = 0; k < kPer; ++k) s += v[k];
+        for (int k = 0; k < kPer; ++k) v[k] = a.partials[at[k]];
+    };
+    if (n) {
+        load_round(0);
+    } else {
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) v[k] = 0.0;
+    }
+    const DevState s0 = *st;
+    float b1n = 1.0f, b2n = 1.0f, b1s = 1.0f, b2s = 1.0f;
+    if (a.count_t && a.want_bias) {
+        b1n = bias_entry(a.bias_tab, a.bias_len, s0.t + 1, 0);
+        b2n = bias_entry(a.bias_tab, a.bias_len, s0.t + 1, 1);
+        b1s = bias_entry(a.bias_tab, a.bias_len, s0.t, 0);
+        b2s = bias_entry(a.bias_tab, a.bias_len, s0.t, 1);
+    }
+    // keeps the compiler from moving the first round's adds (which wait for the partials)
+    // ahead of the state loads
+    __builtin_amdgcn_sched_barrier(0);
+    double s = 0.0;
+    for (uint32_t base = 0;;) {
+#pragma unroll
+        for (int k = 0; k < kPer; ++k)
+            s += base + (uint32_t)k * kBlock + threadIdx.x < n ? v[k] : 0.0;
+        base += kBlock * kPer;
+        if (base >= n) break;
+        load_round(base);
     }
     s = block_sum(s, lds);
     if (threadIdx.x != 0) return;
 
-    DevState* st = a.st;
-    const float inv = a.scaler_on ? (float)(1.0 / (double)st->scale) : 1.0f;
+    const float inv = a.scaler_on ? (float)(1.0 / (double)s0.scale) : 1.0f;
+    const double norm = sqrt(s);
     st->sumsq = s;
-    st->norm = sqrt(s);
+    st->norm = norm;
     if (a.probe) return;
     const int found = !(s <= 1.7976931348623157e308);  // inf or NaN
     const int skip = a.scaler_on && found;
     float coef = 1.0f;
     if (a.max_norm > 0.0) {
-        double cd = a.max_norm / (st->norm + 1e-6);
+        double cd = a.max_norm / (norm + 1e-6);
         if (cd > 1.0) cd = 1.0;
         coef = (float)cd;
     }
@@ -372,18 +413,23 @@ __global__ __launch_bounds__(kBlock) void norm_finalize_kernel(FinalizeArgs a) {
     st->inv_scale = inv;
     st->clip_coef = coef;
     if (a.count_t) {
-        if (!skip) st->t += 1;
+        st->t = skip ? s0.t : s0.t + 1;
         if (a.want_bias) {
-            const uint64_t t = st->t;
-            st->bias1 = (t >= 1 && t <= a.bias_len) ? a.bias_tab[2 * (t - 1)] : 1.0f;
-            st->bias2 = (t >= 1 && t <= a.bias_len) ? a.bias_tab[2 * (t - 1) + 1] : 1.0f;
+            st->bias1 = skip ? b1s : b1n;
+            st->bias2 = skip ? b2s : b2n;
         }
     }
     if (a.scaler_on) {
-        if (a.defer_scale)
-            st->pending |= kPendingStep | (found ? kPendingInf : 0);
-        else
-            scaler_update(st, found, a.growth_interval, a.growth_factor, a.backoff_factor);
+        if (a.defer_scale) {
+            st->pending = s0.pending | kPendingStep | (found ? kPendingInf : 0);
+        } else {
+            const ScaleUpdate u = next_scale(s0.scale, s0.growth_tracker, s0.pending, found,
+                                             a.growth_interval, a.growth_factor,
+                                             a.backoff_factor);
+            st->scale = u.scale;
+            st->growth_tracker = u.tracker;
+            st->pending = 0;
+        }
     }
 }
 
@@ -391,8 +437,13 @@ __global__ __launch_bounds__(kBlock) void norm_finalize_kernel(FinalizeArgs a) {
 // when no step deferred it since the last update, so an iteration's scale never moves twice
 __global__ void scaler_update_kernel(DevState* st, int32_t growth_interval, double growth_factor,
                                      double backoff_factor) {
-    if (threadIdx.x == 0 && blockIdx.x == 0 && (st->pending & kPendingStep))
-        scaler_update(st, 0, growth_interval, growth_factor, backoff_factor);
+    if (threadIdx.x == 0 && blockIdx.x == 0 && (st->pending & kPendingStep)) {
+        const ScaleUpdate u = next_scale(st->scale, st->growth_tracker, st->pending, 0,
+                                         growth_interval, growth_factor, backoff_factor);
+        st->scale = u.scale;
+        st->growth_tracker = u.tracker;
+        st->pending = 0;
+    }
 }
 
 // Per-tensor sums of squares (ttp_grad_sumsq_tensors), from one norm_partials_kernel block per
