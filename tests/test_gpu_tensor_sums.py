@@ -430,3 +430,44 @@ def test_bucket_sums_on_a_side_stream_wait_for_the_backward():
     del views
     store.close()
     twin.close()
+
+
+def test_step_from_sums_of_more_tensors_than_one_finalize_round():
+    """The finalize sums at most 8 x 256 partials per round; a step over 3000 tensors takes its
+    norm from 3000 per-tensor sums, read through the tensor list in two rounds, with loss
+    scaling and clipping (and an overflow on one step), against the oracle and a twin that
+    runs the norm pass."""
+    torch = torch_mod()
+    rng = np.random.default_rng(130)
+    shapes = [(int(n),) for n in rng.integers(1, 300, size=3000)]
+    decay = [bool(x) for x in rng.integers(0, 2, size=len(shapes))]
+    store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=131)
+    twin, _ = make_pair(shapes, decay, O.MODE_MIXED, seed=131)
+    for s in (store, twin):
+        s.configure_scaler(True, init_scale=256.0, growth_interval=2)
+    ref.configure_scaler(True, 256.0, growth_interval=2)
+    hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, decoupled=True,
+              max_grad_norm=0.5)
+    gen = torch.Generator(device="cuda").manual_seed(132)
+    from ttperf import _lib as L
+    for step in range(4):
+        inf_at = store.offsets[2500] if step == 2 else None
+        host = device_grads(store, gen, 1e-2, scale=ref.scale, inf_at=inf_at)
+        twin.upload(L.BUF_GRAD, L.ALL_TENSORS, store.download(L.BUF_GRAD))
+        ref.grad[:store.total] = host
+        for i in range(ref.n):
+            ref.set_has_grad(i, True)
+        for b in _buckets(len(shapes), size=700):
+            store.grad_sumsq_tensors(b)
+        r = store.adam_step(report=True, tensor_sums=True, **hp)
+        rt = twin.adam_step(report=True, **hp)
+        e = ref.adam_step(**hp)
+        print(f"step {step}: norm {r['grad_norm']!r} (norm pass {rt['grad_norm']!r}, oracle "
+              f"{e['grad_norm']!r}), skipped {r['skipped']}", flush=True)
+        for k in ("skipped", "found_inf", "step", "scale", "growth_tracker"):
+            assert r[k] == rt[k] == e[k], (k, r, rt, e)
+        if np.isfinite(e["grad_norm"]):
+            assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-10 * e["grad_norm"]
+        compare_state(store, ref, max_ulp=2)
+    store.close()
+    twin.close()
