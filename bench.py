@@ -602,9 +602,9 @@ def main():
         gcopy_ms = e0.elapsed_time(e1) / args.steps
     del gview, backup
 
-    # skipped (overflow) steps: only the norm pass and the finalize do work; K of them
-    # between one event pair (each backs the loss scale off; it is reset afterwards)
-    skip_ms = None
+    # skipped (overflow) steps: only the norm pass and the finalize do work; min(K, 20) of
+    # them between one event pair (each backs the loss scale off; it is reset afterwards)
+    skip_ms, n_skip = None, 0
     if args.optimizer == "adamw" and cfg["scaler"]:
         store.upload(L.BUF_GRAD, 0, torch.full((store.tensors[0].numel,), float("inf"),
                                                device=dev, dtype=torch.bfloat16 if mode == "mixed"
@@ -688,7 +688,7 @@ def main():
                     "writes them) then the step, between one event pair (pair_ms); the copies "
                     "alone (grad_copy_ms); step_ms is the difference"},
         "skipped_step_ms": round(skip_ms, 4) if skip_ms is not None else None,
-        "skipped_step_note": "mean of 20 overflow steps between one event pair",
+        "skipped_step_note": f"mean of {n_skip} overflow steps between one event pair",
         "bucketed_norm": sums,
         "torch_copy_GBps": round(copy_gbps, 1),
         "ceilings": {"nt_copy_GBps": round(nt_copy_gbps, 1),
