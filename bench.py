@@ -10,10 +10,12 @@ Prints ONE JSON line: Gparams/s and ms/step of the timed region (K steps between
 pair, after --settle-ms of untimed steps and then W warmup steps), the roofline of the
 dominant (update) kernel from HIP events recorded around each of its launches on the
 kernel's stream during a second pass of K steps, and the CPU oracle baseline timed on this
-host's cores on a bounded sample.  Beside the headline: the step with a cold Infinity Cache
-(512 MB of unrelated reads before each step, outside its event pair), the mean skipped
-(overflow) step, and the other configurations' steps (the MLP, nanoGPT-char, GPT-2 774M
-mixed AdamW, GPT-2 XL fp32 AdamW and SGD momentum), each in a store of its own.
+host's cores on a bounded sample.  Beside the headline: the same steps timed right after the
+set-up (before the settle steps), the step with a cold Infinity Cache (512 MB of unrelated
+reads before each step, outside its event pair), the step right after a rewrite of its
+gradients, the mean skipped (overflow) step, the step with its norm from bucketed sums, and
+the other configurations' steps (the MLP, nanoGPT-char, GPT-2 774M mixed AdamW, GPT-2 XL
+fp32 AdamW and SGD momentum), each in a store of its own.
 """
 import argparse
 import ctypes
@@ -27,8 +29,9 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(REPO, "tt-perf_amd"))
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
-# gradient bytes up to which libttperf_hip runs the four-element update kernels, the lane forms
-# beyond (kCachedGradBytes in tt-perf_amd/csrc/ttperf.hip): names the kernel in the roofline
+# gradient bytes up to which libttperf_hip counts a store's gradients as Infinity-Cache resident
+# and picks its update form accordingly (kCachedGradBytes in tt-perf_amd/csrc/ttperf.hip):
+# names the kernel in the roofline
 CACHED_GRAD_BYTES = 256 << 20
 # algorithmic bytes per parameter of one update-kernel pass (and of the norm pass)
 UPDATE_BYTES = {("adamw", "mixed"): 28, ("adamw", "fp32"): 28, ("sgdm", "fp32"): 20,
