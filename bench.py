@@ -15,7 +15,8 @@ set-up (before the settle steps), the step with a cold Infinity Cache (512 MB of
 reads before each step, outside its event pair), the step right after a rewrite of its
 gradients, the mean skipped (overflow) step, the step with its norm from bucketed sums, and
 the other configurations' steps (the MLP, nanoGPT-char, GPT-2 774M mixed AdamW, GPT-2 XL
-fp32 AdamW and SGD momentum), each in a store of its own.
+fp32 AdamW and SGD momentum), each in a store of its own, and the step of the reference's
+GPT benchmark model through the C++ drop-in surface (tests/cpp/bench_gpt2_step).
 """
 import argparse
 import ctypes
@@ -377,7 +378,8 @@ def update_kernel_name(optimizer, mode, total_elems):
     """The update instantiation libttperf_hip launches for a store (its rocprof name): the lane
     form with its elements per lane, lanes per block and pieces per block (kLaneAdamMixed ...
     in tt-perf_amd/csrc/ttperf.hip), except while the gradients fit the Infinity Cache: MIXED
-    Adam then takes the kLaneAdamMixedCached shape, and MIXED SGD the four-element kernel."""
+    Adam then takes the kLaneAdamMixedCached shape, and MIXED SGD momentum (the only SGD this
+    bench steps) the four-element kernel."""
     grad_t, mixed_t = ("unsigned short", "true") if mode == "mixed" else ("float", "false")
     kname = "adam" if optimizer == "adamw" else "sgd"
     if mode == "mixed" and total_elems * 2 <= CACHED_GRAD_BYTES:
@@ -472,6 +474,31 @@ def other_config(config, optimizer, steps, warmup, settle_ms):
             "update_kernel": upd_kernel,
             "params": n_params, "tensors": len(numels), "mode": mode,
             "steps": steps, "warmup": warmup, "settle_steps": settle_n}
+
+
+def cpp_dropin(steps, warmup, settle_ms):
+    """The optimizer step of the reference's GPT benchmark model (traced::
+    TracedTransformerWithEmbedding<12> at GPT-2 small dimensions, bench/autograd/
+    bench_gpt2_full.cpp:74-100), timed by the C++ drop-in program tests/cpp/bench_gpt2_step
+    through autograd::AdamW and the model's sgd_step(), in a process of its own.  Returns its
+    JSON line, and whether its checks passed."""
+    import subprocess
+    exe = os.path.join(REPO, "tests", "cpp", "build", "bench_gpt2_step")
+    if not os.access(exe, os.X_OK):
+        return {"error": f"{exe} is not built (make -C tests/cpp)"}
+    env = dict(os.environ, BENCH_ITERS=str(steps), BENCH_WARMUP=str(warmup),
+               BENCH_SETTLE_MS=str(int(settle_ms)))
+    p = subprocess.run([exe], capture_output=True, text=True, timeout=300, env=env)
+    line = next((ln for ln in p.stdout.splitlines() if ln.startswith('{"bench"')), None)
+    if p.returncode != 0 or line is None:
+        return {"error": f"exit {p.returncode}: {(p.stdout + p.stderr)[-500:]}"}
+    res = json.loads(line)
+    res["checks_passed"] = "bench_gpt2_step: PASS" in p.stdout
+    res["note"] = ("C++ drop-in surface, mixed precision, 200 ms of settle steps then W warmup "
+                   "and K steps between two synchronisations (std::chrono, as the reference's "
+                   "bench); AdamW with loss scaling 2^16 and clip 1.0 at 30 B/param, the "
+                   "model's sgd_step at 12 B/param; no tied embedding, so 163M params")
+    return res
 
 
 def main():
@@ -712,6 +739,7 @@ def main():
                      "algorithmic_bytes_per_launch": n_params * ub},
         "cpu_baseline": None,
         "other_configs": None,
+        "cpp_dropin": None,
     }
     store.close()
     del store
@@ -732,6 +760,8 @@ def main():
             "pair per launch) and closed before the next; no CPU leg; the copy ceilings only "
             "where the update moves at least 1 GiB (the MLP's 269 KB step is launch-bound and "
             "the char model's 323 MB mostly Infinity-Cache resident)")
+        log("bench: the C++ drop-in program (tests/cpp/bench_gpt2_step) ...")
+        out["cpp_dropin"] = cpp_dropin(args.steps, args.warmup, args.settle_ms)
     if grads_host is not None:
         log("bench: timing the CPU oracle baseline ...")
         out["cpu_baseline"] = cpu_baseline(numels, [1 if d else 0 for d in decay],

@@ -241,9 +241,11 @@ def test_each_optimizer_keeps_its_own_step_count():
 
 
 def test_cpp_dropin_headers_compile():
-    """The C++ drop-in tests (tests/cpp) build against include/ and the library."""
+    """The C++ drop-in tests and bench program (tests/cpp) build against include/ and the
+    library."""
     subprocess.run(["make", "-s", "-C", os.path.join(REPO, "tests", "cpp")], check=True)
-    for t in ("test_sgd", "test_traced", "test_adam", "test_modules", "train_mlp"):
+    for t in ("test_sgd", "test_traced", "test_adam", "test_modules", "train_mlp", "test_store",
+              "bench_gpt2_step"):
         assert os.access(os.path.join(REPO, "tests", "cpp", "build", t), os.X_OK)
 
 

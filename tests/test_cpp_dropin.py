@@ -36,6 +36,29 @@ def test_cpp_dropin(name):
     assert f"{name}: PASS" in p.stdout
 
 
+def test_gpt2_step_bench_program_at_small_dimensions():
+    """tests/cpp/bench_gpt2_step (bench.py's C++ drop-in leg) on a 2-layer GPT model of small
+    dimensions: its checks pass (step count and loss scale after the AdamW steps, bf16 weights
+    = RNE of the master, an overflow step skipped through autograd::AdamW, sgd_step = w - lr*g)
+    and it prints its JSON line.  300 ms of settle steps at this size are usually more than
+    2000 steps, so the scale grows on the way (the program checks the scale either way)."""
+    import json
+    exe = os.path.join(CPP, "build", "bench_gpt2_step")
+    if not os.access(exe, os.X_OK):
+        subprocess.run(["make", "-s", "-C", CPP], check=True)
+    env = dict(os.environ, BENCH_LAYERS="2", BENCH_DIM="128", BENCH_HEADS="4", BENCH_SEQ="64",
+               BENCH_VOCAB="1000", BENCH_ITERS="5", BENCH_WARMUP="2", BENCH_SETTLE_MS="300")
+    p = _run(exe, env)
+    assert p.returncode == 0, f"exited {p.returncode}:\n{p.stdout[-3000:]}\n{p.stderr[-2000:]}"
+    assert "bench_gpt2_step: PASS" in p.stdout
+    res = json.loads(next(ln for ln in p.stdout.splitlines() if ln.startswith('{"bench"')))
+    # 2 embeddings + 2 blocks of 16 tensors + the output projection's weight and bias
+    assert res["tensors"] == 36 and res["layers"] == 2
+    assert res["params"] == 1000 * 128 + 64 * 128 + 2 * (4 * 128 + 4 * (128 * 128 + 128) +
+                                                          2 * 128 * 512 + 512 + 128) + 128 * 1000 + 1000
+    assert res["adamw_ms_per_step"] > 0 and res["sgd_ms_per_step"] > 0
+
+
 @pytest.mark.parametrize("name", TESTS)
 def test_cpp_dropin_host_sanitizers(name):
     exe = os.path.join(CPP, "build-asan", name)
