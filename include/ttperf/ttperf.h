@@ -35,14 +35,14 @@
  *
  * Environment, read at ttp_create (tuning only):
  *   TTP_UPD_BLOCKS_PER_CU  resident update blocks per CU of the four-element update (MIXED SGD
- *                          up to 256 MiB of gradients; default 4; 0: no cap); every other
+ *                          with momentum up to 256 MiB of gradients; default 4; 0: no cap); every other
  *                          update runs uncapped.  Results do not depend on it.
  *   TTP_NORM_GRID          blocks of each gradient-norm launch (default 8 x CUs, at most
  *                          65536; the pass is two launches above 256 MiB of gradients).  It
  *                          fixes the fp64 summation order of the norm: deterministic for a
  *                          given value, last bits may differ between values.
  *   TTP_LANE_LAUNCH_BLOCKS most blocks per launch of the lane-form updates (all but MIXED SGD
- *                          up to 256 MiB of gradients; default: what 2^32 - 1 work-items
+ *                          with momentum up to 256 MiB of gradients; default: what 2^32 - 1 work-items
  *                          allow); a larger update is split into several launches.  Results
  *                          do not depend on it.
  */

@@ -399,12 +399,13 @@ def test_cfg5_gpt2_xl_fp32_adamw_then_sgd_momentum():
 @pytest.mark.parametrize("mode", ["mixed", "fp32"])
 def test_update_forms_on_both_sides_of_the_cached_gradient_bound(mode):
     """Mixed-precision updates take their form from the stepped set's gradient bytes: up to
-    256 MiB the four-element kernel (SGD) or Adam's 128-lane form, beyond that the 256-lane
-    lane forms; FP32 updates run the same lane forms (one or two elements per lane) on both
-    sides.  SGD with momentum and dampening, then AdamW, on a store just over the bound, each
-    against the oracle: the whole store and a subset that stays over it (lane forms with
-    inactive tensors between and after the active ones), then a subset under it.  The FP32
-    store's first tensor has an odd element count, so the two-element lanes end on a lone
+    256 MiB the four-element kernel (SGD momentum) or Adam's 128-lane form, beyond that the
+    256-lane lane forms; plain SGD (no momentum) runs its two-element 256-lane form on both
+    sides; FP32 updates run the same lane forms (one or two elements per lane) on both sides.
+    SGD with momentum and dampening, plain SGD with weight decay, then AdamW, on a store just
+    over the bound, each against the oracle: the whole store and a subset that stays over it
+    (lane forms with inactive tensors between and after the active ones), then a subset under
+    it.  Both stores hold tensors of odd element count, so two-element lanes end on a lone
     element."""
     torch = torch_mod()
     if mode == "mixed":
@@ -426,6 +427,7 @@ def test_update_forms_on_both_sides_of_the_cached_gradient_bound(mode):
     assert sum(sizes[i] for i in subsets[2]) * gbytes <= bound
     gen = torch.Generator(device="cuda").manual_seed(81)
     sgd = dict(lr=1e-2, momentum=0.9, dampening=0.1, max_grad_norm=1.0)
+    plain = dict(lr=1e-2, weight_decay=0.01, max_grad_norm=1.0)
     adam = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
     slots = ("master", "param", "momentum") if mode == "mixed" else ("master", "momentum")
     adam_slots = ("master", "exp_avg", "exp_avg_sq") + (("param",) if mode == "mixed" else ())
@@ -440,6 +442,15 @@ def test_update_forms_on_both_sides_of_the_cached_gradient_bound(mode):
             e = ref.sgd_step(**sgd)
             assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
             print(f"{mode} {label} sgd-m step {step}: norm {r['grad_norm']:.6f}", flush=True)
+        compare_state(store, ref, which=slots, max_ulp=2)
+        host = device_grads(store, gen, 1e-3)
+        ref.grad[:] = host
+        for i in range(ref.n):
+            ref.set_has_grad(i, subset is None or i in subset)
+        r = store.sgd_step(report=True, indices=subset, **plain)
+        e = ref.sgd_step(**plain)
+        assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
+        print(f"{mode} {label} sgd step: norm {r['grad_norm']:.6f}", flush=True)
         compare_state(store, ref, which=slots, max_ulp=2)
         for step in range(2):
             host = device_grads(store, gen, 1e-3)
@@ -459,8 +470,8 @@ def test_lane_form_update_split_into_several_launches(mode, monkeypatch):
     """A lane-form update over more blocks than one launch may hold runs as several launches
     at increasing part offsets.  TTP_LANE_LAUNCH_BLOCKS (read at ttp_create) lowers that limit
     to 4099 blocks, so that a store just over the 256 MiB bound takes dozens of launches, whose
-    boundaries fall inside chunks and tensors; SGD with momentum and AdamW on the whole store
-    and on a subset, against the oracle.  In mixed precision also a subset under the bound,
+    boundaries fall inside chunks and tensors; SGD with momentum, plain SGD and AdamW on the
+    whole store and on a subset, against the oracle.  In mixed precision also a subset under the bound,
     which MIXED Adam steps in its 128-lane form (37 launches)."""
     torch = torch_mod()
     monkeypatch.setenv("TTP_LANE_LAUNCH_BLOCKS", "4099")
@@ -476,6 +487,7 @@ def test_lane_form_update_split_into_several_launches(mode, monkeypatch):
         store, ref = make_pair(shapes, decay, O.MODE_FP32, seed=85)
     gen = torch.Generator(device="cuda").manual_seed(86)
     sgd = dict(lr=1e-2, momentum=0.9, dampening=0.1, max_grad_norm=1.0)
+    plain = dict(lr=1e-2, weight_decay=0.01, max_grad_norm=1.0)
     adam = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
     slots = ("master", "param", "momentum") if mode == "mixed" else ("master", "momentum")
     adam_slots = ("master", "exp_avg", "exp_avg_sq") + (("param",) if mode == "mixed" else ())
@@ -483,14 +495,15 @@ def test_lane_form_update_split_into_several_launches(mode, monkeypatch):
     if mode == "mixed":
         legs.append(("cached-gradient subset", [0, 3, 4]))
     for label, sub in legs:
-        for name, hp in (("sgd-m", sgd), ("adamw", adam)):
+        for name, hp in (("sgd-m", sgd), ("sgd", plain), ("adamw", adam)):
             host = device_grads(store, gen, 1e-3)
             ref.grad[:] = host
             for i in range(ref.n):
                 ref.set_has_grad(i, sub is None or i in sub)
-            step = store.sgd_step if name == "sgd-m" else store.adam_step
+            sgd_like = name.startswith("sgd")
+            step = store.sgd_step if sgd_like else store.adam_step
             r = step(report=True, indices=sub, **hp)
-            e = (ref.sgd_step if name == "sgd-m" else ref.adam_step)(**hp)
+            e = (ref.sgd_step if sgd_like else ref.adam_step)(**hp)
             assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
             print(f"{mode} {label} {name}: norm {r['grad_norm']:.6f}", flush=True)
         compare_state(store, ref, which=slots, max_ulp=2)
@@ -503,7 +516,8 @@ def test_lane_form_with_many_small_tensors(mode):
     """A store just over the 256 MiB bound made of one large tensor of odd length and 1500
     small ones of 1..200 elements (most chunks hold less than one lane-form piece, many
     blocks have nothing to do): AdamW with loss scaling and clipping, then SGD with Nesterov
-    momentum, against the oracle; the second Adam step on a subset of every third tensor."""
+    momentum, then plain SGD with weight decay, against the oracle; the second Adam step on a
+    subset of every third tensor."""
     torch = torch_mod()
     rng = np.random.default_rng(87)
     big = (1 << 27) + 3 if mode == "mixed" else (1 << 26) + 5
@@ -539,6 +553,14 @@ def test_lane_form_with_many_small_tensors(mode):
         e = ref.sgd_step(**sgd)
         assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
     compare_state(store, ref, which=("master", "momentum") + (("param",) if mode == "mixed" else ()),
+                  max_ulp=2)
+    plain = dict(lr=1e-2, weight_decay=0.01, max_grad_norm=0.5)
+    host = device_grads(store, gen, 1e-3, scale=ref.scale)
+    ref.grad[:] = host
+    r = store.sgd_step(report=True, **plain)
+    e = ref.sgd_step(**plain)
+    assert r["skipped"] == e["skipped"] and abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
+    compare_state(store, ref, which=("master",) + (("param",) if mode == "mixed" else ()),
                   max_ulp=2)
     store.close()
 

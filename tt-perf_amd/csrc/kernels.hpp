@@ -13,8 +13,8 @@
 //   adam_lane_kernel /    one fused pass per element: grad transform (unscale, clip), weight
 //   sgd_lane_kernel       decay, the optimizer update and the bf16 copy, one or two elements
 //                         per lane; sgd_kernel does the same with four elements per lane
-//                         (16-byte fp32 and 8-byte bf16 vectors) for MIXED SGD updates whose
-//                         gradients fit the Infinity Cache.  Each element is touched once.
+//                         (16-byte fp32 and 8-byte bf16 vectors) for MIXED SGD momentum
+//                         updates whose gradients fit the Infinity Cache.  Each element is touched once.
 // Optimizer state is stored in records (see kRec): in MIXED mode each 64-element group of the
 // flat store keeps its fp32 master, m and v side by side in one 768-byte record; in FP32 mode
 // (where the fp32 master is the model-facing weight and stays contiguous) m and v share
@@ -26,7 +26,7 @@
 // Work is a table of chunks of kChunk elements (the last chunk of a tensor is shorter; every
 // chunk starts on a 64-element boundary).  Update blocks are dispatched in (reverse) chunk
 // order, so the resident blocks sweep a narrow window of each buffer, which keeps DRAM pages
-// open.  The four-element update (MIXED SGD with cached gradients) runs one 256-thread block
+// open.  The four-element update (MIXED SGD momentum, cached gradients) runs one 256-thread block
 // per chunk, one vector per lane, at most kUpdBlocksPerCU blocks per CU; for it 16K-element
 // chunks, a persistent grid, two or four vectors per lane, 512-thread blocks and unlimited
 // occupancy each measured 3-12% slower (as a four-element Adam update, which the lane forms
@@ -717,10 +717,10 @@ __device__ __forceinline__ void sgd_elem(float& p, float g, float& b, const SgdA
 }
 
 // The four-element SGD update: one block per chunk (grid == nchunks), blocks in reverse chunk
-// order, one 4-element vector per lane, for MIXED gradients that fit the Infinity Cache (at
-// most 2^17 chunks), at most kUpdBlocksPerCU blocks per CU.  master is the master slot base
-// (MIXED: slot 0 of
-// the [master|m|v] records; FP32: the contiguous weights); momentum is contiguous.
+// order, one 4-element vector per lane, for MIXED momentum steps whose gradients fit the
+// Infinity Cache (at most 2^17 chunks), at most kUpdBlocksPerCU blocks per CU.  master is
+// the master slot base (MIXED: slot 0 of the [master|m|v] records; FP32: the contiguous
+// weights); momentum is contiguous.
 template <typename GradT, bool kMixed>
 __global__ __launch_bounds__(kUpdBlock) void sgd_kernel(const GradT* __restrict__ grad,
                                                         float* __restrict__ master,

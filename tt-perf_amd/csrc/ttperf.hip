@@ -537,7 +537,8 @@ int set_dev(const ttp_ctx* c) {
 }
 
 // whether the gradients of an update over `w` fit the Infinity Cache (see kCachedGradBytes):
-// MIXED SGD then runs the four-element kernel, MIXED Adam its cached-gradient lane shape.
+// MIXED SGD momentum then runs the four-element kernel, MIXED Adam its cached-gradient lane
+// shape.
 // The four-element kernel launches one 256-lane block per chunk in one launch, which holds
 // at most 2^32 - 1 work-items; a set of that many chunks (millions of tiny tensors) counts as
 // not cached and takes the lane forms, which split.
@@ -550,8 +551,8 @@ bool grads_cached(const ttp_ctx* c, const WorkTables* w) {
 // 2^30 work-items, well inside the 2^32 a launch may hold; they loop over the rest.
 constexpr uint32_t kMaxGridBlocks = 1u << 22;
 
-// MIXED SGD updates whose gradients fit the Infinity Cache run the four-element kernel, one
-// block per chunk (at most 2^17 chunks); every other update runs a lane form: kE elements per
+// MIXED SGD momentum updates whose gradients fit the Infinity Cache run the four-element
+// kernel, one block per chunk (at most 2^17 chunks); every other update runs a lane form: kE elements per
 // lane in blocks of kLanes, each block walking kIt consecutive pieces of kLanes x kE
 // elements, one block per 1/lane_parts<kE, kLanes, kIt>() of a chunk.
 // MIXED Adam with cached gradients (GPT-2 124M; whole steps of bench.py after its settle
@@ -588,6 +589,18 @@ constexpr int kLaneAdamMixed = 1, kLanesAdamMixed = 256, kItAdamMixed = 2;
 constexpr int kLaneAdamFp32 = 1, kLanesAdamFp32 = 128, kItAdamFp32 = 2;
 constexpr int kLaneSgdMixed = 1, kLanesSgdMixed = 256, kItSgdMixed = 2;
 constexpr int kLaneSgdFp32 = 2, kLanesSgdFp32 = 64, kItSgdFp32 = 1;
+// MIXED SGD without momentum (the traced layers' sgd_step, autograd::SGD) moves 12 B per
+// element, a third of them as bf16: two elements per lane make its gradient loads and bf16
+// stores 4-byte words.  Step times, ms (back to back / after a device copy of the gradients,
+// the copy excluded; 50 steps per event pair, two interleaved rounds on one box):
+//   GPT-2 774M   2 x 256 x 1  1.611 / 1.593   (2 x 128 x 1 1.655 / 1.640, 1 x 256 x 2
+//                2.074 / 2.062, the four-element form 1.635 / 1.618)
+//   GPT-2 124M   2 x 256 x 1  0.268 / 0.261   (2 x 128 x 1 0.249 / 0.270, the four-element
+//                form 0.274 / 0.269, 1 x 256 x 2 0.314 back to back)
+// 5.76 TB/s at 774M, against 5.98 TB/s for the FP32 store's plain SGD (contiguous weights)
+// and 4.48 TB/s for the 1 x 256 x 2 shape that momentum prefers.  One shape at every size:
+// after a gradient rewrite, as in training, it is the fastest at both sizes.
+constexpr int kLaneSgdPlainMixed = 2, kLanesSgdPlainMixed = 256, kItSgdPlainMixed = 1;
 
 // One launch holds at most 2^32 - 1 work-items, so at most (2^32 - 1) / lanes blocks.  A
 // lane-form update over more parts is split into launches at increasing part offsets
@@ -983,7 +996,7 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
     c->stream = c->own_stream;
 
     {
-        // occupancy cap of the four-element update (MIXED SGD with cached gradients):
+        // occupancy cap of the four-element update (MIXED SGD momentum, cached gradients):
         // LDS_per_CU / blocks_per_CU bytes of dynamic LDS per block
         int lds_cu = 0, lds_blk = 0;
         const uint64_t per_cu = env_u64("TTP_UPD_BLOCKS_PER_CU", ttp::kUpdBlocksPerCU);
@@ -1536,7 +1549,18 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
         ttp::SgdArgs al = a;
         al.st = c->st;  // the lane forms read the device state unconditionally
         clear_hip_error();
-        if (grads_cached(c, w) && c->mode == TTP_MODE_MIXED)
+        if (!mom && c->mode == TTP_MODE_MIXED)
+            launch_lanes(c,
+                         (uint64_t)n * ttp::lane_parts<kLaneSgdPlainMixed, kLanesSgdPlainMixed,
+                                                       kItSgdPlainMixed>(),
+                         kLanesSgdPlainMixed, [&](dim3 g, uint64_t p0) {
+                hipLaunchKernelGGL(
+                    (ttp::sgd_lane_kernel<uint16_t, true, kLaneSgdPlainMixed, kLanesSgdPlainMixed,
+                                          kItSgdPlainMixed>), g,
+                    dim3(kLanesSgdPlainMixed), 0, c->stream, g16, c->master, c->momentum, p16, al,
+                    p0);
+            });
+        else if (grads_cached(c, w) && c->mode == TTP_MODE_MIXED)
             hipLaunchKernelGGL((ttp::sgd_kernel<uint16_t, true>), dim3(n), block, c->upd_lds,
                                c->stream, g16, c->master, c->momentum, p16, a);
         else if (c->mode == TTP_MODE_MIXED)
