@@ -488,7 +488,10 @@ def cpp_dropin(steps, warmup, settle_ms):
         return {"error": f"{exe} is not built (make -C tests/cpp)"}
     env = dict(os.environ, BENCH_ITERS=str(steps), BENCH_WARMUP=str(warmup),
                BENCH_SETTLE_MS=str(int(settle_ms)))
-    p = subprocess.run([exe], capture_output=True, text=True, timeout=300, env=env)
+    try:
+        p = subprocess.run([exe], capture_output=True, text=True, timeout=300, env=env)
+    except subprocess.TimeoutExpired:
+        return {"error": f"{exe} did not finish within 300 s"}
     line = next((ln for ln in p.stdout.splitlines() if ln.startswith('{"bench"')), None)
     if p.returncode != 0 or line is None:
         return {"error": f"exit {p.returncode}: {(p.stdout + p.stderr)[-500:]}"}
