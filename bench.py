@@ -113,9 +113,12 @@ def settle(step, ms):
     return n, round((time.perf_counter() - t0) * 1e3, 1)
 
 
-def traffic_from_profiles(config):
-    """HBM bytes per update launch from the committed rocprofv3 --pmc summary, if any."""
-    path = os.path.join(REPO, "profiles", f"adam_kernel_{config}_pmc.md")
+def traffic_from_profiles(config, optimizer):
+    """HBM bytes per update launch from the committed rocprofv3 --pmc summary of the AdamW
+    update, if any (none is committed for the SGD updates)."""
+    if optimizer != "adamw":
+        return None
+    path = os.path.join(REPO, "profiles", f"adam_lane_kernel_{config}_pmc.md")
     if not os.path.exists(path):
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
@@ -737,7 +740,7 @@ def main():
                                "update's byte count; 10 launches between one event pair"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic_from_profiles(args.config),
+                     "traffic": traffic_from_profiles(args.config, args.optimizer),
                      "kernel": upd_kernel,
                      "algorithmic_bytes_per_launch": n_params * ub},
         "cpu_baseline": None,
