@@ -178,15 +178,21 @@ int run(uint32_t seq, uint32_t dim, uint32_t heads, uint32_t ffn, uint32_t vocab
 
 int main() {
     test::DeviceGuard dg;
-    // GPT-2 small by default; the reference's bench defaults are the nano_gpt shapes
-    const uint32_t seq = env_u32("BENCH_SEQ", 1024), dim = env_u32("BENCH_DIM", 768);
-    const uint32_t heads = env_u32("BENCH_HEADS", 12), ffn = env_u32("BENCH_FFN_MULT", 4);
-    const uint32_t vocab = env_u32("BENCH_VOCAB", 50257), layers = env_u32("BENCH_LAYERS", 12);
-    if (!heads || dim % heads != 0) {
-        std::printf("ERROR: dim (%u) must be divisible by heads (%u)\n", dim, heads);
-        return 1;
-    }
     try {
+        // GPT-2 small by default; the reference's bench defaults are the nano_gpt shapes
+        const uint32_t seq = env_u32("BENCH_SEQ", 1024), dim = env_u32("BENCH_DIM", 768);
+        const uint32_t heads = env_u32("BENCH_HEADS", 12), ffn = env_u32("BENCH_FFN_MULT", 4);
+        const uint32_t vocab = env_u32("BENCH_VOCAB", 50257);
+        const uint32_t layers = env_u32("BENCH_LAYERS", 12);
+        if (!heads || dim % heads != 0) {
+            std::printf("ERROR: dim (%u) must be divisible by heads (%u)\n", dim, heads);
+            return 1;
+        }
+        if (!seq || !dim || !ffn || !vocab || !env_u32("BENCH_ITERS", 50)) {
+            std::printf("ERROR: BENCH_SEQ, BENCH_DIM, BENCH_FFN_MULT, BENCH_VOCAB and "
+                        "BENCH_ITERS must be positive\n");
+            return 1;
+        }
         switch (layers) {
             case 1: return run<1>(seq, dim, heads, ffn, vocab);
             case 2: return run<2>(seq, dim, heads, ffn, vocab);
