@@ -116,6 +116,9 @@ struct Adam {
         if (!(betas.first > 0 && betas.first < 1 && betas.second > 0 && betas.second < 1))
             throw std::invalid_argument("betas must be in (0, 1)");
         if (!(weight_decay >= 0)) throw std::invalid_argument("weight_decay must be >= 0");
+        // an arena whose store does not exist yet is then created in Adam's layout
+        for (const auto& p : params)
+            if (p) p->arena->adam_declared = true;
         opts.lr = lr;
         opts.beta1 = betas.first;
         opts.beta2 = betas.second;

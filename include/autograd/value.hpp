@@ -21,17 +21,32 @@ namespace autograd {
 
 class ParamArena;
 
+// Which store layout an arena creates (ttp::Layout).  Auto: the SGD layout for a Mixed
+// arena, unless an Adam / AdamW over its parameters was constructed before the store exists
+// (the store is created on first use).  An Adam constructed later converts the store at its
+// first step, once.
+enum class ArenaLayout { Auto, Default, Sgd };
+
 struct ArenaState {
     ttp::Mode mode = ttp::Mode::FP32;
     int device = 0;
+    ArenaLayout layout = ArenaLayout::Auto;
+    bool adam_declared = false;  // an Adam over this arena's parameters was constructed
     std::vector<ttp::TensorSpec> specs;
     std::vector<std::vector<float>> init;  // initial fp32 weights (uploaded at creation)
     std::vector<bool> grad_always;         // pre-allocated grads (traced/static layers)
     std::unique_ptr<ttp::Store> store;
 
+    ttp::Layout store_layout() const {
+        if (layout == ArenaLayout::Sgd) return ttp::Layout::Sgd;
+        if (layout == ArenaLayout::Default) return ttp::Layout::Default;
+        return mode == ttp::Mode::Mixed && !adam_declared ? ttp::Layout::Sgd
+                                                          : ttp::Layout::Default;
+    }
+
     ttp::Store& get() {
         if (!store) {
-            store = std::make_unique<ttp::Store>(specs, mode, device);
+            store = std::make_unique<ttp::Store>(specs, mode, device, store_layout());
             for (uint32_t i = 0; i < specs.size(); ++i) {
                 if (!init[i].empty()) store->set_weights(i, init[i]);
                 if (grad_always[i]) store->set_has_grad(i, true);
@@ -107,10 +122,12 @@ struct Value {
 // Declares parameters; all of them live in one store created on first use.
 class ParamArena {
 public:
-    explicit ParamArena(ttp::Mode mode = ttp::Mode::FP32, int device = 0)
+    explicit ParamArena(ttp::Mode mode = ttp::Mode::FP32, int device = 0,
+                        ArenaLayout layout = ArenaLayout::Auto)
         : s_(std::make_shared<ArenaState>()) {
         s_->mode = mode;
         s_->device = device;
+        s_->layout = layout;
     }
 
     ValuePtr parameter(std::vector<uint64_t> shape, std::vector<float> init = {},

@@ -56,7 +56,15 @@
 extern "C" {
 #endif
 
-#define TTP_ABI_VERSION 1
+/* ABI version, returned by ttp_abi_version().  Changes:
+ *   2  TTP_STORE_SGD (the SGD layout of a MIXED store, OR'd into ttp_create's mode).
+ *      Behaviour changes of existing entry points, which a caller written against version 1
+ *      must follow: ttp_zero_grad_subset with set_to_none = 0 leaves the has-grad flags as
+ *      they were (version 1 marked the listed tensors as having a grad); a captured
+ *      ttp_accumulate_grad is refused unless an earlier call of the same capture set that
+ *      tensor's has-grad flag.
+ *   1  first version. */
+#define TTP_ABI_VERSION 2
 
 /* ---- status codes ---------------------------------------------------------------- */
 #define TTP_OK 0
@@ -70,6 +78,28 @@ extern "C" {
 /* ---- precision modes -------------------------------------------------------------- */
 #define TTP_MODE_FP32 0  /* fp32 params/grads; the param buffer is the master copy    */
 #define TTP_MODE_MIXED 1 /* bf16 params/grads + fp32 master; bf16 param = RNE(master) */
+
+/* ---- store layout flags, OR'd into ttp_create's mode -------------------------------- */
+/* TTP_STORE_SGD: the SGD layout of a MIXED store.  By default a MIXED store keeps each
+ * 64-element group's fp32 master, m and v side by side in one [master|m|v] record (Adam reads
+ * and writes all three in one pass).  A store stepped only by SGD never touches m and v, and
+ * its update would read the master as one 256-byte slot of every 768-byte record.  With this
+ * flag the fp32 master is one contiguous buffer and no m / v exist (4 B/param instead of
+ * 12 B/param of optimizer state), which lets the SGD update stream its four buffers (bf16
+ * grad, master read and write, bf16 weights) like a copy.  The first Adam step, or any call
+ * that asks for EXP_AVG / EXP_AVG_SQ (ttp_buffer_ptr, ttp_buffer_layout, ttp_upload,
+ * ttp_download, ttp_load_state of a file holding them), converts the store to the default
+ * layout once: it allocates the records, moves the master into them (values unchanged) and
+ * frees the contiguous copy, waiting for the queued work.  That conversion is refused
+ * (TTP_ERR_STATE, nothing changed) while capturing, while graphs of the context are alive
+ * (they hold the old master's address) and by ttp_adam_step_noalloc.  A master pointer from
+ * ttp_buffer_ptr is invalid after it.  ttp_mode reports the precision mode only; the layout
+ * shows in ttp_buffer_layout (MASTER: stride 64 in the SGD layout, 192 in the default one).
+ * In FP32 mode the master is the contiguous model-facing weight and m, v are allocated on
+ * first Adam use anyway, so the flag changes nothing there.  Checkpoint files do not depend
+ * on the layout.  No counterpart in the reference, whose SGD updates each parameter's own
+ * tensor (autograd/dynamic/optim.hpp:21-27, autograd/traced/nn.hpp:93-96). */
+#define TTP_STORE_SGD 0x100
 
 /* ---- buffers of the flat store ---------------------------------------------------- */
 #define TTP_BUF_PARAM 0      /* model-facing weights: fp32 (FP32) or bf16 (MIXED)       */
@@ -184,6 +214,7 @@ typedef struct ttp_step_report {
 
 /* ---- context lifetime --------------------------------------------------------------- */
 int ttp_device_count(int* count);
+/* mode: TTP_MODE_FP32 or TTP_MODE_MIXED, optionally | TTP_STORE_SGD. */
 int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n_tensors, int mode,
                ttp_ctx** out);
 int ttp_destroy(ttp_ctx* ctx);
@@ -206,7 +237,8 @@ int ttp_tensor_info(const ttp_ctx* ctx, uint32_t index, uint64_t* offset, uint64
                     uint32_t* flags);
 /* Device address of buffer `which` for tensor `index` (or the flat base for
  * TTP_ALL_TENSORS), for the buffers stored contiguously: PARAM, GRAD and MOMENTUM always,
- * MASTER in FP32 mode (where it is PARAM).  The optimizer-private fp32 state is kept in
+ * MASTER in FP32 mode (where it is PARAM) and in a MIXED store's SGD layout.  The
+ * optimizer-private fp32 state is otherwise kept in
  * interleaved records (MIXED: master, m and v of each 64-element group side by side; FP32:
  * m and v), for which this returns TTP_ERR_STATE; use ttp_buffer_layout, or ttp_upload /
  * ttp_download, which convert.  Moment/momentum buffers are allocated on first use; asking
@@ -216,8 +248,9 @@ int ttp_buffer_ptr(ttp_ctx* ctx, int which, uint32_t index, void** ptr);
 /* Addressing of any buffer: flat element e of `which` sits at
  *   base + (e / group) * stride + e % group   (in elements of the buffer's type).
  * group == stride for a contiguous buffer; MIXED-mode MASTER/EXP_AVG/EXP_AVG_SQ have
- * group 64, stride 192 (slots 0, 1, 2 of one record); FP32-mode EXP_AVG/EXP_AVG_SQ group 64,
- * stride 128.  Each tensor starts on a record boundary.  Allocates like ttp_buffer_ptr.
+ * group 64, stride 192 (slots 0, 1, 2 of one record), except MASTER in the SGD layout
+ * (TTP_STORE_SGD: contiguous); FP32-mode EXP_AVG/EXP_AVG_SQ group 64, stride 128.  Each
+ * tensor starts on a record boundary.  Allocates like ttp_buffer_ptr.
  * No counterpart in the reference, whose optimizer state is private per-tensor ttnn
  * tensors (py/optim.py:58-71). */
 int ttp_buffer_layout(ttp_ctx* ctx, int which, void** base, uint32_t* group, uint32_t* stride);

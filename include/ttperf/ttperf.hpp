@@ -30,6 +30,11 @@ inline void check(int rc) {
 }
 
 enum class Mode { FP32 = TTP_MODE_FP32, Mixed = TTP_MODE_MIXED };
+// Store layout of a Mixed store (TTP_STORE_SGD): Default keeps master, m and v in shared
+// records (Adam's layout); Sgd keeps a contiguous master and no m / v, for stores that SGD
+// steps (the first Adam step converts it to Default).  FP32 stores are laid out alike either
+// way.
+enum class Layout { Default = 0, Sgd = TTP_STORE_SGD };
 
 struct TensorSpec {
     std::vector<uint64_t> shape;
@@ -134,7 +139,14 @@ private:
 
 class Store {
 public:
-    Store(const std::vector<TensorSpec>& specs, Mode mode, int device = 0) : specs_(specs), mode_(mode) {
+    Store(const std::vector<TensorSpec>& specs, Mode mode, int device = 0,
+          Layout layout = Layout::Default)
+        : specs_(specs), mode_(mode) {
+        // a library built against another ABI version would read these arguments differently
+        if (ttp_abi_version() != TTP_ABI_VERSION)
+            throw std::runtime_error("libttperf_hip implements ABI version " +
+                                     std::to_string(ttp_abi_version()) + ", this header " +
+                                     std::to_string(TTP_ABI_VERSION));
         std::vector<ttp_tensor_desc> d(specs.size());
         for (size_t i = 0; i < specs.size(); ++i) {
             d[i].numel = specs[i].numel();
@@ -142,7 +154,7 @@ public:
             d[i].reserved = 0;
         }
         ttp_ctx* c = nullptr;
-        check(ttp_create(device, d.data(), (uint32_t)d.size(), (int)mode, &c));
+        check(ttp_create(device, d.data(), (uint32_t)d.size(), (int)mode | (int)layout, &c));
         ctx_ = c;
     }
     ~Store() {
@@ -154,6 +166,13 @@ public:
     ttp_ctx* get() const { return ctx_; }
     uint64_t uid() const { return uid_; }
     Mode mode() const { return mode_; }
+    // Sgd while a Mixed store keeps the SGD layout's contiguous master (until an Adam step)
+    Layout layout() const {
+        void* base = nullptr;
+        uint32_t group = 0, stride = 0;
+        check(ttp_buffer_layout(ctx_, TTP_BUF_MASTER, &base, &group, &stride));
+        return mode_ == Mode::Mixed && stride == group ? Layout::Sgd : Layout::Default;
+    }
     size_t size() const { return specs_.size(); }
     const TensorSpec& spec(uint32_t i) const { return specs_.at(i); }
     uint64_t numel(uint32_t i) const { return specs_.at(i).numel(); }

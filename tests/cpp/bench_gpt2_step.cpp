@@ -5,12 +5,15 @@
 // traced::TracedTransformerWithEmbedding<N> from BENCH_* environment variables
 // (:103-121), runs warmup iterations, then times N_ITERS train steps between two device
 // synchronisations with std::chrono.  This program builds the same model class over a
-// mixed-precision ParamArena (bf16 weights and gradients, fp32 master, m and v) at GPT-2
-// small dimensions by default and times, the same way, the two optimizer surfaces a
-// training loop calls on it:
+// mixed-precision ParamArena (bf16 weights and gradients, fp32 master) at GPT-2 small
+// dimensions by default and times, the same way, the two optimizer surfaces a training loop
+// calls on it, each on a model of its own:
 //   - autograd::AdamW over model.parameters(), with dynamic loss scaling (2^16, growth 2x
-//     every 2000 clean steps, backoff 0.5) and a global grad-norm clip at 1.0;
-//   - the model's own sgd_step() (autograd/traced/transformer_train.hpp:487-494).
+//     every 2000 clean steps, backoff 0.5) and a global grad-norm clip at 1.0; the AdamW is
+//     declared before the store exists, so the arena lays out master, m and v in records;
+//   - the model's own sgd_step() (autograd/traced/transformer_train.hpp:487-494) on a model
+//     whose arena only SGD steps, which therefore takes the SGD layout (contiguous master,
+//     no m and v).
 // The forward and backward passes are not part of this engine; the gradients are written
 // once from the host, scaled by the loss scale.  Before the timed steps each surface runs
 // back to back for BENCH_SETTLE_MS (200 by default): the GPU leaves its idle clocks during
@@ -100,7 +103,11 @@ int run(uint32_t seq, uint32_t dim, uint32_t heads, uint32_t ffn, uint32_t vocab
     const std::vector<ValuePtr> params = model.parameters();
     uint64_t numel = 0;
     for (auto& p : params) numel += p->numel();
+    // 1) AdamW (config of the GPT-2 runs: lr 6e-4, betas (0.9, 0.95), wd 0.1, clip 1.0),
+    // declared before the store exists: Adam's layout
+    autograd::AdamW opt(params, 6e-4f, {0.9, 0.95}, 1e-8f, 0.1f, 1.0);
     ttp::Store& store = arena.store();
+    test::check(store.layout() == ttp::Layout::Default, "AdamW's arena: the default layout");
     store.configure_scaler(init_scale, 2.0, 0.5, 2000, true);
     for (size_t k = 0; k < params.size(); ++k)
         params[k]->grad = grad_values(params[k]->numel(), 1e-3f * (float)init_scale, (uint32_t)k);
@@ -108,8 +115,6 @@ int run(uint32_t seq, uint32_t dim, uint32_t heads, uint32_t ffn, uint32_t vocab
                 "ffn_mult=%u vocab=%u; %zu tensors, %llu params, mixed precision\n",
                 N, seq, dim, heads, ffn, vocab, params.size(), (unsigned long long)numel);
 
-    // 1) AdamW (config of the GPT-2 runs: lr 6e-4, betas (0.9, 0.95), wd 0.1, clip 1.0)
-    autograd::AdamW opt(params, 6e-4f, {0.9, 0.95}, 1e-8f, 0.1f, 1.0);
     uint64_t adam_steps = 0;
     const Timing ta = time_steps(store, [&] { opt.step(); }, settle_ms, warmup, iters, &adam_steps);
     const double adam_gps = (double)numel / (ta.ms_per_step * 1e-3) / 1e9;
@@ -145,29 +150,39 @@ int run(uint32_t seq, uint32_t dim, uint32_t heads, uint32_t ffn, uint32_t vocab
                       "an overflow step leaves the embedding");
     probe->grad = g_keep;
 
-    // 3) the model's sgd_step (w - lr*g per tensor, no loss scale): timed, then one exact check
-    store.configure_scaler(init_scale, 2.0, 0.5, 2000, false);
+    // 3) sgd_step (w - lr*g per tensor, no loss scale) on a second model whose arena only SGD
+    // steps: timed, then one exact check
+    ParamArena sgd_arena(ttp::Mode::Mixed);
+    traced::TracedTransformerWithEmbedding<N> sgd_model(/*batch=*/8, seq, dim, heads, ffn, vocab,
+                                                        sgd_lr, sgd_arena);
+    const std::vector<ValuePtr> sgd_params = sgd_model.parameters();
+    ttp::Store& sgd_store = sgd_arena.store();
+    test::check(sgd_store.layout() == ttp::Layout::Sgd, "sgd_step's arena: the SGD layout");
+    for (size_t k = 0; k < sgd_params.size(); ++k)
+        sgd_params[k]->grad = grad_values(sgd_params[k]->numel(), 1e-3f, (uint32_t)k);
     uint64_t sgd_steps = 0;
-    const Timing ts =
-        time_steps(store, [&] { model.sgd_step(); }, settle_ms, warmup, iters, &sgd_steps);
+    const Timing ts = time_steps(sgd_store, [&] { sgd_model.sgd_step(); }, settle_ms, warmup,
+                                 iters, &sgd_steps);
     const double sgd_gps = (double)numel / (ts.ms_per_step * 1e-3) / 1e9;
     std::printf("sgd_step: %.4f ms/step, %.1f Gparams/s (%.0f GB/s at 12 B/param)\n",
                 ts.ms_per_step, sgd_gps, sgd_gps * 12.0);
     {
-        const std::vector<float> w0 = probe->master(), g = probe->grad.value();
-        model.sgd_step();
+        const ValuePtr& sp = sgd_model.layers[0].ln1.beta;
+        const std::vector<float> w0 = sp->master(), g = sp->grad.value();
+        sgd_model.sgd_step();
         std::vector<float> want(w0.size());
         for (size_t i = 0; i < w0.size(); ++i) {
             const float update = g[i] * sgd_lr;
             want[i] = w0[i] - update;
         }
-        test::assert_bits(probe->master(), want, "sgd_step = w - lr*g");
+        test::assert_bits(sp->master(), want, "sgd_step = w - lr*g");
     }
 
     std::printf("{\"bench\": \"gpt2_step_dropin\", \"layers\": %zu, \"tensors\": %zu, "
                 "\"params\": %llu, \"adamw_ms_per_step\": %.5f, \"adamw_Gparams_per_s\": %.2f, "
                 "\"adamw_settle_steps\": %d, \"sgd_ms_per_step\": %.5f, "
-                "\"sgd_Gparams_per_s\": %.2f, \"sgd_settle_steps\": %d, \"warmup\": %u, "
+                "\"sgd_Gparams_per_s\": %.2f, \"sgd_settle_steps\": %d, \"sgd_layout\": \"sgd\", "
+                "\"warmup\": %u, "
                 "\"iters\": %u}\n",
                 N, params.size(), (unsigned long long)numel, ta.ms_per_step, adam_gps,
                 ta.settle_steps, ts.ms_per_step, sgd_gps, ts.settle_steps, warmup, iters);

@@ -4,6 +4,7 @@
 // and TracedMLP<N>::sgd_step (autograd/traced/mlp.hpp:106-110).
 // Each sgd_step must update exactly its module's tensors, bit-exact against `w - lr*dw`
 // (one rounding per op, bf16 weights = RNE of the fp32 master), in ONE update launch.
+#include "autograd/optim.hpp"
 #include "autograd/static.hpp"
 #include "autograd/traced.hpp"
 #include "common.hpp"
@@ -107,6 +108,8 @@ int main() {
         test::check(ps.size() == 2 + 2 * 16 + 2, "GPT parameter count 36");
         Ref r = snapshot(ps, true, 2.0f);
         ttp::Store& store = arena.store();
+        test::check(store.layout() == ttp::Layout::Sgd,
+                    "a Mixed arena no Adam was declared over takes the SGD layout");
         ttp::check(ttp_timing_enable(store.get(), 1));
         update_launches(store);
         gpt.sgd_step();
@@ -146,6 +149,36 @@ int main() {
         stack.sgd_step();
         for (size_t k = 0; k < ps.size(); ++k) apply(r, k, 0.2f);
         check_all(ps, r, false, "stack sgd_step");
+    }
+    // ---- arena layouts: an Adam declared before first use gets Adam's layout; one declared
+    // after converts the SGD layout at its first step, from the values SGD left ----------
+    {
+        ParamArena a(ttp::Mode::Mixed);
+        auto w = a.parameter({300}, ramp(300, 0.1f, 0.001f), "w", true);
+        autograd::AdamW opt({w}, 1e-3f);
+        test::check(a.store().layout() == ttp::Layout::Default,
+                    "an Adam declared before first use: the default layout");
+        ParamArena b(ttp::Mode::Mixed);
+        auto v = b.parameter({300}, ramp(300, 0.1f, 0.001f), "v", true);
+        v->grad = ramp(300, 0.02f, 0.0005f);
+        autograd::SGD sgd({v}, 0.1f);
+        sgd.step();
+        test::check(b.store().layout() == ttp::Layout::Sgd, "SGD alone: the SGD layout");
+        const std::vector<float> before = v->master();
+        autograd::AdamW late({v}, 1e-3f, {0.9, 0.95}, 1e-8f, 0.0f);
+        late.step();
+        test::check(b.store().layout() == ttp::Layout::Default,
+                    "a later Adam step converts the store");
+        // AdamW's first step with wd 0 moves each weight by lr * sign(g) (m_hat / sqrt(v_hat)
+        // is g / |g| up to eps): check that it started from the SGD-updated master
+        const std::vector<float> after = v->master(), g = v->grad.value();
+        size_t bad = 0;
+        for (size_t i = 0; i < after.size(); ++i) {
+            const float moved = before[i] - after[i];
+            const float want = g[i] > 0 ? 1e-3f : (g[i] < 0 ? -1e-3f : 0.0f);
+            bad += std::fabs(moved - want) > 1e-6f;
+        }
+        test::check(bad == 0, "the converted store's first Adam step starts from SGD's master");
     }
     return test::finish("test_modules");
 }

@@ -7,6 +7,7 @@
 // Device memory for the TTP_DEVICE transfers comes from a second context's flat grad buffer,
 // so the test needs only the C ABI.
 #include <cstdio>
+#include <cstring>
 #include <string>
 #include <vector>
 
@@ -195,10 +196,123 @@ void run_mode(int mode) {
     ttp_destroy(c);
 }
 
+// The SGD layout of a MIXED store (TTP_STORE_SGD): a contiguous master and no m / v.  Master
+// uploads keep the bf16 copy; plain and momentum SGD steps give w - lr*g and torch's first
+// momentum step; the first use of m / v converts the store to the record layout with the
+// master unchanged, and that conversion is refused while capturing and while graphs live.
+void run_sgd_layout() {
+    const std::vector<uint64_t> numel = {0, 1, 3, 63, 64, 65, 1000, 2049, 100003};
+    ttp_ctx* c = create(numel, TTP_MODE_MIXED | TTP_STORE_SGD);
+    int mode = -1;
+    test::check(ttp_mode(c, &mode) == TTP_OK && mode == TTP_MODE_MIXED,
+                "ttp_mode reports the precision mode of an SGD-layout store");
+    uint64_t total = 0;
+    ttp_flat_numel(c, &total);
+    std::vector<uint64_t> off(numel.size());
+    for (uint32_t i = 0; i < numel.size(); ++i) ttp_tensor_info(c, i, &off[i], nullptr, nullptr);
+    void* base = nullptr;
+    uint32_t group = 0, stride = 0;
+    test::check(ttp_buffer_layout(c, TTP_BUF_MASTER, &base, &group, &stride) == TTP_OK &&
+                    group == 64 && stride == 64,
+                "SGD layout: the master is contiguous");
+    void* p3 = nullptr;
+    test::check(ttp_buffer_ptr(c, TTP_BUF_MASTER, 3, &p3) == TTP_OK &&
+                    p3 == (char*)base + off[3] * 4,
+                "SGD layout: master pointer of a tensor");
+    std::vector<std::vector<float>> w(numel.size()), g(numel.size());
+    for (uint32_t i = 0; i < numel.size(); ++i) {
+        w[i] = randn(numel[i], 700 + i);
+        g[i] = randn(numel[i], 800 + i);
+        test::check(ttp_upload(c, TTP_BUF_MASTER, i, w[i].data(), w[i].size(), TTP_HOST) == TTP_OK,
+                    std::string("sgd layout upload master: ") + ttp_last_error());
+        auto p = download16(c, TTP_BUF_PARAM, i, numel[i]);
+        size_t bad = 0;
+        for (size_t k = 0; k < p.size(); ++k) bad += p[k] != to_bf16(w[i][k]);
+        test::check(bad == 0, "SGD layout: bf16 copy of an uploaded master");
+        std::vector<uint16_t> h(numel[i]);
+        for (size_t k = 0; k < h.size(); ++k) {
+            h[k] = to_bf16(g[i][k]);
+            const uint32_t u = (uint32_t)h[k] << 16;
+            std::memcpy(&g[i][k], &u, 4);  // the gradient value the store holds
+        }
+        ttp_upload(c, TTP_BUF_GRAD, i, h.data(), h.size(), TTP_HOST);
+    }
+    // plain SGD: w - (g*lr), rounded after the multiply and after the subtract
+    const float lr = 0.01f;
+    ttp_sgd_hparams plain = {lr, 0.0, 0.0, 0.0, 0, 0, 0.0};
+    test::check(ttp_sgd_step(c, &plain, nullptr) == TTP_OK, std::string("sgd: ") + ttp_last_error());
+    for (uint32_t i = 0; i < numel.size(); ++i)
+        for (size_t k = 0; k < w[i].size(); ++k) {
+            const float update = g[i][k] * lr;
+            w[i][k] = w[i][k] - update;
+        }
+    for (uint32_t i = 0; i < numel.size(); ++i)
+        test::assert_bits(download(c, TTP_BUF_MASTER, i, numel[i]), w[i],
+                          "SGD layout: plain step, tensor " + std::to_string(i));
+    // momentum 0.9: the first step stores buf = g and applies w - buf*lr
+    ttp_sgd_hparams mom = {lr, 0.9, 0.0, 0.0, 0, 0, 0.0};
+    test::check(ttp_sgd_step(c, &mom, nullptr) == TTP_OK, std::string("sgd m: ") + ttp_last_error());
+    for (uint32_t i = 0; i < numel.size(); ++i) {
+        for (size_t k = 0; k < w[i].size(); ++k) {
+            const float update = g[i][k] * lr;
+            w[i][k] = w[i][k] - update;
+        }
+        test::assert_bits(download(c, TTP_BUF_MASTER, i, numel[i]), w[i],
+                          "SGD layout: first momentum step, tensor " + std::to_string(i));
+        test::assert_bits(download(c, TTP_BUF_MOMENTUM, i, numel[i]), g[i],
+                          "SGD layout: first momentum buffer, tensor " + std::to_string(i));
+        auto p = download16(c, TTP_BUF_PARAM, i, numel[i]);
+        size_t bad = 0;
+        for (size_t k = 0; k < p.size(); ++k) bad += p[k] != to_bf16(w[i][k]);
+        test::check(bad == 0, "SGD layout: bf16 weights after the steps");
+    }
+
+    // the conversion is refused while capturing and while a graph lives
+    test::check(ttp_capture_begin(c) == TTP_OK, "capture begin");
+    ttp_adam_hparams hp = {1e-3, 0.9, 0.95, 1e-8, 0.1, 1, 0, 0.0};
+    test::check(ttp_adam_step(c, &hp, nullptr) == TTP_ERR_STATE, "no conversion while capturing");
+    test::check(ttp_sgd_step(c, &plain, nullptr) == TTP_OK, "capture an SGD step");
+    ttp_graph* graph = nullptr;
+    test::check(ttp_capture_end(c, &graph) == TTP_OK && graph, "capture end");
+    test::check(ttp_buffer_layout(c, TTP_BUF_EXP_AVG, nullptr, nullptr, nullptr) == TTP_ERR_STATE,
+                "no conversion while a graph lives");
+    test::check(ttp_adam_step_noalloc(c, &hp, nullptr, 0) == TTP_ERR_STATE,
+                "the no-allocation step does not convert");
+    test::check(ttp_graph_launch(graph) == TTP_OK, "graph launch");
+    for (uint32_t i = 0; i < numel.size(); ++i)
+        for (size_t k = 0; k < w[i].size(); ++k) {
+            const float update = g[i][k] * lr;
+            w[i][k] = w[i][k] - update;
+        }
+    test::check(ttp_graph_destroy(graph) == TTP_OK, "graph destroy");
+    ttp_buffer_layout(c, TTP_BUF_MASTER, nullptr, &group, &stride);
+    test::check(stride == 64, "a refused conversion leaves the SGD layout");
+
+    // asking for m converts: master and bf16 weights unchanged, m and v zero
+    const auto p16_before = download16(c, TTP_BUF_PARAM, TTP_ALL_TENSORS, total);
+    test::check(ttp_buffer_layout(c, TTP_BUF_EXP_AVG, nullptr, &group, &stride) == TTP_OK &&
+                    stride == 192,
+                std::string("conversion on first use of m: ") + ttp_last_error());
+    ttp_buffer_layout(c, TTP_BUF_MASTER, nullptr, &group, &stride);
+    test::check(stride == 192, "after the conversion the master sits in the records");
+    for (uint32_t i = 0; i < numel.size(); ++i)
+        test::assert_bits(download(c, TTP_BUF_MASTER, i, numel[i]), w[i],
+                          "conversion keeps the master, tensor " + std::to_string(i));
+    test::check(download16(c, TTP_BUF_PARAM, TTP_ALL_TENSORS, total) == p16_before,
+                "conversion keeps the bf16 weights");
+    test::assert_bits(download(c, TTP_BUF_EXP_AVG_SQ, TTP_ALL_TENSORS, total),
+                      std::vector<float>(total, 0.0f), "conversion: v starts at zero");
+    test::check(ttp_adam_step(c, &hp, nullptr) == TTP_OK, std::string("adam: ") + ttp_last_error());
+    ttp_destroy(c);
+}
+
 }  // namespace
 
 int main() {
     test::DeviceGuard guard;
+    // first: the ASan build's allocator then ends the process in the same state as without
+    // this section (device chunks it still holds at exit are freed after the HIP runtime)
+    run_sgd_layout();
     run_mode(TTP_MODE_MIXED);
     run_mode(TTP_MODE_FP32);
     // a table past the 2^40-element bound is refused before any allocation

@@ -19,13 +19,14 @@ def torch_mod():
     return torch
 
 
-def make_pair(shapes, decay, mode, init_std=0.02, seed=0, init="normal"):
-    """GPU store + oracle store holding identical fp32 master weights."""
+def make_pair(shapes, decay, mode, init_std=0.02, seed=0, init="normal", layout="default"):
+    """GPU store + oracle store holding identical fp32 master weights.  layout="sgd": a mixed
+    store in the SGD layout (contiguous master, no m / v until an Adam step converts it)."""
     import ttperf
     from ttperf import _lib as L
     torch = torch_mod()
     store = ttperf.ParamStore(shapes, mode="mixed" if mode == O.MODE_MIXED else "fp32",
-                              decay=decay)
+                              decay=decay, layout=layout)
     store.set_stream(torch.cuda.current_stream())
     numels = [t.numel for t in store.tensors]
     ref = O.OracleStore(numels, flags=[1 if d else 0 for d in decay], mode=mode,

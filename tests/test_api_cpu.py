@@ -45,8 +45,17 @@ def test_ceiling_probe_library_exports_its_entry_points():
 
 
 def test_abi_version():
+    """The library, the header and the ctypes binding agree on the ABI version (2: the SGD
+    layout flag, and the has-grad behaviour of zero_grad_subset / captured accumulates)."""
     from ttperf import _lib as L
-    assert L.lib.ttp_abi_version() == 1
+    text = open(HEADER).read()
+    header = int(re.search(r"#define TTP_ABI_VERSION (\d+)", text).group(1))
+    assert L.lib.ttp_abi_version() == header == L.ABI_VERSION == 2
+    assert int(re.search(r"#define TTP_STORE_SGD (0x[0-9a-fA-F]+)", text).group(1), 16) == \
+        L.STORE_SGD
+    # the C++ wrapper refuses a library of another version
+    hpp = open(os.path.join(REPO, "include", "ttperf", "ttperf.hpp")).read()
+    assert "ttp_abi_version() != TTP_ABI_VERSION" in hpp
 
 
 def test_struct_layouts_match_the_header(tmp_path):

@@ -14,7 +14,7 @@ import pytest
 
 import oracle as O
 from conftest import f32_ulp_diff
-from gpu_util import LONG, compare_state, device_grads, make_pair, torch_mod
+from gpu_util import compare_state, device_grads, make_pair, torch_mod
 
 pytestmark = pytest.mark.gpu
 
@@ -173,13 +173,20 @@ SGD_CASES = {
 }
 
 
-@pytest.mark.parametrize("mode", [O.MODE_MIXED, O.MODE_FP32])
+# (precision mode, store layout): the mixed store in its default layout ([master|m|v]
+# records) and in the SGD layout (contiguous master), and the fp32 store
+STORE_KINDS = {"mixed": (O.MODE_MIXED, "default"), "mixed_sgd": (O.MODE_MIXED, "sgd"),
+               "fp32": (O.MODE_FP32, "default")}
+
+
+@pytest.mark.parametrize("kind", list(STORE_KINDS))
 @pytest.mark.parametrize("case", list(SGD_CASES))
-def test_sgd_family_parity(case, mode):
+def test_sgd_family_parity(case, kind):
     from ttperf import configs
     torch = torch_mod()
+    mode, layout = STORE_KINDS[kind]
     _, shapes, decay, _ = configs.table("nanogpt_char")
-    store, ref = make_pair(shapes, decay, mode, seed=40)
+    store, ref = make_pair(shapes, decay, mode, seed=40, layout=layout)
     gen = torch.Generator(device="cuda").manual_seed(41)
     hp = SGD_CASES[case]
     for step in range(3):
@@ -197,6 +204,7 @@ def test_sgd_family_parity(case, mode):
     if hp.get("momentum"):
         which.append("momentum")
     compare_state(store, ref, which=tuple(which), max_ulp=2 if hp.get("max_grad_norm") else 0)
+    assert store.sgd_layout == (layout == "sgd")
 
 
 # ---- subsets, missing grads, loss-scale growth, ragged and empty tables --------------------
@@ -363,14 +371,14 @@ def test_cfg5_gpt2_xl_fp32_adamw_then_sgd_momentum():
     """Config 5: 580 tensors, 1.56B fp32 params (~25 GB resident with m and v, ~31 GB with
     the momentum buffer).  Grads N(0, 1e-3) with 1% drawn from N(0, 1) (clip path active).
     AdamW lr 1.5e-4 betas (0.9, 0.95) wd 0.1 clip 1.0, then SGD momentum 0.9 on the same
-    buffers.  2 + 2 steps by default, 10 + 10 with TTP_LONG_TESTS=1."""
+    buffers: the configuration's 10 + 10 steps."""
     from ttperf import configs
     torch = torch_mod()
     _, shapes, decay, numels = configs.table("gpt2_1558m")
     assert len(shapes) == 580 and sum(numels) == 1557611200
     store, ref = make_pair(shapes, decay, O.MODE_FP32, seed=70)
     gen = torch.Generator(device="cuda").manual_seed(71)
-    steps = 10 if LONG else 2
+    steps = 10  # BASELINE.json configs[4]
     hp = dict(lr=1.5e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
     for step in range(steps):
         host = device_grads(store, gen, 1e-3, heavy_frac=0.01, heavy_std=1.0)
@@ -396,7 +404,7 @@ def test_cfg5_gpt2_xl_fp32_adamw_then_sgd_momentum():
     compare_state(store, ref, which=("master", "momentum"), max_ulp=2)
 
 
-@pytest.mark.parametrize("mode", ["mixed", "fp32"])
+@pytest.mark.parametrize("mode", ["mixed", "mixed_sgd", "fp32"])
 def test_update_forms_on_both_sides_of_the_cached_gradient_bound(mode):
     """Mixed-precision updates take their form from the stepped set's gradient bytes: up to
     256 MiB the four-element kernel (SGD momentum) or Adam's 128-lane form, beyond that the
@@ -406,13 +414,16 @@ def test_update_forms_on_both_sides_of_the_cached_gradient_bound(mode):
     over the bound, each against the oracle: the whole store and a subset that stays over it
     (lane forms with inactive tensors between and after the active ones), then a subset under
     it.  Both stores hold tensors of odd element count, so two-element lanes end on a lone
-    element."""
+    element.  "mixed_sgd": the mixed store in the SGD layout (contiguous master, four- and
+    two-element SGD lanes, which then end on one to three elements); its first AdamW step
+    converts it to the records, from the master the SGD steps left."""
     torch = torch_mod()
-    if mode == "mixed":
+    if mode != "fp32":
         shapes = [(50257, 768), (8192, 8192), (7000, 5000), (768,), (3,)]  # 140.7M params
         decay = [True, True, True, False, False]
         subsets = (None, [0, 1, 2], [0, 3, 4])
-        store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=80)
+        store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=80,
+                               layout="sgd" if mode == "mixed_sgd" else "default")
         gbytes = 2
     else:
         shapes = [(8193, 8191), (77,), (3,)]  # 67.1M params
@@ -429,8 +440,8 @@ def test_update_forms_on_both_sides_of_the_cached_gradient_bound(mode):
     sgd = dict(lr=1e-2, momentum=0.9, dampening=0.1, max_grad_norm=1.0)
     plain = dict(lr=1e-2, weight_decay=0.01, max_grad_norm=1.0)
     adam = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
-    slots = ("master", "param", "momentum") if mode == "mixed" else ("master", "momentum")
-    adam_slots = ("master", "exp_avg", "exp_avg_sq") + (("param",) if mode == "mixed" else ())
+    slots = ("master", "param", "momentum") if mode != "fp32" else ("master", "momentum")
+    adam_slots = ("master", "exp_avg", "exp_avg_sq") + (("param",) if mode != "fp32" else ())
     for label, subset in zip(("whole store", "lane-form subset", "cached-gradient subset"),
                              subsets):
         for step in range(2):
@@ -465,21 +476,23 @@ def test_update_forms_on_both_sides_of_the_cached_gradient_bound(mode):
     store.close()
 
 
-@pytest.mark.parametrize("mode", ["mixed", "fp32"])
+@pytest.mark.parametrize("mode", ["mixed", "mixed_sgd", "fp32"])
 def test_lane_form_update_split_into_several_launches(mode, monkeypatch):
     """A lane-form update over more blocks than one launch may hold runs as several launches
     at increasing part offsets.  TTP_LANE_LAUNCH_BLOCKS (read at ttp_create) lowers that limit
     to 4099 blocks, so that a store just over the 256 MiB bound takes dozens of launches, whose
     boundaries fall inside chunks and tensors; SGD with momentum, plain SGD and AdamW on the
     whole store and on a subset, against the oracle.  In mixed precision also a subset under the bound,
-    which MIXED Adam steps in its 128-lane form (37 launches)."""
+    which MIXED Adam steps in its 128-lane form (37 launches).  "mixed_sgd": the SGD layout's
+    SGD forms split the same way, then the AdamW step converts the store."""
     torch = torch_mod()
     monkeypatch.setenv("TTP_LANE_LAUNCH_BLOCKS", "4099")
-    if mode == "mixed":
+    if mode != "fp32":
         shapes = [(50257, 768), (8192, 8192), (7000, 5000), (768,), (3,)]
         decay = [True, True, True, False, False]
         subset = [0, 1, 2]
-        store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=84)
+        store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=84,
+                               layout="sgd" if mode == "mixed_sgd" else "default")
     else:
         shapes = [(8193, 8191), (77,), (3,)]
         decay = [True, False, False]
@@ -489,10 +502,10 @@ def test_lane_form_update_split_into_several_launches(mode, monkeypatch):
     sgd = dict(lr=1e-2, momentum=0.9, dampening=0.1, max_grad_norm=1.0)
     plain = dict(lr=1e-2, weight_decay=0.01, max_grad_norm=1.0)
     adam = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
-    slots = ("master", "param", "momentum") if mode == "mixed" else ("master", "momentum")
-    adam_slots = ("master", "exp_avg", "exp_avg_sq") + (("param",) if mode == "mixed" else ())
+    slots = ("master", "param", "momentum") if mode != "fp32" else ("master", "momentum")
+    adam_slots = ("master", "exp_avg", "exp_avg_sq") + (("param",) if mode != "fp32" else ())
     legs = [("whole store", None), ("subset", subset)]
-    if mode == "mixed":
+    if mode != "fp32":
         legs.append(("cached-gradient subset", [0, 3, 4]))
     for label, sub in legs:
         for name, hp in (("sgd-m", sgd), ("sgd", plain), ("adamw", adam)):
@@ -511,20 +524,21 @@ def test_lane_form_update_split_into_several_launches(mode, monkeypatch):
     store.close()
 
 
-@pytest.mark.parametrize("mode", ["mixed", "fp32"])
+@pytest.mark.parametrize("mode", ["mixed", "mixed_sgd", "fp32"])
 def test_lane_form_with_many_small_tensors(mode):
     """A store just over the 256 MiB bound made of one large tensor of odd length and 1500
     small ones of 1..200 elements (most chunks hold less than one lane-form piece, many
     blocks have nothing to do): AdamW with loss scaling and clipping, then SGD with Nesterov
     momentum, then plain SGD with weight decay, against the oracle; the second Adam step on a
-    subset of every third tensor."""
+    subset of every third tensor.  "mixed_sgd": a store created in the SGD layout, which the
+    first AdamW step converts."""
     torch = torch_mod()
     rng = np.random.default_rng(87)
-    big = (1 << 27) + 3 if mode == "mixed" else (1 << 26) + 5
+    big = (1 << 27) + 3 if mode != "fp32" else (1 << 26) + 5
     small = [int(x) for x in rng.integers(1, 201, size=1500)]
     shapes = [(big,)] + [(n,) for n in small]
     decay = [True] + [bool(x) for x in rng.integers(0, 2, size=len(small))]
-    store, ref = make_pair(shapes, decay, O.MODE_MIXED if mode == "mixed" else O.MODE_FP32,
+    store, ref = make_pair(shapes, decay, O.MODE_MIXED if mode != "fp32" else O.MODE_FP32,
                            seed=88)
     store.configure_scaler(True, init_scale=4096.0)
     ref.configure_scaler(True, 4096.0)
@@ -541,7 +555,7 @@ def test_lane_form_with_many_small_tensors(mode):
         assert r["skipped"] == e["skipped"] and r["step"] == e["step"]
         assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
         print(f"{mode} adamw step {step}: norm {r['grad_norm']:.6f}", flush=True)
-    slots = ("master", "exp_avg", "exp_avg_sq") + (("param",) if mode == "mixed" else ())
+    slots = ("master", "exp_avg", "exp_avg_sq") + (("param",) if mode != "fp32" else ())
     compare_state(store, ref, which=slots, max_ulp=2)
     sgd = dict(lr=1e-2, momentum=0.9, nesterov=True, max_grad_norm=0.5)
     for step in range(2):
@@ -552,7 +566,7 @@ def test_lane_form_with_many_small_tensors(mode):
         r = store.sgd_step(report=True, **sgd)
         e = ref.sgd_step(**sgd)
         assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
-    compare_state(store, ref, which=("master", "momentum") + (("param",) if mode == "mixed" else ()),
+    compare_state(store, ref, which=("master", "momentum") + (("param",) if mode != "fp32" else ()),
                   max_ulp=2)
     plain = dict(lr=1e-2, weight_decay=0.01, max_grad_norm=0.5)
     host = device_grads(store, gen, 1e-3, scale=ref.scale)
@@ -560,7 +574,7 @@ def test_lane_form_with_many_small_tensors(mode):
     r = store.sgd_step(report=True, **plain)
     e = ref.sgd_step(**plain)
     assert r["skipped"] == e["skipped"] and abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
-    compare_state(store, ref, which=("master",) + (("param",) if mode == "mixed" else ()),
+    compare_state(store, ref, which=("master",) + (("param",) if mode != "fp32" else ()),
                   max_ulp=2)
     store.close()
 

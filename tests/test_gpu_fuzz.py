@@ -1,8 +1,9 @@
 """Stateful differential fuzzing of libttperf_hip against the CPU oracle.
 
 Each seeded case builds a small ragged store (empty, 1-element, odd, 2-D tensors; decay
-flags; fp32 or mixed precision) and runs a random sequence of operations drawn from the whole
-host interface, mirrored on the oracle:
+flags; fp32 or mixed precision, half the mixed stores in the SGD layout, which the first Adam
+step converts and live graphs keep it from converting) and runs a random sequence of
+operations drawn from the whole host interface, mirrored on the oracle:
 
   gradients written flat or per tensor, from host or device memory (an occasional +inf while
   loss scaling is on); gradients accumulated from fp32 or bf16 sources, host or device;
@@ -60,7 +61,11 @@ class Case:
         self.decay = [len(s) == 2 for s in self.shapes]
         self.mixed = bool(rng.integers(0, 2))
         mode = O.MODE_MIXED if self.mixed else O.MODE_FP32
-        self.store, self.ref = make_pair(self.shapes, self.decay, mode, seed=seed)
+        # half the mixed cases start in the SGD layout (a generator of its own keeps the other
+        # draws of a seed as they were); the first Adam step converts the store
+        self.sgd_layout = self.mixed and np.random.default_rng(seed + 7777).random() < 0.5
+        self.store, self.ref = make_pair(self.shapes, self.decay, mode, seed=seed,
+                                         layout="sgd" if self.sgd_layout else "default")
         self.store.set_stream(None)  # the store's own stream: capturable
         self.numels = [t.numel for t in self.store.tensors]
         self.graphs = []      # (graph, hp, captured active set)
@@ -194,6 +199,23 @@ class Case:
         if np.isfinite(e["grad_norm"]) and e["grad_norm"] > 0 and np.isfinite(r["grad_norm"]):
             assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
 
+    def _conversion_refused(self, step):
+        """An Adam step on a store still in the SGD layout converts it, which is refused while
+        graphs live (they hold the master's address): checks that the refusal changed nothing.
+        True when the step was refused."""
+        import ttperf
+        from ttperf import _lib as L
+        live = len(self.graphs) + len(self.zero_graphs)
+        if not (self.store.sgd_layout and live):
+            return False
+        t0 = self.store.step_count
+        with pytest.raises(ttperf.TTPError) as e:
+            step()
+        assert e.value.code == L.ERR_STATE and "SGD layout" in str(e.value)
+        assert self.store.step_count == t0 and self.store.sgd_layout
+        print(f"   refused: converting the SGD layout with {live} live graph(s)", flush=True)
+        return True
+
     def op_adam(self):
         rng = self.rng
         wd = 0.0 if rng.random() < 0.3 else float(rng.uniform(0.01, 0.2))
@@ -212,6 +234,10 @@ class Case:
         r = None
         if noalloc and not self._noalloc_adam(hp, indices, defer):
             noalloc = False  # refused, nothing changed: the allocating step instead
+        if not noalloc and self._conversion_refused(
+                lambda: self.store.adam_step(report=report, indices=indices,
+                                             update_scale=not defer, **hp)):
+            return
         if not noalloc:
             r = self.store.adam_step(report=report, indices=indices, update_scale=not defer,
                                      **hp)
@@ -313,6 +339,9 @@ class Case:
             return
         active = self._active(indices)
         step = self.store.adam_step if adam else self.store.sgd_step
+        if adam and self._conversion_refused(
+                lambda: step(report=True, indices=indices, tensor_sums=True, **hp)):
+            return
         r = step(report=True, indices=indices, tensor_sums=True, **hp)
         e = self._ref_step(kind, hp, active)
         self._check_report(r, e)
@@ -478,6 +507,8 @@ class Case:
         if self.mom_seen:
             which += ["momentum"]
         compare_state(self.store, self.ref, which=tuple(which), max_ulp=2)
+        # the SGD layout lasts until the first Adam step
+        assert self.store.sgd_layout == (self.sgd_layout and not self.adam_seen)
         got = self.store.download(L.BUF_GRAD)
         want = self.ref.grad[:self.store.total]
         assert np.array_equal(got.view(np.uint8), want.view(np.uint8)), "gradients differ"
@@ -499,7 +530,8 @@ class Case:
 @pytest.mark.parametrize("seed", SEEDS)
 def test_random_operation_sequence(seed, tmp_path):
     c = Case(seed, tmp_path)
-    print(f"case {seed}: {'mixed' if c.mixed else 'fp32'} shapes={c.shapes}", flush=True)
+    print(f"case {seed}: {'mixed' if c.mixed else 'fp32'}"
+          f"{' (SGD layout)' if c.sgd_layout else ''} shapes={c.shapes}", flush=True)
     names = [n for n, _ in Case.OPS]
     weights = np.array([w for _, w in Case.OPS], np.float64)
     weights /= weights.sum()

@@ -2,9 +2,10 @@
 configurations, each printed before it runs.
 
 Every case draws a ragged tensor table (empty, 1-element, odd and 2-D tensors, decay flags),
-a precision mode, an optimizer (Adam with decoupled, L2 or no weight decay; SGD plain, with
-momentum, dampening, nesterov, L2), clipping on or off, and in mixed precision loss scaling
-with a short growth interval and an injected +inf on some steps.  Three steps run, each with
+a precision mode (a mixed store in its default or its SGD layout), an optimizer (Adam with
+decoupled, L2 or no weight decay; SGD plain, with momentum, dampening, nesterov, L2),
+clipping on or off, and in mixed precision loss scaling with a short growth interval and an
+injected +inf on some steps.  Three steps run, each with
 fresh gradients, a random active set (a subset step, None grads, or every tensor), and the
 full state and step report are compared after every step: bf16 bit-exact, fp32 within the
 2-ulp bar of the other parity tests, identical skip / scale / step-count decisions.
@@ -44,8 +45,11 @@ def _draw(seed):
     clip = None if rng.random() < 0.4 else float(10 ** rng.uniform(-2, 1))
     scaler = mixed and rng.random() < 0.6
     init_scale = float(2.0 ** int(rng.integers(4, 17))) if rng.random() < 0.7 else 1000.0
+    # half the mixed cases in the SGD layout (drawn from a generator of its own, so the
+    # other draws of a seed stay as they were); an Adam step converts such a store
+    sgd_layout = mixed and np.random.default_rng(seed + 7777).random() < 0.5
     return dict(rng=rng, shapes=shapes, decay=decay, mixed=mixed, opt=opt, clip=clip,
-                scaler=scaler, init_scale=init_scale)
+                scaler=scaler, init_scale=init_scale, sgd_layout=sgd_layout)
 
 
 def _hp(opt, rng):
@@ -71,10 +75,13 @@ def test_random_configuration(seed):
     c = _draw(seed)
     rng = c["rng"]
     kind, hp = _hp(c["opt"], rng)
-    print(f"case {seed}: {'mixed' if c['mixed'] else 'fp32'} {c['opt']} clip={c['clip']} "
+    print(f"case {seed}: {'mixed' if c['mixed'] else 'fp32'}"
+          f"{' (SGD layout)' if c['sgd_layout'] else ''} {c['opt']} clip={c['clip']} "
           f"scaler={c['scaler']}({c['init_scale']:g}) hp={hp} shapes={c['shapes']}", flush=True)
     mode = O.MODE_MIXED if c["mixed"] else O.MODE_FP32
-    store, ref = make_pair(c["shapes"], c["decay"], mode, seed=seed)
+    store, ref = make_pair(c["shapes"], c["decay"], mode, seed=seed,
+                           layout="sgd" if c["sgd_layout"] else "default")
+    assert store.sgd_layout == c["sgd_layout"]
     if c["scaler"]:
         store.configure_scaler(True, init_scale=c["init_scale"], growth_interval=2)
         ref.configure_scaler(True, c["init_scale"], growth_interval=2)
@@ -126,4 +133,6 @@ def test_random_configuration(seed):
         if (c["clip"] or c["scaler"]) and np.isfinite(e["grad_norm"]) and e["grad_norm"] > 0:
             assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
         compare_state(store, ref, which=tuple(which), max_ulp=2)
+        # an SGD-layout store keeps its layout through SGD steps; an Adam step converts it
+        assert store.sgd_layout == (c["sgd_layout"] and kind == "sgd")
     store.close()

@@ -1,0 +1,180 @@
+"""GPU tests of the SGD layout of a mixed store (TTP_STORE_SGD): a contiguous fp32 master and
+no m / v, which the update of the reference's own optimizer (autograd::SGD, TracedSGD, every
+module's sgd_step: `w - lr*g`, autograd/dynamic/optim.hpp:21-27) and SGD with momentum stream
+like a copy.
+
+Checked against the oracle at GPT-2 124M (config 3's table) and at GPT-2 774M (config 4's):
+plain SGD (the reference's) and SGD with momentum, with loss scaling, an overflow step and
+clipping, whole-store steps and module-sized subset steps; the raw device memory of the
+master against ttp_buffer_layout's addressing; a captured SGD step replayed between eager
+steps; and the conversion to the default layout by the first Adam step.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_util import compare_state, device_grads, make_pair, torch_mod
+
+pytestmark = pytest.mark.gpu
+
+
+def _set_all(ref, active=None):
+    for i in range(ref.n):
+        ref.set_has_grad(i, active is None or i in active)
+
+
+def _check(r, e, scaler):
+    assert (r["skipped"], r["found_inf"], r["step"]) == (e["skipped"], e["found_inf"], e["step"])
+    if scaler:
+        assert (r["scale"], r["growth_tracker"]) == (e["scale"], e["growth_tracker"])
+    if np.isfinite(e["grad_norm"]) and e["grad_norm"] > 0:
+        assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
+
+
+def test_gpt2_124m_plain_and_momentum_sgd_match_the_oracle():
+    """Config 3's 148 tensors in the SGD layout: the reference's plain SGD with loss scaling
+    (2^16, growth every 3 clean steps) and clipping at 1.0, a +inf on step 3 (skipped, scale
+    halved); then one block's 12 tensors stepped alone (a module's sgd_step); then SGD with
+    momentum 0.9 over everything.  bf16 weights bit-exact, master and momentum within 2 ulp,
+    identical skip / scale / step decisions, norm within 1e-5."""
+    from ttperf import configs
+    torch = torch_mod()
+    _, shapes, decay, _ = configs.table("gpt2_124m")
+    store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=300, layout="sgd")
+    assert store.sgd_layout
+    store.configure_scaler(True, init_scale=65536.0, growth_interval=3)
+    ref.configure_scaler(True, 65536.0, growth_interval=3)
+    gen = torch.Generator(device="cuda").manual_seed(301)
+    plain = dict(lr=1e-2, max_grad_norm=1.0)
+    for step in range(6):
+        inf_at = store.offsets[40] + 17 if step == 3 else None
+        ref.grad[:] = device_grads(store, gen, 1e-3, scale=ref.scale, inf_at=inf_at)
+        _set_all(ref)
+        r = store.sgd_step(report=True, **plain)
+        e = ref.sgd_step(**plain)
+        print(f"  plain step {step}: skipped {e['skipped']} scale {e['scale']:g} "
+              f"norm {e['grad_norm']:.6g}", flush=True)
+        _check(r, e, True)
+        assert e["skipped"] == (step == 3)
+    compare_state(store, ref, which=("master", "param"), max_ulp=2)
+    block = list(range(2 + 12 * 5, 2 + 12 * 6))  # h.5's tensors
+    ref.grad[:] = device_grads(store, gen, 1e-3, scale=ref.scale)
+    _set_all(ref, block)
+    r = store.sgd_step(report=True, indices=block, lr=0.05)
+    e = ref.sgd_step(lr=0.05)
+    _check(r, e, True)
+    compare_state(store, ref, which=("master", "param"), max_ulp=2)
+    mom = dict(lr=1e-2, momentum=0.9, max_grad_norm=1.0)
+    for step in range(3):
+        ref.grad[:] = device_grads(store, gen, 1e-3, scale=ref.scale)
+        _set_all(ref)
+        r = store.sgd_step(report=True, **mom)
+        e = ref.sgd_step(**mom)
+        _check(r, e, True)
+    compare_state(store, ref, which=("master", "param", "momentum"), max_ulp=2)
+    assert store.sgd_layout
+    store.close()
+
+
+def test_gpt2_774m_sgd_layout_matches_the_oracle():
+    """Config 4's 436 ragged tensors (1,280 to 64.3M elements) in the SGD layout: plain SGD
+    with clipping, then SGD with momentum and dampening; the norm pass takes its two launches
+    (non-temporal, then cached) above 256 MiB of gradients."""
+    from ttperf import configs
+    torch = torch_mod()
+    _, shapes, decay, _ = configs.table("gpt2_774m")
+    store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=310, layout="sgd")
+    gen = torch.Generator(device="cuda").manual_seed(311)
+    legs = [dict(lr=1e-2, max_grad_norm=1.0)] * 2 + \
+        [dict(lr=1e-2, momentum=0.9, dampening=0.1, max_grad_norm=1.0)] * 2
+    for k, hp in enumerate(legs):
+        ref.grad[:] = device_grads(store, gen, 1e-3)
+        _set_all(ref)
+        r = store.sgd_step(report=True, **hp)
+        e = ref.sgd_step(**hp)
+        print(f"  step {k} {hp}: norm {e['grad_norm']:.6g}", flush=True)
+        _check(r, e, False)
+    compare_state(store, ref, which=("master", "param", "momentum"), max_ulp=2)
+    store.close()
+
+
+def test_sgd_layout_matches_raw_device_memory():
+    """ttp_buffer_layout reports the master as contiguous (group = stride = 64), and the raw
+    device memory at that base, read with hipMemcpy, equals the master download; the pointer
+    of each tensor is base + offset * 4."""
+    from ttperf import _lib as L
+    torch = torch_mod()
+    shapes = [(1,), (63,), (65,), (7, 9), (130,), (64, 64), (3,)]
+    decay = [False, False, False, True, False, True, False]
+    store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=320, layout="sgd")
+    gen = torch.Generator(device="cuda").manual_seed(321)
+    for _ in range(2):
+        ref.grad[:] = device_grads(store, gen, 1e-2)
+        _set_all(ref)
+        store.sgd_step(lr=0.1, momentum=0.5)
+        ref.sgd_step(lr=0.1, momentum=0.5)
+    compare_state(store, ref, which=("master", "param", "momentum"), max_ulp=0)
+    base, group, stride = store.layout(L.BUF_MASTER)
+    assert (group, stride) == (64, 64)
+    for i in range(len(shapes)):
+        assert store.ptr(L.BUF_MASTER, i) == base + store.offsets[i] * 4
+    torch.cuda.synchronize()
+    hip = C.CDLL("libamdhip64.so.7")
+    hip.hipMemcpy.restype = C.c_int
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    raw = np.empty(store.total, np.float32)
+    assert hip.hipMemcpy(raw.ctypes.data, base, store.total * 4, 2) == 0
+    assert np.array_equal(raw.view(np.uint32), store.download(L.BUF_MASTER).view(np.uint32))
+    store.close()
+
+
+def test_captured_sgd_step_replays_between_eager_steps():
+    """A plain SGD step with loss scaling captured on an SGD-layout store, replayed three
+    times with new gradients (one holding +inf) and eager momentum-free steps in between, each
+    against the oracle; the store keeps its layout, and the first Adam step's conversion waits
+    until the graph is gone."""
+    import ttperf
+    from ttperf import _lib as L
+    torch = torch_mod()
+    shapes = [(300, 7), (64,), (129, 33), (5,), (4097,)]
+    decay = [True, False, True, False, False]
+    store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=330, layout="sgd")
+    store.set_stream(None)  # the store's own stream: capturable
+    store.configure_scaler(True, init_scale=256.0, growth_interval=2)
+    ref.configure_scaler(True, 256.0, growth_interval=2)
+    gen = torch.Generator(device="cuda").manual_seed(331)
+    hp = dict(lr=0.02, max_grad_norm=0.5)
+    ref.grad[:] = device_grads(store, gen, 1e-2, scale=ref.scale)
+    _set_all(ref)
+    _check(store.sgd_step(report=True, **hp), ref.sgd_step(**hp), True)  # builds the tables
+    store.begin_capture()
+    store.sgd_step(**hp)
+    graph = store.end_capture()
+    for k in range(3):
+        ref.grad[:] = device_grads(store, gen, 1e-2, scale=ref.scale,
+                                   inf_at=store.offsets[2] + 9 if k == 1 else None)
+        _set_all(ref)
+        graph.replay()
+        e = ref.sgd_step(**hp)
+        store.sync()
+        assert store.step_count == e["step"]
+        assert store.scaler_state() == (np.float32(e["scale"]), e["growth_tracker"])
+        compare_state(store, ref, which=("master", "param"), max_ulp=2)
+        ref.grad[:] = device_grads(store, gen, 1e-2, scale=ref.scale)
+        _set_all(ref)
+        _check(store.sgd_step(report=True, lr=0.01), ref.sgd_step(lr=0.01), True)
+        compare_state(store, ref, which=("master", "param"), max_ulp=2)
+    assert store.sgd_layout
+    with pytest.raises(ttperf.TTPError) as e:
+        store.adam_step(lr=1e-3)
+    assert e.value.code == L.ERR_STATE and store.sgd_layout
+    graph.close()
+    adam = dict(lr=1e-3, betas=(0.9, 0.95), weight_decay=0.1)
+    ref.grad[:] = device_grads(store, gen, 1e-2, scale=ref.scale)
+    _set_all(ref)
+    _check(store.adam_step(report=True, **adam), ref.adam_step(**adam), True)
+    assert not store.sgd_layout
+    compare_state(store, ref, max_ulp=2)
+    store.close()

@@ -564,25 +564,39 @@ constexpr uint32_t lane_parts() {
     return kChunk / (kLanes * kE * kIt);
 }
 
-// kE gradients as fp32 (ordinary loads: faster here than non-temporal ones at 774M)
+// kE (1, 2 or 4) gradients as fp32 (ordinary loads: faster here than non-temporal ones at
+// 774M).  A lane's kE elements start at a multiple of kE and tensors start on 64-element
+// boundaries, so a lane whose tensor ends inside it still reads inside the tensor's footprint.
 template <int kE>
 __device__ __forceinline__ void ld_grad_lane(const uint16_t* g, uint64_t i, float* out) {
+    static_assert(kE == 1 || kE == 2 || kE == 4, "1, 2 or 4 elements per lane");
     if constexpr (kE == 1) {
         out[0] = __uint_as_float((uint32_t)g[i] << 16);
-    } else {
+    } else if constexpr (kE == 2) {
         const uint32_t w = *reinterpret_cast<const uint32_t*>(g + i);
         out[0] = bf16_lo(w);
         out[1] = bf16_hi(w);
+    } else {
+        const u32x2 w = *reinterpret_cast<const u32x2*>(g + i);
+        out[0] = bf16_lo(w.x);
+        out[1] = bf16_hi(w.x);
+        out[2] = bf16_lo(w.y);
+        out[3] = bf16_hi(w.y);
     }
 }
 template <int kE>
 __device__ __forceinline__ void ld_grad_lane(const float* g, uint64_t i, float* out) {
+    static_assert(kE == 1 || kE == 2 || kE == 4, "1, 2 or 4 elements per lane");
     if constexpr (kE == 1) {
         out[0] = g[i];
-    } else {
+    } else if constexpr (kE == 2) {
         const f32x2 w = *reinterpret_cast<const f32x2*>(g + i);
         out[0] = w.x;
         out[1] = w.y;
+    } else {
+        const f32x4 w = *reinterpret_cast<const f32x4*>(g + i);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out[j] = w[j];
     }
 }
 // kE fp32 values, non-temporal
@@ -590,26 +604,56 @@ template <int kE>
 __device__ __forceinline__ void ld_lane(const float* p, float* out) {
     if constexpr (kE == 1) {
         out[0] = __builtin_nontemporal_load(p);
-    } else {
+    } else if constexpr (kE == 2) {
         const f32x2 w = __builtin_nontemporal_load(reinterpret_cast<const f32x2*>(p));
         out[0] = w.x;
         out[1] = w.y;
+    } else {
+        const f32x4 w = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out[j] = w[j];
     }
 }
-// the first n (1..kE) of kE fp32 values, non-temporal
+// the first n (1..kE) of kE fp32 values, non-temporal: one vector store when n == kE
 template <int kE>
 __device__ __forceinline__ void st_lane(float* p, const float* v, int n) {
-    if (kE == 2 && n == 2)
-        __builtin_nontemporal_store(f32x2{v[0], v[kE - 1]}, reinterpret_cast<f32x2*>(p));
-    else
+    if constexpr (kE == 1) {
         __builtin_nontemporal_store(v[0], p);
+    } else if constexpr (kE == 2) {
+        if (n == 2)
+            __builtin_nontemporal_store(f32x2{v[0], v[1]}, reinterpret_cast<f32x2*>(p));
+        else
+            __builtin_nontemporal_store(v[0], p);
+    } else {
+        if (n == 4) {
+            __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]},
+                                        reinterpret_cast<f32x4*>(p));
+        } else {
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+                if (j < n) __builtin_nontemporal_store(v[j], p + j);
+        }
+    }
 }
 template <int kE>
 __device__ __forceinline__ void st_bf16_lane(uint16_t* p, const float* v, int n) {
-    if (kE == 2 && n == 2)
-        __builtin_nontemporal_store(bf16_pack(v[0], v[kE - 1]), reinterpret_cast<uint32_t*>(p));
-    else
+    if constexpr (kE == 1) {
         __builtin_nontemporal_store((uint16_t)bf16_rne(v[0]), p);
+    } else if constexpr (kE == 2) {
+        if (n == 2)
+            __builtin_nontemporal_store(bf16_pack(v[0], v[1]), reinterpret_cast<uint32_t*>(p));
+        else
+            __builtin_nontemporal_store((uint16_t)bf16_rne(v[0]), p);
+    } else {
+        if (n == 4) {
+            __builtin_nontemporal_store(u32x2{bf16_pack(v[0], v[1]), bf16_pack(v[2], v[3])},
+                                        reinterpret_cast<u32x2*>(p));
+        } else {
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+                if (j < n) __builtin_nontemporal_store((uint16_t)bf16_rne(v[j]), p + j);
+        }
+    }
 }
 
 // One piece of the lane-form Adam update: this lane's kE elements at flat index i (the first
@@ -716,12 +760,20 @@ __device__ __forceinline__ void sgd_elem(float& p, float g, float& b, const SgdA
     p = p - update;                 // autograd/dynamic/optim.hpp:25
 }
 
+// Flat element i of a master slot with kMStride elements per record: kRec is a contiguous
+// master (FP32 mode, and the SGD layout of a MIXED store), kStrideMixed slot 0 of the
+// [master|m|v] records.
+template <uint32_t kMStride>
+__device__ __forceinline__ uint64_t master_index(uint64_t i) {
+    if constexpr (kMStride == kRec) return i;
+    else return rec_index(i, kMStride);
+}
+
 // The four-element SGD update: one block per chunk (grid == nchunks), blocks in reverse chunk
 // order, one 4-element vector per lane, for MIXED momentum steps whose gradients fit the
 // Infinity Cache (at most 2^17 chunks), at most kUpdBlocksPerCU blocks per CU.  master is
-// the master slot base (MIXED: slot 0 of the [master|m|v] records; FP32: the contiguous
-// weights); momentum is contiguous.
-template <typename GradT, bool kMixed>
+// the master slot base (see master_index); momentum is contiguous.
+template <typename GradT, bool kMixed, uint32_t kMStride>
 __global__ __launch_bounds__(kUpdBlock) void sgd_kernel(const GradT* __restrict__ grad,
                                                         float* __restrict__ master,
                                                         float* __restrict__ momentum,
@@ -742,7 +794,7 @@ __global__ __launch_bounds__(kUpdBlock) void sgd_kernel(const GradT* __restrict_
     const bool decay = (ch.meta & kChunkDecay) && (a.flags & kWdOn);
     const bool first = mom_on && a.mom_init[ch.meta >> 8] == 0u;
     const uint64_t i = ch.begin + off;
-    float* pp = master + (kMixed ? rec_index(i, kStrideMixed) : i);
+    float* pp = master + master_index<kMStride>(i);
     f32x4 g = ld_grad4(grad, i);
     f32x4 p = ld4(pp);
     f32x4 b = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -758,7 +810,7 @@ __global__ __launch_bounds__(kUpdBlock) void sgd_kernel(const GradT* __restrict_
 }
 
 // One piece of the lane-form SGD update (see adam_piece).
-template <typename GradT, bool kMixed, int kE>
+template <typename GradT, bool kMixed, uint32_t kMStride, int kE>
 __device__ __forceinline__ void sgd_piece(const GradT* __restrict__ grad,
                                           float* __restrict__ master,
                                           float* __restrict__ momentum,
@@ -766,7 +818,7 @@ __device__ __forceinline__ void sgd_piece(const GradT* __restrict__ grad,
                                           float inv, float clip, bool use_inv, bool use_clip,
                                           bool decay, bool mom_on, bool first, bool nesterov,
                                           uint64_t i, int n) {
-    float* pp = master + (kMixed ? rec_index(i, kStrideMixed) : i);
+    float* pp = master + master_index<kMStride>(i);
     float g[kE], p[kE], bm[kE];
     ld_grad_lane<kE>(grad, i, g);
     ld_lane<kE>(pp, p);
@@ -786,9 +838,8 @@ __device__ __forceinline__ void sgd_piece(const GradT* __restrict__ grad,
 }
 
 // The lane-form SGD update, launched and shaped as adam_lane_kernel.  master is the master
-// slot base (MIXED: the [master|m|v] record array; FP32: the contiguous weights); momentum is
-// contiguous.  a.st must be valid.
-template <typename GradT, bool kMixed, int kE, int kLanes, int kIt>
+// slot base (see master_index); momentum is contiguous.  a.st must be valid.
+template <typename GradT, bool kMixed, uint32_t kMStride, int kE, int kLanes, int kIt>
 __global__ __launch_bounds__(kLanes) void sgd_lane_kernel(const GradT* __restrict__ grad,
                                                           float* __restrict__ master,
                                                           float* __restrict__ momentum,
@@ -808,17 +859,19 @@ __global__ __launch_bounds__(kLanes) void sgd_lane_kernel(const GradT* __restric
     const bool first = mom_on && a.mom_init[ch.meta >> 8] == 0u;
     const float inv = st->inv_scale, clip = st->clip_coef;
     if constexpr (kIt == 1) {
-        sgd_piece<GradT, kMixed, kE>(grad, master, momentum, param16, a, inv, clip, use_inv,
-                                     use_clip, decay, mom_on, first, nesterov, ch.begin + off,
-                                     (int)min(ch.count - off, (uint32_t)kE));
+        sgd_piece<GradT, kMixed, kMStride, kE>(grad, master, momentum, param16, a, inv, clip,
+                                               use_inv, use_clip, decay, mom_on, first, nesterov,
+                                               ch.begin + off,
+                                               (int)min(ch.count - off, (uint32_t)kE));
     } else {
 #pragma unroll 1
         for (int q = 0; q < kIt; ++q) {
             const uint32_t o = off + q * kPiece;
             if (o >= ch.count) break;
-            sgd_piece<GradT, kMixed, kE>(grad, master, momentum, param16, a, inv, clip, use_inv,
-                                         use_clip, decay, mom_on, first, nesterov,
-                                         ch.begin + o, (int)min(ch.count - o, (uint32_t)kE));
+            sgd_piece<GradT, kMixed, kMStride, kE>(grad, master, momentum, param16, a, inv, clip,
+                                                   use_inv, use_clip, decay, mom_on, first,
+                                                   nesterov, ch.begin + o,
+                                                   (int)min(ch.count - o, (uint32_t)kE));
         }
     }
 }

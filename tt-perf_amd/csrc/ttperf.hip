@@ -5,9 +5,11 @@
 //     fp32, 128 B for bf16), so every lane's 4-element vector stays inside one tensor's
 //     footprint; the padding is zero and never written by a step;
 //   * optimizer state in records of 64-element slots (ttp::kRec): MIXED mode keeps master,
-//     m and v of each 64-element group in one [master|m|v] record, allocated with the store;
-//     FP32 mode keeps its contiguous master (the model-facing weights) and puts m and v in
-//     [m|v] records on first Adam use.  Momentum and the model-facing buffers are contiguous.
+//     m and v of each 64-element group in one [master|m|v] record, allocated with the store
+//     (in its SGD layout, TTP_STORE_SGD, a contiguous master and no m / v until the first
+//     Adam step converts it); FP32 mode keeps its contiguous master (the model-facing
+//     weights) and puts m and v in [m|v] records on first Adam use.  Momentum and the
+//     model-facing buffers are contiguous.
 //     Uploads, downloads and checkpoints convert between records and contiguous arrays;
 //   * work table: chunks of <= kChunk (1024) elements of one tensor.  The table of all
 //     tensors is built once; a second table is built only while some tensor has no grad
@@ -150,12 +152,16 @@ struct ttp_ctx {
 
     void* param = nullptr;  // bf16 (MIXED) or == master (FP32)
     void* grad = nullptr;   // bf16 (MIXED) or fp32 (FP32)
-    // slot bases (see buffer_stride): MIXED, the three slots of `records`; FP32, the
-    // contiguous master and the two slots of `records` (null until the first Adam use)
+    // slot bases (see buffer_stride): MIXED, the three slots of `records`; FP32 and the
+    // MIXED SGD layout, the contiguous master and the two slots of `records` (null until the
+    // first Adam use)
     float* master = nullptr;
     float* exp_avg = nullptr;
     float* exp_avg_sq = nullptr;
     float* records = nullptr;   // the state record array (the allocation)
+    // MIXED store in the SGD layout (TTP_STORE_SGD): `master` is its own contiguous
+    // allocation and `records` does not exist; cleared by the conversion of the first Adam use
+    bool sgd_layout = false;
     float* momentum = nullptr;  // contiguous
     uint32_t* mom_init = nullptr;        // device, per tensor
     std::vector<uint8_t> host_mom_init;  // host view (exact while loss scaling is off)
@@ -369,13 +375,47 @@ int alloc_zero(ttp_ctx* c, void** p, uint64_t bytes) {
     return zero_device(c, *p, bytes);
 }
 
+// blocks of a grid-stride elementwise kernel over n elements: at most 16 per CU
+uint32_t elementwise_grid(const ttp_ctx* c, uint64_t n) {
+    return (uint32_t)std::max<uint64_t>(
+        1, std::min<uint64_t>((n + ttp::kBlock - 1) / ttp::kBlock, (uint64_t)c->num_cus * 16));
+}
+
 int ensure_adam_state(ttp_ctx* c) {
     // py/optim.py:58-71: m and v start as zeros on first use.  MIXED mode allocates them
     // (zero) with the master in its records at ttp_create; FP32 mode allocates the [m|v]
-    // records here.
+    // records here; a MIXED store in the SGD layout is converted to the [master|m|v] records
+    // here (the master's values move unchanged, the bf16 weights stay as they are).
     if (c->exp_avg) return TTP_OK;
     int rc;
     if ((rc = no_capture(c, "first Adam step (allocates m, v)"))) return rc;
+    if (c->mode == TTP_MODE_MIXED && c->sgd_layout) {
+        if (c->n_graphs)
+            return fail(TTP_ERR_STATE, "the first Adam use of a store in the SGD layout moves "
+                                       "its master into new state records, and live graphs "
+                                       "of this context hold the old master's address: "
+                                       "destroy them first");
+        float* rec = nullptr;
+        if ((rc = alloc_zero(c, (void**)&rec, c->total * 4 * 3))) {
+            if (rec) (void)hipFree(rec);
+            return rc;
+        }
+        clear_hip_error();
+        hipLaunchKernelGGL(ttp::scatter_slot_kernel, dim3(elementwise_grid(c, c->total)),
+                           dim3(ttp::kBlock), 0, c->stream, rec, ttp::kStrideMixed, (uint64_t)0,
+                           c->total, (const float*)c->master, (uint16_t*)nullptr);
+        if (hipGetLastError() != hipSuccess || hipStreamSynchronize(c->stream) != hipSuccess) {
+            (void)hipFree(rec);
+            return fail(TTP_ERR_HIP, "moving the master into state records failed");
+        }
+        HIP_TRY(hipFree(c->master));
+        c->records = rec;
+        c->master = rec;
+        c->exp_avg = rec + ttp::kRec;
+        c->exp_avg_sq = rec + 2 * ttp::kRec;
+        c->sgd_layout = false;
+        return TTP_OK;
+    }
     if ((rc = alloc_zero(c, (void**)&c->records, c->total * 4 * 2))) return rc;
     c->exp_avg = c->records;
     c->exp_avg_sq = c->records + ttp::kRec;
@@ -601,6 +641,30 @@ constexpr int kLaneSgdFp32 = 2, kLanesSgdFp32 = 64, kItSgdFp32 = 1;
 // and 4.48 TB/s for the 1 x 256 x 2 shape that momentum prefers.  One shape at every size:
 // after a gradient rewrite, as in training, it is the fastest at both sizes.
 constexpr int kLaneSgdPlainMixed = 2, kLanesSgdPlainMixed = 256, kItSgdPlainMixed = 1;
+// The SGD layout of a MIXED store (TTP_STORE_SGD: contiguous master and momentum).  Measured
+// with the product kernels in a timing-only program (GPT-2 tables and the C++ drop-in's
+// 163M traced GPT, three rounds, medians, x a 64-lane non-temporal copy of the same bytes;
+// back to back / after a device copy of the gradients):
+//   plain    4 x 64 x 1:  124M 1.082 / 1.035, 163M 1.002 / 1.021, 774M 0.984 / 1.018
+//                         (2x256x2 0.96-1.02, 4x128x1 0.94-1.04, 4x256x1 0.95-1.03,
+//                         2x256x1 0.86-0.91, 1x256x2 0.69-0.73; the record master's
+//                         2x256x1 0.82-0.89)
+//   momentum 2 x 128 x 1: 124M 0.998 / 0.992, 163M 0.973 / 0.986, 774M 0.989 / 1.018
+//                         (2x64x1 0.94-1.01, 4x64x1 0.94-1.04, 2x256x1 0.94-0.99,
+//                         1x256x2 0.92-0.95; the record master's 1x256x2 0.88-0.92)
+// Four elements per lane give the plain update 16-byte master loads and stores and 8-byte
+// gradient and bf16 words, the copy's pattern; with its momentum stream the update does
+// best with two.  One shape at every size (the gradients' place in the Infinity Cache made
+// no difference to the ranking).
+constexpr int kLaneSgdPlainContig = 4, kLanesSgdPlainContig = 64, kItSgdPlainContig = 1;
+constexpr int kLaneSgdMomContig = 2, kLanesSgdMomContig = 128, kItSgdMomContig = 1;
+// FP32 SGD without momentum (fp32 gradients and weights, 12 B per element), the same program
+// and method (124M / 774M / 1558M, x the 64-lane copy, back to back / after a gradient
+// copy): 2 x 256 x 2 0.993 / 0.976, 1.003 / 1.013, 1.001 / 1.018 (4x256x1 0.97-0.99,
+// 4x64x1 0.94-0.99, the momentum shape 2x64x1 0.86-0.88).  With momentum the 2 x 64 x 1 shape
+// above stays: 0.976 / 0.959, 0.973 / 0.977, 0.986 / 0.992 (2x128x1 0.97-1.00, 4x64x1
+// 0.91-0.97).
+constexpr int kLaneSgdPlainFp32 = 2, kLanesSgdPlainFp32 = 256, kItSgdPlainFp32 = 2;
 
 // One launch holds at most 2^32 - 1 work-items, so at most (2^32 - 1) / lanes blocks.  A
 // lane-form update over more parts is split into launches at increasing part offsets
@@ -771,7 +835,7 @@ int check_index(const ttp_ctx* c, uint32_t i) {
 uint32_t buffer_stride(const ttp_ctx* c, int which) {
     const bool mixed = c->mode == TTP_MODE_MIXED;
     switch (which) {
-        case TTP_BUF_MASTER: return mixed ? ttp::kStrideMixed : ttp::kRec;
+        case TTP_BUF_MASTER: return mixed && !c->sgd_layout ? ttp::kStrideMixed : ttp::kRec;
         case TTP_BUF_EXP_AVG:
         case TTP_BUF_EXP_AVG_SQ: return mixed ? ttp::kStrideMixed : ttp::kStrideMV;
     }
@@ -824,11 +888,6 @@ int resolve_range(ttp_ctx* c, uint32_t index, uint64_t n, uint64_t* off, uint64_
     *off = c->tensors[index].offset;
     *count = n;
     return TTP_OK;
-}
-
-uint32_t elementwise_grid(const ttp_ctx* c, uint64_t n) {
-    return (uint32_t)std::max<uint64_t>(
-        1, std::min<uint64_t>((n + ttp::kBlock - 1) / ttp::kBlock, (uint64_t)c->num_cus * 16));
 }
 
 // Device staging buffer of at least `bytes` (host transfers pass through it).  Growing it
@@ -916,9 +975,10 @@ void release(ttp_ctx* c) {
     free_tables(c->all);
     for (auto& kv : c->tables) free_tables(kv.second);
     for (void* p : c->retired) (void)hipFree(p);
-    // MIXED: param is the bf16 copy and master lives in `records`; FP32: param == master
+    // MIXED: param is the bf16 copy and master lives in `records` (in the SGD layout, in an
+    // allocation of its own); FP32: param == master
     if (c->mode == TTP_MODE_MIXED && c->param) (void)hipFree(c->param);
-    if (c->mode == TTP_MODE_FP32 && c->master) (void)hipFree(c->master);
+    if ((c->mode == TTP_MODE_FP32 || c->sgd_layout) && c->master) (void)hipFree(c->master);
     for (auto& v : c->ev)
         for (auto& p : v) {
             (void)hipEventDestroy(p.a);
@@ -952,8 +1012,11 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
     if (!out) return fail(TTP_ERR_INVALID, "null output pointer");
     *out = nullptr;
     if (n && !descs) return fail(TTP_ERR_INVALID, "null tensor table");
+    const bool sgd_layout = (mode & TTP_STORE_SGD) != 0;
+    mode &= ~TTP_STORE_SGD;
     if (mode != TTP_MODE_FP32 && mode != TTP_MODE_MIXED)
-        return fail(TTP_ERR_INVALID, "mode must be TTP_MODE_FP32 or TTP_MODE_MIXED");
+        return fail(TTP_ERR_INVALID, "mode must be TTP_MODE_FP32 or TTP_MODE_MIXED, optionally "
+                                     "| TTP_STORE_SGD");
     // per-tensor kernels launch one 256-lane block per tensor: fewer than 2^32 work-items
     if (n >= (1u << 24)) return fail(TTP_ERR_INVALID, "too many tensors (max 2^24 - 1)");
     // the table must describe a store that fits one GPU: the padded footprint sum cannot
@@ -1023,7 +1086,12 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
     }
     c->total = off;
     int rc;
-    if (mode == TTP_MODE_MIXED) {
+    if (mode == TTP_MODE_MIXED && sgd_layout) {
+        // the SGD layout: a contiguous master, no m / v (until the first Adam use), bf16 copy
+        c->sgd_layout = true;
+        if ((rc = alloc_zero(c, (void**)&c->master, c->total * 4))) return bail(rc);
+        if ((rc = alloc_zero(c, &c->param, c->total * 2))) return bail(rc);
+    } else if (mode == TTP_MODE_MIXED) {
         // [master|m|v] records (m, v zero until the first Adam step) and the bf16 copy
         if ((rc = alloc_zero(c, (void**)&c->records, c->total * 4 * 3))) return bail(rc);
         c->master = c->records;
@@ -1198,6 +1266,13 @@ int ttp_upload(ttp_ctx* c, int which, uint32_t index, const void* src, uint64_t 
             hipLaunchKernelGGL(ttp::bf16_to_master_kernel, dim3(elementwise_grid(c, cnt)),
                                dim3(ttp::kBlock), 0, c->stream, (const uint16_t*)c->param,
                                c->master, buffer_stride(c, TTP_BUF_MASTER), off, cnt);
+            HIP_TRY(hipGetLastError());
+        } else if (c->mode == TTP_MODE_MIXED && which == TTP_BUF_MASTER) {
+            // the SGD layout's contiguous master: its bf16 copy follows, as for records
+            clear_hip_error();
+            hipLaunchKernelGGL(ttp::master_to_bf16_kernel, dim3(elementwise_grid(c, cnt)),
+                               dim3(ttp::kBlock), 0, c->stream, (const float*)c->master,
+                               ttp::kRec, (uint16_t*)c->param, off, cnt);
             HIP_TRY(hipGetLastError());
         }
         if (kind == TTP_HOST) HIP_TRY(hipStreamSynchronize(c->stream));
@@ -1386,8 +1461,9 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
     if (report && (rc = no_capture(c, "a step report (synchronises)"))) return rc;
     if ((rc = set_dev(c))) return rc;
     if (noalloc && !c->exp_avg)
-        return fail(TTP_ERR_STATE, "the first Adam step of an FP32 store allocates m and v, "
-                                   "which the no-allocation step does not: step once with "
+        return fail(TTP_ERR_STATE, "the first Adam step of an FP32 store, or of a MIXED store "
+                                   "in the SGD layout, allocates m and v, which the "
+                                   "no-allocation step does not: step once with "
                                    "ttp_adam_step[_subset] first");
     if ((rc = ensure_adam_state(c))) return rc;
     const WorkTables* w;
@@ -1549,39 +1625,35 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
         ttp::SgdArgs al = a;
         al.st = c->st;  // the lane forms read the device state unconditionally
         clear_hip_error();
-        if (!mom && c->mode == TTP_MODE_MIXED)
-            launch_lanes(c,
-                         (uint64_t)n * ttp::lane_parts<kLaneSgdPlainMixed, kLanesSgdPlainMixed,
-                                                       kItSgdPlainMixed>(),
-                         kLanesSgdPlainMixed, [&](dim3 g, uint64_t p0) {
-                hipLaunchKernelGGL(
-                    (ttp::sgd_lane_kernel<uint16_t, true, kLaneSgdPlainMixed, kLanesSgdPlainMixed,
-                                          kItSgdPlainMixed>), g,
-                    dim3(kLanesSgdPlainMixed), 0, c->stream, g16, c->master, c->momentum, p16, al,
-                    p0);
-            });
+        // launches the lane-form kernel of shape <E, LN, IT> with master stride MS
+#define TTP_SGD_LANES(GT, MIXED, MS, E, LN, IT, G, P16)                                        \
+    launch_lanes(c, (uint64_t)n * ttp::lane_parts<E, LN, IT>(), LN, [&](dim3 g, uint64_t p0) { \
+        hipLaunchKernelGGL((ttp::sgd_lane_kernel<GT, MIXED, MS, E, LN, IT>), g, dim3(LN), 0,  \
+                           c->stream, G, c->master, c->momentum, P16, al, p0);                \
+    })
+        if (c->mode == TTP_MODE_MIXED && c->sgd_layout && !mom)
+            TTP_SGD_LANES(uint16_t, true, ttp::kRec, kLaneSgdPlainContig, kLanesSgdPlainContig,
+                          kItSgdPlainContig, g16, p16);
+        else if (c->mode == TTP_MODE_MIXED && c->sgd_layout)
+            TTP_SGD_LANES(uint16_t, true, ttp::kRec, kLaneSgdMomContig, kLanesSgdMomContig,
+                          kItSgdMomContig, g16, p16);
+        else if (!mom && c->mode == TTP_MODE_MIXED)
+            TTP_SGD_LANES(uint16_t, true, ttp::kStrideMixed, kLaneSgdPlainMixed,
+                          kLanesSgdPlainMixed, kItSgdPlainMixed, g16, p16);
         else if (grads_cached(c, w) && c->mode == TTP_MODE_MIXED)
-            hipLaunchKernelGGL((ttp::sgd_kernel<uint16_t, true>), dim3(n), block, c->upd_lds,
-                               c->stream, g16, c->master, c->momentum, p16, a);
+            hipLaunchKernelGGL((ttp::sgd_kernel<uint16_t, true, ttp::kStrideMixed>), dim3(n),
+                               block, c->upd_lds, c->stream, g16, c->master, c->momentum, p16,
+                               a);
         else if (c->mode == TTP_MODE_MIXED)
-            launch_lanes(c,
-                         (uint64_t)n *
-                             ttp::lane_parts<kLaneSgdMixed, kLanesSgdMixed, kItSgdMixed>(),
-                         kLanesSgdMixed, [&](dim3 g, uint64_t p0) {
-                hipLaunchKernelGGL(
-                    (ttp::sgd_lane_kernel<uint16_t, true, kLaneSgdMixed, kLanesSgdMixed,
-                                          kItSgdMixed>), g,
-                    dim3(kLanesSgdMixed), 0, c->stream, g16, c->master, c->momentum, p16, al, p0);
-            });
+            TTP_SGD_LANES(uint16_t, true, ttp::kStrideMixed, kLaneSgdMixed, kLanesSgdMixed,
+                          kItSgdMixed, g16, p16);
+        else if (!mom)
+            TTP_SGD_LANES(float, false, ttp::kRec, kLaneSgdPlainFp32, kLanesSgdPlainFp32,
+                          kItSgdPlainFp32, g32, (uint16_t*)nullptr);
         else
-            launch_lanes(c,
-                         (uint64_t)n * ttp::lane_parts<kLaneSgdFp32, kLanesSgdFp32, kItSgdFp32>(),
-                         kLanesSgdFp32, [&](dim3 g, uint64_t p0) {
-                hipLaunchKernelGGL(
-                    (ttp::sgd_lane_kernel<float, false, kLaneSgdFp32, kLanesSgdFp32, kItSgdFp32>),
-                    g, dim3(kLanesSgdFp32), 0, c->stream, g32, c->master, c->momentum,
-                    (uint16_t*)nullptr, al, p0);
-            });
+            TTP_SGD_LANES(float, false, ttp::kRec, kLaneSgdFp32, kLanesSgdFp32, kItSgdFp32, g32,
+                          (uint16_t*)nullptr);
+#undef TTP_SGD_LANES
         HIP_TRY(hipGetLastError());
         tl.done();
         if (mom) {

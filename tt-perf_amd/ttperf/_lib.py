@@ -13,6 +13,8 @@ LIB_PATH = os.environ.get("TTPERF_LIB", os.path.join(_PKG, "lib", "libttperf_hip
 OK = 0
 ERR_INVALID, ERR_NO_DEVICE, ERR_HIP, ERR_OOM, ERR_STATE, ERR_RANGE = -1, -2, -3, -4, -5, -6
 MODE_FP32, MODE_MIXED = 0, 1
+STORE_SGD = 0x100
+ABI_VERSION = 2
 BUF_PARAM, BUF_GRAD, BUF_MASTER, BUF_EXP_AVG, BUF_EXP_AVG_SQ, BUF_MOMENTUM = range(6)
 ALL_TENSORS = 0xFFFFFFFF
 TENSOR_DECAY = 1
@@ -152,6 +154,9 @@ def _load():
 
 
 lib = _load()
+if lib.ttp_abi_version() != ABI_VERSION:
+    raise ImportError(f"{LIB_PATH} implements ABI version {lib.ttp_abi_version()}; this binding "
+                      f"is written against version {ABI_VERSION}: rebuild the library")
 
 
 def check(rc):

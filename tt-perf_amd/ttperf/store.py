@@ -210,12 +210,17 @@ class ParamStore:
     mode   : "fp32" (fp32 params/grads, params are the master copy) or
              "mixed" (bf16 params/grads + fp32 master, m, v)
     decay  : per-tensor bools (weight decay applies), default: tensors with >= 2 dims
+    layout : "default", or "sgd": a mixed store for SGD, with a contiguous fp32 master and no
+             m / v (TTP_STORE_SGD; the first Adam step converts it to the default layout)
     """
 
-    def __init__(self, shapes, *, mode="fp32", decay=None, names=None, device=0):
+    def __init__(self, shapes, *, mode="fp32", decay=None, names=None, device=0,
+                 layout="default"):
         shapes = [tuple(s) if isinstance(s, (tuple, list)) else (int(s),) for s in shapes]
         if mode not in ("fp32", "mixed"):
             raise ValueError("mode must be 'fp32' or 'mixed'")
+        if layout not in ("default", "sgd"):
+            raise ValueError("layout must be 'default' or 'sgd'")
         self.mode = L.MODE_MIXED if mode == "mixed" else L.MODE_FP32
         if decay is None:
             decay = [len(s) >= 2 for s in shapes]
@@ -226,7 +231,8 @@ class ParamStore:
             descs[i].numel = int(math.prod(s)) if s else 1
             descs[i].flags = self.flags[i]
         h = C.c_void_p()
-        L.check(L.lib.ttp_create(device, descs, n, self.mode, C.byref(h)))
+        create_mode = self.mode | (L.STORE_SGD if layout == "sgd" else 0)
+        L.check(L.lib.ttp_create(device, descs, n, create_mode, C.byref(h)))
         self._h = h
         self.device = device
         names = names or [f"p{i}" for i in range(n)]
@@ -297,10 +303,19 @@ class ParamStore:
     # ---- buffers -----------------------------------------------------------------------------
     def ptr(self, which, index=L.ALL_TENSORS):
         """Device address of a contiguously stored buffer (PARAM, GRAD, MOMENTUM; MASTER in
-        FP32 mode); the interleaved optimizer state raises (see layout())."""
+        FP32 mode and in the SGD layout); the interleaved optimizer state raises (see
+        layout())."""
         p = C.c_void_p()
         L.check(L.lib.ttp_buffer_ptr(self._h, which, index, C.byref(p)))
         return p.value
+
+    @property
+    def sgd_layout(self):
+        """Whether the master is contiguous because of the SGD layout (a mixed store created
+        with layout="sgd" that no Adam step has converted yet)."""
+        if self.mode != L.MODE_MIXED:
+            return False
+        return self.layout(L.BUF_MASTER)[2] == 64
 
     def layout(self, which):
         """(base, group, stride): flat element e of `which` sits at
