@@ -15,8 +15,11 @@ set-up (before the settle steps), the step with a cold Infinity Cache (512 MB of
 reads before each step, outside its event pair), the step right after a rewrite of its
 gradients, the mean skipped (overflow) step, the step with its norm from bucketed sums, and
 the other configurations' steps (the MLP, nanoGPT-char, GPT-2 774M mixed AdamW, GPT-2 XL
-fp32 AdamW and SGD momentum), each in a store of its own, and the step of the reference's
-GPT benchmark model through the C++ drop-in surface (tests/cpp/bench_gpt2_step).
+fp32 AdamW and SGD momentum; the reference's plain SGD and SGD momentum in mixed precision at
+GPT-2 124M and 774M on stores in the SGD layout, and SGD momentum at 774M in the default
+layout), each in a store of its own, and the step of the reference's GPT benchmark model
+through the C++ drop-in surface (tests/cpp/bench_gpt2_step).  `--optimizer sgd|sgdm` and
+`--layout sgd` time those steps as the main leg instead (for profiling).
 """
 import argparse
 import ctypes
@@ -36,7 +39,11 @@ HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
 CACHED_GRAD_BYTES = 256 << 20
 # algorithmic bytes per parameter of one update-kernel pass (and of the norm pass)
 UPDATE_BYTES = {("adamw", "mixed"): 28, ("adamw", "fp32"): 28, ("sgdm", "fp32"): 20,
-                ("sgdm", "mixed"): 20}
+                ("sgdm", "mixed"): 20, ("sgd", "mixed"): 12, ("sgd", "fp32"): 12}
+# update legs below this many algorithmic bytes are launch-bound or Infinity-Cache resident:
+# an event pair around each launch then measures mostly its own overhead, and a copy of their
+# bytes no ceiling, so neither is reported for them
+MIN_TIMED_UPDATE_BYTES = 1 << 30
 NORM_BYTES = {"mixed": 2, "fp32": 4}
 
 # The step of each BASELINE.json configuration: optimizer hyperparameters, loss scaling, and
@@ -74,7 +81,12 @@ def parse():
     ap.add_argument("--config", default="gpt2_124m", choices=sorted(BENCH),
                     help="a BASELINE.json configuration (gpt2_124m is the headline metric's), "
                          "or gpt2_124m_shard8: one GPU's ZeRO-1 shard of it")
-    ap.add_argument("--optimizer", default="adamw", choices=["adamw", "sgdm"])
+    ap.add_argument("--optimizer", default="adamw", choices=["adamw", "sgdm", "sgd"],
+                    help="adamw (the headline); sgdm: SGD with momentum 0.9 and the "
+                         "configuration's clipping; sgd: the reference's plain SGD, w - lr*g")
+    ap.add_argument("--layout", default="default", choices=["default", "sgd"],
+                    help="store layout of a mixed store (sgd: TTP_STORE_SGD, a contiguous "
+                         "master and no m / v)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--overlap", action="store_true",
@@ -125,6 +137,17 @@ def traffic_from_profiles(config, optimizer):
     return float(m.group(1)) if m else None
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or None."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(numels, flags, mode_mixed, grads_host, hp, seconds, scaler):
     """The CPU oracle (C restatement of the reference's optimizer) on this host's cores:
     the fused step on all threads (the reported value), the same on 1 thread, and the
@@ -162,7 +185,7 @@ def cpu_baseline(numels, flags, mode_mixed, grads_host, hp, seconds, scaler):
     total = sum(numels)
     n, el = res["fused"]
     out = {"value": round(total * n / el / 1e9, 4), "unit": "Gparams/s", "cores": nthreads,
-           "kind": "port",
+           "cpu_model": cpu_model(), "kind": "port",
            "sample": f"full {len(numels)}-tensor table ({total} params), {n} fused steps "
                      f"(the same step as the GPU's) in {el:.1f} s on {nthreads} threads",
            "ms_per_step": round(el / n * 1e3, 3)}
@@ -274,6 +297,70 @@ def bucketed_norm(store, stream, args, hp, mode, numels):
             "overlap": overlap}
 
 
+def producer_step(store, stream, args, hp, mode, numels):
+    """The step fed by a backward's gradient producer: zero_grad(set_to_none), then one
+    ttp_accumulate_grad per tensor from device memory (in reverse tensor order, as a backward
+    produces them; the gradients are a device copy of the store's own), then the step.  Each
+    variant is captured once as a hipGraph (so the host's 100+ calls per iteration do not pace
+    the GPU) and replayed K times between one event pair:
+      norm_pass:   plain accumulates, then the step with its norm pass;
+      fused_sums:  accumulates that also store each tensor's sum (TTP_ACCUM_SUMSQ), then the
+                   step from those sums (TTP_STEP_TENSOR_SUMS: no norm pass);
+    and the producer alone (zero_grad + accumulates) with and without the sums.  Returns the
+    JSON object."""
+    import torch
+    from ttperf import _lib as L
+
+    src = store.torch_view(L.BUF_GRAD).clone()  # the store's layout, so tensor i at offsets[i]
+    base, esz = src.data_ptr(), src.element_size()
+    dtype = L.DTYPE_BF16 if mode == "mixed" else L.DTYPE_F32
+    order = [i for i in reversed(range(len(numels))) if numels[i]]
+
+    def produce(sums):
+        store.zero_grad(set_to_none=True)
+        flag = L.ACCUM_SUMSQ if sums else 0
+        for i in order:
+            L.check(L.lib.ttp_accumulate_grad(store.handle, i,
+                                              ctypes.c_void_p(base + store.offsets[i] * esz),
+                                              numels[i], dtype | flag, L.DEVICE))
+
+    def iteration(sums, step=True):
+        produce(sums)
+        if step:
+            store.adam_step(tensor_sums=sums, **hp)
+
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    out = {}
+    for key, sums, step in (("norm_pass_ms", False, True), ("fused_sums_ms", True, True),
+                            ("producer_ms", False, False), ("producer_with_sums_ms", True, False)):
+        iteration(sums, step)  # eagerly once: work tables and the tile-sum buffer
+        torch.cuda.synchronize()
+        store.begin_capture()
+        iteration(sums, step)
+        graph = store.end_capture()
+        for _ in range(3):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(args.steps):
+            graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        out[key] = round(e0.elapsed_time(e1) / args.steps, 4)
+        graph.close()
+    del src
+    out["step_saved_ms"] = round(out["norm_pass_ms"] - out["fused_sums_ms"], 4)
+    out["tensors"] = len(order)
+    out["note"] = ("zero_grad(set_to_none) + one ttp_accumulate_grad per tensor from device "
+                   "memory + the AdamW step, captured as one hipGraph and replayed K times "
+                   "between one event pair; fused_sums: the accumulates also store each "
+                   "tensor's gradient sum and the step runs no norm pass; producer_*: the "
+                   "zero_grad and accumulates alone")
+    log(f"bench: producer + step: {out['norm_pass_ms']} ms with the norm pass, "
+        f"{out['fused_sums_ms']} ms with fused sums")
+    return out
+
+
 def ceilings(stream, update_bytes):
     """The practical ceilings of the update's traffic on this GPU, over its byte count
     `update_bytes`: torch's device copy (a blit kernel), and libttperf_ceiling's non-temporal
@@ -335,10 +422,11 @@ def ceilings(stream, update_bytes):
     return copy_gbps, nt_copy_gbps, nt_read_gbps, copy_bytes, nt_copy64_gbps
 
 
-def make_store(config, seed=1234):
-    """A store of `config`'s table on cuda:0 with N(0, 0.02) master weights and the
-    configuration's synthetic gradients resident in HBM, on a created stream.  Returns
-    (store, stream, grads as a device tensor)."""
+def make_store(config, seed=1234, layout="default", scaler=True):
+    """A store of `config`'s table on cuda:0 (in `layout`) with N(0, 0.02) master weights and
+    the configuration's synthetic gradients resident in HBM, on a created stream; loss scaling
+    as the configuration has it, unless `scaler` is False.  Returns (store, stream, grads as a
+    device tensor)."""
     import torch
     import ttperf
     from ttperf import _lib as L
@@ -347,18 +435,18 @@ def make_store(config, seed=1234):
     names, shapes, decay, numels = configs.table(config)
     mode = configs.mode(config)
     dev = torch.device("cuda:0")
-    store = ttperf.ParamStore(shapes, mode=mode, decay=decay, names=names)
+    store = ttperf.ParamStore(shapes, mode=mode, decay=decay, names=names, layout=layout)
     # a created stream (the legacy default stream cannot be captured); torch's events and
     # synchronisation see it
     stream = torch.cuda.Stream()
     store.set_stream(stream)
     cfg = BENCH[config]
-    scale = cfg["scaler"] or 1.0
+    scale = (cfg["scaler"] or 1.0) if scaler else 1.0
     gen = torch.Generator(device=dev).manual_seed(seed)
     w = torch.randn(store.total, generator=gen, device=dev) * 0.02
     store.upload(L.BUF_MASTER, L.ALL_TENSORS, w)
     del w
-    if cfg["scaler"]:
+    if cfg["scaler"] and scaler:
         store.configure_scaler(True, init_scale=scale)
     g = torch.randn(store.total, generator=gen, device=dev) * cfg["std"]
     if cfg["heavy"]:
@@ -371,33 +459,49 @@ def make_store(config, seed=1234):
     return store, stream, g
 
 
+# the reference's SGD (autograd/dynamic/optim.hpp:21-27, every traced sgd_step): w - lr*g, no
+# clipping or loss scaling (bench/autograd/bench_gpt2_full.cpp:110 trains at lr 0.01)
+SGD_LR = 0.01
+
+
 def step_fn(store, optimizer, hp):
     if optimizer == "adamw":
         return lambda: store.adam_step(**hp)
+    if optimizer == "sgd":
+        return lambda: store.sgd_step(lr=SGD_LR)
     return lambda: store.sgd_step(lr=hp["lr"], momentum=0.9, max_grad_norm=hp["max_grad_norm"])
 
 
-def update_kernel_name(optimizer, mode, total_elems):
+def update_kernel_name(optimizer, mode, total_elems, layout="default"):
     """The update instantiation libttperf_hip launches for a store (its rocprof name): the lane
     form with its elements per lane, lanes per block and pieces per block (kLaneAdamMixed ...
-    in tt-perf_amd/csrc/ttperf.hip), except while the gradients fit the Infinity Cache: MIXED
-    Adam then takes the kLaneAdamMixedCached shape, and MIXED SGD momentum (the only SGD this
-    bench steps) the four-element kernel."""
+    in tt-perf_amd/csrc/ttperf.hip; the SGD forms also with their master's record stride, 64
+    for a contiguous master), except while the gradients fit the Infinity Cache: MIXED Adam
+    then takes the kLaneAdamMixedCached shape, and MIXED SGD momentum in the default layout the
+    four-element kernel."""
     grad_t, mixed_t = ("unsigned short", "true") if mode == "mixed" else ("float", "false")
-    kname = "adam" if optimizer == "adamw" else "sgd"
-    if mode == "mixed" and total_elems * 2 <= CACHED_GRAD_BYTES:
-        if kname == "adam":
+    if optimizer == "adamw":
+        if mode == "mixed" and total_elems * 2 <= CACHED_GRAD_BYTES:
             return f"adam_lane_kernel<{grad_t}, {mixed_t}, 1, 128, 2>"
-        return f"sgd_kernel<{grad_t}, {mixed_t}>"
-    shape = {("adam", "mixed"): (1, 256, 2), ("adam", "fp32"): (1, 128, 2),
-             ("sgd", "mixed"): (1, 256, 2), ("sgd", "fp32"): (2, 64, 1)}[(kname, mode)]
-    return f"{kname}_lane_kernel<{grad_t}, {mixed_t}, {shape[0]}, {shape[1]}, {shape[2]}>"
+        e, ln, it = (1, 256, 2) if mode == "mixed" else (1, 128, 2)
+        return f"adam_lane_kernel<{grad_t}, {mixed_t}, {e}, {ln}, {it}>"
+    contiguous = mode == "fp32" or layout == "sgd"
+    stride = "64u" if contiguous else "192u"
+    if optimizer == "sgdm" and not contiguous and total_elems * 2 <= CACHED_GRAD_BYTES:
+        return f"sgd_kernel<{grad_t}, {mixed_t}, {stride}>"
+    shape = {("sgdm", "mixed", False): (1, 256, 2), ("sgd", "mixed", False): (2, 256, 1),
+             ("sgdm", "mixed", True): (2, 128, 1), ("sgd", "mixed", True): (4, 64, 1),
+             ("sgdm", "fp32", True): (2, 64, 1), ("sgd", "fp32", True): (2, 256, 2)}[
+        (optimizer, mode, contiguous)]
+    return f"sgd_lane_kernel<{grad_t}, {mixed_t}, {stride}, {shape[0]}, {shape[1]}, {shape[2]}>"
 
 
-def other_config(config, optimizer, steps, warmup, settle_ms):
+def other_config(config, optimizer, steps, warmup, settle_ms, layout="default"):
     """One more configuration's step in a store of its own (created, timed, closed): settle
     steps and W warmup steps, K steps between one event pair, then K more with an event pair
-    around every launch for the update kernel's own time.  Returns the JSON object."""
+    around every launch for the update kernel's own time.  The SGD legs step without loss
+    scaling (plain SGD: the reference's w - lr*g, no norm pass; SGD momentum: the
+    configuration's clipping).  Returns the JSON object."""
     import torch
     from ttperf import _lib as L
     from ttperf import configs
@@ -407,7 +511,8 @@ def other_config(config, optimizer, steps, warmup, settle_ms):
     n_params = sum(numels)
     cfg = BENCH[config]
     hp = dict(cfg["hp"], decoupled=cfg["decoupled"])
-    store, stream, g = make_store(config)
+    scaler = bool(cfg["scaler"]) and optimizer == "adamw"
+    store, stream, g = make_store(config, layout=layout, scaler=scaler)
     del g
     torch.cuda.empty_cache()
     step = step_fn(store, optimizer, hp)
@@ -431,11 +536,12 @@ def other_config(config, optimizer, steps, warmup, settle_ms):
     upd_ms, upd_n = store.timing_collect(L.KERNEL_UPDATE)
     nrm_ms, nrm_n = store.timing_collect(L.KERNEL_NORM)
     store.timing(False)
-    upd_kernel = update_kernel_name(optimizer, mode, store.total)
+    upd_kernel = update_kernel_name(optimizer, mode, store.total, layout)
+    sgd_layout = store.sgd_layout
     # with loss scaling: 20 overflow steps between one event pair (a +inf planted in the
     # first tensor's gradients), as for the headline configuration
     skip_ms = None
-    if optimizer == "adamw" and cfg["scaler"]:
+    if scaler:
         store.upload(L.BUF_GRAD, 0, torch.full((numels[0],), float("inf"), device="cuda",
                                                dtype=torch.bfloat16 if mode == "mixed"
                                                else torch.float32))
@@ -451,30 +557,39 @@ def other_config(config, optimizer, steps, warmup, settle_ms):
     store.close()
     torch.cuda.empty_cache()
     ub = UPDATE_BYTES[(optimizer, mode)]
-    # the norm pass runs only with clipping or loss scaling
-    nb = NORM_BYTES[mode] if (cfg["hp"]["max_grad_norm"] or cfg["scaler"]) else 0
+    # the norm pass runs only with clipping or loss scaling (plain SGD has neither)
+    norm_runs = optimizer != "sgd" and bool(cfg["hp"]["max_grad_norm"] or scaler)
+    nb = NORM_BYTES[mode] if norm_runs else 0
     upd_avg = upd_ms / max(upd_n, 1)
     step_gbps = n_params * (ub + nb) / (ms / 1e3) / 1e9
     upd_gbps = n_params * ub / (upd_avg / 1e3) / 1e9
-    # the plain non-temporal copies of the update's bytes on this GPU, in the same run (not
-    # for stores whose traffic is launch-bound or cache-resident)
+    # the plain non-temporal copies of the update's bytes on this GPU, in the same run; the
+    # update's own time and rate only where they mean something (MIN_TIMED_UPDATE_BYTES)
+    timed = n_params * ub >= MIN_TIMED_UPDATE_BYTES
     nt_copy_gbps = nt_copy64_gbps = None
-    if n_params * ub >= 1 << 30:
+    if timed:
         _, nt_copy_gbps, _, _, nt_copy64_gbps = ceilings(stream, n_params * ub)
-    log(f"bench: {config} {optimizer}: {ms:.4f} ms/step, update {upd_avg:.4f} ms")
+    log(f"bench: {config} {optimizer} ({layout} layout): {ms:.4f} ms/step, "
+        f"update {upd_avg:.4f} ms")
     return {"ms_per_step": round(ms, 4),
             "Gparams_per_s": round(n_params / (ms / 1e3) / 1e9, 3),
             "step_bytes_per_param": ub + nb,
             "step_hbm_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
-            "update_ms": round(upd_avg, 4),
-            "update_frac": round(upd_gbps / HBM_PEAK_GBPS, 4),
+            "update_ms": round(upd_avg, 4) if timed else None,
+            "update_frac": round(upd_gbps / HBM_PEAK_GBPS, 4) if timed else None,
             "update_vs_nt_copy": round(upd_gbps / nt_copy_gbps, 4) if nt_copy_gbps else None,
             "nt_copy_GBps": round(nt_copy_gbps, 1) if nt_copy_gbps else None,
             "update_vs_nt_copy64": round(upd_gbps / nt_copy64_gbps, 4) if nt_copy64_gbps else None,
             "nt_copy64_GBps": round(nt_copy64_gbps, 1) if nt_copy64_gbps else None,
-            "norm_pass_ms": round(nrm_ms / max(nrm_n, 1), 4),
+            "norm_pass_ms": round(nrm_ms / max(nrm_n, 1), 4) if (timed and norm_runs) else None,
             "skipped_step_ms": round(skip_ms, 4) if skip_ms is not None else None,
             "update_kernel": upd_kernel,
+            "optimizer": {"adamw": "AdamW", "sgdm": "SGD momentum 0.9",
+                          "sgd": f"SGD (w - lr*g, lr {SGD_LR})"}[optimizer]
+                         + (", clip 1.0" if optimizer != "sgd" and cfg["hp"]["max_grad_norm"]
+                            else "")
+                         + (f", loss scaling {cfg['scaler']:g}" if scaler else ""),
+            "layout": "sgd" if sgd_layout else "default",
             "params": n_params, "tensors": len(numels), "mode": mode,
             "steps": steps, "warmup": warmup, "settle_steps": settle_n}
 
@@ -527,8 +642,11 @@ def main():
     torch.cuda.set_device(dev)
     cfg = BENCH[args.config]
     hp = dict(cfg["hp"], decoupled=cfg["decoupled"])
-    scale = cfg["scaler"] or 1.0
-    store, stream, g = make_store(args.config)
+    # the SGD steps run without loss scaling (see other_config)
+    scaler = bool(cfg["scaler"]) and args.optimizer == "adamw"
+    scale = cfg["scaler"] if scaler else 1.0
+    norm_runs = args.optimizer != "sgd" and bool(cfg["hp"]["max_grad_norm"] or scaler)
+    store, stream, g = make_store(args.config, layout=args.layout, scaler=scaler)
     store_total = store.total
     grads_host = None
     if not args.no_cpu_baseline and args.optimizer == "adamw":
@@ -641,7 +759,7 @@ def main():
     # skipped (overflow) steps: only the norm pass and the finalize do work; min(K, 20) of
     # them between one event pair (each backs the loss scale off; it is reset afterwards)
     skip_ms, n_skip = None, 0
-    if args.optimizer == "adamw" and cfg["scaler"]:
+    if scaler:
         store.upload(L.BUF_GRAD, 0, torch.full((store.tensors[0].numel,), float("inf"),
                                                device=dev, dtype=torch.bfloat16 if mode == "mixed"
                                                else torch.float32))
@@ -660,22 +778,26 @@ def main():
     # context: the step with its norm from bucketed per-tensor sums (first undoing the overflow
     # planted above), and the practical ceilings of the update's traffic on this GPU
     sums = None
-    if cfg["hp"]["max_grad_norm"] or cfg["scaler"]:
+    if norm_runs:
         store.upload(L.BUF_GRAD, 0, torch.zeros(store.tensors[0].numel, device=dev,
                                                 dtype=torch.bfloat16 if mode == "mixed"
                                                 else torch.float32))
         sums = bucketed_norm(store, stream, args, hp, mode, numels)
+    producer = None
+    if norm_runs and args.optimizer == "adamw":
+        producer = producer_step(store, stream, args, hp, mode, numels)
     ub = UPDATE_BYTES[(args.optimizer, mode)]
-    nb = NORM_BYTES[mode]
+    nb = NORM_BYTES[mode] if norm_runs else 0
     copy_gbps, nt_copy_gbps, nt_read_gbps, copy_bytes, nt_copy64_gbps = \
         ceilings(stream, n_params * ub)
 
     achieved = n_params * ub / (upd_avg / 1e3) / 1e9
-    upd_kernel = update_kernel_name(args.optimizer, mode, store_total)
+    upd_kernel = update_kernel_name(args.optimizer, mode, store_total, args.layout)
     step_gbps = n_params * (ub + nb) / (ms_step / 1e3) / 1e9
     out = {
         "metric": HEADLINE if args.config == "gpt2_124m" and args.optimizer == "adamw" else
-                  f"fused {args.optimizer} step Gparams/s + % of HBM peak, {args.config} {mode}",
+                  f"fused {args.optimizer} step Gparams/s + % of HBM peak, {args.config} {mode}"
+                  + (" (SGD layout)" if args.layout == "sgd" else ""),
         "value": round(n_params / (ms_step / 1e3) / 1e9, 3),
         "unit": "Gparams/s",
         "n_gpus": 1,
@@ -689,16 +811,19 @@ def main():
         "launch": "hipGraph replay of the captured step" if args.graph else "eager launches",
         "data": f"synthetic (seeded N(0,{cfg['std']:g})"
                 + (f", {cfg['heavy']:g} of them N(0,1)" if cfg["heavy"] else "")
-                + (f" x loss scale {scale:g}" if cfg["scaler"] else "")
+                + (f" x loss scale {scale:g}" if scaler else "")
                 + (" bf16" if mode == "mixed" else " fp32") + " grads, N(0,0.02) fp32 master)",
         "config": {"workload": f"{args.config} {args.optimizer} step: {len(numels)} tensors, "
                                f"{n_params} params, {mode} precision, "
-                               + (f"loss scaling {scale:g}, " if cfg["scaler"] else "")
-                               + (f"clip {hp['max_grad_norm']}, " if hp["max_grad_norm"] else "")
+                               + (f"loss scaling {scale:g}, " if scaler else "")
+                               + (f"clip {hp['max_grad_norm']}, "
+                                  if hp["max_grad_norm"] and args.optimizer != "sgd" else "")
                                + (f"lr {hp['lr']:g}, betas {hp['betas']}, "
                                   f"wd {hp['weight_decay']:g} on 2-D tensors"
                                   if args.optimizer == "adamw" else
-                                  f"lr {hp['lr']:g}, momentum 0.9"),
+                                  f"lr {hp['lr']:g}, momentum 0.9" if args.optimizer == "sgdm"
+                                  else f"lr {SGD_LR:g} (w - lr*g)")
+                               + (", SGD layout" if args.layout == "sgd" else ""),
                    "params": n_params, "tensors": len(numels), "mode": mode,
                    "bytes_per_param": ub + nb},
         "step_hbm_GBps": round(step_gbps, 1),
@@ -726,6 +851,7 @@ def main():
         "skipped_step_ms": round(skip_ms, 4) if skip_ms is not None else None,
         "skipped_step_note": f"mean of {n_skip} overflow steps between one event pair",
         "bucketed_norm": sums,
+        "producer_step": producer,
         "torch_copy_GBps": round(copy_gbps, 1),
         "ceilings": {"nt_copy_GBps": round(nt_copy_gbps, 1),
                      "nt_copy_frac": round(nt_copy_gbps / HBM_PEAK_GBPS, 4),
@@ -752,20 +878,30 @@ def main():
     torch.cuda.empty_cache()
     if not args.no_other_configs and args.config == "gpt2_124m" and args.optimizer == "adamw":
         # the other large configurations, one store at a time (GPT-2 XL fp32 holds 31 GB)
-        legs = (("mlp_fp32_adam", "mlp", "adamw"),
-                ("nanogpt_char_mixed_adamw", "nanogpt_char", "adamw"),
-                ("gpt2_774m_mixed_adamw", "gpt2_774m", "adamw"),
-                ("gpt2_1558m_fp32_adamw", "gpt2_1558m", "adamw"),
-                ("gpt2_1558m_fp32_sgdm", "gpt2_1558m", "sgdm"))
+        legs = (("mlp_fp32_adam", "mlp", "adamw", "default"),
+                ("nanogpt_char_mixed_adamw", "nanogpt_char", "adamw", "default"),
+                ("gpt2_774m_mixed_adamw", "gpt2_774m", "adamw", "default"),
+                ("gpt2_1558m_fp32_adamw", "gpt2_1558m", "adamw", "default"),
+                ("gpt2_1558m_fp32_sgdm", "gpt2_1558m", "sgdm", "default"),
+                # the reference's own optimizer (plain SGD) and SGD momentum in mixed
+                # precision, on stores in the SGD layout; SGD momentum also in the default
+                # layout ([master|m|v] records), which a store that Adam also steps keeps
+                ("gpt2_124m_mixed_sgd", "gpt2_124m", "sgd", "sgd"),
+                ("gpt2_774m_mixed_sgd", "gpt2_774m", "sgd", "sgd"),
+                ("gpt2_124m_mixed_sgdm", "gpt2_124m", "sgdm", "sgd"),
+                ("gpt2_774m_mixed_sgdm", "gpt2_774m", "sgdm", "sgd"),
+                ("gpt2_774m_mixed_sgdm_default_layout", "gpt2_774m", "sgdm", "default"))
         out["other_configs"] = {
-            key: other_config(config, opt, args.steps, args.warmup, args.settle_ms)
-            for key, config, opt in legs}
+            key: other_config(config, opt, args.steps, args.warmup, args.settle_ms, layout)
+            for key, config, opt, layout in legs}
         out["other_configs"]["note"] = (
             "each in a store of its own, created, timed (settle steps and W warmup steps, then "
             "K steps between one event pair; the update alone from a second pass with an event "
-            "pair per launch) and closed before the next; no CPU leg; the copy ceilings only "
-            "where the update moves at least 1 GiB (the MLP's 269 KB step is launch-bound and "
-            "the char model's 323 MB mostly Infinity-Cache resident)")
+            "pair per launch) and closed before the next; no CPU leg; the update's own time, "
+            "the copy ceilings and the norm pass's time only where the update moves at least "
+            "1 GiB (the MLP's 269 KB step is launch-bound and the char model's 301 MB update "
+            "mostly Infinity-Cache resident: an event pair around each of their launches "
+            "measures mostly its own overhead; see profiles/ for their kernels' durations)")
         log("bench: the C++ drop-in program (tests/cpp/bench_gpt2_step) ...")
         out["cpp_dropin"] = cpp_dropin(args.steps, args.warmup, args.settle_ms)
     if grads_host is not None:

@@ -105,15 +105,17 @@ struct Value {
 
     // autograd/dynamic/autograd.hpp:78-83: grad = grad + incoming, or the first assignment;
     // done on the GPU in the flat grad buffer (one launch, no host round trip of the grad)
-    void accumulate_grad(const std::vector<float>& incoming) {
+    // sums: the same launch also stores this parameter's gradient sum of squares, so that an
+    // optimizer with tensor_sums set needs no pass over the gradients after the backward
+    void accumulate_grad(const std::vector<float>& incoming, bool sums = false) {
         if (!requires_grad) return;
         if (incoming.size() != numel()) throw std::invalid_argument("grad shape mismatch");
-        store().accumulate_grad(index, incoming);
+        store().accumulate_grad(index, incoming, sums);
     }
     // the same with a device-resident gradient (TTP_DTYPE_F32 or TTP_DTYPE_BF16)
-    void accumulate_grad_device(const void* incoming, int dtype) {
+    void accumulate_grad_device(const void* incoming, int dtype, bool sums = false) {
         if (!requires_grad) return;
-        store().accumulate_grad_device(index, incoming, dtype);
+        store().accumulate_grad_device(index, incoming, dtype, sums);
     }
     // device address of this parameter's gradient slice, for backward kernels that write it
     void* grad_ptr() { return store().device_ptr(TTP_BUF_GRAD, index); }

@@ -57,7 +57,8 @@ extern "C" {
 #endif
 
 /* ABI version, returned by ttp_abi_version().  Changes:
- *   2  TTP_STORE_SGD (the SGD layout of a MIXED store, OR'd into ttp_create's mode).
+ *   2  TTP_STORE_SGD (the SGD layout of a MIXED store, OR'd into ttp_create's mode);
+ *      TTP_ACCUM_SUMSQ (ttp_accumulate_grad also stores the tensor's gradient sum).
  *      Behaviour changes of existing entry points, which a caller written against version 1
  *      must follow: ttp_zero_grad_subset with set_to_none = 0 leaves the has-grad flags as
  *      they were (version 1 marked the listed tensors as having a grad); a captured
@@ -122,6 +123,9 @@ extern "C" {
 /* Element types of incoming gradients (ttp_accumulate_grad). */
 #define TTP_DTYPE_F32 0
 #define TTP_DTYPE_BF16 1
+/* OR'd into ttp_accumulate_grad's src_dtype: also store the tensor's sum of squares of its
+ * resulting gradients for a TTP_STEP_TENSOR_SUMS step (see ttp_accumulate_grad). */
+#define TTP_ACCUM_SUMSQ 0x100
 
 typedef struct ttp_ctx ttp_ctx;
 typedef struct ttp_graph ttp_graph;
@@ -294,7 +298,18 @@ int ttp_zero_grad_subset(ttp_ctx* ctx, const uint32_t* indices, uint32_t n_indic
  * Captured, the call's choice between assigning and adding is fixed at capture time, so it
  * is refused (TTP_ERR_STATE) unless an earlier call of the same capture set that tensor's
  * has-grad flag (ttp_zero_grad[_subset] with set_to_none = 1, ttp_set_has_grad, a gradient
- * upload or an accumulate): every launch then finds the flag as the capture did. */
+ * upload or an accumulate): every launch then finds the flag as the capture did.
+ * src_dtype | TTP_ACCUM_SUMSQ: the same launch also computes the sum of squares of the
+ * tensor's resulting gradients (unscaled by the current loss scale, as
+ * ttp_grad_sumsq_tensors does, tile for tile in the same order, so bit-identical to it) and
+ * stores it as the tensor's current sum: a backward that accumulates every parameter's last
+ * gradient this way leaves a TTP_STEP_TENSOR_SUMS step nothing to read twice (no norm pass, no
+ * bucket call).  It adds no launch and no memory traffic to the accumulate: the launch writes
+ * one partial per wave of each 16 KiB tile into a store-wide array (32 B per 16 KiB of
+ * gradients, allocated with the store), and the next step from sums combines the pending
+ * partials of all its tensors in one launch.  The loss scale must not change between this call and the step (as
+ * for any sum).  A tensor of 2^24 or more 16 KiB tiles of gradients is refused with
+ * TTP_ERR_RANGE. */
 int ttp_accumulate_grad(ttp_ctx* ctx, uint32_t index, const void* src, uint64_t n,
                         int src_dtype, int src_kind);
 

@@ -216,13 +216,16 @@ public:
         check(ttp_zero_grad_subset(ctx_, indices.data(), (uint32_t)indices.size(),
                                    set_to_none ? 1 : 0));
     }
-    // grad = g if tensor i has none, else grad + g (fp32 add, one rounding to the grad type)
-    void accumulate_grad(uint32_t i, const std::vector<float>& g) {
-        check(ttp_accumulate_grad(ctx_, i, g.data(), g.size(), TTP_DTYPE_F32, TTP_HOST));
+    // grad = g if tensor i has none, else grad + g (fp32 add, one rounding to the grad type);
+    // sums: also store tensor i's gradient sum for a tensor_sums step (TTP_ACCUM_SUMSQ)
+    void accumulate_grad(uint32_t i, const std::vector<float>& g, bool sums = false) {
+        check(ttp_accumulate_grad(ctx_, i, g.data(), g.size(),
+                                  TTP_DTYPE_F32 | (sums ? TTP_ACCUM_SUMSQ : 0), TTP_HOST));
     }
     // the same from device memory (fp32 or bf16 bits), e.g. a backward kernel's output
-    void accumulate_grad_device(uint32_t i, const void* src, int dtype) {
-        check(ttp_accumulate_grad(ctx_, i, src, numel(i), dtype, TTP_DEVICE));
+    void accumulate_grad_device(uint32_t i, const void* src, int dtype, bool sums = false) {
+        check(ttp_accumulate_grad(ctx_, i, src, numel(i), dtype | (sums ? TTP_ACCUM_SUMSQ : 0),
+                                  TTP_DEVICE));
     }
     void* device_ptr(int which, uint32_t i = TTP_ALL_TENSORS) {
         void* p = nullptr;

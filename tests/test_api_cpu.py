@@ -53,6 +53,8 @@ def test_abi_version():
     assert L.lib.ttp_abi_version() == header == L.ABI_VERSION == 2
     assert int(re.search(r"#define TTP_STORE_SGD (0x[0-9a-fA-F]+)", text).group(1), 16) == \
         L.STORE_SGD
+    assert int(re.search(r"#define TTP_ACCUM_SUMSQ (0x[0-9a-fA-F]+)", text).group(1), 16) == \
+        L.ACCUM_SUMSQ
     # the C++ wrapper refuses a library of another version
     hpp = open(os.path.join(REPO, "include", "ttperf", "ttperf.hpp")).read()
     assert "ttp_abi_version() != TTP_ABI_VERSION" in hpp
@@ -361,22 +363,33 @@ def test_bench_names_the_update_shapes_the_library_launches():
     import bench
     assert bench.CACHED_GRAD_BYTES == bound
     big = 1 << 30
-    for (opt, mode, name, grad_t, mixed_t) in (
-            ("adamw", "mixed", "AdamMixed", "unsigned short", "true"),
-            ("adamw", "fp32", "AdamFp32", "float", "false"),
-            ("sgdm", "mixed", "SgdMixed", "unsigned short", "true"),
-            ("sgdm", "fp32", "SgdFp32", "float", "false")):
+    # (optimizer, mode, layout, shape constant, master stride of an SGD form)
+    for (opt, mode, layout, name, stride) in (
+            ("adamw", "mixed", "default", "AdamMixed", None),
+            ("adamw", "fp32", "default", "AdamFp32", None),
+            ("sgdm", "mixed", "default", "SgdMixed", "192u"),
+            ("sgd", "mixed", "default", "SgdPlainMixed", "192u"),
+            ("sgdm", "mixed", "sgd", "SgdMomContig", "64u"),
+            ("sgd", "mixed", "sgd", "SgdPlainContig", "64u"),
+            ("sgdm", "fp32", "default", "SgdFp32", "64u"),
+            ("sgd", "fp32", "default", "SgdPlainFp32", "64u")):
+        grad_t, mixed_t = ("unsigned short", "true") if mode == "mixed" else ("float", "false")
         e, lanes, it = shape(name)
         kname = "adam" if opt == "adamw" else "sgd"
-        assert bench.update_kernel_name(opt, mode, big) == \
-            f"{kname}_lane_kernel<{grad_t}, {mixed_t}, {e}, {lanes}, {it}>"
-        # below the bound: MIXED Adam its cached-gradient lane shape, MIXED SGD the
-        # four-element kernel, FP32 Adam and SGD the same lane forms as above it
+        tmpl = f"{grad_t}, {mixed_t}, " + (f"{stride}, " if stride else "")
+        want = f"{kname}_lane_kernel<{tmpl}{e}, {lanes}, {it}>"
+        assert bench.update_kernel_name(opt, mode, big, layout) == want, (opt, mode, layout)
+        # below the bound: MIXED Adam its cached-gradient lane shape, MIXED SGD momentum in
+        # the default layout the four-element kernel, every other update the same lane form
         if name == "AdamMixed":
             e, lanes, it = shape("AdamMixedCached")
-        small = (f"sgd_kernel<{grad_t}, {mixed_t}>" if name == "SgdMixed" else
-                 f"{kname}_lane_kernel<{grad_t}, {mixed_t}, {e}, {lanes}, {it}>")
-        assert bench.update_kernel_name(opt, mode, 1 << 20) == small
+            want = f"adam_lane_kernel<{tmpl}{e}, {lanes}, {it}>"
+        if name == "SgdMixed":
+            want = f"sgd_kernel<{grad_t}, {mixed_t}, {stride}>"
+        assert bench.update_kernel_name(opt, mode, 1 << 20, layout) == want, (opt, mode, layout)
+        # and the library launches that instantiation
+        kern = re.sub(r"<.*", "", want)
+        assert kern in src
     # the library launches no four-element Adam kernel, and the four-element SGD kernel only
     # in mixed precision
     assert "adam_kernel<" not in src

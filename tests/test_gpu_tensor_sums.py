@@ -471,3 +471,165 @@ def test_step_from_sums_of_more_tensors_than_one_finalize_round():
         compare_state(store, ref, max_ulp=2)
     store.close()
     twin.close()
+
+
+def _bits(t):
+    """A torch tensor's host copy in the oracle's types (bf16 bits or float32)."""
+    import torch
+    t = t.detach().cpu()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+@pytest.mark.parametrize("mode", [O.MODE_MIXED, O.MODE_FP32])
+def test_accumulate_with_sums_feeds_a_tensor_sums_step(mode):
+    """The gradient producer's side of the bucketed norm: a backward accumulates two
+    gradients into every tensor (assign, then add), the second with TTP_ACCUM_SUMSQ, which
+    stores the tensor's sum of squares of its resulting gradients in the same launch; the
+    step then takes its norm from those sums (no norm pass, no bucket call).  Sources vary:
+    device bf16 / fp32, host fp32 / bf16 bits, and a device source that is not 16-byte aligned.
+    Against the oracle (orc_accumulate_grad, then its own norm): gradients bit-exact, the
+    same skip / found_inf / scale / step decisions, the norm within 1e-10, the state within
+    2 ulp; against a twin store given the same accumulates without sums and a bucket-sums
+    call over every tensor: the norm and the whole state bit-identical (the sums are the same
+    tile for tile).  With loss scaling (mixed), an incoming +inf on step 2 makes the sum
+    non-finite and the step skip.  An accumulate without sums after one with them leaves the
+    tensor's sum stale, and the step is refused."""
+    import ttperf
+    from ttperf import _lib as L
+    torch = torch_mod()
+    store, ref = make_pair(SHAPES, DECAY, mode, seed=140)
+    twin, _ = make_pair(SHAPES, DECAY, mode, seed=140)
+    mixed = mode == O.MODE_MIXED
+    if mixed:
+        for s in (store, twin):
+            s.configure_scaler(True, init_scale=512.0, growth_interval=2)
+        ref.configure_scaler(True, 512.0, growth_interval=2)
+    hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=0.5)
+    gen = torch.Generator(device="cuda").manual_seed(141)
+    n = len(SHAPES)
+    for step in range(5):
+        scale = ref.scale if mixed else 1.0
+        for s in (store, twin):
+            s.zero_grad(set_to_none=True)
+        ref.zero_grad(set_to_none=True)
+        for i in reversed(range(n)):  # the order a backward produces them
+            numel = store.tensors[i].numel
+            g1 = torch.randn(numel, generator=gen, device="cuda") * 1e-2 * scale
+            g1 = g1.to(torch.bfloat16) if mixed else g1
+            g2 = (torch.randn(numel, generator=gen, device="cuda") * 1e-2 * scale)
+            if mixed and step == 2 and i == 9:
+                g2[77] = float("inf")
+            if i == 5:  # a device source at an odd address: element-wise loads
+                buf = torch.zeros(numel + 1, device="cuda", dtype=torch.float32)
+                buf[1:] = g2
+                src2 = buf[1:]
+                assert src2.data_ptr() % 16
+                host2 = _bits(src2)
+            elif mixed:
+                src2 = host2 = g2.cpu().numpy()  # host fp32 into bf16 gradients
+            else:
+                src2 = host2 = _bits(g2.to(torch.bfloat16))  # host bf16 bits into fp32
+            for s in (store, twin):
+                s.accumulate_grad(i, g1)
+            store.accumulate_grad(i, src2, sums=True)
+            twin.accumulate_grad(i, src2)
+            ref.accumulate_grad(i, _bits(g1))
+            ref.accumulate_grad(i, host2)
+        twin.grad_sumsq_tensors(list(range(n)))
+        r = store.adam_step(report=True, tensor_sums=True, **hp)
+        rt = twin.adam_step(report=True, tensor_sums=True, **hp)
+        e = ref.adam_step(**hp)
+        print(f"step {step}: norm {r['grad_norm']!r} (bucket sums {rt['grad_norm']!r}, oracle "
+              f"{e['grad_norm']!r}), skipped {r['skipped']}", flush=True)
+        for k in ("skipped", "found_inf", "step", "scale", "growth_tracker"):
+            assert r[k] == rt[k] == e[k], (k, r, rt, e)
+        assert r["skipped"] == (mixed and step == 2)
+        assert np.array_equal(np.float64(r["grad_norm"]), np.float64(rt["grad_norm"])) or \
+            not np.isfinite(rt["grad_norm"])
+        if np.isfinite(e["grad_norm"]):
+            assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-10 * e["grad_norm"]
+        got = store.download(L.BUF_GRAD)
+        assert np.array_equal(got.view(np.uint8), ref.grad[:store.total].view(np.uint8))
+        compare_state(store, ref, max_ulp=2)
+    for which in (L.BUF_MASTER, L.BUF_EXP_AVG, L.BUF_EXP_AVG_SQ, L.BUF_PARAM):
+        assert np.array_equal(store.download(which).view(np.uint8),
+                              twin.download(which).view(np.uint8)), which
+    # a later accumulate without sums makes that tensor's sum stale: refused, nothing changed
+    store.accumulate_grad(3, np.ones(store.tensors[3].numel, np.float32), sums=True)
+    store.accumulate_grad(3, np.ones(store.tensors[3].numel, np.float32))
+    t0 = store.step_count
+    with pytest.raises(ttperf.TTPError) as err:
+        store.adam_step(tensor_sums=True, indices=[3], **hp)
+    assert err.value.code == L.ERR_STATE and store.step_count == t0
+    store.close()
+    twin.close()
+
+
+def test_captured_accumulates_with_sums_and_step_replay():
+    """A backward's accumulates with their sums and the step from those sums captured as one
+    graph (zero_grad to None, one accumulate per tensor from device memory, the AdamW step
+    with loss scaling and clipping), replayed four times with new source gradients (one with
+    +inf), each against the oracle; eager steps from bucket sums between the replays, and the
+    first replay before any eager accumulate with sums (the captured step combines the pending
+    tile sums whatever the eager history)."""
+    from ttperf import _lib as L
+    torch = torch_mod()
+    store, ref = make_pair(SHAPES, DECAY, O.MODE_MIXED, seed=150)
+    store.set_stream(None)  # the store's own stream: capturable
+    store.configure_scaler(True, init_scale=256.0, growth_interval=3)
+    ref.configure_scaler(True, 256.0, growth_interval=3)
+    hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=0.5)
+    gen = torch.Generator(device="cuda").manual_seed(151)
+    n = len(SHAPES)
+    srcs = [torch.zeros(store.tensors[i].numel, device="cuda", dtype=torch.bfloat16)
+            for i in range(n)]
+
+    def refill(inf=False):
+        for i in range(n):
+            srcs[i].copy_((torch.randn(srcs[i].numel(), generator=gen, device="cuda") * 1e-2
+                           * ref.scale).to(torch.bfloat16))
+        if inf:
+            srcs[6][11] = float("inf")
+        torch.cuda.synchronize()
+
+    def ref_iteration():
+        ref.zero_grad(set_to_none=True)
+        for i in reversed(range(n)):
+            ref.accumulate_grad(i, _bits(srcs[i]))
+        return ref.adam_step(**hp)
+
+    # one eager Adam step builds the work and bias tables a capture cannot build
+    ref.grad[:store.total] = device_grads(store, gen, 1e-2, scale=ref.scale)
+    for i in range(n):
+        ref.set_has_grad(i, True)
+    store.adam_step(**hp)
+    ref.adam_step(**hp)
+    store.begin_capture()
+    store.zero_grad(set_to_none=True)
+    for i in reversed(range(n)):
+        store.accumulate_grad(i, srcs[i], sums=True)
+    store.adam_step(tensor_sums=True, **hp)
+    graph = store.end_capture()
+    for k in range(4):
+        refill(inf=(k == 2))
+        graph.replay()
+        e = ref_iteration()
+        store.sync()
+        print(f"replay {k}: oracle norm {e['grad_norm']!r}, skipped {e['skipped']}", flush=True)
+        assert store.step_count == e["step"]
+        assert store.scaler_state() == (np.float32(e["scale"]), e["growth_tracker"])
+        assert e["skipped"] == (k == 2)
+        compare_state(store, ref, max_ulp=2)
+        # an eager step from bucket sums in between
+        ref.grad[:store.total] = device_grads(store, gen, 1e-2, scale=ref.scale)
+        for i in range(n):
+            ref.set_has_grad(i, True)
+        store.grad_sumsq_tensors(list(range(n)))
+        r = store.adam_step(report=True, tensor_sums=True, **hp)
+        e = ref.adam_step(**hp)
+        assert (r["skipped"], r["step"], r["scale"]) == (e["skipped"], e["step"], e["scale"])
+        compare_state(store, ref, max_ulp=2)
+    graph.close()
+    store.close()

@@ -208,12 +208,17 @@ struct GradVec<uint16_t> {
     static __device__ __forceinline__ float at(const raw& w, int j) {
         return (j & 1) ? bf16_hi(w[j >> 1]) : bf16_lo(w[j >> 1]);
     }
+    // element j of a vector that starts as zeros
+    static __device__ __forceinline__ void put(raw& w, int j, uint16_t h) {
+        w[j >> 1] |= (j & 1) ? ((uint32_t)h << 16) : (uint32_t)h;
+    }
 };
 template <>
 struct GradVec<float> {
     static constexpr int kElems = 4;
     typedef f32x4 raw;
     static __device__ __forceinline__ float at(const raw& w, int j) { return w[j]; }
+    static __device__ __forceinline__ void put(raw& w, int j, float x) { w[j] = x; }
 };
 
 // Norm tiles: kNormLoads 16-byte loads per lane, so a tile is 16 KiB of gradients (8192 bf16
@@ -450,14 +455,12 @@ __global__ void scaler_update_kernel(DevState* st, int32_t growth_interval, doub
 // tile: block t adds the tile sums of the t-th listed tensor, tiles tile_start[t] ..
 // tile_start[t+1]-1, each lane in tile order, then the fixed block reduction, into
 // sums[tensor_ids[t]].
-__global__ __launch_bounds__(kBlock) void tensor_sums_kernel(const double* __restrict__ tile_sums,
-                                                             const uint32_t* __restrict__ tile_start,
-                                                             const uint32_t* __restrict__ tensor_ids,
-                                                             double* __restrict__ sums) {
-    __shared__ double lds[kBlock / 64];
-    const uint32_t t = blockIdx.x;
-    const uint32_t b = tile_start[t], e = tile_start[t + 1];
-    // as norm_finalize_kernel: a round's loads issued before its adds, each lane's order fixed
+// the sum of tile_sums[b .. e-1] in a fixed order (valid in thread 0): each lane adds its tiles
+// in tile order, a round's loads issued before its adds (as norm_finalize_kernel), then the
+// fixed block reduction.  One order for every caller, so a tensor's sum does not depend on
+// which call computed its tiles.
+__device__ __forceinline__ double sum_tiles(const double* __restrict__ tile_sums, uint32_t b,
+                                            uint32_t e, double* lds) {
     constexpr int kPer = 8;
     double s = 0.0;
     for (uint32_t base = b; base < e; base += kBlock * kPer) {
@@ -470,8 +473,69 @@ __global__ __launch_bounds__(kBlock) void tensor_sums_kernel(const double* __res
 #pragma unroll
         for (int k = 0; k < kPer; ++k) s += v[k];
     }
+    return block_sum(s, lds);
+}
+
+// A tensor's sum supersedes tile sums an earlier accumulate with sums left pending for it.
+__global__ __launch_bounds__(kBlock) void tensor_sums_kernel(const double* __restrict__ tile_sums,
+                                                             const uint32_t* __restrict__ tile_start,
+                                                             const uint32_t* __restrict__ tensor_ids,
+                                                             double* __restrict__ sums,
+                                                             uint32_t* __restrict__ pending) {
+    __shared__ double lds[kBlock / 64];
+    const uint32_t t = blockIdx.x;
+    const double s = sum_tiles(tile_sums, tile_start[t], tile_start[t + 1], lds);
+    if (threadIdx.x == 0) {
+        sums[tensor_ids[t]] = s;
+        pending[tensor_ids[t]] = 0u;
+    }
+}
+
+// The wave partials an accumulate with sums leaves per 16 KiB tile (kWaves of them, in wave
+// order; see accumulate_grad_tiles_kernel): tile k's sum is their total added as block_sum
+// adds its waves' sums, (((0 + w0) + w1) + w2) + w3, so it equals the norm pass's partial of
+// that tile bit for bit.
+constexpr int kWaves = kBlock / 64;
+__device__ __forceinline__ double tile_from_waves(const double* __restrict__ w, uint32_t k) {
+    double r = 0.0;
+#pragma unroll
+    for (int j = 0; j < kWaves; ++j) r += w[(uint64_t)k * kWaves + j];
+    return r;
+}
+
+// Before a step that takes its norm from per-tensor sums: block t combines the t-th stepped
+// tensor's tile sums that accumulates with their sums left in the store-wide array (the wave
+// partials of its tiles, from kWaves x tile_base[tensor]), if it has any pending: each tile
+// from its waves, then the tiles in sum_tiles' order, so the tensor's sum equals what
+// ttp_grad_sumsq_tensors gives for the same gradients.  One launch per step instead of one
+// per accumulate.
+__global__ __launch_bounds__(kBlock) void combine_pending_sums_kernel(
+    const double* __restrict__ acc_waves, const uint32_t* __restrict__ tile_base,
+    const uint32_t* __restrict__ tile_start, const uint32_t* __restrict__ tensor_ids,
+    uint32_t* __restrict__ pending, double* __restrict__ sums) {
+    __shared__ double lds[kBlock / 64];
+    const uint32_t t = blockIdx.x, i = tensor_ids[t];
+    if (!pending[i]) return;  // uniform over the block
+    const double* w = acc_waves + (uint64_t)tile_base[i] * kWaves;
+    const uint32_t e = tile_start[t + 1] - tile_start[t];
+    // sum_tiles' order, over tile values formed from the wave partials
+    constexpr int kPer = 8;
+    double s = 0.0;
+    for (uint32_t base = 0; base < e; base += kBlock * kPer) {
+        double v[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const uint32_t j = base + (uint32_t)k * kBlock + threadIdx.x;
+            v[k] = j < e ? tile_from_waves(w, j) : 0.0;
+        }
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) s += v[k];
+    }
     s = block_sum(s, lds);
-    if (threadIdx.x == 0) sums[tensor_ids[t]] = s;
+    if (threadIdx.x == 0) {
+        sums[i] = s;
+        pending[i] = 0u;
+    }
 }
 
 // ------------------------------------------------------------------------------------
@@ -920,6 +984,155 @@ __device__ __forceinline__ void zero_vec(uint16_t* g, uint64_t i, int n) {
         __builtin_nontemporal_store(u32x2{0u, 0u}, reinterpret_cast<u32x2*>(g + i));
     } else {
         for (int j = 0; j < n; ++j) g[i + j] = 0;
+    }
+}
+
+// The same accumulation over one tensor of n elements in 16 KiB norm tiles, one block per tile,
+// all of a lane's loads of a whole tile issued before its arithmetic (the grid-stride kernel
+// above, one element per lane per iteration, serves tensors of 2^24 or more tiles only).
+// kSums: it also computes the sum of squares of the resulting (stored) gradients, unscaled by
+// 1/scale when scaler_on: block b takes tile b (tiles start at the tensor's first element, as
+// the norm pass's tiles do), each lane the elements the norm pass's lane takes in that tile
+// (kNormLoads vectors of GradVec<GradT>::kElems), the squares go into the two accumulators in
+// the norm pass's order, and each wave's total (wave_sum, block_sum's first stage) is stored
+// as that tile's partial of that wave.  tile_from_waves then adds a tile's wave partials as
+// block_sum does, so the tile sums are bit-identical to norm_partials_kernel's over the same
+// gradients.  A wave's partial needs no LDS and no barrier (a block reduction lengthened each
+// launch by 0.6-2.4 us).  Block 0 marks the tensor's partials pending.  The squares come from
+// values already in registers, so the sums add no memory traffic.  kVecSrc: the source is
+// 16-byte aligned and read in vectors (else element by element).
+template <int E, bool kVecSrc>
+__device__ __forceinline__ void ld_src(const uint16_t* p, float* out) {
+    if constexpr (kVecSrc && E == 8) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            out[2 * j] = bf16_lo(w[j]);
+            out[2 * j + 1] = bf16_hi(w[j]);
+        }
+    } else if constexpr (kVecSrc && E == 4) {
+        const u32x2 w = *reinterpret_cast<const u32x2*>(p);
+        out[0] = bf16_lo(w.x);
+        out[1] = bf16_hi(w.x);
+        out[2] = bf16_lo(w.y);
+        out[3] = bf16_hi(w.y);
+    } else {
+#pragma unroll
+        for (int j = 0; j < E; ++j) out[j] = to_f32(p[j]);
+    }
+}
+template <int E, bool kVecSrc>
+__device__ __forceinline__ void ld_src(const float* p, float* out) {
+    if constexpr (kVecSrc) {
+#pragma unroll
+        for (int h = 0; h < E / 4; ++h) {
+            const f32x4 w = *reinterpret_cast<const f32x4*>(p + 4 * h);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) out[4 * h + j] = w[j];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < E; ++j) out[j] = p[j];
+    }
+}
+
+template <typename SrcT, typename GradT, bool kVecSrc, bool kSums>
+__global__ __launch_bounds__(kBlock) void accumulate_grad_tiles_kernel(
+    GradT* __restrict__ grad, const SrcT* __restrict__ src, uint64_t n, int first,
+    const DevState* __restrict__ st, int32_t scaler_on, double* __restrict__ wave_sums,
+    uint32_t* __restrict__ pending) {
+    typedef GradVec<GradT> GV;
+    typedef typename GV::raw R;
+    constexpr int E = GV::kElems;
+    constexpr uint32_t kTile = norm_tile_elems<GradT>();
+    const float inv = (kSums && scaler_on) ? (float)(1.0 / (double)st->scale) : 1.0f;
+    const uint64_t t0 = (uint64_t)blockIdx.x * kTile;
+    const uint32_t count = (uint32_t)min((uint64_t)kTile, n - t0);
+    double acc[2] = {0.0, 0.0};
+    // the squares of a vector's stored values, in the norm pass's order
+    auto add_squares = [&](const float* v, uint32_t nv) {
+        if constexpr (kSums) {
+#pragma unroll
+            for (int j = 0; j < E; ++j) {
+                const double x = (uint32_t)j < nv ? (double)(v[j] * inv) : 0.0;
+                acc[j & 1] = __builtin_fma(x, x, acc[j & 1]);
+            }
+        }
+    };
+    // a whole vector's new values from the incoming ones (and the old gradient vector w),
+    // stored as one 16-byte word; v receives the stored values
+    auto store_vec = [&](uint64_t i, const float* in, const R& w, float* v) {
+#pragma unroll
+        for (int j = 0; j < E; ++j) {
+            const float r = first ? in[j] : GV::at(w, j) + in[j];
+            GradT h;
+            from_f32(r, &h);
+            v[j] = to_f32(h);
+        }
+        if constexpr (E == 8) {
+            u32x4 o;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = bf16_pack(v[2 * j], v[2 * j + 1]);
+            *reinterpret_cast<u32x4*>(grad + i) = o;
+        } else {
+            *reinterpret_cast<f32x4*>(grad + i) = f32x4{v[0], v[1], v[2], v[3]};
+        }
+    };
+    if (count == kTile) {
+        // a whole tile: every load of the lane issued before the arithmetic (the scheduling
+        // barrier keeps them ahead of it, as in the norm pass: with one vector in flight at a
+        // time the call ran at a fraction of the copy rate)
+        float in[kNormLoads][E];
+        R w[kNormLoads];
+#pragma unroll
+        for (int l = 0; l < kNormLoads; ++l) {
+            const uint64_t i = t0 + (uint32_t)(l * kBlock + threadIdx.x) * E;
+            ld_src<E, kVecSrc>(src + i, in[l]);
+            if (!first) w[l] = *reinterpret_cast<const R*>(grad + i);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int l = 0; l < kNormLoads; ++l) {
+            float v[E];
+            store_vec(t0 + (uint32_t)(l * kBlock + threadIdx.x) * E, in[l], w[l], v);
+            add_squares(v, (uint32_t)E);
+        }
+    } else {  // a tensor's last tile: the vectors (and elements) below its count
+#pragma unroll
+        for (int l = 0; l < kNormLoads; ++l) {
+            const uint32_t off = (uint32_t)(l * kBlock + threadIdx.x) * E;
+            const uint32_t nv = off < count ? min(count - off, (uint32_t)E) : 0u;
+            if (!nv) continue;
+            const uint64_t i = t0 + off;
+            float v[E];
+            if (nv == (uint32_t)E) {
+                float in[E];
+                ld_src<E, kVecSrc>(src + i, in);
+                R w;
+                if (!first) w = *reinterpret_cast<const R*>(grad + i);
+                store_vec(i, in, w, v);
+            } else {  // the tensor's last, partial vector
+#pragma unroll
+                for (int j = 0; j < E; ++j) {
+                    v[j] = 0.0f;
+                    if ((uint32_t)j < nv) {
+                        const float x = to_f32(src[i + j]);
+                        const float r = first ? x : to_f32(grad[i + j]) + x;
+                        GradT h;
+                        from_f32(r, &h);
+                        grad[i + j] = h;
+                        v[j] = to_f32(h);
+                    }
+                }
+            }
+            add_squares(v, nv);
+        }
+    }
+    if constexpr (kSums) {
+        // each wave's total, the first stage of block_sum, with no LDS or barrier after it
+        const double part = wave_sum(acc[0] + acc[1]);
+        if ((threadIdx.x & 63) == 0) wave_sums[(uint64_t)blockIdx.x * kWaves + threadIdx.x / 64] = part;
+        if (blockIdx.x == 0 && threadIdx.x == 0) *pending = 1u;
     }
 }
 

@@ -194,6 +194,16 @@ struct ttp_ctx {
     std::vector<uint8_t> cap_touched, cap_fresh0, cap_grad0, cap_needs;
     double* tile_sums = nullptr;  // one per norm tile of a ttp_grad_sumsq_tensors call
     uint32_t tile_sums_cap = 0;
+    // accumulates with their sums (TTP_ACCUM_SUMSQ): per norm tile of the store, one partial
+    // per wave (tensor i's from kWaves x tile_base[i]), and per tensor whether they are still to be
+    // combined into tsum (device flags; the next step from sums combines them).  acc_sums_used
+    // is set by the first such accumulate: eager steps from sums combine from then on,
+    // captured ones always
+    double* acc_tiles = nullptr;
+    uint32_t* tile_base = nullptr;
+    std::vector<uint32_t> host_tile_base;
+    uint32_t* tsum_pending = nullptr;
+    bool acc_sums_used = false;
     std::vector<void*> retired;   // replaced buffers that live graphs may still write
 
     // bias-correction tables of every betas pair stepped with (kept, since captured graphs
@@ -334,11 +344,34 @@ int check_sums_current(ttp_ctx* c, const std::vector<uint32_t>& active) {
         if (!c->tsum_fresh[i])
             return fail(TTP_ERR_STATE, "tensor " + std::to_string(i) +
                                            " has no current gradient sum: call "
-                                           "ttp_grad_sumsq_tensors after its last gradient write "
-                                           "and after the previous step");
+                                           "ttp_grad_sumsq_tensors (or accumulate its gradient "
+                                           "with TTP_ACCUM_SUMSQ) after its last gradient write, "
+                                           "after the last step that updated it and after the "
+                                           "last change of the loss scale");
     if (c->capturing)
         for (uint32_t i : active)
             if (!(c->cap_touched[i] & kCapFresh)) c->cap_needs[i] = 1;
+    return TTP_OK;
+}
+
+// The per-tile sums buffer of ttp_grad_sumsq_tensors and of accumulates with their sums, grown
+// to `tiles` entries (at least one); `what` names the call in the refusal while capturing.
+int ensure_tile_sums(ttp_ctx* c, uint32_t tiles, const char* what) {
+    tiles = std::max<uint32_t>(tiles, 1);
+    if (tiles <= c->tile_sums_cap) return TTP_OK;
+    int rc;
+    if ((rc = no_capture(c, (std::string(what) + " (allocates)").c_str()))) return rc;
+    HIP_TRY(hipStreamSynchronize(c->stream));  // queued calls may still use the old buffer
+    if (c->tile_sums) {
+        if (c->n_graphs)
+            c->retired.push_back(c->tile_sums);  // a captured call may write it on replay
+        else
+            HIP_TRY(hipFree(c->tile_sums));
+    }
+    c->tile_sums = nullptr;
+    c->tile_sums_cap = 0;
+    HIP_TRY(hipMalloc((void**)&c->tile_sums, (size_t)tiles * sizeof(double)));
+    c->tile_sums_cap = tiles;
     return TTP_OK;
 }
 
@@ -737,6 +770,16 @@ int launch_prologue(ttp_ctx* c, const WorkTables* w, bool run_norm, double max_n
     a.partials = partials;
     a.npartials = run_norm ? ns.partials() : 0;
     if (run_norm && from_sums) {  // the step's tensors' sums, in tensor order
+        // tile sums that accumulates with their sums left pending: combined first (a captured
+        // step always launches this, since its replays may find them pending)
+        if (w->n_tensors && (c->capturing || c->acc_sums_used)) {
+            clear_hip_error();
+            hipLaunchKernelGGL(ttp::combine_pending_sums_kernel, dim3(w->n_tensors),
+                               dim3(ttp::kBlock), 0, c->stream, (const double*)c->acc_tiles,
+                               (const uint32_t*)c->tile_base, (const uint32_t*)w->tile_start,
+                               (const uint32_t*)w->tensor_ids, c->tsum_pending, c->tsum);
+            HIP_TRY(hipGetLastError());
+        }
         a.partials = c->tsum;
         a.idx = w->tensor_ids;
         a.npartials = w->n_tensors;
@@ -969,7 +1012,8 @@ void release(ttp_ctx* c) {
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     for (void* p : {(void*)c->grad, (void*)c->records, (void*)c->momentum, (void*)c->mom_init,
                     (void*)c->st, (void*)c->partials, c->staging, (void*)c->tsum,
-                    (void*)c->tile_sums})
+                    (void*)c->tile_sums, (void*)c->acc_tiles, (void*)c->tile_base,
+                    (void*)c->tsum_pending})
         if (p) (void)hipFree(p);
     for (auto& kv : c->bias_tables) (void)hipFree(kv.second.first);
     free_tables(c->all);
@@ -1110,6 +1154,23 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
     if ((rc = alloc_zero(c, (void**)&c->partials, (uint64_t)c->partials_cap * 8))) return bail(rc);
     if ((rc = alloc_zero(c, (void**)&c->tsum, std::max<uint64_t>(n, 1) * 8))) return bail(rc);
     c->tsum_fresh.assign(n, 0);
+    // the tile sums of accumulates with their sums: 32 B per 16 KiB of gradients
+    {
+        const uint64_t tile = norm_tile(c);
+        uint64_t tiles = 0;
+        c->host_tile_base.resize(std::max<uint32_t>(n, 1), 0);
+        for (uint32_t i = 0; i < n; ++i) {
+            c->host_tile_base[i] = (uint32_t)tiles;  // at most 2^40 / 4096 tiles
+            tiles += (descs[i].numel + tile - 1) / tile;
+        }
+        if ((rc = alloc_zero(c, (void**)&c->acc_tiles,
+                             std::max<uint64_t>(tiles, 1) * ttp::kWaves * 8)))
+            return bail(rc);
+        if ((rc = alloc_zero(c, (void**)&c->tsum_pending, std::max<uint64_t>(n, 1) * 4)))
+            return bail(rc);
+        if ((rc = alloc_zero(c, (void**)&c->tile_base, (uint64_t)c->host_tile_base.size() * 4)))
+            return bail(rc);
+    }
 
     std::vector<uint32_t> every;
     for (uint32_t i = 0; i < n; ++i)
@@ -1125,6 +1186,9 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
     s.scale = (float)c->scaler.init_scale;
     if (hipMemcpy(c->st, &s, sizeof(s), hipMemcpyHostToDevice) != hipSuccess)
         return bail(fail(TTP_ERR_HIP, "state upload failed"));
+    if (hipMemcpy(c->tile_base, c->host_tile_base.data(), c->host_tile_base.size() * 4,
+                  hipMemcpyHostToDevice) != hipSuccess)
+        return bail(fail(TTP_ERR_HIP, "tile table upload failed"));
     *out = c;
     return TTP_OK;
 }
@@ -1380,8 +1444,11 @@ int ttp_accumulate_grad(ttp_ctx* c, uint32_t index, const void* src, uint64_t n,
     int rc = check_ctx(c);
     if (rc) return rc;
     if ((rc = check_index(c, index))) return rc;
+    const bool with_sums = (dtype & TTP_ACCUM_SUMSQ) != 0;
+    dtype &= ~TTP_ACCUM_SUMSQ;
     if (dtype != TTP_DTYPE_F32 && dtype != TTP_DTYPE_BF16)
-        return fail(TTP_ERR_INVALID, "src_dtype must be TTP_DTYPE_F32 or TTP_DTYPE_BF16");
+        return fail(TTP_ERR_INVALID, "src_dtype must be TTP_DTYPE_F32 or TTP_DTYPE_BF16, "
+                                     "optionally | TTP_ACCUM_SUMSQ");
     if (kind != TTP_HOST && kind != TTP_DEVICE) return fail(TTP_ERR_INVALID, "bad memory kind");
     if (kind == TTP_HOST && (rc = no_capture(c, "accumulating a host gradient"))) return rc;
     // Whether the kernel assigns (no grad yet) or adds is fixed when the call is captured.
@@ -1406,6 +1473,15 @@ int ttp_accumulate_grad(ttp_ctx* c, uint32_t index, const void* src, uint64_t n,
     if (kind == TTP_DEVICE &&
         (rc = check_device_buffer(c, src, n * sbytes, "the incoming gradient")))
         return rc;
+    // with its sum: one block per 16 KiB norm tile of the tensor's gradients
+    const uint64_t ntiles = with_sums ? (n + norm_tile(c) - 1) / norm_tile(c) : 0;
+    if (with_sums) {
+        if (ntiles >= (1u << 24))
+            return fail(TTP_ERR_RANGE, "tensor " + std::to_string(index) + " has " +
+                                           std::to_string(ntiles) +
+                                           " tiles of 16 KiB of gradients; an accumulate with "
+                                           "its sum takes at most 2^24 - 1");
+    }
     if (n) {
         const void* dsrc = src;
         if (kind == TTP_HOST) {
@@ -1414,30 +1490,65 @@ int ttp_accumulate_grad(ttp_ctx* c, uint32_t index, const void* src, uint64_t n,
             dsrc = c->staging;
         }
         const int first = t.has_grad ? 0 : 1;
-        const uint32_t grid = elementwise_grid(c, n);
-        const bool mixed = c->mode == TTP_MODE_MIXED;
+        const bool mixed = c->mode == TTP_MODE_MIXED, bf16 = dtype == TTP_DTYPE_BF16;
+        const uint64_t tiles = (n + norm_tile(c) - 1) / norm_tile(c);
         clear_hip_error();
-        if (mixed && dtype == TTP_DTYPE_BF16)
-            hipLaunchKernelGGL((ttp::accumulate_grad_kernel<uint16_t, uint16_t>), dim3(grid),
-                               dim3(ttp::kBlock), 0, c->stream, (uint16_t*)c->grad + t.offset,
-                               (const uint16_t*)dsrc, n, first);
-        else if (mixed)
-            hipLaunchKernelGGL((ttp::accumulate_grad_kernel<float, uint16_t>), dim3(grid),
-                               dim3(ttp::kBlock), 0, c->stream, (uint16_t*)c->grad + t.offset,
-                               (const float*)dsrc, n, first);
-        else if (dtype == TTP_DTYPE_BF16)
-            hipLaunchKernelGGL((ttp::accumulate_grad_kernel<uint16_t, float>), dim3(grid),
-                               dim3(ttp::kBlock), 0, c->stream, (float*)c->grad + t.offset,
-                               (const uint16_t*)dsrc, n, first);
-        else
-            hipLaunchKernelGGL((ttp::accumulate_grad_kernel<float, float>), dim3(grid),
-                               dim3(ttp::kBlock), 0, c->stream, (float*)c->grad + t.offset,
-                               (const float*)dsrc, n, first);
+        if (tiles < (1u << 24)) {
+            // one block per 16 KiB tile of the tensor's gradients (with_sums: their sums too)
+            const int32_t scaler_on = c->scaler.enabled ? 1 : 0;
+            const bool vec = ((uintptr_t)dsrc & 15u) == 0;
+            const dim3 grid((uint32_t)tiles), block(ttp::kBlock);
+            const DevState* st = c->st;
+            double* ts = c->acc_tiles + (uint64_t)c->host_tile_base[index] * ttp::kWaves;
+            uint32_t* pend = c->tsum_pending + index;
+#define TTP_ACC_TILES(S, G, V, SUMS)                                                             \
+    hipLaunchKernelGGL((ttp::accumulate_grad_tiles_kernel<S, G, V, SUMS>), grid, block, 0,       \
+                       c->stream, (G*)c->grad + t.offset, (const S*)dsrc, n, first, st, scaler_on, \
+                       ts, pend)
+#define TTP_ACC_SRC(S, G)                                   \
+    do {                                                    \
+        if (vec && with_sums) TTP_ACC_TILES(S, G, true, true);   \
+        else if (vec) TTP_ACC_TILES(S, G, true, false);          \
+        else if (with_sums) TTP_ACC_TILES(S, G, false, true);    \
+        else TTP_ACC_TILES(S, G, false, false);                  \
+    } while (0)
+            if (mixed && bf16)
+                TTP_ACC_SRC(uint16_t, uint16_t);
+            else if (mixed)
+                TTP_ACC_SRC(float, uint16_t);
+            else if (bf16)
+                TTP_ACC_SRC(uint16_t, float);
+            else
+                TTP_ACC_SRC(float, float);
+#undef TTP_ACC_SRC
+#undef TTP_ACC_TILES
+        } else {
+            // beyond a launch's 2^32 work-items at one tile per block: the grid-stride kernel
+            const uint32_t grid = elementwise_grid(c, n);
+            if (mixed && bf16)
+                hipLaunchKernelGGL((ttp::accumulate_grad_kernel<uint16_t, uint16_t>), dim3(grid),
+                                   dim3(ttp::kBlock), 0, c->stream, (uint16_t*)c->grad + t.offset,
+                                   (const uint16_t*)dsrc, n, first);
+            else if (mixed)
+                hipLaunchKernelGGL((ttp::accumulate_grad_kernel<float, uint16_t>), dim3(grid),
+                                   dim3(ttp::kBlock), 0, c->stream, (uint16_t*)c->grad + t.offset,
+                                   (const float*)dsrc, n, first);
+            else if (bf16)
+                hipLaunchKernelGGL((ttp::accumulate_grad_kernel<uint16_t, float>), dim3(grid),
+                                   dim3(ttp::kBlock), 0, c->stream, (float*)c->grad + t.offset,
+                                   (const uint16_t*)dsrc, n, first);
+            else
+                hipLaunchKernelGGL((ttp::accumulate_grad_kernel<float, float>), dim3(grid),
+                                   dim3(ttp::kBlock), 0, c->stream, (float*)c->grad + t.offset,
+                                   (const float*)dsrc, n, first);
+        }
         HIP_TRY(hipGetLastError());
         if (kind == TTP_HOST) HIP_TRY(hipStreamSynchronize(c->stream));
     }
+    // an empty tensor's sum is never read (no step updates it)
+    if (with_sums) c->acc_sums_used = true;
     set_grad_flag(c, index, true);
-    set_fresh(c, index, false);
+    set_fresh(c, index, with_sums);
     return TTP_OK;
 }
 
@@ -1747,21 +1858,8 @@ int ttp_grad_sumsq_tensors(ttp_ctx* c, const uint32_t* indices, uint32_t n) {
         return fail(TTP_ERR_RANGE, "a gradient-sum call covers " + std::to_string(w->n_tiles) +
                                        " tiles of 16 KiB; at most 2^24 - 1 (256 GiB of "
                                        "gradients) per call: split the bucket");
-    if (w->n_tiles > c->tile_sums_cap) {
-        if ((rc = no_capture(c, "a first gradient-sum call over this many tiles (allocates)")))
-            return rc;
-        HIP_TRY(hipStreamSynchronize(c->stream));  // queued calls may still use the old buffer
-        if (c->tile_sums) {
-            if (c->n_graphs)
-                c->retired.push_back(c->tile_sums);  // a captured call may write it on replay
-            else
-                HIP_TRY(hipFree(c->tile_sums));
-        }
-        c->tile_sums = nullptr;
-        c->tile_sums_cap = 0;
-        HIP_TRY(hipMalloc((void**)&c->tile_sums, (size_t)w->n_tiles * sizeof(double)));
-        c->tile_sums_cap = w->n_tiles;
-    }
+    if ((rc = ensure_tile_sums(c, w->n_tiles, "a first gradient-sum call over this many tiles")))
+        return rc;
     if (w->n_tiles) {
         // one norm-pass block per tile (each block's partial is its tile's sum), then one
         // block per tensor over its run of tiles
@@ -1779,7 +1877,8 @@ int ttp_grad_sumsq_tensors(ttp_ctx* c, const uint32_t* indices, uint32_t n) {
         HIP_TRY(hipGetLastError());
         clear_hip_error();
         hipLaunchKernelGGL(ttp::tensor_sums_kernel, dim3(w->n_tensors), dim3(ttp::kBlock), 0,
-                           c->stream, c->tile_sums, w->tile_start, w->tensor_ids, c->tsum);
+                           c->stream, c->tile_sums, w->tile_start, w->tensor_ids, c->tsum,
+                           c->tsum_pending);
         HIP_TRY(hipGetLastError());
     }
     for (uint32_t i : active) set_fresh(c, i, true);

@@ -20,6 +20,7 @@ ALL_TENSORS = 0xFFFFFFFF
 TENSOR_DECAY = 1
 HOST, DEVICE = 0, 1
 DTYPE_F32, DTYPE_BF16 = 0, 1
+ACCUM_SUMSQ = 0x100
 STEP_TENSOR_SUMS = 1
 STEP_DEFER_SCALE = 2
 KERNEL_NORM, KERNEL_UPDATE = 0, 1

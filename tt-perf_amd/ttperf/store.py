@@ -65,10 +65,12 @@ class Tensor:
     def zero_grad(self):
         self.grad = None
 
-    def accumulate_grad(self, value):
+    def accumulate_grad(self, value, sums=False):
         """py/engine.py:149-156 `_add_grad`: grad = value if grad is None else grad + value,
-        summed in fp32 and rounded once to the grad buffer's type (bf16 in MIXED mode)."""
-        self.store.accumulate_grad(self.index, value)
+        summed in fp32 and rounded once to the grad buffer's type (bf16 in MIXED mode).
+        sums=True also stores this tensor's gradient sum of squares for a tensor_sums step
+        (TTP_ACCUM_SUMSQ)."""
+        self.store.accumulate_grad(self.index, value, sums=sums)
 
     # ---- data ----------------------------------------------------------------------------
     def numpy(self):
@@ -465,10 +467,14 @@ class ParamStore:
         idx, n = self._index_array(indices)
         L.check(L.lib.ttp_zero_grad_subset(self._h, idx, n, 1 if set_to_none else 0))
 
-    def accumulate_grad(self, index, value):
+    def accumulate_grad(self, index, value, sums=False):
         """Add an incoming gradient (numpy float32 / uint16 bf16 bits, or a torch float32 /
-        bfloat16 tensor on the host or the GPU) into tensor `index`'s grad."""
+        bfloat16 tensor on the host or the GPU) into tensor `index`'s grad.  sums=True: the
+        same launch also stores the sum of squares of the tensor's resulting (unscaled)
+        gradients, as grad_sumsq_tensors([index]) would, bit for bit, so that a step with
+        tensor_sums=True needs no pass over them (TTP_ACCUM_SUMSQ)."""
         n = self.tensors[index].numel
+        flag = L.ACCUM_SUMSQ if sums else 0
         if _is_torch(value):
             import torch
             if value.dtype not in (torch.float32, torch.bfloat16):
@@ -481,15 +487,15 @@ class ParamStore:
                     raise ValueError(f"a captured accumulate needs a contiguous device tensor "
                                      f"of {n} elements, used in place")
                 L.check(L.lib.ttp_accumulate_grad(self._h, index, C.c_void_p(value.data_ptr()),
-                                                  n, dtype, L.DEVICE))
+                                                  n, dtype | flag, L.DEVICE))
                 return
             t = value.detach().contiguous()
             if t.numel() != n:
                 raise ValueError(f"expected {n} elements, got {t.numel()}")
             if t.is_cuda:
                 torch.cuda.current_stream(t.device).synchronize()
-            L.check(L.lib.ttp_accumulate_grad(self._h, index, C.c_void_p(t.data_ptr()), n, dtype,
-                                              L.DEVICE if t.is_cuda else L.HOST))
+            L.check(L.lib.ttp_accumulate_grad(self._h, index, C.c_void_p(t.data_ptr()), n,
+                                              dtype | flag, L.DEVICE if t.is_cuda else L.HOST))
             if t.is_cuda:
                 self.sync()  # `t` may be freed and reused by torch as soon as we return
             return
@@ -502,8 +508,8 @@ class ParamStore:
         a = np.ascontiguousarray(a).ravel()
         if a.size != n:
             raise ValueError(f"expected {n} elements, got {a.size}")
-        L.check(L.lib.ttp_accumulate_grad(self._h, index, a.ctypes.data_as(C.c_void_p), n, dtype,
-                                          L.HOST))
+        L.check(L.lib.ttp_accumulate_grad(self._h, index, a.ctypes.data_as(C.c_void_p), n,
+                                          dtype | flag, L.HOST))
 
     # ---- steps -----------------------------------------------------------------------------------
     @staticmethod
