@@ -335,12 +335,18 @@ int ttp_sgd_step_subset(ttp_ctx* ctx, const ttp_sgd_hparams* hp, const uint32_t*
  * held until the process ends) instead of the context's own buffer; a step whose norm pass
  * would write more (one per block: up to TTP_NORM_GRID, twice that above 256 MiB of
  * gradients) fails with TTP_ERR_RANGE.  Every
- * no-allocation step on one device shares that array: two that overlap in time on one
- * device (contexts on different streams) race, so order them (one stream, or events).
+ * no-allocation step on one device shares that array.  Eager calls are ordered by the
+ * library: a call on another stream than the previous call's waits for that call's work
+ * (an event made at ttp_create; no allocation).  Captured calls are not: graph launches of
+ * such steps on different streams of one device race unless the caller orders them.
  * Whatever the step would have to allocate is refused with TTP_ERR_STATE before any work is
  * queued: a tensor set, or (with loss scaling or after a capture) betas, not stepped before,
- * and in FP32 mode the m and v of the first Adam step.  Step once with ttp_adam_step[_subset]
- * first.  There is no report: ttp_scaler_get and ttp_get_step read the results. */
+ * and the m and v of the first Adam step of an FP32 store or of a MIXED store in the SGD
+ * layout.  Step once with ttp_adam_step[_subset] first.  In host-count mode (no loss
+ * scaling, never captured) the step needs no bias-correction table and builds none: a later
+ * capture of Adam steps with those betas needs one allocating step with them first (the
+ * capture refuses them otherwise).  There is no report: ttp_scaler_get and ttp_get_step
+ * read the results. */
 int ttp_adam_step_noalloc(ttp_ctx* ctx, const ttp_adam_hparams* hp, const uint32_t* indices,
                           uint32_t n_indices);
 /* Global L2 norm of the gradients that exist, unscaled by the current loss scale when

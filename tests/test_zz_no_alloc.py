@@ -205,3 +205,103 @@ def test_noalloc_step_refuses_what_it_would_have_to_allocate():
     big.adam_step(**HP)
     refused(big, L.ERR_RANGE, ["10240 partials", "8192"])
     big.close()
+
+
+def test_captured_noalloc_step_replays_like_the_eager_step():
+    """The entry point's first callers: code under HIP graph capture.  A no-allocation step
+    with loss scaling and clipping over a store just above the 256 MiB bound (so the
+    two-launch norm pass writes its ~2850 partials into the scratch array) is captured, then
+    replayed four times with new gradients, one holding +inf (skipped, scale halved); each
+    replay is bit-compared with an eager ttp_adam_step on a twin store, with eager work of the
+    program (gradient uploads and synchronisations) between the replays.  Around an eager
+    no-allocation call the device's free memory does not change."""
+    from ttperf import _lib as L
+    torch = torch_mod()
+    gen = torch.Generator(device="cuda").manual_seed(180)
+    shapes = [(50257, 768), (8192, 8192), (7000, 5000), (768,), (3,)]  # 281 MB of bf16 grads
+    decay = [True, True, True, False, False]
+    A, A2, refA = _pair_of_twins(shapes, decay, 181)
+    del refA
+    A2.set_stream(None)  # the store's own stream: capturable
+    for _ in range(2):  # set-up with the allocating entry point: bias and work tables
+        _same_grads_no_oracle(A, A2, gen)
+        A.adam_step(**HP)
+        A2.adam_step(**HP)
+    torch.cuda.synchronize()
+    _identical(A, A2, "set-up")
+    # an eager no-allocation call allocates nothing on the device
+    _same_grads_no_oracle(A, A2, gen)
+    A.adam_step(**HP)
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    assert _noalloc(A2) == L.OK, L.lib.ttp_last_error()
+    A2.sync()
+    free1, _ = torch.cuda.mem_get_info()
+    assert free1 == free0, (free0, free1)
+    _identical(A, A2, "eager no-allocation step")
+    A2.begin_capture()
+    assert _noalloc(A2) == L.OK, L.lib.ttp_last_error()
+    graph = A2.end_capture()
+    for k in range(4):
+        inf_at = int(A.offsets[1]) + 4321 if k == 2 else None
+        host = device_grads(A, gen, 1e-3, scale=A.scaler_state()[0], inf_at=inf_at)
+        A2.upload(L.BUF_GRAD, L.ALL_TENSORS, host)
+        A2.sync()
+        r = A.adam_step(report=True, **HP)
+        graph.replay()
+        A2.sync()
+        assert r["skipped"] == (k == 2)
+        _identical(A, A2, f"replay {k}")
+    graph.close()
+    A.close()
+    A2.close()
+
+
+def test_noalloc_steps_of_two_stores_on_two_streams():
+    """Two stores on two torch streams take eager no-allocation steps in turn, without any
+    synchronisation between the calls: the library orders each call after the previous one
+    on the shared scratch array, so each store ends bit-identical to its allocating twin."""
+    from ttperf import _lib as L
+    from ttperf import configs
+    torch = torch_mod()
+    gen = torch.Generator(device="cuda").manual_seed(190)
+    _, shapes, decay, _ = configs.table("nanogpt_char")
+    A, A2, _ = _pair_of_twins(shapes, decay, 191)
+    B, B2, _ = _pair_of_twins(shapes, decay, 192)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    A2.set_stream(s1)
+    B2.set_stream(s2)
+    for x, x2 in ((A, A2), (B, B2)):
+        _same_grads_no_oracle(x, x2, gen)
+        x.adam_step(**HP)
+        x2.adam_step(**HP)
+    torch.cuda.synchronize()
+    for k in range(6):
+        for x, x2 in ((A, A2), (B, B2)):
+            _same_grads_no_oracle(x, x2, gen)
+        torch.cuda.synchronize()
+        A.adam_step(**HP)
+        B.adam_step(**HP)
+        assert _noalloc(A2) == L.OK, L.lib.ttp_last_error()
+        assert _noalloc(B2) == L.OK, L.lib.ttp_last_error()
+    torch.cuda.synchronize()
+    _identical(A, A2, "store on stream 1")
+    _identical(B, B2, "store on stream 2")
+    for s in (A, A2, B, B2):
+        s.close()
+
+
+def test_noalloc_step_refuses_to_convert_the_sgd_layout():
+    """A mixed store in the SGD layout has no m and v until its first Adam step converts it;
+    the no-allocation step refuses that step, with the store unchanged."""
+    from ttperf import _lib as L
+    torch = torch_mod()
+    gen = torch.Generator(device="cuda").manual_seed(195)
+    store, _ = make_pair([(300, 7), (64,)], [True, False], O.MODE_MIXED, seed=196, layout="sgd")
+    device_grads(store, gen, 1e-3)
+    master = store.download(L.BUF_MASTER).tobytes()
+    assert _noalloc(store) == L.ERR_STATE
+    msg = L.lib.ttp_last_error().decode()
+    assert "SGD layout" in msg and "allocates m and v" in msg, msg
+    assert store.sgd_layout and store.download(L.BUF_MASTER).tobytes() == master
+    store.close()

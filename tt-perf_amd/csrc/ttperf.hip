@@ -119,23 +119,28 @@ static __device__ __align__(256) double scratch[kNoAllocPartials];
 
 namespace {
 
+// Per device: its copy of `scratch`, and the stream and an event of the last eager
+// no-allocation step, so that one on another stream (another context) waits for it instead
+// of overwriting partials it has not consumed yet.  Both are made at ttp_create, so a step
+// allocates nothing.
+struct ScratchDev {
+    double* ptr = nullptr;
+    hipEvent_t done = nullptr;      // recorded after each eager no-allocation step
+    hipStream_t last = nullptr;     // the stream it was recorded on
+    bool used = false;
+};
 std::mutex g_scratch_mu;
-std::map<int, double*> g_scratch;  // device -> its copy of `scratch`
+std::map<int, ScratchDev> g_scratch;  // device -> its scratch array and ordering
 
 // Called with `device` current: finds this device's copy of the scratch array once.
 int ensure_scratch(int device) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (g_scratch.count(device)) return TTP_OK;
-    double* ptr = nullptr;
-    HIP_TRY(hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch)));
-    g_scratch[device] = ptr;
+    ScratchDev d;
+    HIP_TRY(hipGetSymbolAddress((void**)&d.ptr, HIP_SYMBOL(scratch)));
+    HIP_TRY(hipEventCreateWithFlags(&d.done, hipEventDisableTiming));
+    g_scratch[device] = d;
     return TTP_OK;
-}
-
-double* scratch_ptr(int device) {
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    auto it = g_scratch.find(device);
-    return it == g_scratch.end() ? nullptr : it->second;
 }
 
 }  // namespace
@@ -1813,9 +1818,24 @@ int ttp_adam_step_noalloc(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
     int rc = check_ctx(c);
     if (rc) return rc;
     if (n && !indices) return fail(TTP_ERR_INVALID, "null index list");
-    double* sp = scratch_ptr(c->device);
-    if (!sp) return fail(TTP_ERR_STATE, "no scratch array found for this device");
-    return adam_step_impl(c, hp, indices, n, nullptr, sp);
+    if ((rc = set_dev(c))) return rc;
+    // The device's scratch array is shared by every context: an eager step on another stream
+    // than the last one's first waits for that step's event (host calls on one device are
+    // serialised by the lock).  A captured step is ordered by its caller at each launch.
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    auto it = g_scratch.find(c->device);
+    if (it == g_scratch.end() || !it->second.ptr)
+        return fail(TTP_ERR_STATE, "no scratch array found for this device");
+    ScratchDev& d = it->second;
+    if (!c->capturing && d.used && d.last != c->stream)
+        HIP_TRY(hipStreamWaitEvent(c->stream, d.done, 0));
+    rc = adam_step_impl(c, hp, indices, n, nullptr, d.ptr);
+    if (rc == TTP_OK && !c->capturing) {
+        HIP_TRY(hipEventRecord(d.done, c->stream));
+        d.last = c->stream;
+        d.used = true;
+    }
+    return rc;
 }
 
 int ttp_sgd_step(ttp_ctx* c, const ttp_sgd_hparams* hp, ttp_step_report* report) {
