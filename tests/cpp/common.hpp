@@ -84,12 +84,15 @@ inline void assert_all_close(const std::vector<float>& got, float expected, floa
         }
 }
 
+// the verdict is flushed at once: what the runtimes do at exit cannot lose it
 inline int finish(const char* name) {
     if (g_failures) {
         std::printf("%s: %d check(s) failed\n", name, g_failures);
+        std::fflush(stdout);
         return 1;
     }
     std::printf("%s: PASS\n", name);
+    std::fflush(stdout);
     return 0;
 }
 

@@ -11,8 +11,6 @@ from conftest import REPO, f32_ulp_diff
 
 sys.path.insert(0, os.path.join(REPO, "tt-perf_amd"))
 
-LONG = os.environ.get("TTP_LONG_TESTS", "0") == "1"
-
 
 def torch_mod():
     import torch
@@ -61,9 +59,13 @@ def pad_mask(store):
     return m
 
 
-def device_grads(store, gen, std, scale=1.0, heavy_frac=0.0, heavy_std=1.0, inf_at=None):
+def device_grads(store, gen, std, scale=1.0, heavy_frac=0.0, heavy_std=1.0, inf_at=None,
+                 into=None):
     """Seeded N(0, std) * scale grads on the device (bf16 in MIXED), written into the store;
-    returns the host copy (uint16 bits or float32) for the oracle."""
+    returns the host copy (uint16 bits or float32) for the oracle.  into: an oracle's grad
+    array, which receives the copy directly (no host temporary of the store's size, which at
+    billions of elements costs more than the step under test); its first store.total elements
+    are returned."""
     torch = torch_mod()
     g = torch.randn(store.total, generator=gen, device="cuda", dtype=torch.float32) * std
     if heavy_frac:
@@ -77,6 +79,12 @@ def device_grads(store, gen, std, scale=1.0, heavy_frac=0.0, heavy_std=1.0, inf_
     if store.mode == L.MODE_MIXED:
         g = g.to(torch.bfloat16)
     store.upload(L.BUF_GRAD, L.ALL_TENSORS, g)
+    if into is not None:
+        bits = store.mode == L.MODE_MIXED
+        assert into.dtype == (np.uint16 if bits else np.float32) and len(into) >= store.total
+        dst = torch.from_numpy(into.view(np.int16) if bits else into)[:store.total]
+        dst.copy_(g.view(torch.int16) if bits else g)
+        return into[:store.total]
     host = g.cpu()
     if store.mode == L.MODE_MIXED:
         return host.view(torch.int16).numpy().view(np.uint16)

@@ -64,8 +64,16 @@ def test_cpp_dropin_host_sanitizers(name):
     exe = os.path.join(CPP, "build-asan", name)
     if not os.access(exe, os.X_OK):
         pytest.skip("sanitizer build absent (make -C tt-perf_amd asan && make -C tests/cpp asan)")
-    # leak checking is off: the HIP runtime keeps allocations until exit by design
-    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0",
+    # Leak checking is off: the HIP runtime keeps allocations until exit by design.  The
+    # quarantine (freed memory held back to catch use after free) is made larger than these
+    # programs ever free, so it never recycles: at exit the HIP runtime's teardown frees its
+    # host objects through ASan after the device runtime is gone, and a recycle at that point
+    # returns a quarantined device chunk to ASan's device allocator, which aborts ("CHECK
+    # failed: sanitizer_allocator_device.h ... dev_runtime_unloaded_") after the program's own
+    # checks have passed.  Whether a program hits it depended on how full the quarantine
+    # happened to be at exit.
+    env = dict(os.environ,
+               ASAN_OPTIONS="detect_leaks=0:abort_on_error=0:quarantine_size_mb=16384",
                UBSAN_OPTIONS="print_stacktrace=1")
     p = _run(exe, env)
     assert p.returncode == 0, f"{name} (ASan/UBSan) exited {p.returncode}:\n{p.stdout[-3000:]}\n{p.stderr[-4000:]}"

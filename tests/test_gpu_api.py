@@ -190,8 +190,7 @@ def test_sgd_family_parity(case, kind):
     gen = torch.Generator(device="cuda").manual_seed(41)
     hp = SGD_CASES[case]
     for step in range(3):
-        host = device_grads(store, gen, 1e-1 if hp.get("max_grad_norm") else 1e-3)
-        ref.grad[:] = host
+        host = device_grads(store, gen, 1e-1 if hp.get("max_grad_norm") else 1e-3, into=ref.grad)
         for i in range(ref.n):
             ref.set_has_grad(i, True)
         r = store.sgd_step(report=True, **hp)
@@ -217,8 +216,7 @@ def test_subset_step_touches_only_listed_tensors():
     decay = [True, False, True, False, False, True]
     store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=50)
     gen = torch.Generator(device="cuda").manual_seed(51)
-    host = device_grads(store, gen, 1e-2)
-    ref.grad[:] = host
+    host = device_grads(store, gen, 1e-2, into=ref.grad)
     listed = [0, 3, 5]
     for i in range(ref.n):
         ref.set_has_grad(i, i in listed)  # the oracle sees only the listed tensors
@@ -239,8 +237,7 @@ def test_none_grad_tensors_untouched_and_out_of_the_norm():
     shapes = [(1000,), (64, 64), (77,), (3, 3)]
     store, ref = make_pair(shapes, [False, True, False, True], O.MODE_FP32, seed=52)
     gen = torch.Generator(device="cuda").manual_seed(53)
-    host = device_grads(store, gen, 1.0)
-    ref.grad[:] = host
+    host = device_grads(store, gen, 1.0, into=ref.grad)
     for i in range(ref.n):
         ref.set_has_grad(i, True)
     store.tensors[1].grad = None
@@ -270,8 +267,7 @@ def test_scaler_growth_and_backoff_sequence():
     expect = [(2048.0, 0, 1, 0), (2048.0, 1, 2, 0), (1024.0, 0, 2, 1), (1024.0, 1, 3, 0)]
     for k, (scale, tracker, t, skipped) in enumerate(expect):
         host = device_grads(store, gen, 1e-3, scale=ref.scale,
-                            inf_at=store.offsets[1] + 7 if k == 2 else None)
-        ref.grad[:] = host
+                            inf_at=store.offsets[1] + 7 if k == 2 else None, into=ref.grad)
         for i in range(ref.n):
             ref.set_has_grad(i, True)
         r = store.adam_step(report=True, **hp)
@@ -296,8 +292,7 @@ def test_ragged_sizes_and_empty_tensors():
         gen = torch.Generator(device="cuda").manual_seed(57)
         hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=0.1)
         for _ in range(3):
-            host = device_grads(store, gen, 1e-2, scale=ref.scale)
-            ref.grad[:] = host
+            host = device_grads(store, gen, 1e-2, scale=ref.scale, into=ref.grad)
             for i in range(ref.n):
                 ref.set_has_grad(i, True)
             r = store.adam_step(report=True, **hp)
@@ -381,8 +376,7 @@ def test_cfg5_gpt2_xl_fp32_adamw_then_sgd_momentum():
     steps = 10
     hp = dict(lr=1.5e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
     for step in range(steps):
-        host = device_grads(store, gen, 1e-3, heavy_frac=0.01, heavy_std=1.0)
-        ref.grad[:] = host
+        host = device_grads(store, gen, 1e-3, heavy_frac=0.01, heavy_std=1.0, into=ref.grad)
         del host
         for i in range(ref.n):
             ref.set_has_grad(i, True)
@@ -394,8 +388,7 @@ def test_cfg5_gpt2_xl_fp32_adamw_then_sgd_momentum():
     compare_state(store, ref, which=("master", "exp_avg", "exp_avg_sq"), max_ulp=2)
     sgd = dict(lr=1e-3, momentum=0.9, max_grad_norm=1.0)
     for step in range(steps):
-        host = device_grads(store, gen, 1e-3, heavy_frac=0.01, heavy_std=1.0)
-        ref.grad[:] = host
+        host = device_grads(store, gen, 1e-3, heavy_frac=0.01, heavy_std=1.0, into=ref.grad)
         del host
         r = store.sgd_step(report=True, **sgd)
         e = ref.sgd_step(**sgd)
@@ -445,8 +438,7 @@ def test_update_forms_on_both_sides_of_the_cached_gradient_bound(mode):
     for label, subset in zip(("whole store", "lane-form subset", "cached-gradient subset"),
                              subsets):
         for step in range(2):
-            host = device_grads(store, gen, 1e-3)
-            ref.grad[:] = host
+            host = device_grads(store, gen, 1e-3, into=ref.grad)
             for i in range(ref.n):
                 ref.set_has_grad(i, subset is None or i in subset)
             r = store.sgd_step(report=True, indices=subset, **sgd)
@@ -454,8 +446,7 @@ def test_update_forms_on_both_sides_of_the_cached_gradient_bound(mode):
             assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
             print(f"{mode} {label} sgd-m step {step}: norm {r['grad_norm']:.6f}", flush=True)
         compare_state(store, ref, which=slots, max_ulp=2)
-        host = device_grads(store, gen, 1e-3)
-        ref.grad[:] = host
+        host = device_grads(store, gen, 1e-3, into=ref.grad)
         for i in range(ref.n):
             ref.set_has_grad(i, subset is None or i in subset)
         r = store.sgd_step(report=True, indices=subset, **plain)
@@ -464,8 +455,7 @@ def test_update_forms_on_both_sides_of_the_cached_gradient_bound(mode):
         print(f"{mode} {label} sgd step: norm {r['grad_norm']:.6f}", flush=True)
         compare_state(store, ref, which=slots, max_ulp=2)
         for step in range(2):
-            host = device_grads(store, gen, 1e-3)
-            ref.grad[:] = host
+            host = device_grads(store, gen, 1e-3, into=ref.grad)
             for i in range(ref.n):
                 ref.set_has_grad(i, subset is None or i in subset)
             r = store.adam_step(report=True, indices=subset, **adam)
@@ -509,8 +499,7 @@ def test_lane_form_update_split_into_several_launches(mode, monkeypatch):
         legs.append(("cached-gradient subset", [0, 3, 4]))
     for label, sub in legs:
         for name, hp in (("sgd-m", sgd), ("sgd", plain), ("adamw", adam)):
-            host = device_grads(store, gen, 1e-3)
-            ref.grad[:] = host
+            host = device_grads(store, gen, 1e-3, into=ref.grad)
             for i in range(ref.n):
                 ref.set_has_grad(i, sub is None or i in sub)
             sgd_like = name.startswith("sgd")
@@ -530,8 +519,9 @@ def test_lane_form_with_many_small_tensors(mode):
     small ones of 1..200 elements (most chunks hold less than one lane-form piece, many
     blocks have nothing to do): AdamW with loss scaling and clipping, then SGD with Nesterov
     momentum, then plain SGD with weight decay, against the oracle; the second Adam step on a
-    subset of every third tensor.  "mixed_sgd": a store created in the SGD layout, which the
-    first AdamW step converts."""
+    subset of every third tensor.  "mixed_sgd": a store created in the SGD layout takes the
+    SGD legs first (the layout's own four- and two-element forms over the small tensors), and
+    the first AdamW step then converts it."""
     torch = torch_mod()
     rng = np.random.default_rng(87)
     big = (1 << 27) + 3 if mode != "fp32" else (1 << 26) + 5
@@ -539,43 +529,52 @@ def test_lane_form_with_many_small_tensors(mode):
     shapes = [(big,)] + [(n,) for n in small]
     decay = [True] + [bool(x) for x in rng.integers(0, 2, size=len(small))]
     store, ref = make_pair(shapes, decay, O.MODE_MIXED if mode != "fp32" else O.MODE_FP32,
-                           seed=88)
+                           seed=88, layout="sgd" if mode == "mixed_sgd" else "default")
     store.configure_scaler(True, init_scale=4096.0)
     ref.configure_scaler(True, 4096.0)
     gen = torch.Generator(device="cuda").manual_seed(89)
-    adam = dict(lr=1e-3, betas=(0.9, 0.99), eps=1e-8, weight_decay=0.05, max_grad_norm=0.5)
-    subset = list(range(0, len(shapes), 3))
-    for step, sub in enumerate((None, subset)):
-        host = device_grads(store, gen, 1e-3, scale=ref.scale)
-        ref.grad[:] = host
-        for i in range(ref.n):
-            ref.set_has_grad(i, sub is None or i in sub)
-        r = store.adam_step(report=True, indices=sub, **adam)
-        e = ref.adam_step(**adam)
-        assert r["skipped"] == e["skipped"] and r["step"] == e["step"]
+    param = ("param",) if mode != "fp32" else ()
+
+    def adam_legs():
+        adam = dict(lr=1e-3, betas=(0.9, 0.99), eps=1e-8, weight_decay=0.05, max_grad_norm=0.5)
+        subset = list(range(0, len(shapes), 3))
+        for step, sub in enumerate((None, subset)):
+            device_grads(store, gen, 1e-3, scale=ref.scale, into=ref.grad)
+            for i in range(ref.n):
+                ref.set_has_grad(i, sub is None or i in sub)
+            r = store.adam_step(report=True, indices=sub, **adam)
+            e = ref.adam_step(**adam)
+            assert r["skipped"] == e["skipped"] and r["step"] == e["step"]
+            assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
+            print(f"{mode} adamw step {step}: norm {r['grad_norm']:.6f}", flush=True)
+        compare_state(store, ref, which=("master", "exp_avg", "exp_avg_sq") + param, max_ulp=2)
+
+    def sgd_legs():
+        sgd = dict(lr=1e-2, momentum=0.9, nesterov=True, max_grad_norm=0.5)
+        for step in range(2):
+            device_grads(store, gen, 1e-3, scale=ref.scale, into=ref.grad)
+            for i in range(ref.n):
+                ref.set_has_grad(i, True)
+            r = store.sgd_step(report=True, **sgd)
+            e = ref.sgd_step(**sgd)
+            assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
+        compare_state(store, ref, which=("master", "momentum") + param, max_ulp=2)
+        plain = dict(lr=1e-2, weight_decay=0.01, max_grad_norm=0.5)
+        device_grads(store, gen, 1e-3, scale=ref.scale, into=ref.grad)
+        r = store.sgd_step(report=True, **plain)
+        e = ref.sgd_step(**plain)
+        assert r["skipped"] == e["skipped"]
         assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
-        print(f"{mode} adamw step {step}: norm {r['grad_norm']:.6f}", flush=True)
-    slots = ("master", "exp_avg", "exp_avg_sq") + (("param",) if mode != "fp32" else ())
-    compare_state(store, ref, which=slots, max_ulp=2)
-    sgd = dict(lr=1e-2, momentum=0.9, nesterov=True, max_grad_norm=0.5)
-    for step in range(2):
-        host = device_grads(store, gen, 1e-3, scale=ref.scale)
-        ref.grad[:] = host
-        for i in range(ref.n):
-            ref.set_has_grad(i, True)
-        r = store.sgd_step(report=True, **sgd)
-        e = ref.sgd_step(**sgd)
-        assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
-    compare_state(store, ref, which=("master", "momentum") + (("param",) if mode != "fp32" else ()),
-                  max_ulp=2)
-    plain = dict(lr=1e-2, weight_decay=0.01, max_grad_norm=0.5)
-    host = device_grads(store, gen, 1e-3, scale=ref.scale)
-    ref.grad[:] = host
-    r = store.sgd_step(report=True, **plain)
-    e = ref.sgd_step(**plain)
-    assert r["skipped"] == e["skipped"] and abs(r["grad_norm"] - e["grad_norm"]) <= 1e-5 * e["grad_norm"]
-    compare_state(store, ref, which=("master",) + (("param",) if mode != "fp32" else ()),
-                  max_ulp=2)
+        compare_state(store, ref, which=("master",) + param, max_ulp=2)
+
+    if mode == "mixed_sgd":
+        sgd_legs()
+        assert store.sgd_layout
+        adam_legs()
+        assert not store.sgd_layout
+    else:
+        adam_legs()
+        sgd_legs()
     store.close()
 
 
@@ -593,8 +592,7 @@ def test_zero1_shard_step_matches_oracle():
     gen = torch.Generator(device="cuda").manual_seed(91)
     hp = dict(lr=6e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
     for step in range(3):
-        host = device_grads(store, gen, 1e-3, scale=ref.scale)
-        ref.grad[:] = host
+        host = device_grads(store, gen, 1e-3, scale=ref.scale, into=ref.grad)
         for i in range(ref.n):
             ref.set_has_grad(i, True)
         r = store.adam_step(report=True, **hp)

@@ -23,7 +23,8 @@ def _table(name):
 
 
 def _set_ref_grads(ref, host):
-    ref.grad[:] = host
+    """host: device_grads' copy, taken straight into ref.grad (into=ref.grad)."""
+    assert np.shares_memory(host, ref.grad)
     for i in range(ref.n):
         ref.set_has_grad(i, True)
 
@@ -47,7 +48,7 @@ def test_cfg1_mlp_fp32_adam_bit_exact():
     gen = torch.Generator(device="cuda").manual_seed(2)
     hp = dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8)
     for step in range(100):
-        host = device_grads(store, gen, 1e-2)
+        host = device_grads(store, gen, 1e-2, into=ref.grad)
         _set_ref_grads(ref, host)
         r = store.adam_step(report=(step % 25 == 24), **hp)
         e = ref.adam_step(**hp)
@@ -67,7 +68,7 @@ def test_cfg2_nanogpt_mixed_adamw_clip():
     hp = dict(lr=6e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
     steps = 50
     for step in range(steps):
-        host = device_grads(store, gen, 1e-3)
+        host = device_grads(store, gen, 1e-3, into=ref.grad)
         _set_ref_grads(ref, host)
         r = store.adam_step(report=True, **hp)
         e = ref.adam_step(**hp)
@@ -99,7 +100,7 @@ def test_cfg3_gpt2_small_scaler_inf_skip():
         if step % 50 == 0:
             t = int(rng.integers(0, len(shapes)))
             inf_at = store.offsets[t] + int(rng.integers(0, store.tensors[t].numel))
-        host = device_grads(store, gen, 1e-3, scale=scale, inf_at=inf_at)
+        host = device_grads(store, gen, 1e-3, scale=scale, inf_at=inf_at, into=ref.grad)
         _set_ref_grads(ref, host)
         r = store.adam_step(report=True, **hp)
         e = ref.adam_step(**hp)
@@ -137,7 +138,7 @@ def test_cfg4_gpt2_large_scaler_clip_inf_skip():
         if step in inf_steps:
             t = int(rng.integers(0, len(shapes)))
             inf_at = store.offsets[t] + int(rng.integers(0, store.tensors[t].numel))
-        host = device_grads(store, gen, 1e-3, scale=ref.scale, inf_at=inf_at)
+        host = device_grads(store, gen, 1e-3, scale=ref.scale, inf_at=inf_at, into=ref.grad)
         _set_ref_grads(ref, host)
         r = store.adam_step(report=True, **hp)
         e = ref.adam_step(**hp)

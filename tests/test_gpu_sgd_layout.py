@@ -50,7 +50,7 @@ def test_gpt2_124m_plain_and_momentum_sgd_match_the_oracle():
     plain = dict(lr=1e-2, max_grad_norm=1.0)
     for step in range(6):
         inf_at = store.offsets[40] + 17 if step == 3 else None
-        ref.grad[:] = device_grads(store, gen, 1e-3, scale=ref.scale, inf_at=inf_at)
+        device_grads(store, gen, 1e-3, scale=ref.scale, inf_at=inf_at, into=ref.grad)
         _set_all(ref)
         r = store.sgd_step(report=True, **plain)
         e = ref.sgd_step(**plain)
@@ -60,7 +60,7 @@ def test_gpt2_124m_plain_and_momentum_sgd_match_the_oracle():
         assert e["skipped"] == (step == 3)
     compare_state(store, ref, which=("master", "param"), max_ulp=2)
     block = list(range(2 + 12 * 5, 2 + 12 * 6))  # h.5's tensors
-    ref.grad[:] = device_grads(store, gen, 1e-3, scale=ref.scale)
+    device_grads(store, gen, 1e-3, scale=ref.scale, into=ref.grad)
     _set_all(ref, block)
     r = store.sgd_step(report=True, indices=block, lr=0.05)
     e = ref.sgd_step(lr=0.05)
@@ -68,7 +68,7 @@ def test_gpt2_124m_plain_and_momentum_sgd_match_the_oracle():
     compare_state(store, ref, which=("master", "param"), max_ulp=2)
     mom = dict(lr=1e-2, momentum=0.9, max_grad_norm=1.0)
     for step in range(3):
-        ref.grad[:] = device_grads(store, gen, 1e-3, scale=ref.scale)
+        device_grads(store, gen, 1e-3, scale=ref.scale, into=ref.grad)
         _set_all(ref)
         r = store.sgd_step(report=True, **mom)
         e = ref.sgd_step(**mom)
@@ -90,7 +90,7 @@ def test_gpt2_774m_sgd_layout_matches_the_oracle():
     legs = [dict(lr=1e-2, max_grad_norm=1.0)] * 2 + \
         [dict(lr=1e-2, momentum=0.9, dampening=0.1, max_grad_norm=1.0)] * 2
     for k, hp in enumerate(legs):
-        ref.grad[:] = device_grads(store, gen, 1e-3)
+        device_grads(store, gen, 1e-3, into=ref.grad)
         _set_all(ref)
         r = store.sgd_step(report=True, **hp)
         e = ref.sgd_step(**hp)
@@ -111,7 +111,7 @@ def test_sgd_layout_matches_raw_device_memory():
     store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=320, layout="sgd")
     gen = torch.Generator(device="cuda").manual_seed(321)
     for _ in range(2):
-        ref.grad[:] = device_grads(store, gen, 1e-2)
+        device_grads(store, gen, 1e-2, into=ref.grad)
         _set_all(ref)
         store.sgd_step(lr=0.1, momentum=0.5)
         ref.sgd_step(lr=0.1, momentum=0.5)
@@ -146,15 +146,15 @@ def test_captured_sgd_step_replays_between_eager_steps():
     ref.configure_scaler(True, 256.0, growth_interval=2)
     gen = torch.Generator(device="cuda").manual_seed(331)
     hp = dict(lr=0.02, max_grad_norm=0.5)
-    ref.grad[:] = device_grads(store, gen, 1e-2, scale=ref.scale)
+    device_grads(store, gen, 1e-2, scale=ref.scale, into=ref.grad)
     _set_all(ref)
     _check(store.sgd_step(report=True, **hp), ref.sgd_step(**hp), True)  # builds the tables
     store.begin_capture()
     store.sgd_step(**hp)
     graph = store.end_capture()
     for k in range(3):
-        ref.grad[:] = device_grads(store, gen, 1e-2, scale=ref.scale,
-                                   inf_at=store.offsets[2] + 9 if k == 1 else None)
+        device_grads(store, gen, 1e-2, scale=ref.scale,
+                     inf_at=store.offsets[2] + 9 if k == 1 else None, into=ref.grad)
         _set_all(ref)
         graph.replay()
         e = ref.sgd_step(**hp)
@@ -162,7 +162,7 @@ def test_captured_sgd_step_replays_between_eager_steps():
         assert store.step_count == e["step"]
         assert store.scaler_state() == (np.float32(e["scale"]), e["growth_tracker"])
         compare_state(store, ref, which=("master", "param"), max_ulp=2)
-        ref.grad[:] = device_grads(store, gen, 1e-2, scale=ref.scale)
+        device_grads(store, gen, 1e-2, scale=ref.scale, into=ref.grad)
         _set_all(ref)
         _check(store.sgd_step(report=True, lr=0.01), ref.sgd_step(lr=0.01), True)
         compare_state(store, ref, which=("master", "param"), max_ulp=2)
@@ -172,7 +172,7 @@ def test_captured_sgd_step_replays_between_eager_steps():
     assert e.value.code == L.ERR_STATE and store.sgd_layout
     graph.close()
     adam = dict(lr=1e-3, betas=(0.9, 0.95), weight_decay=0.1)
-    ref.grad[:] = device_grads(store, gen, 1e-2, scale=ref.scale)
+    device_grads(store, gen, 1e-2, scale=ref.scale, into=ref.grad)
     _set_all(ref)
     _check(store.adam_step(report=True, **adam), ref.adam_step(**adam), True)
     assert not store.sgd_layout
