@@ -463,6 +463,61 @@ def test_accumulate_grad_host_and_device_sources(mode):
     compare_state(store, ref, max_ulp=2)
 
 
+# ragged sizes: empty, one vector or less, partial last vectors, several tiles with a partial
+# last tile (8192 bf16 / 4096 fp32 elements per tile), and an exact number of tiles
+BACKWARD_SHAPES = [(300, 7), (64,), (129, 33), (5,), (2048,), (1, 2049), (4097,), (96, 64),
+                   (0,), (40000,), (3,), (8192, 3)]
+
+
+@pytest.mark.parametrize("mode", [O.MODE_MIXED, O.MODE_FP32])
+def test_accumulates_in_backward_order_leave_other_tensors_untouched(mode):
+    """A backward delivers gradients in reverse tensor order, so the tensor after each one
+    already holds its gradient when that one's accumulate runs.  Assigns, then adds with and
+    without sums, from host and device memory in both source types (one device source at an
+    odd address), in that order; after every call the whole gradient buffer, padding
+    included, equals the oracle's bit for bit.  A kernel that wrote past a tensor's end (a
+    last tile taken whole) fails here at the first call; in forward order the next tensor's
+    own assign would overwrite the damage."""
+    torch = torch_mod()
+    from ttperf import _lib as L
+    decay = [len(sh) == 2 for sh in BACKWARD_SHAPES]
+    store, ref = make_pair(BACKWARD_SHAPES, decay, mode, seed=150)
+    gen = torch.Generator(device="cuda").manual_seed(151)
+    store.zero_grad(set_to_none=True)
+    ref.zero_grad(set_to_none=True)
+    kinds = ["dev_bf16", "host_f32", "dev_f32_odd", "host_bf16", "dev_f32"]
+    calls = 0
+    for rnd, sums in enumerate((False, False, True)):  # assign, add, add with sums
+        for i in reversed(range(len(BACKWARD_SHAPES))):
+            numel = store.tensors[i].numel
+            kind = kinds[(i + rnd) % len(kinds)]
+            x = torch.randn(numel, generator=gen, device="cuda") * 1e-2
+            if kind.endswith("bf16"):
+                x = x.to(torch.bfloat16)
+                host = x.cpu().view(torch.int16).numpy().view(np.uint16)
+            else:
+                host = x.cpu().numpy()
+            if kind == "dev_f32_odd":
+                buf = torch.zeros(numel + 1, device="cuda")
+                buf[1:] = x
+                src = buf[1:]
+                assert numel == 0 or src.data_ptr() % 16
+            elif kind.startswith("host"):
+                src = host
+            else:
+                src = x
+            store.accumulate_grad(i, src, sums=sums)
+            ref.accumulate_grad(i, host)
+            calls += 1
+            got = store.download(L.BUF_GRAD)
+            bad = np.nonzero(got.view(np.uint8) != ref.grad[:store.total].view(np.uint8))[0]
+            assert bad.size == 0, (f"call {calls} (tensor {i}, {kind}, round {rnd}): bytes "
+                                   f"{bad[:4].tolist()}.. of the gradient buffer differ "
+                                   f"(tensor offsets {list(store.offsets)})")
+    assert calls == 3 * len(BACKWARD_SHAPES)
+    store.close()
+
+
 def test_closing_other_stores_during_capture_is_deferred():
     """A store (or graph) closed while another store is capturing would free device memory on
     the capturing thread, which invalidates the capture: the close waits for the capture to

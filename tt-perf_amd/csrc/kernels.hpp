@@ -1047,7 +1047,12 @@ __global__ __launch_bounds__(kBlock) void accumulate_grad_tiles_kernel(
     constexpr uint32_t kTile = norm_tile_elems<GradT>();
     const float inv = (kSums && scaler_on) ? (float)(1.0 / (double)st->scale) : 1.0f;
     const uint64_t t0 = (uint64_t)blockIdx.x * kTile;
-    const uint32_t count = (uint32_t)min((uint64_t)kTile, n - t0);
+    // Elements from this tile's start to the tensor's end; below kTile, the last tile's count.
+    // No min() of the two ahead of the branch: hipcc (ROCm 7.2, gfx950) has built such a
+    // min as a scalar select at the top of the last-tile branch that read the condition code
+    // of another compare (of `first`), so that an assign into a last tile took the whole tile
+    // and wrote past the tensor's end (tests/test_isa_cpu.py scans for that form).
+    const uint64_t left = n - t0;
     double acc[2] = {0.0, 0.0};
     // the squares of a vector's stored values, in the norm pass's order
     auto add_squares = [&](const float* v, uint32_t nv) {
@@ -1078,7 +1083,7 @@ __global__ __launch_bounds__(kBlock) void accumulate_grad_tiles_kernel(
             *reinterpret_cast<f32x4*>(grad + i) = f32x4{v[0], v[1], v[2], v[3]};
         }
     };
-    if (count == kTile) {
+    if (left >= kTile) {
         // a whole tile: every load of the lane issued before the arithmetic (the scheduling
         // barrier keeps them ahead of it, as in the norm pass: with one vector in flight at a
         // time the call ran at a fraction of the copy rate)
@@ -1098,6 +1103,7 @@ __global__ __launch_bounds__(kBlock) void accumulate_grad_tiles_kernel(
             add_squares(v, (uint32_t)E);
         }
     } else {  // a tensor's last tile: the vectors (and elements) below its count
+        const uint32_t count = (uint32_t)left;
 #pragma unroll
         for (int l = 0; l < kNormLoads; ++l) {
             const uint32_t off = (uint32_t)(l * kBlock + threadIdx.x) * E;
