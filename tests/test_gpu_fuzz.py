@@ -23,6 +23,8 @@ After every operation the whole state is compared: master, m, v and momentum wit
 bit, the has-grad flags, the step count and the loss-scaler state; step reports must agree
 on skip, found_inf, step count and scale.  Every operation is printed before it runs.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -31,7 +33,8 @@ from gpu_util import compare_state, make_pair, torch_mod
 
 pytestmark = pytest.mark.gpu
 
-SEEDS = list(range(2000, 2100))
+# 100 seeded cases by default; TTP_FUZZ_CASES=N runs N (the same first 100, then more)
+SEEDS = list(range(2000, 2000 + int(os.environ.get("TTP_FUZZ_CASES", "100"))))
 N_OPS = 50
 BETAS = [(0.9, 0.999), (0.9, 0.95), (0.8, 0.99)]
 

@@ -10,6 +10,8 @@ fresh gradients, a random active set (a subset step, None grads, or every tensor
 full state and step report are compared after every step: bf16 bit-exact, fp32 within the
 2-ulp bar of the other parity tests, identical skip / scale / step-count decisions.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -18,7 +20,8 @@ from gpu_util import compare_state, device_grads, make_pair, torch_mod
 
 pytestmark = pytest.mark.gpu
 
-SEEDS = list(range(1000, 1120))
+# 120 seeded cases by default; TTP_RANDOM_CASES=N runs N (the same first 120, then more)
+SEEDS = list(range(1000, 1000 + int(os.environ.get("TTP_RANDOM_CASES", "120"))))
 
 
 def _shape(rng):

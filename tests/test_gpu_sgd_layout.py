@@ -178,3 +178,42 @@ def test_captured_sgd_step_replays_between_eager_steps():
     assert not store.sgd_layout
     compare_state(store, ref, max_ulp=2)
     store.close()
+
+
+def test_refused_adam_steps_leave_the_sgd_layout():
+    """An Adam step that is refused changes nothing, the layout included: the conversion to
+    the record layout (which moves the master, so that a master pointer taken before is no
+    longer valid) comes after every check that can refuse the step.  Refused here: a step
+    from tensor sums made stale by a later gradient write, a step over an unknown tensor
+    index, and bad hyperparameters; each leaves the layout, the master pointer and the state
+    as they were.  A valid step then converts the store and matches the oracle."""
+    import ttperf
+    from ttperf import _lib as L
+    torch = torch_mod()
+    shapes = [(52, 58), (54, 61), (913,)]
+    decay = [True, True, False]
+    store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=340, layout="sgd")
+    gen = torch.Generator(device="cuda").manual_seed(341)
+    device_grads(store, gen, 1e-2, into=ref.grad)
+    _set_all(ref)
+    master_ptr = store.ptr(L.BUF_MASTER)
+    hp = dict(lr=5e-4, betas=(0.9, 0.999), weight_decay=0.05, max_grad_norm=0.5)
+    store.grad_sumsq_tensors([0])
+    store.grad_sumsq_tensors([1, 2])
+    g = torch.randn(store.tensors[1].numel, generator=gen, device="cuda") * 1e-2
+    store.accumulate_grad(1, g)  # tensor 1's sum is now stale
+    ref.accumulate_grad(1, g.cpu().numpy())
+    refusals = [(dict(hp, tensor_sums=True), None, L.ERR_STATE),
+                (hp, [0, 7], L.ERR_RANGE),
+                (dict(hp, lr=0.0), None, L.ERR_INVALID)]
+    for kw, idx, code in refusals:
+        with pytest.raises(ttperf.TTPError) as err:
+            store.adam_step(indices=idx, **kw)
+        assert err.value.code == code, (kw, idx, err.value)
+        assert store.sgd_layout and store.ptr(L.BUF_MASTER) == master_ptr
+        assert store.step_count == 0
+        compare_state(store, ref, which=("master", "param"), max_ulp=0)
+    _check(store.adam_step(report=True, **hp), ref.adam_step(**hp), True)
+    assert not store.sgd_layout
+    compare_state(store, ref, max_ulp=2)
+    store.close()

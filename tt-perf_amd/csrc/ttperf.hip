@@ -1581,7 +1581,6 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
                                    "in the SGD layout, allocates m and v, which the "
                                    "no-allocation step does not: step once with "
                                    "ttp_adam_step[_subset] first");
-    if ((rc = ensure_adam_state(c))) return rc;
     const WorkTables* w;
     std::vector<uint32_t> active;
     if ((rc = select_tables(c, subset, nsub, &w, &active, true, !noalloc))) return rc;
@@ -1607,6 +1606,9 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
     if ((!noalloc || devt) &&
         (rc = ensure_bias_table(c, hp->beta1, hp->beta2, !noalloc)) && (devt || noalloc))
         return rc;
+    // m and v last, once nothing above can refuse the step: in the SGD layout this moves the
+    // master into new records, which a refused call must not do
+    if ((rc = ensure_adam_state(c))) return rc;
     if ((need_norm || devt) &&
         (rc = launch_prologue(c, w, need_norm, hp->max_grad_norm, false, devt, devt, from_sums,
                               defer, scratch_partials)))
