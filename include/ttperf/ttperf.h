@@ -88,10 +88,11 @@ extern "C" {
  * flag the fp32 master is one contiguous buffer and no m / v exist (4 B/param instead of
  * 12 B/param of optimizer state), which lets the SGD update stream its four buffers (bf16
  * grad, master read and write, bf16 weights) like a copy.  The first Adam step, or any call
- * that asks for EXP_AVG / EXP_AVG_SQ (ttp_buffer_ptr, ttp_buffer_layout, ttp_upload,
- * ttp_download, ttp_load_state of a file holding them), converts the store to the default
- * layout once: it allocates the records, moves the master into them (values unchanged) and
- * frees the contiguous copy, waiting for the queued work.  That conversion is refused
+ * that asks for EXP_AVG / EXP_AVG_SQ (ttp_buffer_layout, ttp_upload, ttp_download,
+ * ttp_load_state of a file holding them), converts the store to the default layout once: it
+ * allocates the records, moves the master into them (values unchanged) and frees the
+ * contiguous copy, waiting for the queued work.  A call that is refused for any other reason
+ * converts nothing (the conversion comes after its checks).  That conversion is refused
  * (TTP_ERR_STATE, nothing changed) while capturing, while graphs of the context are alive
  * (they hold the old master's address) and by ttp_adam_step_noalloc.  A master pointer from
  * ttp_buffer_ptr is invalid after it.  ttp_mode reports the precision mode only; the layout

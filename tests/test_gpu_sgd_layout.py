@@ -180,13 +180,14 @@ def test_captured_sgd_step_replays_between_eager_steps():
     store.close()
 
 
-def test_refused_adam_steps_leave_the_sgd_layout():
-    """An Adam step that is refused changes nothing, the layout included: the conversion to
-    the record layout (which moves the master, so that a master pointer taken before is no
-    longer valid) comes after every check that can refuse the step.  Refused here: a step
-    from tensor sums made stale by a later gradient write, a step over an unknown tensor
-    index, and bad hyperparameters; each leaves the layout, the master pointer and the state
-    as they were.  A valid step then converts the store and matches the oracle."""
+def test_refused_calls_leave_the_sgd_layout():
+    """A call that is refused changes nothing, the layout included: the conversion to the
+    record layout (which moves the master, so that a master pointer taken before is no longer
+    valid) comes after every check that can refuse the call.  Refused here: Adam steps (from
+    tensor sums made stale by a later gradient write, over an unknown tensor index, with bad
+    hyperparameters) and the buffer calls that would otherwise convert for m or v; each
+    leaves the layout, the master pointer and the state as they were.  A valid step then
+    converts the store and matches the oracle."""
     import ttperf
     from ttperf import _lib as L
     torch = torch_mod()
@@ -213,7 +214,56 @@ def test_refused_adam_steps_leave_the_sgd_layout():
         assert store.sgd_layout and store.ptr(L.BUF_MASTER) == master_ptr
         assert store.step_count == 0
         compare_state(store, ref, which=("master", "param"), max_ulp=0)
+    # the buffer calls that would convert for m or v, refused for something else first (raw
+    # C ABI calls, so that the library's own checks answer): m has no plain pointer in either
+    # layout; a transfer of the wrong size, of an unknown tensor, or with a host pointer where
+    # device memory is declared
+    h = store.handle
+    buf = np.zeros(store.total + 1, np.float32)
+    out = C.c_void_p()
+    calls = [(L.lib.ttp_buffer_ptr(h, L.BUF_EXP_AVG, L.ALL_TENSORS, C.byref(out)), L.ERR_STATE),
+             (L.lib.ttp_buffer_ptr(h, L.BUF_EXP_AVG_SQ, 0, C.byref(out)), L.ERR_STATE),
+             (L.lib.ttp_upload(h, L.BUF_EXP_AVG, L.ALL_TENSORS, buf.ctypes.data, store.total + 1,
+                               L.HOST), L.ERR_RANGE),
+             (L.lib.ttp_download(h, L.BUF_EXP_AVG_SQ, 7, buf.ctypes.data, 3, L.HOST), L.ERR_RANGE),
+             (L.lib.ttp_upload(h, L.BUF_EXP_AVG, 2, buf.ctypes.data, 913, L.DEVICE),
+              L.ERR_INVALID)]
+    for k, (rc, code) in enumerate(calls):
+        assert rc == code, (k, rc, code)
+        assert store.sgd_layout and store.ptr(L.BUF_MASTER) == master_ptr, k
     _check(store.adam_step(report=True, **hp), ref.adam_step(**hp), True)
     assert not store.sgd_layout
     compare_state(store, ref, max_ulp=2)
+    store.close()
+
+
+def test_refused_momentum_steps_allocate_nothing(tmp_path):
+    """The SGD side of the same rule: a momentum step refused for stale tensor sums leaves
+    the store without a momentum buffer, so a checkpoint taken after it holds the master only
+    (buffer mask 1 at byte 20 of the state file's header); the valid step that follows
+    allocates it, and the next checkpoint holds it (mask 1 | 8)."""
+    import struct
+    import ttperf
+    from ttperf import _lib as L
+    torch = torch_mod()
+    shapes = [(52, 58), (54, 61), (913,)]
+    decay = [True, True, False]
+    store, ref = make_pair(shapes, decay, O.MODE_MIXED, seed=350, layout="sgd")
+    gen = torch.Generator(device="cuda").manual_seed(351)
+    device_grads(store, gen, 1e-2, into=ref.grad)
+    _set_all(ref)
+    hp = dict(lr=0.01, momentum=0.9, max_grad_norm=0.5)
+    store.grad_sumsq_tensors()
+    store.zero_grad(set_to_none=False, indices=[2])  # tensor 2's sum is now stale
+    ref.grad[store.offsets[2]:store.offsets[2] + store.tensors[2].numel] = 0
+    with pytest.raises(ttperf.TTPError) as err:
+        store.sgd_step(tensor_sums=True, **hp)
+    assert err.value.code == L.ERR_STATE
+    mask = lambda p: struct.unpack_from("<I", p.read_bytes(), 20)[0]
+    store.save_state(tmp_path / "a.bin")
+    assert mask(tmp_path / "a.bin") == 1 and store.step_count == 0
+    _check(store.sgd_step(report=True, **hp), ref.sgd_step(**hp), False)
+    store.save_state(tmp_path / "b.bin")
+    assert mask(tmp_path / "b.bin") == 1 | 8
+    compare_state(store, ref, which=("master", "param", "momentum"), max_ulp=2)
     store.close()

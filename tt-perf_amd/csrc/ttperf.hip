@@ -910,11 +910,20 @@ size_t buffer_esize(const ttp_ctx* c, int which) {
     return 4;
 }
 
-int materialize(ttp_ctx* c, int which) {
-    if (which == TTP_BUF_EXP_AVG || which == TTP_BUF_EXP_AVG_SQ) return ensure_adam_state(c);
-    if (which == TTP_BUF_MOMENTUM) return ensure_momentum(c);
+int check_buffer_id(int which) {
     if (which < TTP_BUF_PARAM || which > TTP_BUF_MOMENTUM)
         return fail(TTP_ERR_INVALID, "unknown buffer id " + std::to_string(which));
+    return TTP_OK;
+}
+
+// Allocates the optimizer state a buffer id names (m, v or the momentum) on first use; in the
+// SGD layout, m and v convert the store.  Callers validate everything else first, so that a
+// refused call neither allocates nor converts.
+int materialize(ttp_ctx* c, int which) {
+    int rc = check_buffer_id(which);
+    if (rc) return rc;
+    if (which == TTP_BUF_EXP_AVG || which == TTP_BUF_EXP_AVG_SQ) return ensure_adam_state(c);
+    if (which == TTP_BUF_MOMENTUM) return ensure_momentum(c);
     return TTP_OK;
 }
 
@@ -1280,20 +1289,19 @@ int ttp_buffer_ptr(ttp_ctx* c, int which, uint32_t index, void** ptr) {
     int rc = check_ctx(c);
     if (rc) return rc;
     if (!ptr) return fail(TTP_ERR_INVALID, "null output");
-    if ((rc = set_dev(c))) return rc;
-    if ((rc = materialize(c, which))) return rc;
-    if (in_records(c, which))
+    if ((rc = check_buffer_id(which))) return rc;
+    // m and v live in records in both modes (and are refused before they would be allocated)
+    if (which == TTP_BUF_EXP_AVG || which == TTP_BUF_EXP_AVG_SQ || in_records(c, which))
         return fail(TTP_ERR_STATE,
                     "buffer " + std::to_string(which) +
                         " is kept in interleaved state records in this precision mode; use "
                         "ttp_buffer_layout for its addressing, or ttp_upload / ttp_download");
+    if (index != TTP_ALL_TENSORS && (rc = check_index(c, index))) return rc;
+    if ((rc = set_dev(c))) return rc;
+    if ((rc = materialize(c, which))) return rc;
     char* base = (char*)buffer_base(c, which);
-    if (index == TTP_ALL_TENSORS) {
-        *ptr = base;
-        return TTP_OK;
-    }
-    if ((rc = check_index(c, index))) return rc;
-    *ptr = base + c->tensors[index].offset * buffer_esize(c, which);
+    *ptr = index == TTP_ALL_TENSORS ? base
+                                    : base + c->tensors[index].offset * buffer_esize(c, which);
     return TTP_OK;
 }
 
@@ -1314,13 +1322,14 @@ int ttp_upload(ttp_ctx* c, int which, uint32_t index, const void* src, uint64_t 
     if (kind == TTP_HOST && (rc = no_capture(c, "an upload from host memory"))) return rc;
     if (!src && n) return fail(TTP_ERR_INVALID, "null source");
     if (kind != TTP_HOST && kind != TTP_DEVICE) return fail(TTP_ERR_INVALID, "bad memory kind");
+    if ((rc = check_buffer_id(which))) return rc;
     if ((rc = set_dev(c))) return rc;
-    if ((rc = materialize(c, which))) return rc;
     uint64_t off, cnt;
     if ((rc = resolve_range(c, index, n, &off, &cnt))) return rc;
     const size_t es = buffer_esize(c, which);
     if (kind == TTP_DEVICE && (rc = check_device_buffer(c, src, cnt * es, "the upload source")))
         return rc;
+    if ((rc = materialize(c, which))) return rc;  // after every check
     if (cnt && in_records(c, which)) {
         // record-stored state; a MIXED master upload also writes the bf16 copy
         if ((rc = upload_slot(c, which, off, cnt, src, kind))) return rc;
@@ -1364,14 +1373,15 @@ int ttp_download(ttp_ctx* c, int which, uint32_t index, void* dst, uint64_t n, i
     if (kind == TTP_HOST && (rc = no_capture(c, "a download to host memory"))) return rc;
     if (!dst && n) return fail(TTP_ERR_INVALID, "null destination");
     if (kind != TTP_HOST && kind != TTP_DEVICE) return fail(TTP_ERR_INVALID, "bad memory kind");
+    if ((rc = check_buffer_id(which))) return rc;
     if ((rc = set_dev(c))) return rc;
-    if ((rc = materialize(c, which))) return rc;
     uint64_t off, cnt;
     if ((rc = resolve_range(c, index, n, &off, &cnt))) return rc;
     const size_t es = buffer_esize(c, which);
     if (kind == TTP_DEVICE &&
         (rc = check_device_buffer(c, dst, cnt * es, "the download destination")))
         return rc;
+    if ((rc = materialize(c, which))) return rc;  // after every check
     if (cnt && in_records(c, which)) {
         if ((rc = download_slot(c, which, off, cnt, dst, kind))) return rc;
         if (kind == TTP_HOST) HIP_TRY(hipStreamSynchronize(c->stream));
@@ -1701,7 +1711,6 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
     if (report && (rc = no_capture(c, "a step report (synchronises)"))) return rc;
     if ((rc = set_dev(c))) return rc;
     const bool mom = hp->momentum != 0.0;
-    if (mom && (rc = ensure_momentum(c))) return rc;
     const WorkTables* w;
     std::vector<uint32_t> active;
     if ((rc = select_tables(c, subset, nsub, &w, &active))) return rc;
@@ -1715,6 +1724,9 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
     const bool from_sums = need_norm && (hp->flags & TTP_STEP_TENSOR_SUMS);
     const bool defer = scaler && (hp->flags & TTP_STEP_DEFER_SCALE);
     if (from_sums && (rc = check_sums_current(c, active))) return rc;
+    // the momentum buffer once nothing above can refuse the step (a refused call changes
+    // nothing, not even what a checkpoint would hold)
+    if (mom && (rc = ensure_momentum(c))) return rc;
     if ((need_norm || devt) &&
         (rc = launch_prologue(c, w, need_norm, hp->max_grad_norm, false, false, devt, from_sums,
                               defer)))
