@@ -10,7 +10,10 @@ operations drawn from the whole host interface, mirrored on the oracle:
   `grad = None`; zero_grad of all or of a subset, to zeros or to None; master or bf16 weight
   uploads; Adam / AdamW / L2 and SGD (momentum, dampening, nesterov, L2) steps over everything
   or over a subset, with or without clipping, with step reports; steps that take their norm
-  from bucket sums (ttp_grad_sumsq_tensors), and their refusal after a gradient write; the
+  from bucket sums (ttp_grad_sumsq_tensors), and their refusal after a gradient write; a
+  backward's gradient producer (accumulates in reverse order whose last one per tensor also
+  stores that tensor's gradient sum, TTP_ACCUM_SUMSQ, some tensors with bucket sums instead)
+  followed by a step from those sums, and its refusal after an accumulate without sums; the
   loss scaler switched on or off; the step count set; the gradient norm probed; a checkpoint
   saved and later loaded; an Adam step captured into a graph (half of them together with
   the bucket sums it takes its norm from), and a zero_grad captured into one, replayed
@@ -355,6 +358,81 @@ class Case:
             self.last_adam = None
             self.mom_seen = True
 
+    def op_producer_step(self):
+        """A backward's gradient producer: one or two accumulates into each tensor of a random
+        set, in reverse order as a backward delivers them, the last one of each with
+        TTP_ACCUM_SUMSQ so that the launch also stores the tensor's gradient sum; a few of the
+        tensors take bucket sums instead; then a step over them from those sums (no norm
+        pass).  Sometimes an accumulate without sums comes last into one of them, which makes
+        its sum stale: the step is refused and changes nothing."""
+        import ttperf
+        from ttperf import _lib as L
+        rng = self.rng
+        if rng.random() < 0.5:
+            print("  zero_grad(set_to_none=True) before the producer", flush=True)
+            self.store.zero_grad(set_to_none=True)
+            self.ref.zero_grad(set_to_none=True)
+        indices = None if rng.random() < 0.5 else self.pick_subset()
+        targets = list(range(self.n)) if indices is None else list(indices)
+        bucket = [i for i in targets if rng.random() < 0.2]
+        adam = rng.random() < 0.6
+        clip = None if (self.scaler_on and rng.random() < 0.3) else float(10 ** rng.uniform(-2, 1))
+        if adam:
+            kind, hp = "adam", dict(lr=float(10 ** rng.uniform(-4, -1.5)),
+                                    betas=BETAS[int(rng.integers(0, 3))], eps=1e-8,
+                                    weight_decay=0.05, decoupled=True, max_grad_norm=clip)
+        else:
+            kind, hp = "sgd", dict(lr=float(10 ** rng.uniform(-3, -1)), momentum=0.9,
+                                   dampening=0.0, weight_decay=0.0, nesterov=False,
+                                   max_grad_norm=clip)
+        log = []
+        for i in reversed(targets):
+            reps = int(rng.integers(1, 3))
+            for rep in range(reps):
+                sums = rep == reps - 1 and i not in bucket
+                bf16 = rng.random() < 0.5
+                dev = rng.random() < 0.5
+                g = (rng.standard_normal(self.numels[i]) * float(10 ** rng.uniform(-4, -1)))
+                g = g.astype(np.float32)
+                if self.scaler_on:
+                    g *= np.float32(self.ref.scale)
+                src = O.bf16_rne(g) if bf16 else g
+                self.store.accumulate_grad(i, self.to_device(src) if dev else src, sums=sums)
+                self.ref.accumulate_grad(i, src)
+                log.append(f"{i}{'s' if sums else ''}")
+        if bucket:
+            self.store.grad_sumsq_tensors(bucket)
+        nonempty = [i for i in targets if self.numels[i]]
+        stale = (clip is not None or self.scaler_on) and nonempty and rng.random() < 0.2
+        print(f"  producer {' '.join(log)}, bucket sums {bucket}, then {kind} {hp} "
+              f"indices={indices}{' after an accumulate without sums' if stale else ''}",
+              flush=True)
+        step = self.store.adam_step if adam else self.store.sgd_step
+        if stale:
+            i = int(rng.choice(nonempty))
+            g = self.grad_values(self.numels[i])
+            self.store.accumulate_grad(i, g)
+            self.ref.accumulate_grad(i, g)
+            t0, layout = self.store.step_count, self.store.sgd_layout
+            with pytest.raises(ttperf.TTPError) as e:
+                step(indices=indices, tensor_sums=True, **hp)
+            assert e.value.code == L.ERR_STATE and self.store.step_count == t0
+            assert self.store.sgd_layout == layout
+            return
+        active = self._active(indices)
+        if adam and self._conversion_refused(
+                lambda: step(report=True, indices=indices, tensor_sums=True, **hp)):
+            return
+        r = step(report=True, indices=indices, tensor_sums=True, **hp)
+        e = self._ref_step(kind, hp, active)
+        self._check_report(r, e)
+        if adam:
+            self.last_adam = (hp, indices, active)
+            self.adam_seen = True
+        else:
+            self.last_adam = None
+            self.mom_seen = True
+
     def op_scaler(self):
         on = not self.scaler_on
         init = float(2.0 ** int(self.rng.integers(4, 14)))
@@ -500,7 +578,8 @@ class Case:
     OPS = [("grads_flat", 6), ("grad_one", 3), ("accumulate", 3), ("drop_grad", 2),
            ("zero_grad", 2), ("upload_weights", 1), ("adam", 6), ("sgd", 4), ("scaler", 1),
            ("set_step", 1), ("grad_norm", 1), ("save", 1), ("load", 1), ("capture", 2),
-           ("replay", 3), ("sums_step", 4), ("zero_graph", 2), ("scaler_update", 1)]
+           ("replay", 3), ("sums_step", 4), ("zero_graph", 2), ("scaler_update", 1),
+           ("producer_step", 3)]
 
     def compare(self):
         from ttperf import _lib as L
