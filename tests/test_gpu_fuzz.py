@@ -13,7 +13,9 @@ operations drawn from the whole host interface, mirrored on the oracle:
   from bucket sums (ttp_grad_sumsq_tensors), and their refusal after a gradient write; a
   backward's gradient producer (accumulates in reverse order whose last one per tensor also
   stores that tensor's gradient sum, TTP_ACCUM_SUMSQ, some tensors with bucket sums instead)
-  followed by a step from those sums, and its refusal after an accumulate without sums; the
+  followed by a step from those sums, and its refusal after an accumulate without sums; such
+  a producer iteration (from device buffers read in place) and its Adam step captured as one
+  graph and launched later with new buffer contents; the
   loss scaler switched on or off; the step count set; the gradient norm probed; a checkpoint
   saved and later loaded; an Adam step captured into a graph (half of them together with
   the bucket sums it takes its norm from), and a zero_grad captured into one, replayed
@@ -76,6 +78,8 @@ class Case:
         self.numels = [t.numel for t in self.store.tensors]
         self.graphs = []      # (graph, hp, captured active set)
         self.zero_graphs = []  # (graph, set_to_none, indices) of captured zero_grad calls
+        # (graph, hp, indices, targets, device sources) of captured producer iterations
+        self.prod_graphs = []
         self.last_adam = None  # (hp, indices, active set) of the last eager Adam step
         self.saved = None     # oracle snapshot of the last checkpoint
         self.path = tmp_path / f"state_{seed}.bin"
@@ -176,6 +180,9 @@ class Case:
             self.store.tensors[i].set_data(x)
             self.ref.set_master(i, x)
 
+    def _live(self):
+        return len(self.graphs) + len(self.zero_graphs) + len(self.prod_graphs)
+
     def _active(self, indices):
         cand = range(self.n) if indices is None else indices
         return [i for i in cand if self.ref.has_grad(i) and self.numels[i]]
@@ -211,7 +218,7 @@ class Case:
         True when the step was refused."""
         import ttperf
         from ttperf import _lib as L
-        live = len(self.graphs) + len(self.zero_graphs)
+        live = self._live()
         if not (self.store.sgd_layout and live):
             return False
         t0 = self.store.step_count
@@ -437,7 +444,7 @@ class Case:
         on = not self.scaler_on
         init = float(2.0 ** int(self.rng.integers(4, 14)))
         interval = int(self.rng.integers(2, 5))
-        live = len(self.graphs) + len(self.zero_graphs)  # every graph holds the settings
+        live = self._live()  # every graph holds the settings
         print(f"  scaler {'on' if on else 'off'} (init {init:g}, interval {interval}), "
               f"{live} live graph(s)", flush=True)
         if live:
@@ -495,7 +502,7 @@ class Case:
         snap = self.saved
         differs = bool(snap["enabled"]) != self.scaler_on or (
             self.scaler_on and snap["interval"] != self.ref.s.growth_interval)
-        live = len(self.graphs) + len(self.zero_graphs)
+        live = self._live()
         print(f"  load_state <- {self.path.name} ({live} live graph(s), "
               f"scaler settings differ: {differs})", flush=True)
         if live and differs:
@@ -545,6 +552,83 @@ class Case:
         g.replay()
         self._ref_step("adam", hp, active)
 
+    def _producer_iteration(self, hp, indices, targets, srcs, graph=None):
+        """New contents for the producer's device sources, then either its eager calls
+        (zero_grad to None, one accumulate with TTP_ACCUM_SUMSQ per tensor in reverse order,
+        the Adam step from those sums) or a launch of their captured graph; the oracle does
+        the same iteration.  Returns the store's step report (eager) or None."""
+        torch = self.torch
+        host = {}
+        for i in reversed(targets):
+            g = (self.rng.standard_normal(self.numels[i]) * float(10 ** self.rng.uniform(-4, -1)))
+            g = g.astype(np.float32)
+            if self.scaler_on:
+                g *= np.float32(self.ref.scale)
+            if srcs[i].dtype == torch.bfloat16:
+                host[i] = O.bf16_rne(g)
+                srcs[i].copy_(torch.from_numpy(host[i].view(np.int16)).view(torch.bfloat16))
+            else:
+                host[i] = g
+                srcs[i].copy_(torch.from_numpy(g))
+        torch.cuda.synchronize()
+        r = None
+        if graph is None:
+            self.store.zero_grad(set_to_none=True)
+            for i in reversed(targets):
+                self.store.accumulate_grad(i, srcs[i], sums=True)
+            r = self.store.adam_step(report=True, indices=indices, tensor_sums=True, **hp)
+        else:
+            graph.replay()
+            self.store.sync()
+        self.ref.zero_grad(set_to_none=True)
+        for i in reversed(targets):
+            self.ref.accumulate_grad(i, host[i])
+        e = self._ref_step("adam", hp, self._active(indices))
+        if r is not None:
+            self._check_report(r, e)
+        self.last_adam = None
+        self.adam_seen = True
+        return r
+
+    def op_producer_graph(self):
+        """A backward's producer and its step captured as one graph: zero_grad to None, one
+        accumulate with TTP_ACCUM_SUMSQ per tensor of a set (reverse order) from device
+        buffers that the graph reads in place, then the AdamW step from those sums.  One eager
+        run of the same calls comes first (it builds the step's tables, which a capture cannot
+        build); each later launch rewrites the buffers first (op_producer_replay)."""
+        torch = self.torch
+        if len(self.prod_graphs) >= 2:
+            return self.op_producer_replay()
+        rng = self.rng
+        indices = None if rng.random() < 0.5 else self.pick_subset()
+        targets = [i for i in (range(self.n) if indices is None else indices) if self.numels[i]]
+        if not targets:
+            return self.op_adam()
+        hp = dict(lr=float(10 ** rng.uniform(-4, -1.5)), betas=BETAS[int(rng.integers(0, 3))],
+                  eps=1e-8, weight_decay=0.05, decoupled=True,
+                  max_grad_norm=float(10 ** rng.uniform(-2, 1)))
+        dt = torch.bfloat16 if rng.random() < 0.5 else torch.float32
+        srcs = {i: torch.zeros(self.numels[i], device="cuda", dtype=dt) for i in targets}
+        print(f"  capture producer + adam from its sums {hp} indices={indices} "
+              f"targets={targets} sources {dt}", flush=True)
+        if self._conversion_refused(lambda: self.store.adam_step(indices=indices, **hp)):
+            return
+        self._producer_iteration(hp, indices, targets, srcs)
+        self.compare()
+        self.store.begin_capture()
+        self.store.zero_grad(set_to_none=True)
+        for i in reversed(targets):
+            self.store.accumulate_grad(i, srcs[i], sums=True)
+        self.store.adam_step(indices=indices, tensor_sums=True, **hp)
+        self.prod_graphs.append((self.store.end_capture(), hp, indices, targets, srcs))
+
+    def op_producer_replay(self):
+        if not self.prod_graphs:
+            return self.op_producer_graph()
+        g, hp, indices, targets, srcs = self.prod_graphs[int(self.rng.integers(0, len(self.prod_graphs)))]
+        print(f"  replay producer + adam {hp} indices={indices} targets={targets}", flush=True)
+        self._producer_iteration(hp, indices, targets, srcs, graph=g)
+
     def _zero_ref(self, none, idx):
         if idx is None:
             self.ref.zero_grad(set_to_none=none)
@@ -579,7 +663,7 @@ class Case:
            ("zero_grad", 2), ("upload_weights", 1), ("adam", 6), ("sgd", 4), ("scaler", 1),
            ("set_step", 1), ("grad_norm", 1), ("save", 1), ("load", 1), ("capture", 2),
            ("replay", 3), ("sums_step", 4), ("zero_graph", 2), ("scaler_update", 1),
-           ("producer_step", 3)]
+           ("producer_step", 3), ("producer_graph", 1), ("producer_replay", 2)]
 
     def compare(self):
         from ttperf import _lib as L
@@ -602,10 +686,11 @@ class Case:
             assert (scale, tracker) == (np.float32(self.ref.scale), self.ref.growth_tracker)
 
     def close(self):
-        for g, _, _ in self.graphs + self.zero_graphs:
+        for g in [x[0] for x in self.graphs + self.zero_graphs + self.prod_graphs]:
             g.close()
         self.graphs.clear()
         self.zero_graphs.clear()
+        self.prod_graphs.clear()
         self.store.close()
 
 
