@@ -316,27 +316,51 @@ def producer_step(store, stream, args, hp, mode, numels):
     dtype = L.DTYPE_BF16 if mode == "mixed" else L.DTYPE_F32
     order = [i for i in reversed(range(len(numels))) if numels[i]]
 
-    def produce(sums):
+    # buckets for the multi-tensor calls: consecutive tensors of the backward order, up to
+    # 25 MB of gradients and ACCUM_MULTI_MAX tensors each
+    buckets, cur, size = [], [], 0
+    for i in order:
+        cur.append(i)
+        size += numels[i] * esz
+        if size >= 25 << 20 or len(cur) == L.ACCUM_MULTI_MAX:
+            buckets.append(cur)
+            cur, size = [], 0
+    if cur:
+        buckets.append(cur)
+    tables = [((ctypes.c_uint32 * len(b))(*b),
+               (ctypes.c_void_p * len(b))(*[base + store.offsets[i] * esz for i in b]))
+              for b in buckets]
+
+    def produce(sums, multi=False):
         store.zero_grad(set_to_none=True)
         flag = L.ACCUM_SUMSQ if sums else 0
+        if multi:
+            for b, (idx, ptrs) in zip(buckets, tables):
+                L.check(L.lib.ttp_accumulate_grad_multi(store.handle, idx, ptrs, len(b),
+                                                        dtype | flag))
+            return
         for i in order:
             L.check(L.lib.ttp_accumulate_grad(store.handle, i,
                                               ctypes.c_void_p(base + store.offsets[i] * esz),
                                               numels[i], dtype | flag, L.DEVICE))
 
-    def iteration(sums, step=True):
-        produce(sums)
+    def iteration(sums, step=True, multi=False):
+        produce(sums, multi)
         if step:
             store.adam_step(tensor_sums=sums, **hp)
 
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     out = {}
-    for key, sums, step in (("norm_pass_ms", False, True), ("fused_sums_ms", True, True),
-                            ("producer_ms", False, False), ("producer_with_sums_ms", True, False)):
-        iteration(sums, step)  # eagerly once: work tables and the tile-sum buffer
+    for key, sums, step, multi in (
+            ("norm_pass_ms", False, True, False), ("fused_sums_ms", True, True, False),
+            ("producer_ms", False, False, False), ("producer_with_sums_ms", True, False, False),
+            ("multi_norm_pass_ms", False, True, True), ("multi_fused_sums_ms", True, True, True),
+            ("multi_producer_ms", False, False, True),
+            ("multi_producer_with_sums_ms", True, False, True)):
+        iteration(sums, step, multi)  # eagerly once: work tables and the tile-sum buffer
         torch.cuda.synchronize()
         store.begin_capture()
-        iteration(sums, step)
+        iteration(sums, step, multi)
         graph = store.end_capture()
         for _ in range(3):
             graph.replay()
@@ -350,14 +374,18 @@ def producer_step(store, stream, args, hp, mode, numels):
         graph.close()
     del src
     out["step_saved_ms"] = round(out["norm_pass_ms"] - out["fused_sums_ms"], 4)
+    out["multi_step_saved_ms"] = round(out["multi_norm_pass_ms"] - out["multi_fused_sums_ms"], 4)
     out["tensors"] = len(order)
+    out["buckets"] = len(buckets)
     out["note"] = ("zero_grad(set_to_none) + one ttp_accumulate_grad per tensor from device "
                    "memory + the AdamW step, captured as one hipGraph and replayed K times "
                    "between one event pair; fused_sums: the accumulates also store each "
                    "tensor's gradient sum and the step runs no norm pass; producer_*: the "
-                   "zero_grad and accumulates alone")
+                   "zero_grad and accumulates alone; multi_*: the same with one "
+                   "ttp_accumulate_grad_multi call per bucket of up to 25 MB of gradients")
     log(f"bench: producer + step: {out['norm_pass_ms']} ms with the norm pass, "
-        f"{out['fused_sums_ms']} ms with fused sums")
+        f"{out['fused_sums_ms']} ms with fused sums; in {len(buckets)} bucket calls "
+        f"{out['multi_norm_pass_ms']} / {out['multi_fused_sums_ms']} ms")
     return out
 
 

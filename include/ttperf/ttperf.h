@@ -58,7 +58,8 @@ extern "C" {
 
 /* ABI version, returned by ttp_abi_version().  Changes:
  *   2  TTP_STORE_SGD (the SGD layout of a MIXED store, OR'd into ttp_create's mode);
- *      TTP_ACCUM_SUMSQ (ttp_accumulate_grad also stores the tensor's gradient sum).
+ *      TTP_ACCUM_SUMSQ (ttp_accumulate_grad also stores the tensor's gradient sum);
+ *      ttp_accumulate_grad_multi (several tensors' gradients in one launch).
  *      Behaviour changes of existing entry points, which a caller written against version 1
  *      must follow: ttp_zero_grad_subset with set_to_none = 0 leaves the has-grad flags as
  *      they were (version 1 marked the listed tensors as having a grad); a captured
@@ -313,6 +314,18 @@ int ttp_zero_grad_subset(ttp_ctx* ctx, const uint32_t* indices, uint32_t n_indic
  * TTP_ERR_RANGE. */
 int ttp_accumulate_grad(ttp_ctx* ctx, uint32_t index, const void* src, uint64_t n,
                         int src_dtype, int src_kind);
+/* Several tensors' incoming gradients in one launch, as a backward hands over a bucket of
+ * them: for k < n, tensor indices[k] receives srcs[k] (its numel values of src_dtype, in
+ * device memory) exactly as ttp_accumulate_grad(ctx, indices[k], srcs[k], numel, src_dtype,
+ * TTP_DEVICE) would, bit for bit, TTP_ACCUM_SUMSQ included; same capture rule.  Each index
+ * at most once, at most TTP_ACCUM_MULTI_MAX per call, and fewer than 2^24 tiles of 16 KiB of
+ * gradients in all.  The call's table travels in the kernel's arguments: it allocates and
+ * copies nothing.  A refused call changes nothing.  It extends Value::accumulate_grad
+ * (autograd/dynamic/autograd.hpp:78-83) to a bucket: one launch instead of n, which for a
+ * backward's many small tensors is mostly launch latency saved. */
+#define TTP_ACCUM_MULTI_MAX 64
+int ttp_accumulate_grad_multi(ttp_ctx* ctx, const uint32_t* indices, const void* const* srcs,
+                              uint32_t n, int src_dtype);
 
 /* ---- optimizer steps ------------------------------------------------------------------ */
 int ttp_adam_step(ttp_ctx* ctx, const ttp_adam_hparams* hp, ttp_step_report* report);

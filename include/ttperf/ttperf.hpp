@@ -227,6 +227,16 @@ public:
         check(ttp_accumulate_grad(ctx_, i, src, numel(i), dtype | (sums ? TTP_ACCUM_SUMSQ : 0),
                                   TTP_DEVICE));
     }
+    // a backward's bucket in one launch: tensor idx[k] receives srcs[k] (device memory, all
+    // of one dtype), as accumulate_grad_device(idx[k], srcs[k], dtype, sums) would
+    void accumulate_grads_device(const std::vector<uint32_t>& idx,
+                                 const std::vector<const void*>& srcs, int dtype,
+                                 bool sums = false) {
+        if (idx.size() != srcs.size())
+            throw std::invalid_argument("accumulate_grads_device: one source per index");
+        check(ttp_accumulate_grad_multi(ctx_, idx.data(), srcs.data(), (uint32_t)idx.size(),
+                                        dtype | (sums ? TTP_ACCUM_SUMSQ : 0)));
+    }
     void* device_ptr(int which, uint32_t i = TTP_ALL_TENSORS) {
         void* p = nullptr;
         check(ttp_buffer_ptr(ctx_, which, i, &p));

@@ -306,6 +306,85 @@ void run_sgd_layout() {
     ttp_destroy(c);
 }
 
+// ttp_accumulate_grad_multi against one ttp_accumulate_grad per tensor: an assign round, then
+// an add round with sums, from fp32 device sources (the grads of an FP32 context of the same
+// table), into a MIXED store and its twin; the gradients and flags match bit for bit, and
+// the steps from the sums give the same state.  Duplicate indices and more than
+// TTP_ACCUM_MULTI_MAX tensors are refused.
+void run_multi_accumulate() {
+    const std::vector<uint64_t> numel = {3000, 1, 2 * 8192 + 5, 0, 777, 8192};
+    const uint64_t n = numel.size();
+    ttp_ctx* src = create(numel, TTP_MODE_FP32);
+    ttp_ctx* a = create(numel, TTP_MODE_MIXED);
+    ttp_ctx* b = create(numel, TTP_MODE_MIXED);
+    std::vector<uint32_t> idx;
+    std::vector<const void*> ptr;
+    for (uint32_t i = (uint32_t)n; i-- > 0;) {  // a backward's order
+        idx.push_back(i);
+        void* p = nullptr;
+        test::check(ttp_buffer_ptr(src, TTP_BUF_GRAD, i, &p) == TTP_OK, "source pointer");
+        ptr.push_back(p);
+    }
+    ttp_adam_hparams hp{};
+    hp.lr = 1e-3;
+    hp.beta1 = 0.9;
+    hp.beta2 = 0.95;
+    hp.eps = 1e-8;
+    hp.weight_decay = 0.1;
+    hp.decoupled = 1;
+    hp.max_grad_norm = 0.5;
+    hp.flags = TTP_STEP_TENSOR_SUMS;
+    for (int round = 0; round < 2; ++round) {
+        for (uint32_t i = 0; i < n; ++i) {
+            auto v = randn(numel[i], 900 + 10 * round + i);
+            if (numel[i])
+                test::check(ttp_upload(src, TTP_BUF_GRAD, i, v.data(), v.size(), TTP_HOST) == TTP_OK,
+                            "source upload");
+        }
+        const int dtype = TTP_DTYPE_F32 | (round ? TTP_ACCUM_SUMSQ : 0);
+        test::check(ttp_accumulate_grad_multi(a, idx.data(), ptr.data(), (uint32_t)n, dtype) ==
+                        TTP_OK,
+                    std::string("multi accumulate: ") + ttp_last_error());
+        for (uint32_t k = 0; k < n; ++k)
+            test::check(ttp_accumulate_grad(b, idx[k], ptr[k], numel[idx[k]], dtype,
+                                            TTP_DEVICE) == TTP_OK,
+                        std::string("accumulate: ") + ttp_last_error());
+        uint64_t total = 0;
+        ttp_flat_numel(a, &total);
+        test::check(download16(a, TTP_BUF_GRAD, TTP_ALL_TENSORS, total) ==
+                        download16(b, TTP_BUF_GRAD, TTP_ALL_TENSORS, total),
+                    "multi accumulate = per-tensor accumulates, round " + std::to_string(round));
+        for (uint32_t i = 0; i < n; ++i) {
+            int ha = 0, hb = 0;
+            ttp_get_has_grad(a, i, &ha);
+            ttp_get_has_grad(b, i, &hb);
+            test::check(ha == 1 && hb == 1, "has-grad flags after the accumulates");
+        }
+    }
+    ttp_step_report ra{}, rb{};
+    test::check(ttp_adam_step(a, &hp, &ra) == TTP_OK && ttp_adam_step(b, &hp, &rb) == TTP_OK,
+                std::string("steps from the sums: ") + ttp_last_error());
+    test::check(ra.grad_norm == rb.grad_norm && ra.grad_norm > 0, "the same norm from the sums");
+    uint64_t total = 0;
+    ttp_flat_numel(a, &total);
+    test::assert_bits(download(a, TTP_BUF_MASTER, TTP_ALL_TENSORS, total),
+                      download(b, TTP_BUF_MASTER, TTP_ALL_TENSORS, total), "the same master");
+    // refusals
+    std::vector<uint32_t> dup = {0, 2, 0};
+    std::vector<const void*> dptr = {ptr[n - 1], ptr[n - 3], ptr[n - 1]};
+    test::check(ttp_accumulate_grad_multi(a, dup.data(), dptr.data(), 3, TTP_DTYPE_F32) ==
+                    TTP_ERR_INVALID,
+                "an index listed twice is refused");
+    std::vector<uint32_t> many(TTP_ACCUM_MULTI_MAX + 1, 0);
+    std::vector<const void*> mptr(many.size(), ptr[0]);
+    test::check(ttp_accumulate_grad_multi(a, many.data(), mptr.data(), (uint32_t)many.size(),
+                                          TTP_DTYPE_F32) == TTP_ERR_RANGE,
+                "more than TTP_ACCUM_MULTI_MAX tensors are refused");
+    ttp_destroy(a);
+    ttp_destroy(b);
+    ttp_destroy(src);
+}
+
 }  // namespace
 
 int main() {
@@ -315,6 +394,7 @@ int main() {
     run_sgd_layout();
     run_mode(TTP_MODE_MIXED);
     run_mode(TTP_MODE_FP32);
+    run_multi_accumulate();
     // a table past the 2^40-element bound is refused before any allocation
     ttp_tensor_desc big[2] = {{1ull << 40, 0, 0}, {64, 0, 0}};
     ttp_ctx* c = nullptr;

@@ -15,7 +15,8 @@ operations drawn from the whole host interface, mirrored on the oracle:
   stores that tensor's gradient sum, TTP_ACCUM_SUMSQ, some tensors with bucket sums instead)
   followed by a step from those sums, and its refusal after an accumulate without sums; such
   a producer iteration (from device buffers read in place) and its Adam step captured as one
-  graph and launched later with new buffer contents; the
+  graph and launched later with new buffer contents; both producers with their gradients in
+  bucket calls (ttp_accumulate_grad_multi) half of the time; the
   loss scaler switched on or off; the step count set; the gradient norm probed; a checkpoint
   saved and later loaded; an Adam step captured into a graph (half of them together with
   the bucket sums it takes its norm from), and a zero_grad captured into one, replayed
@@ -393,7 +394,31 @@ class Case:
                                    dampening=0.0, weight_decay=0.0, nesterov=False,
                                    max_grad_norm=clip)
         log = []
-        for i in reversed(targets):
+        multi = rng.random() < 0.5  # the tensors in bucket calls (ttp_accumulate_grad_multi)
+        if multi:
+            # two rounds over the reverse order cut into buckets of 1..4 tensors (one source
+            # dtype per call): an add (or assign) round, then a round with sums except for the
+            # tensors that take bucket sums, which get no second round
+            for rnd in range(2):
+                order = [i for i in reversed(targets) if rnd == 0 or i not in bucket]
+                k = 0
+                while k < len(order):
+                    part = order[k:k + int(rng.integers(1, 5))]
+                    k += len(part)
+                    bf16 = rng.random() < 0.5
+                    hosts, devs = [], []
+                    for i in part:
+                        g = (rng.standard_normal(self.numels[i])
+                             * float(10 ** rng.uniform(-4, -1))).astype(np.float32)
+                        if self.scaler_on:
+                            g *= np.float32(self.ref.scale)
+                        hosts.append(O.bf16_rne(g) if bf16 else g)
+                        devs.append(self.to_device(hosts[-1]))
+                    self.store.accumulate_grads(part, devs, sums=rnd == 1)
+                    for i, h in zip(part, hosts):
+                        self.ref.accumulate_grad(i, h)
+                    log.append("[" + " ".join(f"{i}{'s' if rnd == 1 else ''}" for i in part) + "]")
+        for i in ([] if multi else reversed(targets)):
             reps = int(rng.integers(1, 3))
             for rep in range(reps):
                 sums = rep == reps - 1 and i not in bucket
@@ -552,6 +577,20 @@ class Case:
         g.replay()
         self._ref_step("adam", hp, active)
 
+    def _producer_calls(self, targets, srcs):
+        """zero_grad to None, then the targets' gradients with sums in reverse order: one
+        accumulate per tensor, or bucket calls of up to three tensors when the sources were
+        made for them (srcs["multi"])."""
+        self.store.zero_grad(set_to_none=True)
+        order = list(reversed(targets))
+        if srcs.get("multi"):
+            for k in range(0, len(order), 3):
+                part = order[k:k + 3]
+                self.store.accumulate_grads(part, [srcs[i] for i in part], sums=True)
+            return
+        for i in order:
+            self.store.accumulate_grad(i, srcs[i], sums=True)
+
     def _producer_iteration(self, hp, indices, targets, srcs, graph=None):
         """New contents for the producer's device sources, then either its eager calls
         (zero_grad to None, one accumulate with TTP_ACCUM_SUMSQ per tensor in reverse order,
@@ -573,9 +612,7 @@ class Case:
         torch.cuda.synchronize()
         r = None
         if graph is None:
-            self.store.zero_grad(set_to_none=True)
-            for i in reversed(targets):
-                self.store.accumulate_grad(i, srcs[i], sums=True)
+            self._producer_calls(targets, srcs)
             r = self.store.adam_step(report=True, indices=indices, tensor_sums=True, **hp)
         else:
             graph.replay()
@@ -609,16 +646,16 @@ class Case:
                   max_grad_norm=float(10 ** rng.uniform(-2, 1)))
         dt = torch.bfloat16 if rng.random() < 0.5 else torch.float32
         srcs = {i: torch.zeros(self.numels[i], device="cuda", dtype=dt) for i in targets}
+        srcs["multi"] = bool(rng.random() < 0.5)
         print(f"  capture producer + adam from its sums {hp} indices={indices} "
-              f"targets={targets} sources {dt}", flush=True)
+              f"targets={targets} sources {dt}{' in bucket calls' if srcs['multi'] else ''}",
+              flush=True)
         if self._conversion_refused(lambda: self.store.adam_step(indices=indices, **hp)):
             return
         self._producer_iteration(hp, indices, targets, srcs)
         self.compare()
         self.store.begin_capture()
-        self.store.zero_grad(set_to_none=True)
-        for i in reversed(targets):
-            self.store.accumulate_grad(i, srcs[i], sums=True)
+        self._producer_calls(targets, srcs)
         self.store.adam_step(indices=indices, tensor_sums=True, **hp)
         self.prod_graphs.append((self.store.end_capture(), hp, indices, targets, srcs))
 

@@ -1036,17 +1036,20 @@ __device__ __forceinline__ void ld_src(const float* p, float* out) {
     }
 }
 
+// Tile `tile` of one tensor's gradients (grad, n elements) from src: the block's work in
+// both accumulate kernels.  inv: 1/scale for the sums; wave_sums: the tensor's run of the
+// store-wide wave partials; pending: its flag, which the block of its first tile sets.
 template <typename SrcT, typename GradT, bool kVecSrc, bool kSums>
-__global__ __launch_bounds__(kBlock) void accumulate_grad_tiles_kernel(
-    GradT* __restrict__ grad, const SrcT* __restrict__ src, uint64_t n, int first,
-    const DevState* __restrict__ st, int32_t scaler_on, double* __restrict__ wave_sums,
-    uint32_t* __restrict__ pending) {
+__device__ __forceinline__ void accumulate_tile(GradT* __restrict__ grad,
+                                                const SrcT* __restrict__ src, uint64_t n,
+                                                int first, float inv, uint32_t tile,
+                                                double* __restrict__ wave_sums,
+                                                uint32_t* __restrict__ pending) {
     typedef GradVec<GradT> GV;
     typedef typename GV::raw R;
     constexpr int E = GV::kElems;
     constexpr uint32_t kTile = norm_tile_elems<GradT>();
-    const float inv = (kSums && scaler_on) ? (float)(1.0 / (double)st->scale) : 1.0f;
-    const uint64_t t0 = (uint64_t)blockIdx.x * kTile;
+    const uint64_t t0 = (uint64_t)tile * kTile;
     // Elements from this tile's start to the tensor's end; below kTile, the last tile's count.
     // No min() of the two ahead of the branch: hipcc (ROCm 7.2, gfx950) has built such a
     // min as a scalar select at the top of the last-tile branch that read the condition code
@@ -1137,9 +1140,57 @@ __global__ __launch_bounds__(kBlock) void accumulate_grad_tiles_kernel(
     if constexpr (kSums) {
         // each wave's total, the first stage of block_sum, with no LDS or barrier after it
         const double part = wave_sum(acc[0] + acc[1]);
-        if ((threadIdx.x & 63) == 0) wave_sums[(uint64_t)blockIdx.x * kWaves + threadIdx.x / 64] = part;
-        if (blockIdx.x == 0 && threadIdx.x == 0) *pending = 1u;
+        if ((threadIdx.x & 63) == 0) wave_sums[(uint64_t)tile * kWaves + threadIdx.x / 64] = part;
+        if (tile == 0 && threadIdx.x == 0) *pending = 1u;
     }
+}
+
+// one tensor per launch, one block per tile
+template <typename SrcT, typename GradT, bool kVecSrc, bool kSums>
+__global__ __launch_bounds__(kBlock) void accumulate_grad_tiles_kernel(
+    GradT* __restrict__ grad, const SrcT* __restrict__ src, uint64_t n, int first,
+    const DevState* __restrict__ st, int32_t scaler_on, double* __restrict__ wave_sums,
+    uint32_t* __restrict__ pending) {
+    const float inv = (kSums && scaler_on) ? (float)(1.0 / (double)st->scale) : 1.0f;
+    accumulate_tile<SrcT, GradT, kVecSrc, kSums>(grad, src, n, first, inv, blockIdx.x, wave_sums,
+                                                 pending);
+}
+
+// Several tensors per launch (a backward's bucket): the table travels in the kernel
+// arguments, so a call allocates and copies nothing and can be captured.  Tensor k takes
+// blocks [tile_end[k-1], tile_end[k]); its fields as in accumulate_grad_tiles_kernel.
+constexpr uint32_t kMultiMax = 64;
+struct MultiAccArgs {
+    uint32_t n;                      // tensors in the table (each with at least one element)
+    uint32_t first[kMultiMax / 32];  // bit k: tensor k has no grad yet (its values assign)
+    uint32_t tile_end[kMultiMax];    // tiles of tensors 0..k
+    uint32_t tile_base[kMultiMax];   // its first tile in the store-wide wave partials
+    uint32_t tensor[kMultiMax];      // its index in the tensor table (its pending flag)
+    uint64_t offset[kMultiMax];      // its first element in the flat grad buffer
+    uint64_t numel[kMultiMax];
+    const void* src[kMultiMax];
+};
+
+template <typename SrcT, typename GradT, bool kVecSrc, bool kSums>
+__global__ __launch_bounds__(kBlock) void accumulate_grads_multi_kernel(
+    GradT* __restrict__ grad, const MultiAccArgs a, const DevState* __restrict__ st,
+    int32_t scaler_on, double* __restrict__ wave_sums, uint32_t* __restrict__ pending) {
+    // the block's tensor: the first k with blockIdx.x < tile_end[k] (uniform in the block)
+    uint32_t lo = 0, hi = a.n - 1;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (blockIdx.x < a.tile_end[mid])
+            hi = mid;
+        else
+            lo = mid + 1;
+    }
+    const uint32_t k = lo;
+    const uint32_t tile = blockIdx.x - (k ? a.tile_end[k - 1] : 0u);
+    const float inv = (kSums && scaler_on) ? (float)(1.0 / (double)st->scale) : 1.0f;
+    accumulate_tile<SrcT, GradT, kVecSrc, kSums>(
+        grad + a.offset[k], static_cast<const SrcT*>(a.src[k]), a.numel[k],
+        (int)((a.first[k >> 5] >> (k & 31)) & 1u), inv, tile,
+        wave_sums + (uint64_t)a.tile_base[k] * kWaves, pending + a.tensor[k]);
 }
 
 template <typename GradT>

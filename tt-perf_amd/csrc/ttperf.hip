@@ -1567,6 +1567,98 @@ int ttp_accumulate_grad(ttp_ctx* c, uint32_t index, const void* src, uint64_t n,
     return TTP_OK;
 }
 
+static_assert(ttp::kMultiMax == TTP_ACCUM_MULTI_MAX, "the header's limit is the kernel table's");
+
+int ttp_accumulate_grad_multi(ttp_ctx* c, const uint32_t* indices, const void* const* srcs,
+                              uint32_t n, int dtype) {
+    int rc = check_ctx(c);
+    if (rc) return rc;
+    if (n > ttp::kMultiMax)
+        return fail(TTP_ERR_RANGE, std::to_string(n) + " tensors in one call; at most " +
+                                       std::to_string(ttp::kMultiMax));
+    if (n && (!indices || !srcs)) return fail(TTP_ERR_INVALID, "null index or source list");
+    const bool with_sums = (dtype & TTP_ACCUM_SUMSQ) != 0;
+    dtype &= ~TTP_ACCUM_SUMSQ;
+    if (dtype != TTP_DTYPE_F32 && dtype != TTP_DTYPE_BF16)
+        return fail(TTP_ERR_INVALID, "src_dtype must be TTP_DTYPE_F32 or TTP_DTYPE_BF16, "
+                                     "optionally | TTP_ACCUM_SUMSQ");
+    if ((rc = set_dev(c))) return rc;
+    const size_t sbytes = dtype == TTP_DTYPE_BF16 ? 2 : 4;
+    const uint64_t tile = norm_tile(c);
+    std::vector<uint8_t> seen(c->tensors.size(), 0);
+    ttp::MultiAccArgs a{};
+    uint64_t tiles = 0;
+    bool vec = true;
+    // every check first: a refused call changes nothing
+    for (uint32_t k = 0; k < n; ++k) {
+        const uint32_t i = indices[k];
+        if ((rc = check_index(c, i))) return rc;
+        if (seen[i]) return fail(TTP_ERR_INVALID, "tensor index " + std::to_string(i) +
+                                                      " listed twice");
+        seen[i] = 1;
+        if (c->capturing && !(c->cap_touched[i] & kCapGrad))
+            return fail(TTP_ERR_STATE,
+                        "a captured accumulate into tensor " + std::to_string(i) +
+                            " must follow a call of the same capture that sets that tensor's "
+                            "has-grad flag (zero_grad with set_to_none, set_has_grad, a "
+                            "gradient upload or an accumulate): whether it assigns or adds is "
+                            "fixed when it is captured");
+        const TensorRec& t = c->tensors[i];
+        if (!t.numel) continue;
+        if (!srcs[k]) return fail(TTP_ERR_INVALID, "null source for tensor " + std::to_string(i));
+        if ((rc = check_device_buffer(c, srcs[k], t.numel * sbytes, "an incoming gradient")))
+            return rc;
+        vec = vec && ((uintptr_t)srcs[k] & 15u) == 0;
+        tiles += (t.numel + tile - 1) / tile;
+        if (tiles >= (1u << 24))
+            return fail(TTP_ERR_RANGE, "the call covers " + std::to_string(tiles) +
+                                           " or more tiles of 16 KiB of gradients; at most "
+                                           "2^24 - 1 per call: split it");
+        const uint32_t m = a.n++;
+        if (!t.has_grad) a.first[m >> 5] |= 1u << (m & 31);
+        a.tile_end[m] = (uint32_t)tiles;
+        a.tile_base[m] = c->host_tile_base[i];
+        a.tensor[m] = i;
+        a.offset[m] = t.offset;
+        a.numel[m] = t.numel;
+        a.src[m] = srcs[k];
+    }
+    if (a.n) {
+        const int32_t scaler_on = c->scaler.enabled ? 1 : 0;
+        const bool mixed = c->mode == TTP_MODE_MIXED, bf16 = dtype == TTP_DTYPE_BF16;
+        const dim3 grid((uint32_t)tiles), block(ttp::kBlock);
+        clear_hip_error();
+#define TTP_ACC_MULTI(S, G, V, SUMS)                                                          \
+    hipLaunchKernelGGL((ttp::accumulate_grads_multi_kernel<S, G, V, SUMS>), grid, block, 0,   \
+                       c->stream, (G*)c->grad, a, (const DevState*)c->st, scaler_on,           \
+                       c->acc_tiles, c->tsum_pending)
+#define TTP_ACC_MULTI_SRC(S, G)                                   \
+    do {                                                          \
+        if (vec && with_sums) TTP_ACC_MULTI(S, G, true, true);    \
+        else if (vec) TTP_ACC_MULTI(S, G, true, false);           \
+        else if (with_sums) TTP_ACC_MULTI(S, G, false, true);     \
+        else TTP_ACC_MULTI(S, G, false, false);                   \
+    } while (0)
+        if (mixed && bf16)
+            TTP_ACC_MULTI_SRC(uint16_t, uint16_t);
+        else if (mixed)
+            TTP_ACC_MULTI_SRC(float, uint16_t);
+        else if (bf16)
+            TTP_ACC_MULTI_SRC(uint16_t, float);
+        else
+            TTP_ACC_MULTI_SRC(float, float);
+#undef TTP_ACC_MULTI_SRC
+#undef TTP_ACC_MULTI
+        HIP_TRY(hipGetLastError());
+    }
+    if (with_sums) c->acc_sums_used = true;
+    for (uint32_t k = 0; k < n; ++k) {
+        set_grad_flag(c, indices[k], true);
+        set_fresh(c, indices[k], with_sums);
+    }
+    return TTP_OK;
+}
+
 // `scratch_partials` non-null: the no-allocation step.  It builds no work or bias table and
 // allocates no state (each missing one is refused with TTP_ERR_STATE), records no timing
 // events, and its norm pass writes its partials there (at most kNoAllocPartials).

@@ -21,6 +21,7 @@ TENSOR_DECAY = 1
 HOST, DEVICE = 0, 1
 DTYPE_F32, DTYPE_BF16 = 0, 1
 ACCUM_SUMSQ = 0x100
+ACCUM_MULTI_MAX = 64  # tensors per ttp_accumulate_grad_multi call
 STEP_TENSOR_SUMS = 1
 STEP_DEFER_SCALE = 2
 KERNEL_NORM, KERNEL_UPDATE = 0, 1
@@ -81,6 +82,8 @@ SIGNATURES = {
     "ttp_zero_grad": (C.c_int, [_P, C.c_int]),
     "ttp_zero_grad_subset": (C.c_int, [_P, C.POINTER(C.c_uint32), C.c_uint32, C.c_int]),
     "ttp_accumulate_grad": (C.c_int, [_P, C.c_uint32, _P, C.c_uint64, C.c_int, C.c_int]),
+    "ttp_accumulate_grad_multi": (C.c_int, [_P, C.POINTER(C.c_uint32), C.POINTER(_P), C.c_uint32,
+                                            C.c_int]),
     "ttp_adam_step": (C.c_int, [_P, C.POINTER(AdamHParams), C.POINTER(StepReport)]),
     "ttp_sgd_step": (C.c_int, [_P, C.POINTER(SgdHParams), C.POINTER(StepReport)]),
     "ttp_adam_step_subset": (C.c_int, [_P, C.POINTER(AdamHParams), C.POINTER(C.c_uint32),

@@ -511,6 +511,35 @@ class ParamStore:
         L.check(L.lib.ttp_accumulate_grad(self._h, index, a.ctypes.data_as(C.c_void_p), n,
                                           dtype | flag, L.HOST))
 
+    def accumulate_grads(self, indices, values, sums=False):
+        """Several tensors' incoming gradients in one launch (ttp_accumulate_grad_multi), as a
+        backward hands over a bucket: tensor indices[k] receives values[k], a contiguous
+        float32 or bfloat16 torch tensor on the GPU (one dtype for the call), exactly as
+        accumulate_grad(indices[k], values[k], sums) would.  At most ACCUM_MULTI_MAX tensors
+        per call.  While capturing, the graph reads each value in place at every launch."""
+        import torch
+        indices = [int(i) for i in indices]
+        if len(values) != len(indices):
+            raise ValueError("one value per index")
+        dtypes = {v.dtype for v in values}
+        if not dtypes <= {torch.float32, torch.bfloat16} or len(dtypes) > 1:
+            raise ValueError("incoming gradients must be all float32 or all bfloat16")
+        dtype = L.DTYPE_BF16 if dtypes == {torch.bfloat16} else L.DTYPE_F32
+        for i, v in zip(indices, values):
+            if not (_is_torch(v) and v.is_cuda and v.is_contiguous()
+                    and v.numel() == self.tensors[i].numel):
+                raise ValueError(f"tensor {i}: a contiguous device tensor of "
+                                 f"{self.tensors[i].numel} elements is needed")
+        if not self._in_capture and values:
+            torch.cuda.current_stream(values[0].device).synchronize()
+        n = len(indices)
+        idx = (C.c_uint32 * max(n, 1))(*indices)
+        ptrs = (C.c_void_p * max(n, 1))(*[v.data_ptr() for v in values])
+        L.check(L.lib.ttp_accumulate_grad_multi(self._h, idx, ptrs, n,
+                                                dtype | (L.ACCUM_SUMSQ if sums else 0)))
+        if not self._in_capture:
+            self.sync()  # the values may be freed and reused by torch as soon as we return
+
     # ---- steps -----------------------------------------------------------------------------------
     @staticmethod
     def _index_array(indices):
