@@ -9,6 +9,7 @@
 #pragma once
 
 #include <cstdint>
+#include <algorithm>
 #include <memory>
 #include <optional>
 #include <stdexcept>
@@ -120,6 +121,34 @@ struct Value {
     // device address of this parameter's gradient slice, for backward kernels that write it
     void* grad_ptr() { return store().device_ptr(TTP_BUF_GRAD, index); }
 };
+
+// A backward's bucket of parameter gradients (ttp_accumulate_grad_multi, at most
+// TTP_ACCUM_MULTI_MAX per launch): params[k] receives incoming[k], device memory of one dtype
+// for all, exactly as params[k]->accumulate_grad_device(incoming[k], dtype, sums) would.  The
+// parameters belong to one arena; those without requires_grad are left out, as there.
+inline void accumulate_grads_device(const std::vector<ValuePtr>& params,
+                                    const std::vector<const void*>& incoming, int dtype,
+                                    bool sums = false) {
+    if (params.size() != incoming.size())
+        throw std::invalid_argument("accumulate_grads_device: one source per parameter");
+    if (params.empty()) return;
+    std::vector<uint32_t> idx;
+    std::vector<const void*> src;
+    for (size_t k = 0; k < params.size(); ++k) {
+        if (params[k]->arena != params[0]->arena)
+            throw std::invalid_argument("accumulate_grads_device: parameters of one arena");
+        if (!params[k]->requires_grad) continue;
+        idx.push_back(params[k]->index);
+        src.push_back(incoming[k]);
+    }
+    ttp::Store& store = params[0]->store();
+    for (size_t k = 0; k < idx.size(); k += TTP_ACCUM_MULTI_MAX) {
+        const size_t e = std::min(idx.size(), k + TTP_ACCUM_MULTI_MAX);
+        store.accumulate_grads_device(std::vector<uint32_t>(idx.begin() + k, idx.begin() + e),
+                                      std::vector<const void*>(src.begin() + k, src.begin() + e),
+                                      dtype, sums);
+    }
+}
 
 // Declares parameters; all of them live in one store created on first use.
 class ParamArena {

@@ -289,6 +289,48 @@ static void run_tensor_sums() {
     test::check(thrown, "tensor sums: a step after a gradient write without new sums throws");
 }
 
+// A backward's gradients in one bucket call (autograd::accumulate_grads_device over
+// ttp_accumulate_grad_multi) against one accumulate_grad_device per parameter, both with sums
+// and in reverse parameter order, from the same device sources (the grads of a third arena):
+// AdamW steps from those sums give the same weights, bit for bit.
+static void run_bucket_producer() {
+    ParamArena a1(ttp::Mode::Mixed), a2(ttp::Mode::Mixed), as(ttp::Mode::FP32);
+    MLP m1(64, 128, 10, a1), m2(64, 128, 10, a2), ms(64, 128, 10, as);
+    auto p1 = m1.parameters(), p2 = m2.parameters(), ps = ms.parameters();
+    AdamW o1(p1, 1e-2f, {0.9, 0.95}, 1e-8f, 0.1f, /*max_grad_norm*/ 0.05);
+    AdamW o2(p2, 1e-2f, {0.9, 0.95}, 1e-8f, 0.1f, 0.05);
+    o1.opts.tensor_sums = o2.opts.tensor_sums = true;
+    for (size_t k = 0; k < p1.size(); ++k) p2[k]->set_data(p1[k]->master());
+    for (int t = 1; t <= 3; ++t) {
+        std::vector<ValuePtr> rev;
+        std::vector<const void*> src;
+        for (size_t k = ps.size(); k-- > 0;) {
+            ps[k]->grad = grad_of(ps[k]->numel(), 700 + t * 10 + (int)k);
+            rev.push_back(p2[k]);
+            src.push_back(ps[k]->grad_ptr());
+        }
+        for (auto* p : {&p1, &p2})
+            for (auto& v : *p) v->grad = std::nullopt;
+        for (size_t k = p1.size(); k-- > 0;)
+            p1[k]->accumulate_grad_device(ps[k]->grad_ptr(), TTP_DTYPE_F32, true);
+        autograd::accumulate_grads_device(rev, src, TTP_DTYPE_F32, true);
+        auto r1 = o1.step(true);
+        auto r2 = o2.step(true);
+        test::check(r1.grad_norm == r2.grad_norm && r1.clip_coef < 1.0f,
+                    "bucket producer: the same norm from the sums, clip active");
+    }
+    for (size_t k = 0; k < p1.size(); ++k)
+        test::assert_bits(p1[k]->master(), p2[k]->master(),
+                          "bucket producer: param " + std::to_string(k));
+    // parameters of two arenas in one call are refused
+    bool thrown = false;
+    try {
+        autograd::accumulate_grads_device({p1[0], p2[1]}, {ps[0]->grad_ptr(), ps[1]->grad_ptr()},
+                                          TTP_DTYPE_F32);
+    } catch (const std::invalid_argument&) { thrown = true; }
+    test::check(thrown, "bucket producer: parameters of two arenas are refused");
+}
+
 // Saved step counts belong to the store they were saved for: a store created after another
 // was destroyed (here most likely at the same heap address) starts from its own count, not
 // from what an optimizer saved for the destroyed one.
@@ -321,6 +363,7 @@ int main() {
     run_scaled_groups();
     run_graph_groups();
     run_tensor_sums();
+    run_bucket_producer();
     run_counts_outlive_store();
     // py/optim.py:33-41 validation
     ParamArena arena;
