@@ -39,8 +39,10 @@ from gpu_util import compare_state, make_pair, torch_mod
 
 pytestmark = pytest.mark.gpu
 
-# 100 seeded cases by default; TTP_FUZZ_CASES=N runs N (the same first 100, then more)
-SEEDS = list(range(2000, 2000 + int(os.environ.get("TTP_FUZZ_CASES", "100"))))
+# 100 seeded cases by default; TTP_FUZZ_CASES=N runs N (the same first 100, then more), from
+# seed TTP_FUZZ_FIRST on (2000)
+_FIRST = int(os.environ.get("TTP_FUZZ_FIRST", "2000"))
+SEEDS = list(range(_FIRST, _FIRST + int(os.environ.get("TTP_FUZZ_CASES", "100"))))
 N_OPS = int(os.environ.get("TTP_FUZZ_OPS", "50"))  # operations per case
 BETAS = [(0.9, 0.999), (0.9, 0.95), (0.8, 0.99)]
 
