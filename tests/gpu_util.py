@@ -108,6 +108,10 @@ def compare_state(store, ref, which=("master", "exp_avg", "exp_avg_sq", "param")
         worst, nbad = 0, 0
         for a in range(0, store.total, slice_elems):
             b = min(store.total, a + slice_elems)
+            # a bit-identical slice (padding included) has no difference to count: the ulp
+            # arithmetic below costs about 100 times more and runs only where bits differ
+            if np.array_equal(got[a:b].view(np.uint8), want[a:b].view(np.uint8)):
+                continue
             m = mask[a:b]
             if got.dtype == np.uint16:
                 nbad += int(np.count_nonzero((got[a:b] != want[a:b]) & m))
