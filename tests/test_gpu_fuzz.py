@@ -39,11 +39,15 @@ from gpu_util import compare_state, make_pair, torch_mod
 
 pytestmark = pytest.mark.gpu
 
-# 100 seeded cases by default; TTP_FUZZ_CASES=N runs N (the same first 100, then more), from
-# seed TTP_FUZZ_FIRST on (2000)
+# 1000 seeded cases of 50 operations by default; TTP_FUZZ_CASES=N runs N (the same first 1000,
+# then more), from seed TTP_FUZZ_FIRST on (2000), TTP_FUZZ_OPS operations each; and 100 longer
+# cases of 250 operations (TTP_FUZZ_LONG_CASES), which reach deeper states: more live graphs,
+# checkpoints and scale changes per store
 _FIRST = int(os.environ.get("TTP_FUZZ_FIRST", "2000"))
-SEEDS = list(range(_FIRST, _FIRST + int(os.environ.get("TTP_FUZZ_CASES", "100"))))
+SEEDS = list(range(_FIRST, _FIRST + int(os.environ.get("TTP_FUZZ_CASES", "1000"))))
 N_OPS = int(os.environ.get("TTP_FUZZ_OPS", "50"))  # operations per case
+LONG_SEEDS = list(range(90000, 90000 + int(os.environ.get("TTP_FUZZ_LONG_CASES", "100"))))
+LONG_OPS = 250
 BETAS = [(0.9, 0.999), (0.9, 0.95), (0.8, 0.99)]
 
 
@@ -733,8 +737,7 @@ class Case:
         self.store.close()
 
 
-@pytest.mark.parametrize("seed", SEEDS)
-def test_random_operation_sequence(seed, tmp_path):
+def _run_case(seed, tmp_path, n_ops):
     c = Case(seed, tmp_path)
     print(f"case {seed}: {'mixed' if c.mixed else 'fp32'}"
           f"{' (SGD layout)' if c.sgd_layout else ''} shapes={c.shapes}", flush=True)
@@ -742,10 +745,20 @@ def test_random_operation_sequence(seed, tmp_path):
     weights = np.array([w for _, w in Case.OPS], np.float64)
     weights /= weights.sum()
     try:
-        for k in range(N_OPS):
+        for k in range(n_ops):
             op = names[int(c.rng.choice(len(names), p=weights))]
             print(f" op {k}: {op}", flush=True)
             getattr(c, "op_" + op)()
             c.compare()
     finally:
         c.close()
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_random_operation_sequence(seed, tmp_path):
+    _run_case(seed, tmp_path, N_OPS)
+
+
+@pytest.mark.parametrize("seed", LONG_SEEDS)
+def test_long_random_operation_sequence(seed, tmp_path):
+    _run_case(seed, tmp_path, LONG_OPS)

@@ -20,8 +20,8 @@ from gpu_util import compare_state, device_grads, make_pair, torch_mod
 
 pytestmark = pytest.mark.gpu
 
-# 120 seeded cases by default; TTP_RANDOM_CASES=N runs N (the same first 120, then more)
-SEEDS = list(range(1000, 1000 + int(os.environ.get("TTP_RANDOM_CASES", "120"))))
+# 1000 seeded cases by default; TTP_RANDOM_CASES=N runs N (the same first 1000, then more)
+SEEDS = list(range(1000, 1000 + int(os.environ.get("TTP_RANDOM_CASES", "1000"))))
 
 
 def _shape(rng):
