@@ -84,7 +84,7 @@ inline void assert_all_close(const std::vector<float>& got, float expected, floa
         }
 }
 
-// the verdict is flushed at once: what the runtimes do at exit cannot lose it
+// the pass/fail line is flushed at once: what the runtimes do at exit cannot lose it
 inline int finish(const char* name) {
     if (g_failures) {
         std::printf("%s: %d check(s) failed\n", name, g_failures);
