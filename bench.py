@@ -331,8 +331,8 @@ def producer_step(store, stream, args, hp, mode, numels):
                (ctypes.c_void_p * len(b))(*[base + store.offsets[i] * esz for i in b]))
               for b in buckets]
 
-    def produce(sums, multi=False):
-        store.zero_grad(set_to_none=True)
+    def produce(sums, multi=False, fill=True):
+        store.zero_grad(set_to_none=True, fill=fill)
         flag = L.ACCUM_SUMSQ if sums else 0
         if multi:
             for b, (idx, ptrs) in zip(buckets, tables):
@@ -344,23 +344,27 @@ def producer_step(store, stream, args, hp, mode, numels):
                                               ctypes.c_void_p(base + store.offsets[i] * esz),
                                               numels[i], dtype | flag, L.DEVICE))
 
-    def iteration(sums, step=True, multi=False):
-        produce(sums, multi)
+    def iteration(sums, step=True, multi=False, fill=True):
+        produce(sums, multi, fill)
         if step:
             store.adam_step(tensor_sums=sums, **hp)
 
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     out = {}
-    for key, sums, step, multi in (
-            ("norm_pass_ms", False, True, False), ("fused_sums_ms", True, True, False),
-            ("producer_ms", False, False, False), ("producer_with_sums_ms", True, False, False),
-            ("multi_norm_pass_ms", False, True, True), ("multi_fused_sums_ms", True, True, True),
-            ("multi_producer_ms", False, False, True),
-            ("multi_producer_with_sums_ms", True, False, True)):
-        iteration(sums, step, multi)  # eagerly once: work tables and the tile-sum buffer
+    for key, sums, step, multi, fill in (
+            ("norm_pass_ms", False, True, False, True), ("fused_sums_ms", True, True, False, True),
+            ("producer_ms", False, False, False, True),
+            ("producer_with_sums_ms", True, False, False, True),
+            ("multi_norm_pass_ms", False, True, True, True),
+            ("multi_fused_sums_ms", True, True, True, True),
+            ("multi_producer_ms", False, False, True, True),
+            ("multi_producer_with_sums_ms", True, False, True, True),
+            ("multi_fused_sums_nofill_ms", True, True, True, False),
+            ("multi_producer_with_sums_nofill_ms", True, False, True, False)):
+        iteration(sums, step, multi, fill)  # eagerly once: work tables and the tile-sum buffer
         torch.cuda.synchronize()
         store.begin_capture()
-        iteration(sums, step, multi)
+        iteration(sums, step, multi, fill)
         graph = store.end_capture()
         for _ in range(3):
             graph.replay()
@@ -382,10 +386,13 @@ def producer_step(store, stream, args, hp, mode, numels):
                    "between one event pair; fused_sums: the accumulates also store each "
                    "tensor's gradient sum and the step runs no norm pass; producer_*: the "
                    "zero_grad and accumulates alone; multi_*: the same with one "
-                   "ttp_accumulate_grad_multi call per bucket of up to 25 MB of gradients")
+                   "ttp_accumulate_grad_multi call per bucket of up to 25 MB of gradients; "
+                   "*_nofill: zero_grad(set_to_none) clears the has-grad flags only "
+                   "(TTP_ZERO_NO_FILL), the first accumulate assigns each gradient")
     log(f"bench: producer + step: {out['norm_pass_ms']} ms with the norm pass, "
         f"{out['fused_sums_ms']} ms with fused sums; in {len(buckets)} bucket calls "
-        f"{out['multi_norm_pass_ms']} / {out['multi_fused_sums_ms']} ms")
+        f"{out['multi_norm_pass_ms']} / {out['multi_fused_sums_ms']} ms, "
+        f"{out['multi_fused_sums_nofill_ms']} ms without the zero_grad fill")
     return out
 
 

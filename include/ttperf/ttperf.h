@@ -59,7 +59,8 @@ extern "C" {
 /* ABI version, returned by ttp_abi_version().  Changes:
  *   2  TTP_STORE_SGD (the SGD layout of a MIXED store, OR'd into ttp_create's mode);
  *      TTP_ACCUM_SUMSQ (ttp_accumulate_grad also stores the tensor's gradient sum);
- *      ttp_accumulate_grad_multi (several tensors' gradients in one launch).
+ *      ttp_accumulate_grad_multi (several tensors' gradients in one launch);
+ *      TTP_ZERO_NO_FILL (ttp_zero_grad[_subset] to None without the fill).
  *      Behaviour changes of existing entry points, which a caller written against version 1
  *      must follow: ttp_zero_grad_subset with set_to_none = 0 leaves the has-grad flags as
  *      they were (version 1 marked the listed tensors as having a grad); a captured
@@ -281,7 +282,17 @@ int ttp_set_has_grad(ttp_ctx* ctx, uint32_t index, int has_grad);
 int ttp_get_has_grad(const ttp_ctx* ctx, uint32_t index, int* has_grad);
 /* Zero the whole grad buffer; set_to_none = 1 also clears every has_grad flag.
  * One fill over the flat buffer replaces the per-tensor zeros_like allocations of
- * autograd/static/nn.hpp:98-101 and the nullopt loop of autograd/dynamic/optim.hpp:30-34. */
+ * autograd/static/nn.hpp:98-101 and the nullopt loop of autograd/dynamic/optim.hpp:30-34.
+ * set_to_none = 1 | TTP_ZERO_NO_FILL clears the flags without the fill, as the reference's
+ * `grad = std::nullopt` touches no memory.  The gradients then keep their old contents until
+ * written.  Nothing of the library reads them: the next accumulate into a tensor assigns its
+ * whole gradient, and steps, norms and sums skip tensors without a grad.  A flat download or
+ * a view shows the old values, and a caller that writes gradients through ttp_buffer_ptr and
+ * marks them with ttp_set_has_grad must write every element.  For a backward that delivers
+ * every gradient by accumulate, it saves one write of the whole buffer per iteration.
+ * Without set_to_none it is refused (TTP_ERR_INVALID).  The same holds for
+ * ttp_zero_grad_subset. */
+#define TTP_ZERO_NO_FILL 0x100
 int ttp_zero_grad(ttp_ctx* ctx, int set_to_none);
 /* A module's zero_grad: the listed tensors' grads (each index at most once) become zeros
  * (set_to_none = 0: the static layers' zeros_like, autograd/static/nn.hpp:98-101, 183-186)

@@ -211,10 +211,14 @@ public:
         return h != 0;
     }
     void set_has_grad(uint32_t i, bool h) { check(ttp_set_has_grad(ctx_, i, h ? 1 : 0)); }
-    void zero_grad(bool set_to_none = true) { check(ttp_zero_grad(ctx_, set_to_none ? 1 : 0)); }
-    void zero_grad(const std::vector<uint32_t>& indices, bool set_to_none) {
+    // fill = false (with set_to_none): flags only, the gradients keep their old contents
+    // until written (TTP_ZERO_NO_FILL)
+    void zero_grad(bool set_to_none = true, bool fill = true) {
+        check(ttp_zero_grad(ctx_, (set_to_none ? 1 : 0) | (fill ? 0 : TTP_ZERO_NO_FILL)));
+    }
+    void zero_grad(const std::vector<uint32_t>& indices, bool set_to_none, bool fill = true) {
         check(ttp_zero_grad_subset(ctx_, indices.data(), (uint32_t)indices.size(),
-                                   set_to_none ? 1 : 0));
+                                   (set_to_none ? 1 : 0) | (fill ? 0 : TTP_ZERO_NO_FILL)));
     }
     // grad = g if tensor i has none, else grad + g (fp32 add, one rounding to the grad type);
     // sums: also store tensor i's gradient sum for a tensor_sums step (TTP_ACCUM_SUMSQ)

@@ -213,8 +213,10 @@ class OracleStore:
     def has_grad(self, i):
         return bool(self._tensors[i].has_grad)
 
-    def zero_grad(self, set_to_none=True):
-        self.grad[:] = 0
+    def zero_grad(self, set_to_none=True, fill=True):
+        """fill=False (with set_to_none): the flags only, the values stay."""
+        if fill:
+            self.grad[:] = 0
         if set_to_none:
             for i in range(self.n):
                 self._tensors[i].has_grad = 0

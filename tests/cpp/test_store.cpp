@@ -369,6 +369,28 @@ void run_multi_accumulate() {
     ttp_flat_numel(a, &total);
     test::assert_bits(download(a, TTP_BUF_MASTER, TTP_ALL_TENSORS, total),
                       download(b, TTP_BUF_MASTER, TTP_ALL_TENSORS, total), "the same master");
+    // zero_grad to None without the fill: the flags go, the memory stays, and the next
+    // accumulates assign, as after the filling zero_grad
+    const auto kept = download16(a, TTP_BUF_GRAD, TTP_ALL_TENSORS, total);
+    test::check(ttp_zero_grad(a, 1 | TTP_ZERO_NO_FILL) == TTP_OK && ttp_zero_grad(b, 1) == TTP_OK,
+                std::string("zero_grad: ") + ttp_last_error());
+    test::check(download16(a, TTP_BUF_GRAD, TTP_ALL_TENSORS, total) == kept,
+                "zero_grad without the fill leaves the gradients");
+    for (uint32_t i = 0; i < n; ++i) {
+        int ha = 1;
+        ttp_get_has_grad(a, i, &ha);
+        test::check(ha == 0, "zero_grad without the fill clears the has-grad flags");
+    }
+    test::check(ttp_zero_grad(a, TTP_ZERO_NO_FILL) == TTP_ERR_INVALID,
+                "the fill is skipped only for gradients set to None");
+    test::check(ttp_accumulate_grad_multi(a, idx.data(), ptr.data(), (uint32_t)n, TTP_DTYPE_F32) ==
+                        TTP_OK &&
+                    ttp_accumulate_grad_multi(b, idx.data(), ptr.data(), (uint32_t)n,
+                                              TTP_DTYPE_F32) == TTP_OK,
+                std::string("accumulates after zero_grad: ") + ttp_last_error());
+    test::check(download16(a, TTP_BUF_GRAD, TTP_ALL_TENSORS, total) ==
+                    download16(b, TTP_BUF_GRAD, TTP_ALL_TENSORS, total),
+                "accumulates after zero_grad with and without the fill");
     // refusals
     std::vector<uint32_t> dup = {0, 2, 0};
     std::vector<const void*> dptr = {ptr[n - 1], ptr[n - 3], ptr[n - 1]};

@@ -278,3 +278,79 @@ def test_gpt2_124m_buckets_equal_per_tensor_calls():
     compare_state(store, ref, max_ulp=2)
     store.close()
     twin.close()
+
+
+def test_zero_grad_without_fill():
+    """zero_grad(set_to_none=True, fill=False) (TTP_ZERO_NO_FILL) clears the has-grad flags and
+    leaves the gradient memory as it was, for all tensors or a list; without set_to_none it is
+    refused, as is a listed index twice.  A producer iteration after it (bucket calls that
+    assign every gradient, with sums, then the AdamW step from them) gives the state of a twin
+    whose zero_grad filled the buffer, bit for bit, and the oracle's; captured as one graph
+    (the flags-only zero_grad included) it replays against the oracle."""
+    torch = torch_mod()
+    from ttperf import _lib as L
+    store, ref = make_pair(SHAPES, DECAY, O.MODE_MIXED, seed=200)
+    twin, _ = make_pair(SHAPES, DECAY, O.MODE_MIXED, seed=200)
+    store.set_stream(None)  # the store's own stream: capturable
+    hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=0.5)
+    gen = torch.Generator(device="cuda").manual_seed(201)
+    n = len(SHAPES)
+    device_grads(store, gen, 1e-2, into=ref.grad)
+    before = store.download(L.BUF_GRAD).copy()
+    store.mark_grads()
+    store.zero_grad(set_to_none=True, indices=[1, 3], fill=False)
+    assert [store.has_grad(i) for i in range(n)] == [i not in (1, 3) for i in range(n)]
+    store.zero_grad(set_to_none=True, fill=False)
+    assert not any(store.has_grad(i) for i in range(n))
+    assert np.array_equal(store.download(L.BUF_GRAD), before)
+    h = store.handle
+    assert L.lib.ttp_zero_grad(h, L.ZERO_NO_FILL) == L.ERR_INVALID
+    idx = (C.c_uint32 * 2)(2, 2)
+    assert L.lib.ttp_zero_grad_subset(h, idx, 2, 1 | L.ZERO_NO_FILL) == L.ERR_INVALID
+    assert L.lib.ttp_zero_grad_subset(h, idx, 1, L.ZERO_NO_FILL) == L.ERR_INVALID
+    srcs = [torch.zeros(store.tensors[i].numel, device="cuda", dtype=torch.bfloat16)
+            for i in range(n)]
+    order = list(reversed(range(n)))
+    buckets = [order[:5], order[5:]]
+
+    def refill():
+        for i in range(n):
+            srcs[i].copy_((torch.randn(srcs[i].numel(), generator=gen, device="cuda") * 1e-2)
+                          .to(torch.bfloat16))
+        torch.cuda.synchronize()
+
+    def iteration(s, fill):
+        s.zero_grad(set_to_none=True, fill=fill)
+        for b in buckets:
+            s.accumulate_grads(b, [srcs[i] for i in b], sums=True)
+        return s.adam_step(report=True, tensor_sums=True, **hp) if not s._in_capture else \
+            s.adam_step(tensor_sums=True, **hp)
+
+    def ref_iteration():
+        ref.zero_grad(set_to_none=True, fill=False)
+        for b in buckets:
+            for i in b:
+                ref.accumulate_grad(i, _bits(srcs[i]))
+        return ref.adam_step(**hp)
+
+    refill()
+    r, rt, e = iteration(store, False), iteration(twin, True), ref_iteration()
+    assert np.float64(r["grad_norm"]) == np.float64(rt["grad_norm"])
+    assert abs(r["grad_norm"] - e["grad_norm"]) <= 1e-10 * e["grad_norm"]
+    for which in (L.BUF_MASTER, L.BUF_EXP_AVG, L.BUF_EXP_AVG_SQ, L.BUF_PARAM):
+        assert np.array_equal(store.download(which).view(np.uint8),
+                              twin.download(which).view(np.uint8)), which
+    compare_state(store, ref, max_ulp=2)
+    store.begin_capture()
+    iteration(store, False)
+    graph = store.end_capture()
+    for _ in range(2):
+        refill()
+        graph.replay()
+        e = ref_iteration()
+        store.sync()
+        assert store.step_count == e["step"]
+        compare_state(store, ref, max_ulp=2)
+    graph.close()
+    store.close()
+    twin.close()

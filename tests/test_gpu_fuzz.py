@@ -7,7 +7,8 @@ operations drawn from the whole host interface, mirrored on the oracle:
 
   gradients written flat or per tensor, from host or device memory (an occasional +inf while
   loss scaling is on); gradients accumulated from fp32 or bf16 sources, host or device;
-  `grad = None`; zero_grad of all or of a subset, to zeros or to None; master or bf16 weight
+  `grad = None`; zero_grad of all or of a subset, to zeros or to None (with or without the
+  fill); master or bf16 weight
   uploads; Adam / AdamW / L2 and SGD (momentum, dampening, nesterov, L2) steps over everything
   or over a subset, with or without clipping, with step reports; steps that take their norm
   from bucket sums (ttp_grad_sumsq_tensors), and their refusal after a gradient write; a
@@ -84,7 +85,7 @@ class Case:
         self.store.set_stream(None)  # the store's own stream: capturable
         self.numels = [t.numel for t in self.store.tensors]
         self.graphs = []      # (graph, hp, captured active set)
-        self.zero_graphs = []  # (graph, set_to_none, indices) of captured zero_grad calls
+        self.zero_graphs = []  # (graph, set_to_none, indices, fill) of captured zero_grad calls
         # (graph, hp, indices, targets, device sources) of captured producer iterations
         self.prod_graphs = []
         self.last_adam = None  # (hp, indices, active set) of the last eager Adam step
@@ -159,16 +160,19 @@ class Case:
 
     def op_zero_grad(self):
         none = bool(self.rng.integers(0, 2))
+        # to None, half of the time without the fill (TTP_ZERO_NO_FILL: the flags only)
+        fill = not none or bool(self.rng.random() < 0.5)
         if self.rng.random() < 0.5:
-            print(f"  zero_grad(set_to_none={none})", flush=True)
-            self.store.zero_grad(set_to_none=none)
-            self.ref.zero_grad(set_to_none=none)
+            print(f"  zero_grad(set_to_none={none}, fill={fill})", flush=True)
+            self.store.zero_grad(set_to_none=none, fill=fill)
+            self.ref.zero_grad(set_to_none=none, fill=fill)
         else:
             idx = self.pick_subset()
-            print(f"  zero_grad(set_to_none={none}, indices={idx})", flush=True)
-            self.store.zero_grad(set_to_none=none, indices=idx)
+            print(f"  zero_grad(set_to_none={none}, indices={idx}, fill={fill})", flush=True)
+            self.store.zero_grad(set_to_none=none, indices=idx, fill=fill)
             for i in idx:
-                self.ref.view("grad", i)[:] = 0
+                if fill:
+                    self.ref.view("grad", i)[:] = 0
                 if none:  # set_to_none=False leaves the has-grad flags as they are
                     self.ref.set_has_grad(i, False)
 
@@ -383,9 +387,10 @@ class Case:
         from ttperf import _lib as L
         rng = self.rng
         if rng.random() < 0.5:
-            print("  zero_grad(set_to_none=True) before the producer", flush=True)
-            self.store.zero_grad(set_to_none=True)
-            self.ref.zero_grad(set_to_none=True)
+            fill = bool(rng.random() < 0.5)
+            print(f"  zero_grad(set_to_none=True, fill={fill}) before the producer", flush=True)
+            self.store.zero_grad(set_to_none=True, fill=fill)
+            self.ref.zero_grad(set_to_none=True, fill=fill)
         indices = None if rng.random() < 0.5 else self.pick_subset()
         targets = list(range(self.n)) if indices is None else list(indices)
         bucket = [i for i in targets if rng.random() < 0.2]
@@ -587,7 +592,7 @@ class Case:
         """zero_grad to None, then the targets' gradients with sums in reverse order: one
         accumulate per tensor, or bucket calls of up to three tensors when the sources were
         made for them (srcs["multi"])."""
-        self.store.zero_grad(set_to_none=True)
+        self.store.zero_grad(set_to_none=True, fill=srcs.get("fill", True))
         order = list(reversed(targets))
         if srcs.get("multi"):
             for k in range(0, len(order), 3):
@@ -623,7 +628,7 @@ class Case:
         else:
             graph.replay()
             self.store.sync()
-        self.ref.zero_grad(set_to_none=True)
+        self.ref.zero_grad(set_to_none=True, fill=srcs.get("fill", True))
         for i in reversed(targets):
             self.ref.accumulate_grad(i, host[i])
         e = self._ref_step("adam", hp, self._active(indices))
@@ -653,6 +658,7 @@ class Case:
         dt = torch.bfloat16 if rng.random() < 0.5 else torch.float32
         srcs = {i: torch.zeros(self.numels[i], device="cuda", dtype=dt) for i in targets}
         srcs["multi"] = bool(rng.random() < 0.5)
+        srcs["fill"] = bool(rng.random() < 0.5)  # zero_grad with or without the fill
         print(f"  capture producer + adam from its sums {hp} indices={indices} "
               f"targets={targets} sources {dt}{' in bucket calls' if srcs['multi'] else ''}",
               flush=True)
@@ -672,35 +678,37 @@ class Case:
         print(f"  replay producer + adam {hp} indices={indices} targets={targets}", flush=True)
         self._producer_iteration(hp, indices, targets, srcs, graph=g)
 
-    def _zero_ref(self, none, idx):
+    def _zero_ref(self, none, idx, fill=True):
         if idx is None:
-            self.ref.zero_grad(set_to_none=none)
+            self.ref.zero_grad(set_to_none=none, fill=fill)
             return
         for i in idx:
-            self.ref.view("grad", i)[:] = 0
+            if fill:
+                self.ref.view("grad", i)[:] = 0
             if none:
                 self.ref.set_has_grad(i, False)
 
     def op_zero_graph(self):
-        """A captured zero_grad (all tensors or a subset, to zeros or to None).  Capturing it
-        changes nothing, neither the gradients nor the has-grad flags; each launch does what
-        the eager call does.  A subset is zeroed eagerly once first, since a capture cannot
-        build its work table."""
+        """A captured zero_grad (all tensors or a subset, to zeros or to None, to None with or
+        without the fill).  Capturing it changes nothing, neither the gradients nor the
+        has-grad flags; each launch does what the eager call does.  A subset is zeroed eagerly
+        once first, since a capture cannot build its work table."""
         if self.zero_graphs and (len(self.zero_graphs) >= 2 or self.rng.random() < 0.7):
-            g, none, idx = self.zero_graphs[int(self.rng.integers(0, len(self.zero_graphs)))]
-            print(f"  replay zero_grad(set_to_none={none}, indices={idx})", flush=True)
+            g, none, idx, fill = self.zero_graphs[int(self.rng.integers(0, len(self.zero_graphs)))]
+            print(f"  replay zero_grad(set_to_none={none}, indices={idx}, fill={fill})", flush=True)
             g.replay()
-            self._zero_ref(none, idx)
+            self._zero_ref(none, idx, fill)
             return
         none = bool(self.rng.integers(0, 2))
+        fill = not none or bool(self.rng.random() < 0.5)
         idx = None if self.rng.random() < 0.5 else self.pick_subset()
-        print(f"  capture zero_grad(set_to_none={none}, indices={idx})", flush=True)
+        print(f"  capture zero_grad(set_to_none={none}, indices={idx}, fill={fill})", flush=True)
         if idx is not None:
-            self.store.zero_grad(set_to_none=none, indices=idx)
-            self._zero_ref(none, idx)
+            self.store.zero_grad(set_to_none=none, indices=idx, fill=fill)
+            self._zero_ref(none, idx, fill)
         self.store.begin_capture()
-        self.store.zero_grad(set_to_none=none, indices=idx)
-        self.zero_graphs.append((self.store.end_capture(), none, idx))
+        self.store.zero_grad(set_to_none=none, indices=idx, fill=fill)
+        self.zero_graphs.append((self.store.end_capture(), none, idx, fill))
 
     OPS = [("grads_flat", 6), ("grad_one", 3), ("accumulate", 3), ("drop_grad", 2),
            ("zero_grad", 2), ("upload_weights", 1), ("adam", 6), ("sgd", 4), ("scaler", 1),

@@ -1413,11 +1413,24 @@ int ttp_get_has_grad(const ttp_ctx* c, uint32_t i, int* has) {
     return TTP_OK;
 }
 
+// set_to_none with TTP_ZERO_NO_FILL: flags only (the reference's grad = nullopt touches no
+// memory); without set_to_none it would leave present gradients unzeroed, so it is refused
+static int parse_zero_mode(int* set_to_none, bool* fill) {
+    *fill = (*set_to_none & TTP_ZERO_NO_FILL) == 0;
+    *set_to_none &= ~TTP_ZERO_NO_FILL;
+    if (!*fill && !*set_to_none)
+        return fail(TTP_ERR_INVALID, "TTP_ZERO_NO_FILL needs set_to_none: gradients that stay "
+                                     "present must be zeroed");
+    return TTP_OK;
+}
+
 int ttp_zero_grad(ttp_ctx* c, int set_to_none) {
     int rc = check_ctx(c);
     if (rc) return rc;
+    bool fill;
+    if ((rc = parse_zero_mode(&set_to_none, &fill))) return rc;
     if ((rc = set_dev(c))) return rc;
-    if ((rc = zero_device(c, c->grad, c->total * grad_esize(c)))) return rc;
+    if (fill && (rc = zero_device(c, c->grad, c->total * grad_esize(c)))) return rc;
     if (set_to_none) {
         for (uint32_t i = 0; i < (uint32_t)c->tensors.size(); ++i) set_grad_flag(c, i, false);
     }
@@ -1429,7 +1442,24 @@ int ttp_zero_grad_subset(ttp_ctx* c, const uint32_t* indices, uint32_t n, int se
     int rc = check_ctx(c);
     if (rc) return rc;
     if (n && !indices) return fail(TTP_ERR_INVALID, "null index list");
+    bool fill;
+    if ((rc = parse_zero_mode(&set_to_none, &fill))) return rc;
     if ((rc = set_dev(c))) return rc;
+    if (!fill) {  // flags only: the indices are checked here, no work table is needed
+        std::vector<uint8_t> seen(c->tensors.size(), 0);
+        for (uint32_t k = 0; k < n; ++k) {
+            if ((rc = check_index(c, indices[k]))) return rc;
+            if (seen[indices[k]])
+                return fail(TTP_ERR_INVALID,
+                            "tensor index " + std::to_string(indices[k]) + " listed twice");
+            seen[indices[k]] = 1;
+        }
+        for (uint32_t k = 0; k < n; ++k) {
+            set_grad_flag(c, indices[k], false);
+            set_fresh(c, indices[k], false);
+        }
+        return TTP_OK;
+    }
     static const uint32_t none = 0;
     const WorkTables* w;
     std::vector<uint32_t> active;

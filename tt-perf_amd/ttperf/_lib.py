@@ -22,6 +22,7 @@ HOST, DEVICE = 0, 1
 DTYPE_F32, DTYPE_BF16 = 0, 1
 ACCUM_SUMSQ = 0x100
 ACCUM_MULTI_MAX = 64  # tensors per ttp_accumulate_grad_multi call
+ZERO_NO_FILL = 0x100  # OR'd into zero_grad's set_to_none: flags only
 STEP_TENSOR_SUMS = 1
 STEP_DEFER_SCALE = 2
 KERNEL_NORM, KERNEL_UPDATE = 0, 1

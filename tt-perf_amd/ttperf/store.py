@@ -456,16 +456,19 @@ class ParamStore:
             raise RuntimeError("torch copied the buffer instead of wrapping it")
         return t.view(torch.bfloat16) if two else t
 
-    def zero_grad(self, set_to_none=True, indices=None):
+    def zero_grad(self, set_to_none=True, indices=None, fill=True):
         """Zero every grad (one fill), or only the listed tensors' grads (one launch);
         set_to_none also marks them as having no grad.  set_to_none=False leaves the has-grad
         flags alone, as torch's zero_grad(set_to_none=False) does: a tensor without a grad
-        stays without one (mark_grads() marks zeroed grads present)."""
+        stays without one (mark_grads() marks zeroed grads present).  fill=False (with
+        set_to_none): the flags only, as the reference's `grad = None` touches no memory; the
+        gradients keep their old contents until written (TTP_ZERO_NO_FILL)."""
+        mode = (1 if set_to_none else 0) | (0 if fill else L.ZERO_NO_FILL)
         if indices is None:
-            L.check(L.lib.ttp_zero_grad(self._h, 1 if set_to_none else 0))
+            L.check(L.lib.ttp_zero_grad(self._h, mode))
             return
         idx, n = self._index_array(indices)
-        L.check(L.lib.ttp_zero_grad_subset(self._h, idx, n, 1 if set_to_none else 0))
+        L.check(L.lib.ttp_zero_grad_subset(self._h, idx, n, mode))
 
     def accumulate_grad(self, index, value, sums=False):
         """Add an incoming gradient (numpy float32 / uint16 bf16 bits, or a torch float32 /
