@@ -660,7 +660,8 @@ class Case:
         srcs["multi"] = bool(rng.random() < 0.5)
         srcs["fill"] = bool(rng.random() < 0.5)  # zero_grad with or without the fill
         print(f"  capture producer + adam from its sums {hp} indices={indices} "
-              f"targets={targets} sources {dt}{' in bucket calls' if srcs['multi'] else ''}",
+              f"targets={targets} sources {dt}{' in bucket calls' if srcs['multi'] else ''}"
+              f"{'' if srcs['fill'] else ', zero_grad(fill=False)'}",
               flush=True)
         if self._conversion_refused(lambda: self.store.adam_step(indices=indices, **hp)):
             return
