@@ -987,31 +987,41 @@ __device__ __forceinline__ void zero_vec(uint16_t* g, uint64_t i, int n) {
     }
 }
 
-// The same accumulation over one tensor of n elements in 16 KiB norm tiles, one block per tile,
-// all of a lane's loads of a whole tile issued before its arithmetic (the grid-stride kernel
-// above, one element per lane per iteration, serves tensors of 2^24 or more tiles only).
+// The same accumulation over one tensor of n elements in 16 KiB norm tiles, one 64-lane block
+// per wave-share of a tile (kAccBlocksPerTile blocks per tile), all of a lane's loads of a whole
+// tile issued before its arithmetic (the grid-stride kernel above, one element per lane per
+// iteration, serves tensors of 2^24 or more tiles only).
 // kSums: it also computes the sum of squares of the resulting (stored) gradients, unscaled by
-// 1/scale when scaler_on: block b takes tile b (tiles start at the tensor's first element, as
-// the norm pass's tiles do), each lane the elements the norm pass's lane takes in that tile
-// (kNormLoads vectors of GradVec<GradT>::kElems), the squares go into the two accumulators in
-// the norm pass's order, and each wave's total (wave_sum, block_sum's first stage) is stored
-// as that tile's partial of that wave.  tile_from_waves then adds a tile's wave partials as
-// block_sum does, so the tile sums are bit-identical to norm_partials_kernel's over the same
-// gradients.  A wave's partial needs no LDS and no barrier (a block reduction lengthened each
-// launch by 0.6-2.4 us).  Block 0 marks the tensor's partials pending.  The squares come from
-// values already in registers, so the sums add no memory traffic.  kVecSrc: the source is
-// 16-byte aligned and read in vectors (else element by element).
+// 1/scale when scaler_on: tile t of the tensor (tiles start at its first element, as the norm
+// pass's tiles do) is split over kAccBlocksPerTile one-wave blocks, and each lane takes the
+// elements that lane `lane` (0..kBlock-1) of the norm pass takes in that tile (kNormLoads
+// vectors of GradVec<GradT>::kElems); the squares go into the two accumulators in the norm
+// pass's order, and each wave's total (wave_sum, block_sum's first stage) is stored as that
+// tile's partial of that wave.  tile_from_waves then adds a tile's wave partials as block_sum
+// does, so the tile sums are bit-identical to norm_partials_kernel's over the same gradients.
+// A wave's partial needs no LDS and no barrier (a block reduction lengthened each launch by
+// 0.6-2.4 us).  The first wave of tile 0 marks the tensor's partials pending.  The squares come
+// from values already in registers, so the sums add no memory traffic.
+// Measured on MI355X over GPT-2 124M's seven 25 MB buckets of bf16 gradients (assigned; each
+// source written just before its call, as a backward leaves it, or long before): one-wave
+// blocks against 256-lane ones 92-101 against 98-108 us with the sums (within 2% without);
+// non-temporal source loads against cached ones 83-97 against 94-110 us without the sums
+// (added onto the stored gradients: 126 against 132-154 us).  The source is read once.
+// kVecSrc: the source is 16-byte aligned and read in non-temporal vectors (else element by
+// element).
+constexpr uint32_t kAccLanes = 64;
+constexpr uint32_t kAccBlocksPerTile = kBlock / kAccLanes;
 template <int E, bool kVecSrc>
 __device__ __forceinline__ void ld_src(const uint16_t* p, float* out) {
     if constexpr (kVecSrc && E == 8) {
-        const u32x4 w = *reinterpret_cast<const u32x4*>(p);
+        const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             out[2 * j] = bf16_lo(w[j]);
             out[2 * j + 1] = bf16_hi(w[j]);
         }
     } else if constexpr (kVecSrc && E == 4) {
-        const u32x2 w = *reinterpret_cast<const u32x2*>(p);
+        const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
         out[0] = bf16_lo(w.x);
         out[1] = bf16_hi(w.x);
         out[2] = bf16_lo(w.y);
@@ -1026,7 +1036,7 @@ __device__ __forceinline__ void ld_src(const float* p, float* out) {
     if constexpr (kVecSrc) {
 #pragma unroll
         for (int h = 0; h < E / 4; ++h) {
-            const f32x4 w = *reinterpret_cast<const f32x4*>(p + 4 * h);
+            const f32x4 w = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + 4 * h));
 #pragma unroll
             for (int j = 0; j < 4; ++j) out[4 * h + j] = w[j];
         }
@@ -1036,15 +1046,17 @@ __device__ __forceinline__ void ld_src(const float* p, float* out) {
     }
 }
 
-// Tile `tile` of one tensor's gradients (grad, n elements) from src: the block's work in
-// both accumulate kernels.  inv: 1/scale for the sums; wave_sums: the tensor's run of the
-// store-wide wave partials; pending: its flag, which the block of its first tile sets.
+// Tile `tile` of one tensor's gradients (grad, n elements) from src, as the lanes
+// wave * 64 .. wave * 64 + 63 of a 256-lane tile: a one-wave block's work in both accumulate
+// kernels.  inv: 1/scale for the sums; wave_sums: the tensor's run of the store-wide wave
+// partials; pending: its flag, which the first wave of its first tile sets.
 template <typename SrcT, typename GradT, bool kVecSrc, bool kSums>
 __device__ __forceinline__ void accumulate_tile(GradT* __restrict__ grad,
                                                 const SrcT* __restrict__ src, uint64_t n,
                                                 int first, float inv, uint32_t tile,
-                                                double* __restrict__ wave_sums,
+                                                uint32_t wave, double* __restrict__ wave_sums,
                                                 uint32_t* __restrict__ pending) {
+    const uint32_t lane = wave * kAccLanes + threadIdx.x;  // the lane of a 256-lane tile
     typedef GradVec<GradT> GV;
     typedef typename GV::raw R;
     constexpr int E = GV::kElems;
@@ -1094,7 +1106,7 @@ __device__ __forceinline__ void accumulate_tile(GradT* __restrict__ grad,
         R w[kNormLoads];
 #pragma unroll
         for (int l = 0; l < kNormLoads; ++l) {
-            const uint64_t i = t0 + (uint32_t)(l * kBlock + threadIdx.x) * E;
+            const uint64_t i = t0 + (uint32_t)(l * kBlock + lane) * E;
             ld_src<E, kVecSrc>(src + i, in[l]);
             if (!first) w[l] = *reinterpret_cast<const R*>(grad + i);
         }
@@ -1102,14 +1114,14 @@ __device__ __forceinline__ void accumulate_tile(GradT* __restrict__ grad,
 #pragma unroll
         for (int l = 0; l < kNormLoads; ++l) {
             float v[E];
-            store_vec(t0 + (uint32_t)(l * kBlock + threadIdx.x) * E, in[l], w[l], v);
+            store_vec(t0 + (uint32_t)(l * kBlock + lane) * E, in[l], w[l], v);
             add_squares(v, (uint32_t)E);
         }
     } else {  // a tensor's last tile: the vectors (and elements) below its count
         const uint32_t count = (uint32_t)left;
 #pragma unroll
         for (int l = 0; l < kNormLoads; ++l) {
-            const uint32_t off = (uint32_t)(l * kBlock + threadIdx.x) * E;
+            const uint32_t off = (uint32_t)(l * kBlock + lane) * E;
             const uint32_t nv = off < count ? min(count - off, (uint32_t)E) : 0u;
             if (!nv) continue;
             const uint64_t i = t0 + off;
@@ -1140,25 +1152,28 @@ __device__ __forceinline__ void accumulate_tile(GradT* __restrict__ grad,
     if constexpr (kSums) {
         // each wave's total, the first stage of block_sum, with no LDS or barrier after it
         const double part = wave_sum(acc[0] + acc[1]);
-        if ((threadIdx.x & 63) == 0) wave_sums[(uint64_t)tile * kWaves + threadIdx.x / 64] = part;
-        if (tile == 0 && threadIdx.x == 0) *pending = 1u;
+        if (threadIdx.x == 0) wave_sums[(uint64_t)tile * kWaves + wave] = part;
+        if (tile == 0 && lane == 0) *pending = 1u;
     }
 }
 
-// one tensor per launch, one block per tile
+// one tensor per launch, kAccBlocksPerTile one-wave blocks per tile
 template <typename SrcT, typename GradT, bool kVecSrc, bool kSums>
-__global__ __launch_bounds__(kBlock) void accumulate_grad_tiles_kernel(
+__global__ __launch_bounds__(kAccLanes) void accumulate_grad_tiles_kernel(
     GradT* __restrict__ grad, const SrcT* __restrict__ src, uint64_t n, int first,
     const DevState* __restrict__ st, int32_t scaler_on, double* __restrict__ wave_sums,
     uint32_t* __restrict__ pending) {
     const float inv = (kSums && scaler_on) ? (float)(1.0 / (double)st->scale) : 1.0f;
-    accumulate_tile<SrcT, GradT, kVecSrc, kSums>(grad, src, n, first, inv, blockIdx.x, wave_sums,
+    accumulate_tile<SrcT, GradT, kVecSrc, kSums>(grad, src, n, first, inv,
+                                                 blockIdx.x / kAccBlocksPerTile,
+                                                 blockIdx.x % kAccBlocksPerTile, wave_sums,
                                                  pending);
 }
 
 // Several tensors per launch (a backward's bucket): the table travels in the kernel
 // arguments, so a call allocates and copies nothing and can be captured.  Tensor k takes
-// blocks [tile_end[k-1], tile_end[k]); its fields as in accumulate_grad_tiles_kernel.
+// tiles [tile_end[k-1], tile_end[k]) of the launch, kAccBlocksPerTile one-wave blocks each;
+// its fields as in accumulate_grad_tiles_kernel.
 constexpr uint32_t kMultiMax = 64;
 struct MultiAccArgs {
     uint32_t n;                      // tensors in the table (each with at least one element)
@@ -1172,24 +1187,25 @@ struct MultiAccArgs {
 };
 
 template <typename SrcT, typename GradT, bool kVecSrc, bool kSums>
-__global__ __launch_bounds__(kBlock) void accumulate_grads_multi_kernel(
+__global__ __launch_bounds__(kAccLanes) void accumulate_grads_multi_kernel(
     GradT* __restrict__ grad, const MultiAccArgs a, const DevState* __restrict__ st,
     int32_t scaler_on, double* __restrict__ wave_sums, uint32_t* __restrict__ pending) {
-    // the block's tensor: the first k with blockIdx.x < tile_end[k] (uniform in the block)
+    // the block's tensor: the first k with its tile g < tile_end[k] (uniform in the block)
+    const uint32_t g = blockIdx.x / kAccBlocksPerTile;
     uint32_t lo = 0, hi = a.n - 1;
     while (lo < hi) {
         const uint32_t mid = (lo + hi) >> 1;
-        if (blockIdx.x < a.tile_end[mid])
+        if (g < a.tile_end[mid])
             hi = mid;
         else
             lo = mid + 1;
     }
     const uint32_t k = lo;
-    const uint32_t tile = blockIdx.x - (k ? a.tile_end[k - 1] : 0u);
+    const uint32_t tile = g - (k ? a.tile_end[k - 1] : 0u);
     const float inv = (kSums && scaler_on) ? (float)(1.0 / (double)st->scale) : 1.0f;
     accumulate_tile<SrcT, GradT, kVecSrc, kSums>(
         grad + a.offset[k], static_cast<const SrcT*>(a.src[k]), a.numel[k],
-        (int)((a.first[k >> 5] >> (k & 31)) & 1u), inv, tile,
+        (int)((a.first[k >> 5] >> (k & 31)) & 1u), inv, tile, blockIdx.x % kAccBlocksPerTile,
         wave_sums + (uint64_t)a.tile_base[k] * kWaves, pending + a.tensor[k]);
 }
 

@@ -1539,10 +1539,11 @@ int ttp_accumulate_grad(ttp_ctx* c, uint32_t index, const void* src, uint64_t n,
         const uint64_t tiles = (n + norm_tile(c) - 1) / norm_tile(c);
         clear_hip_error();
         if (tiles < (1u << 24)) {
-            // one block per 16 KiB tile of the tensor's gradients (with_sums: their sums too)
+            // one-wave blocks, kAccBlocksPerTile per 16 KiB tile of the tensor's gradients
+            // (with_sums: their sums too); fewer than 2^26 blocks of 64 lanes
             const int32_t scaler_on = c->scaler.enabled ? 1 : 0;
             const bool vec = ((uintptr_t)dsrc & 15u) == 0;
-            const dim3 grid((uint32_t)tiles), block(ttp::kBlock);
+            const dim3 grid((uint32_t)tiles * ttp::kAccBlocksPerTile), block(ttp::kAccLanes);
             const DevState* st = c->st;
             double* ts = c->acc_tiles + (uint64_t)c->host_tile_base[index] * ttp::kWaves;
             uint32_t* pend = c->tsum_pending + index;
@@ -1656,7 +1657,7 @@ int ttp_accumulate_grad_multi(ttp_ctx* c, const uint32_t* indices, const void* c
     if (a.n) {
         const int32_t scaler_on = c->scaler.enabled ? 1 : 0;
         const bool mixed = c->mode == TTP_MODE_MIXED, bf16 = dtype == TTP_DTYPE_BF16;
-        const dim3 grid((uint32_t)tiles), block(ttp::kBlock);
+        const dim3 grid((uint32_t)tiles * ttp::kAccBlocksPerTile), block(ttp::kAccLanes);
         clear_hip_error();
 #define TTP_ACC_MULTI(S, G, V, SUMS)                                                          \
     hipLaunchKernelGGL((ttp::accumulate_grads_multi_kernel<S, G, V, SUMS>), grid, block, 0,   \
