@@ -1518,7 +1518,7 @@ int ttp_accumulate_grad(ttp_ctx* c, uint32_t index, const void* src, uint64_t n,
     if (kind == TTP_DEVICE &&
         (rc = check_device_buffer(c, src, n * sbytes, "the incoming gradient")))
         return rc;
-    // with its sum: one block per 16 KiB norm tile of the tensor's gradients
+    // with its sum: one tile sum per 16 KiB norm tile of the tensor's gradients
     const uint64_t ntiles = with_sums ? (n + norm_tile(c) - 1) / norm_tile(c) : 0;
     if (with_sums) {
         if (ntiles >= (1u << 24))
