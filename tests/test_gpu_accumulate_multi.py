@@ -128,7 +128,9 @@ def test_refused_multi_accumulates_change_nothing():
     """Raw C ABI calls the library refuses, each leaving the gradients and flags as they were:
     more than 64 tensors, an index listed twice, an unknown index, a host pointer, a null
     source for a tensor with elements, an unknown dtype; a call of none is a no-op.  The
-    refusal reasons come from the library's own checks, not from the binding."""
+    refusal reasons come from the library's own checks, not from the binding.  Through the
+    Python binding, an unknown index is the library's TTP_ERR_RANGE too, and a value of the
+    wrong size a ValueError before any call."""
     torch = torch_mod()
     from ttperf import _lib as L
     shapes = [(7,)] * 70
@@ -159,6 +161,15 @@ def test_refused_multi_accumulates_change_nothing():
         assert np.array_equal(store.download(L.BUF_GRAD), before), k
         assert [store.has_grad(i) for i in range(70)] == flags, k
     assert call([], []) == L.OK
+    # through the Python binding: an index out of range is the library's refusal
+    with pytest.raises(L.TTPError) as e:
+        store.accumulate_grads([3, 70], [srcs[3], srcs[4]])
+    assert e.value.code == L.ERR_RANGE
+    with pytest.raises(ValueError):  # a value of the wrong size
+        store.accumulate_grads([3, 4], [srcs[3], torch.zeros(8, device="cuda",
+                                                             dtype=torch.bfloat16)])
+    assert np.array_equal(store.download(L.BUF_GRAD), before)
+    assert [store.has_grad(i) for i in range(70)] == flags
     # 64 tensors is the limit, not an error
     store.accumulate_grads(list(range(64)), srcs[:64])
     assert all(store.has_grad(i) for i in range(64)) and not store.has_grad(64)

@@ -529,7 +529,10 @@ class ParamStore:
             raise ValueError("incoming gradients must be all float32 or all bfloat16")
         dtype = L.DTYPE_BF16 if dtypes == {torch.bfloat16} else L.DTYPE_F32
         for i, v in zip(indices, values):
-            if not (_is_torch(v) and v.is_cuda and v.is_contiguous()
+            # an index out of range is the library's to refuse (TTP_ERR_RANGE), as for a list
+            # that names a tensor twice
+            if 0 <= i < len(self.tensors) and not (
+                    _is_torch(v) and v.is_cuda and v.is_contiguous()
                     and v.numel() == self.tensors[i].numel):
                 raise ValueError(f"tensor {i}: a contiguous device tensor of "
                                  f"{self.tensors[i].numel} elements is needed")
