@@ -125,7 +125,10 @@ struct Value {
 // A backward's bucket of parameter gradients (ttp_accumulate_grad_multi, at most
 // TTP_ACCUM_MULTI_MAX per launch): params[k] receives incoming[k], device memory of one dtype
 // for all, exactly as params[k]->accumulate_grad_device(incoming[k], dtype, sums) would.  The
-// parameters belong to one arena; those without requires_grad are left out, as there.
+// parameters belong to one arena; those without requires_grad are left out, as there.  A
+// parameter listed twice and a null source of a non-empty parameter are refused before any
+// launch, as the library refuses them within one call; a longer list is several calls, and
+// one that the library refuses after another leaves the earlier calls' gradients in place.
 inline void accumulate_grads_device(const std::vector<ValuePtr>& params,
                                     const std::vector<const void*>& incoming, int dtype,
                                     bool sums = false) {
@@ -134,10 +137,16 @@ inline void accumulate_grads_device(const std::vector<ValuePtr>& params,
     if (params.empty()) return;
     std::vector<uint32_t> idx;
     std::vector<const void*> src;
+    std::vector<bool> seen(params[0]->arena->specs.size(), false);
     for (size_t k = 0; k < params.size(); ++k) {
         if (params[k]->arena != params[0]->arena)
             throw std::invalid_argument("accumulate_grads_device: parameters of one arena");
+        if (seen[params[k]->index])
+            throw std::invalid_argument("accumulate_grads_device: a parameter listed twice");
+        seen[params[k]->index] = true;
         if (!params[k]->requires_grad) continue;
+        if (!incoming[k] && params[k]->numel())
+            throw std::invalid_argument("accumulate_grads_device: a null source");
         idx.push_back(params[k]->index);
         src.push_back(incoming[k]);
     }

@@ -329,6 +329,25 @@ static void run_bucket_producer() {
                                           TTP_DTYPE_F32);
     } catch (const std::invalid_argument&) { thrown = true; }
     test::check(thrown, "bucket producer: parameters of two arenas are refused");
+    // a parameter listed twice, or a null source, is refused before any launch
+    const auto before = p2[0]->grad.value();
+    for (int c = 0; c < 2; ++c) {
+        thrown = false;
+        try {
+            if (c == 0)
+                autograd::accumulate_grads_device({p2[0], p2[1], p2[0]},
+                                                  {ps[0]->grad_ptr(), ps[1]->grad_ptr(),
+                                                   ps[0]->grad_ptr()},
+                                                  TTP_DTYPE_F32);
+            else
+                autograd::accumulate_grads_device({p2[0], p2[1]}, {ps[0]->grad_ptr(), nullptr},
+                                                  TTP_DTYPE_F32);
+        } catch (const std::invalid_argument&) { thrown = true; }
+        test::check(thrown, c == 0 ? "bucket producer: a parameter listed twice is refused"
+                                   : "bucket producer: a null source is refused");
+        test::assert_bits(p2[0]->grad.value(), before,
+                          "bucket producer: a refused list changes nothing");
+    }
 }
 
 // Saved step counts belong to the store they were saved for: a store created after another
