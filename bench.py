@@ -138,14 +138,22 @@ def traffic_from_profiles(config, optimizer):
 
 
 def cpu_model():
-    """The host CPU's model name (/proc/cpuinfo), or None."""
+    """The host CPU's model name (/proc/cpuinfo) with its family, model and stepping
+    numbers (a virtual machine may shorten the name to the vendor's brand), or None."""
+    fields = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if not line.strip():
+                break  # the first processor's block
+            key, _, val = line.partition(":")
+            fields.setdefault(key.strip(), val.strip())
     except OSError:
-        pass
-    return None
+        return None
+    name = fields.get("model name")
+    if name is None:
+        return None
+    ids = [f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields]
+    return f"{name} ({', '.join(ids)})" if ids else name
 
 
 def cpu_baseline(numels, flags, mode_mixed, grads_host, hp, seconds, scaler):
