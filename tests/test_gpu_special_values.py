@@ -123,7 +123,8 @@ def _check_report(r, e, scaler, norm_ran):
 
 
 @pytest.mark.parametrize("mode,opt,variant", CASES)
-def test_special_values_match_the_oracle(mode, opt, variant):
+def test_special_values_match_the_oracle(mode, opt, variant, tmp_path):
+    import ttperf
     from ttperf import _lib as L
     kind, hp = OPTS[opt]
     mixed = mode != "fp32"
@@ -188,6 +189,21 @@ def test_special_values_match_the_oracle(mode, opt, variant):
                 "master": "BUF_MASTER", "param": "BUF_PARAM", "exp_avg": "BUF_EXP_AVG",
                 "exp_avg_sq": "BUF_EXP_AVG_SQ", "momentum": "BUF_MOMENTUM"}[name])),
                 getattr(ref, name)[:total], mask)
+    # a checkpoint keeps every bit, NaN payloads included
+    path = tmp_path / "special.ttp"
+    store.save_state(path)
+    fresh = ttperf.ParamStore(SHAPES, mode="mixed" if mixed else "fp32", decay=DECAY,
+                              layout="sgd" if mode == "mixed_sgd_layout" else "default")
+    fresh.load_state(path)
+    assert fresh.step_count == store.step_count
+    if scaler:
+        assert fresh.scaler_state() == store.scaler_state()
+    for name in which:
+        buf = getattr(L, {"master": "BUF_MASTER", "param": "BUF_PARAM", "exp_avg": "BUF_EXP_AVG",
+                          "exp_avg_sq": "BUF_EXP_AVG_SQ", "momentum": "BUF_MOMENTUM"}[name])
+        a, b = store.download(buf)[mask], fresh.download(buf)[mask]
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"{name} after save / load"
+    fresh.close()
     got = store.download(L.BUF_MASTER)[mask]
     print(f"  final weights: {int(np.count_nonzero((got != 0) & (np.abs(got) < np.finfo(np.float32).tiny)))} "
           f"subnormal, {int(np.count_nonzero(~np.isfinite(got)))} non-finite", flush=True)
