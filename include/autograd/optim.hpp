@@ -116,9 +116,14 @@ struct Adam {
         if (!(betas.first > 0 && betas.first < 1 && betas.second > 0 && betas.second < 1))
             throw std::invalid_argument("betas must be in (0, 1)");
         if (!(weight_decay >= 0)) throw std::invalid_argument("weight_decay must be >= 0");
-        // an arena whose store does not exist yet is then created in Adam's layout
-        for (const auto& p : params)
+        // an arena whose store does not exist yet is then created in Adam's layout; a Bf16
+        // arena has no fp32 state for the moments
+        for (const auto& p : params) {
+            if (p && p->arena->mode == ttp::Mode::Bf16)
+                throw std::invalid_argument("Adam needs fp32 moments: a Bf16 arena holds bf16 "
+                                            "weights and gradients only; use a Mixed arena");
             if (p) p->arena->adam_declared = true;
+        }
         opts.lr = lr;
         opts.beta1 = betas.first;
         opts.beta2 = betas.second;

@@ -57,6 +57,8 @@ extern "C" {
 #endif
 
 /* ABI version, returned by ttp_abi_version().  Changes:
+ *   3  TTP_MODE_BF16 (the reference's own storage: bf16 weights and gradients, no fp32
+ *      state; plain SGD with its two bf16 roundings).  Nothing else changes.
  *   2  TTP_STORE_SGD (the SGD layout of a MIXED store, OR'd into ttp_create's mode);
  *      TTP_ACCUM_SUMSQ (ttp_accumulate_grad also stores the tensor's gradient sum);
  *      ttp_accumulate_grad_multi (several tensors' gradients in one launch);
@@ -67,7 +69,7 @@ extern "C" {
  *      ttp_accumulate_grad is refused unless an earlier call of the same capture set that
  *      tensor's has-grad flag.
  *   1  first version. */
-#define TTP_ABI_VERSION 2
+#define TTP_ABI_VERSION 3
 
 /* ---- status codes ---------------------------------------------------------------- */
 #define TTP_OK 0
@@ -81,6 +83,21 @@ extern "C" {
 /* ---- precision modes -------------------------------------------------------------- */
 #define TTP_MODE_FP32 0  /* fp32 params/grads; the param buffer is the master copy    */
 #define TTP_MODE_MIXED 1 /* bf16 params/grads + fp32 master; bf16 param = RNE(master) */
+/* TTP_MODE_BF16: bf16 weights (PARAM) and bf16 gradients (GRAD) and nothing else, the storage
+ * of the reference's C++ autograd, whose parameters and gradients are BFLOAT16 ttnn tensors
+ * (autograd/dynamic/autograd.hpp:72,88-99, autograd/traced/nn.hpp:24-35).  No fp32 master,
+ * moments or momentum: 4 B/param in all.  Its one update is the reference's plain SGD,
+ * `data = subtract(data, multiply(grad, lr))` (autograd/dynamic/optim.hpp:21-27,
+ * autograd/traced/ops.hpp:132-134, autograd/traced/nn.hpp:93-96), with the rounding of each
+ * ttnn op to bf16: update = RNE_bf16(g * lr), param = RNE_bf16(param - update), each product
+ * and difference formed in fp32 first (6 B/param moved per step, against 12 for MIXED SGD).
+ * Loss scaling and clipping apply to g before the product, as in the other modes.  Adam
+ * (every entry point), and SGD with momentum, dampening, nesterov or weight decay, need fp32
+ * state and are refused (TTP_ERR_INVALID, nothing changed); so are MASTER, EXP_AVG,
+ * EXP_AVG_SQ and MOMENTUM in ttp_buffer_ptr, ttp_buffer_layout, ttp_upload and ttp_download,
+ * and TTP_STORE_SGD.  A checkpoint holds the weights in its master buffer (each bf16 value
+ * widened to fp32, exactly), and loading it rounds them back. */
+#define TTP_MODE_BF16 2
 
 /* ---- store layout flags, OR'd into ttp_create's mode -------------------------------- */
 /* TTP_STORE_SGD: the SGD layout of a MIXED store.  By default a MIXED store keeps each
@@ -106,8 +123,8 @@ extern "C" {
 #define TTP_STORE_SGD 0x100
 
 /* ---- buffers of the flat store ---------------------------------------------------- */
-#define TTP_BUF_PARAM 0      /* model-facing weights: fp32 (FP32) or bf16 (MIXED)       */
-#define TTP_BUF_GRAD 1       /* gradients: fp32 (FP32) or bf16 (MIXED)                  */
+#define TTP_BUF_PARAM 0      /* model-facing weights: fp32 (FP32) or bf16 (MIXED, BF16) */
+#define TTP_BUF_GRAD 1       /* gradients: fp32 (FP32) or bf16 (MIXED, BF16)            */
 #define TTP_BUF_MASTER 2     /* fp32 master weights (same memory as PARAM in FP32 mode) */
 #define TTP_BUF_EXP_AVG 3    /* Adam first moment m, fp32                               */
 #define TTP_BUF_EXP_AVG_SQ 4 /* Adam second moment v, fp32                              */
@@ -221,7 +238,7 @@ typedef struct ttp_step_report {
 
 /* ---- context lifetime --------------------------------------------------------------- */
 int ttp_device_count(int* count);
-/* mode: TTP_MODE_FP32 or TTP_MODE_MIXED, optionally | TTP_STORE_SGD. */
+/* mode: TTP_MODE_FP32, TTP_MODE_MIXED (optionally | TTP_STORE_SGD) or TTP_MODE_BF16. */
 int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n_tensors, int mode,
                ttp_ctx** out);
 int ttp_destroy(ttp_ctx* ctx);
@@ -421,7 +438,8 @@ int ttp_scaler_update(ttp_ctx* ctx);
  * failed save leaves an earlier file at `path` as it was.  ttp_load_state requires the same
  * mode and tensor table (numel and flags), and loss-scaler values in the ranges that
  * ttp_scaler_configure and ttp_scaler_set accept; a buffer the file lacks is zeroed; the bf16
- * weights are recomputed from the master.  It reads the whole file and checks its size and
+ * weights are recomputed from the master (a TTP_MODE_BF16 store saves its bf16 weights as the
+ * master, widened exactly, and loads them back).  It reads the whole file and checks its size and
  * checksum before it changes the context, so a damaged, truncated or mismatched file is
  * rejected with the context unchanged (only an I/O error on the second read, or a file
  * replaced during the call, can leave it partly loaded).  While graphs of the context are

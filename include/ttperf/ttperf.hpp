@@ -29,7 +29,10 @@ inline void check(int rc) {
     throw std::runtime_error(msg);
 }
 
-enum class Mode { FP32 = TTP_MODE_FP32, Mixed = TTP_MODE_MIXED };
+// Bf16: the reference C++ autograd's own storage, bf16 weights and gradients and no fp32
+// state; plain SGD only, each op rounded to bf16 as the reference's ttnn ops round theirs
+// (TTP_MODE_BF16).
+enum class Mode { FP32 = TTP_MODE_FP32, Mixed = TTP_MODE_MIXED, Bf16 = TTP_MODE_BF16 };
 // Store layout of a Mixed store (TTP_STORE_SGD): Default keeps master, m and v in shared
 // records (Adam's layout); Sgd keeps a contiguous master and no m / v, for stores that SGD
 // steps (the first Adam step converts it to Default).  FP32 stores are laid out alike either
@@ -168,6 +171,7 @@ public:
     Mode mode() const { return mode_; }
     // Sgd while a Mixed store keeps the SGD layout's contiguous master (until an Adam step)
     Layout layout() const {
+        if (mode_ == Mode::Bf16) return Layout::Default;  // no master to lay out
         void* base = nullptr;
         uint32_t group = 0, stride = 0;
         check(ttp_buffer_layout(ctx_, TTP_BUF_MASTER, &base, &group, &stride));
@@ -178,12 +182,19 @@ public:
     uint64_t numel(uint32_t i) const { return specs_.at(i).numel(); }
 
     // ---- data -------------------------------------------------------------------------------
-    // fp32 weights of tensor i: the master copy (and its bf16 RNE copy in Mixed mode)
+    // fp32 weights of tensor i: the master copy (and its bf16 RNE copy in Mixed mode); in
+    // Bf16 mode the bf16 weights, rounded to nearest even
     void set_weights(uint32_t i, const std::vector<float>& w) {
+        if (mode_ == Mode::Bf16) {
+            std::vector<uint16_t> h(w.size());
+            for (size_t k = 0; k < w.size(); ++k) h[k] = to_bf16(w[k]);
+            check(ttp_upload(ctx_, TTP_BUF_PARAM, i, h.data(), h.size(), TTP_HOST));
+            return;
+        }
         check(ttp_upload(ctx_, TTP_BUF_MASTER, i, w.data(), w.size(), TTP_HOST));
     }
     std::vector<float> master(uint32_t i) const { return download_f32(TTP_BUF_MASTER, i); }
-    // model-facing weights widened to float (bf16 in Mixed mode)
+    // model-facing weights widened to float (bf16 in Mixed and Bf16 mode)
     std::vector<float> weights(uint32_t i) const {
         if (mode_ == Mode::FP32) return download_f32(TTP_BUF_PARAM, i);
         return widen(download_u16(TTP_BUF_PARAM, i));
@@ -191,7 +202,7 @@ public:
     std::vector<uint16_t> weights_bf16(uint32_t i) const { return download_u16(TTP_BUF_PARAM, i); }
     std::vector<float> state(int which, uint32_t i) const { return download_f32(which, i); }
 
-    // gradients: fp32 values (rounded to bf16 in Mixed mode, round-to-nearest-even)
+    // gradients: fp32 values (rounded to bf16 in Mixed and Bf16 mode, round-to-nearest-even)
     void set_grad(uint32_t i, const std::vector<float>& g) {
         if (mode_ == Mode::FP32) {
             check(ttp_upload(ctx_, TTP_BUF_GRAD, i, g.data(), g.size(), TTP_HOST));

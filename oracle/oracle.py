@@ -20,6 +20,7 @@ _LIB_PATH = os.path.join(_HERE, "build", "libttp_oracle.so")
 
 MODE_FP32 = 0
 MODE_MIXED = 1
+MODE_BF16 = 2  # bf16 weights (param) and grads only: plain SGD with bf16 roundings
 DECAY = 1
 DEFER_SCALE = 2  # ORC_STEP_DEFER_SCALE
 ALIGN = 64  # elements; the engine's tensor alignment
@@ -150,8 +151,8 @@ class OracleStore:
             self._tensors[i].numel = self.numels[i]
             self._tensors[i].flags = self.flags[i]
             self._tensors[i].has_grad = 0
-        self.master = np.zeros(tot, np.float32)
-        if mode == MODE_MIXED:
+        self.master = np.zeros(tot, np.float32)  # unused by a BF16 store
+        if mode in (MODE_MIXED, MODE_BF16):
             self.param = np.zeros(tot, np.uint16)
             self.grad = np.zeros(tot, np.uint16)
         else:
@@ -194,7 +195,7 @@ class OracleStore:
             self.view("param", i)[:] = bf16_rne(self.view("master", i))
 
     def set_grad(self, i, g):
-        """g: float32 values (FP32) or uint16 bf16 bits (MIXED)."""
+        """g: float32 values (FP32) or uint16 bf16 bits (MIXED, BF16)."""
         dst = self.view("grad", i)
         dst[:] = np.asarray(g).ravel().astype(dst.dtype, copy=False)
         self._tensors[i].has_grad = 1

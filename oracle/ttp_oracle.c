@@ -152,7 +152,7 @@ static chunk_t* build_chunks(const orc_store* s, uint64_t* nc_out) {
 }
 
 static inline float load_grad(const orc_store* s, uint64_t i) {
-    return s->mode == ORC_MODE_MIXED ? orc_bf16_to_f32(((const uint16_t*)s->grad)[i])
+    return s->mode != ORC_MODE_FP32 ? orc_bf16_to_f32(((const uint16_t*)s->grad)[i])
                                      : ((const float*)s->grad)[i];
 }
 
@@ -188,7 +188,7 @@ void orc_accumulate_grad(orc_store* s, uint32_t index, const void* src, int src_
     for (uint64_t k = 0; k < t->numel; ++k) {
         const float in = src_bf16 ? orc_bf16_to_f32(((const uint16_t*)src)[k]) : ((const float*)src)[k];
         const uint64_t i = t->offset + k;
-        if (s->mode == ORC_MODE_MIXED) {
+        if (s->mode != ORC_MODE_FP32) {
             uint16_t* g = (uint16_t*)s->grad;
             g[i] = orc_bf16_rne(first ? in : orc_bf16_to_f32(g[i]) + in);
         } else {
@@ -304,7 +304,7 @@ static void step_epilogue(orc_store* s, int found_inf, int defer, orc_report* re
 }
 
 int orc_adam_step(orc_store* s, const orc_adam_hp* hp, orc_report* rep) {
-    if (adam_validate(hp)) return -1;
+    if (adam_validate(hp) || s->mode == ORC_MODE_BF16) return -1;
     if (!s->exp_avg || !s->exp_avg_sq) return -5;
     orc_report local;
     orc_report* r = rep ? rep : &local;
@@ -349,7 +349,7 @@ static float* tmp_alloc(uint64_t n) { return (float*)malloc(sizeof(float) * (n ?
     } while (0)
 
 int orc_adam_step_opbyop(orc_store* s, const orc_adam_hp* hp, orc_report* rep) {
-    if (adam_validate(hp)) return -1;
+    if (adam_validate(hp) || s->mode == ORC_MODE_BF16) return -1;
     if (!s->exp_avg || !s->exp_avg_sq) return -5;
     orc_report local;
     orc_report* r = rep ? rep : &local;
@@ -444,9 +444,21 @@ static inline void sgd_elem(float* pp, float g, float* bp, const sgd_coefs* c, i
     *pp = p - update;
 }
 
+/* autograd/dynamic/optim.hpp:24-25 on the reference's BFLOAT16 tensors
+ * (autograd/dynamic/autograd.hpp:72, autograd/traced/nn.hpp:24-35): each ttnn op writes a
+ * bf16 tensor, so multiply(grad, lr) and subtract(data, update) each round their fp32 result
+ * to bf16 (round to nearest even) */
+static inline uint16_t sgd_bf16_elem(uint16_t p, float g, const sgd_coefs* c) {
+    if (c->use_inv) g = g * c->inv_scale;
+    if (c->use_clip) g = g * c->clip;
+    const float update = orc_bf16_to_f32(orc_bf16_rne(g * c->lr)); /* multiply(grad, lr) */
+    return orc_bf16_rne(orc_bf16_to_f32(p) - update);               /* subtract(data, .) */
+}
+
 int orc_sgd_step(orc_store* s, const orc_sgd_hp* hp, orc_report* rep) {
     /* py/optim.py:9-10 (lr > 0); torch.optim.SGD for the rest */
     if (!(hp->lr > 0) || !(hp->momentum >= 0) || !(hp->weight_decay >= 0)) return -1;
+    if (s->mode == ORC_MODE_BF16 && (hp->momentum != 0.0 || hp->weight_decay != 0.0)) return -1;
     if (hp->nesterov && (hp->momentum <= 0 || hp->dampening != 0)) return -1;
     const int mom_on = hp->momentum != 0.0;
     if (mom_on && (!s->momentum || !s->mom_init)) return -5;
@@ -478,6 +490,11 @@ int orc_sgd_step(orc_store* s, const orc_sgd_hp* hp, orc_report* rep) {
             const int decay = (ch[k].flags & ORC_DECAY) != 0;
             const int first = mom_on ? !s->mom_init[ch[k].tensor] : 0;
             for (uint64_t i = ch[k].begin; i < ch[k].end; ++i) {
+                if (s->mode == ORC_MODE_BF16) {
+                    uint16_t* pb = (uint16_t*)s->param;
+                    pb[i] = sgd_bf16_elem(pb[i], load_grad(s, i), &c);
+                    continue;
+                }
                 sgd_elem(&s->master[i], load_grad(s, i), mom_on ? &s->momentum[i] : NULL, &c,
                          decay, first);
                 if (mixed) ((uint16_t*)s->param)[i] = orc_bf16_rne(s->master[i]);

@@ -37,6 +37,10 @@ extern "C" {
 
 #define ORC_MODE_FP32 0
 #define ORC_MODE_MIXED 1
+/* bf16 weights (param) and bf16 grads only, the reference C++ autograd's BFLOAT16 tensors
+ * (autograd/dynamic/autograd.hpp:72): master, moments and momentum are not used; the only
+ * step is plain SGD with each ttnn op rounded to bf16 (see orc_sgd_step) */
+#define ORC_MODE_BF16 2
 #define ORC_DECAY 1u
 
 typedef struct orc_tensor {
@@ -51,8 +55,8 @@ typedef struct orc_store {
     uint32_t n_tensors;
     const orc_tensor* tensors;
     uint64_t total;        /* elements per flat buffer */
-    void* param;           /* float* (FP32) or uint16_t* bf16 bits (MIXED) */
-    void* grad;            /* float* (FP32) or uint16_t* bf16 bits (MIXED) */
+    void* param;           /* float* (FP32) or uint16_t* bf16 bits (MIXED, BF16) */
+    void* grad;            /* float* (FP32) or uint16_t* bf16 bits (MIXED, BF16) */
     float* master;         /* == param in FP32 mode */
     float* exp_avg;
     float* exp_avg_sq;
@@ -130,7 +134,9 @@ double orc_grad_sumsq(const orc_store* s, float inv_scale, int32_t* found_inf);
  * grad type); src is float (src_bf16 = 0) or bf16 bits (src_bf16 = 1). */
 void orc_accumulate_grad(orc_store* s, uint32_t index, const void* src, int src_bf16);
 
-/* one optimizer step over the store (fused: one pass per element) */
+/* one optimizer step over the store (fused: one pass per element).  A BF16 store takes plain
+ * SGD only (momentum and weight decay 0; Adam returns -1): param = RNE_bf16(param -
+ * RNE_bf16(g * lr)), the two bf16 roundings of `subtract(data, multiply(grad, lr))`. */
 int orc_adam_step(orc_store* s, const orc_adam_hp* hp, orc_report* rep);
 int orc_sgd_step(orc_store* s, const orc_sgd_hp* hp, orc_report* rep);
 /* the same Adam step executed op by op as py/optim.py:76-86 issues it: every op is a

@@ -273,6 +273,22 @@ def gen_reference_known_answers():
     grad_b = xb.t() @ torch.ones(32, 32, dtype=torch.bfloat16)
     w_ref = w - 0.1 * grad_b
     out.update(sgd1_w0=bf16_bits(w), sgd1_grad=bf16_bits(grad_b), sgd1_w1=bf16_bits(w_ref))
+    # tests/sgd_optimizer.py:42-78 — two bf16 steps through tanh, each `weight - 0.1 * grad_w`
+    # with grad_w from the current weights; the gradients of both steps are kept so that a
+    # step can be checked on its own inputs
+    x, w = _linear_init(22, 32, 32)
+    xb = x.to(torch.bfloat16)
+
+    def bf16_tanh_grad(weight):
+        z = torch.tanh(xb @ weight)
+        return xb.transpose(-2, -1) @ (torch.ones_like(z) * (1 - z * z))
+
+    g1 = bf16_tanh_grad(w)
+    w1 = w - 0.1 * g1
+    g2 = bf16_tanh_grad(w1)
+    w2 = w1 - 0.1 * g2
+    out.update(sgd2_w0=bf16_bits(w), sgd2_g1=bf16_bits(g1), sgd2_w1=bf16_bits(w1),
+               sgd2_g2=bf16_bits(g2), sgd2_w2=bf16_bits(w2))
     np.savez(os.path.join(OUT, "reference_known_answers.npz"), **out)
 
 

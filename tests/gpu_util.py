@@ -18,12 +18,14 @@ def torch_mod():
 
 
 def make_pair(shapes, decay, mode, init_std=0.02, seed=0, init="normal", layout="default"):
-    """GPU store + oracle store holding identical fp32 master weights.  layout="sgd": a mixed
-    store in the SGD layout (contiguous master, no m / v until an Adam step converts it)."""
+    """GPU store + oracle store holding identical fp32 master weights (a BF16 store: identical
+    bf16 weights, the seeded values rounded to nearest even).  layout="sgd": a mixed store in
+    the SGD layout (contiguous master, no m / v until an Adam step converts it)."""
     import ttperf
     from ttperf import _lib as L
     torch = torch_mod()
-    store = ttperf.ParamStore(shapes, mode="mixed" if mode == O.MODE_MIXED else "fp32",
+    store = ttperf.ParamStore(shapes, mode={O.MODE_MIXED: "mixed", O.MODE_FP32: "fp32",
+                                            O.MODE_BF16: "bf16"}[mode],
                               decay=decay, layout=layout)
     store.set_stream(torch.cuda.current_stream())
     numels = [t.numel for t in store.tensors]
@@ -44,6 +46,11 @@ def make_pair(shapes, decay, mode, init_std=0.02, seed=0, init="normal", layout=
             flat[o:o + t.numel].fill_(1.0)
         else:
             flat[o:o + t.numel].normal_(0.0, init_std, generator=g)
+    if mode == O.MODE_BF16:
+        w = flat.to(torch.bfloat16)
+        store.upload(L.BUF_PARAM, L.ALL_TENSORS, w)
+        ref.param[:store.total] = w.view(torch.int16).cpu().numpy().view(np.uint16)
+        return store, ref
     store.upload(L.BUF_MASTER, L.ALL_TENSORS, flat)
     # the oracle's arrays hold at least one element (an all-empty table has total 0)
     ref.master[:store.total] = flat.cpu().numpy()
@@ -61,7 +68,7 @@ def pad_mask(store):
 
 def device_grads(store, gen, std, scale=1.0, heavy_frac=0.0, heavy_std=1.0, inf_at=None,
                  into=None):
-    """Seeded N(0, std) * scale grads on the device (bf16 in MIXED), written into the store;
+    """Seeded N(0, std) * scale grads on the device (bf16 in MIXED and BF16), written into the store;
     returns the host copy (uint16 bits or float32) for the oracle.  into: an oracle's grad
     array, which receives the copy directly (no host temporary of the store's size, which at
     billions of elements costs more than the step under test); its first store.total elements
@@ -76,17 +83,17 @@ def device_grads(store, gen, std, scale=1.0, heavy_frac=0.0, heavy_std=1.0, inf_
     if inf_at is not None:
         g[inf_at] = float("inf")
     from ttperf import _lib as L
-    if store.mode == L.MODE_MIXED:
+    if store.mode != L.MODE_FP32:
         g = g.to(torch.bfloat16)
     store.upload(L.BUF_GRAD, L.ALL_TENSORS, g)
     if into is not None:
-        bits = store.mode == L.MODE_MIXED
+        bits = store.mode != L.MODE_FP32
         assert into.dtype == (np.uint16 if bits else np.float32) and len(into) >= store.total
         dst = torch.from_numpy(into.view(np.int16) if bits else into)[:store.total]
         dst.copy_(g.view(torch.int16) if bits else g)
         return into[:store.total]
     host = g.cpu()
-    if store.mode == L.MODE_MIXED:
+    if store.mode != L.MODE_FP32:
         return host.view(torch.int16).numpy().view(np.uint16)
     return host.numpy()
 

@@ -45,12 +45,16 @@ def test_ceiling_probe_library_exports_its_entry_points():
 
 
 def test_abi_version():
-    """The library, the header and the ctypes binding agree on the ABI version (2: the SGD
-    layout flag, and the has-grad behaviour of zero_grad_subset / captured accumulates)."""
+    """The library, the header and the ctypes binding agree on the ABI version (3: the BF16
+    store mode; 2: the SGD layout flag, and the has-grad behaviour of zero_grad_subset /
+    captured accumulates), and on the mode and flag values."""
     from ttperf import _lib as L
     text = open(HEADER).read()
     header = int(re.search(r"#define TTP_ABI_VERSION (\d+)", text).group(1))
-    assert L.lib.ttp_abi_version() == header == L.ABI_VERSION == 2
+    assert L.lib.ttp_abi_version() == header == L.ABI_VERSION == 3
+    for name in ("FP32", "MIXED", "BF16"):
+        assert int(re.search(r"#define TTP_MODE_%s (\d+)" % name, text).group(1)) == \
+            getattr(L, "MODE_" + name)
     assert int(re.search(r"#define TTP_STORE_SGD (0x[0-9a-fA-F]+)", text).group(1), 16) == \
         L.STORE_SGD
     assert int(re.search(r"#define TTP_ACCUM_SUMSQ (0x[0-9a-fA-F]+)", text).group(1), 16) == \

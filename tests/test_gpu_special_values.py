@@ -17,7 +17,8 @@ division and square root see subnormal and infinite operands.
 
 Every store mode (fp32, mixed in the default layout, mixed in the SGD layout) and optimizer
 form (AdamW, Adam with L2 decay and eps = 1e-30, the reference's plain SGD, Nesterov SGD with
-decay) runs three steps with and without clipping at 1.0.  After every step the weights, the
+decay) runs three steps with and without clipping at 1.0; so does a BF16 store (bf16 weights
+and gradients only) with the reference's plain SGD, each op rounded to bf16.  After every step the weights, the
 bf16 copies and the optimizer state must equal the oracle's bit for bit, except that two NaNs
 count as equal whatever their sign and payload (x86 and the GPU produce different default
 NaNs; the bf16 conversion maps every NaN to 0x7FC0 on both).  The step reports must agree
@@ -69,6 +70,10 @@ VARIANTS = ["finite", "finite_clip", "nonfinite", "nonfinite_clip", "scaled", "s
 MODES = ["fp32", "mixed", "mixed_sgd_layout"]
 CASES = [(m, o, v) for m in MODES for o in OPTS for v in VARIANTS
          if m != "fp32" or not v.startswith("scaled")]
+# a BF16 store (bf16 weights and grads only) steps plain SGD, each op rounded to bf16
+CASES += [("bf16", "sgd", v) for v in VARIANTS]
+STORE_MODE = {"fp32": O.MODE_FP32, "mixed": O.MODE_MIXED, "mixed_sgd_layout": O.MODE_MIXED,
+              "bf16": O.MODE_BF16}
 
 
 def _mix(rng, total, mask, specials, ordinary):
@@ -130,7 +135,7 @@ def test_special_values_match_the_oracle(mode, opt, variant, tmp_path):
     mixed = mode != "fp32"
     seed = 7000 + CASES.index((mode, opt, variant))
     print(f"case {mode} {opt} {variant} seed {seed}", flush=True)
-    store, ref = make_pair(SHAPES, DECAY, O.MODE_MIXED if mixed else O.MODE_FP32, seed=seed,
+    store, ref = make_pair(SHAPES, DECAY, STORE_MODE[mode], seed=seed,
                            layout="sgd" if mode == "mixed_sgd_layout" else "default")
     rng = np.random.default_rng(seed)
     mask = pad_mask(store)
@@ -142,11 +147,16 @@ def test_special_values_match_the_oracle(mode, opt, variant, tmp_path):
     # weights (non-finite ones too in the non-finite variants), m and v
     wspec = np.concatenate([F32_FINITE, F32_NONFINITE]) if nonfinite else F32_FINITE
     master = _mix(rng, total, mask, wspec, _normal_f32(0.02))
-    store.upload(L.BUF_MASTER, L.ALL_TENSORS, master)
-    ref.master[:total] = master
-    if mixed:
+    if mode == "bf16":  # the weights themselves are bf16: the values rounded, ties included
+        store.upload(L.BUF_PARAM, L.ALL_TENSORS, O.bf16_rne(master))
         ref.param[:total] = O.bf16_rne(master)
-    which = ["master"] + (["param"] if mixed else [])
+        which = ["param"]
+    else:
+        store.upload(L.BUF_MASTER, L.ALL_TENSORS, master)
+        ref.master[:total] = master
+        if mixed:
+            ref.param[:total] = O.bf16_rne(master)
+        which = ["master"] + (["param"] if mixed else [])
     if kind == "adam":
         m = _mix(rng, total, mask, F32_FINITE, _normal_f32(1e-3))
         v = np.abs(_mix(rng, total, mask, F32_FINITE, _normal_f32(1e-3)))
@@ -192,7 +202,8 @@ def test_special_values_match_the_oracle(mode, opt, variant, tmp_path):
     # a checkpoint keeps every bit, NaN payloads included
     path = tmp_path / "special.ttp"
     store.save_state(path)
-    fresh = ttperf.ParamStore(SHAPES, mode="mixed" if mixed else "fp32", decay=DECAY,
+    fresh = ttperf.ParamStore(SHAPES, mode={"mixed_sgd_layout": "mixed"}.get(mode, mode),
+                              decay=DECAY,
                               layout="sgd" if mode == "mixed_sgd_layout" else "default")
     fresh.load_state(path)
     assert fresh.step_count == store.step_count
@@ -204,7 +215,9 @@ def test_special_values_match_the_oracle(mode, opt, variant, tmp_path):
         a, b = store.download(buf)[mask], fresh.download(buf)[mask]
         assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"{name} after save / load"
     fresh.close()
-    got = store.download(L.BUF_MASTER)[mask]
+    got = store.download(L.BUF_PARAM if mode == "bf16" else L.BUF_MASTER)[mask]
+    if mode == "bf16":
+        got = O.bf16_to_f32(got)
     print(f"  final weights: {int(np.count_nonzero((got != 0) & (np.abs(got) < np.finfo(np.float32).tiny)))} "
           f"subnormal, {int(np.count_nonzero(~np.isfinite(got)))} non-finite", flush=True)
     store.close()

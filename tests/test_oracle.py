@@ -150,6 +150,104 @@ def test_sgd_bf16_known_answer():
     np.testing.assert_allclose(got, O.bf16_to_f32(d["sgd1_w1"]).ravel(), atol=5e-2, rtol=5e-2)
 
 
+# ---------------------------------------------------------------------------- BF16 stores
+def test_sgd_bf16_store_reproduces_the_reference_test_formulas_exactly():
+    # tests/sgd_optimizer.py:15-39 and :42-78 compute their expected weights with torch on
+    # bf16 tensors, `w - 0.1 * grad`: the product and the difference each rounded to bf16.
+    # A BF16 store reproduces them bit for bit (its grads are the fixtures' own), over one
+    # step and over two steps of the tanh model; the fp32-master store only within tolerance.
+    d = golden("reference_known_answers.npz")
+    st = O.OracleStore([1024], mode=O.MODE_BF16)
+    st.param[:1024] = d["sgd1_w0"].ravel()
+    st.set_grad(0, d["sgd1_grad"].ravel())
+    st.sgd_step(lr=0.1)
+    assert np.array_equal(st.view("param", 0), d["sgd1_w1"].ravel())
+    st = O.OracleStore([1024], mode=O.MODE_BF16)
+    st.param[:1024] = d["sgd2_w0"].ravel()
+    for g, w in (("sgd2_g1", "sgd2_w1"), ("sgd2_g2", "sgd2_w2")):
+        st.set_grad(0, d[g].ravel())
+        st.sgd_step(lr=0.1)
+        assert np.array_equal(st.view("param", 0), d[w].ravel()), w
+    mixed = O.OracleStore([1024], mode=O.MODE_MIXED)
+    mixed.set_master(0, O.bf16_to_f32(d["sgd1_w0"].ravel()))
+    mixed.set_grad(0, d["sgd1_grad"].ravel())
+    mixed.sgd_step(lr=0.1)
+    assert not np.array_equal(mixed.view("param", 0), d["sgd1_w1"].ravel())
+
+
+def test_sgd_bf16_store_bias_known_answer():
+    # autograd/tests/test_sgd.cpp:45-70 on the reference's bf16 tensors: grad 32 at lr 0.01
+    # gives the update RNE_bf16(0.32) = 0.3203125, so the bias goes to -0.3203125, then to
+    # RNE_bf16(-0.640625) = -0.640625 (within the test's 0.1 of -0.32 and -0.64)
+    st = O.OracleStore([32], mode=O.MODE_BF16)
+    for want in (-0.3203125, -0.640625):
+        st.set_grad(0, O.bf16_rne(np.full(32, 32.0, np.float32)))
+        st.sgd_step(lr=0.01)
+        assert np.all(O.bf16_to_f32(st.view("param", 0)) == np.float32(want))
+
+
+def _rne_rational(x, neg, sig_bits):
+    """x (a Fraction, exact) rounded to nearest, ties to even, in a binary format with
+    `sig_bits` significant bits and fp32's exponent range below (subnormals from 2^-126 down;
+    no overflow in the cases used).  Returns (value, negative) so that zeros keep a sign."""
+    from fractions import Fraction
+    if x == 0:
+        return Fraction(0), neg
+    negative = x < 0
+    a = -x if negative else x
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    q = Fraction(2) ** (max(e, -126) - (sig_bits - 1))
+    n, rem = divmod(a, q)
+    if 2 * rem > q or (2 * rem == q and n % 2 == 1):
+        n += 1
+    r = n * q
+    return (-r if negative else r), negative
+
+
+def _bf16_of(v):
+    value, negative = v
+    f = np.float32(float(value)) if value != 0 else np.float32(-0.0 if negative else 0.0)
+    return int(f.view(np.uint32) >> 16)
+
+
+def test_sgd_bf16_store_against_exact_rational_rounding():
+    # Every finite bf16 weight below 2^126 in magnitude, stepped with a few (grad, lr) pairs,
+    # against exact rational arithmetic rounded by an independent nearest-even routine: the
+    # product g*lr rounded to fp32, then to bf16 (multiply's result), the difference rounded
+    # to fp32, then to bf16 (subtract's).  The signs of zero follow IEEE: an exact zero
+    # difference is +0 unless both operands are -0 and +0; an underflowing product or
+    # difference keeps its sign.
+    from fractions import Fraction
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    vals = O.bf16_to_f32(bits)
+    keep = np.isfinite(vals) & (np.abs(vals) < 2.0 ** 126)
+    bits, vals = bits[keep], vals[keep]
+    for g_f, lr in ((32.0, 0.01), (-3.140625, 1e-3), (2.0 ** -100, 0.1), (0.0078125, 3e-5)):
+        g_bits = int(O.bf16_rne(np.array([g_f], np.float32))[0])
+        st = O.OracleStore([len(bits)], mode=O.MODE_BF16, nthreads=8)
+        st.param[:len(bits)] = bits
+        st.set_grad(0, np.full(len(bits), g_bits, np.uint16))
+        st.sgd_step(lr=lr)
+        got = st.view("param", 0)
+        g = Fraction(float(O.bf16_to_f32(np.array([g_bits], np.uint16))[0]))
+        lr32 = Fraction(float(np.float32(lr)))
+        prod_neg = (g < 0) != (lr32 < 0)
+        u = _rne_rational(*_rne_rational(g * lr32, prod_neg, 24), 8)
+        u_val, u_neg = u
+        want = np.empty(len(bits), np.uint16)
+        for k, (b, v) in enumerate(zip(bits, vals)):
+            p_neg = bool(int(b) >> 15)
+            d = Fraction(float(v)) - u_val
+            # exact zero: -0 - (+0) is -0, every other zero difference +0
+            d_neg = (d < 0) or (d == 0 and p_neg and not u_neg and v == 0 and u_val == 0)
+            want[k] = _bf16_of(_rne_rational(*_rne_rational(d, d_neg, 24), 8))
+        bad = np.flatnonzero(got != want)
+        assert bad.size == 0, (g_f, lr, [(hex(int(bits[i])), hex(int(got[i])), hex(int(want[i])))
+                                         for i in bad[:5]])
+
+
 # ---------------------------------------------------------------------------- torch goldens
 def _adam_run(d, **hp):
     return run_torch_fixture(d, lambda st: st.adam_step(**hp))[1]

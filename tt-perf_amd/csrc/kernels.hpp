@@ -944,6 +944,118 @@ __global__ __launch_bounds__(kLanes) void sgd_lane_kernel(const GradT* __restric
     }
 }
 
+// ------------------------------------------------------------------------------------
+// plain SGD of a TTP_MODE_BF16 store: bf16 weights updated in place, no fp32 state
+// ------------------------------------------------------------------------------------
+// The value of x rounded to bf16 (round to nearest even; NaN -> the quiet NaN 0x7FC0).
+__device__ __forceinline__ float bf16_round(float x) {
+    return __uint_as_float(bf16_rne(x) << 16);
+}
+
+// One element: the grad transforms, then autograd/dynamic/optim.hpp:24-25 on bf16 tensors,
+// each ttnn op's result rounded to bf16: update = multiply(grad, lr), data = subtract(data,
+// update).  Product and difference are formed in fp32 and rounded from there.
+__device__ __forceinline__ float sgd_bf16_elem(float p, float g, float lr, float inv, float clip,
+                                               bool use_inv, bool use_clip) {
+    if (use_inv) g = g * inv;
+    if (use_clip) g = g * clip;
+    const float update = bf16_round(g * lr);  // autograd/dynamic/optim.hpp:24
+    return bf16_round(p - update);            // autograd/dynamic/optim.hpp:25
+}
+
+// kE (2, 4 or 8) bf16 values at p as fp32: one 4-, 8- or 16-byte word (non-temporal: the
+// weights are read once and rewritten)
+template <int kE>
+__device__ __forceinline__ void ld_bf16_lane(const uint16_t* p, float* out) {
+    static_assert(kE == 2 || kE == 4 || kE == 8, "2, 4 or 8 elements per lane");
+    if constexpr (kE == 2) {
+        const uint32_t w = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+        out[0] = bf16_lo(w);
+        out[1] = bf16_hi(w);
+    } else if constexpr (kE == 4) {
+        const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+        out[0] = bf16_lo(w.x);
+        out[1] = bf16_hi(w.x);
+        out[2] = bf16_lo(w.y);
+        out[3] = bf16_hi(w.y);
+    } else {
+        const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            out[2 * j] = bf16_lo(w[j]);
+            out[2 * j + 1] = bf16_hi(w[j]);
+        }
+    }
+}
+// kE gradients as fp32 (ordinary loads, as ld_grad_lane)
+template <int kE>
+__device__ __forceinline__ void ld_grad_bf16_lane(const uint16_t* g, float* out) {
+    if constexpr (kE <= 4) {
+        ld_grad_lane<kE>(g, 0, out);
+    } else {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(g);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            out[2 * j] = bf16_lo(w[j]);
+            out[2 * j + 1] = bf16_hi(w[j]);
+        }
+    }
+}
+// the first n (1..kE) of kE values already rounded to bf16: one word when n == kE
+template <int kE>
+__device__ __forceinline__ void st_bf16_rounded_lane(uint16_t* p, const float* v, int n) {
+    if (n == kE) {
+        if constexpr (kE == 2) {
+            __builtin_nontemporal_store(bf16_pack(v[0], v[1]), reinterpret_cast<uint32_t*>(p));
+        } else if constexpr (kE == 4) {
+            __builtin_nontemporal_store(u32x2{bf16_pack(v[0], v[1]), bf16_pack(v[2], v[3])},
+                                        reinterpret_cast<u32x2*>(p));
+        } else {
+            __builtin_nontemporal_store(u32x4{bf16_pack(v[0], v[1]), bf16_pack(v[2], v[3]),
+                                              bf16_pack(v[4], v[5]), bf16_pack(v[6], v[7])},
+                                        reinterpret_cast<u32x4*>(p));
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < kE - 1; ++j)
+            if (j < n) p[j] = (uint16_t)bf16_rne(v[j]);
+    }
+}
+
+// The plain SGD update of a BF16 store, launched and shaped as the other lane forms (one
+// block per 1/lane_parts of a chunk, the last chunks first): 6 B per element (gradient and
+// weight read, weight written).  A lane's kE elements start at a multiple of kE and tensors
+// start on 64-element boundaries, so the whole-word loads of a tensor's last lane stay inside
+// its footprint; only its first n values are stored.  a.st must be valid.
+template <int kE, int kLanes, int kIt>
+__global__ __launch_bounds__(kLanes) void sgd_bf16_lane_kernel(const uint16_t* __restrict__ grad,
+                                                               uint16_t* __restrict__ param,
+                                                               SgdArgs a, uint64_t part0) {
+    constexpr uint32_t kPiece = kLanes * kE;
+    constexpr uint32_t kP = lane_parts<kE, kLanes, kIt>();
+    const uint64_t r = (uint64_t)a.nchunks * kP - 1 - (part0 + blockIdx.x);
+    const Chunk ch = load_chunk(a.chunks, r / kP);
+    const DevState* st = a.st;
+    const bool run = ((a.flags & kCheckSkip) == 0) | (st->skip == 0);  // see adam_lane_kernel
+    const uint32_t off = (uint32_t)(r % kP) * (kPiece * kIt) + threadIdx.x * kE;
+    if (!(run & (off < ch.count))) return;
+    const bool use_inv = a.flags & kUseInv, use_clip = a.flags & kUseClip;
+    const float inv = st->inv_scale, clip = st->clip_coef;
+#pragma unroll 1
+    for (int q = 0; q < kIt; ++q) {
+        const uint32_t o = off + q * kPiece;
+        if (o >= ch.count) break;
+        const uint64_t i = ch.begin + o;
+        float g[kE], p[kE];
+        ld_grad_bf16_lane<kE>(grad + i, g);
+        ld_bf16_lane<kE>(param + i, p);
+#pragma unroll
+        for (int j = 0; j < kE; ++j)
+            p[j] = sgd_bf16_elem(p[j], g[j], a.lr, inv, clip, use_inv, use_clip);
+        st_bf16_rounded_lane<kE>(param + i, p, (int)min(ch.count - o, (uint32_t)kE));
+    }
+}
+
 // after a momentum step: mark the stepped tensors' buffers as initialised (unless skipped)
 __global__ __launch_bounds__(kBlock) void mark_mom_init_kernel(const Chunk* chunks, uint32_t n,
                                                                uint32_t* mom_init,

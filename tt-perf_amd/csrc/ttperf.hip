@@ -246,7 +246,9 @@ struct ttp_graph {
 
 namespace {
 
-size_t grad_esize(const ttp_ctx* c) { return c->mode == TTP_MODE_MIXED ? 2 : 4; }
+// MIXED and BF16 stores hold bf16 gradients (and bf16 weights in PARAM); FP32 stores fp32
+bool bf16_grads(const ttp_ctx* c) { return c->mode != TTP_MODE_FP32; }
+size_t grad_esize(const ttp_ctx* c) { return bf16_grads(c) ? 2 : 4; }
 
 // The step count (bias-correction t) lives on the device while loss scaling is on (the
 // device decides whether a step is skipped) and once the context has been captured (a
@@ -257,11 +259,20 @@ int no_capture(const ttp_ctx* c, const char* what) {
     if (!c->capturing) return TTP_OK;
     return fail(TTP_ERR_STATE, std::string(what) + " is not allowed while capturing a graph");
 }
-size_t param_esize(const ttp_ctx* c) { return c->mode == TTP_MODE_MIXED ? 2 : 4; }
+size_t param_esize(const ttp_ctx* c) { return bf16_grads(c) ? 2 : 4; }
 
 uint32_t norm_tile(const ttp_ctx* c) {
-    return c->mode == TTP_MODE_MIXED ? ttp::norm_tile_elems<uint16_t>()
-                                     : ttp::norm_tile_elems<float>();
+    return bf16_grads(c) ? ttp::norm_tile_elems<uint16_t>() : ttp::norm_tile_elems<float>();
+}
+
+// A TTP_MODE_BF16 store holds its bf16 weights (PARAM) and gradients (GRAD) and no fp32
+// state: the other buffers, and every call that would create them, are refused.
+int bf16_store_refuses(const ttp_ctx* c, const char* what) {
+    if (c->mode != TTP_MODE_BF16) return TTP_OK;
+    return fail(TTP_ERR_INVALID, std::string(what) +
+                                     ": a TTP_MODE_BF16 store holds bf16 weights and gradients "
+                                     "only (no fp32 master, moments or momentum); create the "
+                                     "store TTP_MODE_MIXED for fp32 optimizer state");
 }
 
 // pieces of <= `piece` elements of each listed non-empty tensor, in tensor order
@@ -426,6 +437,7 @@ int ensure_adam_state(ttp_ctx* c) {
     // here (the master's values move unchanged, the bf16 weights stay as they are).
     if (c->exp_avg) return TTP_OK;
     int rc;
+    if ((rc = bf16_store_refuses(c, "Adam's m and v"))) return rc;
     if ((rc = no_capture(c, "first Adam step (allocates m, v)"))) return rc;
     if (c->mode == TTP_MODE_MIXED && c->sgd_layout) {
         if (c->n_graphs)
@@ -462,6 +474,7 @@ int ensure_adam_state(ttp_ctx* c) {
 
 int ensure_momentum(ttp_ctx* c) {
     int rc;
+    if ((rc = bf16_store_refuses(c, "the momentum buffer"))) return rc;
     if (!c->momentum && (rc = no_capture(c, "first momentum step (allocates the buffer)"))) return rc;
     if (!c->momentum && (rc = alloc_zero(c, (void**)&c->momentum, c->total * 4))) return rc;
     return TTP_OK;
@@ -696,6 +709,9 @@ constexpr int kLaneSgdPlainMixed = 2, kLanesSgdPlainMixed = 256, kItSgdPlainMixe
 // no difference to the ranking).
 constexpr int kLaneSgdPlainContig = 4, kLanesSgdPlainContig = 64, kItSgdPlainContig = 1;
 constexpr int kLaneSgdMomContig = 2, kLanesSgdMomContig = 128, kItSgdMomContig = 1;
+// Plain SGD of a BF16 store (bf16 gradients and weights, 6 B per element): eight elements per
+// lane, one 16-byte word per stream as the 64-lane copy moves them.
+constexpr int kLaneSgdBf16 = 8, kLanesSgdBf16 = 64, kItSgdBf16 = 1;
 // FP32 SGD without momentum (fp32 gradients and weights, 12 B per element), the same program
 // and method (124M / 774M / 1558M, x the 64-lane copy, back to back / after a gradient
 // copy): 2 x 256 x 2 0.993 / 0.976, 1.003 / 1.013, 1.001 / 1.018 (4x256x1 0.97-0.99,
@@ -765,7 +781,7 @@ int launch_prologue(ttp_ctx* c, const WorkTables* w, bool run_norm, double max_n
     if (!partials) partials = c->partials;
     if (run_norm && !from_sums) {
         clear_hip_error();
-        if (c->mode == TTP_MODE_MIXED)
+        if (bf16_grads(c))
             launch_norm_pass<uint16_t>(c, w, ns, scaler_on, partials);
         else
             launch_norm_pass<float>(c, w, ns, scaler_on, partials);
@@ -916,6 +932,15 @@ int check_buffer_id(int which) {
     return TTP_OK;
 }
 
+// a buffer id the context holds (or creates on first use): a BF16 store, PARAM and GRAD only
+int check_buffer_in_mode(const ttp_ctx* c, int which) {
+    int rc = check_buffer_id(which);
+    if (rc) return rc;
+    if (which != TTP_BUF_PARAM && which != TTP_BUF_GRAD)
+        return bf16_store_refuses(c, ("buffer " + std::to_string(which)).c_str());
+    return TTP_OK;
+}
+
 // Allocates the optimizer state a buffer id names (m, v or the momentum) on first use; in the
 // SGD layout, m and v convert the store.  Callers validate everything else first, so that a
 // refused call neither allocates nor converts.
@@ -965,9 +990,17 @@ int ensure_staging(ttp_ctx* c, uint64_t bytes) {
 constexpr uint64_t kPieceElems = 16ull << 20;
 
 // slot elements [first, first + n) of record-stored buffer `which` -> contiguous device array
+// (a BF16 store's checkpoint master: its bf16 weights, widened exactly)
 int gather_slot(ttp_ctx* c, int which, uint64_t first, uint64_t n, float* dst) {
     if (!n) return TTP_OK;
     clear_hip_error();
+    if (c->mode == TTP_MODE_BF16 && which == TTP_BUF_MASTER) {
+        hipLaunchKernelGGL(ttp::bf16_to_master_kernel, dim3(elementwise_grid(c, n)),
+                           dim3(ttp::kBlock), 0, c->stream, (const uint16_t*)c->param + first,
+                           dst, ttp::kRec, (uint64_t)0, n);
+        HIP_TRY(hipGetLastError());
+        return TTP_OK;
+    }
     hipLaunchKernelGGL(ttp::gather_slot_kernel, dim3(elementwise_grid(c, n)), dim3(ttp::kBlock),
                        0, c->stream, (const float*)buffer_base(c, which),
                        buffer_stride(c, which), first, n, dst);
@@ -977,8 +1010,19 @@ int gather_slot(ttp_ctx* c, int which, uint64_t first, uint64_t n, float* dst) {
 
 // contiguous device array (null: zeros) -> slot elements [first, first + n); an upload of
 // MIXED-mode master weights also writes their bf16 copy
+// (a BF16 store's checkpoint master: rounded to its bf16 weights, exactly for values that
+// came from bf16)
 int scatter_slot(ttp_ctx* c, int which, uint64_t first, uint64_t n, const float* src) {
     if (!n) return TTP_OK;
+    if (c->mode == TTP_MODE_BF16 && which == TTP_BUF_MASTER) {
+        if (!src) return fail(TTP_ERR_STATE, "a BF16 store's weights cannot be zeroed here");
+        clear_hip_error();
+        hipLaunchKernelGGL(ttp::master_to_bf16_kernel, dim3(elementwise_grid(c, n)),
+                           dim3(ttp::kBlock), 0, c->stream, src, ttp::kRec,
+                           (uint16_t*)c->param + first, (uint64_t)0, n);
+        HIP_TRY(hipGetLastError());
+        return TTP_OK;
+    }
     uint16_t* p16 = (c->mode == TTP_MODE_MIXED && which == TTP_BUF_MASTER) ? (uint16_t*)c->param
                                                                           : nullptr;
     clear_hip_error();
@@ -1035,7 +1079,7 @@ void release(ttp_ctx* c) {
     for (void* p : c->retired) (void)hipFree(p);
     // MIXED: param is the bf16 copy and master lives in `records` (in the SGD layout, in an
     // allocation of its own); FP32: param == master
-    if (c->mode == TTP_MODE_MIXED && c->param) (void)hipFree(c->param);
+    if (c->mode != TTP_MODE_FP32 && c->param) (void)hipFree(c->param);
     if ((c->mode == TTP_MODE_FP32 || c->sgd_layout) && c->master) (void)hipFree(c->master);
     for (auto& v : c->ev)
         for (auto& p : v) {
@@ -1072,9 +1116,12 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
     if (n && !descs) return fail(TTP_ERR_INVALID, "null tensor table");
     const bool sgd_layout = (mode & TTP_STORE_SGD) != 0;
     mode &= ~TTP_STORE_SGD;
-    if (mode != TTP_MODE_FP32 && mode != TTP_MODE_MIXED)
-        return fail(TTP_ERR_INVALID, "mode must be TTP_MODE_FP32 or TTP_MODE_MIXED, optionally "
-                                     "| TTP_STORE_SGD");
+    if (mode != TTP_MODE_FP32 && mode != TTP_MODE_MIXED && mode != TTP_MODE_BF16)
+        return fail(TTP_ERR_INVALID, "mode must be TTP_MODE_FP32, TTP_MODE_MIXED (optionally "
+                                     "| TTP_STORE_SGD) or TTP_MODE_BF16");
+    if (mode == TTP_MODE_BF16 && sgd_layout)
+        return fail(TTP_ERR_INVALID, "TTP_STORE_SGD is a layout of a TTP_MODE_MIXED store's "
+                                     "fp32 master; a TTP_MODE_BF16 store has none");
     // per-tensor kernels launch one 256-lane block per tensor: fewer than 2^32 work-items
     if (n >= (1u << 24)) return fail(TTP_ERR_INVALID, "too many tensors (max 2^24 - 1)");
     // the table must describe a store that fits one GPU: the padded footprint sum cannot
@@ -1155,6 +1202,9 @@ int ttp_create(int device, const ttp_tensor_desc* descs, uint32_t n, int mode, t
         c->master = c->records;
         c->exp_avg = c->records + ttp::kRec;
         c->exp_avg_sq = c->records + 2 * ttp::kRec;
+        if ((rc = alloc_zero(c, &c->param, c->total * 2))) return bail(rc);
+    } else if (mode == TTP_MODE_BF16) {
+        // the bf16 weights alone: no master, no records
         if ((rc = alloc_zero(c, &c->param, c->total * 2))) return bail(rc);
     } else {
         if ((rc = alloc_zero(c, (void**)&c->master, c->total * 4))) return bail(rc);
@@ -1289,7 +1339,7 @@ int ttp_buffer_ptr(ttp_ctx* c, int which, uint32_t index, void** ptr) {
     int rc = check_ctx(c);
     if (rc) return rc;
     if (!ptr) return fail(TTP_ERR_INVALID, "null output");
-    if ((rc = check_buffer_id(which))) return rc;
+    if ((rc = check_buffer_in_mode(c, which))) return rc;
     // m and v live in records in both modes (and are refused before they would be allocated)
     if (which == TTP_BUF_EXP_AVG || which == TTP_BUF_EXP_AVG_SQ || in_records(c, which))
         return fail(TTP_ERR_STATE,
@@ -1308,6 +1358,7 @@ int ttp_buffer_ptr(ttp_ctx* c, int which, uint32_t index, void** ptr) {
 int ttp_buffer_layout(ttp_ctx* c, int which, void** base, uint32_t* group, uint32_t* stride) {
     int rc = check_ctx(c);
     if (rc) return rc;
+    if ((rc = check_buffer_in_mode(c, which))) return rc;
     if ((rc = set_dev(c))) return rc;
     if ((rc = materialize(c, which))) return rc;
     if (base) *base = buffer_base(c, which);
@@ -1322,7 +1373,7 @@ int ttp_upload(ttp_ctx* c, int which, uint32_t index, const void* src, uint64_t 
     if (kind == TTP_HOST && (rc = no_capture(c, "an upload from host memory"))) return rc;
     if (!src && n) return fail(TTP_ERR_INVALID, "null source");
     if (kind != TTP_HOST && kind != TTP_DEVICE) return fail(TTP_ERR_INVALID, "bad memory kind");
-    if ((rc = check_buffer_id(which))) return rc;
+    if ((rc = check_buffer_in_mode(c, which))) return rc;
     if ((rc = set_dev(c))) return rc;
     uint64_t off, cnt;
     if ((rc = resolve_range(c, index, n, &off, &cnt))) return rc;
@@ -1373,7 +1424,7 @@ int ttp_download(ttp_ctx* c, int which, uint32_t index, void* dst, uint64_t n, i
     if (kind == TTP_HOST && (rc = no_capture(c, "a download to host memory"))) return rc;
     if (!dst && n) return fail(TTP_ERR_INVALID, "null destination");
     if (kind != TTP_HOST && kind != TTP_DEVICE) return fail(TTP_ERR_INVALID, "bad memory kind");
-    if ((rc = check_buffer_id(which))) return rc;
+    if ((rc = check_buffer_in_mode(c, which))) return rc;
     if ((rc = set_dev(c))) return rc;
     uint64_t off, cnt;
     if ((rc = resolve_range(c, index, n, &off, &cnt))) return rc;
@@ -1467,7 +1518,7 @@ int ttp_zero_grad_subset(ttp_ctx* c, const uint32_t* indices, uint32_t n, int se
     if (w->n_chunks) {
         const uint32_t grid = std::min(w->n_chunks, kMaxGridBlocks);  // grid-stride kernel
         clear_hip_error();
-        if (c->mode == TTP_MODE_MIXED)
+        if (bf16_grads(c))
             hipLaunchKernelGGL(ttp::zero_chunks_kernel<uint16_t>, dim3(grid), dim3(ttp::kUpdBlock),
                                0, c->stream, (uint16_t*)c->grad, w->chunks, w->n_chunks);
         else
@@ -1535,7 +1586,7 @@ int ttp_accumulate_grad(ttp_ctx* c, uint32_t index, const void* src, uint64_t n,
             dsrc = c->staging;
         }
         const int first = t.has_grad ? 0 : 1;
-        const bool mixed = c->mode == TTP_MODE_MIXED, bf16 = dtype == TTP_DTYPE_BF16;
+        const bool mixed = bf16_grads(c), bf16 = dtype == TTP_DTYPE_BF16;
         const uint64_t tiles = (n + norm_tile(c) - 1) / norm_tile(c);
         clear_hip_error();
         if (tiles < (1u << 24)) {
@@ -1656,7 +1707,7 @@ int ttp_accumulate_grad_multi(ttp_ctx* c, const uint32_t* indices, const void* c
     }
     if (a.n) {
         const int32_t scaler_on = c->scaler.enabled ? 1 : 0;
-        const bool mixed = c->mode == TTP_MODE_MIXED, bf16 = dtype == TTP_DTYPE_BF16;
+        const bool mixed = bf16_grads(c), bf16 = dtype == TTP_DTYPE_BF16;
         const dim3 grid((uint32_t)tiles * ttp::kAccBlocksPerTile), block(ttp::kAccLanes);
         clear_hip_error();
 #define TTP_ACC_MULTI(S, G, V, SUMS)                                                          \
@@ -1699,6 +1750,7 @@ static int adam_step_impl(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
     const bool noalloc = scratch_partials != nullptr;
     int rc = check_ctx(c);
     if (rc) return rc;
+    if ((rc = bf16_store_refuses(c, "an Adam step"))) return rc;
     if (!hp) return fail(TTP_ERR_INVALID, "null hyperparameters");
     // py/optim.py:33-41
     if (!(hp->lr > 0)) return fail(TTP_ERR_INVALID, "lr must be > 0");
@@ -1831,6 +1883,11 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
     if (hp->nesterov && (hp->momentum <= 0 || hp->dampening != 0))
         return fail(TTP_ERR_INVALID, "nesterov needs momentum > 0 and zero dampening");
     if (hp->flags & ~kStepFlags) return fail(TTP_ERR_INVALID, "unknown step flags");
+    if (c->mode == TTP_MODE_BF16 && (hp->momentum != 0.0 || hp->weight_decay != 0.0))
+        return fail(TTP_ERR_INVALID, "a TTP_MODE_BF16 store steps plain SGD only (the "
+                                     "reference's `data - lr * grad` in bf16): momentum and "
+                                     "weight decay need fp32 state; create the store "
+                                     "TTP_MODE_MIXED for them");
     if (report && (rc = no_capture(c, "a step report (synchronises)"))) return rc;
     if ((rc = set_dev(c))) return rc;
     const bool mom = hp->momentum != 0.0;
@@ -1884,7 +1941,14 @@ static int sgd_step_impl(ttp_ctx* c, const ttp_sgd_hparams* hp, const uint32_t* 
         hipLaunchKernelGGL((ttp::sgd_lane_kernel<GT, MIXED, MS, E, LN, IT>), g, dim3(LN), 0,  \
                            c->stream, G, c->master, c->momentum, P16, al, p0);                \
     })
-        if (c->mode == TTP_MODE_MIXED && c->sgd_layout && !mom)
+        if (c->mode == TTP_MODE_BF16)
+            launch_lanes(c, (uint64_t)n * ttp::lane_parts<kLaneSgdBf16, kLanesSgdBf16, kItSgdBf16>(),
+                         kLanesSgdBf16, [&](dim3 g, uint64_t p0) {
+                hipLaunchKernelGGL((ttp::sgd_bf16_lane_kernel<kLaneSgdBf16, kLanesSgdBf16,
+                                                              kItSgdBf16>),
+                                   g, dim3(kLanesSgdBf16), 0, c->stream, g16, p16, al, p0);
+            });
+        else if (c->mode == TTP_MODE_MIXED && c->sgd_layout && !mom)
             TTP_SGD_LANES(uint16_t, true, ttp::kRec, kLaneSgdPlainContig, kLanesSgdPlainContig,
                           kItSgdPlainContig, g16, p16);
         else if (c->mode == TTP_MODE_MIXED && c->sgd_layout)
@@ -1955,6 +2019,7 @@ int ttp_adam_step_noalloc(ttp_ctx* c, const ttp_adam_hparams* hp, const uint32_t
     int rc = check_ctx(c);
     if (rc) return rc;
     if (n && !indices) return fail(TTP_ERR_INVALID, "null index list");
+    if ((rc = bf16_store_refuses(c, "an Adam step"))) return rc;
     if ((rc = set_dev(c))) return rc;
     // The device's scratch array is shared by every context: an eager step on another stream
     // than the last one's first waits for that step's event (host calls on one device are
@@ -2022,7 +2087,7 @@ int ttp_grad_sumsq_tensors(ttp_ctx* c, const uint32_t* indices, uint32_t n) {
         // block per tensor over its run of tiles
         const int32_t scaler_on = c->scaler.enabled ? 1 : 0;
         clear_hip_error();
-        if (c->mode == TTP_MODE_MIXED)
+        if (bf16_grads(c))
             hipLaunchKernelGGL((ttp::norm_partials_kernel<uint16_t, false>), dim3(w->n_tiles),
                                dim3(ttp::kBlock), 0, c->stream, (const uint16_t*)c->grad,
                                w->tiles, 0u, w->n_tiles, (const DevState*)c->st, scaler_on,

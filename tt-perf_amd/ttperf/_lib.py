@@ -12,9 +12,9 @@ LIB_PATH = os.environ.get("TTPERF_LIB", os.path.join(_PKG, "lib", "libttperf_hip
 
 OK = 0
 ERR_INVALID, ERR_NO_DEVICE, ERR_HIP, ERR_OOM, ERR_STATE, ERR_RANGE = -1, -2, -3, -4, -5, -6
-MODE_FP32, MODE_MIXED = 0, 1
+MODE_FP32, MODE_MIXED, MODE_BF16 = 0, 1, 2
 STORE_SGD = 0x100
-ABI_VERSION = 2
+ABI_VERSION = 3
 BUF_PARAM, BUF_GRAD, BUF_MASTER, BUF_EXP_AVG, BUF_EXP_AVG_SQ, BUF_MOMENTUM = range(6)
 ALL_TENSORS = 0xFFFFFFFF
 TENSOR_DECAY = 1

@@ -28,6 +28,13 @@ def _bf16_bits_to_f32(h):
     return (np.asarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
+def _f32_to_bf16_bits(x):
+    """float32 values -> bf16 bit patterns, rounded to nearest even (NaN -> 0x7FC0)."""
+    u = np.ascontiguousarray(x, np.float32).ravel().view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(np.isnan(np.asarray(x, np.float32).ravel()), np.uint16(0x7FC0), r)
+
+
 class Tensor:
     """A parameter: a view of one tensor of a ParamStore.
 
@@ -74,9 +81,9 @@ class Tensor:
 
     # ---- data ----------------------------------------------------------------------------
     def numpy(self):
-        """Model-facing weights as float32 (bf16 widened in MIXED mode)."""
+        """Model-facing weights as float32 (bf16 widened in MIXED and BF16 mode)."""
         x = self.store.download(L.BUF_PARAM, self.index)
-        if self.store.mode == L.MODE_MIXED:
+        if self.store.mode != L.MODE_FP32:
             x = _bf16_bits_to_f32(x)
         return x.reshape(self.shape)
 
@@ -84,7 +91,11 @@ class Tensor:
         return self.store.download(L.BUF_MASTER, self.index).reshape(self.shape)
 
     def set_data(self, value):
-        """fp32 values -> master (and the bf16 copy in MIXED mode)."""
+        """fp32 values -> master (and the bf16 copy in MIXED mode); in BF16 mode, the bf16
+        weights (rounded to nearest even)."""
+        if self.store.mode == L.MODE_BF16:
+            self.store.upload(L.BUF_PARAM, self.index, _f32_to_bf16_bits(value))
+            return
         self.store.upload(L.BUF_MASTER, self.index, value)
 
     def data_ptr(self, which=L.BUF_PARAM):
@@ -106,7 +117,7 @@ class GradView:
 
     def numpy(self):
         x = self.p.store.download(L.BUF_GRAD, self.p.index)
-        if self.p.store.mode == L.MODE_MIXED:
+        if self.p.store.mode != L.MODE_FP32:
             x = _bf16_bits_to_f32(x)
         return x.reshape(self.p.shape)
 
@@ -209,8 +220,10 @@ class ParamStore:
     """One context: tensors laid out 64-element aligned in caller order.
 
     shapes : list of shapes (tuples) or element counts
-    mode   : "fp32" (fp32 params/grads, params are the master copy) or
-             "mixed" (bf16 params/grads + fp32 master, m, v)
+    mode   : "fp32" (fp32 params/grads, params are the master copy),
+             "mixed" (bf16 params/grads + fp32 master, m, v) or
+             "bf16" (bf16 params/grads only, the reference C++ autograd's tensors: plain SGD
+             with each op rounded to bf16; Adam and SGD with momentum or decay refuse)
     decay  : per-tensor bools (weight decay applies), default: tensors with >= 2 dims
     layout : "default", or "sgd": a mixed store for SGD, with a contiguous fp32 master and no
              m / v (TTP_STORE_SGD; the first Adam step converts it to the default layout)
@@ -219,11 +232,11 @@ class ParamStore:
     def __init__(self, shapes, *, mode="fp32", decay=None, names=None, device=0,
                  layout="default"):
         shapes = [tuple(s) if isinstance(s, (tuple, list)) else (int(s),) for s in shapes]
-        if mode not in ("fp32", "mixed"):
-            raise ValueError("mode must be 'fp32' or 'mixed'")
+        if mode not in ("fp32", "mixed", "bf16"):
+            raise ValueError("mode must be 'fp32', 'mixed' or 'bf16'")
         if layout not in ("default", "sgd"):
             raise ValueError("layout must be 'default' or 'sgd'")
-        self.mode = L.MODE_MIXED if mode == "mixed" else L.MODE_FP32
+        self.mode = {"fp32": L.MODE_FP32, "mixed": L.MODE_MIXED, "bf16": L.MODE_BF16}[mode]
         if decay is None:
             decay = [len(s) >= 2 for s in shapes]
         self.flags = [L.TENSOR_DECAY if d else 0 for d in decay]
@@ -327,7 +340,7 @@ class ParamStore:
         return p.value, g.value, s.value
 
     def _esize(self, which):
-        if which in (L.BUF_PARAM, L.BUF_GRAD) and self.mode == L.MODE_MIXED:
+        if which in (L.BUF_PARAM, L.BUF_GRAD) and self.mode != L.MODE_FP32:
             return 2
         return 4
 
