@@ -17,7 +17,8 @@ gradients, the mean skipped (overflow) step, the step with its norm from buckete
 the other configurations' steps (the MLP, nanoGPT-char, GPT-2 774M mixed AdamW, GPT-2 XL
 fp32 AdamW and SGD momentum; the reference's plain SGD and SGD momentum in mixed precision at
 GPT-2 124M and 774M on stores in the SGD layout, and SGD momentum at 774M in the default
-layout), each in a store of its own, and the step of the reference's GPT benchmark model
+layout; the reference's plain SGD on its own bf16-only storage at GPT-2 124M and 774M), each
+in a store of its own, and the step of the reference's GPT benchmark model
 through the C++ drop-in surface (tests/cpp/bench_gpt2_step).  `--optimizer sgd|sgdm` and
 `--layout sgd` time those steps as the main leg instead (for profiling).
 """
@@ -39,12 +40,14 @@ HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
 CACHED_GRAD_BYTES = 256 << 20
 # algorithmic bytes per parameter of one update-kernel pass (and of the norm pass)
 UPDATE_BYTES = {("adamw", "mixed"): 28, ("adamw", "fp32"): 28, ("sgdm", "fp32"): 20,
-                ("sgdm", "mixed"): 20, ("sgd", "mixed"): 12, ("sgd", "fp32"): 12}
+                ("sgdm", "mixed"): 20, ("sgd", "mixed"): 12, ("sgd", "fp32"): 12,
+                # a BF16 store: bf16 gradient and weight read, weight written
+                ("sgd", "bf16"): 6}
 # update legs below this many algorithmic bytes are launch-bound or Infinity-Cache resident:
 # an event pair around each launch then measures mostly its own overhead, and a copy of their
 # bytes no ceiling, so neither is reported for them
 MIN_TIMED_UPDATE_BYTES = 1 << 30
-NORM_BYTES = {"mixed": 2, "fp32": 4}
+NORM_BYTES = {"mixed": 2, "fp32": 4, "bf16": 2}
 
 # The step of each BASELINE.json configuration: optimizer hyperparameters, loss scaling, and
 # the synthetic gradient distribution (N(0, std), a fraction `heavy` drawn from N(0, 1)).
@@ -465,18 +468,19 @@ def ceilings(stream, update_bytes):
     return copy_gbps, nt_copy_gbps, nt_read_gbps, copy_bytes, nt_copy64_gbps
 
 
-def make_store(config, seed=1234, layout="default", scaler=True):
+def make_store(config, seed=1234, layout="default", scaler=True, mode=None):
     """A store of `config`'s table on cuda:0 (in `layout`) with N(0, 0.02) master weights and
     the configuration's synthetic gradients resident in HBM, on a created stream; loss scaling
-    as the configuration has it, unless `scaler` is False.  Returns (store, stream, grads as a
-    device tensor)."""
+    as the configuration has it, unless `scaler` is False.  mode: the store's precision mode
+    instead of the configuration's ("bf16": the same values as bf16 weights, no master).
+    Returns (store, stream, grads as a device tensor)."""
     import torch
     import ttperf
     from ttperf import _lib as L
     from ttperf import configs
 
     names, shapes, decay, numels = configs.table(config)
-    mode = configs.mode(config)
+    mode = mode or configs.mode(config)
     dev = torch.device("cuda:0")
     store = ttperf.ParamStore(shapes, mode=mode, decay=decay, names=names, layout=layout)
     # a created stream (the legacy default stream cannot be captured); torch's events and
@@ -487,7 +491,10 @@ def make_store(config, seed=1234, layout="default", scaler=True):
     scale = (cfg["scaler"] or 1.0) if scaler else 1.0
     gen = torch.Generator(device=dev).manual_seed(seed)
     w = torch.randn(store.total, generator=gen, device=dev) * 0.02
-    store.upload(L.BUF_MASTER, L.ALL_TENSORS, w)
+    if mode == "bf16":
+        store.upload(L.BUF_PARAM, L.ALL_TENSORS, w.to(torch.bfloat16))
+    else:
+        store.upload(L.BUF_MASTER, L.ALL_TENSORS, w)
     del w
     if cfg["scaler"] and scaler:
         store.configure_scaler(True, init_scale=scale)
@@ -497,7 +504,7 @@ def make_store(config, seed=1234, layout="default", scaler=True):
         g = torch.where(pick, torch.randn(store.total, generator=gen, device=dev), g)
         del pick
     g = g * scale
-    g = g.to(torch.bfloat16) if mode == "mixed" else g
+    g = g.to(torch.bfloat16) if mode != "fp32" else g
     store.upload(L.BUF_GRAD, L.ALL_TENSORS, g)
     return store, stream, g
 
@@ -521,7 +528,9 @@ def update_kernel_name(optimizer, mode, total_elems, layout="default"):
     in tt-perf_amd/csrc/ttperf.hip; the SGD forms also with their master's record stride, 64
     for a contiguous master), except while the gradients fit the Infinity Cache: MIXED Adam
     then takes the kLaneAdamMixedCached shape, and MIXED SGD momentum in the default layout the
-    four-element kernel."""
+    four-element kernel; a BF16 store's plain SGD its own kernel (kLaneSgdBf16)."""
+    if mode == "bf16":
+        return "sgd_bf16_lane_kernel<8, 64, 1>"
     grad_t, mixed_t = ("unsigned short", "true") if mode == "mixed" else ("float", "false")
     if optimizer == "adamw":
         if mode == "mixed" and total_elems * 2 <= CACHED_GRAD_BYTES:
@@ -539,23 +548,25 @@ def update_kernel_name(optimizer, mode, total_elems, layout="default"):
     return f"sgd_lane_kernel<{grad_t}, {mixed_t}, {stride}, {shape[0]}, {shape[1]}, {shape[2]}>"
 
 
-def other_config(config, optimizer, steps, warmup, settle_ms, layout="default"):
+def other_config(config, optimizer, steps, warmup, settle_ms, layout="default", mode=None):
     """One more configuration's step in a store of its own (created, timed, closed): settle
     steps and W warmup steps, K steps between one event pair, then K more with an event pair
     around every launch for the update kernel's own time.  The SGD legs step without loss
     scaling (plain SGD: the reference's w - lr*g, no norm pass; SGD momentum: the
-    configuration's clipping).  Returns the JSON object."""
+    configuration's clipping).  mode: the store's precision mode instead of the
+    configuration's ("bf16": the reference's own bf16-only storage).  Returns the JSON
+    object."""
     import torch
     from ttperf import _lib as L
     from ttperf import configs
 
     _, _, _, numels = configs.table(config)
-    mode = configs.mode(config)
+    mode = mode or configs.mode(config)
     n_params = sum(numels)
     cfg = BENCH[config]
     hp = dict(cfg["hp"], decoupled=cfg["decoupled"])
     scaler = bool(cfg["scaler"]) and optimizer == "adamw"
-    store, stream, g = make_store(config, layout=layout, scaler=scaler)
+    store, stream, g = make_store(config, layout=layout, scaler=scaler, mode=mode)
     del g
     torch.cuda.empty_cache()
     step = step_fn(store, optimizer, hp)
@@ -933,10 +944,15 @@ def main():
                 ("gpt2_774m_mixed_sgd", "gpt2_774m", "sgd", "sgd"),
                 ("gpt2_124m_mixed_sgdm", "gpt2_124m", "sgdm", "sgd"),
                 ("gpt2_774m_mixed_sgdm", "gpt2_774m", "sgdm", "sgd"),
-                ("gpt2_774m_mixed_sgdm_default_layout", "gpt2_774m", "sgdm", "default"))
+                ("gpt2_774m_mixed_sgdm_default_layout", "gpt2_774m", "sgdm", "default"),
+                # the reference's own storage and arithmetic: bf16 weights and gradients only,
+                # plain SGD with each op rounded to bf16 (TTP_MODE_BF16)
+                ("gpt2_124m_bf16_sgd", "gpt2_124m", "sgd", "default", "bf16"),
+                ("gpt2_774m_bf16_sgd", "gpt2_774m", "sgd", "default", "bf16"))
         out["other_configs"] = {
-            key: other_config(config, opt, args.steps, args.warmup, args.settle_ms, layout)
-            for key, config, opt, layout in legs}
+            leg[0]: other_config(leg[1], leg[2], args.steps, args.warmup, args.settle_ms,
+                                 *leg[3:])
+            for leg in legs}
         out["other_configs"]["note"] = (
             "each in a store of its own, created, timed (settle steps and W warmup steps, then "
             "K steps between one event pair; the update alone from a second pass with an event "
