@@ -87,6 +87,9 @@ def parse():
     ap.add_argument("--optimizer", default="adamw", choices=["adamw", "sgdm", "sgd"],
                     help="adamw (the headline); sgdm: SGD with momentum 0.9 and the "
                          "configuration's clipping; sgd: the reference's plain SGD, w - lr*g")
+    ap.add_argument("--mode", default="config", choices=["config", "bf16"],
+                    help="the store's precision mode: the configuration's, or bf16 (the "
+                         "reference's bf16-only storage, TTP_MODE_BF16; with --optimizer sgd)")
     ap.add_argument("--layout", default="default", choices=["default", "sgd"],
                     help="store layout of a mixed store (sgd: TTP_STORE_SGD, a contiguous "
                          "master and no m / v)")
@@ -597,7 +600,7 @@ def other_config(config, optimizer, steps, warmup, settle_ms, layout="default", 
     skip_ms = None
     if scaler:
         store.upload(L.BUF_GRAD, 0, torch.full((numels[0],), float("inf"), device="cuda",
-                                               dtype=torch.bfloat16 if mode == "mixed"
+                                               dtype=torch.bfloat16 if mode != "fp32"
                                                else torch.float32))
         rs = store.adam_step(report=True, **hp)
         assert rs["skipped"], rs
@@ -690,7 +693,9 @@ def main():
     from ttperf import configs
 
     names, shapes, decay, numels = configs.table(args.config)
-    mode = configs.mode(args.config)
+    mode = configs.mode(args.config) if args.mode == "config" else args.mode
+    if mode == "bf16" and args.optimizer != "sgd":
+        sys.exit("bench.py: a bf16 store steps plain SGD only (--optimizer sgd)")
     n_params = sum(numels)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -700,7 +705,7 @@ def main():
     scaler = bool(cfg["scaler"]) and args.optimizer == "adamw"
     scale = cfg["scaler"] if scaler else 1.0
     norm_runs = args.optimizer != "sgd" and bool(cfg["hp"]["max_grad_norm"] or scaler)
-    store, stream, g = make_store(args.config, layout=args.layout, scaler=scaler)
+    store, stream, g = make_store(args.config, layout=args.layout, scaler=scaler, mode=mode)
     store_total = store.total
     grads_host = None
     if not args.no_cpu_baseline and args.optimizer == "adamw":
@@ -815,7 +820,7 @@ def main():
     skip_ms, n_skip = None, 0
     if scaler:
         store.upload(L.BUF_GRAD, 0, torch.full((store.tensors[0].numel,), float("inf"),
-                                               device=dev, dtype=torch.bfloat16 if mode == "mixed"
+                                               device=dev, dtype=torch.bfloat16 if mode != "fp32"
                                                else torch.float32))
         rs = store.adam_step(report=True, **hp)
         assert rs["skipped"], rs
@@ -834,7 +839,7 @@ def main():
     sums = None
     if norm_runs:
         store.upload(L.BUF_GRAD, 0, torch.zeros(store.tensors[0].numel, device=dev,
-                                                dtype=torch.bfloat16 if mode == "mixed"
+                                                dtype=torch.bfloat16 if mode != "fp32"
                                                 else torch.float32))
         sums = bucketed_norm(store, stream, args, hp, mode, numels)
     producer = None
@@ -861,12 +866,13 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
+        "dtype": "bf16" if mode == "bf16" else "fp32",
         "launch": "hipGraph replay of the captured step" if args.graph else "eager launches",
         "data": f"synthetic (seeded N(0,{cfg['std']:g})"
                 + (f", {cfg['heavy']:g} of them N(0,1)" if cfg["heavy"] else "")
                 + (f" x loss scale {scale:g}" if scaler else "")
-                + (" bf16" if mode == "mixed" else " fp32") + " grads, N(0,0.02) fp32 master)",
+                + (" bf16" if mode != "fp32" else " fp32") + " grads, N(0,0.02) "
+                + ("bf16 weights)" if mode == "bf16" else "fp32 master)"),
         "config": {"workload": f"{args.config} {args.optimizer} step: {len(numels)} tensors, "
                                f"{n_params} params, {mode} precision, "
                                + (f"loss scaling {scale:g}, " if scaler else "")
