@@ -675,7 +675,9 @@ def cpp_dropin(steps, warmup, settle_ms):
     res["note"] = ("C++ drop-in surface, mixed precision, 200 ms of settle steps then W warmup "
                    "and K steps between two synchronisations (std::chrono, as the reference's "
                    "bench); AdamW with loss scaling 2^16 and clip 1.0 at 30 B/param, the "
-                   "model's sgd_step at 12 B/param; no tied embedding, so 163M params")
+                   "model's sgd_step at 12 B/param (SGD layout), and the same sgd_step on the "
+                   "reference's bf16-only storage (sgd_bf16_*, a Bf16 arena, 6 B/param); no "
+                   "tied embedding, so 163M params")
     return res
 
 

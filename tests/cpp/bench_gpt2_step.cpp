@@ -178,14 +178,41 @@ int run(uint32_t seq, uint32_t dim, uint32_t heads, uint32_t ffn, uint32_t vocab
         test::assert_bits(sp->master(), want, "sgd_step = w - lr*g");
     }
 
+    // 4) the same sgd_step on the reference's own storage (a Bf16 arena: bf16 weights and
+    // gradients, no master; each op rounded to bf16 as the reference's ttnn ops round theirs)
+    ParamArena bf16_arena(ttp::Mode::Bf16);
+    traced::TracedTransformerWithEmbedding<N> bf16_model(/*batch=*/8, seq, dim, heads, ffn, vocab,
+                                                         sgd_lr, bf16_arena);
+    const std::vector<ValuePtr> bf16_params = bf16_model.parameters();
+    ttp::Store& bf16_store = bf16_arena.store();
+    for (size_t k = 0; k < bf16_params.size(); ++k)
+        bf16_params[k]->grad = grad_values(bf16_params[k]->numel(), 1e-3f, (uint32_t)k);
+    uint64_t bf16_steps = 0;
+    const Timing tb = time_steps(bf16_store, [&] { bf16_model.sgd_step(); }, settle_ms, warmup,
+                                 iters, &bf16_steps);
+    const double bf16_gps = (double)numel / (tb.ms_per_step * 1e-3) / 1e9;
+    std::printf("sgd_step on bf16 storage: %.4f ms/step, %.1f Gparams/s (%.0f GB/s at 6 B/param)\n",
+                tb.ms_per_step, bf16_gps, bf16_gps * 6.0);
+    {
+        const ValuePtr& sp = bf16_model.layers[0].ln1.beta;
+        const std::vector<float> w0 = sp->data(), g = sp->grad.value();
+        bf16_model.sgd_step();
+        std::vector<float> want(w0.size());
+        for (size_t i = 0; i < w0.size(); ++i)
+            want[i] = test::bf16_round(w0[i] - test::bf16_round(g[i] * sgd_lr));
+        test::assert_bits(sp->data(), want, "bf16 sgd_step = RNE(w - RNE(g*lr))");
+    }
+
     std::printf("{\"bench\": \"gpt2_step_dropin\", \"layers\": %zu, \"tensors\": %zu, "
                 "\"params\": %llu, \"adamw_ms_per_step\": %.5f, \"adamw_Gparams_per_s\": %.2f, "
                 "\"adamw_settle_steps\": %d, \"sgd_ms_per_step\": %.5f, "
                 "\"sgd_Gparams_per_s\": %.2f, \"sgd_settle_steps\": %d, \"sgd_layout\": \"sgd\", "
-                "\"warmup\": %u, "
+                "\"sgd_bf16_ms_per_step\": %.5f, \"sgd_bf16_Gparams_per_s\": %.2f, "
+                "\"sgd_bf16_settle_steps\": %d, \"warmup\": %u, "
                 "\"iters\": %u}\n",
                 N, params.size(), (unsigned long long)numel, ta.ms_per_step, adam_gps,
-                ta.settle_steps, ts.ms_per_step, sgd_gps, ts.settle_steps, warmup, iters);
+                ta.settle_steps, ts.ms_per_step, sgd_gps, ts.settle_steps, tb.ms_per_step,
+                bf16_gps, tb.settle_steps, warmup, iters);
     return test::finish("bench_gpt2_step");
 }
 

@@ -323,6 +323,15 @@ class Case:
         self.last_adam = None
         self.mom_seen = self.mom_seen or hp["momentum"] > 0
 
+    def _adam_ok(self, adam):
+        """Whether a step drawn as Adam stays Adam (a store without fp32 state steps SGD)."""
+        return adam
+
+    def _sums_sgd_hp(self, lr, clip):
+        """The SGD step that follows bucket sums or a producer: momentum 0.9."""
+        return dict(lr=lr, momentum=0.9, dampening=0.0, weight_decay=0.0, nesterov=False,
+                    max_grad_norm=clip)
+
     def op_sums_step(self):
         """Bucket sums over a random partition of the tensors, then a step that takes its norm
         from them; sometimes a gradient write in between, after which the step is refused
@@ -335,7 +344,7 @@ class Case:
         buckets = [sorted(perm[a:b]) for a, b in zip([0] + cuts, cuts + [self.n]) if b > a]
         for b in buckets:
             self.store.grad_sumsq_tensors(b)
-        adam = rng.random() < 0.6
+        adam = self._adam_ok(rng.random() < 0.6)
         clip = None if rng.random() < 0.3 else float(10 ** rng.uniform(-2, 1))
         indices = None if rng.random() < 0.6 else self.pick_subset()
         if adam:
@@ -343,9 +352,7 @@ class Case:
                                     betas=BETAS[int(rng.integers(0, 3))], eps=1e-8,
                                     weight_decay=0.05, decoupled=True, max_grad_norm=clip)
         else:
-            kind, hp = "sgd", dict(lr=float(10 ** rng.uniform(-3, -1)), momentum=0.9,
-                                   dampening=0.0, weight_decay=0.0, nesterov=False,
-                                   max_grad_norm=clip)
+            kind, hp = "sgd", self._sums_sgd_hp(float(10 ** rng.uniform(-3, -1)), clip)
         cand = [i for i in (range(self.n) if indices is None else indices) if self.numels[i]]
         stale = (clip or self.scaler_on) and cand and rng.random() < 0.3
         print(f"  sums over {buckets} then {kind} {hp} indices={indices}"
@@ -394,16 +401,14 @@ class Case:
         indices = None if rng.random() < 0.5 else self.pick_subset()
         targets = list(range(self.n)) if indices is None else list(indices)
         bucket = [i for i in targets if rng.random() < 0.2]
-        adam = rng.random() < 0.6
+        adam = self._adam_ok(rng.random() < 0.6)
         clip = None if (self.scaler_on and rng.random() < 0.3) else float(10 ** rng.uniform(-2, 1))
         if adam:
             kind, hp = "adam", dict(lr=float(10 ** rng.uniform(-4, -1.5)),
                                     betas=BETAS[int(rng.integers(0, 3))], eps=1e-8,
                                     weight_decay=0.05, decoupled=True, max_grad_norm=clip)
         else:
-            kind, hp = "sgd", dict(lr=float(10 ** rng.uniform(-3, -1)), momentum=0.9,
-                                   dampening=0.0, weight_decay=0.0, nesterov=False,
-                                   max_grad_norm=clip)
+            kind, hp = "sgd", self._sums_sgd_hp(float(10 ** rng.uniform(-3, -1)), clip)
         log = []
         multi = rng.random() < 0.5  # the tensors in bucket calls (ttp_accumulate_grad_multi)
         if multi:
