@@ -79,30 +79,37 @@ def test_torch_forward_backward_with_zero_copy_store(mode, opt_name):
     store.close()
 
 
-def test_reference_traced_mlp_known_answers():
+@pytest.mark.parametrize("mode", ["mixed", "bf16"])
+def test_reference_traced_mlp_known_answers(mode):
     """examples/train_mlp_traced.cpp:100-186, whose PyTorch reference is
     verify/verify_comparison.py:13-101: a 512 -> 256 -> 128 MLP with every weight 0.01 and
     zero biases, x = 1, target = 0.5, batch 1024, MSE, SGD lr 0.01, 5 steps in bf16.  The
     reference prints the expected initial loss 159.390625 and final loss 0.000244
     (train_mlp_traced.cpp:183-185).
 
-    Here torch runs the bf16 forward/backward over zero-copy views of a mixed-precision store
-    and libttperf_hip takes the steps (fp32 master weights, bf16 working copy).  Both known
-    answers are met exactly (0.000244 is 2^-12), and each step's master and bf16 weights
-    match the oracle, fed the same gradients, bit for bit."""
+    Here torch runs the bf16 forward/backward over zero-copy views of the store and
+    libttperf_hip takes the steps: in a mixed-precision store (fp32 master weights, bf16
+    working copy), and in a BF16 store, the reference's own storage, whose steps round the
+    product and the difference to bf16 as the reference's ttnn multiply and subtract do.  The
+    mixed store meets both known answers exactly (0.000244 is 2^-12); the BF16 store meets the
+    initial one and converges to 0.000187 (see below).  In both, each step's weights match the
+    oracle, fed the same gradients, bit for bit."""
     import ttperf
     from ttperf import _lib as L
     torch = torch_mod()
     F = torch.nn.functional
     shapes = [(256, 512), (256,), (128, 256), (128,)]  # nn.Linear weights are [out, in]
-    store = ttperf.ParamStore(shapes, mode="mixed", decay=[True, False, True, False])
+    store = ttperf.ParamStore(shapes, mode=mode, decay=[True, False, True, False])
     store.set_stream(torch.cuda.current_stream())
     ref = O.OracleStore([t.numel for t in store.tensors], flags=[1, 0, 1, 0],
-                        mode=O.MODE_MIXED, nthreads=2)
+                        mode=O.MODE_MIXED if mode == "mixed" else O.MODE_BF16, nthreads=2)
     for i, s in enumerate(shapes):
         w = np.full(store.tensors[i].numel, 0.01 if len(s) == 2 else 0.0, np.float32)
         store.tensors[i].set_data(w)
-        ref.set_master(i, w)
+        if mode == "mixed":
+            ref.set_master(i, w)
+        else:
+            ref.view("param", i)[:] = O.bf16_rne(w)
     params = [torch.nn.Parameter(t.torch_view(L.BUF_PARAM)) for t in store.tensors]
     for p, t in zip(params, store.tensors):
         p.grad = t.torch_view(L.BUF_GRAD)
@@ -129,14 +136,24 @@ def test_reference_traced_mlp_known_answers():
             ref.set_has_grad(i, True)
         opt.step()
         ref.sgd_step(lr=0.01)
-        compare_state(store, ref, which=("master", "param"), max_ulp=0)
+        compare_state(store, ref, which=("master", "param") if mode == "mixed" else ("param",),
+                      max_ulp=0)
         with torch.no_grad():
             after.append(loss_of().item())
         print(f"step {step}: loss_before={loss.item():.6f}, loss_after={after[-1]:.6f}",
               flush=True)
     assert initial == 159.390625, initial            # train_mlp_traced.cpp:184
-    assert f"{after[-1]:.6f}" == "0.000244", after   # train_mlp_traced.cpp:185
-    assert after[-1] == 2.0 ** -12
+    if mode == "mixed":
+        assert f"{after[-1]:.6f}" == "0.000244", after   # train_mlp_traced.cpp:185
+        assert after[-1] == 2.0 ** -12
+    else:
+        # The printed final loss is torch.optim.SGD's (verify/verify_comparison.py:38), whose
+        # bf16 update rounds p - lr*g once.  The reference's own C++ step rounds the product
+        # and the difference separately (autograd/traced/nn.hpp:93-96), as this store does:
+        # the same five steps then end at 0.000187 (0.315857, 0.053116, 0.008789, 0.001377),
+        # each step's weights equal to the oracle's.
+        assert all(b < a for a, b in zip([initial] + after, after)), after
+        assert 0.0 < after[-1] < 1e-3, after
     store.close()
 
 
