@@ -3,7 +3,8 @@
 // layer / stack / GPT sgd_step (autograd/traced/transformer_train.hpp:259-268,335-339,487-494)
 // and TracedMLP<N>::sgd_step (autograd/traced/mlp.hpp:106-110).
 // Each sgd_step must update exactly its module's tensors, bit-exact against `w - lr*dw`
-// (one rounding per op, bf16 weights = RNE of the fp32 master), in ONE update launch.
+// (one rounding per op, bf16 weights = RNE of the fp32 master; in a Bf16 arena each op
+// rounded to bf16), in ONE update launch.
 #include "autograd/optim.hpp"
 #include "autograd/static.hpp"
 #include "autograd/traced.hpp"
@@ -149,6 +150,42 @@ int main() {
         stack.sgd_step();
         for (size_t k = 0; k < ps.size(); ++k) apply(r, k, 0.2f);
         check_all(ps, r, false, "stack sgd_step");
+    }
+    // ---- the same GPT on the reference's own storage (a Bf16 arena: bf16 weights and
+    // gradients, no master): each sgd_step is RNE(w - RNE(g*lr)) over its module's tensors,
+    // the rounding of the reference's ttnn multiply and subtract, in one update launch ------
+    {
+        ParamArena arena(ttp::Mode::Bf16);
+        traced::TracedTransformerWithEmbedding<2> gpt(4, 32, 64, 4, 4, 65, 0.05f, arena);
+        auto ps = gpt.parameters();
+        std::vector<std::vector<float>> w, g;
+        for (size_t k = 0; k < ps.size(); ++k) {
+            w.push_back(ps[k]->data());
+            auto gk = ramp(ps[k]->numel(), 0.02f, 0.003f * (float)(k + 1));
+            ps[k]->grad = gk;  // rounded to bf16 by the store
+            for (auto& x : gk) x = test::bf16_round(x);
+            g.push_back(gk);
+        }
+        auto step = [&](size_t k, float lr) {
+            for (size_t i = 0; i < w[k].size(); ++i)
+                w[k][i] = test::bf16_round(w[k][i] - test::bf16_round(g[k][i] * lr));
+        };
+        auto check = [&](const std::string& what) {
+            for (size_t k = 0; k < ps.size(); ++k)
+                test::assert_bits(ps[k]->data(), w[k], what + " " + std::to_string(k));
+        };
+        ttp::Store& store = arena.store();
+        ttp::check(ttp_timing_enable(store.get(), 1));
+        update_launches(store);
+        gpt.sgd_step();
+        test::check(update_launches(store) == 1, "bf16 GPT sgd_step is one update launch");
+        for (size_t k = 0; k < ps.size(); ++k) step(k, 0.05f);
+        check("bf16 GPT sgd_step");
+        gpt.layers[0].sgd_step();  // block 0's 16 tensors only (after the 2 embeddings)
+        test::check(update_launches(store) == 1, "bf16 block sgd_step is one update launch");
+        for (size_t k = 2; k < 2 + 16; ++k) step(k, 0.05f);
+        check("bf16 block sgd_step");
+        ttp::check(ttp_timing_enable(store.get(), 0));
     }
     // ---- arena layouts: an Adam declared before first use gets Adam's layout; one declared
     // after converts the SGD layout at its first step, from the values SGD left ----------
