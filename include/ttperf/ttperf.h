@@ -387,8 +387,9 @@ int ttp_sgd_step_subset(ttp_ctx* ctx, const ttp_sgd_hparams* hp, const uint32_t*
  * layout.  Step once with ttp_adam_step[_subset] first.  In host-count mode (no loss
  * scaling, never captured) the step needs no bias-correction table and builds none: a later
  * capture of Adam steps with those betas needs one allocating step with them first (the
- * capture refuses them otherwise).  There is no report: ttp_scaler_get and ttp_get_step
- * read the results. */
+ * capture refuses them otherwise).  A TTP_MODE_BF16 store refuses it (TTP_ERR_INVALID), as
+ * it refuses every Adam step.  There is no report: ttp_scaler_get and ttp_get_step read the
+ * results. */
 int ttp_adam_step_noalloc(ttp_ctx* ctx, const ttp_adam_hparams* hp, const uint32_t* indices,
                           uint32_t n_indices);
 /* Global L2 norm of the gradients that exist, unscaled by the current loss scale when
