@@ -252,3 +252,31 @@ def test_refusals_change_nothing():
     ref.sgd_step(lr=0.1)
     _same_weights(store, ref, "after the refusals")
     store.close()
+
+
+def test_split_launches_and_many_small_tensors(monkeypatch):
+    """The BF16 update over more blocks than one launch may hold runs as several launches at
+    increasing part offsets: TTP_LANE_LAUNCH_BLOCKS (read at ttp_create) lowers that limit to
+    4099 blocks, so the store below takes dozens of launches whose boundaries fall inside
+    chunks and tensors.  The store mixes two large tensors of odd sizes with 600 tensors of
+    1..200 elements (most chunks hold less than one piece of 512 elements, and many lanes end
+    inside a tensor's last word).  Plain SGD with loss scaling and clipping over the whole
+    store and over a subset of every third tensor, against the oracle."""
+    torch = torch_mod()
+    monkeypatch.setenv("TTP_LANE_LAUNCH_BLOCKS", "4099")
+    rng = np.random.default_rng(440)
+    small = [(int(n),) for n in rng.integers(1, 201, size=600)]
+    shapes = [(50257, 768), (7001, 4999)] + small + [(3,)]
+    decay = [True, True] + [False] * (len(small) + 1)
+    store, ref = make_pair(shapes, decay, O.MODE_BF16, seed=441)
+    store.configure_scaler(True, init_scale=4096.0, growth_interval=2)
+    ref.configure_scaler(True, 4096.0, growth_interval=2)
+    gen = torch.Generator(device="cuda").manual_seed(442)
+    hp = dict(lr=1e-2, max_grad_norm=1.0)
+    subset = list(range(0, len(shapes), 3))
+    for label, sub in (("whole store", None), ("subset", subset), ("whole store", None)):
+        device_grads(store, gen, 1e-3, scale=ref.scale, into=ref.grad)
+        _set_all(ref, sub)
+        _check(store.sgd_step(report=True, indices=sub, **hp), ref.sgd_step(**hp), True)
+        _same_weights(store, ref, label)
+    store.close()
