@@ -24,8 +24,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from gpu_util import make_pair
-from test_gpu_fuzz import Case, _shapes
+from test_gpu_fuzz import Case
 
 pytestmark = pytest.mark.gpu
 
@@ -36,26 +35,8 @@ N_OPS = int(os.environ.get("TTP_FUZZ_OPS", "50"))
 
 class Bf16Case(Case):
     def __init__(self, seed, tmp_path):
-        self.torch = __import__("torch")
-        self.rng = np.random.default_rng(seed)
-        self.shapes = _shapes(self.rng)
-        self.n = len(self.shapes)
-        self.decay = [len(s) == 2 for s in self.shapes]
-        self.mixed = True  # bf16 gradients, as a mixed store's
-        self.sgd_layout = False
-        self.store, self.ref = make_pair(self.shapes, self.decay, O.MODE_BF16, seed=seed)
-        self.store.set_stream(None)  # the store's own stream: capturable
-        self.numels = [t.numel for t in self.store.tensors]
-        self.graphs = []       # (graph, hp, captured active set) of captured SGD steps
-        self.zero_graphs = []
-        self.prod_graphs = []
-        self.last_adam = None
-        self.last_sgd = None   # (hp, indices, active set) of the last eager SGD step
-        self.saved = None
-        self.path = tmp_path / f"state_{seed}.bin"
-        self.scaler_on = False
-        self.adam_seen = False
-        self.mom_seen = False
+        super().__init__(seed, tmp_path, bf16=True)
+        self.last_sgd = None  # (hp, indices, active set) of the last eager SGD step
 
     def _adam_ok(self, adam):
         return False

@@ -68,18 +68,24 @@ def _shapes(rng):
 
 
 class Case:
-    def __init__(self, seed, tmp_path):
+    def __init__(self, seed, tmp_path, bf16=False):
+        """bf16: a BF16 store (bf16 weights and gradients only) instead of a drawn mode."""
         self.torch = torch_mod()
         self.rng = np.random.default_rng(seed)
         rng = self.rng
         self.shapes = _shapes(rng)
         self.n = len(self.shapes)
         self.decay = [len(s) == 2 for s in self.shapes]
-        self.mixed = bool(rng.integers(0, 2))
-        mode = O.MODE_MIXED if self.mixed else O.MODE_FP32
-        # half the mixed cases start in the SGD layout (a generator of its own keeps the other
-        # draws of a seed as they were); the first Adam step converts the store
-        self.sgd_layout = self.mixed and np.random.default_rng(seed + 7777).random() < 0.5
+        if bf16:
+            self.mixed = True  # bf16 gradients, as a mixed store's
+            mode = O.MODE_BF16
+            self.sgd_layout = False
+        else:
+            self.mixed = bool(rng.integers(0, 2))
+            mode = O.MODE_MIXED if self.mixed else O.MODE_FP32
+            # half the mixed cases start in the SGD layout (a generator of its own keeps the
+            # other draws of a seed as they were); the first Adam step converts the store
+            self.sgd_layout = self.mixed and np.random.default_rng(seed + 7777).random() < 0.5
         self.store, self.ref = make_pair(self.shapes, self.decay, mode, seed=seed,
                                          layout="sgd" if self.sgd_layout else "default")
         self.store.set_stream(None)  # the store's own stream: capturable
