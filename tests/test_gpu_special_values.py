@@ -227,8 +227,8 @@ def test_special_values_match_the_oracle(mode, opt, variant, tmp_path):
 F32_SUMMABLE = F32_FINITE[np.abs(F32_FINITE) < 1e38]
 BF16_SUMMABLE = BF16_FINITE[np.abs(O.bf16_to_f32(BF16_FINITE)) < 1e38]
 
-ACC_CASES = [(mode, src, multi, sums) for mode in ("fp32", "mixed") for src in ("f32", "bf16")
-             for multi in (False, True) for sums in (False, True)]
+ACC_CASES = [(mode, src, multi, sums) for mode in ("fp32", "mixed", "bf16")
+             for src in ("f32", "bf16") for multi in (False, True) for sums in (False, True)]
 
 
 @pytest.mark.parametrize("mode,src,multi,sums", ACC_CASES)
@@ -238,14 +238,15 @@ def test_special_values_accumulate_match_the_oracle(mode, src, multi, sums):
     inf + -inf = NaN, ...), one call per tensor or one bucket call, with or without the tiles'
     sums; the gradients must equal the oracle's bit for bit after each call.  Then an AdamW
     step with clipping (and loss scaling in a mixed store) takes its norm from the sums, or
-    from its norm pass, and must match the oracle's step.  Two iterations: finite incoming
+    from its norm pass, and must match the oracle's step; a BF16 store takes the reference's
+    plain SGD there, with clipping and loss scaling.  Two iterations: finite incoming
     values whose sums stay finite, then the largest and the non-finite ones too."""
     import torch
     from ttperf import _lib as L
-    mixed = mode == "mixed"
+    mixed = mode != "fp32"  # bf16 gradients (and loss scaling below)
     seed = 7500 + ACC_CASES.index((mode, src, multi, sums))
     print(f"case {mode} src {src} multi {multi} sums {sums} seed {seed}", flush=True)
-    store, ref = make_pair(SHAPES, DECAY, O.MODE_MIXED if mixed else O.MODE_FP32, seed=seed)
+    store, ref = make_pair(SHAPES, DECAY, STORE_MODE[mode], seed=seed)
     rng = np.random.default_rng(seed)
     mask = pad_mask(store)
     total = store.total
@@ -254,6 +255,8 @@ def test_special_values_accumulate_match_the_oracle(mode, src, multi, sums):
         ref.configure_scaler(True, 65536.0, growth_interval=2)
     hp = dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.1, decoupled=True)
     which = ["master", "exp_avg", "exp_avg_sq"] + (["param"] if mixed else [])
+    if mode == "bf16":
+        hp, which = dict(lr=1e-2), ["param"]
     n = len(SHAPES)
     numels = [t.numel for t in store.tensors]
     for it, bad in enumerate((False, True)):
@@ -281,8 +284,12 @@ def test_special_values_accumulate_match_the_oracle(mode, src, multi, sums):
                     store.accumulate_grad(i, vals[i], sums=sums)
             _check_bits(f"grad after round {rnd}", store.download(L.BUF_GRAD), ref.grad[:total],
                         mask)
-        r = store.adam_step(report=True, max_grad_norm=1.0, tensor_sums=sums, **hp)
-        e = ref.adam_step(max_grad_norm=1.0, **hp)
+        if mode == "bf16":
+            r = store.sgd_step(report=True, max_grad_norm=1.0, tensor_sums=sums, **hp)
+            e = ref.sgd_step(max_grad_norm=1.0, **hp)
+        else:
+            r = store.adam_step(report=True, max_grad_norm=1.0, tensor_sums=sums, **hp)
+            e = ref.adam_step(max_grad_norm=1.0, **hp)
         print(f" iteration {it}: skipped {e['skipped']} found_inf {e['found_inf']} "
               f"norm {e['grad_norm']:.6g} coef {e['clip_coef']:.6g}", flush=True)
         _check_report(r, e, mixed, norm_ran=True)
