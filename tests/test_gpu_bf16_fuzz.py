@@ -9,8 +9,9 @@ store takes, and the ones it refuses:
   reference's plain SGD over everything or a subset, with or without clipping and reports,
   deferring the scale update or not; steps from bucket sums and from a producer's sums (and
   their refusals after a gradient write); the loss scaler switched on or off; the step count
-  set; the gradient norm probed; checkpoints saved and loaded; SGD steps and zero_grad calls
-  captured into graphs and replayed later; and the calls that need fp32 state (Adam through
+  set; the gradient norm probed; checkpoints saved and loaded; SGD steps, zero_grad calls and
+  whole producer iterations (zero_grad, accumulates with sums, the SGD step from them)
+  captured into graphs and replayed later with new sources; and the calls that need fp32 state (Adam through
   every entry point, SGD with momentum or weight decay), which must be refused with
   TTP_ERR_INVALID and change nothing.
 
@@ -44,6 +45,15 @@ class Bf16Case(Case):
     def _sums_sgd_hp(self, lr, clip):
         return dict(lr=lr, momentum=0.0, dampening=0.0, weight_decay=0.0, nesterov=False,
                     max_grad_norm=clip)
+
+    # a captured producer iteration ends with the reference's SGD from the producer's sums
+    PRODUCER_KIND = "sgd"
+
+    def _producer_hp(self, rng):
+        return dict(lr=float(10 ** rng.uniform(-3, -1)), max_grad_norm=float(10 ** rng.uniform(-2, 1)))
+
+    def _producer_step(self, indices, hp, report):
+        return self.store.sgd_step(report=report, indices=indices, tensor_sums=True, **hp)
 
     def _plain_hp(self):
         rng = self.rng
@@ -140,7 +150,7 @@ class Bf16Case(Case):
            ("zero_grad", 2), ("upload_weights", 1), ("adam", 2), ("sgd", 8), ("scaler", 1),
            ("set_step", 1), ("grad_norm", 1), ("save", 1), ("load", 1), ("capture", 2),
            ("replay", 3), ("sums_step", 4), ("zero_graph", 2), ("scaler_update", 1),
-           ("producer_step", 3)]
+           ("producer_step", 3), ("producer_graph", 1), ("producer_replay", 2)]
 
     def compare(self):
         from ttperf import _lib as L

@@ -333,6 +333,17 @@ class Case:
         """Whether a step drawn as Adam stays Adam (a store without fp32 state steps SGD)."""
         return adam
 
+    # the step a captured producer iteration ends with: AdamW from the producer's sums
+    PRODUCER_KIND = "adam"
+
+    def _producer_hp(self, rng):
+        return dict(lr=float(10 ** rng.uniform(-4, -1.5)), betas=BETAS[int(rng.integers(0, 3))],
+                    eps=1e-8, weight_decay=0.05, decoupled=True,
+                    max_grad_norm=float(10 ** rng.uniform(-2, 1)))
+
+    def _producer_step(self, indices, hp, report):
+        return self.store.adam_step(report=report, indices=indices, tensor_sums=True, **hp)
+
     def _sums_sgd_hp(self, lr, clip):
         """The SGD step that follows bucket sums or a producer: momentum 0.9."""
         return dict(lr=lr, momentum=0.9, dampening=0.0, weight_decay=0.0, nesterov=False,
@@ -635,18 +646,18 @@ class Case:
         r = None
         if graph is None:
             self._producer_calls(targets, srcs)
-            r = self.store.adam_step(report=True, indices=indices, tensor_sums=True, **hp)
+            r = self._producer_step(indices, hp, True)
         else:
             graph.replay()
             self.store.sync()
         self.ref.zero_grad(set_to_none=True, fill=srcs.get("fill", True))
         for i in reversed(targets):
             self.ref.accumulate_grad(i, host[i])
-        e = self._ref_step("adam", hp, self._active(indices))
+        e = self._ref_step(self.PRODUCER_KIND, hp, self._active(indices))
         if r is not None:
             self._check_report(r, e)
         self.last_adam = None
-        self.adam_seen = True
+        self.adam_seen = self.adam_seen or self.PRODUCER_KIND == "adam"
         return r
 
     def op_producer_graph(self):
@@ -663,14 +674,12 @@ class Case:
         targets = [i for i in (range(self.n) if indices is None else indices) if self.numels[i]]
         if not targets:
             return self.op_adam()
-        hp = dict(lr=float(10 ** rng.uniform(-4, -1.5)), betas=BETAS[int(rng.integers(0, 3))],
-                  eps=1e-8, weight_decay=0.05, decoupled=True,
-                  max_grad_norm=float(10 ** rng.uniform(-2, 1)))
+        hp = self._producer_hp(rng)
         dt = torch.bfloat16 if rng.random() < 0.5 else torch.float32
         srcs = {i: torch.zeros(self.numels[i], device="cuda", dtype=dt) for i in targets}
         srcs["multi"] = bool(rng.random() < 0.5)
         srcs["fill"] = bool(rng.random() < 0.5)  # zero_grad with or without the fill
-        print(f"  capture producer + adam from its sums {hp} indices={indices} "
+        print(f"  capture producer + {self.PRODUCER_KIND} from its sums {hp} indices={indices} "
               f"targets={targets} sources {dt}{' in bucket calls' if srcs['multi'] else ''}"
               f"{'' if srcs['fill'] else ', zero_grad(fill=False)'}",
               flush=True)
@@ -680,14 +689,15 @@ class Case:
         self.compare()
         self.store.begin_capture()
         self._producer_calls(targets, srcs)
-        self.store.adam_step(indices=indices, tensor_sums=True, **hp)
+        self._producer_step(indices, hp, False)
         self.prod_graphs.append((self.store.end_capture(), hp, indices, targets, srcs))
 
     def op_producer_replay(self):
         if not self.prod_graphs:
             return self.op_producer_graph()
         g, hp, indices, targets, srcs = self.prod_graphs[int(self.rng.integers(0, len(self.prod_graphs)))]
-        print(f"  replay producer + adam {hp} indices={indices} targets={targets}", flush=True)
+        print(f"  replay producer + {self.PRODUCER_KIND} {hp} indices={indices} "
+              f"targets={targets}", flush=True)
         self._producer_iteration(hp, indices, targets, srcs, graph=g)
 
     def _zero_ref(self, none, idx, fill=True):
