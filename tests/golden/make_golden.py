@@ -289,6 +289,13 @@ def gen_reference_known_answers():
     w2 = w1 - 0.1 * g2
     out.update(sgd2_w0=bf16_bits(w), sgd2_g1=bf16_bits(g1), sgd2_w1=bf16_bits(w1),
                sgd2_g2=bf16_bits(g2), sgd2_w2=bf16_bits(w2))
+    # py/optim.py:19-21 itself on bf16 tensors: lr filled into a tensor of the gradient's dtype
+    # (full_like, so lr rounds to bf16), then mul and sub, each result a bf16 tensor; on the
+    # one-step fixture's weights and gradients
+    w0 = torch.from_numpy(out["sgd1_w0"].view(np.int16)).view(torch.bfloat16)
+    gb = torch.from_numpy(out["sgd1_grad"].view(np.int16)).view(torch.bfloat16)
+    lr_tt = torch.full_like(gb, 0.1)
+    out.update(sgd_pyopt_w1=bf16_bits(w0 - gb * lr_tt))
     np.savez(os.path.join(OUT, "reference_known_answers.npz"), **out)
 
 

@@ -49,7 +49,8 @@ def _same_weights(store, ref, what):
 def test_reference_sgd_test_formulas_bit_for_bit():
     """tests/sgd_optimizer.py:15-39 and :42-78: the expected weights the reference's tests
     compute with torch in bf16 (`w - 0.1 * grad`), from the fixtures' own weights and
-    gradients, one step and two steps, equal bit for bit."""
+    gradients, one step and two steps, equal bit for bit; and the drop-in SGD of py/optim.py
+    equal to torch's run of that file's own three ops on bf16 tensors."""
     import ttperf
     from ttperf import _lib as L
     d = golden("reference_known_answers.npz")
@@ -63,6 +64,13 @@ def test_reference_sgd_test_formulas_bit_for_bit():
         store.upload(L.BUF_GRAD, 0, d[g].ravel())
         store.sgd_step(lr=0.1)
         assert np.array_equal(store.download(L.BUF_PARAM, 0), d[w].ravel()), w
+    # the drop-in py/optim.py SGD (ttperf.SGD) on the same weights: py/optim.py:19 fills lr
+    # into a bf16 tensor, so the step equals torch's run of full_like / mul / sub on bf16
+    # tensors (lr 0.1 rounded to 0.10009765625)
+    store.upload(L.BUF_PARAM, 0, d["sgd1_w0"].ravel())
+    store.upload(L.BUF_GRAD, 0, d["sgd1_grad"].ravel())
+    ttperf.SGD(store.parameters(), lr=0.1).step()
+    assert np.array_equal(store.download(L.BUF_PARAM, 0), d["sgd_pyopt_w1"].ravel())
     store.close()
 
 

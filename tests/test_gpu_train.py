@@ -96,6 +96,7 @@ def test_reference_traced_mlp_known_answers(mode):
     oracle, fed the same gradients, bit for bit."""
     import ttperf
     from ttperf import _lib as L
+    from ttperf.store import bf16_value
     torch = torch_mod()
     F = torch.nn.functional
     shapes = [(256, 512), (256,), (128, 256), (128,)]  # nn.Linear weights are [out, in]
@@ -135,7 +136,8 @@ def test_reference_traced_mlp_known_answers(mode):
         for i in range(ref.n):
             ref.set_has_grad(i, True)
         opt.step()
-        ref.sgd_step(lr=0.01)
+        # on a BF16 store the drop-in SGD rounds lr to bf16, as py/optim.py:19's full_like does
+        ref.sgd_step(lr=0.01 if mode == "mixed" else bf16_value(0.01))
         compare_state(store, ref, which=("master", "param") if mode == "mixed" else ("param",),
                       max_ulp=0)
         with torch.no_grad():

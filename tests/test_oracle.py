@@ -168,6 +168,17 @@ def test_sgd_bf16_store_reproduces_the_reference_test_formulas_exactly():
         st.set_grad(0, d[g].ravel())
         st.sgd_step(lr=0.1)
         assert np.array_equal(st.view("param", 0), d[w].ravel()), w
+    # py/optim.py:19-21 itself on bf16 tensors fills lr into a bf16 tensor (full_like), so its
+    # product uses lr = RNE_bf16(0.1): a BF16 store stepped with that lr equals torch's run of
+    # the same three ops on bf16 tensors, which differs from the fp32-lr formula above
+    st = O.OracleStore([1024], mode=O.MODE_BF16)
+    st.param[:1024] = d["sgd1_w0"].ravel()
+    st.set_grad(0, d["sgd1_grad"].ravel())
+    lr16 = float(O.bf16_to_f32(O.bf16_rne(np.array([0.1], np.float32)))[0])
+    assert lr16 == 0.10009765625
+    st.sgd_step(lr=lr16)
+    assert np.array_equal(st.view("param", 0), d["sgd_pyopt_w1"].ravel())
+    assert not np.array_equal(d["sgd_pyopt_w1"], d["sgd1_w1"])
     mixed = O.OracleStore([1024], mode=O.MODE_MIXED)
     mixed.set_master(0, O.bf16_to_f32(d["sgd1_w0"].ravel()))
     mixed.set_grad(0, d["sgd1_grad"].ravel())

@@ -2,7 +2,9 @@
 
 SGD   — py/optim.py:6-27 (`SGD(params, *, lr)`, ValueError on lr <= 0 and on non-Tensor
         params, skips params whose grad is None, `zero_grad` sets grads to None), extended
-        with momentum / dampening / nesterov / weight_decay (torch.optim.SGD semantics).
+        with momentum / dampening / nesterov / weight_decay (torch.optim.SGD semantics).  On a
+        BF16 store (the reference's bf16 tensors) lr is rounded to bf16 first, as
+        py/optim.py:19's full_like fill of the gradient's dtype rounds it.
 Adam  — py/optim.py:30-92 (`Adam(params, *, lr=1e-3, betas=(0.9, 0.999), eps=1e-8)`, the
         same validation, a step count that advances on every step() call, bias corrections
         in host double), extended with weight_decay (L2) and max_grad_norm.
@@ -22,7 +24,8 @@ from __future__ import annotations
 
 import weakref
 
-from .store import Tensor
+from . import _lib as L
+from .store import Tensor, bf16_value
 
 
 def _group_by_store(params, what):
@@ -115,7 +118,12 @@ class SGD(_Optimizer):
         self.max_grad_norm = max_grad_norm
 
     def _step_store(self, store, indices, tensor_sums, update_scale):
-        store.sgd_step(self.lr, self.momentum, self.dampening, self.weight_decay,
+        lr = self.lr
+        if store.mode == L.MODE_BF16:
+            # py/optim.py:19 fills lr into a tensor of the gradient's dtype (ttnn.full_like):
+            # on the reference's bf16 tensors the product uses lr rounded to bf16
+            lr = bf16_value(lr)
+        store.sgd_step(lr, self.momentum, self.dampening, self.weight_decay,
                        self.nesterov, self.max_grad_norm, indices=indices,
                        tensor_sums=tensor_sums, update_scale=update_scale)
 

@@ -28,6 +28,11 @@ def _bf16_bits_to_f32(h):
     return (np.asarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
+def bf16_value(x):
+    """The float x rounded to bf16 (nearest even), as a Python float."""
+    return float(_bf16_bits_to_f32(_f32_to_bf16_bits(np.float32(x)))[0])
+
+
 def _f32_to_bf16_bits(x):
     """float32 values -> bf16 bit patterns, rounded to nearest even (NaN -> 0x7FC0)."""
     u = np.ascontiguousarray(x, np.float32).ravel().view(np.uint32).astype(np.uint64)
