@@ -187,6 +187,7 @@ class _CountingStore:
 
     def __init__(self, n):
         import ttperf
+        self.mode = ttperf._lib.MODE_MIXED
         self._t = 0
         self.reads = self.writes = 0
         self._t_owner = None
