@@ -4,7 +4,8 @@
  * AddressSanitizer/UBSan (tests/test_oracle_sanitizers.py) catches any out-of-bounds access or
  * undefined behaviour in the checker itself.  It also re-checks two invariants on the way:
  * the op-by-op Adam (py/optim.py:76-86 as separate passes) equals the fused step bit for bit,
- * and a step skipped on a non-finite gradient leaves the state untouched.
+ * and a step skipped on a non-finite gradient leaves the state untouched.  A BF16 store runs with
+ * no fp32 state allocated at all.
  * Prints "oracle_san: PASS" and exits 0 when every check holds.
  */
 #include <math.h>
@@ -192,9 +193,119 @@ static void run_mode(int mode) {
     release(&b);
 }
 
+/* A BF16 store holds only bf16 weights and bf16 gradients: its fp32 state pointers stay NULL,
+ * so any read or write of them in this mode faults here.  Adam and SGD with momentum or decay
+ * are refused with nothing changed; plain SGD runs the same with 4 threads as with 1; a
+ * non-finite gradient under loss scaling skips the step. */
+static void run_bf16(void) {
+    const uint64_t numel[] = {0, 1, 3, 63, 64, 65, 1000, 2049, 4097, 10};
+    const uint32_t n = sizeof numel / sizeof numel[0];
+    orc_tensor ta[sizeof numel / sizeof numel[0]], tb[sizeof numel / sizeof numel[0]];
+    uint64_t off[sizeof numel / sizeof numel[0]];
+    const uint64_t total = orc_layout(numel, n, 64, off);
+    for (uint32_t i = 0; i < n; ++i) {
+        ta[i].offset = off[i];
+        ta[i].numel = numel[i];
+        ta[i].flags = (i % 2) ? ORC_DECAY : 0u;
+        ta[i].has_grad = 1;
+    }
+    memcpy(tb, ta, sizeof ta);
+    orc_store a, b;
+    memset(&a, 0, sizeof a);
+    a.mode = ORC_MODE_BF16;
+    a.n_tensors = n;
+    a.tensors = ta;
+    a.total = total;
+    a.param = xmalloc(total * 2);
+    a.grad = xmalloc(total * 2);
+    a.growth_interval = 3;
+    a.growth_factor = 2.0;
+    a.backoff_factor = 0.5;
+    a.scale = 1024.0f;
+    a.nthreads = 4;
+    b = a;
+    b.tensors = tb;
+    b.param = xmalloc(total * 2);
+    b.grad = xmalloc(total * 2);
+    b.nthreads = 1;
+    uint16_t* pa = a.param;
+    uint16_t* ga = a.grad;
+    uint16_t* keep = xmalloc(total * 2);
+    for (uint64_t k = 0; k < total; ++k) {
+        pa[k] = orc_bf16_rne(frand(0.5f));
+        ga[k] = orc_bf16_rne(frand(0.1f));
+    }
+    orc_report r;
+    memcpy(keep, pa, total * 2);
+    orc_adam_hp adam = {1e-3, 0.9, 0.999, 1e-8, 0.0, 1, 0, 0.0};
+    CHECK(orc_adam_step(&a, &adam, &r) == -1, "BF16 store refuses Adam");
+    CHECK(orc_adam_step_opbyop(&a, &adam, NULL) == -1, "BF16 store refuses op-by-op Adam");
+    orc_sgd_hp refused[2] = {{1e-2, 0.9, 0.0, 0.0, 0, 0, 0.0}, {1e-2, 0.0, 0.0, 1e-2, 0, 0, 0.0}};
+    for (int v = 0; v < 2; ++v)
+        CHECK(orc_sgd_step(&a, &refused[v], &r) == -1, "BF16 store refuses momentum and decay");
+    CHECK(memcmp(pa, keep, total * 2) == 0 && a.t == 0, "refusals change nothing");
+
+    // plain SGD, with and without clipping, a None grad: 4 threads against 1, bit for bit
+    ta[4].has_grad = tb[4].has_grad = 0;
+    orc_sgd_hp plain[2] = {{1e-2, 0.0, 0.0, 0.0, 0, 0, 0.0}, {5e-2, 0.0, 0.0, 0.0, 0, 0, 0.25}};
+    for (int step = 0; step < 4; ++step) {
+        for (uint64_t k = 0; k < total; ++k) ga[k] = orc_bf16_rne(frand(0.1f));
+        memcpy(b.param, a.param, total * 2);
+        memcpy(b.grad, a.grad, total * 2);
+        memcpy(keep, pa, total * 2);
+        CHECK(orc_sgd_step(&a, &plain[step % 2], &r) == 0 &&
+                  orc_sgd_step(&b, &plain[step % 2], NULL) == 0, "BF16 sgd");
+        CHECK(memcmp(a.param, b.param, total * 2) == 0, "BF16 sgd: 4 threads == 1 thread");
+        CHECK(memcmp(pa + ta[4].offset, keep + ta[4].offset, numel[4] * 2) == 0,
+              "BF16 sgd: a None grad leaves its weights");
+        CHECK(a.t == (uint64_t)step + 1 && b.t == (uint64_t)step + 1, "BF16 sgd: step count");
+    }
+    // one element by hand: 1.0 - bf16(1.0 * 0.5) = 0.5, exact in bf16
+    pa[ta[1].offset] = 0x3F80;
+    ga[ta[1].offset] = 0x3F80;
+    orc_sgd_hp half = {0.5, 0.0, 0.0, 0.0, 0, 0, 0.0};
+    CHECK(orc_sgd_step(&a, &half, NULL) == 0 && pa[ta[1].offset] == 0x3F00, "BF16 sgd: 1 - 0.5");
+
+    // loss scaling: a +inf gradient skips the step and backs the scale off
+    a.scaler_enabled = 1;
+    for (uint64_t k = 0; k < total; ++k) ga[k] = orc_bf16_rne(frand(0.1f) * a.scale);
+    ga[ta[7].offset + 5] = 0x7F80;
+    memcpy(keep, pa, total * 2);
+    const uint64_t t0 = a.t;
+    const float scale = a.scale;
+    CHECK(orc_sgd_step(&a, &plain[1], &r) == 0, "BF16 sgd (inf)");
+    CHECK(r.found_inf && r.skipped && a.t == t0, "BF16 sgd: inf found and step skipped");
+    CHECK(a.scale == scale * 0.5f && memcmp(pa, keep, total * 2) == 0, "BF16 skipped step");
+
+    // accumulation into bf16 gradients from fp32 and bf16 sources, then the norm pass
+    for (uint32_t i = 0; i < n; ++i) {
+        float* f = xmalloc((numel[i] ? numel[i] : 1) * 4);
+        uint16_t* h = xmalloc((numel[i] ? numel[i] : 1) * 2);
+        for (uint64_t k = 0; k < numel[i]; ++k) f[k] = frand(1e-2f);
+        orc_f32_to_bf16_array(f, h, numel[i]);
+        ta[i].has_grad = 0;
+        orc_accumulate_grad(&a, i, f, 0);
+        orc_accumulate_grad(&a, i, h, 1);
+        CHECK(ta[i].has_grad == 1, "BF16 accumulate marks the grad present");
+        for (uint64_t k = 0; k < numel[i]; ++k)  // h + h with h exact in bf16: exactly 2h
+            CHECK(ga[ta[i].offset + k] == orc_bf16_rne(2.0f * orc_bf16_to_f32(h[k])),
+                  "BF16 accumulate: h + h");
+        free(f);
+        free(h);
+    }
+    int32_t inf = 0;
+    CHECK(orc_grad_sumsq(&a, 1.0f, &inf) >= 0.0 && !inf, "BF16 grad_sumsq");
+    free(keep);
+    free(a.param);
+    free(a.grad);
+    free(b.param);
+    free(b.grad);
+}
+
 int main(void) {
     run_mode(ORC_MODE_FP32);
     run_mode(ORC_MODE_MIXED);
+    run_bf16();
     // bf16 helpers: a slice of the exhaustive rounding check, special values, array forms
     CHECK(orc_bf16_check_range(0x7F7F0000ull, 0x7F810000ull, 2) == 0, "bf16 near overflow/inf/NaN");
     CHECK(orc_bf16_check_range(0x00000000ull, 0x00020000ull, 2) == 0, "bf16 denormals");
