@@ -4,8 +4,8 @@ rounding, `data = RNE(data - RNE(grad * lr))` (autograd/dynamic/optim.hpp:21-27,
 autograd/traced/ops.hpp:132-134 on BFLOAT16 tensors, autograd/dynamic/autograd.hpp:72).
 
 Checked against the oracle bit for bit: the reference's own test formulas
-(tests/sgd_optimizer.py, whose expected weights torch computes in bf16), GPT-2 124M's table
-with loss scaling, an overflow, clipping and a module-sized subset step, accumulation per
+(tests/sgd_optimizer.py, whose expected weights torch computes in bf16), GPT-2 124M's and
+774M's tables with loss scaling, an overflow, clipping and a module-sized subset step, accumulation per
 tensor and in buckets with the step's norm from their sums, a captured step replayed between
 eager ones, and a checkpoint round trip; the calls that would need fp32 state are refused
 with nothing changed.
@@ -111,6 +111,42 @@ def test_gpt2_124m_plain_sgd_matches_the_oracle():
         store.sgd_step(lr=0.05)
         ref.sgd_step(lr=0.05)
         _same_weights(store, ref, f"unscaled step {step}")
+    store.close()
+
+
+def test_gpt2_774m_plain_sgd_at_full_size():
+    """Config 4's table (436 tensors, 774,030,080 params) in a BF16 store, the reference's own
+    storage at the largest model its configurations hold that a BF16 store takes: plain SGD
+    with loss scaling and clipping at 1.0 for five steps, a +inf on step 2 (skipped, scale
+    halved), then a step without either.  Every bf16 weight equal to the oracle's after every
+    step, the reports equal."""
+    from ttperf import configs
+    torch = torch_mod()
+    _, shapes, decay, _ = configs.table("gpt2_774m")
+    store, ref = make_pair(shapes, decay, O.MODE_BF16, seed=410)
+    print(f"  {store.total} elements in {len(shapes)} tensors", flush=True)
+    store.configure_scaler(True, init_scale=65536.0, growth_interval=2)
+    ref.configure_scaler(True, 65536.0, growth_interval=2)
+    gen = torch.Generator(device="cuda").manual_seed(411)
+    hp = dict(lr=1e-2, max_grad_norm=1.0)
+    for step in range(5):
+        inf_at = store.offsets[300] + 1234 if step == 2 else None
+        device_grads(store, gen, 1e-3, scale=ref.scale, inf_at=inf_at, into=ref.grad)
+        _set_all(ref)
+        r = store.sgd_step(report=True, **hp)
+        e = ref.sgd_step(**hp)
+        print(f"  step {step}: skipped {e['skipped']} scale {e['scale']:g} "
+              f"norm {e['grad_norm']:.6g} clip {e['clip_coef']:.6g}", flush=True)
+        _check(r, e, True)
+        assert e["skipped"] == (step == 2)
+        _same_weights(store, ref, f"step {step}")
+    store.configure_scaler(False)
+    ref.configure_scaler(False)
+    device_grads(store, gen, 1e-1, into=ref.grad)
+    _set_all(ref)
+    store.sgd_step(lr=0.05)
+    ref.sgd_step(lr=0.05)
+    _same_weights(store, ref, "unscaled step")
     store.close()
 
 
