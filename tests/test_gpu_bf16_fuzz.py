@@ -29,8 +29,10 @@ from test_gpu_fuzz import Case
 
 pytestmark = pytest.mark.gpu
 
-# 300 seeded cases of 50 operations by default; TTP_BF16_FUZZ_CASES=N runs N
-SEEDS = list(range(5000, 5000 + int(os.environ.get("TTP_BF16_FUZZ_CASES", "300"))))
+# 300 seeded cases of 50 operations by default; TTP_BF16_FUZZ_CASES=N runs N, from seed
+# TTP_BF16_FUZZ_FIRST (5000)
+_FIRST = int(os.environ.get("TTP_BF16_FUZZ_FIRST", "5000"))
+SEEDS = list(range(_FIRST, _FIRST + int(os.environ.get("TTP_BF16_FUZZ_CASES", "300"))))
 N_OPS = int(os.environ.get("TTP_FUZZ_OPS", "50"))
 
 
